@@ -1,0 +1,146 @@
+"""Seeded synthetic inputs and ggml-block quantizers for the benchmark and the tests.
+
+The reference quantizes weights with ggml's ``quantize_row_q8_0_ref`` (used by the backend at load
+time, sw/ggml-tesseract/tsr-weights.cpp:33-49) and its test models with a Q4_K encoder
+(sw/ggml-tesseract/tests/gen_tiny_models.py:91-122). Neither is importable here, so this module
+carries its own:
+
+* ``normal(seed, n, std)``: counter-based SplitMix64 -> two uniforms -> Box-Muller in float64, rounded
+  to float32. Every value depends only on (seed, index), so CPU and GPU harnesses draw identical bits.
+* ``quantize_q8_0``: d = amax / 127 in f32, q = round-half-away(x / d ... as x * (1/d)), fp16(d) -- the
+  rule of quantize_row_q8_0_ref, which is also QACT A32's (sw/sim/tsr_ref.c:472-487).
+* ``quantize_q4_k``: per 32-value sub-block an affine step/min, 6-bit scales and mins packed as ggml's
+  get_scale_min_k4 reads them (sw/sim/tsr_ref.c:359-367), 4-bit quants low nibble = sub-block 2g,
+  high = 2g+1. Only the resulting blocks matter for parity; any valid Q4_K encoder would do.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+_M64 = (1 << 64) - 1
+_GOLD = np.uint64(0x9E3779B97F4A7C15)
+_MIX1 = np.uint64(0xBF58476D1CE4E5B9)
+_MIX2 = np.uint64(0x94D049BB133111EB)
+
+
+def _splitmix(seed: int, start: int, n: int) -> np.ndarray:
+    idx = np.arange(start, start + n, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed & _M64) + (idx + np.uint64(1)) * _GOLD
+        z = (z ^ (z >> np.uint64(30))) * _MIX1
+        z = (z ^ (z >> np.uint64(27))) * _MIX2
+        z = z ^ (z >> np.uint64(31))
+    return z
+
+
+def uniform(seed: int, n: int, start: int = 0) -> np.ndarray:
+    """n float64 uniforms in [0, 1) (53-bit)."""
+    return (_splitmix(seed, start, n) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+
+
+def normal(seed: int, n: int, std: float = 1.0, chunk: int = 1 << 24) -> np.ndarray:
+    """n float32 values ~ N(0, std^2); value i uses uniforms 2i and 2i+1 of the seed's stream."""
+    out = np.empty(n, np.float32)
+    for s in range(0, n, chunk):
+        m = min(chunk, n - s)
+        u = uniform(seed, 2 * m, 2 * s).reshape(m, 2)
+        r = np.sqrt(-2.0 * np.log1p(-u[:, 0]))
+        out[s:s + m] = (r * np.cos(2.0 * np.pi * u[:, 1]) * std).astype(np.float32)
+    return out
+
+
+def seed_of(config: str, tensor: str) -> int:
+    """A documented 64-bit seed per (config, tensor): FNV-1a over 'config/tensor'."""
+    h = 0xCBF29CE484222325
+    for b in f"{config}/{tensor}".encode():
+        h = ((h ^ b) * 0x100000001B3) & _M64
+    return h
+
+
+# ---------------------------------------------------------------------------------------------
+# Q8_0: blocks of 32, {fp16 d, int8 qs[32]} = 34 bytes
+# ---------------------------------------------------------------------------------------------
+def _round_half_away(v: np.ndarray) -> np.ndarray:
+    t = np.trunc(v)
+    frac = v - t                                   # exact for |v| < 2^23
+    return t + np.where(np.abs(frac) >= 0.5, np.sign(v), 0.0).astype(v.dtype)
+
+
+def quantize_q8_0(w: np.ndarray) -> np.ndarray:
+    """f32 [N, K] (K % 32 == 0) -> uint8 [N, K/32 * 34]."""
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    b = w.reshape(N, K // 32, 32)
+    amax = np.abs(b).max(axis=2)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, np.float32(1.0)), np.float32(0.0)).astype(np.float32)
+    q = np.clip(_round_half_away((b * idv[:, :, None]).astype(np.float32)), -128, 127).astype(np.int8)
+    out = np.empty((N, K // 32, 34), np.uint8)
+    out[:, :, 0:2] = d.astype(np.float16).view(np.uint8).reshape(N, K // 32, 2)
+    out[:, :, 2:] = q.view(np.uint8)
+    return out.reshape(N, K // 32 * 34)
+
+
+def dequantize_q8_0(blocks: np.ndarray, K: int) -> np.ndarray:
+    b = np.ascontiguousarray(blocks, np.uint8).reshape(-1, K // 32, 34)
+    d = b[:, :, 0:2].copy().view(np.float16).astype(np.float32)
+    q = b[:, :, 2:].view(np.int8).astype(np.float32)
+    return (q * d).reshape(-1, K)
+
+
+# ---------------------------------------------------------------------------------------------
+# Q4_K: super-blocks of 256 = 8 sub-blocks of 32; {fp16 d, fp16 dmin, u8 scales[12], u8 qs[128]}
+# ---------------------------------------------------------------------------------------------
+def quantize_q4_k(w: np.ndarray) -> np.ndarray:
+    """f32 [N, K] (K % 256 == 0) -> uint8 [N, K/256 * 144].
+
+    Sub-block j: x ~ d*sc_j*q - dmin*m_j with q in 0..15, sc_j and m_j 6-bit unsigned."""
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    nb = N * (K // 256)
+    x = w.reshape(nb, 8, 32)
+    lo = np.minimum(x.min(axis=2), 0.0)
+    hi = np.maximum(x.max(axis=2), lo)
+    step = (hi - lo) / 15.0
+    mins = -lo
+    d = (step.max(axis=1) / 63.0).astype(np.float16)
+    dmin = (mins.max(axis=1) / 63.0).astype(np.float16)
+    d32, m32 = d.astype(np.float32), dmin.astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        sc = np.where(d32[:, None] > 0, np.rint(step / d32[:, None]), 0).clip(0, 63).astype(np.uint8)
+        mn = np.where(m32[:, None] > 0, np.rint(mins / m32[:, None]), 0).clip(0, 63).astype(np.uint8)
+        eff = d32[:, None] * sc.astype(np.float32)
+        off = m32[:, None] * mn.astype(np.float32)
+        q = np.where(eff[:, :, None] > 0, np.rint((x + off[:, :, None]) / eff[:, :, None]), 0).clip(0, 15).astype(np.uint8)
+    scales = np.empty((nb, 12), np.uint8)
+    scales[:, 0:4] = (sc[:, 0:4] & 63) | ((sc[:, 4:8] >> 4) << 6)
+    scales[:, 4:8] = (mn[:, 0:4] & 63) | ((mn[:, 4:8] >> 4) << 6)
+    scales[:, 8:12] = (sc[:, 4:8] & 15) | ((mn[:, 4:8] & 15) << 4)
+    q = q.reshape(nb, 4, 2, 32)
+    qs = (q[:, :, 0, :] | (q[:, :, 1, :] << 4)).reshape(nb, 128)
+    out = np.concatenate([d.view(np.uint8).reshape(nb, 2), dmin.view(np.uint8).reshape(nb, 2), scales, qs], axis=1)
+    return out.reshape(N, K // 256 * 144)
+
+
+def q4k_scale_min(scales: np.ndarray):
+    """The 8 (sc, m) pairs of each 12-byte scales row (get_scale_min_k4)."""
+    s = scales.astype(np.int32)
+    sc = np.empty(s.shape[:-1] + (8,), np.int32)
+    mn = np.empty_like(sc)
+    sc[..., :4] = s[..., 0:4] & 63
+    mn[..., :4] = s[..., 4:8] & 63
+    sc[..., 4:] = (s[..., 8:12] & 15) | ((s[..., 0:4] >> 6) << 4)
+    mn[..., 4:] = (s[..., 8:12] >> 4) | ((s[..., 4:8] >> 6) << 4)
+    return sc, mn
+
+
+def dequantize_q4_k(blocks: np.ndarray, K: int) -> np.ndarray:
+    b = np.ascontiguousarray(blocks, np.uint8).reshape(-1, 144)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    dmin = b[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    sc, mn = q4k_scale_min(b[:, 4:16])
+    qs = b[:, 16:].reshape(-1, 4, 32)
+    q = np.stack([qs & 15, qs >> 4], axis=2).reshape(-1, 8, 32).astype(np.float32)
+    y = (d[:, None] * sc)[:, :, None] * q - (dmin[:, None] * mn)[:, :, None]
+    return y.reshape(-1, K)

@@ -1,0 +1,194 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-inference hot path on one MI355X.
+
+Workload: the Llama-3-8B FFN matrix-vector pair at batch 1 --
+Q4_K W_up [14336 x 4096] then Q4_K W_down [4096 x 14336], activation f32 quantized on the fly to
+Q8_K (A256). One step = one up MUL_MAT followed by one down MUL_MAT on its output, i.e. the
+weight stream of one FFN of one decode token. Weights are fp32 N(0, 0.02) from fixed seeds
+quantized to Q4_K; the activation is N(0, 1). Inputs are resident in HBM before timing.
+
+Honest HBM numbers: the step rotates through distinct device copies of the weights whose total
+exceeds twice the 256 MB Infinity Cache, so weight reads come from HBM.
+
+Output: one JSON line (metric, value = algorithmic weight+activation bytes per step / time,
+roofline of the dominant kernel measured live with HIP events on the launch stream, and the CPU
+baseline: this repository's oracle (the reference's numerics restated in C) on the host cores).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "tesseract-npu_amd"))
+
+import tsr_hip  # noqa: E402
+import tsr_synth as S  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+METRIC = "decode tok/s (8B Q4_K, ctx 4096); matvec/attn HBM GB/s as % of peak"
+
+
+class HipEvents:
+    """hipEvent timing on a given stream (libamdhip64 via ctypes)."""
+
+    def __init__(self):
+        self.h = C.CDLL("libamdhip64.so")
+        self.h.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.h.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.h.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.h.hipDeviceSynchronize.argtypes = []
+
+    def event(self):
+        e = C.c_void_p()
+        assert self.h.hipEventCreate(C.byref(e)) == 0
+        return e
+
+    def record(self, e, stream):
+        assert self.h.hipEventRecord(e, stream) == 0
+
+    def elapsed_ms(self, a, b) -> float:
+        assert self.h.hipEventSynchronize(b) == 0
+        ms = C.c_float()
+        assert self.h.hipEventElapsedTime(C.byref(ms), a, b) == 0
+        return ms.value
+
+    def device_sync(self):
+        assert self.h.hipDeviceSynchronize() == 0
+
+
+def mv_bytes(N: int, K: int) -> int:
+    """Algorithmic bytes of one Q4_K matvec: weights + f32 x + f32 y."""
+    return N * (K // 256) * 144 + 4 * K + 4 * N
+
+
+def cpu_baseline(blocks_up, x, seconds: float = 10.0) -> dict:
+    """The oracle's MUL_MAT (the reference numerics restated in C) on the host cores, on whole
+    W_up matvecs, repeated for about `seconds`. Reported in weight GB/s like the GPU value."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle
+    oc = oracle.Oracle()
+    threads = min(16, os.cpu_count() or 1)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oc.mul_mat(1, blocks_up, 4096, x[None, :], threads=threads)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            break
+    per = dt / n
+    return {"value": round(mv_bytes(14336, 4096) / per / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{n} x Q4_K matvec 14336x4096 (oracle/oc_num.c, {threads} threads), {per * 1e3:.1f} ms each"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=0, help="distinct weight copies (0: enough for 2x MALL)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is a "
+                                   "design note in DESIGN.md, not measured)"}))
+        return 2
+
+    dev = tsr_hip.Device(0)
+    info = dev.info()
+    stream = dev.stream
+    ev = HipEvents()
+
+    N_up, K_up, N_dn, K_dn = 14336, 4096, 4096, 14336
+    up_blocks = S.quantize_q4_k(S.normal(S.seed_of("cfg2", "w_up"), N_up * K_up, 0.02).reshape(N_up, K_up))
+    dn_blocks = S.quantize_q4_k(S.normal(S.seed_of("cfg2", "w_down"), N_dn * K_dn, 0.02).reshape(N_dn, K_dn))
+    x = S.normal(S.seed_of("cfg2", "x"), K_up)
+    per_copy = up_blocks.nbytes + dn_blocks.nbytes
+    copies = args.copies or max(2, -(-2 * MALL_BYTES // per_copy))
+    ups = [dev.weight(1, up_blocks, N_up, K_up) for _ in range(copies)]
+    dns = [dev.weight(1, dn_blocks, N_dn, K_dn) for _ in range(copies)]
+    xb = dev.upload(x)
+    hb = dev.alloc(4 * N_up)
+    yb = dev.alloc(4 * N_dn)
+
+    def step(i):
+        dev.mul_mat(ups[i % copies], xb, 1, K_up, hb, N_up, stream=stream)
+        dev.mul_mat(dns[i % copies], hb, 1, K_dn, yb, N_dn, stream=stream)
+
+    for i in range(args.warmup):
+        step(i)
+    ev.device_sync()
+    e0, e1 = ev.event(), ev.event()
+    ev.record(e0, stream)
+    for i in range(args.steps):
+        step(i)
+    ev.record(e1, stream)
+    ms = ev.elapsed_ms(e0, e1)
+    ev.device_sync()
+    ms_step = ms / args.steps
+    step_bytes = mv_bytes(N_up, K_up) + mv_bytes(N_dn, K_dn)
+
+    # per-kernel launch durations (HIP events on the launch stream), each over rotating copies
+    def time_kernel(fn, n):
+        a, b = ev.event(), ev.event()
+        for i in range(5):
+            fn(i)
+        ev.record(a, stream)
+        for i in range(n):
+            fn(i)
+        ev.record(b, stream)
+        return ev.elapsed_ms(a, b) / n
+
+    n_k = max(50, args.steps)
+    up_ms = time_kernel(lambda i: dev.mul_mat(ups[i % copies], xb, 1, K_up, hb, N_up, stream=stream), n_k)
+    dn_ms = time_kernel(lambda i: dev.mul_mat(dns[i % copies], hb, 1, K_dn, yb, N_dn, stream=stream), n_k)
+    kern = [("k_mv_q4k (up 14336x4096)", up_ms, mv_bytes(N_up, K_up)),
+            ("k_mv_q4k (down 4096x14336)", dn_ms, mv_bytes(N_dn, K_dn))]
+    name, kms, kbytes = max(kern, key=lambda r: r[1])
+    achieved = kbytes / (kms * 1e-3) / 1e9
+
+    y = yb.read(np.float32, (N_dn,))
+    if not np.isfinite(y).all():
+        print(json.dumps({"error": "non-finite output"}))
+        return 1
+
+    cpu = None if args.no_cpu else cpu_baseline(up_blocks, x)
+    out = {
+        "metric": METRIC,
+        "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k x q8_k -> f32 (int8 dot, f32 accumulate)",
+        "data": "synthetic: seeded N(0,0.02) weights quantized to Q4_K, N(0,1) activation",
+        "config": {"workload": "Llama-3-8B FFN up+down Q4_K matvec pair, batch 1 (BASELINE configs[1])",
+                   "shapes": "W_up 14336x4096, W_down 4096x14336", "weight_copies": copies,
+                   "copy_bytes": per_copy, "device": info["arch"], "n_cu": info["n_cu"]},
+        "roofline": {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "launch_us": round(kms * 1e3, 3), "algorithmic_bytes": kbytes,
+                     "other_kernels": {n: {"launch_us": round(t * 1e3, 3), "GB/s": round(b / (t * 1e-3) / 1e9, 1)}
+                                       for n, t, b in kern}},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+    dev.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,176 @@
+/* tsr_hip.h -- C ABI of libtsr_hip, the MI355X (gfx950) implementation of Tesseract's quantized
+ * inference hot path: on-the-fly activation quantization (QACT A32 / A256), Q8_0 and Q4_K
+ * MUL_MAT, the q8_0 KV cache (SET_ROWS, byte get / set) and flash attention over it.
+ *
+ * The library sits where the reference's ggml backend hands work to its device: the backend's
+ * buffer, tensor and graph-compute callbacks (sw/ggml-tesseract/ggml-tesseract.cpp) and the
+ * transport below them (sw/transport/tsr_transport.h:61-134). Each entry point below names the
+ * reference interface it replaces. Results are the reference simulator's bits (sw/sim/tsr_ref*.c):
+ * integer block sums and quantized activations bit-exact, f32 outputs bit-exact (the contract
+ * allows 1e-5 relative), attention bit-exact (the contract allows 2e-3 absolute).
+ *
+ * Conventions
+ *   - Every function returns 0 or a negative TSR_HIP_E_* code; tsr_hip_strerror names it.
+ *   - Pointers named *_dev are device addresses (from tsr_hip_alloc or any HIP allocation on the
+ *     context's device); every other pointer is host memory.
+ *   - `stream` is a hipStream_t of the context's device, or NULL for the context's own stream.
+ *     Kernel entry points are asynchronous on that stream; tsr_hip_sync waits.
+ *   - A context is thread-safe: calls on one context are serialized by its mutex (the reference
+ *     backend's device mutex, ggml-tesseract.cpp:3932).
+ *   - Strides are in elements (floats) unless named *_bytes.
+ */
+#ifndef TSR_HIP_H
+#define TSR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes (the transport's TSR_TE_* role, sw/transport/tsr_transport.h:266-276) ---- */
+#define TSR_HIP_OK          0
+#define TSR_HIP_E_ARG      -1   /* a NULL or malformed argument */
+#define TSR_HIP_E_SHAPE    -2   /* a shape the op does not support (K % block, D, GQA ratio, ...) */
+#define TSR_HIP_E_NOMEM    -3   /* device or host allocation failed */
+#define TSR_HIP_E_HIP      -4   /* a HIP runtime call failed */
+#define TSR_HIP_E_RANGE    -5   /* a byte range or cell index beyond the object */
+#define TSR_HIP_E_NODEV    -6   /* no such device */
+#define TSR_HIP_E_FMT      -7   /* unknown weight format / QA kind */
+#define TSR_HIP_E_MASK     -8   /* the mask summary needs the f32 mask copy, or is malformed */
+
+/* weight formats (ISA MVM sub field, sw/sim/include/tsr_tables.h:103-104) */
+#define TSR_HIP_FMT_Q8_0    0u
+#define TSR_HIP_FMT_Q4_K    1u
+/* QA kinds (QACT sub field, sw/sim/include/tsr_tables.h:105-106) */
+#define TSR_HIP_QA_A32      0u
+#define TSR_HIP_QA_A256     1u
+/* KV planes (KVST sub field, sw/sim/include/tsr_ref_at.h:56-57) */
+#define TSR_HIP_KV_K        0u
+#define TSR_HIP_KV_V        1u
+/* tsr_hip_mul_mat flags (the MUL_MAT record's FLAGS word, sw/ctrl/ref/mulmat_ref.hpp:14-16) */
+#define TSR_HIP_MM_ACC_DST  0x1u  /* y = FA(y_old, W.x) */
+
+typedef struct tsr_hip_ctx tsr_hip_ctx;
+typedef struct tsr_hip_weight tsr_hip_weight;
+typedef struct tsr_hip_kv tsr_hip_kv;
+
+/* ---- device and context ---------------------------------------------------------------------
+ * Replaces the backend's device open (tsr_dev_open_locked, ggml-tesseract.cpp:463) and
+ * tsr_transport_open / _close (tsr_transport.h:61-72). One context per (process, device); it owns a
+ * default-priority hipStream and its scratch memory. */
+int         tsr_hip_open(int device, tsr_hip_ctx ** out);
+int         tsr_hip_close(tsr_hip_ctx * ctx);
+const char * tsr_hip_strerror(int code);
+/* The context's stream (a hipStream_t) for callers that order their own work against it. */
+void *      tsr_hip_stream(tsr_hip_ctx * ctx);
+/* Wait for all work on `stream` (NULL: the context's stream). Replaces tsr_transport_wait
+ * (tsr_transport.h:112-116). */
+int         tsr_hip_sync(tsr_hip_ctx * ctx, void * stream);
+/* Number of compute units and the device name (get_props / get_memory, ggml-tesseract.cpp:4312-4328). */
+int         tsr_hip_device_info(tsr_hip_ctx * ctx, int * n_cu, char * name, size_t name_len,
+                                size_t * mem_free, size_t * mem_total);
+
+/* ---- raw device buffers (ggml buffer alloc / set_tensor / get_tensor / memset_tensor / free for
+ * non-weight tensors, ggml-tesseract.cpp:1905-2042; tsr_transport_write / _read, tsr_transport.h:80-98) */
+int tsr_hip_alloc(tsr_hip_ctx * ctx, size_t bytes, void ** dev_out);
+int tsr_hip_free(tsr_hip_ctx * ctx, void * dev);
+int tsr_hip_write(tsr_hip_ctx * ctx, void * dst_dev, const void * src, size_t bytes);
+int tsr_hip_read(tsr_hip_ctx * ctx, void * dst, const void * src_dev, size_t bytes);
+int tsr_hip_memset(tsr_hip_ctx * ctx, void * dst_dev, int value, size_t bytes);
+
+/* ---- weights ---------------------------------------------------------------------------------
+ * Upload an N x K weight given as ggml blocks (row n = K/32 block_q8_0 or K/256 block_q4_K,
+ * consecutive) and convert it to the device layout: per-row scale ("meta") bytes split from the
+ * quant bytes, both row-contiguous. Replaces the weight path of set_tensor: tsr_buffer_set_tensor
+ * -> tsr_store_weight_rows -> tsr_repack_row (ggml-tesseract.cpp:852-878, 1905-1945;
+ * sw/sim/tsr_ref.c:296-316). K must be a positive multiple of the block size and <= 32768
+ * (K_MAX, sw/sim/include/tsr_isa.h:64-67); N >= 1. */
+int tsr_hip_weight_upload(tsr_hip_ctx * ctx, uint32_t fmt, const void * ggml_blocks, uint32_t N, uint32_t K,
+                          tsr_hip_weight ** out);
+/* The exact ggml blocks back (get_tensor of a weight; tsr_unrepack_row, sw/sim/tsr_ref.c:318-333). */
+int tsr_hip_weight_read(tsr_hip_ctx * ctx, const tsr_hip_weight * w, void * ggml_blocks);
+int tsr_hip_weight_free(tsr_hip_ctx * ctx, tsr_hip_weight * w);
+/* Format, N, K and the device bytes a weight occupies. */
+int tsr_hip_weight_info(const tsr_hip_weight * w, uint32_t * fmt, uint32_t * N, uint32_t * K, size_t * dev_bytes);
+
+/* ---- QACT --------------------------------------------------------------------------------------
+ * T token rows x_dev[t * x_stride + k] (f32, k < K) -> T QA images in the spec layout
+ * (QS int8[K] | D f32[K/bs] | BS int16[K/16] for A256, each region padded to 64 bytes, tails zero;
+ * docs/spec.md:402-425) at qa_dev + t * tsr_hip_qa_bytes(kind, K). The QACT tile op
+ * (sw/sim/tsr_sim.c:1507-1522, tsr_qact sw/sim/tsr_ref.c:456). MUL_MAT and FLASH_ATTN quantize
+ * their activations themselves; this entry point exposes the quantizer for checking and for
+ * callers that keep QA images. */
+size_t tsr_hip_qa_bytes(uint32_t kind, uint32_t K);
+int tsr_hip_qact(tsr_hip_ctx * ctx, uint32_t kind, const float * x_dev, uint32_t K, uint32_t T, uint64_t x_stride,
+                 uint8_t * qa_dev, void * stream);
+
+/* ---- MUL_MAT -------------------------------------------------------------------------------------
+ * GGML_OP_MUL_MAT with a Q8_0 / Q4_K weight and f32 activations (the MUL_MAT kind record,
+ * sw/ctrl/include/tsr/opl.hpp:214-218; lowered by tsr_lower_mul_mat, ggml-tesseract.cpp:2790-2928;
+ * executed as QACT -> MVM per token, sw/ctrl/ref/mulmat_ref.cpp:43-105):
+ *   y_dev[t * y_stride + n] = v                      v = tree16 row dot of W row n and QACT(x_t)
+ *                           = FA(add_dev[t * add_stride + n], v)   with an addend (add_stride 0: row 0)
+ *                           = FA(y_old, v)                          with TSR_HIP_MM_ACC_DST
+ * for t < T, n < N. An addend together with ACC_DST is refused (TSR_HIP_E_ARG), as the kernel's record
+ * check does. x, y and add must not overlap. T >= 1. */
+int tsr_hip_mul_mat(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T, uint64_t x_stride,
+                    float * y_dev, uint64_t y_stride, const float * add_dev, uint64_t add_stride, uint32_t flags,
+                    void * stream);
+/* The exact integer part of MUL_MAT for checking: for token 0, the per-block sums of every row
+ * (Q8_0: isum per 32-block, N x K/32; Q4_K: isum and msum per super-block interleaved,
+ * N x 2K/256) as the MVM computes them (term_q8_0 / term_q4_K, sw/sim/tsr_ref.c:525-567). */
+int tsr_hip_mul_mat_isums(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, int32_t * isums_dev,
+                          void * stream);
+
+/* ---- KV cache ----------------------------------------------------------------------------------
+ * A q8_0 K or V cache of kv_size cells of E = n_head_kv * D values (llama.cpp's cache_k_l<n> /
+ * cache_v_l<n> tensors, q8_0; recognized by the backend in tsr-kvbuf.h:61-63). The device layout is
+ * the library's own; get / set bytes convert to and from the ggml q8_0 image exactly
+ * (tsr_kv_set_bytes / tsr_kv_get_bytes, sw/sim/tsr_ref_at.c:178-212). E % 64 == 0. */
+int tsr_hip_kv_create(tsr_hip_ctx * ctx, uint32_t E, uint32_t kv_size, tsr_hip_kv ** out);
+int tsr_hip_kv_free(tsr_hip_ctx * ctx, tsr_hip_kv * kv);
+/* Bytes [off, off + bytes) of the ggml image of plane `which` (row j = cell j, E/32 * 34 bytes). */
+int tsr_hip_kv_set_bytes(tsr_hip_ctx * ctx, tsr_hip_kv * kv, uint32_t which, size_t off, const void * src, size_t bytes);
+int tsr_hip_kv_get_bytes(tsr_hip_ctx * ctx, const tsr_hip_kv * kv, uint32_t which, size_t off, void * dst, size_t bytes);
+/* GGML_OP_SET_ROWS into the cache (the SET_ROWS_KV kind, sw/ctrl/ref/kv_ref.cpp:20-45): rows
+ * src_dev[i * src_stride + e] (f32, e < E) are quantized (QACT A32, fp16 scales) into cells
+ * idx_dev[i] (int64, device), i < n_rows. Every index must be < kv_size (checked on the device: an
+ * out-of-range index stores nothing and sets *bad_dev if bad_dev is not NULL). */
+int tsr_hip_kv_set_rows(tsr_hip_ctx * ctx, tsr_hip_kv * kv, uint32_t which, const float * src_dev, uint32_t n_rows,
+                        uint64_t src_stride, const int64_t * idx_dev, int32_t * bad_dev, void * stream);
+
+/* ---- mask summary (the backend's MSUM producer, tsr_msum_build_f16 sw/sim/tsr_ref_at.c:646-693) --
+ * words: 8 + 4 * n_q uint32 (host). Returns the flags word (bit 0 GENERAL) or a negative code. */
+int tsr_hip_msum_build_f16(const uint16_t * mask, size_t row_stride, uint32_t n_kv, uint32_t n_q, uint32_t * words);
+
+/* ---- FLASH_ATTN_EXT ----------------------------------------------------------------------------
+ * GGML_OP_FLASH_ATTN_EXT with f32 q and a q8_0 K / V cache (the FLASH_ATTN kind, lowered by
+ * tsr_lower_fa sw/ggml-tesseract/tsr-build.cpp:673-773; numerics tsr_ref_fa sw/sim/tsr_ref_at.c:774-860):
+ *   q_dev  [T][n_head][D] f32, token t at q_dev + t * q_stride
+ *   out_dev[T][n_head][D] f32, token t at out_dev + t * out_stride
+ *   msum   the host MSUM words of the op's mask (n_q = T, n_kv cells visible at most)
+ *   mask_f32_dev  the f32 mask copy (rows of 16*ceil(n_kv/16) floats, fdiv(mask, scale), -inf pad;
+ *          tsr_msum_mask_f32) -- required only when the MSUM is GENERAL, else NULL
+ *   new_runs / n_new  cell runs [lo, hi) written in this launch (their chunks are merged last)
+ * D in {64, 128, 256, 512}; n_head % n_head_kv == 0; n_head / n_head_kv <= 64; n_head_kv * D == E of
+ * both caches; scale finite, normal and > 0. */
+int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint64_t q_stride,
+                       const tsr_hip_kv * kc, const tsr_hip_kv * vc, uint32_t D, uint32_t n_head, uint32_t n_head_kv,
+                       float scale, const uint32_t * msum, const float * mask_f32_dev,
+                       const uint32_t (*new_runs)[2], uint32_t n_new, float * out_dev, uint64_t out_stride,
+                       void * stream);
+
+/* ---- counters (the backend's TSR_STATS report, ggml-tesseract.cpp:3799-3866) --------------------- */
+typedef struct tsr_hip_counters {
+    uint64_t mul_mat_calls, mul_mat_rows, mul_mat_weight_bytes;
+    uint64_t flash_attn_calls, flash_attn_kv_bytes;
+    uint64_t set_rows_calls, qact_calls;
+} tsr_hip_counters;
+int tsr_hip_get_counters(tsr_hip_ctx * ctx, tsr_hip_counters * out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

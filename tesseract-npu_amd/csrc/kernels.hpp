@@ -1,0 +1,94 @@
+// kernels.hpp -- argument blocks and launchers of the gfx950 kernels (host and device side).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tsr {
+
+struct QactArgs {
+    const float * x;
+    uint64_t x_stride;       // floats between token rows
+    uint8_t * qa;
+    uint32_t qa_bytes;       // bytes between QA images
+    uint32_t K, kind;
+    uint32_t d_off, bs_off;  // byte offsets of the D and BS regions
+};
+
+// MUL_MAT over the device weight layout:
+//   Q8_0: meta = fp16 d [N][K/32], quant = int8 [N][K/32][32]
+//   Q4_K: meta = {fp16 d, fp16 dmin, u8 scales[12]} [N][K/256], quant = u8 [N][K/256][128]
+struct MvArgs {
+    const uint8_t * wm;
+    const uint8_t * wq;
+    const float * x;
+    uint64_t x_stride;
+    float * y;
+    uint64_t y_stride;
+    const float * add;       // nullable
+    uint64_t add_stride;
+    int32_t * isums;         // nullable: per-block integer sums of token 0 (checking)
+    uint32_t N, K, T;
+    uint32_t acc;            // y = FA(y_old, v)
+};
+
+// A KV plane (see k_kv.hip for the layout).
+struct KvArgs {
+    uint8_t * base;          // meta region at 0
+    size_t quant_off;        // byte offset of the quant region
+    uint32_t E, kv_size;
+};
+
+// EXPK constants (VU 6.3): LK = round(log2(e) 2^38), c_k = round(ln(2)^k / k! 2^32),
+// t64[j] = round(2^(j/64) 2^30); computed on the host from their definitions.
+struct ExpkTab {
+    uint32_t t64[64];
+    uint64_t lk, c1, c2, c3;
+};
+
+// One chunk of one query token (the planner's output), in execution order per token.
+struct FaItem {
+    uint32_t t;              // token
+    uint32_t u0, n;          // groups [u0, u0 + n)
+    uint32_t c_lo, c_hi;     // visible chunk-relative cells (FAST)
+    uint32_t general;        // GENERAL chunk: all cells, f32 mask added
+    uint32_t s_off;          // first score cell of the item in S (scores at S + s_off * n_head)
+    uint32_t tile0, ntiles;  // its score tiles
+    uint32_t pad[3];
+};
+struct FaTile {
+    uint32_t item, c0;       // 256 chunk-relative cells [c0, c0 + 256)
+};
+
+struct FaArgs {
+    const uint8_t * qa;      // QA(A32) image of each token's query row (n_head * D values)
+    uint32_t qa_bytes, qa_d_off;
+    KvArgs kc, vc;
+    uint32_t D, G, n_head, n_head_kv, E;
+    float scale;
+    const float * mask;      // GENERAL: f32 mask rows of mstride floats
+    uint32_t mstride;
+    const FaItem * items;
+    const FaTile * tiles;
+    const uint32_t * tok_first;
+    const uint32_t * tok_count;
+    float * S;               // scores
+    float * Mpart;           // [tile][n_head] tile maxima
+    float * MK;              // [item][n_head] chunk maxima
+    float * OP;              // [item][4][n_head][D] channel partials
+    float * LP;              // [item][4][n_head] channel row sums
+    float * out;
+    uint64_t out_stride;
+    ExpkTab ex;
+};
+
+}  // namespace tsr
+
+int tsr_launch_qact(const tsr::QactArgs & a, uint32_t T, hipStream_t s);
+int tsr_launch_mv_q8_0(const tsr::MvArgs & a, hipStream_t s);
+int tsr_launch_mv_q4_k(const tsr::MvArgs & a, hipStream_t s);
+int tsr_launch_kv_bytes(const tsr::KvArgs & a, uint32_t which, uint64_t off, uint64_t n, uint8_t * stage, int to_dev,
+                        hipStream_t s);
+int tsr_launch_kv_set_rows(const tsr::KvArgs & a, uint32_t which, const float * src, uint32_t n_rows,
+                           uint64_t src_stride, const int64_t * idx, int32_t * bad, hipStream_t s);
+int tsr_launch_fa(const tsr::FaArgs & a, uint32_t n_tiles, uint32_t n_items, uint32_t T, hipStream_t s);

@@ -1,0 +1,132 @@
+// tsr_dev.hpp -- device helpers shared by the gfx950 kernels: the spec's f32 rules, exact
+// conversions, QACT rounding and wavefront (wave64) exchange primitives.
+//
+// f32 rules (sw/sim/tsr_ref.c:54-104; docs/spec.md:1405-1418): inputs with a zero exponent field
+// are signed zeros (DAZ), the operation is one IEEE binary32 RNE operation with gradual underflow,
+// a subnormal result becomes a signed zero (FTZ) and any NaN result 0x7FC00000. The kernels are
+// compiled with -ffp-contract=off (no FMA fusion) and run with f32 denormals enabled, so the native
+// operation is the gradual-underflow result the rule post-processes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tsr {
+
+constexpr uint32_t kNaN = 0x7FC00000u;
+constexpr uint32_t kNegInf = 0xFF800000u;
+
+__device__ __forceinline__ uint32_t fb(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float bf(uint32_t u) { return __uint_as_float(u); }
+
+__device__ __forceinline__ float daz(float x) {
+    const uint32_t u = fb(x);
+    return (u & 0x7F800000u) ? x : bf(u & 0x80000000u);
+}
+__device__ __forceinline__ float fin(float r) {
+    const uint32_t u = fb(r), e = u & 0x7F800000u;
+    if (e == 0x7F800000u) return (u & 0x007FFFFFu) ? bf(kNaN) : r;
+    if (e == 0u) return bf(u & 0x80000000u);
+    return r;
+}
+// NaN -> canonical only (results that cannot be subnormal).
+__device__ __forceinline__ float canon(float r) { return (fb(r) & 0x7FFFFFFFu) > 0x7F800000u ? bf(kNaN) : r; }
+
+__device__ __forceinline__ float sadd(float a, float b) { return fin(daz(a) + daz(b)); }
+__device__ __forceinline__ float ssub(float a, float b) { return fin(daz(a) - daz(b)); }
+__device__ __forceinline__ float smul(float a, float b) { return fin(daz(a) * daz(b)); }
+__device__ __forceinline__ float sdiv(float a, float b) { return fin(daz(a) / daz(b)); }
+__device__ __forceinline__ float srcp(float a) { return fin(1.0f / daz(a)); }
+
+// int32 -> f32 RNE (v_cvt_f32_i32 rounds to nearest even).
+__device__ __forceinline__ float i2f(int32_t v) { return (float)v; }
+
+// fp16 bits -> f32, exact for every input; a NaN keeps sign and payload with the quiet bit set
+// (sw/sim/tsr_ref.c:136-160).
+__device__ __forceinline__ float h2f_exact(uint32_t h) {
+    const uint32_t s = (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u;
+    if (e == 31u) return bf(s | 0x7F800000u | (m ? (0x00400000u | (m << 13)) : 0u));
+    if (e == 0u) return bf(s | fb((float)m * 5.9604644775390625e-08f));
+    return bf(s | ((e + 112u) << 23) | (m << 13));
+}
+// fp16 -> f32 by the hardware conversion: exact for every non-NaN input (f16 denormals enabled).
+// Used for weight scales in the hot loops, where any NaN is canonicalized by a later f32 op.
+__device__ __forceinline__ float h2f_fast(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
+}
+
+// f32 -> fp16 bits, RNE, overflow -> Inf, NaN -> sign | 0x7E00 (sw/sim/tsr_ref.c:162-198).
+__device__ __forceinline__ uint32_t f2h_exact(float f) {
+    const uint32_t u = fb(f), s = (u >> 16) & 0x8000u, a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return s | 0x7E00u;
+    if (a == 0x7F800000u) return s | 0x7C00u;
+    const int be = (int)(a >> 23);
+    if (be == 0) return s;
+    const int e = be - 127;
+    if (e > 15) return s | 0x7C00u;
+    if (e < -25) return s;
+    const uint32_t sig = 0x00800000u | (a & 0x007FFFFFu);
+    const uint32_t rs = e >= -14 ? 13u : (uint32_t)(-e - 1);   // 13 .. 24
+    uint32_t q = sig >> rs;
+    const uint32_t rem = sig & ((1u << rs) - 1u), half = 1u << (rs - 1u);
+    if (rem > half || (rem == half && (q & 1u))) q += 1u;
+    const uint32_t out = e >= -14 ? ((uint32_t)(e + 15) << 10) + (q - 1024u) : q;
+    return s | out;
+}
+
+// QACT f32 -> int8: NaN -> 0; |x| >= 256 saturates; else round (half away: A32, half even: A256)
+// and clamp to [-128, 127] (sw/sim/tsr_ref.c:200-232).
+__device__ __forceinline__ int32_t round_away8(float x) {
+    if (__builtin_isnan(x)) return 0;
+    if (__builtin_fabsf(x) >= 256.0f) return x < 0.0f ? -128 : 127;
+    const float t = __builtin_truncf(x);
+    const float fr = x - t;                                   // exact
+    float r = t;
+    if (__builtin_fabsf(fr) >= 0.5f) r = x < 0.0f ? t - 1.0f : t + 1.0f;
+    const int32_t v = (int32_t)r;
+    return v < -128 ? -128 : (v > 127 ? 127 : v);
+}
+__device__ __forceinline__ int32_t round_even8(float x) {
+    if (__builtin_isnan(x)) return 0;
+    if (__builtin_fabsf(x) >= 256.0f) return x < 0.0f ? -128 : 127;
+    const int32_t v = (int32_t)__builtin_rintf(x);            // v_rndne_f32: nearest, ties to even
+    return v < -128 ? -128 : (v > 127 ? 127 : v);
+}
+
+// ---- wave64 exchange ----------------------------------------------------------------------------
+// DPP controls (GCN/CDNA encoding).
+constexpr int kDppXor1 = 0xB1;            // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;            // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <- 7 - i within each 8
+constexpr int kDppRowMirror = 0x140;      // lane i <- 15 - i within each 16
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Lane i <- lane i ^ 16 (within 32-lane halves) and lane i <- lane i ^ 32.
+__device__ __forceinline__ int xor16_i(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x401F); }
+__device__ __forceinline__ float xor16_f(float v) { return __int_as_float(xor16_i(__float_as_int(v))); }
+__device__ __forceinline__ int xor32_i(int v) {
+    return __builtin_amdgcn_ds_bpermute(((int)__lane_id() ^ 32) << 2, v);
+}
+__device__ __forceinline__ float xor32_f(float v) { return __int_as_float(xor32_i(__float_as_int(v))); }
+__device__ __forceinline__ int shfl_i(int v, int src_lane) { return __builtin_amdgcn_ds_bpermute(src_lane << 2, v); }
+__device__ __forceinline__ float shfl_f(float v, int src_lane) { return __int_as_float(shfl_i(__float_as_int(v), src_lane)); }
+
+// Sum over the 8 lanes of an aligned group of 8 (every lane gets the total). Integer: exact in any order.
+__device__ __forceinline__ int sum8_i(int v) {
+    v += dpp_i<kDppXor1>(v);
+    v += dpp_i<kDppXor2>(v);
+    v += dpp_i<kDppRowHalfMirror>(v);
+    return v;
+}
+
+// Byte-wise signed dot product of 4 int8 pairs plus an accumulator (v_dot4_i32_i8).
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+}  // namespace tsr

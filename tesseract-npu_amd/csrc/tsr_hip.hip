@@ -1,0 +1,395 @@
+// tsr_hip.hip -- host side of libtsr_hip: contexts, buffers, the weight layout, argument checks and
+// kernel launches behind the C ABI of include/tsr_hip.h.
+#include "tsr_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <thread>
+#include <vector>
+
+#include "kernels.hpp"
+#include "runtime.hpp"
+
+// ---------------------------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------------------------
+const char * tsr_hip_strerror(int code) {
+    switch (code) {
+        case TSR_HIP_OK: return "ok";
+        case TSR_HIP_E_ARG: return "invalid argument";
+        case TSR_HIP_E_SHAPE: return "unsupported shape";
+        case TSR_HIP_E_NOMEM: return "out of memory";
+        case TSR_HIP_E_HIP: return "HIP runtime error";
+        case TSR_HIP_E_RANGE: return "range beyond the object";
+        case TSR_HIP_E_NODEV: return "no such device";
+        case TSR_HIP_E_FMT: return "unknown weight format or QA kind";
+        case TSR_HIP_E_MASK: return "mask summary malformed or needs the f32 mask copy";
+        default: return "unknown error";
+    }
+}
+
+namespace tsr {
+
+int hip_err(hipError_t e, const char * what) {
+    if (e == hipSuccess) return TSR_HIP_OK;
+    if (getenv("TSR_HIP_DEBUG")) fprintf(stderr, "tsr_hip: %s: %s\n", what, hipGetErrorString(e));
+    return e == hipErrorOutOfMemory ? TSR_HIP_E_NOMEM : TSR_HIP_E_HIP;
+}
+
+}  // namespace tsr
+
+using tsr::hip_err;
+
+// EXPK constants from their definitions (long double: 64-bit significand, exact enough for every
+// rounding here; VU 6.3 fixes LK = round(log2(e) 2^38), c_k = round(ln2^k / k! 2^32),
+// t64[j] = round(2^(j/64) 2^30)).
+void tsr_expk_table(tsr::ExpkTab * t) {
+    const long double ln2 = 0.693147180559945309417232121458176568L;
+    const long double log2e = 1.442695040888963407359924681001892137L;
+    t->lk = (uint64_t)llroundl(ldexpl(log2e, 38));
+    t->c1 = (uint64_t)llroundl(ldexpl(ln2, 32));
+    t->c2 = (uint64_t)llroundl(ldexpl(ln2 * ln2 / 2.0L, 32));
+    t->c3 = (uint64_t)llroundl(ldexpl(ln2 * ln2 * ln2 / 6.0L, 32));
+    for (int j = 0; j < 64; ++j) t->t64[j] = (uint32_t)llroundl(ldexpl(exp2l((long double)j / 64.0L), 30));
+}
+
+// ---------------------------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------------------------
+int tsr_hip_open(int device, tsr_hip_ctx ** out) {
+    if (out == nullptr) return TSR_HIP_E_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return TSR_HIP_E_NODEV;
+    int rc = hip_err(hipSetDevice(device), "hipSetDevice");
+    if (rc) return rc;
+    auto * c = new (std::nothrow) tsr_hip_ctx();
+    if (c == nullptr) return TSR_HIP_E_NOMEM;
+    c->device = device;
+    hipDeviceProp_t p;
+    if ((rc = hip_err(hipGetDeviceProperties(&p, device), "hipGetDeviceProperties")) != 0) { delete c; return rc; }
+    c->n_cu = p.multiProcessorCount;
+    snprintf(c->name, sizeof c->name, "%s", p.gcnArchName);
+    tsr_expk_table(&c->expk);
+    if ((rc = hip_err(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate")) != 0) {
+        delete c;
+        return rc;
+    }
+    *out = c;
+    return TSR_HIP_OK;
+}
+
+int tsr_hip_close(tsr_hip_ctx * ctx) {
+    if (ctx == nullptr) return TSR_HIP_E_ARG;
+    {
+        std::lock_guard<std::mutex> lk(ctx->mtx);
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        ctx->scratch.release();
+        (void)hipStreamDestroy(ctx->stream);
+    }
+    delete ctx;
+    return TSR_HIP_OK;
+}
+
+void * tsr_hip_stream(tsr_hip_ctx * ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int tsr_hip_sync(tsr_hip_ctx * ctx, void * stream) {
+    if (ctx == nullptr) return TSR_HIP_E_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    return hip_err(hipStreamSynchronize(ctx->pick(stream)), "hipStreamSynchronize");
+}
+
+int tsr_hip_device_info(tsr_hip_ctx * ctx, int * n_cu, char * name, size_t name_len, size_t * mem_free,
+                        size_t * mem_total) {
+    if (ctx == nullptr) return TSR_HIP_E_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    if (n_cu) *n_cu = ctx->n_cu;
+    if (name && name_len) snprintf(name, name_len, "%s", ctx->name);
+    if (mem_free || mem_total) {
+        size_t f = 0, t = 0;
+        const int rc = hip_err(hipMemGetInfo(&f, &t), "hipMemGetInfo");
+        if (rc) return rc;
+        if (mem_free) *mem_free = f;
+        if (mem_total) *mem_total = t;
+    }
+    return TSR_HIP_OK;
+}
+
+int tsr_hip_get_counters(tsr_hip_ctx * ctx, tsr_hip_counters * out) {
+    if (ctx == nullptr || out == nullptr) return TSR_HIP_E_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    *out = ctx->ctr;
+    return TSR_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// raw buffers
+// ---------------------------------------------------------------------------------------------
+int tsr_hip_alloc(tsr_hip_ctx * ctx, size_t bytes, void ** dev_out) {
+    if (ctx == nullptr || dev_out == nullptr) return TSR_HIP_E_ARG;
+    *dev_out = nullptr;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    return hip_err(hipMalloc(dev_out, bytes ? bytes : 1u), "hipMalloc");
+}
+
+int tsr_hip_free(tsr_hip_ctx * ctx, void * dev) {
+    if (ctx == nullptr) return TSR_HIP_E_ARG;
+    if (dev == nullptr) return TSR_HIP_OK;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    return hip_err(hipFree(dev), "hipFree");
+}
+
+int tsr_hip_write(tsr_hip_ctx * ctx, void * dst_dev, const void * src, size_t bytes) {
+    if (ctx == nullptr || (bytes && (dst_dev == nullptr || src == nullptr))) return TSR_HIP_E_ARG;
+    if (bytes == 0) return TSR_HIP_OK;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    int rc = hip_err(hipMemcpyAsync(dst_dev, src, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpy H2D");
+    if (rc == 0) rc = hip_err(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return rc;
+}
+
+int tsr_hip_read(tsr_hip_ctx * ctx, void * dst, const void * src_dev, size_t bytes) {
+    if (ctx == nullptr || (bytes && (dst == nullptr || src_dev == nullptr))) return TSR_HIP_E_ARG;
+    if (bytes == 0) return TSR_HIP_OK;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    int rc = hip_err(hipMemcpyAsync(dst, src_dev, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpy D2H");
+    if (rc == 0) rc = hip_err(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return rc;
+}
+
+int tsr_hip_memset(tsr_hip_ctx * ctx, void * dst_dev, int value, size_t bytes) {
+    if (ctx == nullptr || (bytes && dst_dev == nullptr)) return TSR_HIP_E_ARG;
+    if (bytes == 0) return TSR_HIP_OK;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    int rc = hip_err(hipMemsetAsync(dst_dev, value, bytes, ctx->stream), "hipMemset");
+    if (rc == 0) rc = hip_err(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return rc;
+}
+
+// ---------------------------------------------------------------------------------------------
+// weights: ggml blocks <-> device layout (meta region | quant region, both row-contiguous)
+// ---------------------------------------------------------------------------------------------
+namespace {
+
+constexpr uint32_t kKMax = 32768u;
+
+uint32_t blk_values(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 32u : 256u; }
+uint32_t blk_bytes(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 34u : 144u; }
+uint32_t blk_meta(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 2u : 16u; }
+uint32_t blk_quant(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 32u : 128u; }
+
+template <class F>
+void parallel_rows(uint32_t N, F && f) {
+    const uint32_t nt = std::max(1u, std::min<uint32_t>(16u, std::thread::hardware_concurrency()));
+    if (N < 1024u || nt == 1u) { f(0u, N); return; }
+    std::vector<std::thread> th;
+    const uint32_t per = (N + nt - 1u) / nt;
+    for (uint32_t lo = 0; lo < N; lo += per) th.emplace_back(f, lo, std::min(N, lo + per));
+    for (auto & x : th) x.join();
+}
+
+}  // namespace
+
+int tsr_hip_weight_upload(tsr_hip_ctx * ctx, uint32_t fmt, const void * ggml_blocks, uint32_t N, uint32_t K,
+                          tsr_hip_weight ** out) {
+    if (ctx == nullptr || ggml_blocks == nullptr || out == nullptr) return TSR_HIP_E_ARG;
+    *out = nullptr;
+    if (fmt != TSR_HIP_FMT_Q8_0 && fmt != TSR_HIP_FMT_Q4_K) return TSR_HIP_E_FMT;
+    if (N == 0u || K == 0u || K % blk_values(fmt) != 0u || K > kKMax) return TSR_HIP_E_SHAPE;
+    const size_t nb = K / blk_values(fmt);
+    const size_t meta_bytes = (size_t)N * nb * blk_meta(fmt);
+    const size_t quant_off = (meta_bytes + 255u) & ~(size_t)255u;
+    const size_t quant_bytes = (size_t)N * nb * blk_quant(fmt);
+    std::vector<uint8_t> host;
+    try {
+        host.resize(quant_off + quant_bytes);
+    } catch (...) {
+        return TSR_HIP_E_NOMEM;
+    }
+    const uint8_t * src = (const uint8_t *)ggml_blocks;
+    const uint32_t bb = blk_bytes(fmt), bm = blk_meta(fmt), bq = blk_quant(fmt);
+    parallel_rows(N, [&](uint32_t lo, uint32_t hi) {
+        for (size_t r = lo; r < hi; ++r)
+            for (size_t i = 0; i < nb; ++i) {
+                const uint8_t * b = src + (r * nb + i) * bb;
+                memcpy(host.data() + (r * nb + i) * bm, b, bm);
+                memcpy(host.data() + quant_off + (r * nb + i) * bq, b + bm, bq);
+            }
+    });
+    auto * w = new (std::nothrow) tsr_hip_weight();
+    if (w == nullptr) return TSR_HIP_E_NOMEM;
+    w->fmt = fmt;
+    w->N = N;
+    w->K = K;
+    w->quant_off = quant_off;
+    w->bytes = host.size();
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    int rc = hip_err(hipMalloc((void **)&w->dev, w->bytes), "hipMalloc weight");
+    if (rc == 0) rc = hip_err(hipMemcpyAsync(w->dev, host.data(), w->bytes, hipMemcpyHostToDevice, ctx->stream), "weight H2D");
+    if (rc == 0) rc = hip_err(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (rc != 0) {
+        if (w->dev) (void)hipFree(w->dev);
+        delete w;
+        return rc;
+    }
+    *out = w;
+    return TSR_HIP_OK;
+}
+
+int tsr_hip_weight_read(tsr_hip_ctx * ctx, const tsr_hip_weight * w, void * ggml_blocks) {
+    if (ctx == nullptr || w == nullptr || ggml_blocks == nullptr) return TSR_HIP_E_ARG;
+    std::vector<uint8_t> host(w->bytes);
+    {
+        std::lock_guard<std::mutex> lk(ctx->mtx);
+        (void)hipSetDevice(ctx->device);
+        int rc = hip_err(hipMemcpyAsync(host.data(), w->dev, w->bytes, hipMemcpyDeviceToHost, ctx->stream), "weight D2H");
+        if (rc == 0) rc = hip_err(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        if (rc) return rc;
+    }
+    const size_t nb = w->K / blk_values(w->fmt);
+    const uint32_t bb = blk_bytes(w->fmt), bm = blk_meta(w->fmt), bq = blk_quant(w->fmt);
+    uint8_t * dst = (uint8_t *)ggml_blocks;
+    parallel_rows(w->N, [&](uint32_t lo, uint32_t hi) {
+        for (size_t r = lo; r < hi; ++r)
+            for (size_t i = 0; i < nb; ++i) {
+                uint8_t * b = dst + (r * nb + i) * bb;
+                memcpy(b, host.data() + (r * nb + i) * bm, bm);
+                memcpy(b + bm, host.data() + w->quant_off + (r * nb + i) * bq, bq);
+            }
+    });
+    return TSR_HIP_OK;
+}
+
+int tsr_hip_weight_free(tsr_hip_ctx * ctx, tsr_hip_weight * w) {
+    if (ctx == nullptr) return TSR_HIP_E_ARG;
+    if (w == nullptr) return TSR_HIP_OK;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    const int rc = hip_err(hipFree(w->dev), "hipFree weight");
+    delete w;
+    return rc;
+}
+
+int tsr_hip_weight_info(const tsr_hip_weight * w, uint32_t * fmt, uint32_t * N, uint32_t * K, size_t * dev_bytes) {
+    if (w == nullptr) return TSR_HIP_E_ARG;
+    if (fmt) *fmt = w->fmt;
+    if (N) *N = w->N;
+    if (K) *K = w->K;
+    if (dev_bytes) *dev_bytes = w->bytes;
+    return TSR_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// QACT
+// ---------------------------------------------------------------------------------------------
+size_t tsr_hip_qa_bytes(uint32_t kind, uint32_t K) {
+    if (kind > 1u) return 0;
+    const uint32_t bs = kind == 0u ? 32u : 256u;
+    size_t n = (K + 63u) / 64u * 64u + (4u * (K / bs) + 63u) / 64u * 64u;
+    if (kind == 1u) n += (2u * (K / 16u) + 63u) / 64u * 64u;
+    return n;
+}
+
+static bool aligned16(const void * p) { return ((uintptr_t)p & 15u) == 0u; }
+
+int tsr_hip_qact(tsr_hip_ctx * ctx, uint32_t kind, const float * x_dev, uint32_t K, uint32_t T, uint64_t x_stride,
+                 uint8_t * qa_dev, void * stream) {
+    if (ctx == nullptr || x_dev == nullptr || qa_dev == nullptr || T == 0u) return TSR_HIP_E_ARG;
+    if (kind > 1u) return TSR_HIP_E_FMT;
+    const uint32_t bs = kind == 0u ? 32u : 256u;
+    if (K == 0u || K % bs != 0u || K > kKMax) return TSR_HIP_E_SHAPE;
+    if (!aligned16(x_dev) || (T > 1u && x_stride % 4u != 0u) || T > 65535u) return TSR_HIP_E_ARG;
+    tsr::QactArgs a{};
+    a.x = x_dev;
+    a.x_stride = x_stride;
+    a.qa = qa_dev;
+    a.qa_bytes = (uint32_t)tsr_hip_qa_bytes(kind, K);
+    a.K = K;
+    a.kind = kind;
+    a.d_off = (K + 63u) / 64u * 64u;
+    a.bs_off = a.d_off + (4u * (K / bs) + 63u) / 64u * 64u;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    ctx->ctr.qact_calls++;
+    return tsr_launch_qact(a, T, ctx->pick(stream));
+}
+
+// ---------------------------------------------------------------------------------------------
+// MUL_MAT
+// ---------------------------------------------------------------------------------------------
+static int mul_mat_common(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T,
+                          uint64_t x_stride, float * y_dev, uint64_t y_stride, const float * add_dev,
+                          uint64_t add_stride, uint32_t flags, int32_t * isums, void * stream) {
+    if (ctx == nullptr || w == nullptr || x_dev == nullptr || y_dev == nullptr || T == 0u) return TSR_HIP_E_ARG;
+    if ((flags & ~TSR_HIP_MM_ACC_DST) != 0u || (add_dev != nullptr && (flags & TSR_HIP_MM_ACC_DST))) return TSR_HIP_E_ARG;
+    if (!aligned16(x_dev) || (T > 1u && x_stride % 4u != 0u)) return TSR_HIP_E_ARG;
+    if (T > 1u && (x_stride < w->K || y_stride < w->N)) return TSR_HIP_E_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    hipStream_t s = ctx->pick(stream);
+    tsr::MvArgs a{};
+    const size_t nb = w->K / blk_values(w->fmt);
+    a.wm = w->dev;
+    a.wq = w->dev + w->quant_off;
+    a.x = x_dev;
+    a.x_stride = x_stride;
+    a.y = y_dev;
+    a.y_stride = y_stride;
+    a.add = add_dev;
+    a.add_stride = add_stride;
+    a.isums = isums;
+    a.N = w->N;
+    a.K = w->K;
+    a.acc = (flags & TSR_HIP_MM_ACC_DST) ? 1u : 0u;
+    ctx->ctr.mul_mat_calls++;
+    ctx->ctr.mul_mat_rows += (uint64_t)w->N * T;
+    ctx->ctr.mul_mat_weight_bytes += (uint64_t)w->N * nb * blk_bytes(w->fmt);
+    for (uint32_t t0 = 0; t0 < T; t0 += 65535u) {
+        const uint32_t tt = std::min(T - t0, 65535u);
+        a.x = x_dev + (size_t)t0 * x_stride;
+        a.y = y_dev + (size_t)t0 * y_stride;
+        a.add = add_dev ? add_dev + (size_t)t0 * add_stride : nullptr;
+        a.T = tt;
+        const int rc = w->fmt == TSR_HIP_FMT_Q8_0 ? tsr_launch_mv_q8_0(a, s) : tsr_launch_mv_q4_k(a, s);
+        if (rc) return rc == -2 ? TSR_HIP_E_SHAPE : TSR_HIP_E_HIP;
+    }
+    return TSR_HIP_OK;
+}
+
+int tsr_hip_mul_mat(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T, uint64_t x_stride,
+                    float * y_dev, uint64_t y_stride, const float * add_dev, uint64_t add_stride, uint32_t flags,
+                    void * stream) {
+    return mul_mat_common(ctx, w, x_dev, T, x_stride, y_dev, y_stride, add_dev, add_stride, flags, nullptr, stream);
+}
+
+int tsr_hip_mul_mat_isums(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, int32_t * isums_dev,
+                          void * stream) {
+    if (isums_dev == nullptr || w == nullptr) return TSR_HIP_E_ARG;
+    // y goes to scratch: the integer sums are the product of this call
+    float * y = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(ctx->mtx);
+        (void)hipSetDevice(ctx->device);
+        const int rc = ctx->scratch.reserve(ctx, (size_t)w->N * sizeof(float));
+        if (rc) return rc;
+        y = (float *)ctx->scratch.ptr;
+    }
+    return mul_mat_common(ctx, w, x_dev, 1u, w->K, y, w->N, nullptr, 0u, 0u, isums_dev, stream);
+}

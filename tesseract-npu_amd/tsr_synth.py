@@ -6,7 +6,7 @@ time, sw/ggml-tesseract/tsr-weights.cpp:33-49) and its test models with a Q4_K e
 carries its own:
 
 * ``normal(seed, n, std)``: counter-based SplitMix64 -> two uniforms -> Box-Muller in float64, rounded
-  to float32. Every value depends only on (seed, index), so CPU and GPU harnesses draw identical bits.
+  to float32 (C helper synth/tsr_synth.c). Every value depends only on (seed, index).
 * ``quantize_q8_0``: d = amax / 127 in f32, q = round-half-away(x / d ... as x * (1/d)), fp16(d) -- the
   rule of quantize_row_q8_0_ref, which is also QACT A32's (sw/sim/tsr_ref.c:472-487).
 * ``quantize_q4_k``: per 32-value sub-block an affine step/min, 6-bit scales and mins packed as ggml's
@@ -17,35 +17,29 @@ from __future__ import annotations
 
 import numpy as np
 
+import ctypes as _C
+import os as _os
+
 _M64 = (1 << 64) - 1
-_GOLD = np.uint64(0x9E3779B97F4A7C15)
-_MIX1 = np.uint64(0xBF58476D1CE4E5B9)
-_MIX2 = np.uint64(0x94D049BB133111EB)
+_LIB = None
 
 
-def _splitmix(seed: int, start: int, n: int) -> np.ndarray:
-    idx = np.arange(start, start + n, dtype=np.uint64)
-    with np.errstate(over="ignore"):
-        z = np.uint64(seed & _M64) + (idx + np.uint64(1)) * _GOLD
-        z = (z ^ (z >> np.uint64(30))) * _MIX1
-        z = (z ^ (z >> np.uint64(27))) * _MIX2
-        z = z ^ (z >> np.uint64(31))
-    return z
+def _lib():
+    global _LIB
+    if _LIB is None:
+        path = _os.path.join(_os.path.dirname(_os.path.abspath(__file__)), "libtsr_synth.so")
+        if not _os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built: run `make -C {_os.path.dirname(path)}`")
+        _LIB = _C.CDLL(path)
+        _LIB.tsr_synth_normal.argtypes = [_C.c_uint64, _C.c_uint64, _C.c_uint64, _C.c_float, _C.c_void_p]
+    return _LIB
 
 
-def uniform(seed: int, n: int, start: int = 0) -> np.ndarray:
-    """n float64 uniforms in [0, 1) (53-bit)."""
-    return (_splitmix(seed, start, n) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
-
-
-def normal(seed: int, n: int, std: float = 1.0, chunk: int = 1 << 24) -> np.ndarray:
-    """n float32 values ~ N(0, std^2); value i uses uniforms 2i and 2i+1 of the seed's stream."""
+def normal(seed: int, n: int, std: float = 1.0, start: int = 0) -> np.ndarray:
+    """n float32 values ~ N(0, std^2): value i uses uniforms 2i and 2i+1 of the seed's SplitMix64
+    stream (synth/tsr_synth.c). Values depend only on (seed, index)."""
     out = np.empty(n, np.float32)
-    for s in range(0, n, chunk):
-        m = min(chunk, n - s)
-        u = uniform(seed, 2 * m, 2 * s).reshape(m, 2)
-        r = np.sqrt(-2.0 * np.log1p(-u[:, 0]))
-        out[s:s + m] = (r * np.cos(2.0 * np.pi * u[:, 1]) * std).astype(np.float32)
+    _lib().tsr_synth_normal(seed & _M64, start, n, std, out.ctypes.data)
     return out
 
 

@@ -90,6 +90,72 @@ def cpu_baseline(blocks_up, x, seconds: float = 10.0) -> dict:
             "sample": f"{n} x Q4_K matvec 14336x4096 (oracle/oc_num.c, {threads} threads), {per * 1e3:.1f} ms each"}
 
 
+def extra_workloads(dev, ev, stream, n: int) -> dict:
+    """The other single-GPU BASELINE configs, each timed over rotating device copies (> 2x MALL):
+    configs[0] Q8_0 matvec 4864x896 and configs[2] q8-KV flash-decode (32 q / 8 KV heads, D 128,
+    n_kv 8192, batch 1). Per-call time from HIP events on the launch stream."""
+    out = {}
+    n = max(n, 100)
+
+    def timed(fn):
+        a, b = ev.event(), ev.event()
+        for i in range(5):
+            fn(i)
+        ev.record(a, stream)
+        for i in range(n):
+            fn(i)
+        ev.record(b, stream)
+        return ev.elapsed_ms(a, b) / n
+
+    # configs[0]: Q8_0 4864 x 896
+    N, K = 4864, 896
+    blocks = S.quantize_q8_0(S.normal(S.seed_of("cfg1", "w"), N * K, 0.02).reshape(N, K))
+    per = blocks.nbytes
+    copies = -(-2 * MALL_BYTES // per)
+    ws = [dev.weight(0, blocks, N, K) for _ in range(copies)]
+    xb = dev.upload(S.normal(S.seed_of("cfg1", "x"), K))
+    yb = dev.alloc(4 * N)
+    ms = timed(lambda i: dev.mul_mat(ws[i % copies], xb, 1, K, yb, N, stream=stream))
+    nbytes = N * (K // 32) * 34 + 4 * K + 4 * N
+    out["q8_0_matvec_4864x896"] = {"us_per_call": round(ms * 1e3, 3), "algorithmic_bytes": nbytes,
+                                   "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                   "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                   "copies": copies}
+    del ws
+
+    # configs[2]: flash-decode over a q8_0 KV cache
+    n_head, n_kv_head, D, n_kv = 32, 8, 128, 8192
+    E = n_kv_head * D
+    kf = dev.upload(S.normal(S.seed_of("cfg3", "k"), n_kv * E))
+    vf = dev.upload(S.normal(S.seed_of("cfg3", "v"), n_kv * E))
+    idx = dev.upload(np.arange(n_kv, dtype=np.int64))
+    k0, v0 = dev.kv(E, n_kv), dev.kv(E, n_kv)
+    dev.kv_set_rows(k0, 0, kf, n_kv, E, idx)
+    dev.kv_set_rows(v0, 1, vf, n_kv, E, idx)
+    kimg, vimg = k0.get_bytes(0), v0.get_bytes(1)
+    per = kimg.nbytes + vimg.nbytes
+    copies = max(2, -(-2 * MALL_BYTES // per))
+    caches = [(k0, v0)]
+    for _ in range(copies - 1):
+        kc, vc = dev.kv(E, n_kv), dev.kv(E, n_kv)
+        kc.set_bytes(0, kimg)
+        vc.set_bytes(1, vimg)
+        caches.append((kc, vc))
+    q = S.normal(S.seed_of("cfg3", "q"), n_head * D).astype(np.float16).astype(np.float32)
+    qb = dev.upload(q)
+    ob = dev.alloc(4 * n_head * D)
+    msum = tsr_hip.msum_build_f16(np.zeros((1, n_kv), np.float16))
+    scale = np.float32(1.0 / np.sqrt(D))
+    ms = timed(lambda i: dev.flash_attn(qb, 1, n_head * D, caches[i % copies][0], caches[i % copies][1], D,
+                                        n_head, n_kv_head, scale, msum, ob, n_head * D, stream=stream))
+    nbytes = 2 * n_kv * E // 32 * 34 + 2 * n_head * D + 4 * n_head * D
+    out["fa_decode_q8kv_8192_32q8kv_d128"] = {"us_per_call": round(ms * 1e3, 3), "algorithmic_bytes": nbytes,
+                                              "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                              "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                              "copies": copies, "launches_per_call": 4}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -97,6 +163,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--copies", type=int, default=0, help="distinct weight copies (0: enough for 2x MALL)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is a "
@@ -161,6 +228,7 @@ def main() -> int:
         print(json.dumps({"error": "non-finite output"}))
         return 1
 
+    also = {} if args.no_extra else extra_workloads(dev, ev, stream, args.steps)
     cpu = None if args.no_cpu else cpu_baseline(up_blocks, x)
     out = {
         "metric": METRIC,
@@ -184,6 +252,7 @@ def main() -> int:
                      "other_kernels": {n: {"launch_us": round(t * 1e3, 3), "GB/s": round(b / (t * 1e-3) / 1e9, 1)}
                                        for n, t, b in kern}},
         "cpu_baseline": cpu,
+        "also": also,
     }
     print(json.dumps(out))
     dev.close()

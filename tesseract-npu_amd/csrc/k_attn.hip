@@ -9,18 +9,19 @@
 // (AMERGE), and finally O / l (ANORM). On the GPU the chunks of a token and the channels of a chunk
 // are independent until the merge, so they run as parallel workgroups (split-K); only the f32 steps
 // that the reference orders are kept in its order:
-//   k_fa_qk     scores of a 256-cell tile of one chunk for the query heads of one KV head, and the
-//               tile's maxima (MAXT is an order-free total-order maximum)
-//   k_fa_pv     one (chunk, channel, KV head, 64-value slice): EXP, block float per segment, the
-//               f32 segment sums in segment order, the segment row-sums (LSUM)
-//   k_fa_merge  one (token, head): CTREE of the channels, the online merge in chunk order, ANORM
+//   k_fa_qk     QACT of the query heads, scores of a 256-cell tile of one chunk for the query heads
+//               of one KV head, and the tile's maxima (MAXT is an order-free total-order maximum)
+//   k_fa_pv     one (chunk, channel, KV head, 64-value slice): EXP, block float per segment, the f32
+//               segment sums in segment order, the segment row-sums (LSUM)
+//   k_fa_merge  one (token, KV head, slice): CTREE of the channels, the online merge in chunk order,
+//               ANORM
 //
 // Block float (AT 6.4; sw/sim/tsr_ref_at.c:380-488): in a segment every weight w = p dV is scaled
 // to an integer W = RNE(w 2^(23 - E_S)) (|W| <= 2^24) and A = sum W q is exact. W is split into four
 // balanced base-256 digits d_k in [-128, 127] (W = sum d_k 256^k), so A = sum_k 256^k (sum d_k q)
 // runs on v_dot4_i32_i8 with exact int32 partial sums (|sum| <= 64 * 128 * 128).
 #include "kernels.hpp"
-#include "tsr_dev.hpp"
+#include "qact.hpp"
 
 namespace tsr {
 
@@ -69,20 +70,36 @@ __device__ __forceinline__ float maxt(float a, float b) {
     if ((ua & 0x7FFFFFFFu) > 0x7F800000u || (ub & 0x7FFFFFFFu) > 0x7F800000u) return bf(kNaN);
     return maxt_key(ua) >= maxt_key(ub) ? bf(ua) : bf(ub);
 }
-__device__ __forceinline__ float wave_maxt(float v) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v = maxt(v, shfl_f(v, (int)__lane_id() ^ off));
-    return v;
+// Order-preserving key of MAXT's total order (DAZ applied; NaN above everything; -0 < +0).
+__device__ __forceinline__ uint32_t maxt_key_f(float v) {
+    const uint32_t u = fb(daz(v));
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0xFFFFFFFFu;
+    return (u >> 31) ? ~u : (u | 0x80000000u);
 }
-__device__ __forceinline__ int wave_max_i(int v) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) { const int o = shfl_i(v, (int)__lane_id() ^ off); v = o > v ? o : v; }
-    return v;
+__device__ __forceinline__ float maxt_unkey(uint32_t k) {
+    if (k == 0xFFFFFFFFu) return bf(kNaN);
+    return bf((k >> 31) ? (k & 0x7FFFFFFFu) : ~k);
+}
+// Wave-wide max / sum with DPP inside rows, a swizzle across the halves and two readlanes (every
+// lane of the wave must be active).
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+    v = umax_u(v, (uint32_t)dpp_i<kDppXor1>((int)v));
+    v = umax_u(v, (uint32_t)dpp_i<kDppXor2>((int)v));
+    v = umax_u(v, (uint32_t)dpp_i<kDppRowHalfMirror>((int)v));
+    v = umax_u(v, (uint32_t)dpp_i<kDppRowMirror>((int)v));
+    v = umax_u(v, (uint32_t)xor16_i((int)v));
+    return umax_u((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 32));
+}
+__device__ __forceinline__ int wave_max_i(int v) {   // via the order-preserving unsigned map
+    return (int)(wave_max_u((uint32_t)v ^ 0x80000000u) ^ 0x80000000u);
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v += shfl_i(v, (int)__lane_id() ^ off);
-    return v;
+    v += dpp_i<kDppXor1>(v);
+    v += dpp_i<kDppXor2>(v);
+    v += dpp_i<kDppRowHalfMirror>(v);
+    v += dpp_i<kDppRowMirror>(v);
+    v += xor16_i(v);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
 }
 
 // RNE_int(w 2^(23 - es)), exponent(w) <= es; zero / subnormal w -> 0 (sw/sim/tsr_ref_at.c:386-410).
@@ -124,32 +141,54 @@ __device__ __forceinline__ float bf_f(int64_t A, int32_t k) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// scores: block (tile, KV head g); thread = one cell of the tile
+// scores: block (tile, KV head g), thread = one cell of the tile. The block quantizes the query
+// values of the KV head's G heads (QACT A32: its 32-blocks never cross a head, so they are the
+// blocks of the whole query row) while the K rows of its cells load.
 // ---------------------------------------------------------------------------------------------
+template <int D>
 __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
+    constexpr uint32_t NBD = D / 32u;                             // blocks per head
+    constexpr bool KREG = D <= 128;                                // K row of the cell kept in registers
     const FaTile tl = a.tiles[blockIdx.x];
     const FaItem it = a.items[tl.item];
-    const uint32_t g = blockIdx.y, G = a.G, D = a.D, nbd = D / 32u;
+    const uint32_t g = blockIdx.y, G = a.G;
     int8_t * s_q = (int8_t *)lds;                                 // G*D quants of the KV head's query heads
     float * s_dx = (float *)(lds + G * D);                        // G*D/32 scales
-    float * s_red = s_dx + G * nbd;                               // 4 waves x G maxima
-    const uint8_t * qa = a.qa + (size_t)it.t * a.qa_bytes;
-    for (uint32_t i = threadIdx.x; i < G * D / 16u; i += blockDim.x)
-        ((uint4 *)s_q)[i] = ((const uint4 *)(qa + (size_t)g * G * D))[i];
-    for (uint32_t i = threadIdx.x; i < G * nbd; i += blockDim.x)
-        s_dx[i] = ((const float *)(qa + a.qa_d_off))[(size_t)g * G * nbd + i];
-    __syncthreads();
+    uint32_t * s_red = (uint32_t *)(s_dx + G * NBD);              // 4 waves x G maxima (keys)
+    const int lane = (int)__lane_id(), wave = (int)(threadIdx.x >> 6);
 
     const uint32_t n16 = 16u * it.n, j = tl.c0 + threadIdx.x;
     const bool in = j < n16;
-    const uint32_t cell = 16u * it.u0 + j, u = cell >> 4, rr = cell & 15u;
+    const uint32_t cell = 16u * it.u0 + j;
+    const uint32_t ng = (a.kc.kv_size + 15u) / 16u;
+    const uint32_t u = min(cell >> 4, ng - 1u), rr = cell & 15u;  // clamped: loads stay inside the plane
     const bool vis = in && (it.general || (j >= it.c_lo && j < it.c_hi));
     const uint32_t E = a.E, nbk = E / 32u;
-    const uint16_t * kmeta = (const uint16_t *)a.kc.base + ((size_t)u * 16u + rr) * nbk + (size_t)g * nbd;
+    const uint16_t * kmeta = (const uint16_t *)a.kc.base + ((size_t)u * 16u + rr) * nbk + (size_t)g * NBD;
     const uint8_t * kq = a.kc.base + a.kc.quant_off + (size_t)u * 16u * E + (size_t)rr * 16u;
+    const uint32_t ci0 = g * D / 16u;                             // first 16-byte chunk of the head
+
+    int4 kr[KREG ? 2 * NBD : 1];
+    uint32_t km[NBD];
+#pragma unroll
+    for (uint32_t kb = 0; kb < NBD; ++kb) km[kb] = kmeta[kb];
+    if constexpr (KREG) {
+#pragma unroll
+        for (uint32_t c = 0; c < 2 * NBD; ++c) kr[c] = *(const int4 *)(kq + (size_t)(ci0 + c) * 256u);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    const float * qrow = a.q + (size_t)it.t * a.q_stride + (size_t)g * G * D;
+    for (uint32_t slot = threadIdx.x; slot < G * D / 4u; slot += blockDim.x) {   // 8 lanes per 32-block
+        float Dq;
+        const uint32_t qv = qact_a32_lane(*(const float4 *)(qrow + 4u * slot), &Dq);
+        *(uint32_t *)(s_q + 4u * slot) = qv;
+        if ((lane & 7) == 0) s_dx[slot >> 3] = Dq;
+    }
+    __syncthreads();
+
     float * S = a.S + (size_t)it.s_off * a.n_head;
-    const int lane = (int)__lane_id(), wave = (int)(threadIdx.x >> 6);
     for (uint32_t i = 0; i < G; ++i) {
         const uint32_t h = g * G + i;
         float s = bf(kNegInf);
@@ -157,10 +196,14 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a) {
             float p[16];
 #pragma unroll
             for (int k = 0; k < 16; ++k) p[k] = 0.0f;
-            for (uint32_t kb = 0; kb < nbd; ++kb) {
-                const uint32_t ci = (g * D + 32u * kb) >> 4;      // first 16-byte chunk of the block
-                const int4 w0 = *(const int4 *)(kq + (size_t)ci * 256u);
-                const int4 w1 = *(const int4 *)(kq + (size_t)(ci + 1u) * 256u);
+#pragma unroll
+            for (uint32_t kb = 0; kb < NBD; ++kb) {
+                int4 w0, w1;
+                if constexpr (KREG) { w0 = kr[2 * kb]; w1 = kr[2 * kb + 1]; }
+                else {
+                    w0 = *(const int4 *)(kq + (size_t)(ci0 + 2 * kb) * 256u);
+                    w1 = *(const int4 *)(kq + (size_t)(ci0 + 2 * kb + 1) * 256u);
+                }
                 const int4 * xq = (const int4 *)(s_q + (size_t)i * D + 32u * kb);
                 const int4 x0 = xq[0], x1 = xq[1];
                 int is = dot4(w0.x, x0.x, 0);
@@ -171,10 +214,11 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a) {
                 is = dot4(w1.y, x1.y, is);
                 is = dot4(w1.z, x1.z, is);
                 is = dot4(w1.w, x1.w, is);
-                const float t = (h2f_fast(kmeta[kb]) * s_dx[i * nbd + kb]) * (float)is;
+                // SEG (AT 6.2): p_k = +0 + (dK Dx) f32(isum); |terms| >= 2^-48 or 0 (fp16 scales), so
+                // the plain operations never meet a subnormal; NaN is canonicalized below
+                const float t = (h2f_fast(km[kb]) * s_dx[i * NBD + kb]) * (float)is;
                 p[kb] = 0.0f + t;
             }
-            // tree16 of the segment's partials (k >= D/32 stay +0)
 #pragma unroll
             for (int w = 16; w > 1; w >>= 1)
 #pragma unroll
@@ -186,73 +230,90 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a) {
             }
         }
         if (in) S[(size_t)h * n16 + j] = s;
-        float mx = wave_maxt(in ? s : bf(kMFloor));
-        if (lane == 0) s_red[wave * G + i] = mx;
+        const uint32_t mk = wave_max_u(in ? maxt_key_f(s) : maxt_key_f(bf(kMFloor)));
+        if (lane == 0) s_red[wave * G + i] = mk;
     }
     __syncthreads();
-    if (threadIdx.x < G) {
-        float m = s_red[threadIdx.x];
-        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = maxt(m, s_red[w * G + threadIdx.x]);
-        a.Mpart[(size_t)blockIdx.x * a.n_head + g * G + threadIdx.x] = m;
+    for (uint32_t i = threadIdx.x; i < G; i += blockDim.x) {
+        uint32_t m = s_red[i];
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = umax_u(m, s_red[w * G + i]);
+        a.Mpart[(size_t)blockIdx.x * a.n_head + g * G + i] = maxt_unkey(m);
     }
 }
 
 // ---------------------------------------------------------------------------------------------
-// P.V: block (item * 4 + channel, KV head g, slice); wave = one query head at a time
+// P.V and the merge: block (item * 4 + channel c, KV head g, slice sl), 16 waves.
+// A unit is (segment, head): lane = cell for EXP, the block-float weights and LSUM, then lane =
+// value of the 64-value slice for the exact sum A = sum W q on v_dot4 over the base-256 digits.
+// The per-segment results go to LDS; the f32 segment chain then runs in segment order.
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_fa_pv(FaArgs a) {
-    __shared__ __align__(16) int8_t s_dig[4][2][4][64];           // wave, block e, digit, cell
+constexpr int kHB = 16;                                           // heads per LDS batch
+constexpr int kMaxSeg = 8;                                        // NCG <= 128 -> <= 32 groups per channel
+
+__device__ __forceinline__ float ctree4(float x0, float x1, float x2, float x3) { return sadd(sadd(x0, x1), sadd(x2, x3)); }
+
+__global__ __launch_bounds__(1024) void k_fa_pv(FaArgs a) {
+    __shared__ __align__(16) int8_t s_dig[16][2][4][64];          // wave, block e, digit, cell
+    __shared__ float s_c[kMaxSeg][kHB][64];
+    __shared__ float s_l[kMaxSeg][kHB];
+    __shared__ float s_m[64];
     const uint32_t item = blockIdx.x >> 2, c = blockIdx.x & 3u, g = blockIdx.y, sl = blockIdx.z;
     const FaItem it = a.items[item];
-    const uint32_t G = a.G, D = a.D, E = a.E, n16 = 16u * it.n, nbk = E / 32u;
+    const uint32_t G = a.G, D = a.D, E = a.E, n16 = 16u * it.n, nbk = E / 32u, nh = a.n_head, nsl = D / 64u;
     const int lane = (int)__lane_id(), wave = (int)(threadIdx.x >> 6), nw = (int)(blockDim.x >> 6);
     const uint32_t u_first = it.u0 + ((c + 4u - (it.u0 & 3u)) & 3u);
     const uint32_t u_end = it.u0 + it.n;
     const uint32_t nu = u_first < u_end ? (u_end - 1u - u_first) / 4u + 1u : 0u;
     const uint32_t nseg = (nu + 3u) / 4u;
-    const uint32_t sa = g * (D / 64u) + sl;                       // slice of the cell row
+    const uint32_t sa = g * nsl + sl;                             // slice of the cell row
     const uint32_t d = 64u * sa + (uint32_t)lane;                 // this lane's value in the cell row
     const int e_l = lane >> 5;
-    const float * S = a.S + (size_t)it.s_off * a.n_head;
+    const float * S = a.S + (size_t)it.s_off * nh;
     const uint16_t * vmeta = (const uint16_t *)a.vc.base;
     const uint8_t * vq = a.vc.base + a.vc.quant_off;
 
-    for (uint32_t i = (uint32_t)wave; i < G; i += (uint32_t)nw) {
-        const uint32_t h = g * G + i;
+    for (uint32_t i = threadIdx.x; i < G; i += blockDim.x) {      // chunk maxima (MAXOUT over the tiles)
         float m = bf(kMFloor);
-        for (uint32_t tt = 0; tt < it.ntiles; ++tt) m = maxt(m, a.Mpart[(size_t)(it.tile0 + tt) * a.n_head + h]);
-        if (c == 0u && sl == 0u && lane == 0) a.MK[(size_t)item * a.n_head + h] = m;
-        float O = 0.0f, l = 0.0f;
-        for (uint32_t sg = 0; sg < nseg; ++sg) {
-            // --- lane = cell k of the segment -----------------------------------------------
-            const uint32_t grp = 4u * sg + ((uint32_t)lane >> 4);
+        for (uint32_t tt = 0; tt < it.ntiles; ++tt) m = maxt(m, a.Mpart[(size_t)(it.tile0 + tt) * nh + g * G + i]);
+        s_m[i] = m;
+    }
+    __syncthreads();
+
+    for (uint32_t hb0 = 0; hb0 < G; hb0 += kHB) {
+        const uint32_t hbn = min((uint32_t)kHB, G - hb0), units = nseg * hbn;
+        for (uint32_t unit = (uint32_t)wave; unit < units; unit += (uint32_t)nw) {
+            const uint32_t seg = unit / hbn, hi = unit % hbn, h = g * G + hb0 + hi;
+            const float m = s_m[hb0 + hi];
+            const uint32_t ngr = min(nu - 4u * seg, 4u);
+            // loads first: V quants of the slice (lane = value) and, lane = cell, score and V scales
+            int4 vqd[4];
+#pragma unroll
+            for (uint32_t gi = 0; gi < 4; ++gi) {
+                const uint32_t ug = u_first + 4u * (4u * seg + min(gi, ngr - 1u));
+                vqd[gi] = *(const int4 *)(vq + (size_t)ug * 16u * E + (size_t)d * 16u);
+            }
+            const uint32_t grp = 4u * seg + ((uint32_t)lane >> 4);
             const bool cv = grp < nu;
-            const uint32_t u = u_first + 4u * grp, rr = (uint32_t)lane & 15u;
-            float p = 0.0f;
-            if (cv) p = expk(smul(ssub(S[(size_t)h * n16 + 16u * (u - it.u0) + rr], m), a.scale), a.ex);
+            const uint32_t u = u_first + 4u * min(grp, nu - 1u), rr = (uint32_t)lane & 15u;
+            const float sv = S[(size_t)h * n16 + 16u * (u - it.u0) + rr];
+            const uint32_t mv = *(const uint32_t *)(vmeta + ((size_t)u * 16u + rr) * nbk + 2u * sa);
+            // --- lane = cell k of the segment ---------------------------------------------
+            const float p = cv ? expk(smul(ssub(sv, m), a.scale), a.ex) : 0.0f;
             const float pz = daz(p);
             const bool live = cv && (fb(pz) & 0x7FFFFFFFu) != 0u;
-            float w0 = 0.0f, w1 = 0.0f;
-            if (live) {
-                const uint16_t * mv = vmeta + ((size_t)u * 16u + rr) * nbk + 2u * sa;
-                w0 = smul(p, h2f_exact(mv[0]));
-                w1 = smul(p, h2f_exact(mv[1]));
-            }
-            const bool nf0 = live && (fb(w0) & 0x7F800000u) == 0x7F800000u;
-            const bool nf1 = live && (fb(w1) & 0x7F800000u) == 0x7F800000u;
-            const bool bad0 = __any(nf0), bad1 = __any(nf1);
+            const float w0 = live ? smul(p, h2f_exact(mv & 0xFFFFu)) : 0.0f;
+            const float w1 = live ? smul(p, h2f_exact(mv >> 16)) : 0.0f;
+            const bool nf0 = (fb(w0) & 0x7F800000u) == 0x7F800000u;
+            const bool nf1 = (fb(w1) & 0x7F800000u) == 0x7F800000u;
+            const bool bad0 = __ballot(nf0) != 0ull, bad1 = __ballot(nf1) != 0ull;
             int ex = -1000;
-            if (live && !nf0 && (fb(w0) & 0x7FFFFFFFu)) ex = (int)((fb(w0) >> 23) & 0xFFu) - 127;
-            if (live && !nf1 && (fb(w1) & 0x7FFFFFFFu)) { const int e1 = (int)((fb(w1) >> 23) & 0xFFu) - 127; ex = e1 > ex ? e1 : ex; }
+            if (!nf0 && (fb(w0) & 0x7FFFFFFFu)) ex = (int)((fb(w0) >> 23) & 0xFFu) - 127;
+            if (!nf1 && (fb(w1) & 0x7FFFFFFFu)) ex = max(ex, (int)((fb(w1) >> 23) & 0xFFu) - 127);
             const int es = wave_max_i(ex);
             const bool any = es > -1000;
-            int32_t W0 = 0, W1 = 0;
-            if (any && live) {
-                if (!bad0 && !nf0) W0 = bf_int(w0, es);
-                if (!bad1 && !nf1) W1 = bf_int(w1, es);
-            }
-            // balanced base-256 digits of W0, W1 -> LDS
-            int32_t r0 = W0, r1 = W1;
+            const int32_t W0 = (any && !bad0) ? bf_int(w0, es) : 0;
+            const int32_t W1 = (any && !bad1) ? bf_int(w1, es) : 0;
+            int32_t r0 = W0, r1 = W1;                               // balanced base-256 digits
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const int32_t d0 = ((r0 + 128) & 255) - 128, d1 = ((r1 + 128) & 255) - 128;
@@ -261,98 +322,140 @@ __global__ __launch_bounds__(256) void k_fa_pv(FaArgs a) {
                 r0 = (r0 - d0) >> 8;
                 r1 = (r1 - d1) >> 8;
             }
-            if (sl == 0u) {                                        // LSUM of the segment (AT 6.5)
-                const bool pnf = cv && (fb(pz) & 0x7F800000u) == 0x7F800000u;
-                const bool badl = __any(pnf);
-                int ep = -1000;
-                if (cv && !pnf && (fb(pz) & 0x7FFFFFFFu)) ep = (int)((fb(pz) >> 23) & 0xFFu) - 127;
-                ep = wave_max_i(ep);
-                float ls;
-                if (badl) ls = bf(kNaN);
-                else if (ep == -1000) ls = 0.0f;
-                else ls = bf_f((int64_t)wave_sum_i(cv ? bf_int(pz, ep) : 0), ep - 23);
-                l = sadd(l, ls);
-            }
+            // LSUM of the segment (AT 6.5): block float of its p values
+            const bool pnf = cv && (fb(pz) & 0x7F800000u) == 0x7F800000u;
+            const bool badl = __ballot(pnf) != 0ull;
+            int ep = -1000;
+            if (cv && !pnf && (fb(pz) & 0x7FFFFFFFu)) ep = (int)((fb(pz) >> 23) & 0xFFu) - 127;
+            ep = wave_max_i(ep);
+            float ls;
+            if (badl) ls = bf(kNaN);
+            else if (ep == -1000) ls = 0.0f;
+            else ls = bf_f((int64_t)wave_sum_i((cv && !pnf) ? bf_int(pz, ep) : 0), ep - 23);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
-            // --- lane = value d of the slice ------------------------------------------------
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // --- lane = value of the slice ------------------------------------------------
             int32_t sk[4] = { 0, 0, 0, 0 };
-            const uint32_t ng = nu - 4u * sg < 4u ? nu - 4u * sg : 4u;
-            for (uint32_t gi = 0; gi < ng; ++gi) {
-                const uint32_t ug = u_first + 4u * (4u * sg + gi);
-                const int4 q = *(const int4 *)(vq + (size_t)ug * 16u * E + (size_t)d * 16u);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const int4 dg = *(const int4 *)&s_dig[wave][e_l][k][16u * gi];
-                    int acc = sk[k];
-                    acc = dot4(dg.x, q.x, acc);
-                    acc = dot4(dg.y, q.y, acc);
-                    acc = dot4(dg.z, q.z, acc);
-                    acc = dot4(dg.w, q.w, acc);
-                    sk[k] = acc;
+            for (uint32_t gi = 0; gi < 4; ++gi) {
+                if (gi < ngr) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const int4 dg = *(const int4 *)&s_dig[wave][e_l][k][16u * gi];
+                        int acc = sk[k];
+                        acc = dot4(dg.x, vqd[gi].x, acc);
+                        acc = dot4(dg.y, vqd[gi].y, acc);
+                        acc = dot4(dg.z, vqd[gi].z, acc);
+                        acc = dot4(dg.w, vqd[gi].w, acc);
+                        sk[k] = acc;
+                    }
                 }
             }
             const int64_t A = (int64_t)sk[0] + ((int64_t)sk[1] << 8) + ((int64_t)sk[2] << 16) + ((int64_t)sk[3] << 24);
-            const bool badl2 = e_l ? bad1 : bad0;
-            const float cval = badl2 ? bf(kNaN) : (any ? bf_f(A, es - 23) : 0.0f);
-            O = sadd(O, cval);
+            const bool badv = e_l ? bad1 : bad0;
+            s_c[seg][hi][lane] = badv ? bf(kNaN) : (any ? bf_f(A, es - 23) : 0.0f);
+            if (lane == 0) s_l[seg][hi] = ls;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-        const size_t slot = ((size_t)item * 4u + c) * a.n_head + h;
-        a.OP[slot * D + 64u * sl + (uint32_t)lane] = O;
-        if (sl == 0u && lane == 0) a.LP[slot] = l;
+        __syncthreads();
+        for (uint32_t idx = threadIdx.x; idx < hbn * 64u; idx += blockDim.x) {   // segment chains in order
+            const uint32_t hi = idx >> 6, L = idx & 63u, h = g * G + hb0 + hi;
+            float O = 0.0f;
+            for (uint32_t seg = 0; seg < nseg; ++seg) O = sadd(O, s_c[seg][hi][L]);
+            const size_t slot = ((size_t)item * 4u + c) * nh + h;
+            a.OP[slot * D + 64u * sl + L] = O;
+            if (L == 0u) {
+                float l = 0.0f;
+                for (uint32_t seg = 0; seg < nseg; ++seg) l = sadd(l, s_l[seg][hi]);
+                a.LP[slot * nsl + sl] = l;
+            }
+        }
+        __syncthreads();
     }
+
+    if (c == 0u && sl == 0u)                                      // chunk maxima for the merge
+        for (uint32_t i = threadIdx.x; i < G; i += blockDim.x) a.MK[(size_t)item * nh + g * G + i] = s_m[i];
 }
 
 // ---------------------------------------------------------------------------------------------
-// merge: block (token, head); threads over D
+// merge: block (token, KV head g x group of 4 heads, slice sl), lane = (head of the group, value).
+// A round stages up to kMergeItems chunks' channel partials, row sums and maxima in LDS with one
+// round of loads; each lane then runs CTREE over the 4 channels, the online merge in chunk order
+// and finally ANORM (AT 5.6, 5.7).
 // ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ float ctree4(float x0, float x1, float x2, float x3) { return sadd(sadd(x0, x1), sadd(x2, x3)); }
+constexpr uint32_t kMergeItems = 16;                             // chunks staged per round
+constexpr uint32_t kMergeHeads = 4;                              // heads per block
 
 __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a) {
-    const uint32_t t = blockIdx.x, h = blockIdx.y, D = a.D, nh = a.n_head;
+    __shared__ float s_op[kMergeItems][4][kMergeHeads][64];
+    __shared__ float s_lp[kMergeItems][4][kMergeHeads];
+    __shared__ float s_mk[kMergeItems][kMergeHeads];
+    const uint32_t G = a.G, D = a.D, nh = a.n_head, nsl = D / 64u;
+    const uint32_t ngrp = (G + kMergeHeads - 1u) / kMergeHeads;
+    const uint32_t t = blockIdx.x, g = blockIdx.y / ngrp, h0 = g * G + (blockIdx.y % ngrp) * kMergeHeads;
+    const uint32_t hn = min(kMergeHeads, g * G + G - h0), sl = blockIdx.z;
     const uint32_t first = a.tok_first[t], cnt = a.tok_count[t];
-    float O[2] = { 0.0f, 0.0f };
-    float l = 0.0f, m = 0.0f;
-    for (uint32_t k = 0; k < cnt; ++k) {
-        const uint32_t item = first + k;
-        const size_t s0 = (size_t)item * 4u * nh + h;
-        const float lk = ctree4(a.LP[s0], a.LP[s0 + nh], a.LP[s0 + 2u * nh], a.LP[s0 + 3u * nh]);
-        const float mk = a.MK[(size_t)item * nh + h];
-        float fa = 0.0f, fb_ = 0.0f;
-        if (k == 0u) { l = lk; m = mk; }
-        else {
-            const float mn = maxt(m, mk);
-            fa = expk(smul(ssub(m, mn), a.scale), a.ex);
-            fb_ = expk(smul(ssub(mk, mn), a.scale), a.ex);
-            l = sadd(smul(l, fa), smul(lk, fb_));
-            m = mn;
-        }
+    const uint32_t i = threadIdx.x >> 6, L = threadIdx.x & 63u;
+    float O = 0.0f, l = 0.0f, mr = 0.0f;
+    for (uint32_t k0 = 0; k0 < cnt; k0 += kMergeItems) {
+        const uint32_t kn = min(kMergeItems, cnt - k0);
+        for (uint32_t k = 0; k < kn; ++k) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const uint32_t dd = threadIdx.x + 256u * (uint32_t)r;
-            if (dd < D) {
-                const float ok = ctree4(a.OP[s0 * D + dd], a.OP[(s0 + nh) * D + dd], a.OP[(s0 + 2u * nh) * D + dd],
-                                        a.OP[(s0 + 3u * nh) * D + dd]);
-                O[r] = k == 0u ? ok : sadd(smul(O[r], fa), smul(ok, fb_));
+            for (uint32_t c = 0; c < 4u; ++c) {
+                if (i < hn) {
+                    const size_t slot = ((size_t)(first + k0 + k) * 4u + c) * nh + h0 + i;
+                    s_op[k][c][i][L] = a.OP[slot * D + 64u * sl + L];
+                }
             }
         }
+        for (uint32_t idx = threadIdx.x; idx < kn * 4u * hn; idx += blockDim.x) {
+            const uint32_t hi = idx % hn, c = idx / hn % 4u, k = idx / hn / 4u;
+            s_lp[k][c][hi] = a.LP[(((size_t)(first + k0 + k) * 4u + c) * nh + h0 + hi) * nsl + sl];
+        }
+        for (uint32_t idx = threadIdx.x; idx < kn * hn; idx += blockDim.x)
+            s_mk[idx / hn][idx % hn] = a.MK[(size_t)(first + k0 + idx / hn) * nh + h0 + idx % hn];
+        __syncthreads();
+        if (i < hn) {
+            for (uint32_t k = 0; k < kn; ++k) {
+                const float ok = ctree4(s_op[k][0][i][L], s_op[k][1][i][L], s_op[k][2][i][L], s_op[k][3][i][L]);
+                const float lk = ctree4(s_lp[k][0][i], s_lp[k][1][i], s_lp[k][2][i], s_lp[k][3][i]);
+                const float mk = s_mk[k][i];
+                if (k0 + k == 0u) { O = ok; l = lk; mr = mk; }
+                else {
+                    const float mn = maxt(mr, mk);
+                    const float fa = expk(smul(ssub(mr, mn), a.scale), a.ex);
+                    const float fbv = expk(smul(ssub(mk, mn), a.scale), a.ex);
+                    l = sadd(smul(l, fa), smul(lk, fbv));
+                    O = sadd(smul(O, fa), smul(ok, fbv));
+                    mr = mn;
+                }
+            }
+        }
+        __syncthreads();
     }
-    const float rinv = srcp(maxt(l, bf(kLFloor)));
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const uint32_t dd = threadIdx.x + 256u * (uint32_t)r;
-        if (dd < D) a.out[(size_t)t * a.out_stride + (size_t)h * D + dd] = smul(O[r], rinv);
-    }
+    if (i < hn)
+        a.out[(size_t)t * a.out_stride + (size_t)(h0 + i) * D + 64u * sl + L] = smul(O, srcp(maxt(l, bf(kLFloor))));
 }
 
 }  // namespace tsr
 
 int tsr_launch_fa(const tsr::FaArgs & a, uint32_t n_tiles, uint32_t n_items, uint32_t T, hipStream_t s) {
     const size_t lds_qk = (size_t)a.G * a.D + 4u * (size_t)a.G * (a.D / 32u) + 4u * 4u * a.G;
-    hipLaunchKernelGGL(tsr::k_fa_qk, dim3(n_tiles, a.n_head_kv), dim3(256), lds_qk, s, a);
+    const dim3 gqk(n_tiles, a.n_head_kv);
+    switch (a.D) {
+        case 64: hipLaunchKernelGGL(tsr::k_fa_qk<64>, gqk, dim3(256), lds_qk, s, a); break;
+        case 128: hipLaunchKernelGGL(tsr::k_fa_qk<128>, gqk, dim3(256), lds_qk, s, a); break;
+        case 256: hipLaunchKernelGGL(tsr::k_fa_qk<256>, gqk, dim3(256), lds_qk, s, a); break;
+        case 512: hipLaunchKernelGGL(tsr::k_fa_qk<512>, gqk, dim3(256), lds_qk, s, a); break;
+        default: return -2;
+    }
     if (hipGetLastError() != hipSuccess) return -4;
-    hipLaunchKernelGGL(tsr::k_fa_pv, dim3(4u * n_items, a.n_head_kv, a.D / 64u), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(tsr::k_fa_pv, dim3(4u * n_items, a.n_head_kv, a.D / 64u), dim3(1024), 0, s, a);
     if (hipGetLastError() != hipSuccess) return -4;
-    hipLaunchKernelGGL(tsr::k_fa_merge, dim3(T, a.n_head), dim3(256), 0, s, a);
+    const uint32_t ngrp = (a.G + tsr::kMergeHeads - 1u) / tsr::kMergeHeads;
+    hipLaunchKernelGGL(tsr::k_fa_merge, dim3(T, a.n_head_kv * ngrp, a.D / 64u), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }

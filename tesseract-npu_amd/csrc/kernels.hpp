@@ -61,8 +61,8 @@ struct FaTile {
 };
 
 struct FaArgs {
-    const uint8_t * qa;      // QA(A32) image of each token's query row (n_head * D values)
-    uint32_t qa_bytes, qa_d_off;
+    const float * q;         // query rows [T][n_head][D] f32, token t at q + t * q_stride
+    uint64_t q_stride;
     KvArgs kc, vc;
     uint32_t D, G, n_head, n_head_kv, E;
     float scale;
@@ -74,9 +74,9 @@ struct FaArgs {
     const uint32_t * tok_count;
     float * S;               // scores
     float * Mpart;           // [tile][n_head] tile maxima
-    float * MK;              // [item][n_head] chunk maxima
     float * OP;              // [item][4][n_head][D] channel partials
-    float * LP;              // [item][4][n_head] channel row sums
+    float * LP;              // [item][4][n_head][D / 64] channel row sums (one per slice)
+    float * MK;              // [item][n_head] chunk maxima
     float * out;
     uint64_t out_stride;
     ExpkTab ex;
@@ -85,8 +85,8 @@ struct FaArgs {
 }  // namespace tsr
 
 int tsr_launch_qact(const tsr::QactArgs & a, uint32_t T, hipStream_t s);
-int tsr_launch_mv_q8_0(const tsr::MvArgs & a, hipStream_t s);
-int tsr_launch_mv_q4_k(const tsr::MvArgs & a, hipStream_t s);
+int tsr_launch_mv_q8_0(const tsr::MvArgs & a, uint32_t n_cu, hipStream_t s);
+int tsr_launch_mv_q4_k(const tsr::MvArgs & a, uint32_t n_cu, hipStream_t s);
 int tsr_launch_kv_bytes(const tsr::KvArgs & a, uint32_t which, uint64_t off, uint64_t n, uint8_t * stage, int to_dev,
                         hipStream_t s);
 int tsr_launch_kv_set_rows(const tsr::KvArgs & a, uint32_t which, const float * src, uint32_t n_rows,

@@ -32,45 +32,68 @@ __device__ __forceinline__ uint32_t qact_a32_lane(const float4 v, float * D) {
     m = umax_u(m, (uint32_t)dpp_i<kDppRowHalfMirror>((int)m));
     const float d = sdiv(bf(m), 127.0f);
     const float id = (fb(d) & 0x7FFFFFFFu) ? srcp(d) : 0.0f;
+    // With amax >= 2^-60 (or Inf) the plain product rounds to the same integer as FM: a subnormal x
+    // gives |x id| < 2^-59 (-> 0, as DAZ), a subnormal product also rounds to 0, NaN -> 0 either way.
+    float pr[4];
+    if (m >= 0x21800000u) {                                     // uniform within the 8-lane group
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pr[i] = xs[i] * id;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pr[i] = smul(xs[i], id);
+    }
     uint32_t packed = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) packed |= ((uint32_t)round_away8(smul(xs[i], id)) & 0xFFu) << (8 * i);
+    for (int i = 0; i < 4; ++i) packed |= ((uint32_t)round_away8(pr[i]) & 0xFFu) << (8 * i);
     *D = h2f_exact(f2h_exact(d));
     return packed;
 }
 
+// Wave-wide maximum of an unsigned value (every lane gets it).
+__device__ __forceinline__ uint32_t wave_umax(uint32_t m) {
+    m = umax_u(m, (uint32_t)dpp_i<kDppXor1>((int)m));
+    m = umax_u(m, (uint32_t)dpp_i<kDppXor2>((int)m));
+    m = umax_u(m, (uint32_t)dpp_i<kDppRowHalfMirror>((int)m));
+    m = umax_u(m, (uint32_t)dpp_i<kDppRowMirror>((int)m));
+    m = umax_u(m, (uint32_t)xor16_i((int)m));
+    return umax_u((uint32_t)__builtin_amdgcn_readlane((int)m, 0), (uint32_t)__builtin_amdgcn_readlane((int)m, 32));
+}
+
 // One A256 block held by a whole wave (lane l: values 4l .. 4l+3). Returns this lane's 4 quants
 // packed; *d = the block's d (every lane); *sum4 = the sum of this lane's 4 quants.
+// First largest |x|: the wave maximum of the lane maxima, then the lowest lane holding it (lane l
+// holds indices 4l .. 4l+3, and its own first largest is kept), read with one readlane.
 __device__ __forceinline__ uint32_t qact_a256_lane(const float4 v, int lane, float * d, int * sum4) {
+    (void)lane;
     const float xs[4] = { v.x, v.y, v.z, v.w };
     uint32_t m = 0;
-    int at = 0;
     float best = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t a = mag_bits(xs[i]);
-        if (a <= 0x7F800000u && a > m) { m = a; at = 4 * lane + i; best = daz(xs[i]); }
+        if (a <= 0x7F800000u && a > m) { m = a; best = daz(xs[i]); }
     }
-    // wave-wide: the largest magnitude, the smallest index among equals
-    uint32_t km = m, ki = 0xFFFFu - (uint32_t)at;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t om = (uint32_t)shfl_i((int)km, lane ^ off);
-        const uint32_t oi = (uint32_t)shfl_i((int)ki, lane ^ off);
-        if (om > km || (om == km && oi > ki)) { km = om; ki = oi; }
-    }
+    const uint32_t amax = wave_umax(m);
     uint32_t packed = 0;
     int s = 0;
     float dd = 0.0f;
-    if (km != 0u) {
-        const int win = (int)(0xFFFFu - ki);
-        const float mx = shfl_f(best, win >> 2);
+    if (amax != 0u) {
+        const uint64_t hold = __ballot(m == amax);
+        const int win = __builtin_ctzll(hold);
+        const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(best), win));
         const float iscale = sdiv(-127.0f, mx);
+        int qi[4];
+        if (amax >= 0x21800000u) {                              // wave-uniform; as in qact_a32_lane
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qi[i] = round_even8(iscale * xs[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qi[i] = round_even8(smul(iscale, xs[i]));
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int q = round_even8(smul(iscale, xs[i]));
-            s += q;
-            packed |= ((uint32_t)q & 0xFFu) << (8 * i);
+            s += qi[i];
+            packed |= ((uint32_t)qi[i] & 0xFFu) << (8 * i);
         }
         dd = srcp(iscale);
     }

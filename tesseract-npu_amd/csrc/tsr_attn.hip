@@ -264,19 +264,18 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
         }
     }
     if (cells * n_head > 0xFFFFFFFFull || items.size() * 4u > 0x7FFFFFFFull) return TSR_HIP_E_SHAPE;
-    const size_t qa_bytes = tsr_hip_qa_bytes(0u, K);
+    const uint32_t nsl = D / 64u;
     const size_t n_items = items.size(), n_tiles = tiles.size();
     size_t off = 0;
-    const size_t o_qa = off; off = up256(off + (size_t)T * qa_bytes);
     const size_t o_items = off; off = up256(off + n_items * sizeof(tsr::FaItem));
     const size_t o_tiles = off; off = up256(off + n_tiles * sizeof(tsr::FaTile));
     const size_t o_tf = off; off = up256(off + 4u * (size_t)T);
     const size_t o_tc = off; off = up256(off + 4u * (size_t)T);
     const size_t o_S = off; off = up256(off + 4u * (size_t)cells * n_head);
     const size_t o_Mp = off; off = up256(off + 4u * n_tiles * n_head);
-    const size_t o_MK = off; off = up256(off + 4u * n_items * n_head);
     const size_t o_OP = off; off = up256(off + 4u * n_items * kC * n_head * D);
-    const size_t o_LP = off; off = up256(off + 4u * n_items * kC * n_head);
+    const size_t o_LP = off; off = up256(off + 4u * n_items * kC * n_head * nsl);
+    const size_t o_MK = off; off = up256(off + 4u * n_items * n_head);
 
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
@@ -290,21 +289,9 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     if (!rc) rc = hip_err(hipMemcpyAsync(base + o_tc, tok_count.data(), 4u * T, hipMemcpyHostToDevice, s), "fa tok_count");
     if (rc) return rc;
 
-    tsr::QactArgs qa{};
-    qa.x = q_dev;
-    qa.x_stride = q_stride;
-    qa.qa = base + o_qa;
-    qa.qa_bytes = (uint32_t)qa_bytes;
-    qa.K = K;
-    qa.kind = 0u;
-    qa.d_off = (K + 63u) / 64u * 64u;
-    qa.bs_off = qa.d_off + (4u * (K / 32u) + 63u) / 64u * 64u;
-    if (tsr_launch_qact(qa, T, s)) return TSR_HIP_E_HIP;
-
     tsr::FaArgs a{};
-    a.qa = base + o_qa;
-    a.qa_bytes = (uint32_t)qa_bytes;
-    a.qa_d_off = qa.d_off;
+    a.q = q_dev;
+    a.q_stride = q_stride;
     a.kc = kv_args(kc);
     a.vc = kv_args(vc);
     a.D = D;
@@ -321,9 +308,9 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     a.tok_count = (const uint32_t *)(base + o_tc);
     a.S = (float *)(base + o_S);
     a.Mpart = (float *)(base + o_Mp);
-    a.MK = (float *)(base + o_MK);
     a.OP = (float *)(base + o_OP);
     a.LP = (float *)(base + o_LP);
+    a.MK = (float *)(base + o_MK);
     a.out = out_dev;
     a.out_stride = out_stride;
     a.ex = ctx->expk;

@@ -23,11 +23,11 @@ __device__ __forceinline__ float daz(float x) {
     const uint32_t u = fb(x);
     return (u & 0x7F800000u) ? x : bf(u & 0x80000000u);
 }
+// Written as selects (no early returns) so that it compiles to straight-line code.
 __device__ __forceinline__ float fin(float r) {
     const uint32_t u = fb(r), e = u & 0x7F800000u;
-    if (e == 0x7F800000u) return (u & 0x007FFFFFu) ? bf(kNaN) : r;
-    if (e == 0u) return bf(u & 0x80000000u);
-    return r;
+    const uint32_t nan = (e == 0x7F800000u && (u & 0x007FFFFFu)) ? kNaN : u;
+    return bf(e == 0u ? (u & 0x80000000u) : nan);
 }
 // NaN -> canonical only (results that cannot be subnormal).
 __device__ __forceinline__ float canon(float r) { return (fb(r) & 0x7FFFFFFFu) > 0x7F800000u ? bf(kNaN) : r; }
@@ -76,21 +76,19 @@ __device__ __forceinline__ uint32_t f2h_exact(float f) {
 
 // QACT f32 -> int8: NaN -> 0; |x| >= 256 saturates; else round (half away: A32, half even: A256)
 // and clamp to [-128, 127] (sw/sim/tsr_ref.c:200-232).
+// Straight-line forms: NaN is replaced by 0 first, the clamp then saturates Inf and |x| >= 256.
 __device__ __forceinline__ int32_t round_away8(float x) {
-    if (__builtin_isnan(x)) return 0;
-    if (__builtin_fabsf(x) >= 256.0f) return x < 0.0f ? -128 : 127;
-    const float t = __builtin_truncf(x);
-    const float fr = x - t;                                   // exact
-    float r = t;
-    if (__builtin_fabsf(fr) >= 0.5f) r = x < 0.0f ? t - 1.0f : t + 1.0f;
-    const int32_t v = (int32_t)r;
-    return v < -128 ? -128 : (v > 127 ? 127 : v);
+    const float v = __builtin_isnan(x) ? 0.0f : x;
+    const float t = __builtin_truncf(v);
+    const float fr = v - t;                                   // exact (|v| >= 2^23 is integral; Inf gives NaN)
+    const float up = __builtin_fabsf(fr) >= 0.5f ? __builtin_copysignf(1.0f, v) : 0.0f;
+    const float r = __builtin_fminf(__builtin_fmaxf(t + up, -128.0f), 127.0f);
+    return (int32_t)r;
 }
 __device__ __forceinline__ int32_t round_even8(float x) {
-    if (__builtin_isnan(x)) return 0;
-    if (__builtin_fabsf(x) >= 256.0f) return x < 0.0f ? -128 : 127;
-    const int32_t v = (int32_t)__builtin_rintf(x);            // v_rndne_f32: nearest, ties to even
-    return v < -128 ? -128 : (v > 127 ? 127 : v);
+    const float v = __builtin_isnan(x) ? 0.0f : x;
+    const float r = __builtin_fminf(__builtin_fmaxf(__builtin_rintf(v), -128.0f), 127.0f);   // rintf: ties to even
+    return (int32_t)r;
 }
 
 // ---- wave64 exchange ----------------------------------------------------------------------------

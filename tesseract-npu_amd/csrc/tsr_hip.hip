@@ -193,6 +193,37 @@ uint32_t blk_bytes(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 34u : 144u; 
 uint32_t blk_meta(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 2u : 16u; }
 uint32_t blk_quant(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 32u : 128u; }
 
+// Q4_K scales: ggml packs eight 6-bit scales sc_j and mins m_j into 12 bytes (get_scale_min_k4,
+// sw/sim/tsr_ref.c:359-367). The device keeps the same 96 bits re-arranged so that one bit-field
+// extract gives each value: byte j (j < 8) = sc_j | (m_j & 3) << 6, bytes 8-11 = the nibbles
+// m_j >> 2 (nibble j at bit 4j). A bijection of the 12 bytes, so weight reads give back the exact
+// ggml blocks.
+void q4k_meta_encode(const uint8_t * q, uint8_t * e) {
+    uint32_t hi = 0;
+    for (int j = 0; j < 8; ++j) {
+        int sc, m;
+        if (j < 4) { sc = q[j] & 63; m = q[j + 4] & 63; }
+        else { sc = (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4); m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4); }
+        e[j] = (uint8_t)(sc | ((m & 3) << 6));
+        hi |= (uint32_t)(m >> 2) << (4 * j);
+    }
+    for (int k = 0; k < 4; ++k) e[8 + k] = (uint8_t)(hi >> (8 * k));
+}
+
+void q4k_meta_decode(const uint8_t * e, uint8_t * q) {
+    const uint32_t hi = e[8] | (uint32_t)e[9] << 8 | (uint32_t)e[10] << 16 | (uint32_t)e[11] << 24;
+    int sc[8], m[8];
+    for (int j = 0; j < 8; ++j) {
+        sc[j] = e[j] & 63;
+        m[j] = (e[j] >> 6) | (int)(((hi >> (4 * j)) & 15u) << 2);
+    }
+    for (int j = 0; j < 4; ++j) {
+        q[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+        q[j + 4] = (uint8_t)(m[j] | ((m[j + 4] >> 4) << 6));
+        q[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+    }
+}
+
 template <class F>
 void parallel_rows(uint32_t N, F && f) {
     const uint32_t nt = std::max(1u, std::min<uint32_t>(16u, std::thread::hardware_concurrency()));
@@ -227,7 +258,9 @@ int tsr_hip_weight_upload(tsr_hip_ctx * ctx, uint32_t fmt, const void * ggml_blo
         for (size_t r = lo; r < hi; ++r)
             for (size_t i = 0; i < nb; ++i) {
                 const uint8_t * b = src + (r * nb + i) * bb;
-                memcpy(host.data() + (r * nb + i) * bm, b, bm);
+                uint8_t * m = host.data() + (r * nb + i) * bm;
+                memcpy(m, b, bm);
+                if (fmt == TSR_HIP_FMT_Q4_K) q4k_meta_encode(b + 4, m + 4);
                 memcpy(host.data() + quant_off + (r * nb + i) * bq, b + bm, bq);
             }
     });
@@ -270,6 +303,7 @@ int tsr_hip_weight_read(tsr_hip_ctx * ctx, const tsr_hip_weight * w, void * ggml
             for (size_t i = 0; i < nb; ++i) {
                 uint8_t * b = dst + (r * nb + i) * bb;
                 memcpy(b, host.data() + (r * nb + i) * bm, bm);
+                if (w->fmt == TSR_HIP_FMT_Q4_K) q4k_meta_decode(host.data() + (r * nb + i) * bm + 4, b + 4);
                 memcpy(b + bm, host.data() + w->quant_off + (r * nb + i) * bq, bq);
             }
     });
@@ -367,7 +401,8 @@ static int mul_mat_common(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
         a.y = y_dev + (size_t)t0 * y_stride;
         a.add = add_dev ? add_dev + (size_t)t0 * add_stride : nullptr;
         a.T = tt;
-        const int rc = w->fmt == TSR_HIP_FMT_Q8_0 ? tsr_launch_mv_q8_0(a, s) : tsr_launch_mv_q4_k(a, s);
+        const uint32_t ncu = (uint32_t)ctx->n_cu;
+        const int rc = w->fmt == TSR_HIP_FMT_Q8_0 ? tsr_launch_mv_q8_0(a, ncu, s) : tsr_launch_mv_q4_k(a, ncu, s);
         if (rc) return rc == -2 ? TSR_HIP_E_SHAPE : TSR_HIP_E_HIP;
     }
     return TSR_HIP_OK;

@@ -145,20 +145,25 @@ __device__ __forceinline__ float bf_f(int64_t A, int32_t k) {
 // values of the KV head's G heads (QACT A32: its 32-blocks never cross a head, so they are the
 // blocks of the whole query row) while the K rows of its cells load.
 // ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ FaItem fa_item(const FaArgs & a, const FaPlan & p, uint32_t i) {
+    return a.items ? a.items[i] : p.items[i];
+}
+
 template <int D>
-__global__ __launch_bounds__(256) void k_fa_qk(FaArgs a) {
+__global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr uint32_t NBD = D / 32u;                             // blocks per head
     constexpr bool KREG = D <= 128;                                // K row of the cell kept in registers
-    const FaTile tl = a.tiles[blockIdx.x];
-    const FaItem it = a.items[tl.item];
+    const uint32_t tt = blockIdx.x % p.maxtiles;
+    const FaItem it = fa_item(a, p, blockIdx.x / p.maxtiles);
+    if (tt >= it.ntiles) return;                                  // the item has fewer tiles (block-uniform)
     const uint32_t g = blockIdx.y, G = a.G;
     int8_t * s_q = (int8_t *)lds;                                 // G*D quants of the KV head's query heads
     float * s_dx = (float *)(lds + G * D);                        // G*D/32 scales
     uint32_t * s_red = (uint32_t *)(s_dx + G * NBD);              // 4 waves x G maxima (keys)
     const int lane = (int)__lane_id(), wave = (int)(threadIdx.x >> 6);
 
-    const uint32_t n16 = 16u * it.n, j = tl.c0 + threadIdx.x;
+    const uint32_t n16 = 16u * it.n, j = 256u * tt + threadIdx.x;
     const bool in = j < n16;
     const uint32_t cell = 16u * it.u0 + j;
     const uint32_t ng = (a.kc.kv_size + 15u) / 16u;
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a) {
     for (uint32_t i = threadIdx.x; i < G; i += blockDim.x) {
         uint32_t m = s_red[i];
         for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = umax_u(m, s_red[w * G + i]);
-        a.Mpart[(size_t)blockIdx.x * a.n_head + g * G + i] = maxt_unkey(m);
+        a.Mpart[(size_t)(it.tile0 + tt) * a.n_head + g * G + i] = maxt_unkey(m);
     }
 }
 
@@ -252,13 +257,14 @@ constexpr int kMaxSeg = 8;                                        // NCG <= 128 
 
 __device__ __forceinline__ float ctree4(float x0, float x1, float x2, float x3) { return sadd(sadd(x0, x1), sadd(x2, x3)); }
 
-__global__ __launch_bounds__(1024) void k_fa_pv(FaArgs a) {
+__global__ __launch_bounds__(1024) void k_fa_pv(FaArgs a, FaPlan p) {
     __shared__ __align__(16) int8_t s_dig[16][2][4][64];          // wave, block e, digit, cell
     __shared__ float s_c[kMaxSeg][kHB][64];
     __shared__ float s_l[kMaxSeg][kHB];
     __shared__ float s_m[64];
+    __shared__ uint32_t s_mkey[64];
     const uint32_t item = blockIdx.x >> 2, c = blockIdx.x & 3u, g = blockIdx.y, sl = blockIdx.z;
-    const FaItem it = a.items[item];
+    const FaItem it = fa_item(a, p, item);
     const uint32_t G = a.G, D = a.D, E = a.E, n16 = 16u * it.n, nbk = E / 32u, nh = a.n_head, nsl = D / 64u;
     const int lane = (int)__lane_id(), wave = (int)(threadIdx.x >> 6), nw = (int)(blockDim.x >> 6);
     const uint32_t u_first = it.u0 + ((c + 4u - (it.u0 & 3u)) & 3u);
@@ -272,11 +278,13 @@ __global__ __launch_bounds__(1024) void k_fa_pv(FaArgs a) {
     const uint16_t * vmeta = (const uint16_t *)a.vc.base;
     const uint8_t * vq = a.vc.base + a.vc.quant_off;
 
-    for (uint32_t i = threadIdx.x; i < G; i += blockDim.x) {      // chunk maxima (MAXOUT over the tiles)
-        float m = bf(kMFloor);
-        for (uint32_t tt = 0; tt < it.ntiles; ++tt) m = maxt(m, a.Mpart[(size_t)(it.tile0 + tt) * nh + g * G + i]);
-        s_m[i] = m;
-    }
+    // chunk maxima (MAXOUT over the tiles; MAXT is a total order, so the order of the folds is free)
+    for (uint32_t i = threadIdx.x; i < G; i += blockDim.x) s_mkey[i] = maxt_key_f(bf(kMFloor));
+    __syncthreads();
+    for (uint32_t idx = threadIdx.x; idx < G * it.ntiles; idx += blockDim.x)   // one load per thread
+        atomicMax(&s_mkey[idx % G], maxt_key_f(a.Mpart[(size_t)(it.tile0 + idx / G) * nh + g * G + idx % G]));
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < G; i += blockDim.x) s_m[i] = maxt_unkey(s_mkey[i]);
     __syncthreads();
 
     for (uint32_t hb0 = 0; hb0 < G; hb0 += kHB) {
@@ -382,80 +390,73 @@ __global__ __launch_bounds__(1024) void k_fa_pv(FaArgs a) {
 
 // ---------------------------------------------------------------------------------------------
 // merge: block (token, KV head g x group of 4 heads, slice sl), lane = (head of the group, value).
-// A round stages up to kMergeItems chunks' channel partials, row sums and maxima in LDS with one
-// round of loads; each lane then runs CTREE over the 4 channels, the online merge in chunk order
-// and finally ANORM (AT 5.6, 5.7).
+// Each lane loads the channel partials, row sums and maxima of up to kMergeItems chunks at once,
+// then runs CTREE over the 4 channels, the online merge in chunk order and finally ANORM (AT 5.6,
+// 5.7). No LDS and no barriers.
 // ---------------------------------------------------------------------------------------------
-constexpr uint32_t kMergeItems = 16;                             // chunks staged per round
+constexpr uint32_t kMergeItems = 8;                              // chunks loaded per round
 constexpr uint32_t kMergeHeads = 4;                              // heads per block
 
-__global__ __launch_bounds__(256) void k_fa_merge(FaArgs a) {
-    __shared__ float s_op[kMergeItems][4][kMergeHeads][64];
-    __shared__ float s_lp[kMergeItems][4][kMergeHeads];
-    __shared__ float s_mk[kMergeItems][kMergeHeads];
+__global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
     const uint32_t G = a.G, D = a.D, nh = a.n_head, nsl = D / 64u;
     const uint32_t ngrp = (G + kMergeHeads - 1u) / kMergeHeads;
     const uint32_t t = blockIdx.x, g = blockIdx.y / ngrp, h0 = g * G + (blockIdx.y % ngrp) * kMergeHeads;
     const uint32_t hn = min(kMergeHeads, g * G + G - h0), sl = blockIdx.z;
-    const uint32_t first = a.tok_first[t], cnt = a.tok_count[t];
     const uint32_t i = threadIdx.x >> 6, L = threadIdx.x & 63u;
+    if (i >= hn) return;                                          // whole waves
+    const uint32_t first = a.tok_first ? a.tok_first[t] : p.tok_first[t];
+    const uint32_t cnt = a.tok_count ? a.tok_count[t] : p.tok_count[t];
+    const uint32_t h = h0 + i;
     float O = 0.0f, l = 0.0f, mr = 0.0f;
     for (uint32_t k0 = 0; k0 < cnt; k0 += kMergeItems) {
         const uint32_t kn = min(kMergeItems, cnt - k0);
-        for (uint32_t k = 0; k < kn; ++k) {
+        float op[kMergeItems][4], lp[kMergeItems][4], mk[kMergeItems];
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeItems; ++k) {                // clamped: every load is issued up front
+            const size_t kk = first + k0 + min(k, kn - 1u);
 #pragma unroll
             for (uint32_t c = 0; c < 4u; ++c) {
-                if (i < hn) {
-                    const size_t slot = ((size_t)(first + k0 + k) * 4u + c) * nh + h0 + i;
-                    s_op[k][c][i][L] = a.OP[slot * D + 64u * sl + L];
-                }
+                const size_t slot = (kk * 4u + c) * nh + h;
+                op[k][c] = a.OP[slot * D + 64u * sl + L];
+                lp[k][c] = a.LP[slot * nsl + sl];
+            }
+            mk[k] = a.MK[kk * nh + h];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeItems; ++k) {
+            if (k >= kn) break;
+            const float ok = ctree4(op[k][0], op[k][1], op[k][2], op[k][3]);
+            const float lk = ctree4(lp[k][0], lp[k][1], lp[k][2], lp[k][3]);
+            if (k0 + k == 0u) { O = ok; l = lk; mr = mk[k]; }
+            else {
+                const float mn = maxt(mr, mk[k]);
+                const float fa = expk(smul(ssub(mr, mn), a.scale), a.ex);
+                const float fbv = expk(smul(ssub(mk[k], mn), a.scale), a.ex);
+                l = sadd(smul(l, fa), smul(lk, fbv));
+                O = sadd(smul(O, fa), smul(ok, fbv));
+                mr = mn;
             }
         }
-        for (uint32_t idx = threadIdx.x; idx < kn * 4u * hn; idx += blockDim.x) {
-            const uint32_t hi = idx % hn, c = idx / hn % 4u, k = idx / hn / 4u;
-            s_lp[k][c][hi] = a.LP[(((size_t)(first + k0 + k) * 4u + c) * nh + h0 + hi) * nsl + sl];
-        }
-        for (uint32_t idx = threadIdx.x; idx < kn * hn; idx += blockDim.x)
-            s_mk[idx / hn][idx % hn] = a.MK[(size_t)(first + k0 + idx / hn) * nh + h0 + idx % hn];
-        __syncthreads();
-        if (i < hn) {
-            for (uint32_t k = 0; k < kn; ++k) {
-                const float ok = ctree4(s_op[k][0][i][L], s_op[k][1][i][L], s_op[k][2][i][L], s_op[k][3][i][L]);
-                const float lk = ctree4(s_lp[k][0][i], s_lp[k][1][i], s_lp[k][2][i], s_lp[k][3][i]);
-                const float mk = s_mk[k][i];
-                if (k0 + k == 0u) { O = ok; l = lk; mr = mk; }
-                else {
-                    const float mn = maxt(mr, mk);
-                    const float fa = expk(smul(ssub(mr, mn), a.scale), a.ex);
-                    const float fbv = expk(smul(ssub(mk, mn), a.scale), a.ex);
-                    l = sadd(smul(l, fa), smul(lk, fbv));
-                    O = sadd(smul(O, fa), smul(ok, fbv));
-                    mr = mn;
-                }
-            }
-        }
-        __syncthreads();
     }
-    if (i < hn)
-        a.out[(size_t)t * a.out_stride + (size_t)(h0 + i) * D + 64u * sl + L] = smul(O, srcp(maxt(l, bf(kLFloor))));
+    a.out[(size_t)t * a.out_stride + (size_t)h * D + 64u * sl + L] = smul(O, srcp(maxt(l, bf(kLFloor))));
 }
 
 }  // namespace tsr
 
-int tsr_launch_fa(const tsr::FaArgs & a, uint32_t n_tiles, uint32_t n_items, uint32_t T, hipStream_t s) {
+int tsr_launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, hipStream_t s) {
     const size_t lds_qk = (size_t)a.G * a.D + 4u * (size_t)a.G * (a.D / 32u) + 4u * 4u * a.G;
-    const dim3 gqk(n_tiles, a.n_head_kv);
+    const dim3 gqk(p.n_items * p.maxtiles, a.n_head_kv);
     switch (a.D) {
-        case 64: hipLaunchKernelGGL(tsr::k_fa_qk<64>, gqk, dim3(256), lds_qk, s, a); break;
-        case 128: hipLaunchKernelGGL(tsr::k_fa_qk<128>, gqk, dim3(256), lds_qk, s, a); break;
-        case 256: hipLaunchKernelGGL(tsr::k_fa_qk<256>, gqk, dim3(256), lds_qk, s, a); break;
-        case 512: hipLaunchKernelGGL(tsr::k_fa_qk<512>, gqk, dim3(256), lds_qk, s, a); break;
+        case 64: hipLaunchKernelGGL(tsr::k_fa_qk<64>, gqk, dim3(256), lds_qk, s, a, p); break;
+        case 128: hipLaunchKernelGGL(tsr::k_fa_qk<128>, gqk, dim3(256), lds_qk, s, a, p); break;
+        case 256: hipLaunchKernelGGL(tsr::k_fa_qk<256>, gqk, dim3(256), lds_qk, s, a, p); break;
+        case 512: hipLaunchKernelGGL(tsr::k_fa_qk<512>, gqk, dim3(256), lds_qk, s, a, p); break;
         default: return -2;
     }
     if (hipGetLastError() != hipSuccess) return -4;
-    hipLaunchKernelGGL(tsr::k_fa_pv, dim3(4u * n_items, a.n_head_kv, a.D / 64u), dim3(1024), 0, s, a);
+    hipLaunchKernelGGL(tsr::k_fa_pv, dim3(4u * p.n_items, a.n_head_kv, a.D / 64u), dim3(1024), 0, s, a, p);
     if (hipGetLastError() != hipSuccess) return -4;
     const uint32_t ngrp = (a.G + tsr::kMergeHeads - 1u) / tsr::kMergeHeads;
-    hipLaunchKernelGGL(tsr::k_fa_merge, dim3(T, a.n_head_kv * ngrp, a.D / 64u), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(tsr::k_fa_merge, dim3(T, a.n_head_kv * ngrp, a.D / 64u), dim3(256), 0, s, a, p);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }

@@ -53,13 +53,16 @@ struct FaItem {
     uint32_t c_lo, c_hi;     // visible chunk-relative cells (FAST)
     uint32_t general;        // GENERAL chunk: all cells, f32 mask added
     uint32_t s_off;          // first score cell of the item in S (scores at S + s_off * n_head)
-    uint32_t tile0, ntiles;  // its score tiles
-    uint32_t pad[3];
+    uint32_t tile0, ntiles;  // its 256-cell score tiles (rows tile0 .. tile0 + ntiles - 1 of Mpart)
 };
-struct FaTile {
-    uint32_t item, c0;       // 256 chunk-relative cells [c0, c0 + 256)
+// The work list of one call. Small lists (decode) travel inline in the kernel arguments; larger ones
+// are copied to device memory once per call and the kernels read them there (FaArgs::items != 0).
+constexpr uint32_t kFaInlItems = 48, kFaInlTok = 8;
+struct FaPlan {
+    uint32_t n_items, maxtiles;                        // items; tiles of the largest item
+    uint32_t tok_first[kFaInlTok], tok_count[kFaInlTok];
+    FaItem items[kFaInlItems];
 };
-
 struct FaArgs {
     const float * q;         // query rows [T][n_head][D] f32, token t at q + t * q_stride
     uint64_t q_stride;
@@ -68,8 +71,7 @@ struct FaArgs {
     float scale;
     const float * mask;      // GENERAL: f32 mask rows of mstride floats
     uint32_t mstride;
-    const FaItem * items;
-    const FaTile * tiles;
+    const FaItem * items;    // device copy of a large work list, else 0 (inline FaPlan)
     const uint32_t * tok_first;
     const uint32_t * tok_count;
     float * S;               // scores
@@ -91,4 +93,4 @@ int tsr_launch_kv_bytes(const tsr::KvArgs & a, uint32_t which, uint64_t off, uin
                         hipStream_t s);
 int tsr_launch_kv_set_rows(const tsr::KvArgs & a, uint32_t which, const float * src, uint32_t n_rows,
                            uint64_t src_stride, const int64_t * idx, int32_t * bad, hipStream_t s);
-int tsr_launch_fa(const tsr::FaArgs & a, uint32_t n_tiles, uint32_t n_items, uint32_t T, hipStream_t s);
+int tsr_launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, hipStream_t s);

@@ -235,17 +235,17 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
         (T > 1u && out_stride < K) || T > 65535u)
         return TSR_HIP_E_ARG;
 
-    // plan every token row; flatten into items (chunks) and 256-cell score tiles
+    // plan every token row; flatten into items (chunks) with their 256-cell score tiles
     std::vector<tsr::FaItem> items;
-    std::vector<tsr::FaTile> tiles;
-    std::vector<uint32_t> tok_first(T), tok_count(T);
+    std::vector<uint32_t> tok(2u * (size_t)T);                    // tok_first [T] | tok_count [T]
     std::vector<Chunk> ch;
     uint64_t cells = 0;
+    uint32_t n_tiles = 0, maxtiles = 1;
     for (uint32_t t = 0; t < T; ++t) {
         ch.clear();
         if (!plan_row(E, D, msum, t, new_runs, n_new, ch)) return TSR_HIP_E_MASK;
-        tok_first[t] = (uint32_t)items.size();
-        tok_count[t] = (uint32_t)ch.size();
+        tok[t] = (uint32_t)items.size();
+        tok[T + t] = (uint32_t)ch.size();
         for (const Chunk & c : ch) {
             if (c.general && mask_f32_dev == nullptr) return TSR_HIP_E_MASK;
             tsr::FaItem it{};
@@ -256,26 +256,39 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
             it.c_hi = c.c_hi;
             it.general = c.general;
             it.s_off = (uint32_t)cells;
-            it.tile0 = (uint32_t)tiles.size();
+            it.tile0 = n_tiles;
             it.ntiles = (16u * c.n + 255u) / 256u;
-            for (uint32_t k = 0; k < it.ntiles; ++k) tiles.push_back({ (uint32_t)items.size(), 256u * k });
+            n_tiles += it.ntiles;
+            maxtiles = std::max(maxtiles, it.ntiles);
             cells += 16u * c.n;
             items.push_back(it);
         }
     }
-    if (cells * n_head > 0xFFFFFFFFull || items.size() * 4u > 0x7FFFFFFFull) return TSR_HIP_E_SHAPE;
+    const size_t n_items = items.size();
+    if (cells * n_head > 0xFFFFFFFFull || n_items * 4u > 0x7FFFFFFFull || n_items * maxtiles > 0x7FFFFFFFull)
+        return TSR_HIP_E_SHAPE;
+    const bool inl = n_items <= tsr::kFaInlItems && T <= tsr::kFaInlTok;
     const uint32_t nsl = D / 64u;
-    const size_t n_items = items.size(), n_tiles = tiles.size();
     size_t off = 0;
-    const size_t o_items = off; off = up256(off + n_items * sizeof(tsr::FaItem));
-    const size_t o_tiles = off; off = up256(off + n_tiles * sizeof(tsr::FaTile));
-    const size_t o_tf = off; off = up256(off + 4u * (size_t)T);
-    const size_t o_tc = off; off = up256(off + 4u * (size_t)T);
+    const size_t o_items = off; off = up256(off + (inl ? 0u : n_items * sizeof(tsr::FaItem) + 8u * (size_t)T));
     const size_t o_S = off; off = up256(off + 4u * (size_t)cells * n_head);
-    const size_t o_Mp = off; off = up256(off + 4u * n_tiles * n_head);
+    const size_t o_Mp = off; off = up256(off + 4u * (size_t)n_tiles * n_head);
     const size_t o_OP = off; off = up256(off + 4u * n_items * kC * n_head * D);
     const size_t o_LP = off; off = up256(off + 4u * n_items * kC * n_head * nsl);
     const size_t o_MK = off; off = up256(off + 4u * n_items * n_head);
+
+    tsr::FaPlan p{};
+    p.n_items = (uint32_t)n_items;
+    p.maxtiles = maxtiles;
+    std::vector<uint8_t> packed;
+    if (inl) {
+        std::copy(items.begin(), items.end(), p.items);
+        for (uint32_t t = 0; t < T; ++t) { p.tok_first[t] = tok[t]; p.tok_count[t] = tok[T + t]; }
+    } else {                                                      // items | tok_first | tok_count, one copy
+        packed.resize(n_items * sizeof(tsr::FaItem) + 8u * (size_t)T);
+        memcpy(packed.data(), items.data(), n_items * sizeof(tsr::FaItem));
+        memcpy(packed.data() + n_items * sizeof(tsr::FaItem), tok.data(), 8u * (size_t)T);
+    }
 
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
@@ -283,11 +296,10 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     int rc = ctx->scratch.reserve(ctx, off);
     if (rc) return rc;
     uint8_t * base = (uint8_t *)ctx->scratch.ptr;
-    rc = hip_err(hipMemcpyAsync(base + o_items, items.data(), n_items * sizeof(tsr::FaItem), hipMemcpyHostToDevice, s), "fa items");
-    if (!rc) rc = hip_err(hipMemcpyAsync(base + o_tiles, tiles.data(), n_tiles * sizeof(tsr::FaTile), hipMemcpyHostToDevice, s), "fa tiles");
-    if (!rc) rc = hip_err(hipMemcpyAsync(base + o_tf, tok_first.data(), 4u * T, hipMemcpyHostToDevice, s), "fa tok_first");
-    if (!rc) rc = hip_err(hipMemcpyAsync(base + o_tc, tok_count.data(), 4u * T, hipMemcpyHostToDevice, s), "fa tok_count");
-    if (rc) return rc;
+    if (!inl) {
+        rc = hip_err(hipMemcpyAsync(base + o_items, packed.data(), packed.size(), hipMemcpyHostToDevice, s), "fa plan");
+        if (rc) return rc;
+    }
 
     tsr::FaArgs a{};
     a.q = q_dev;
@@ -302,10 +314,11 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     a.scale = scale;
     a.mask = mask_f32_dev;
     a.mstride = 16u * ((msum[2] + 15u) / 16u);
-    a.items = (const tsr::FaItem *)(base + o_items);
-    a.tiles = (const tsr::FaTile *)(base + o_tiles);
-    a.tok_first = (const uint32_t *)(base + o_tf);
-    a.tok_count = (const uint32_t *)(base + o_tc);
+    if (!inl) {
+        a.items = (const tsr::FaItem *)(base + o_items);
+        a.tok_first = (const uint32_t *)(base + o_items + n_items * sizeof(tsr::FaItem));
+        a.tok_count = a.tok_first + T;
+    }
     a.S = (float *)(base + o_S);
     a.Mpart = (float *)(base + o_Mp);
     a.OP = (float *)(base + o_OP);
@@ -316,5 +329,5 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     a.ex = ctx->expk;
     ctx->ctr.flash_attn_calls++;
     ctx->ctr.flash_attn_kv_bytes += cells * (uint64_t)E / 32u * 34u * 2u;
-    return tsr_launch_fa(a, (uint32_t)n_tiles, (uint32_t)n_items, T, s) ? TSR_HIP_E_HIP : TSR_HIP_OK;
+    return tsr_launch_fa(a, p, T, s) ? TSR_HIP_E_HIP : TSR_HIP_OK;
 }

@@ -17,10 +17,15 @@ baseline: this repository's oracle (the reference's numerics restated in C) on t
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes as C
+import glob
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -152,8 +157,83 @@ def extra_workloads(dev, ev, stream, n: int) -> dict:
     out["fa_decode_q8kv_8192_32q8kv_d128"] = {"us_per_call": round(ms * 1e3, 3), "algorithmic_bytes": nbytes,
                                               "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
                                               "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                              "copies": copies, "launches_per_call": 4}
+                                              "copies": copies, "launches_per_call": 3}
     return out
+
+
+COPY_BYTES = 256 << 20          # calibration copy (device to device)
+
+
+def pmc_child(workdir: str, reps: int = 3) -> int:
+    """Counter-collection child (run under rocprofv3 --pmc): a device-to-device copy of COPY_BYTES,
+    then the up and down matvecs, `reps` dispatches each, on the weights the parent saved."""
+    up = np.load(os.path.join(workdir, "up.npy"))
+    dn = np.load(os.path.join(workdir, "dn.npy"))
+    x = np.load(os.path.join(workdir, "x.npy"))
+    dev = tsr_hip.Device(0)
+    ev = HipEvents()
+    ev.h.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    src, dst = dev.alloc(COPY_BYTES), dev.alloc(COPY_BYTES)
+    src.fill(1)
+    w_up, w_dn = dev.weight(1, up, 14336, 4096), dev.weight(1, dn, 4096, 14336)
+    xb, hb, yb = dev.upload(x), dev.alloc(4 * 14336), dev.alloc(4 * 4096)
+    for _ in range(reps):
+        assert ev.h.hipMemcpyAsync(dst.ptr, src.ptr, COPY_BYTES, 3, dev.stream) == 0   # 3: device to device
+    ev.device_sync()
+    for _ in range(reps):
+        dev.mul_mat(w_up, xb, 1, 4096, hb, 14336, stream=dev.stream)
+    for _ in range(reps):
+        dev.mul_mat(w_dn, hb, 1, 14336, yb, 4096, stream=dev.stream)
+    ev.device_sync()
+    dev.close()
+    return 0
+
+
+def _pmc_pass(counter: str, workdir: str) -> list:
+    """One rocprofv3 --pmc pass over the child; returns [(dispatch id, kernel name, KiB)] in
+    dispatch order."""
+    out = os.path.join(workdir, "pmc_" + counter)
+    cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", counter, "--output-format", "csv",
+           "-d", out, "-o", "pmc", "--", sys.executable, os.path.abspath(__file__), "--pmc-child", workdir]
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, cwd=workdir)
+    files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+    if r.returncode != 0 and not files:
+        raise RuntimeError(f"rocprofv3 --pmc {counter} failed ({r.returncode}): {r.stdout[-400:]}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") == counter:
+                    rows.append((int(row["Dispatch_Id"]), row["Kernel_Name"], float(row["Counter_Value"])))
+    return sorted(rows)
+
+
+def measure_traffic(up_blocks, dn_blocks, x, reps: int = 3) -> dict:
+    """HBM bytes per launch of the two matvecs: FETCH_SIZE and WRITE_SIZE (KiB per dispatch, two
+    separate rocprofv3 passes), each scaled by the same counter's reading for the calibration copy
+    (COPY_BYTES read and COPY_BYTES written). The child dispatches the copies, then `reps` up
+    matvecs, then `reps` down matvecs."""
+    if shutil.which("rocprofv3") is None:
+        return {"error": "rocprofv3 not found"}
+    workdir = tempfile.mkdtemp(prefix="tsr_pmc_")
+    try:
+        np.save(os.path.join(workdir, "up.npy"), up_blocks)
+        np.save(os.path.join(workdir, "dn.npy"), dn_blocks)
+        np.save(os.path.join(workdir, "x.npy"), x)
+        res = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            rows = _pmc_pass(counter, workdir)
+            copy = [v for _, k, v in rows if "copyBuffer" in k]
+            mv = [v for _, k, v in rows if "k_mv_q4k" in k]
+            if not copy or len(mv) != 2 * reps:
+                raise RuntimeError(f"{counter}: unexpected dispatches {[(k, v) for _, k, v in rows][:12]}")
+            cal = COPY_BYTES / (float(np.median(copy)) * 1024.0)   # true bytes per counted byte
+            res[counter] = {"calibration_factor": round(cal, 4), "copy_KiB": float(np.median(copy)),
+                            "up": float(np.median(mv[:reps])) * 1024.0 * cal,
+                            "down": float(np.median(mv[reps:])) * 1024.0 * cal}
+        return res
+    finally:
+        shutil.rmtree(workdir, ignore_errors=True)
 
 
 def main() -> int:
@@ -164,7 +244,11 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=0, help="distinct weight copies (0: enough for 2x MALL)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configs")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
+    ap.add_argument("--pmc-child", metavar="DIR", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.pmc_child:
+        return pmc_child(args.pmc_child)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is a "
                                    "design note in DESIGN.md, not measured)"}))
@@ -179,6 +263,13 @@ def main() -> int:
     up_blocks = S.quantize_q4_k(S.normal(S.seed_of("cfg2", "w_up"), N_up * K_up, 0.02).reshape(N_up, K_up))
     dn_blocks = S.quantize_q4_k(S.normal(S.seed_of("cfg2", "w_down"), N_dn * K_dn, 0.02).reshape(N_dn, K_dn))
     x = S.normal(S.seed_of("cfg2", "x"), K_up)
+    # traffic passes first: child processes under rocprofv3, before this process touches the GPU
+    traffic = None
+    if not args.no_traffic:
+        try:
+            traffic = measure_traffic(up_blocks, dn_blocks, x)
+        except Exception as e:  # reported, not fatal: the timing below does not depend on it
+            traffic = {"error": str(e)[:300]}
     per_copy = up_blocks.nbytes + dn_blocks.nbytes
     copies = args.copies or max(2, -(-2 * MALL_BYTES // per_copy))
     ups = [dev.weight(1, up_blocks, N_up, K_up) for _ in range(copies)]
@@ -221,6 +312,10 @@ def main() -> int:
     kern = [("k_mv_q4k (up 14336x4096)", up_ms, mv_bytes(N_up, K_up)),
             ("k_mv_q4k (down 4096x14336)", dn_ms, mv_bytes(N_dn, K_dn))]
     name, kms, kbytes = max(kern, key=lambda r: r[1])
+    tag = "up" if "(up" in name else "down"
+    traffic_bytes = None
+    if traffic and "error" not in traffic and tag in traffic.get("FETCH_SIZE", {}) and tag in traffic.get("WRITE_SIZE", {}):
+        traffic_bytes = round(traffic["FETCH_SIZE"][tag] + traffic["WRITE_SIZE"][tag])
     achieved = kbytes / (kms * 1e-3) / 1e9
 
     y = yb.read(np.float32, (N_dn,))
@@ -247,7 +342,8 @@ def main() -> int:
                    "shapes": "W_up 14336x4096, W_down 4096x14336", "weight_copies": copies,
                    "copy_bytes": per_copy, "device": info["arch"], "n_cu": info["n_cu"]},
         "roofline": {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_bytes,
+                     "traffic_detail": traffic,
                      "launch_us": round(kms * 1e3, 3), "algorithmic_bytes": kbytes,
                      "other_kernels": {n: {"launch_us": round(t * 1e3, 3), "GB/s": round(b / (t * 1e-3) / 1e9, 1)}
                                        for n, t, b in kern}},

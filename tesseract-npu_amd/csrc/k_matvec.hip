@@ -1,50 +1,37 @@
 // k_matvec.hip -- decode MUL_MAT (matrix-vector) kernels for Q8_0 and Q4_K weights on gfx950.
 //
-// Numerics (sw/sim/tsr_ref.c:525-635; docs/spec.md:438-477): per row, term i of block / super-block i
-// is added into partial p[i mod 16] in order, then y = ((p0+p1)+(p2+p3))+... (the 16-partial tree);
-// Q8_0 term = (d Dx) f32(isum), Q4_K term = (d Dx) f32(isum) - (dmin Dx) f32(msum). The integer sums
-// are exact in any order, so they are split over lanes freely; the f32 adds keep the reference's
-// pairing: each partial is owned by one lane group and the tree is a butterfly whose pairs are the
-// tree's pairs (f32 addition is commutative).
+// Numerics (sw/sim/tsr_ref.c:525-635; docs/spec.md:438-477): per row, the term of block (Q8_0) or
+// super-block (Q4_K) s is added into partial p[s mod 16] in order of s, then y = ((p0+p1)+(p2+p3))+...
+// (the 16-partial tree). Q8_0 term = (d Dx) f32(isum); Q4_K term = (d Dx) f32(isum) -
+// (dmin Dx) f32(msum) with isum = sum_j sc_j S_j and msum = sum_j m_j (bs[2j] + bs[2j+1]).
 //
-// Each wave first issues the loads of its slice of x and of all its weight rows (16-byte coalesced
-// loads, one 1 KiB wave load per instruction), then the workgroup quantizes x into LDS (QACT) while
-// the weights stream in; the rows are then reduced with v_dot4_i32_i8 and DPP.
+// Work split. A workgroup of 16 waves owns a contiguous range of rows; wave w computes the terms
+// of the blocks s = w + 16 k (the blocks of partial p[w]) of every row in the range. The weight
+// layout (wlayout.hpp) stores exactly these blocks of 16 consecutive rows contiguously, so a wave
+// load of (4 slots x 16 rows) lanes reads 256-byte runs. A lane computes a whole term: the integer
+// sums stay in its registers and need no cross-lane reduction. Each wave quantizes the blocks of x
+// it uses (QACT into its own LDS area), so no workgroup barrier separates the weight stream from
+// the compute. The terms go to LDS; after the only barriers, the partials are summed in the order
+// of s and the tree runs once per row.
 //
 // Fast and exact f32 paths. With f32 denormals on and no FMA contraction, plain IEEE operations give
 // the spec result whenever no operand or result is subnormal; NaN payloads are the only other
-// difference and the stored y is canonicalized. Every term is (d Dx) f32(int) with d an fp16 value
-// (|d| >= 2^-24 or 0) and |Dx| >= 2^-24 (A32: an fp16 value) or, for A256, checked per row of x:
-// when every nonzero |Dx| >= 2^-60, every nonzero term and partial sum is a multiple of 2^-107 and
-// so never subnormal. Otherwise (tiny A256 scales) the kernel takes the exact path with the spec
-// operations on every step.
+// difference and the stored y is canonicalized. A term is (d Dx) f32(int) [- (dmin Dx) f32(int)]
+// with d, dmin fp16 values (0 or >= 2^-24 in magnitude) and Dx an fp16 value (A32) or, for A256,
+// any f32. When every nonzero |Dx| >= 2^-60, every product d Dx is 0 or a normal multiple of
+// 2^-107, and so is every term and every sum of terms: nothing is ever subnormal. A wave that
+// quantizes a block with 0 < |Dx| < 2^-60 computes its terms with the spec operations, and then the
+// partial sums and the tree of the workgroup do too.
 #include "kernels.hpp"
 #include "qact.hpp"
+#include "wlayout.hpp"
+
+#include <algorithm>
 
 namespace tsr {
 
-// Scales of the device meta (see q4k_meta_encode in tsr_hip.hip): bytes 4-11 hold sc_j | (m_j & 3) << 6,
-// bytes 12-15 the nibbles m_j >> 2. Lane piece h (group g = h / 2) needs sc_2g, sc_2g+1 and m_h.
-struct Q4kLane {
-    uint32_t sc_sh, m_sh, mh_sh;   // bit offsets inside the selected words
-    bool sc_w2, m_w2;              // scales in bytes 8-11 (j >= 4)
-};
-__device__ __forceinline__ Q4kLane q4k_lane(int h) {
-    const int g = h >> 1;
-    Q4kLane l;
-    l.sc_w2 = g >= 2;
-    l.sc_sh = 16u * (uint32_t)(g & 1);
-    l.m_w2 = h >= 4;
-    l.m_sh = 8u * (uint32_t)(h & 3) + 6u;
-    l.mh_sh = 4u * (uint32_t)h;
-    return l;
-}
-__device__ __forceinline__ void q4k_scales(const Q4kLane & l, uint4 mt, int & sc_lo, int & sc_hi, int & mn) {
-    const uint32_t ws = l.sc_w2 ? mt.z : mt.y, wm = l.m_w2 ? mt.z : mt.y;
-    sc_lo = (int)__builtin_amdgcn_ubfe(ws, l.sc_sh, 6);
-    sc_hi = (int)__builtin_amdgcn_ubfe(ws, l.sc_sh + 8u, 6);
-    mn = (int)(__builtin_amdgcn_ubfe(wm, l.m_sh, 2) | (__builtin_amdgcn_ubfe(mt.w, l.mh_sh, 4) << 2));
-}
+constexpr int kMvWaves = 16;
+constexpr uint32_t kXq4Stride = 272u;   // LDS bytes per quantized 256-value block (k slots on distinct banks)
 
 __device__ __forceinline__ void store_y(const MvArgs & a, uint32_t t, uint32_t row, float v) {
     float * yp = a.y + (size_t)t * a.y_stride + row;
@@ -53,337 +40,378 @@ __device__ __forceinline__ void store_y(const MvArgs & a, uint32_t t, uint32_t r
     *yp = v;
 }
 
-// ---------------------------------------------------------------------------------------------
-// Q4_K. A block of W waves owns W * R consecutive rows, R per wave. Every wave first issues all
-// weight loads of its R rows, then the block quantizes x into LDS (QACT A256) while those loads are
-// in flight. Lane L, load i covers quant chunk c = 64 i + L (16 bytes) of a row: super-block
-// s = c / 8, piece h = c % 8 of its 128 quant bytes, i.e. group g = h / 2 (sub-block 2g in the low
-// nibbles, 2g+1 in the high nibbles), half h % 2. Eight lanes hold a super-block; its term goes to
-// partial s mod 16 = 8 (i mod 2) + L / 8, kept in pa (i even) / pb (i odd) of the row.
-// ---------------------------------------------------------------------------------------------
-template <int NL, int R, int WMAX, bool ISUMS>
-__global__ __launch_bounds__(64 * WMAX) void k_mv_q4k(MvArgs a) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    const uint32_t K = a.K, nsb = K / 256u;
-    int8_t * s_qs = (int8_t *)lds;
-    float * s_dx = (float *)(lds + K);
-    int * s_bsp = (int *)(s_dx + nsb);                          // sum of the 32 q of each sub-block
-    const int lane = (int)__lane_id(), wave = (int)(threadIdx.x >> 6), nw = (int)(blockDim.x >> 6);
-    const uint32_t t = blockIdx.y;
-    const float * x = a.x + (size_t)t * a.x_stride;
-    const uint32_t row0 = (blockIdx.x * (uint32_t)nw + (uint32_t)wave) * R;
-    const uint32_t nchunk = nsb * 8u;
-
-    // x slices of this wave's QACT blocks first: the vector-memory counter retires in order, so
-    // loads issued before the weight loads can be waited for without waiting for the weights
-    constexpr int XP = 4;
-    float4 xv[XP];
-#pragma unroll
-    for (int k = 0; k < XP; ++k) {
-        const uint32_t s = min((uint32_t)wave + (uint32_t)(k * nw), nsb - 1u);   // clamped: no branch
-        xv[k] = *(const float4 *)(x + 256u * s + 4u * (uint32_t)lane);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    // weight loads: rows and chunks beyond the matrix read a clamped (valid) address; their values
-    // are never used (masked below), which keeps the load sequence free of branches
-    uint4 qv[R][NL], mv[R][NL];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t row = min(row0 + (uint32_t)r, a.N - 1u);
-        const uint8_t * rq = a.wq + (size_t)row * nsb * 128u;
-        const uint8_t * rm = a.wm + (size_t)row * nsb * 16u;
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const uint32_t c = min(64u * (uint32_t)i + (uint32_t)lane, nchunk - 1u);
-            qv[r][i] = *(const uint4 *)(rq + 16u * c);
-            mv[r][i] = *(const uint4 *)(rm + 16u * (c >> 3));
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    int slow = 0;
-    auto qact_sb = [&](uint32_t s, const float4 v) {
-        float d;
-        int s4;
-        const uint32_t q = qact_a256_lane(v, lane, &d, &s4);
-        *(uint32_t *)(s_qs + 256u * s + 4u * (uint32_t)lane) = q;
-        const int s32 = sum8_i(s4);
-        if (lane == 0) s_dx[s] = d;
-        if ((lane & 7) == 0) s_bsp[8u * s + (uint32_t)(lane >> 3)] = s32;
-        const uint32_t ad = fb(d) & 0x7FFFFFFFu;
-        slow |= (ad != 0u && ad < 0x21800000u) ? 1 : 0;          // 0 < |d| < 2^-60
-    };
-#pragma unroll
-    for (int k = 0; k < XP; ++k) {
-        const uint32_t s = (uint32_t)wave + (uint32_t)(k * nw);
-        if (s < nsb) qact_sb(s, xv[k]);
-    }
-    for (uint32_t s = (uint32_t)wave + (uint32_t)(XP * nw); s < nsb; s += (uint32_t)nw)
-        qact_sb(s, *(const float4 *)(x + 256u * s + 4u * (uint32_t)lane));
-    slow = __syncthreads_or(slow);
-    if (row0 >= a.N) return;
-
-    const int h = lane & 7, g = h >> 1, half = h & 1;
-    const Q4kLane ql = q4k_lane(h);
-    float pa[R], pb[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) { pa[r] = 0.0f; pb[r] = 0.0f; }
-#pragma unroll
-    for (int i = 0; i < NL; ++i) {
-        const uint32_t c = 64u * (uint32_t)i + (uint32_t)lane;
-        const uint32_t s = c >> 3;
-        const bool valid = c < nchunk;
-        int4 xl = make_int4(0, 0, 0, 0), xh = make_int4(0, 0, 0, 0);
-        int bsp = 0;
-        float dx = 0.0f;
-        if (valid) {
-            xl = *(const int4 *)(s_qs + 256u * s + 64u * (uint32_t)g + 16u * (uint32_t)half);
-            xh = *(const int4 *)(s_qs + 256u * s + 64u * (uint32_t)g + 32u + 16u * (uint32_t)half);
-            bsp = s_bsp[8u * s + (uint32_t)h];
-            dx = s_dx[s];
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint32_t m4 = 0x0F0F0F0Fu;
-            const uint4 qw = qv[r][i], mt = mv[r][i];
-            int slo = dot4((int)(qw.x & m4), xl.x, 0);
-            slo = dot4((int)(qw.y & m4), xl.y, slo);
-            slo = dot4((int)(qw.z & m4), xl.z, slo);
-            slo = dot4((int)(qw.w & m4), xl.w, slo);
-            int shi = dot4((int)((qw.x >> 4) & m4), xh.x, 0);
-            shi = dot4((int)((qw.y >> 4) & m4), xh.y, shi);
-            shi = dot4((int)((qw.z >> 4) & m4), xh.z, shi);
-            shi = dot4((int)((qw.w >> 4) & m4), xh.w, shi);
-            int sc_lo, sc_hi, mn;
-            q4k_scales(ql, mt, sc_lo, sc_hi, mn);
-            const int ip = sum8_i(__mul24(sc_lo, slo) + __mul24(sc_hi, shi));   // |operands| < 2^23: v_mul_i32_i24
-            const int mp = sum8_i(__mul24(mn, bsp));
-            const uint32_t row = row0 + (uint32_t)r;
-            if (ISUMS && t == 0u && h == 0 && valid && row < a.N) {
-                a.isums[(size_t)row * 2u * nsb + 2u * s] = ip;
-                a.isums[(size_t)row * 2u * nsb + 2u * s + 1u] = mp;
-            }
-            const float d = h2f_fast(mt.x & 0xFFFFu), dm = h2f_fast(mt.x >> 16);
-            float tt;
-            if (!slow) {
-                const float t1 = (d * dx) * (float)ip;
-                const float t2 = (dm * dx) * (float)mp;
-                tt = t1 - t2;
-            } else {
-                tt = ssub(smul(smul(d, dx), i2f(ip)), smul(smul(dm, dx), i2f(mp)));
-            }
-            if (valid) {
-                if (i & 1) pb[r] = slow ? sadd(pb[r], tt) : pb[r] + tt;
-                else pa[r] = slow ? sadd(pa[r], tt) : pa[r] + tt;
-            }
-        }
-    }
-    // tree: slots L/8 pair by xor 1, 2, 4 of the slot (lanes xor 8, 16, 32); pa = p0..p7, pb = p8..p15
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t row = row0 + (uint32_t)r;
-        float qa_ = pa[r], qb_ = pb[r], y;
+// Partial p[w] of every row of the workgroup, by wave w from its own terms in LDS (s_t[row][s], nb
+// terms per row): p = ((+0 + t_w) + t_w+16) + ... in order of s. The same wave wrote those terms,
+// and the LDS executes one wave's operations in order, so no workgroup barrier is needed here.
+__device__ __forceinline__ void mv_wave_partials(const WGeom & g, const float * s_t, float * s_p, uint32_t nrow,
+                                                 uint32_t w, bool slow) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t cw = wl_count(g, w);
+    for (uint32_t rl = __lane_id(); rl < nrow; rl += 64u) {
+        const float * tr = s_t + (size_t)rl * g.nb + w;
+        float p = 0.0f;
         if (!slow) {
-            qa_ = qa_ + dpp_f<kDppRowMirror>(qa_);
-            qb_ = qb_ + dpp_f<kDppRowMirror>(qb_);
-            qa_ = qa_ + xor16_f(qa_);
-            qb_ = qb_ + xor16_f(qb_);
-            qa_ = qa_ + xor32_f(qa_);
-            qb_ = qb_ + xor32_f(qb_);
-            y = canon(qa_ + qb_);
+            for (uint32_t k = 0; k < cw; ++k) p = p + tr[16u * k];
         } else {
-            qa_ = sadd(qa_, dpp_f<kDppRowMirror>(qa_));
-            qb_ = sadd(qb_, dpp_f<kDppRowMirror>(qb_));
-            qa_ = sadd(qa_, xor16_f(qa_));
-            qb_ = sadd(qb_, xor16_f(qb_));
-            qa_ = sadd(qa_, xor32_f(qa_));
-            qb_ = sadd(qb_, xor32_f(qb_));
-            y = sadd(qa_, qb_);
+            for (uint32_t k = 0; k < cw; ++k) p = sadd(p, tr[16u * k]);
         }
-        if (lane == 0 && row < a.N) store_y(a, t, row, y);
+        s_p[16u * rl + w] = p;
     }
 }
 
+// After a workgroup barrier: the 16-partial tree of each row on an aligned 16-lane row of threads
+// (lane i holds p[i]; the DPP pairs xor 1, xor 2, half mirror, mirror are the tree's pairs, and
+// f32 addition is commutative), then y. Every thread of the workgroup calls it.
+__device__ __forceinline__ void mv_tree_store(const MvArgs & a, const float * s_p, uint32_t nrow, uint32_t row_lo,
+                                              uint32_t t, bool slow) {
+    for (uint32_t base = 0; base < nrow * 16u; base += blockDim.x) {   // uniform trip count
+        const uint32_t idx = base + threadIdx.x, rl = idx >> 4;
+        float v = rl < nrow ? s_p[idx] : 0.0f;
+        if (!slow) {
+            v = v + dpp_f<kDppXor1>(v);
+            v = v + dpp_f<kDppXor2>(v);
+            v = v + dpp_f<kDppRowHalfMirror>(v);
+            v = v + dpp_f<kDppRowMirror>(v);
+            v = canon(v);
+        } else {
+            v = sadd(v, dpp_f<kDppXor1>(v));
+            v = sadd(v, dpp_f<kDppXor2>(v));
+            v = sadd(v, dpp_f<kDppRowHalfMirror>(v));
+            v = sadd(v, dpp_f<kDppRowMirror>(v));
+        }
+        if ((idx & 15u) == 0u && rl < nrow) store_y(a, t, row_lo + rl, v);
+    }
+}
+
+// The unit of lane `lane` in pass p: unit u = 4 p + lane / 16 of the wave's ngrp * cnt units
+// (group-major), row = 16 G + lane % 16. Rows outside [row_lo, row_hi) load a row of the same group
+// that is inside (the cache lines of a valid lane); units beyond the last, and every unit of a wave
+// without blocks (cnt == 0), load a valid address and are not used.
+struct MvUnit {
+    uint32_t G, k, row, rowc;
+    bool valid;
+};
+__device__ __forceinline__ MvUnit mv_unit(uint32_t p, int lane, uint32_t cnt, uint32_t nunit, uint32_t G0,
+                                          uint32_t row_lo, uint32_t row_hi) {
+    const uint32_t u = 4u * p + ((uint32_t)lane >> 4);
+    const uint32_t uc = min(u, (nunit ? nunit : 1u) - 1u), cc = cnt ? cnt : 1u;
+    MvUnit m;
+    const uint32_t gi = uc / cc;
+    m.k = uc - gi * cc;
+    m.G = G0 + gi;
+    m.row = 16u * m.G + ((uint32_t)lane & 15u);
+    m.valid = u < nunit && m.row >= row_lo && m.row < row_hi;
+    m.rowc = min(max(m.row, row_lo), row_hi - 1u);
+    return m;
+}
+
 // ---------------------------------------------------------------------------------------------
-// Q8_0. A block of W waves owns W * R consecutive rows, R per wave; loads first, then QACT A32 into
-// LDS. Lane L, load i covers quant chunk c = 64 i + L: block b = 32 i + L / 2, half L % 2. Blocks b
-// (lane L < 32) and b + 16 (lane L + 32) both belong to partial b mod 16 = (L / 2) mod 16, in that
-// order; the lower half of the wave owns the partials.
+// Q4_K. LDS: x quants [16 waves][kx][272 B] | sub-block sums [16][kx][8] int | d [16][kx] |
+// terms [rb][nsb] | partials [rb][16] | slow flags [16].
+// Lane unit = (row, super-block): 8 quant loads (piece j: group g = j / 2, low nibbles = values
+// 64g + 16 (j % 2) + 0..15, high nibbles = the same + 32) and one meta load.
 // ---------------------------------------------------------------------------------------------
-template <int NL, int R, int WMAX, bool ISUMS>
-__global__ __launch_bounds__(64 * WMAX) void k_mv_q80(MvArgs a) {
+template <int P, bool ISUMS>      // P: passes whose loads are in registers at once
+__global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const uint32_t K = a.K, nb = K / 32u;
-    int8_t * s_qs = (int8_t *)lds;
-    float * s_dx = (float *)(lds + K);
-    const int lane = (int)__lane_id(), wave = (int)(threadIdx.x >> 6), nw = (int)(blockDim.x >> 6);
+    const WGeom g = wgeom(a.N, a.K >> 8);
+    const uint32_t nsb = g.nb, kx = g.q + (g.rem ? 1u : 0u);
+    const int lane = (int)__lane_id();
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), cnt = wl_count(g, w);
     const uint32_t t = blockIdx.y;
     const float * x = a.x + (size_t)t * a.x_stride;
-    const uint32_t row0 = (blockIdx.x * (uint32_t)nw + (uint32_t)wave) * R;
+    const uint32_t row_lo = blockIdx.x * a.rb, row_hi = min(a.N, row_lo + a.rb), nrow = row_hi - row_lo;
+    const uint32_t G0 = row_lo >> 4, ngrp = ((row_hi - 1u) >> 4) - G0 + 1u;
+    const uint32_t nunit = ngrp * cnt, npass = (nunit + 3u) >> 2;
+    int8_t * s_xq = (int8_t *)lds;
+    int * s_xb = (int *)(lds + kMvWaves * kx * kXq4Stride);
+    float * s_xd = (float *)(s_xb + kMvWaves * kx * 8u);
+    float * s_t = s_xd + kMvWaves * kx;
+    float * s_p = s_t + ((a.rb * nsb + 3u) & ~3u);                // 16-byte aligned
+    int * s_slow = (int *)(s_p + a.rb * 16u);
 
-    constexpr int XP = 4;                                        // x slots first (see k_mv_q4k)
-    float4 xv[XP];
+    // x first (vector-memory counters retire in order): the 16-lane row h = lane / 16 of the wave
+    // holds block k = 4 i + h of round i, lane i of the row its values 16 i .. 16 i + 15
+    const uint32_t h4 = (uint32_t)lane >> 4, l16 = (uint32_t)lane & 15u;
+    auto load_x = [&](uint32_t i, float4 (&xr)[4]) {
+        const uint32_t s = min(w + 16u * (4u * i + h4), nsb - 1u);
 #pragma unroll
-    for (int k = 0; k < XP; ++k) {
-        const uint32_t slot = min(threadIdx.x + (uint32_t)k * blockDim.x, K / 4u - 1u);
-        xv[k] = *(const float4 *)(x + 4u * slot);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    uint4 qv[R][NL];
-    uint32_t dv[R][NL];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {                                // clamped addresses, as in k_mv_q4k
-        const uint32_t row = min(row0 + (uint32_t)r, a.N - 1u);
-        const uint8_t * rq = a.wq + (size_t)row * nb * 32u;
-        const uint16_t * rm = (const uint16_t *)(a.wm + (size_t)row * nb * 2u);
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const uint32_t c = min(64u * (uint32_t)i + (uint32_t)lane, 2u * nb - 1u);
-            qv[r][i] = *(const uint4 *)(rq + 16u * c);
-            dv[r][i] = rm[c >> 1];
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    auto qact_slot = [&](uint32_t slot, const float4 v) {       // 8 lanes per 32-block
-        float D;
-        const uint32_t q = qact_a32_lane(v, &D);
-        *(uint32_t *)(s_qs + 4u * slot) = q;
-        if ((lane & 7) == 0) s_dx[slot >> 3] = D;
+        for (int c = 0; c < 4; ++c) xr[c] = *(const float4 *)(x + 256u * s + 16u * l16 + 4u * (uint32_t)c);
     };
-#pragma unroll
-    for (int k = 0; k < XP; ++k) {
-        const uint32_t slot = threadIdx.x + (uint32_t)k * blockDim.x;
-        if (slot < K / 4u) qact_slot(slot, xv[k]);
-    }
-    for (uint32_t slot = threadIdx.x + (uint32_t)XP * blockDim.x; slot < K / 4u; slot += blockDim.x)
-        qact_slot(slot, *(const float4 *)(x + 4u * slot));
-    __syncthreads();
-    if (row0 >= a.N) return;
+    float4 xv[4];
+    load_x(0u, xv);
+    __builtin_amdgcn_sched_barrier(0);
 
-    float p[R];
+    uint4 qv[P][8], mv[P];
+    auto load = [&](uint32_t p0) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) p[r] = 0.0f;
+        for (int pp = 0; pp < P; ++pp) {
+            const MvUnit m = mv_unit(min(p0 + (uint32_t)pp, npass ? npass - 1u : 0u), lane, cnt, nunit, G0, row_lo, row_hi);
+            const uint32_t sl = min(wl_slot(g, w, m.k), nsb - 1u), r = m.rowc & 15u;
+            mv[pp] = *(const uint4 *)(a.wm + q4k_meta_off(g, m.G, sl, r));
 #pragma unroll
-    for (int i = 0; i < NL; ++i) {
-        const uint32_t c = 64u * (uint32_t)i + (uint32_t)lane, b = c >> 1;
-        int4 xv = make_int4(0, 0, 0, 0);
-        float dx = 0.0f;
-        if (b < nb) {
-            xv = *(const int4 *)(s_qs + 16u * c);
-            dx = s_dx[b];
+            for (uint32_t j = 0; j < 8u; ++j) qv[pp][j] = *(const uint4 *)(a.wq + q4k_quant_off(g, m.G, j, sl, r));
         }
+    };
+    // QACT A256 of the wave's blocks s = w + 16 k, four at a time. Round 0 is outside the loop: a
+    // loop whose body loads makes the compiler wait for every outstanding load at its header, and
+    // round 0 must wait only for the x loads issued before the weights.
+    bool tiny_any = false;
+    auto qact_round = [&](uint32_t i, const float4 (&xr)[4]) {
+        float d;
+        int s16;
+        bool tiny;
+        const uint4 qq = qact_a256_row(xr, &d, &s16, &tiny);
+        const int s32 = s16 + dpp_i<kDppXor1>(s16);               // sum of the 32 quants of a sub-block
+        const uint32_t k = 4u * i + h4;
+        if (k < cnt) {
+            const uint32_t xo = w * kx + k;
+            *(uint4 *)(s_xq + xo * kXq4Stride + 16u * l16) = qq;
+            if ((l16 & 1u) == 0u) s_xb[xo * 8u + (l16 >> 1)] = s32;
+            if (l16 == 0u) s_xd[xo] = d;
+            tiny_any |= tiny;
+        }
+    };
+    // Waves 8..15 quantize their first round before they issue their weight loads: the weight
+    // stream of a compute unit is accepted at the rate HBM delivers it, so these waves would wait
+    // to issue anyway, and their QACT is then off the critical path. Waves 0..7 keep the memory
+    // pipe busy from the start and quantize while their loads are in flight.
+    if (w >= 8u && cnt) qact_round(0u, xv);
+    load(0u);                                                     // unconditional (clamped)
+    __builtin_amdgcn_sched_barrier(0);
+    if (w < 8u && cnt) qact_round(0u, xv);
+    for (uint32_t i = 1; 4u * i < cnt; ++i) {                     // K > 16384 only
+        float4 xr[4];
+        load_x(i, xr);
+        qact_round(i, xr);
+    }
+    const bool slow = __ballot(tiny_any) != 0ull;                 // wave-uniform
+
+    const uint32_t m4 = 0x0F0F0F0Fu;
+    for (uint32_t p0 = 0; p0 < npass; p0 += P) {
+        if (p0) load(p0);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            int is = dot4((int)qv[r][i].x, xv.x, 0);
-            is = dot4((int)qv[r][i].y, xv.y, is);
-            is = dot4((int)qv[r][i].z, xv.z, is);
-            is = dot4((int)qv[r][i].w, xv.w, is);
-            is += dpp_i<kDppXor1>(is);
-            const uint32_t row = row0 + (uint32_t)r;
-            if (ISUMS && t == 0u && (lane & 1) == 0 && b < nb && row < a.N) a.isums[(size_t)row * nb + b] = is;
-            const float tt = (h2f_fast(dv[r][i]) * dx) * (float)is;
-            const float tu = xor32_f(tt);
-            if (lane < 32) {
-                if (b < nb) p[r] = p[r] + tt;
-                if (b + 16u < nb) p[r] = p[r] + tu;
+        for (int pp = 0; pp < P; ++pp) {
+            if (p0 + (uint32_t)pp >= npass) break;
+            const MvUnit m = mv_unit(p0 + (uint32_t)pp, lane, cnt, nunit, G0, row_lo, row_hi);
+            const uint32_t xo = w * kx + m.k;
+            const int8_t * xb = s_xq + xo * kXq4Stride;
+            int S[8];
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) {
+                int lo = 0, hi = 0;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const uint4 qw = qv[pp][2 * gg + hh];
+                    const int4 xl = *(const int4 *)(xb + 64 * gg + 16 * hh);
+                    const int4 xh = *(const int4 *)(xb + 64 * gg + 32 + 16 * hh);
+                    lo = dot4((int)(qw.x & m4), xl.x, lo);
+                    lo = dot4((int)(qw.y & m4), xl.y, lo);
+                    lo = dot4((int)(qw.z & m4), xl.z, lo);
+                    lo = dot4((int)(qw.w & m4), xl.w, lo);
+                    hi = dot4((int)((qw.x >> 4) & m4), xh.x, hi);
+                    hi = dot4((int)((qw.y >> 4) & m4), xh.y, hi);
+                    hi = dot4((int)((qw.z >> 4) & m4), xh.z, hi);
+                    hi = dot4((int)((qw.w >> 4) & m4), xh.w, hi);
+                }
+                S[2 * gg] = lo;
+                S[2 * gg + 1] = hi;
+            }
+            const int4 b0 = *(const int4 *)(s_xb + xo * 8u), b1 = *(const int4 *)(s_xb + xo * 8u + 4u);
+            const int bs[8] = { b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w };
+            const float dx = s_xd[xo];
+            // scales: byte 4 + j = sc_j | (m_j & 3) << 6; nibble j of bytes 12..15 = m_j >> 2
+            const uint4 mt = mv[pp];
+            int isum = 0, msum = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < 8u; ++j) {
+                const uint32_t wd = j < 4u ? mt.y : mt.z, sh = 8u * (j & 3u);
+                const int sc = (int)__builtin_amdgcn_ubfe(wd, sh, 6);
+                const int mn = (int)(__builtin_amdgcn_ubfe(wd, sh + 6u, 2) | (__builtin_amdgcn_ubfe(mt.w, 4u * j, 4) << 2));
+                isum += __mul24(sc, S[j]);                        // |S_j| < 2^16, sc < 64: v_mad_i32_i24
+                msum += __mul24(mn, bs[j]);
+            }
+            const float d = h2f_fast(mt.x & 0xFFFFu), dm = h2f_fast(mt.x >> 16);
+            float tt;
+            if (!slow) tt = (d * dx) * (float)isum - (dm * dx) * (float)msum;
+            else tt = ssub(smul(smul(d, dx), i2f(isum)), smul(smul(dm, dx), i2f(msum)));
+            const uint32_t s = w + 16u * m.k;
+            if (m.valid) {
+                s_t[(m.row - row_lo) * nsb + s] = tt;
+                if (ISUMS && t == 0u) {
+                    a.isums[(size_t)m.row * 2u * nsb + 2u * s] = isum;
+                    a.isums[(size_t)m.row * 2u * nsb + 2u * s + 1u] = msum;
+                }
             }
         }
     }
+    mv_wave_partials(g, s_t, s_p, nrow, w, slow);
+    if (lane == 0) s_slow[w] = slow ? 1 : 0;
+    lds_barrier();
+    bool any_slow = false;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        float v = p[r];
-        v = v + dpp_f<kDppXor2>(v);
-        v = v + dpp_f<kDppRowHalfMirror>(v);
-        v = v + dpp_f<kDppRowMirror>(v);
-        v = v + xor16_f(v);
-        const uint32_t row = row0 + (uint32_t)r;
-        if (lane == 0 && row < a.N) store_y(a, t, row, canon(v));
+    for (int i = 0; i < kMvWaves; ++i) any_slow |= s_slow[i] != 0;
+    mv_tree_store(a, s_p, nrow, row_lo, t, any_slow);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Q8_0. LDS: x quants [16 waves][kx][32 B] | D [16][kx] | terms [rb][nb] | partials [rb][16].
+// Lane unit = (row, block): two 16-byte quant loads and the fp16 scale. The A32 activation scale is
+// an fp16 value, so every term is exact with plain IEEE operations.
+// ---------------------------------------------------------------------------------------------
+template <int P, bool ISUMS>
+__global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const WGeom g = wgeom(a.N, a.K >> 5);
+    const uint32_t nb = g.nb, kx = g.q + (g.rem ? 1u : 0u);
+    const int lane = (int)__lane_id();
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), cnt = wl_count(g, w);
+    const uint32_t t = blockIdx.y;
+    const float * x = a.x + (size_t)t * a.x_stride;
+    const uint32_t row_lo = blockIdx.x * a.rb, row_hi = min(a.N, row_lo + a.rb), nrow = row_hi - row_lo;
+    const uint32_t G0 = row_lo >> 4, ngrp = ((row_hi - 1u) >> 4) - G0 + 1u;
+    const uint32_t nunit = ngrp * cnt, npass = (nunit + 3u) >> 2;
+    int8_t * s_xq = (int8_t *)lds;
+    float * s_xd = (float *)(lds + kMvWaves * kx * 32u);
+    float * s_t = s_xd + kMvWaves * kx;
+    float * s_p = s_t + ((a.rb * nb + 3u) & ~3u);                 // 16-byte aligned
+
+    // x: 8 lanes per block; round i covers blocks k = 8 i + lane / 8 of this wave
+    constexpr int XP = 2;
+    float4 xv[XP];
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+        const uint32_t k = 8u * (uint32_t)i + ((uint32_t)lane >> 3);
+        const uint32_t b = min(w + 16u * k, nb - 1u);
+        xv[i] = *(const float4 *)(x + 32u * b + 4u * ((uint32_t)lane & 7u));
     }
+    __builtin_amdgcn_sched_barrier(0);
+
+    uint4 q0[P], q1[P];
+    uint32_t dv[P];
+    auto load = [&](uint32_t p0) {
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp) {
+            const MvUnit m = mv_unit(min(p0 + (uint32_t)pp, npass ? npass - 1u : 0u), lane, cnt, nunit, G0, row_lo, row_hi);
+            const uint32_t sl = min(wl_slot(g, w, m.k), nb - 1u), r = m.rowc & 15u;
+            q0[pp] = *(const uint4 *)(a.wq + q80_quant_off(g, m.G, 0u, sl, r));
+            q1[pp] = *(const uint4 *)(a.wq + q80_quant_off(g, m.G, 1u, sl, r));
+            dv[pp] = *(const uint16_t *)(a.wm + q80_meta_off(g, m.G, sl, r));
+        }
+    };
+    load(0u);                                                     // unconditional: no join before QACT
+    __builtin_amdgcn_sched_barrier(0);
+
+    auto qact_round = [&](uint32_t i, const float4 v) {
+        const uint32_t k = 8u * i + ((uint32_t)lane >> 3);
+        float D;
+        const uint32_t qq = qact_a32_lane(v, &D);
+        if (k < cnt) {
+            *(uint32_t *)(s_xq + (w * kx + k) * 32u + 4u * ((uint32_t)lane & 7u)) = qq;
+            if ((lane & 7) == 0) s_xd[w * kx + k] = D;
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < XP; ++i)
+        if (8u * (uint32_t)i < cnt) qact_round((uint32_t)i, xv[i]);
+    for (uint32_t i = XP; 8u * i < cnt; ++i) {
+        const uint32_t k = 8u * i + ((uint32_t)lane >> 3);
+        const uint32_t b = min(w + 16u * k, nb - 1u);
+        qact_round(i, *(const float4 *)(x + 32u * b + 4u * ((uint32_t)lane & 7u)));
+    }
+
+    for (uint32_t p0 = 0; p0 < npass; p0 += P) {
+        if (p0) load(p0);
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp) {
+            if (p0 + (uint32_t)pp >= npass) break;
+            const MvUnit m = mv_unit(p0 + (uint32_t)pp, lane, cnt, nunit, G0, row_lo, row_hi);
+            const uint32_t xo = w * kx + m.k;
+            const int4 xa = *(const int4 *)(s_xq + xo * 32u), xb = *(const int4 *)(s_xq + xo * 32u + 16u);
+            int is = dot4((int)q0[pp].x, xa.x, 0);
+            is = dot4((int)q0[pp].y, xa.y, is);
+            is = dot4((int)q0[pp].z, xa.z, is);
+            is = dot4((int)q0[pp].w, xa.w, is);
+            is = dot4((int)q1[pp].x, xb.x, is);
+            is = dot4((int)q1[pp].y, xb.y, is);
+            is = dot4((int)q1[pp].z, xb.z, is);
+            is = dot4((int)q1[pp].w, xb.w, is);
+            const float tt = (h2f_fast(dv[pp]) * s_xd[xo]) * (float)is;
+            const uint32_t b = w + 16u * m.k;
+            if (m.valid) {
+                s_t[(m.row - row_lo) * nb + b] = tt;
+                if (ISUMS && t == 0u) a.isums[(size_t)m.row * nb + b] = is;
+            }
+        }
+    }
+    mv_wave_partials(g, s_t, s_p, nrow, w, false);
+    lds_barrier();
+    mv_tree_store(a, s_p, nrow, row_lo, t, false);
 }
 
 }  // namespace tsr
 
 // ---- launchers ------------------------------------------------------------------------------------
-// R rows per wave and W waves per block: about one block per compute unit with up to 16 waves, R
-// as small as that allows (more waves hide more latency), capped so the weight registers of R rows
-// (R * NL loads per lane) fit the register budget of WMAX waves per compute unit.
-struct MvShape {
-    uint32_t R, W;
-};
-static MvShape mv_shape(uint32_t N, uint32_t NL, uint32_t regs_per_load, uint32_t n_cu) {
-    const uint32_t per_cu = (N + n_cu - 1u) / n_cu;
-    uint32_t R = 1u;
-    while (R < 8u && R * 16u < per_cu && 2u * R * NL * regs_per_load <= 64u) R *= 2u;
-    uint32_t W = (per_cu + R - 1u) / R;
-    W = W < 1u ? 1u : (W > 16u ? 16u : W);
-    return { R, W };
+// One workgroup of 16 waves per rb consecutive rows, rb = ceil(N / n_cu) (at least 16), so that every
+// compute unit holds one workgroup with its whole share of the matrix; rb is lowered when the terms
+// would not fit the LDS budget.
+static size_t mv_lds_rows(uint32_t rb, uint32_t nb) {   // terms (16-byte padded) and partials
+    return 4u * ((((size_t)rb * nb + 3u) & ~(size_t)3u) + 16u * (size_t)rb);
+}
+static uint32_t mv_rows_per_block(uint32_t N, uint32_t nb, uint32_t n_cu, size_t lds_fixed) {
+    uint32_t rb = (N + n_cu - 1u) / n_cu;
+    if (rb < 16u) rb = 16u;
+    while (rb > 1u && lds_fixed + mv_lds_rows(rb, nb) > 120u * 1024u) rb = (rb + 1u) / 2u;
+    return rb;
 }
 
-template <int NL, int R>
-static void launch_q4k(const tsr::MvArgs & a, uint32_t W, size_t lds, hipStream_t s) {
-    constexpr int WMAX = (R * NL * 8 <= 64) ? 16 : 8;
-    if (W > (uint32_t)WMAX) W = WMAX;
-    const dim3 grid((a.N + W * R - 1u) / (W * R), a.T);
-    if (a.isums) hipLaunchKernelGGL((tsr::k_mv_q4k<NL, R, WMAX, true>), grid, dim3(64u * W), lds, s, a);
-    else hipLaunchKernelGGL((tsr::k_mv_q4k<NL, R, WMAX, false>), grid, dim3(64u * W), lds, s, a);
-}
-template <int NL, int R>
-static void launch_q80(const tsr::MvArgs & a, uint32_t W, size_t lds, hipStream_t s) {
-    constexpr int WMAX = (R * NL * 5 <= 80) ? 16 : 8;
-    if (W > (uint32_t)WMAX) W = WMAX;
-    const dim3 grid((a.N + W * R - 1u) / (W * R), a.T);
-    if (a.isums) hipLaunchKernelGGL((tsr::k_mv_q80<NL, R, WMAX, true>), grid, dim3(64u * W), lds, s, a);
-    else hipLaunchKernelGGL((tsr::k_mv_q80<NL, R, WMAX, false>), grid, dim3(64u * W), lds, s, a);
-}
-
-template <int NL>
-static void dispatch_q4k(const tsr::MvArgs & a, MvShape sh, size_t lds, hipStream_t s) {
-    if constexpr (NL <= 1) { if (sh.R >= 8u) return launch_q4k<NL, 8>(a, sh.W, lds, s); }
-    if constexpr (NL <= 2) { if (sh.R >= 4u) return launch_q4k<NL, 4>(a, sh.W, lds, s); }
-    if constexpr (NL <= 4) { if (sh.R >= 2u) return launch_q4k<NL, 2>(a, sh.W, lds, s); }
-    launch_q4k<NL, 1>(a, sh.W, lds, s);
-}
-template <int NL>
-static void dispatch_q80(const tsr::MvArgs & a, MvShape sh, size_t lds, hipStream_t s) {
-    if constexpr (NL <= 1) { if (sh.R >= 8u) return launch_q80<NL, 8>(a, sh.W, lds, s); }
-    if constexpr (NL <= 2) { if (sh.R >= 4u) return launch_q80<NL, 4>(a, sh.W, lds, s); }
-    if constexpr (NL <= 4) { if (sh.R >= 2u) return launch_q80<NL, 2>(a, sh.W, lds, s); }
-    launch_q80<NL, 1>(a, sh.W, lds, s);
-}
-
-#define TSR_CASE(f, n) case n: f<n>(a, sh, lds, s); break;
-
-int tsr_launch_mv_q4_k(const tsr::MvArgs & a, uint32_t n_cu, hipStream_t s) {
-    const uint32_t nsb = a.K / 256u, NL = (nsb + 7u) / 8u;
-    const size_t lds = (size_t)a.K + 4u * nsb + 32u * nsb;
-    const MvShape sh = mv_shape(a.N, NL, 8u, n_cu);
-    switch (NL) {
-        TSR_CASE(dispatch_q4k, 1) TSR_CASE(dispatch_q4k, 2) TSR_CASE(dispatch_q4k, 3) TSR_CASE(dispatch_q4k, 4)
-        TSR_CASE(dispatch_q4k, 5) TSR_CASE(dispatch_q4k, 6) TSR_CASE(dispatch_q4k, 7) TSR_CASE(dispatch_q4k, 8)
-        TSR_CASE(dispatch_q4k, 9) TSR_CASE(dispatch_q4k, 10) TSR_CASE(dispatch_q4k, 11) TSR_CASE(dispatch_q4k, 12)
-        TSR_CASE(dispatch_q4k, 13) TSR_CASE(dispatch_q4k, 14) TSR_CASE(dispatch_q4k, 15) TSR_CASE(dispatch_q4k, 16)
-        default: return -2;
+// The largest number of 4-unit passes of any wave: ngrp * ceil(nb / 16) units for the workgroup
+// whose rows touch the most 16-row groups.
+static uint32_t mv_max_pass(uint32_t N, uint32_t rb, uint32_t nb) {
+    uint32_t ngrp = 0;
+    for (uint32_t lo = 0; lo < N; lo += rb) {
+        const uint32_t hi = std::min(N, lo + rb);
+        ngrp = std::max(ngrp, ((hi - 1u) >> 4) - (lo >> 4) + 1u);
+        if (lo >= 64u * rb) break;                               // the pattern of row_lo mod 16 repeats
     }
+    return (ngrp * ((nb + 15u) / 16u) + 3u) / 4u;
+}
+
+template <int P>
+static void launch_q4k(const tsr::MvArgs & a, dim3 grid, size_t lds, hipStream_t s) {
+    if (a.isums) hipLaunchKernelGGL((tsr::k_mv_q4k<P, true>), grid, dim3(1024), lds, s, a);
+    else hipLaunchKernelGGL((tsr::k_mv_q4k<P, false>), grid, dim3(1024), lds, s, a);
+}
+template <int P>
+static void launch_q80(const tsr::MvArgs & a, dim3 grid, size_t lds, hipStream_t s) {
+    if (a.isums) hipLaunchKernelGGL((tsr::k_mv_q80<P, true>), grid, dim3(1024), lds, s, a);
+    else hipLaunchKernelGGL((tsr::k_mv_q80<P, false>), grid, dim3(1024), lds, s, a);
+}
+
+int tsr_launch_mv_q4_k(const tsr::MvArgs & a0, uint32_t n_cu, hipStream_t s) {
+    tsr::MvArgs a = a0;
+    const uint32_t nsb = a.K / 256u, kx = (nsb + 15u) / 16u;
+    const size_t fixed = (size_t)tsr::kMvWaves * kx * (tsr::kXq4Stride + 32u + 4u) + 64u;
+    a.rb = mv_rows_per_block(a.N, nsb, n_cu, fixed);
+    const size_t lds = fixed + mv_lds_rows(a.rb, nsb);
+    const dim3 grid((a.N + a.rb - 1u) / a.rb, a.T);
+    launch_q4k<1>(a, grid, lds, s);                               // 36 load registers per pass
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-int tsr_launch_mv_q8_0(const tsr::MvArgs & a, uint32_t n_cu, hipStream_t s) {
-    const uint32_t nb = a.K / 32u, NL = (nb + 31u) / 32u;
-    const size_t lds = (size_t)a.K + 4u * nb;
-    const MvShape sh = mv_shape(a.N, NL, 5u, n_cu);
-    switch (NL) {
-        TSR_CASE(dispatch_q80, 1) TSR_CASE(dispatch_q80, 2) TSR_CASE(dispatch_q80, 3) TSR_CASE(dispatch_q80, 4)
-        TSR_CASE(dispatch_q80, 5) TSR_CASE(dispatch_q80, 6) TSR_CASE(dispatch_q80, 7) TSR_CASE(dispatch_q80, 8)
-        TSR_CASE(dispatch_q80, 9) TSR_CASE(dispatch_q80, 10) TSR_CASE(dispatch_q80, 11) TSR_CASE(dispatch_q80, 12)
-        TSR_CASE(dispatch_q80, 13) TSR_CASE(dispatch_q80, 14) TSR_CASE(dispatch_q80, 15) TSR_CASE(dispatch_q80, 16)
-        TSR_CASE(dispatch_q80, 17) TSR_CASE(dispatch_q80, 18) TSR_CASE(dispatch_q80, 19) TSR_CASE(dispatch_q80, 20)
-        TSR_CASE(dispatch_q80, 21) TSR_CASE(dispatch_q80, 22) TSR_CASE(dispatch_q80, 23) TSR_CASE(dispatch_q80, 24)
-        TSR_CASE(dispatch_q80, 25) TSR_CASE(dispatch_q80, 26) TSR_CASE(dispatch_q80, 27) TSR_CASE(dispatch_q80, 28)
-        TSR_CASE(dispatch_q80, 29) TSR_CASE(dispatch_q80, 30) TSR_CASE(dispatch_q80, 31) TSR_CASE(dispatch_q80, 32)
-        default: return -2;
-    }
+int tsr_launch_mv_q8_0(const tsr::MvArgs & a0, uint32_t n_cu, hipStream_t s) {
+    tsr::MvArgs a = a0;
+    const uint32_t nb = a.K / 32u, kx = (nb + 15u) / 16u;
+    const size_t fixed = (size_t)tsr::kMvWaves * kx * (32u + 4u);
+    a.rb = mv_rows_per_block(a.N, nb, n_cu, fixed);
+    const size_t lds = fixed + mv_lds_rows(a.rb, nb);
+    const dim3 grid((a.N + a.rb - 1u) / a.rb, a.T);
+    const uint32_t mp = mv_max_pass(a.N, a.rb, nb);
+    if (mp <= 1u) launch_q80<1>(a, grid, lds, s);
+    else if (mp <= 2u) launch_q80<2>(a, grid, lds, s);
+    else if (mp <= 4u) launch_q80<4>(a, grid, lds, s);
+    else launch_q80<8>(a, grid, lds, s);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }

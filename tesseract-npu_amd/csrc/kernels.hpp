@@ -30,6 +30,7 @@ struct MvArgs {
     int32_t * isums;         // nullable: per-block integer sums of token 0 (checking)
     uint32_t N, K, T;
     uint32_t acc;            // y = FA(y_old, v)
+    uint32_t rb;             // rows per workgroup (set by the launcher)
 };
 
 // A KV plane (see k_kv.hip for the layout).

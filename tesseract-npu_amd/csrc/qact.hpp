@@ -102,4 +102,73 @@ __device__ __forceinline__ uint32_t qact_a256_lane(const float4 v, int lane, flo
     return packed;
 }
 
+// Max / min / or over an aligned 16-lane row (every lane of the row gets the result).
+__device__ __forceinline__ uint32_t row16_umax(uint32_t m) {
+    m = umax_u(m, (uint32_t)dpp_i<kDppXor1>((int)m));
+    m = umax_u(m, (uint32_t)dpp_i<kDppXor2>((int)m));
+    m = umax_u(m, (uint32_t)dpp_i<kDppRowHalfMirror>((int)m));
+    return umax_u(m, (uint32_t)dpp_i<kDppRowMirror>((int)m));
+}
+__device__ __forceinline__ uint32_t row16_umin(uint32_t m) {
+    m = min(m, (uint32_t)dpp_i<kDppXor1>((int)m));
+    m = min(m, (uint32_t)dpp_i<kDppXor2>((int)m));
+    m = min(m, (uint32_t)dpp_i<kDppRowHalfMirror>((int)m));
+    return min(m, (uint32_t)dpp_i<kDppRowMirror>((int)m));
+}
+__device__ __forceinline__ uint32_t row16_or(uint32_t m) {
+    m |= (uint32_t)dpp_i<kDppXor1>((int)m);
+    m |= (uint32_t)dpp_i<kDppXor2>((int)m);
+    m |= (uint32_t)dpp_i<kDppRowHalfMirror>((int)m);
+    return m | (uint32_t)dpp_i<kDppRowMirror>((int)m);
+}
+
+// One A256 block held by an aligned 16-lane row: lane i of the row holds values 16 i .. 16 i + 15
+// (v[0..3]); the four rows of a wave quantize four blocks at once. Every lane of the wave must be
+// active. Returns the lane's 16 quants (bytes in value order); *d = the block's d (every lane of
+// the row); *s16 = the sum of the lane's 16 quants; *tiny = 0 < |d| < 2^-60.
+// First largest |x|: the row maximum of the lane maxima, then the lowest lane of the row holding it
+// (its own first largest), fetched with an OR over the row (every other lane contributes 0).
+// The plain product iscale x rounds like FM(iscale, x) when the block's amax >= 2^-60 (see
+// qact_a32_lane); if any row of the wave has 0 < amax < 2^-60 the whole wave uses FM.
+__device__ __forceinline__ uint4 qact_a256_row(const float4 (&v)[4], float * d, int * s16, bool * tiny) {
+    float xs[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { xs[4 * i] = v[i].x; xs[4 * i + 1] = v[i].y; xs[4 * i + 2] = v[i].z; xs[4 * i + 3] = v[i].w; }
+    uint32_t m = 0;
+    float best = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t a = mag_bits(xs[i]);
+        if (a <= 0x7F800000u && a > m) { m = a; best = daz(xs[i]); }
+    }
+    const uint32_t amax = row16_umax(m);
+    const uint32_t l16 = __lane_id() & 15u;
+    const uint32_t win = row16_umin(m == amax ? l16 : 16u);
+    const float mx = bf(row16_or(l16 == win ? fb(best) : 0u));
+    const bool zero = amax == 0u;
+    const bool exact = __ballot(!zero && amax < 0x21800000u) != 0ull;   // wave-uniform
+    const float iscale = zero ? 0.0f : sdiv(-127.0f, mx);
+    int q[16];
+    if (!exact) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) q[i] = round_even8(iscale * xs[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) q[i] = round_even8(smul(iscale, xs[i]));
+    }
+    uint32_t pk[4] = { 0u, 0u, 0u, 0u };
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        s += q[i];
+        pk[i >> 2] |= ((uint32_t)q[i] & 0xFFu) << (8 * (i & 3));
+    }
+    const float dd = zero ? 0.0f : srcp(iscale);
+    const uint32_t ad = fb(dd) & 0x7FFFFFFFu;
+    *d = dd;
+    *s16 = s;
+    *tiny = ad != 0u && ad < 0x21800000u;
+    return make_uint4(pk[0], pk[1], pk[2], pk[3]);
+}
+
 }  // namespace tsr

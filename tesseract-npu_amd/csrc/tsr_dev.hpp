@@ -76,19 +76,23 @@ __device__ __forceinline__ uint32_t f2h_exact(float f) {
 
 // QACT f32 -> int8: NaN -> 0; |x| >= 256 saturates; else round (half away: A32, half even: A256)
 // and clamp to [-128, 127] (sw/sim/tsr_ref.c:200-232).
-// Straight-line forms: NaN is replaced by 0 first, the clamp then saturates Inf and |x| >= 256.
+// v_cvt_i32_f32 converts NaN to 0 and saturates out-of-range values (Inf included) to INT_MIN /
+// INT_MAX; the integer clamp then gives the int8 saturation. Written in asm because a C++
+// float-to-int conversion of NaN or of an out-of-range value is undefined.
+__device__ __forceinline__ int32_t cvt_i32_sat(float x) {
+    int32_t r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+__device__ __forceinline__ int32_t clamp8(int32_t v) { return min(max(v, -128), 127); }
 __device__ __forceinline__ int32_t round_away8(float x) {
-    const float v = __builtin_isnan(x) ? 0.0f : x;
-    const float t = __builtin_truncf(v);
-    const float fr = v - t;                                   // exact (|v| >= 2^23 is integral; Inf gives NaN)
-    const float up = __builtin_fabsf(fr) >= 0.5f ? __builtin_copysignf(1.0f, v) : 0.0f;
-    const float r = __builtin_fminf(__builtin_fmaxf(t + up, -128.0f), 127.0f);
-    return (int32_t)r;
+    const float t = __builtin_truncf(x);
+    const float fr = x - t;                                   // exact; NaN for NaN and Inf inputs
+    const float up = __builtin_fabsf(fr) >= 0.5f ? __builtin_copysignf(1.0f, x) : 0.0f;
+    return clamp8(cvt_i32_sat(t + up));                       // NaN -> 0, +-Inf -> 127 / -128
 }
 __device__ __forceinline__ int32_t round_even8(float x) {
-    const float v = __builtin_isnan(x) ? 0.0f : x;
-    const float r = __builtin_fminf(__builtin_fmaxf(__builtin_rintf(v), -128.0f), 127.0f);   // rintf: ties to even
-    return (int32_t)r;
+    return clamp8(cvt_i32_sat(__builtin_rintf(x)));          // rintf: ties to even
 }
 
 // ---- wave64 exchange ----------------------------------------------------------------------------
@@ -126,5 +130,18 @@ __device__ __forceinline__ int sum8_i(int v) {
 
 // Byte-wise signed dot product of 4 int8 pairs plus an accumulator (v_dot4_i32_i8).
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// Workgroup barrier that orders LDS only. It waits for this wave's LDS (and scalar) operations
+// (s_waitcnt lgkmcnt(0); the vmcnt and expcnt fields are left at their maxima), then s_barrier.
+// Global loads still in flight stay in flight: __syncthreads() is a release/acquire fence and
+// waits for every outstanding vector-memory operation first, which would serialize a kernel's
+// compute behind its whole weight stream. The signal fences keep the compiler from moving memory
+// operations across the barrier. Use it only where the barrier publishes LDS data.
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 }  // namespace tsr

@@ -15,6 +15,7 @@
 
 #include "kernels.hpp"
 #include "runtime.hpp"
+#include "wlayout.hpp"
 
 // ---------------------------------------------------------------------------------------------
 // errors
@@ -182,7 +183,7 @@ int tsr_hip_memset(tsr_hip_ctx * ctx, void * dst_dev, int value, size_t bytes) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// weights: ggml blocks <-> device layout (meta region | quant region, both row-contiguous)
+// weights: ggml blocks <-> the device layout of wlayout.hpp (meta region | quant region)
 // ---------------------------------------------------------------------------------------------
 namespace {
 
@@ -242,27 +243,38 @@ int tsr_hip_weight_upload(tsr_hip_ctx * ctx, uint32_t fmt, const void * ggml_blo
     *out = nullptr;
     if (fmt != TSR_HIP_FMT_Q8_0 && fmt != TSR_HIP_FMT_Q4_K) return TSR_HIP_E_FMT;
     if (N == 0u || K == 0u || K % blk_values(fmt) != 0u || K > kKMax) return TSR_HIP_E_SHAPE;
-    const size_t nb = K / blk_values(fmt);
-    const size_t meta_bytes = (size_t)N * nb * blk_meta(fmt);
+    const uint32_t nb = K / blk_values(fmt);
+    const tsr::WGeom g = tsr::wgeom(N, nb);
+    const size_t rows = 16u * (size_t)g.ng;                       // padded to whole row groups
+    const size_t meta_bytes = rows * nb * blk_meta(fmt);
     const size_t quant_off = (meta_bytes + 255u) & ~(size_t)255u;
-    const size_t quant_bytes = (size_t)N * nb * blk_quant(fmt);
+    const size_t quant_bytes = rows * nb * blk_quant(fmt);
     std::vector<uint8_t> host;
     try {
-        host.resize(quant_off + quant_bytes);
+        host.assign(quant_off + quant_bytes, 0u);                 // padding rows stay zero
     } catch (...) {
         return TSR_HIP_E_NOMEM;
     }
     const uint8_t * src = (const uint8_t *)ggml_blocks;
-    const uint32_t bb = blk_bytes(fmt), bm = blk_meta(fmt), bq = blk_quant(fmt);
+    uint8_t * hm = host.data(), * hq = host.data() + quant_off;
+    const uint32_t bb = blk_bytes(fmt);
     parallel_rows(N, [&](uint32_t lo, uint32_t hi) {
-        for (size_t r = lo; r < hi; ++r)
-            for (size_t i = 0; i < nb; ++i) {
-                const uint8_t * b = src + (r * nb + i) * bb;
-                uint8_t * m = host.data() + (r * nb + i) * bm;
-                memcpy(m, b, bm);
-                if (fmt == TSR_HIP_FMT_Q4_K) q4k_meta_encode(b + 4, m + 4);
-                memcpy(host.data() + quant_off + (r * nb + i) * bq, b + bm, bq);
+        for (uint32_t n = lo; n < hi; ++n) {
+            const uint32_t G = n >> 4, r = n & 15u;
+            for (uint32_t s = 0; s < nb; ++s) {
+                const uint8_t * b = src + ((size_t)n * nb + s) * bb;
+                const uint32_t sl = tsr::wl_slot_of(g, s);
+                if (fmt == TSR_HIP_FMT_Q4_K) {
+                    uint8_t * m = hm + tsr::q4k_meta_off(g, G, sl, r);
+                    memcpy(m, b, 4);
+                    q4k_meta_encode(b + 4, m + 4);
+                    for (uint32_t j = 0; j < 8u; ++j) memcpy(hq + tsr::q4k_quant_off(g, G, j, sl, r), b + 16u + 16u * j, 16);
+                } else {
+                    memcpy(hm + tsr::q80_meta_off(g, G, sl, r), b, 2);
+                    for (uint32_t h = 0; h < 2u; ++h) memcpy(hq + tsr::q80_quant_off(g, G, h, sl, r), b + 2u + 16u * h, 16);
+                }
             }
+        }
     });
     auto * w = new (std::nothrow) tsr_hip_weight();
     if (w == nullptr) return TSR_HIP_E_NOMEM;
@@ -295,17 +307,27 @@ int tsr_hip_weight_read(tsr_hip_ctx * ctx, const tsr_hip_weight * w, void * ggml
         if (rc == 0) rc = hip_err(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
         if (rc) return rc;
     }
-    const size_t nb = w->K / blk_values(w->fmt);
-    const uint32_t bb = blk_bytes(w->fmt), bm = blk_meta(w->fmt), bq = blk_quant(w->fmt);
+    const uint32_t nb = w->K / blk_values(w->fmt), bb = blk_bytes(w->fmt);
+    const tsr::WGeom g = tsr::wgeom(w->N, nb);
+    const uint8_t * hm = host.data(), * hq = host.data() + w->quant_off;
     uint8_t * dst = (uint8_t *)ggml_blocks;
     parallel_rows(w->N, [&](uint32_t lo, uint32_t hi) {
-        for (size_t r = lo; r < hi; ++r)
-            for (size_t i = 0; i < nb; ++i) {
-                uint8_t * b = dst + (r * nb + i) * bb;
-                memcpy(b, host.data() + (r * nb + i) * bm, bm);
-                if (w->fmt == TSR_HIP_FMT_Q4_K) q4k_meta_decode(host.data() + (r * nb + i) * bm + 4, b + 4);
-                memcpy(b + bm, host.data() + w->quant_off + (r * nb + i) * bq, bq);
+        for (uint32_t n = lo; n < hi; ++n) {
+            const uint32_t G = n >> 4, r = n & 15u;
+            for (uint32_t s = 0; s < nb; ++s) {
+                uint8_t * b = dst + ((size_t)n * nb + s) * bb;
+                const uint32_t sl = tsr::wl_slot_of(g, s);
+                if (w->fmt == TSR_HIP_FMT_Q4_K) {
+                    const uint8_t * m = hm + tsr::q4k_meta_off(g, G, sl, r);
+                    memcpy(b, m, 4);
+                    q4k_meta_decode(m + 4, b + 4);
+                    for (uint32_t j = 0; j < 8u; ++j) memcpy(b + 16u + 16u * j, hq + tsr::q4k_quant_off(g, G, j, sl, r), 16);
+                } else {
+                    memcpy(b, hm + tsr::q80_meta_off(g, G, sl, r), 2);
+                    for (uint32_t h = 0; h < 2u; ++h) memcpy(b + 2u + 16u * h, hq + tsr::q80_quant_off(g, G, h, sl, r), 16);
+                }
             }
+        }
     });
     return TSR_HIP_OK;
 }

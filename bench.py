@@ -11,7 +11,8 @@ Honest HBM numbers: the step rotates through distinct device copies of the weigh
 exceeds twice the 256 MB Infinity Cache, so weight reads come from HBM.
 
 Output: one JSON line (metric, value = algorithmic weight+activation bytes per step / time,
-roofline of the dominant kernel measured live with HIP events on the launch stream, and the CPU
+roofline of the dominant kernel measured live with HIP events on the launch stream (the timed
+steps are replayed from a captured HIP graph, as a decode loop runs them), and the CPU
 baseline: this repository's oracle (the reference's numerics restated in C) on the host cores).
 """
 from __future__ import annotations
@@ -42,7 +43,7 @@ METRIC = "decode tok/s (8B Q4_K, ctx 4096); matvec/attn HBM GB/s as % of peak"
 
 
 class HipEvents:
-    """hipEvent timing on a given stream (libamdhip64 via ctypes)."""
+    """hipEvent timing and hipGraph capture / replay on a given stream (libamdhip64 via ctypes)."""
 
     def __init__(self):
         self.h = C.CDLL("libamdhip64.so")
@@ -51,6 +52,12 @@ class HipEvents:
         self.h.hipEventSynchronize.argtypes = [C.c_void_p]
         self.h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
         self.h.hipDeviceSynchronize.argtypes = []
+        self.h.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        self.h.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+        self.h.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+        self.h.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        self.h.hipGraphExecDestroy.argtypes = [C.c_void_p]
+        self.h.hipGraphDestroy.argtypes = [C.c_void_p]
 
     def event(self):
         e = C.c_void_p()
@@ -68,6 +75,40 @@ class HipEvents:
 
     def device_sync(self):
         assert self.h.hipDeviceSynchronize() == 0
+
+    def capture(self, stream, fn, n: int):
+        """A graph of fn(0) .. fn(n - 1) as launched on `stream` (relaxed capture mode)."""
+        assert self.h.hipStreamBeginCapture(stream, 2) == 0
+        for i in range(n):
+            fn(i)
+        g, ge = C.c_void_p(), C.c_void_p()
+        assert self.h.hipStreamEndCapture(stream, C.byref(g)) == 0
+        assert self.h.hipGraphInstantiate(C.byref(ge), g, None, None, 0) == 0
+        return g, ge
+
+    def graph_ms(self, stream, fn, n: int, replays: int = 3) -> tuple:
+        """Milliseconds per call of fn over n calls replayed from one graph: the median of `replays`
+        timed replays after one untimed replay; also the eager (host-launched) time of n calls."""
+        g, ge = self.capture(stream, fn, n)
+        try:
+            assert self.h.hipGraphLaunch(ge, stream) == 0
+            self.device_sync()
+            a, b = self.event(), self.event()
+            times = []
+            for _ in range(replays):
+                self.record(a, stream)
+                assert self.h.hipGraphLaunch(ge, stream) == 0
+                self.record(b, stream)
+                times.append(self.elapsed_ms(a, b) / n)
+            self.record(a, stream)
+            for i in range(n):
+                fn(i)
+            self.record(b, stream)
+            eager = self.elapsed_ms(a, b) / n
+            return float(np.median(times)), eager
+        finally:
+            self.h.hipGraphExecDestroy(ge)
+            self.h.hipGraphDestroy(g)
 
 
 def mv_bytes(N: int, K: int) -> int:
@@ -103,14 +144,10 @@ def extra_workloads(dev, ev, stream, n: int) -> dict:
     n = max(n, 100)
 
     def timed(fn):
-        a, b = ev.event(), ev.event()
         for i in range(5):
             fn(i)
-        ev.record(a, stream)
-        for i in range(n):
-            fn(i)
-        ev.record(b, stream)
-        return ev.elapsed_ms(a, b) / n
+        ev.device_sync()
+        return ev.graph_ms(stream, fn, n)
 
     # Q8_0 4864 x 896
     N, K = 4864, 896
@@ -120,9 +157,10 @@ def extra_workloads(dev, ev, stream, n: int) -> dict:
     ws = [dev.weight(0, blocks, N, K) for _ in range(copies)]
     xb = dev.upload(S.normal(S.seed_of("cfg1", "x"), K))
     yb = dev.alloc(4 * N)
-    ms = timed(lambda i: dev.mul_mat(ws[i % copies], xb, 1, K, yb, N, stream=stream))
+    ms, ms_eager = timed(lambda i: dev.mul_mat(ws[i % copies], xb, 1, K, yb, N, stream=stream))
     nbytes = N * (K // 32) * 34 + 4 * K + 4 * N
-    out["q8_0_matvec_4864x896"] = {"us_per_call": round(ms * 1e3, 3), "algorithmic_bytes": nbytes,
+    out["q8_0_matvec_4864x896"] = {"us_per_call": round(ms * 1e3, 3), "us_per_call_eager": round(ms_eager * 1e3, 3),
+                                   "algorithmic_bytes": nbytes,
                                    "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
                                    "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                    "copies": copies}
@@ -151,10 +189,11 @@ def extra_workloads(dev, ev, stream, n: int) -> dict:
     ob = dev.alloc(4 * n_head * D)
     msum = tsr_hip.msum_build_f16(np.zeros((1, n_kv), np.float16))
     scale = np.float32(1.0 / np.sqrt(D))
-    ms = timed(lambda i: dev.flash_attn(qb, 1, n_head * D, caches[i % copies][0], caches[i % copies][1], D,
-                                        n_head, n_kv_head, scale, msum, ob, n_head * D, stream=stream))
+    ms, ms_eager = timed(lambda i: dev.flash_attn(qb, 1, n_head * D, caches[i % copies][0], caches[i % copies][1], D,
+                                                  n_head, n_kv_head, scale, msum, ob, n_head * D, stream=stream))
     nbytes = 2 * n_kv * E // 32 * 34 + 2 * n_head * D + 4 * n_head * D
-    out["fa_decode_q8kv_8192_32q8kv_d128"] = {"us_per_call": round(ms * 1e3, 3), "algorithmic_bytes": nbytes,
+    out["fa_decode_q8kv_8192_32q8kv_d128"] = {"us_per_call": round(ms * 1e3, 3), "us_per_call_eager": round(ms_eager * 1e3, 3),
+                                              "algorithmic_bytes": nbytes,
                                               "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
                                               "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                               "copies": copies, "launches_per_call": 3}
@@ -285,30 +324,39 @@ def main() -> int:
     for i in range(args.warmup):
         step(i)
     ev.device_sync()
+    # The K timed steps are one captured graph (the launch-bound decode loop as a serving engine
+    # runs it); one untimed replay first, whose output must equal the eager result bit for bit.
+    g, ge = ev.capture(stream, step, args.steps)
+    assert ev.h.hipGraphLaunch(ge, stream) == 0
+    ev.device_sync()
+    y_graph = yb.read(np.float32, (N_dn,))
+    step(args.steps - 1)
+    ev.device_sync()
+    if not np.array_equal(y_graph.view(np.uint32), yb.read(np.float32, (N_dn,)).view(np.uint32)):
+        print(json.dumps({"error": "graph replay differs from the eager step"}))
+        return 1
     e0, e1 = ev.event(), ev.event()
+    ev.device_sync()
+    ev.record(e0, stream)
+    assert ev.h.hipGraphLaunch(ge, stream) == 0
+    ev.record(e1, stream)
+    ms = ev.elapsed_ms(e0, e1)
+    ev.device_sync()
+    ev.h.hipGraphExecDestroy(ge)
+    ev.h.hipGraphDestroy(g)
+    ms_step = ms / args.steps
     ev.record(e0, stream)
     for i in range(args.steps):
         step(i)
     ev.record(e1, stream)
-    ms = ev.elapsed_ms(e0, e1)
-    ev.device_sync()
-    ms_step = ms / args.steps
+    ms_step_eager = ev.elapsed_ms(e0, e1) / args.steps
     step_bytes = mv_bytes(N_up, K_up) + mv_bytes(N_dn, K_dn)
 
-    # per-kernel launch durations (HIP events on the launch stream), each over rotating copies
-    def time_kernel(fn, n):
-        a, b = ev.event(), ev.event()
-        for i in range(5):
-            fn(i)
-        ev.record(a, stream)
-        for i in range(n):
-            fn(i)
-        ev.record(b, stream)
-        return ev.elapsed_ms(a, b) / n
-
+    # per-kernel launch durations (HIP events on the launch stream, graph replay), each over
+    # rotating copies
     n_k = max(50, args.steps)
-    up_ms = time_kernel(lambda i: dev.mul_mat(ups[i % copies], xb, 1, K_up, hb, N_up, stream=stream), n_k)
-    dn_ms = time_kernel(lambda i: dev.mul_mat(dns[i % copies], hb, 1, K_dn, yb, N_dn, stream=stream), n_k)
+    up_ms, _ = ev.graph_ms(stream, lambda i: dev.mul_mat(ups[i % copies], xb, 1, K_up, hb, N_up, stream=stream), n_k)
+    dn_ms, _ = ev.graph_ms(stream, lambda i: dev.mul_mat(dns[i % copies], hb, 1, K_dn, yb, N_dn, stream=stream), n_k)
     kern = [("k_mv_q4k (up 14336x4096)", up_ms, mv_bytes(N_up, K_up)),
             ("k_mv_q4k (down 4096x14336)", dn_ms, mv_bytes(N_dn, K_dn))]
     name, kms, kbytes = max(kern, key=lambda r: r[1])
@@ -333,6 +381,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
+        "ms_per_step_eager": round(ms_step_eager, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

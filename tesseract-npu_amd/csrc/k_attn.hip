@@ -28,39 +28,41 @@ namespace tsr {
 constexpr uint32_t kMFloor = 0xF1800000u;   // -2^100 (AT 6.3)
 constexpr uint32_t kLFloor = 0x00800000u;   // 2^-126 (AT 5.7)
 
-// EXPK(v, P1) (VU 6.3; sw/sim/tsr_ref_math.c:78-159), constants from the host (ExpkTab).
-__device__ __forceinline__ float expk(float v, const ExpkTab & e) {
+// EXPK(v, P1) (VU 6.3; sw/sim/tsr_ref_math.c:78-159), constants from the host (ExpkTab). The
+// 2^(j/64) table is read from LDS (t64): an index into the kernel arguments that differs per lane
+// would be a vector load from the argument segment on every call. Straight-line: the special cases
+// are selected at the end, so a wave never splits into branches here.
+__device__ __forceinline__ float expk(float v, const ExpkTab & e, const uint32_t * t64) {
     const uint32_t u = fb(daz(v));
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return bf(kNaN);
-    const bool neg = (u >> 31) != 0u;
     const uint32_t a = u & 0x7FFFFFFFu;
-    const float big = neg ? 0.0f : bf(0x7F800000u);
-    if (a == 0x7F800000u) return big;
-    if (a == 0u) return 1.0f;
+    const bool neg = (u >> 31) != 0u;
     const uint32_t ev = a >> 23;
-    if (ev > 156u) return big;
+    // T = floor(Mv LK / 2^(156 - ev)) for ev <= 156 (larger ev: overflow / underflow below)
     const uint64_t mv = 0x00800000u | (a & 0x007FFFFFu);
-    const uint32_t sh = 156u - ev;
-    const uint64_t T = sh >= 64u ? 0u : (mv * e.lk) >> sh;
-    if (T >= (1ull << 40)) return big;
-    int32_t n;
-    uint32_t F;
-    if (neg) { n = -(int32_t)((T + 0xFFFFFFFFull) >> 32); F = 0u - (uint32_t)T; }
-    else     { n = (int32_t)(T >> 32);                     F = (uint32_t)T; }
+    const uint32_t sh = 156u - min(ev, 156u);
+    const uint64_t prod = mv * e.lk;
+    const uint64_t T = sh >= 64u ? 0ull : (prod >> sh);
+    const uint32_t Thi = (uint32_t)(T >> 32), Tlo = (uint32_t)T;
+    const int32_t n0 = neg ? -(int32_t)(Thi + (Tlo ? 1u : 0u)) : (int32_t)Thi;
+    const uint32_t F = neg ? 0u - Tlo : Tlo;
     const uint64_t G = F & 0x03FFFFFFu;
     const uint64_t pf = (G * (e.c1 + ((G * (e.c2 + ((G * e.c3) >> 32))) >> 32))) >> 32;
-    const uint64_t t = e.t64[F >> 26];
+    const uint64_t t = t64[F >> 26];
     const uint64_t M = t + ((t * pf) >> 32);
-    uint32_t drop = 7u;
-    if (M >= (1ull << 31)) { drop = 8u; n += 1; }
-    uint64_t sig = M >> drop;
-    const uint64_t rem = M & ((1ull << drop) - 1u), half = 1ull << (drop - 1u);
-    if (rem > half || (rem == half && (sig & 1u))) sig += 1u;
-    if (sig == (1ull << 24)) { sig >>= 1; n += 1; }
-    const int32_t be = n + 127;
-    if (be >= 255) return bf(0x7F800000u);
-    if (be <= 0) return 0.0f;
-    return bf(((uint32_t)be << 23) | (uint32_t)(sig & 0x007FFFFFu));
+    const bool hiM = M >= (1ull << 31);
+    const uint32_t drop = hiM ? 8u : 7u;
+    uint32_t sig = (uint32_t)(M >> drop);
+    const uint32_t rem = (uint32_t)M & ((1u << drop) - 1u), half = 1u << (drop - 1u);
+    sig += (rem > half || (rem == half && (sig & 1u))) ? 1u : 0u;
+    const bool carry = sig == (1u << 24);
+    const int32_t be = n0 + (hiM ? 1 : 0) + (carry ? 1 : 0) + 127;
+    const uint32_t mant = (carry ? sig >> 1 : sig) & 0x007FFFFFu;
+    uint32_t r = be >= 255 ? 0x7F800000u : (be <= 0 ? 0u : (((uint32_t)be << 23) | mant));
+    const uint32_t big = neg ? 0u : 0x7F800000u;                  // +Inf, or 0 for large negative v
+    r = (ev > 156u || T >= (1ull << 40) || a == 0x7F800000u) ? big : r;
+    r = a == 0u ? 0x3F800000u : r;
+    r = a > 0x7F800000u ? kNaN : r;
+    return bf(r);
 }
 
 // MAXT (AT 5.4, sw/sim/tsr_ref_at.c:286-292): NaN wins as the canonical NaN; -0 < +0.
@@ -103,41 +105,35 @@ __device__ __forceinline__ int wave_sum_i(int v) {
 }
 
 // RNE_int(w 2^(23 - es)), exponent(w) <= es; zero / subnormal w -> 0 (sw/sim/tsr_ref_at.c:386-410).
+// Straight-line: a shift of 26 or more leaves 0 after rounding (|m| < 2^24), so it is clamped to 31.
 __device__ __forceinline__ int32_t bf_int(float w, int32_t es) {
     const uint32_t u = fb(w), e = (u >> 23) & 0xFFu;
-    if (e == 0u) return 0;
     const uint32_t m = 0x00800000u | (u & 0x007FFFFFu);
-    const int32_t sh = es - ((int32_t)e - 127);
-    uint32_t v;
-    if (sh <= 0) v = m;
-    else if (sh >= 26) v = 0u;
-    else {
-        v = m >> sh;
-        const uint32_t r = m & ((1u << sh) - 1u), h = 1u << (sh - 1);
-        v += (r > h || (r == h && (v & 1u))) ? 1u : 0u;
-    }
-    return (u >> 31) ? -(int32_t)v : (int32_t)v;
+    const int32_t sh0 = es - ((int32_t)e - 127);
+    const uint32_t sh = (uint32_t)min(max(sh0, 0), 31);
+    uint32_t v = m >> sh;
+    const uint32_t r = m & ((1u << sh) - 1u), h = sh ? 1u << (sh - 1u) : 0u;
+    v += (sh && (r > h || (r == h && (v & 1u)))) ? 1u : 0u;
+    const int32_t sv = (u >> 31) ? -(int32_t)v : (int32_t)v;
+    return e == 0u ? 0 : sv;
 }
 // RNE24(A) 2^k; below 2^-126 a signed zero, from 2^128 a signed Inf (sw/sim/tsr_ref_at.c:412-436).
+// Straight-line.
 __device__ __forceinline__ float bf_f(int64_t A, int32_t k) {
-    if (A == 0) return 0.0f;
     const uint32_t s = A < 0 ? 0x80000000u : 0u;
-    uint64_t mag = A < 0 ? (uint64_t)0 - (uint64_t)A : (uint64_t)A;
-    const int32_t msb = 63 - __builtin_clzll(mag);
-    int64_t e = (int64_t)msb + k;
-    if (msb > 23) {
-        const int32_t sh = msb - 23;
-        uint64_t sig = mag >> sh;
-        const uint64_t r = mag & ((1ull << sh) - 1u), h = 1ull << (sh - 1);
-        if (r > h || (r == h && (sig & 1u))) sig += 1u;
-        if (sig >> 24) { sig >>= 1; e += 1; }
-        mag = sig;
-    } else {
-        mag <<= (23 - msb);
-    }
-    if (e < -126) return bf(s);
-    if (e > 127) return bf(s | 0x7F800000u);
-    return bf(s | ((uint32_t)(e + 127) << 23) | ((uint32_t)mag & 0x007FFFFFu));
+    const uint64_t mag = A < 0 ? (uint64_t)0 - (uint64_t)A : (uint64_t)A;
+    const int32_t msb = 63 - (int32_t)__builtin_clzll(mag | 1ull);
+    const uint32_t shr = (uint32_t)max(msb - 23, 0), shl = (uint32_t)max(23 - msb, 0);
+    uint64_t sig = mag >> shr;
+    const uint64_t r = mag & ((1ull << shr) - 1ull), h = shr ? 1ull << (shr - 1u) : 0ull;
+    sig += (shr && (r > h || (r == h && (sig & 1ull)))) ? 1ull : 0ull;
+    const bool carry = (sig >> 24) != 0ull;
+    sig = carry ? sig >> 1 : sig;
+    sig = sig << shl;
+    const int32_t e = msb + k + (carry ? 1 : 0);
+    uint32_t out = s | ((uint32_t)(e + 127) << 23) | ((uint32_t)sig & 0x007FFFFFu);
+    out = e < -126 ? s : (e > 127 ? (s | 0x7F800000u) : out);
+    return bf(A == 0 ? 0u : out);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -145,17 +141,21 @@ __device__ __forceinline__ float bf_f(int64_t A, int32_t k) {
 // values of the KV head's G heads (QACT A32: its 32-blocks never cross a head, so they are the
 // blocks of the whole query row) while the K rows of its cells load.
 // ---------------------------------------------------------------------------------------------
+// The work list is inline in the kernel arguments (INL, decode) or in device memory: a compile-time
+// choice, so that reading an item is never a branch around a load.
+template <bool INL>
 __device__ __forceinline__ FaItem fa_item(const FaArgs & a, const FaPlan & p, uint32_t i) {
-    return a.items ? a.items[i] : p.items[i];
+    if constexpr (INL) return p.items[i];
+    else return a.items[i];
 }
 
-template <int D>
+template <int D, bool INL>
 __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr uint32_t NBD = D / 32u;                             // blocks per head
     constexpr bool KREG = D <= 128;                                // K row of the cell kept in registers
     const uint32_t tt = blockIdx.x % p.maxtiles;
-    const FaItem it = fa_item(a, p, blockIdx.x / p.maxtiles);
+    const FaItem it = fa_item<INL>(a, p, blockIdx.x / p.maxtiles);
     if (tt >= it.ntiles) return;                                  // the item has fewer tiles (block-uniform)
     const uint32_t g = blockIdx.y, G = a.G;
     int8_t * s_q = (int8_t *)lds;                                 // G*D quants of the KV head's query heads
@@ -174,6 +174,13 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
     const uint8_t * kq = a.kc.base + a.kc.quant_off + (size_t)u * 16u * E + (size_t)rr * 16u;
     const uint32_t ci0 = g * D / 16u;                             // first 16-byte chunk of the head
 
+    // the query values of round 0 first (vector-memory counters retire in order: the QACT then waits
+    // for them only, not for the K rows)
+    const float * qrow = a.q + (size_t)it.t * a.q_stride + (size_t)g * G * D;
+    const uint32_t nslot = G * D / 4u;                             // 8 lanes per 32-block
+    const float4 qv0 = *(const float4 *)(qrow + 4u * min(threadIdx.x, nslot - 1u));
+    __builtin_amdgcn_sched_barrier(0);
+
     int4 kr[KREG ? 2 * NBD : 1];
     uint32_t km[NBD];
 #pragma unroll
@@ -184,14 +191,18 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    const float * qrow = a.q + (size_t)it.t * a.q_stride + (size_t)g * G * D;
-    for (uint32_t slot = threadIdx.x; slot < G * D / 4u; slot += blockDim.x) {   // 8 lanes per 32-block
+    auto qact_slot = [&](uint32_t slot, const float4 v) {
         float Dq;
-        const uint32_t qv = qact_a32_lane(*(const float4 *)(qrow + 4u * slot), &Dq);
-        *(uint32_t *)(s_q + 4u * slot) = qv;
-        if ((lane & 7) == 0) s_dx[slot >> 3] = Dq;
-    }
-    __syncthreads();
+        const uint32_t qq = qact_a32_lane(v, &Dq);
+        if (slot < nslot) {
+            *(uint32_t *)(s_q + 4u * slot) = qq;
+            if ((lane & 7) == 0) s_dx[slot >> 3] = Dq;
+        }
+    };
+    qact_slot(threadIdx.x, qv0);
+    for (uint32_t s0 = blockDim.x; s0 < nslot; s0 += blockDim.x)   // G D > 1024 only
+        qact_slot(s0 + threadIdx.x, *(const float4 *)(qrow + 4u * min(s0 + threadIdx.x, nslot - 1u)));
+    lds_barrier();                                                // the K rows stay in flight
 
     float * S = a.S + (size_t)it.s_off * a.n_head;
     for (uint32_t i = 0; i < G; ++i) {
@@ -257,14 +268,15 @@ constexpr int kMaxSeg = 8;                                        // NCG <= 128 
 
 __device__ __forceinline__ float ctree4(float x0, float x1, float x2, float x3) { return sadd(sadd(x0, x1), sadd(x2, x3)); }
 
+template <bool INL>
 __global__ __launch_bounds__(1024) void k_fa_pv(FaArgs a, FaPlan p) {
     __shared__ __align__(16) int8_t s_dig[16][2][4][64];          // wave, block e, digit, cell
     __shared__ float s_c[kMaxSeg][kHB][64];
     __shared__ float s_l[kMaxSeg][kHB];
-    __shared__ float s_m[64];
-    __shared__ uint32_t s_mkey[64];
+    __shared__ uint32_t s_t64[64];
+    const uint32_t t64v = a.ex.t64[threadIdx.x & 63u];           // first: the table write waits for it only
     const uint32_t item = blockIdx.x >> 2, c = blockIdx.x & 3u, g = blockIdx.y, sl = blockIdx.z;
-    const FaItem it = fa_item(a, p, item);
+    const FaItem it = fa_item<INL>(a, p, item);
     const uint32_t G = a.G, D = a.D, E = a.E, n16 = 16u * it.n, nbk = E / 32u, nh = a.n_head, nsl = D / 64u;
     const int lane = (int)__lane_id(), wave = (int)(threadIdx.x >> 6), nw = (int)(blockDim.x >> 6);
     const uint32_t u_first = it.u0 + ((c + 4u - (it.u0 & 3u)) & 3u);
@@ -278,35 +290,52 @@ __global__ __launch_bounds__(1024) void k_fa_pv(FaArgs a, FaPlan p) {
     const uint16_t * vmeta = (const uint16_t *)a.vc.base;
     const uint8_t * vq = a.vc.base + a.vc.quant_off;
 
-    // chunk maxima (MAXOUT over the tiles; MAXT is a total order, so the order of the folds is free)
-    for (uint32_t i = threadIdx.x; i < G; i += blockDim.x) s_mkey[i] = maxt_key_f(bf(kMFloor));
-    __syncthreads();
-    for (uint32_t idx = threadIdx.x; idx < G * it.ntiles; idx += blockDim.x)   // one load per thread
-        atomicMax(&s_mkey[idx % G], maxt_key_f(a.Mpart[(size_t)(it.tile0 + idx / G) * nh + g * G + idx % G]));
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < G; i += blockDim.x) s_m[i] = maxt_unkey(s_mkey[i]);
-    __syncthreads();
+    // A unit's loads: its V quants (lane = value), score and V scales (lane = cell), and the tile
+    // maxima of its head (lane < ntiles; clamped lanes repeat a tile, which leaves the maximum as it
+    // is). Each wave issues the loads of its next unit before it computes the current one.
+    struct UnitLoads {
+        int4 vqd[4];
+        float sv;
+        uint32_t mv, mkey;
+    };
+    auto load_unit = [&](uint32_t unit, uint32_t hb0, uint32_t hbn) {
+        UnitLoads L;
+        const uint32_t seg = unit / hbn, hi = unit % hbn, h = g * G + hb0 + hi;
+        const uint32_t ngr = min(nu - 4u * seg, 4u);
+#pragma unroll
+        for (uint32_t gi = 0; gi < 4; ++gi) {
+            const uint32_t ug = u_first + 4u * (4u * seg + min(gi, ngr - 1u));
+            L.vqd[gi] = *(const int4 *)(vq + (size_t)ug * 16u * E + (size_t)d * 16u);
+        }
+        const uint32_t grp = 4u * seg + ((uint32_t)lane >> 4);
+        const uint32_t u = u_first + 4u * min(grp, nu - 1u), rr = (uint32_t)lane & 15u;
+        L.sv = S[(size_t)h * n16 + 16u * (u - it.u0) + rr];
+        L.mv = *(const uint32_t *)(vmeta + ((size_t)u * 16u + rr) * nbk + 2u * sa);
+        L.mkey = maxt_key_f(a.Mpart[(size_t)(it.tile0 + min((uint32_t)lane, it.ntiles - 1u)) * nh + h]);
+        return L;
+    };
 
     for (uint32_t hb0 = 0; hb0 < G; hb0 += kHB) {
         const uint32_t hbn = min((uint32_t)kHB, G - hb0), units = nseg * hbn;
+        UnitLoads cur;
+        if ((uint32_t)wave < units) cur = load_unit((uint32_t)wave, hb0, hbn);   // a channel may have no groups
+        if (hb0 == 0u) {
+            if (threadIdx.x < 64u) s_t64[threadIdx.x] = t64v;
+            lds_barrier();                                        // the unit loads stay in flight
+        }
         for (uint32_t unit = (uint32_t)wave; unit < units; unit += (uint32_t)nw) {
-            const uint32_t seg = unit / hbn, hi = unit % hbn, h = g * G + hb0 + hi;
-            const float m = s_m[hb0 + hi];
+            const UnitLoads nxt = load_unit(min(unit + (uint32_t)nw, units - 1u), hb0, hbn);
+            const uint32_t seg = unit / hbn, hi = unit % hbn;
             const uint32_t ngr = min(nu - 4u * seg, 4u);
-            // loads first: V quants of the slice (lane = value) and, lane = cell, score and V scales
-            int4 vqd[4];
-#pragma unroll
-            for (uint32_t gi = 0; gi < 4; ++gi) {
-                const uint32_t ug = u_first + 4u * (4u * seg + min(gi, ngr - 1u));
-                vqd[gi] = *(const int4 *)(vq + (size_t)ug * 16u * E + (size_t)d * 16u);
-            }
+            const int4 * vqd = cur.vqd;
+            const float sv = cur.sv;
+            const uint32_t mv = cur.mv;
+            // MAXOUT of the chunk: the floor and the maxima of its tiles (MAXT: a total order)
+            const float m = maxt_unkey(wave_max_u(max(cur.mkey, maxt_key_f(bf(kMFloor)))));
             const uint32_t grp = 4u * seg + ((uint32_t)lane >> 4);
             const bool cv = grp < nu;
-            const uint32_t u = u_first + 4u * min(grp, nu - 1u), rr = (uint32_t)lane & 15u;
-            const float sv = S[(size_t)h * n16 + 16u * (u - it.u0) + rr];
-            const uint32_t mv = *(const uint32_t *)(vmeta + ((size_t)u * 16u + rr) * nbk + 2u * sa);
             // --- lane = cell k of the segment ---------------------------------------------
-            const float p = cv ? expk(smul(ssub(sv, m), a.scale), a.ex) : 0.0f;
+            const float p = cv ? expk(smul(ssub(sv, m), a.scale), a.ex, s_t64) : 0.0f;
             const float pz = daz(p);
             const bool live = cv && (fb(pz) & 0x7FFFFFFFu) != 0u;
             const float w0 = live ? smul(p, h2f_exact(mv & 0xFFFFu)) : 0.0f;
@@ -367,6 +396,7 @@ __global__ __launch_bounds__(1024) void k_fa_pv(FaArgs a, FaPlan p) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            cur = nxt;
         }
         __syncthreads();
         for (uint32_t idx = threadIdx.x; idx < hbn * 64u; idx += blockDim.x) {   // segment chains in order
@@ -384,8 +414,6 @@ __global__ __launch_bounds__(1024) void k_fa_pv(FaArgs a, FaPlan p) {
         __syncthreads();
     }
 
-    if (c == 0u && sl == 0u)                                      // chunk maxima for the merge
-        for (uint32_t i = threadIdx.x; i < G; i += blockDim.x) a.MK[(size_t)item * nh + g * G + i] = s_m[i];
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -394,23 +422,27 @@ __global__ __launch_bounds__(1024) void k_fa_pv(FaArgs a, FaPlan p) {
 // then runs CTREE over the 4 channels, the online merge in chunk order and finally ANORM (AT 5.6,
 // 5.7). No LDS and no barriers.
 // ---------------------------------------------------------------------------------------------
-constexpr uint32_t kMergeItems = 8;                              // chunks loaded per round
+constexpr uint32_t kMergeItems = 4;                              // chunks loaded per round
 constexpr uint32_t kMergeHeads = 4;                              // heads per block
 
+template <bool INL>
 __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
     const uint32_t G = a.G, D = a.D, nh = a.n_head, nsl = D / 64u;
     const uint32_t ngrp = (G + kMergeHeads - 1u) / kMergeHeads;
     const uint32_t t = blockIdx.x, g = blockIdx.y / ngrp, h0 = g * G + (blockIdx.y % ngrp) * kMergeHeads;
     const uint32_t hn = min(kMergeHeads, g * G + G - h0), sl = blockIdx.z;
     const uint32_t i = threadIdx.x >> 6, L = threadIdx.x & 63u;
+    __shared__ uint32_t s_t64[64];
+    if (threadIdx.x < 64u) s_t64[threadIdx.x] = a.ex.t64[threadIdx.x];
+    __syncthreads();
     if (i >= hn) return;                                          // whole waves
-    const uint32_t first = a.tok_first ? a.tok_first[t] : p.tok_first[t];
-    const uint32_t cnt = a.tok_count ? a.tok_count[t] : p.tok_count[t];
+    const uint32_t first = INL ? p.tok_first[t] : a.tok_first[t];
+    const uint32_t cnt = INL ? p.tok_count[t] : a.tok_count[t];
     const uint32_t h = h0 + i;
     float O = 0.0f, l = 0.0f, mr = 0.0f;
     for (uint32_t k0 = 0; k0 < cnt; k0 += kMergeItems) {
         const uint32_t kn = min(kMergeItems, cnt - k0);
-        float op[kMergeItems][4], lp[kMergeItems][4], mk[kMergeItems];
+        float op[kMergeItems][4], lp[kMergeItems][4];
 #pragma unroll
         for (uint32_t k = 0; k < kMergeItems; ++k) {                // clamped: every load is issued up front
             const size_t kk = first + k0 + min(k, kn - 1u);
@@ -420,22 +452,48 @@ __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
                 op[k][c] = a.OP[slot * D + 64u * sl + L];
                 lp[k][c] = a.LP[slot * nsl + sl];
             }
-            mk[k] = a.MK[kk * nh + h];
+        }
+        // chunk maxima: lane 8 k + j (k < 4) reads tile j (clamped) of chunk k; MAXOUT over the
+        // 8-lane group (an item has at most 8 tiles: NCG <= 128 groups of 16 cells)
+        uint32_t key;
+        {
+            uint32_t tile = 0;
+#pragma unroll
+            for (uint32_t k = 0; k < kMergeItems; ++k) {            // uniform item reads, per-lane select
+                const FaItem itk = fa_item<INL>(a, p, first + k0 + min(k, kn - 1u));
+                if ((L >> 3) == k) tile = itk.tile0 + min(L & 7u, itk.ntiles - 1u);
+            }
+            key = maxt_key_f(a.Mpart[(size_t)tile * nh + h]);
+            key = max(key, maxt_key_f(bf(kMFloor)));
+            key = umax_u(key, (uint32_t)dpp_i<kDppXor1>((int)key));
+            key = umax_u(key, (uint32_t)dpp_i<kDppXor2>((int)key));
+            key = umax_u(key, (uint32_t)dpp_i<kDppRowHalfMirror>((int)key));
+        }
+        float mk[kMergeItems];
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeItems; ++k) mk[k] = maxt_unkey((uint32_t)__builtin_amdgcn_readlane((int)key, 8 * (int)k));
+        // the running maxima and the merge factors of every chunk are independent of O and l:
+        // computed first, so the EXP evaluations of the chunks can overlap
+        float mrun[kMergeItems], fa[kMergeItems], fbv[kMergeItems];
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeItems; ++k) {
+            const float prev = k == 0u ? mr : mrun[k - 1u];
+            const bool first_chunk = k0 + k == 0u;
+            mrun[k] = first_chunk ? mk[k] : maxt(prev, mk[k]);
+            fa[k] = first_chunk ? 1.0f : expk(smul(ssub(prev, mrun[k]), a.scale), a.ex, s_t64);
+            fbv[k] = first_chunk ? 1.0f : expk(smul(ssub(mk[k], mrun[k]), a.scale), a.ex, s_t64);
         }
 #pragma unroll
         for (uint32_t k = 0; k < kMergeItems; ++k) {
             if (k >= kn) break;
             const float ok = ctree4(op[k][0], op[k][1], op[k][2], op[k][3]);
             const float lk = ctree4(lp[k][0], lp[k][1], lp[k][2], lp[k][3]);
-            if (k0 + k == 0u) { O = ok; l = lk; mr = mk[k]; }
+            if (k0 + k == 0u) { O = ok; l = lk; }
             else {
-                const float mn = maxt(mr, mk[k]);
-                const float fa = expk(smul(ssub(mr, mn), a.scale), a.ex);
-                const float fbv = expk(smul(ssub(mk[k], mn), a.scale), a.ex);
-                l = sadd(smul(l, fa), smul(lk, fbv));
-                O = sadd(smul(O, fa), smul(ok, fbv));
-                mr = mn;
+                l = sadd(smul(l, fa[k]), smul(lk, fbv[k]));
+                O = sadd(smul(O, fa[k]), smul(ok, fbv[k]));
             }
+            mr = mrun[k];
         }
     }
     a.out[(size_t)t * a.out_stride + (size_t)h * D + 64u * sl + L] = smul(O, srcp(maxt(l, bf(kLFloor))));
@@ -443,20 +501,25 @@ __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
 
 }  // namespace tsr
 
-int tsr_launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, hipStream_t s) {
+template <bool INL>
+static int launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, hipStream_t s) {
     const size_t lds_qk = (size_t)a.G * a.D + 4u * (size_t)a.G * (a.D / 32u) + 4u * 4u * a.G;
     const dim3 gqk(p.n_items * p.maxtiles, a.n_head_kv);
     switch (a.D) {
-        case 64: hipLaunchKernelGGL(tsr::k_fa_qk<64>, gqk, dim3(256), lds_qk, s, a, p); break;
-        case 128: hipLaunchKernelGGL(tsr::k_fa_qk<128>, gqk, dim3(256), lds_qk, s, a, p); break;
-        case 256: hipLaunchKernelGGL(tsr::k_fa_qk<256>, gqk, dim3(256), lds_qk, s, a, p); break;
-        case 512: hipLaunchKernelGGL(tsr::k_fa_qk<512>, gqk, dim3(256), lds_qk, s, a, p); break;
+        case 64: hipLaunchKernelGGL((tsr::k_fa_qk<64, INL>), gqk, dim3(256), lds_qk, s, a, p); break;
+        case 128: hipLaunchKernelGGL((tsr::k_fa_qk<128, INL>), gqk, dim3(256), lds_qk, s, a, p); break;
+        case 256: hipLaunchKernelGGL((tsr::k_fa_qk<256, INL>), gqk, dim3(256), lds_qk, s, a, p); break;
+        case 512: hipLaunchKernelGGL((tsr::k_fa_qk<512, INL>), gqk, dim3(256), lds_qk, s, a, p); break;
         default: return -2;
     }
     if (hipGetLastError() != hipSuccess) return -4;
-    hipLaunchKernelGGL(tsr::k_fa_pv, dim3(4u * p.n_items, a.n_head_kv, a.D / 64u), dim3(1024), 0, s, a, p);
+    hipLaunchKernelGGL(tsr::k_fa_pv<INL>, dim3(4u * p.n_items, a.n_head_kv, a.D / 64u), dim3(1024), 0, s, a, p);
     if (hipGetLastError() != hipSuccess) return -4;
     const uint32_t ngrp = (a.G + tsr::kMergeHeads - 1u) / tsr::kMergeHeads;
-    hipLaunchKernelGGL(tsr::k_fa_merge, dim3(T, a.n_head_kv * ngrp, a.D / 64u), dim3(256), 0, s, a, p);
+    hipLaunchKernelGGL(tsr::k_fa_merge<INL>, dim3(T, a.n_head_kv * ngrp, a.D / 64u), dim3(256), 0, s, a, p);
     return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int tsr_launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, hipStream_t s) {
+    return a.items ? launch_fa<false>(a, p, T, s) : launch_fa<true>(a, p, T, s);
 }

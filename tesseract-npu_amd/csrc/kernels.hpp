@@ -79,7 +79,6 @@ struct FaArgs {
     float * Mpart;           // [tile][n_head] tile maxima
     float * OP;              // [item][4][n_head][D] channel partials
     float * LP;              // [item][4][n_head][D / 64] channel row sums (one per slice)
-    float * MK;              // [item][n_head] chunk maxima
     float * out;
     uint64_t out_stride;
     ExpkTab ex;

@@ -275,7 +275,6 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     const size_t o_Mp = off; off = up256(off + 4u * (size_t)n_tiles * n_head);
     const size_t o_OP = off; off = up256(off + 4u * n_items * kC * n_head * D);
     const size_t o_LP = off; off = up256(off + 4u * n_items * kC * n_head * nsl);
-    const size_t o_MK = off; off = up256(off + 4u * n_items * n_head);
 
     tsr::FaPlan p{};
     p.n_items = (uint32_t)n_items;
@@ -323,7 +322,6 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     a.Mpart = (float *)(base + o_Mp);
     a.OP = (float *)(base + o_OP);
     a.LP = (float *)(base + o_LP);
-    a.MK = (float *)(base + o_MK);
     a.out = out_dev;
     a.out_stride = out_stride;
     a.ex = ctx->expk;

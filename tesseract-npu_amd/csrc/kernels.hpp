@@ -15,9 +15,7 @@ struct QactArgs {
     uint32_t d_off, bs_off;  // byte offsets of the D and BS regions
 };
 
-// MUL_MAT over the device weight layout:
-//   Q8_0: meta = fp16 d [N][K/32], quant = int8 [N][K/32][32]
-//   Q4_K: meta = {fp16 d, fp16 dmin, u8 scales[12]} [N][K/256], quant = u8 [N][K/256][128]
+// MUL_MAT over the device weight layout of wlayout.hpp (meta region wm, quant region wq).
 struct MvArgs {
     const uint8_t * wm;
     const uint8_t * wq;
@@ -31,6 +29,21 @@ struct MvArgs {
     uint32_t N, K, T;
     uint32_t acc;            // y = FA(y_old, v)
     uint32_t rb;             // rows per workgroup (set by the launcher)
+};
+
+// Prefill MUL_MAT (T >= 16) on the matrix cores: the activations are first quantized into QA
+// images (qa, one per token, qa_stride bytes apart; the f32 scales at d_off).
+struct MmArgs {
+    const uint8_t * wm;
+    const uint8_t * wq;
+    const uint8_t * qa;
+    uint32_t qa_stride, d_off;
+    float * y;
+    uint64_t y_stride;
+    const float * add;       // nullable
+    uint64_t add_stride;
+    uint32_t N, K, T;
+    uint32_t acc;
 };
 
 // A KV plane (see k_kv.hip for the layout).
@@ -89,6 +102,7 @@ struct FaArgs {
 int tsr_launch_qact(const tsr::QactArgs & a, uint32_t T, hipStream_t s);
 int tsr_launch_mv_q8_0(const tsr::MvArgs & a, uint32_t n_cu, hipStream_t s);
 int tsr_launch_mv_q4_k(const tsr::MvArgs & a, uint32_t n_cu, hipStream_t s);
+int tsr_launch_mm_q8_0(const tsr::MmArgs & a, hipStream_t s);
 int tsr_launch_kv_bytes(const tsr::KvArgs & a, uint32_t which, uint64_t off, uint64_t n, uint8_t * stage, int to_dev,
                         hipStream_t s);
 int tsr_launch_kv_set_rows(const tsr::KvArgs & a, uint32_t which, const float * src, uint32_t n_rows,

@@ -188,6 +188,7 @@ int tsr_hip_memset(tsr_hip_ctx * ctx, void * dst_dev, int value, size_t bytes) {
 namespace {
 
 constexpr uint32_t kKMax = 32768u;
+constexpr uint32_t kMmMinTokens = 16u;   // MUL_MAT with at least this many tokens runs on the matrix cores
 
 uint32_t blk_values(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 32u : 256u; }
 uint32_t blk_bytes(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 34u : 144u; }
@@ -417,6 +418,41 @@ static int mul_mat_common(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
     ctx->ctr.mul_mat_calls++;
     ctx->ctr.mul_mat_rows += (uint64_t)w->N * T;
     ctx->ctr.mul_mat_weight_bytes += (uint64_t)w->N * nb * blk_bytes(w->fmt);
+    // prefill: T >= 16 tokens of Q8_0 on the matrix cores (QACT A32 of every token into scratch)
+    if (T >= kMmMinTokens && w->fmt == TSR_HIP_FMT_Q8_0 && isums == nullptr) {
+        const uint32_t qa_bytes = (uint32_t)tsr_hip_qa_bytes(0u, w->K);
+        int rc = ctx->scratch.reserve(ctx, (size_t)std::min(T, 65535u) * qa_bytes);
+        if (rc) return rc;
+        for (uint32_t t0 = 0; t0 < T; t0 += 65535u) {
+            const uint32_t tt = std::min(T - t0, 65535u);
+            tsr::QactArgs q{};
+            q.x = x_dev + (size_t)t0 * x_stride;
+            q.x_stride = x_stride;
+            q.qa = (uint8_t *)ctx->scratch.ptr;
+            q.qa_bytes = qa_bytes;
+            q.K = w->K;
+            q.kind = 0u;
+            q.d_off = (w->K + 63u) / 64u * 64u;
+            q.bs_off = q.d_off + (4u * (w->K / 32u) + 63u) / 64u * 64u;
+            if (tsr_launch_qact(q, tt, s)) return TSR_HIP_E_HIP;
+            tsr::MmArgs m{};
+            m.wm = w->dev;
+            m.wq = w->dev + w->quant_off;
+            m.qa = q.qa;
+            m.qa_stride = qa_bytes;
+            m.d_off = q.d_off;
+            m.y = y_dev + (size_t)t0 * y_stride;
+            m.y_stride = y_stride;
+            m.add = add_dev ? add_dev + (size_t)t0 * add_stride : nullptr;
+            m.add_stride = add_stride;
+            m.N = w->N;
+            m.K = w->K;
+            m.T = tt;
+            m.acc = a.acc;
+            if (tsr_launch_mm_q8_0(m, s)) return TSR_HIP_E_HIP;
+        }
+        return TSR_HIP_OK;
+    }
     for (uint32_t t0 = 0; t0 < T; t0 += 65535u) {
         const uint32_t tt = std::min(T - t0, 65535u);
         a.x = x_dev + (size_t)t0 * x_stride;

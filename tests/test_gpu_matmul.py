@@ -1,0 +1,75 @@
+"""GPU parity of prefill MUL_MAT (T >= 16 tokens, Q8_0 weights, int8 matrix cores) through the C
+ABI against the CPU oracle: bit-exact f32 outputs, as for the matvec path.
+
+The prefill path quantizes every token row (QACT A32), takes the integer block sums from the i8
+matrix core and the scale products from the f32 matrix core; these tests cover ragged tiles (T and
+N not multiples of 64), every K class (one block, under 16 blocks, many rounds of the 16 partials),
+the fused addend / accumulate flags, special activations and weight scales, and the BASELINE
+prefill shape (512 tokens x 4096 x 4096) on a sample of tokens and rows."""
+import numpy as np
+import pytest
+
+import tsr_hip
+import tsr_synth as S
+from helpers import assert_bits_equal, special_row, weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _mm(dev, oc, N, K, T, seed=1, x=None, add=False, acc=False, wblocks=None):
+    blocks = weights(0, N, K, seed) if wblocks is None else wblocks
+    w = dev.weight(0, blocks, N, K)
+    if x is None:
+        x = S.normal(seed + 100, T * K).reshape(T, K)
+    y0 = S.normal(seed + 200, T * N).reshape(T, N)
+    yb = dev.upload(y0)
+    a = S.normal(seed + 300, T * N).reshape(T, N) if add else None
+    dev.mul_mat(w, dev.upload(x), T, K, yb, N, dev.upload(a) if add else None, N if add else 0,
+                tsr_hip.MM_ACC_DST if acc else 0)
+    got = yb.read(np.float32, (T, N))
+    want = oc.mul_mat(0, blocks, K, x, add=(a if add else (y0 if acc else None)), threads=8)
+    return got, want
+
+
+@pytest.mark.parametrize("T,N,K", [(16, 64, 32), (17, 100, 896), (64, 4864, 896), (100, 33, 4096),
+                                   (70, 128, 14336), (16, 1, 512), (130, 200, 1024)])
+def test_mm_q8_0_shapes(dev, oc, T, N, K):
+    got, want = _mm(dev, oc, N, K, T, seed=T + N)
+    assert_bits_equal(got, want, f"T {T} {N}x{K}")
+
+
+def test_mm_q8_0_add_acc(dev, oc):
+    got, want = _mm(dev, oc, 96, 896, 40, seed=3, add=True)
+    assert_bits_equal(got, want, "add")
+    got, want = _mm(dev, oc, 96, 896, 40, seed=4, acc=True)
+    assert_bits_equal(got, want, "acc")
+
+
+def test_mm_q8_0_specials(dev, oc):
+    N, K, T = 48, 1024, 32
+    x = np.stack([special_row(K, t) if t % 3 == 0 else S.normal(50 + t, K, 1e-3 if t % 3 == 1 else 1.0)
+                  for t in range(T)])
+    blocks = weights(0, N, K, 9).copy()
+    v = blocks.reshape(N, -1, 34)
+    rng = np.random.default_rng(3)
+    specials = np.array([0x0001, 0x03FF, 0x8005, 0x7C00, 0xFC00, 0x7E01, 0x0000], np.uint16).view(np.uint8).reshape(-1, 2)
+    for r in range(0, N, 2):
+        v[r, rng.integers(0, v.shape[1]), 0:2] = specials[r % len(specials)]
+    got, want = _mm(dev, oc, N, K, T, x=x, wblocks=blocks)
+    assert_bits_equal(got, want, "specials")
+
+
+def test_mm_q8_0_baseline_prefill_shape(dev, oc):
+    """BASELINE configs[3] (512 tokens x W[4096 x 4096] Q8_0): every output of a sample of tokens,
+    and every token of a sample of rows."""
+    T, N, K = 512, 4096, 4096
+    blocks = S.quantize_q8_0(S.normal(S.seed_of("cfg4", "w_q"), N * K, 0.02).reshape(N, K))
+    x = S.normal(S.seed_of("cfg4", "x"), T * K).reshape(T, K)
+    w = dev.weight(0, blocks, N, K)
+    yb = dev.alloc(4 * T * N)
+    dev.mul_mat(w, dev.upload(x), T, K, yb, N)
+    got = yb.read(np.float32, (T, N))
+    toks = [0, 1, 31, 32, 63, 64, 255, 510, 511]
+    assert_bits_equal(got[toks], oc.mul_mat(0, blocks, K, x[toks], threads=8), "token sample")
+    rows = np.r_[0:40, 2040:2056, 4060:4096]
+    assert_bits_equal(got[:, rows], oc.mul_mat(0, blocks[rows], K, x, threads=8), "row sample")

@@ -143,11 +143,22 @@ def extra_workloads(dev, ev, stream, n: int) -> dict:
     out = {}
     n = max(n, 100)
 
-    def timed(fn):
+    def timed(fn, nn=None):
         for i in range(5):
             fn(i)
         ev.device_sync()
-        return ev.graph_ms(stream, fn, n)
+        return ev.graph_ms(stream, fn, nn or n)
+
+    def timed_eager(fn, nn):
+        for i in range(3):
+            fn(i)
+        ev.device_sync()
+        a, b = ev.event(), ev.event()
+        ev.record(a, stream)
+        for i in range(nn):
+            fn(i)
+        ev.record(b, stream)
+        return ev.elapsed_ms(a, b) / nn
 
     # Q8_0 4864 x 896
     N, K = 4864, 896
@@ -197,6 +208,43 @@ def extra_workloads(dev, ev, stream, n: int) -> dict:
                                               "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
                                               "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                               "copies": copies, "launches_per_call": 3}
+    del caches
+
+    # prefill at Llama-3-8B shapes, 512 tokens: Q8_0 MUL_MAT on the int8 matrix cores
+    T, K = 512, 4096
+    xq = dev.upload(S.normal(S.seed_of("cfg4", "x"), T * K))
+    for name, N in (("prefill_q8_0_512x4096x4096", 4096), ("prefill_q8_0_512x14336x4096", 14336)):
+        blocks = S.quantize_q8_0(S.normal(S.seed_of("cfg4", "w_" + str(N)), N * K, 0.02).reshape(N, K))
+        ws = [dev.weight(0, blocks, N, K) for _ in range(2)]
+        yb = dev.alloc(4 * T * N)
+        ms, ms_eager = timed(lambda i: dev.mul_mat(ws[i % 2], xq, T, K, yb, N, stream=stream), 20)
+        ops = 2 * T * N * K
+        out[name] = {"us_per_call": round(ms * 1e3, 2), "us_per_call_eager": round(ms_eager * 1e3, 2),
+                     "int8_TOPS": round(ops / (ms * 1e-3) / 1e12, 1),
+                     "frac_of_int8_mfma_peak": round(ops / (ms * 1e-3) / 5.0e15, 4),
+                     "launches_per_call": 2, "note": "QACT of the 512 rows + the matrix-core kernel"}
+        del ws, yb
+
+    # causal flash attention over 512 tokens (32 q / 8 KV heads, D 128, q8_0 KV); the
+    # work list of 512 rows is copied to the device per call, so this one is timed eagerly
+    T, n_head, n_kv_head, D = 512, 32, 8, 128
+    E = n_kv_head * D
+    kf = dev.upload(S.normal(S.seed_of("cfg4", "k"), T * E))
+    vf = dev.upload(S.normal(S.seed_of("cfg4", "v"), T * E))
+    idx = dev.upload(np.arange(T, dtype=np.int64))
+    kc, vc = dev.kv(E, T), dev.kv(E, T)
+    dev.kv_set_rows(kc, 0, kf, T, E, idx)
+    dev.kv_set_rows(vc, 1, vf, T, E, idx)
+    mask = np.full((T, T), -np.inf, np.float16)
+    mask[np.tril_indices(T)] = 0
+    msum = tsr_hip.msum_build_f16(mask)
+    qb = dev.upload(S.normal(S.seed_of("cfg4", "q"), T * n_head * D).astype(np.float16).astype(np.float32))
+    ob = dev.alloc(4 * T * n_head * D)
+    scale = np.float32(1.0 / np.sqrt(D))
+    ms = timed_eager(lambda i: dev.flash_attn(qb, T, n_head * D, kc, vc, D, n_head, n_kv_head, scale, msum, ob,
+                                              n_head * D, new_runs=[[0, T]], stream=stream), 20)
+    out["fa_prefill_causal_512_32q8kv_d128"] = {"us_per_call": round(ms * 1e3, 2), "launches_per_call": 3,
+                                                "timing": "eager (host-built work list of 512 rows)"}
     return out
 
 

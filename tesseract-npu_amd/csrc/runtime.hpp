@@ -14,15 +14,35 @@ int hip_err(hipError_t e, const char * what);
 }
 void tsr_expk_table(tsr::ExpkTab * t);
 
-// Device scratch owned by a context (FA partials, the isums y sink). It only grows; growing waits
-// for the context's stream first, so no queued kernel still uses the old block.
+// Device scratch owned by a context (FA partials and work lists, prefill QA images, the isums y
+// sink). It only grows. reserve() orders its users: a call on another stream than the previous
+// user first waits (hipStreamWaitEvent) for the work queued on that stream, so two calls never use
+// the block at once; growing waits for the whole device first, so no queued kernel still uses the
+// old block. Under graph capture neither a growth nor a wait on another stream can be recorded:
+// reserve() then fails with TSR_HIP_E_ARG (warm the context up outside the capture).
+inline bool tsr_capturing(hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
 struct tsr_scratch {
     void * ptr = nullptr;
     size_t bytes = 0;
-    template <class Ctx>
-    int reserve(Ctx * ctx, size_t need) {
+    hipStream_t last = nullptr;
+    hipEvent_t ev = nullptr;
+    int reserve(size_t need, hipStream_t s) {
+        if (last != nullptr && last != s) {
+            if (tsr_capturing(s)) return TSR_HIP_E_ARG;
+            if (ev == nullptr) {
+                const int rc = tsr::hip_err(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "hipEventCreate");
+                if (rc) return rc;
+            }
+            int rc = tsr::hip_err(hipEventRecord(ev, last), "hipEventRecord");
+            if (rc == 0) rc = tsr::hip_err(hipStreamWaitEvent(s, ev, 0), "hipStreamWaitEvent");
+            if (rc) return rc;
+        }
+        last = s;
         if (need <= bytes) return TSR_HIP_OK;
-        (void)ctx;
+        if (tsr_capturing(s)) return TSR_HIP_E_ARG;
         (void)hipDeviceSynchronize();             // no stream may still use the old block
         if (ptr) (void)hipFree(ptr);
         ptr = nullptr;
@@ -34,8 +54,11 @@ struct tsr_scratch {
     }
     void release() {
         if (ptr) (void)hipFree(ptr);
+        if (ev) (void)hipEventDestroy(ev);
         ptr = nullptr;
+        ev = nullptr;
         bytes = 0;
+        last = nullptr;
     }
 };
 

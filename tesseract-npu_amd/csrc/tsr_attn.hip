@@ -68,7 +68,7 @@ static int kv_bytes(tsr_hip_ctx * ctx, const tsr_hip_kv * kv, uint32_t which, si
     if (bytes == 0) return TSR_HIP_OK;
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
-    int rc = ctx->scratch.reserve(ctx, bytes);
+    int rc = ctx->scratch.reserve(bytes, ctx->stream);
     if (rc) return rc;
     uint8_t * stage = (uint8_t *)ctx->scratch.ptr;
     if (to_dev) rc = hip_err(hipMemcpyAsync(stage, host, bytes, hipMemcpyHostToDevice, ctx->stream), "kv H2D");
@@ -292,10 +292,13 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
     hipStream_t s = ctx->pick(stream);
-    int rc = ctx->scratch.reserve(ctx, off);
+    int rc = ctx->scratch.reserve(off, s);
     if (rc) return rc;
     uint8_t * base = (uint8_t *)ctx->scratch.ptr;
     if (!inl) {
+        // a host-to-device copy of a host vector cannot be recorded into a graph (the vector is gone
+        // when the graph replays): long work lists are for eager calls
+        if (tsr_capturing(s)) return TSR_HIP_E_ARG;
         rc = hip_err(hipMemcpyAsync(base + o_items, packed.data(), packed.size(), hipMemcpyHostToDevice, s), "fa plan");
         if (rc) return rc;
     }

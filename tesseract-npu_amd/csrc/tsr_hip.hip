@@ -391,16 +391,15 @@ int tsr_hip_qact(tsr_hip_ctx * ctx, uint32_t kind, const float * x_dev, uint32_t
 // ---------------------------------------------------------------------------------------------
 // MUL_MAT
 // ---------------------------------------------------------------------------------------------
-static int mul_mat_common(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T,
+// The caller holds ctx->mtx.
+static int mul_mat_locked(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T,
                           uint64_t x_stride, float * y_dev, uint64_t y_stride, const float * add_dev,
-                          uint64_t add_stride, uint32_t flags, int32_t * isums, void * stream) {
-    if (ctx == nullptr || w == nullptr || x_dev == nullptr || y_dev == nullptr || T == 0u) return TSR_HIP_E_ARG;
+                          uint64_t add_stride, uint32_t flags, int32_t * isums, hipStream_t s) {
+    if (w == nullptr || x_dev == nullptr || y_dev == nullptr || T == 0u) return TSR_HIP_E_ARG;
     if ((flags & ~TSR_HIP_MM_ACC_DST) != 0u || (add_dev != nullptr && (flags & TSR_HIP_MM_ACC_DST))) return TSR_HIP_E_ARG;
     if (!aligned16(x_dev) || (T > 1u && x_stride % 4u != 0u)) return TSR_HIP_E_ARG;
     if (T > 1u && (x_stride < w->K || y_stride < w->N)) return TSR_HIP_E_ARG;
-    std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
-    hipStream_t s = ctx->pick(stream);
     tsr::MvArgs a{};
     const size_t nb = w->K / blk_values(w->fmt);
     a.wm = w->dev;
@@ -421,7 +420,7 @@ static int mul_mat_common(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
     // prefill: T >= 16 tokens of Q8_0 on the matrix cores (QACT A32 of every token into scratch)
     if (T >= kMmMinTokens && w->fmt == TSR_HIP_FMT_Q8_0 && isums == nullptr) {
         const uint32_t qa_bytes = (uint32_t)tsr_hip_qa_bytes(0u, w->K);
-        int rc = ctx->scratch.reserve(ctx, (size_t)std::min(T, 65535u) * qa_bytes);
+        int rc = ctx->scratch.reserve((size_t)std::min(T, 65535u) * qa_bytes, s);
         if (rc) return rc;
         for (uint32_t t0 = 0; t0 < T; t0 += 65535u) {
             const uint32_t tt = std::min(T - t0, 65535u);
@@ -469,20 +468,20 @@ static int mul_mat_common(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
 int tsr_hip_mul_mat(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T, uint64_t x_stride,
                     float * y_dev, uint64_t y_stride, const float * add_dev, uint64_t add_stride, uint32_t flags,
                     void * stream) {
-    return mul_mat_common(ctx, w, x_dev, T, x_stride, y_dev, y_stride, add_dev, add_stride, flags, nullptr, stream);
+    if (ctx == nullptr) return TSR_HIP_E_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    return mul_mat_locked(ctx, w, x_dev, T, x_stride, y_dev, y_stride, add_dev, add_stride, flags, nullptr,
+                          ctx->pick(stream));
 }
 
 int tsr_hip_mul_mat_isums(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, int32_t * isums_dev,
                           void * stream) {
-    if (isums_dev == nullptr || w == nullptr) return TSR_HIP_E_ARG;
+    if (ctx == nullptr || isums_dev == nullptr || w == nullptr) return TSR_HIP_E_ARG;
     // y goes to scratch: the integer sums are the product of this call
-    float * y = nullptr;
-    {
-        std::lock_guard<std::mutex> lk(ctx->mtx);
-        (void)hipSetDevice(ctx->device);
-        const int rc = ctx->scratch.reserve(ctx, (size_t)w->N * sizeof(float));
-        if (rc) return rc;
-        y = (float *)ctx->scratch.ptr;
-    }
-    return mul_mat_common(ctx, w, x_dev, 1u, w->K, y, w->N, nullptr, 0u, 0u, isums_dev, stream);
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    hipStream_t s = ctx->pick(stream);
+    const int rc = ctx->scratch.reserve((size_t)w->N * sizeof(float), s);
+    if (rc) return rc;
+    return mul_mat_locked(ctx, w, x_dev, 1u, w->K, (float *)ctx->scratch.ptr, w->N, nullptr, 0u, 0u, isums_dev, s);
 }

@@ -5,6 +5,7 @@ import math
 import numpy as np
 import pytest
 
+import tsr_hip
 import tsr_synth as S
 from helpers import assert_bits_equal
 
@@ -89,3 +90,97 @@ def test_fa_special_q(dev, oc):
     q[1, 300:332] = 0
     got, want = _fa(dev, oc, 600, 600, 8, 2, 128, T=2, q=q, mask=np.zeros((2, 600), np.float16))
     assert_bits_equal(got, want, "special q")
+
+
+class _Hip:
+    """The few HIP runtime calls these tests need (libamdhip64 via ctypes)."""
+
+    def __init__(self):
+        import ctypes as C
+        self.C = C
+        self.h = C.CDLL("libamdhip64.so")
+        self.h.hipStreamCreateWithFlags.argtypes = [C.POINTER(C.c_void_p), C.c_uint]
+        self.h.hipStreamDestroy.argtypes = [C.c_void_p]
+        self.h.hipStreamSynchronize.argtypes = [C.c_void_p]
+        self.h.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        self.h.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+        self.h.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+        self.h.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        self.h.hipGraphExecDestroy.argtypes = [C.c_void_p]
+        self.h.hipGraphDestroy.argtypes = [C.c_void_p]
+
+    def stream(self):
+        s = self.C.c_void_p()
+        assert self.h.hipStreamCreateWithFlags(self.C.byref(s), 1) == 0      # non-blocking, default priority
+        return s.value
+
+
+def _decode_case(oc, dev, n_kv, seed):
+    E, n_head, n_head_kv, D = 256, 8, 2, 128
+    kc, vc = _cache(oc, n_kv, E, seed)
+    q = S.normal(seed + 2, n_head * D).reshape(1, n_head * D).astype(np.float16).astype(np.float32)
+    msum = oc.msum(np.zeros((1, n_kv), np.float16))
+    scale = np.float32(1.0 / math.sqrt(D))
+    want = oc.flash_attn(q, kc, vc, D, n_head, n_head_kv, scale, msum)
+    K_, V_ = dev.kv(E, n_kv), dev.kv(E, n_kv)
+    K_.set_bytes(0, kc)
+    V_.set_bytes(1, vc)
+    return dict(q=dev.upload(q), K=K_, V=V_, msum=msum, scale=scale, out=dev.alloc(4 * n_head * D), want=want,
+                args=(D, n_head, n_head_kv))
+
+
+def _run(dev, c, stream=None):
+    D, n_head, n_head_kv = c["args"]
+    dev.flash_attn(c["q"], 1, n_head * D, c["K"], c["V"], D, n_head, n_head_kv, c["scale"], c["msum"], c["out"],
+                   n_head * D, stream=stream)
+
+
+def test_fa_scratch_shared_by_two_streams(dev, oc):
+    """Two calls on different streams share the context's scratch: the second waits for the first."""
+    hip = _Hip()
+    s1 = hip.stream()
+    try:
+        a, b = _decode_case(oc, dev, 4096, 21), _decode_case(oc, dev, 3000, 22)
+        for _ in range(3):
+            _run(dev, a, stream=s1)
+            _run(dev, b)
+            assert hip.h.hipStreamSynchronize(s1) == 0
+            dev.sync()
+            assert_bits_equal(a["out"].read(np.float32, a["want"].shape), a["want"], "stream 1")
+            assert_bits_equal(b["out"].read(np.float32, b["want"].shape), b["want"], "context stream")
+    finally:
+        hip.h.hipStreamDestroy(s1)
+
+
+def test_fa_decode_graph_replays(dev, oc):
+    """A decode call captured into a HIP graph replays exactly, with eager calls between replays;
+    a call whose work list needs a host copy is refused during capture."""
+    hip = _Hip()
+    C = hip.C
+    a, b = _decode_case(oc, dev, 2048, 31), _decode_case(oc, dev, 1000, 32)
+    _run(dev, a)                                        # warm: the scratch is large enough
+    _run(dev, b)
+    dev.sync()
+    T, D, n_head, n_head_kv = 40, 128, 8, 2             # 40 query rows: a host-built work list
+    qq, oo = dev.alloc(4 * T * n_head * D), dev.alloc(4 * T * n_head * D)
+    ms40 = oc.msum(np.zeros((T, 2048), np.float16))
+    s = dev.stream
+    assert hip.h.hipStreamBeginCapture(s, 2) == 0
+    _run(dev, a)
+    with pytest.raises(tsr_hip.TsrHipError):
+        dev.flash_attn(qq, T, n_head * D, a["K"], a["V"], D, n_head, n_head_kv, a["scale"], ms40, oo, n_head * D)
+    g, ge = C.c_void_p(), C.c_void_p()
+    assert hip.h.hipStreamEndCapture(s, C.byref(g)) == 0
+    assert hip.h.hipGraphInstantiate(C.byref(ge), g, None, None, 0) == 0
+    try:
+        for i in range(4):
+            a["out"].fill(0)
+            assert hip.h.hipGraphLaunch(ge, s) == 0
+            dev.sync()
+            assert_bits_equal(a["out"].read(np.float32, a["want"].shape), a["want"], f"replay {i}")
+            _run(dev, b)                               # eager work between the replays
+            dev.sync()
+            assert_bits_equal(b["out"].read(np.float32, b["want"].shape), b["want"], f"eager {i}")
+    finally:
+        hip.h.hipGraphExecDestroy(ge)
+        hip.h.hipGraphDestroy(g)

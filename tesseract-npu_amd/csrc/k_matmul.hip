@@ -2,7 +2,9 @@
 //
 // Numerics (sw/sim/tsr_ref.c:525-635): y[t][n] is the 16-partial tree of the terms
 // (d[n][b] Dx[t][b]) f32(isum[t][n][b]), term b going to partial b mod 16 in order of b; the
-// activation is quantized by QACT A32 first (k_qact, into scratch).
+// activation is quantized by QACT A32 first (k_qact_mm, into scratch, block-major: the quants
+// [block][token][32 B] and the scales [block][token], so that a wave's operand load of 32 tokens
+// is 1 KiB of consecutive bytes).
 //
 // Per 32-value block b and 32 x 32 tile (weight rows x tokens):
 //   isum = v_mfma_i32_32x32x32_i8(W rows, X tokens): one block of K is exactly one instruction,
@@ -15,15 +17,16 @@
 // Dx is an fp16 value and d an fp16 value, so no product or sum is ever subnormal and plain IEEE
 // operations are the spec operations; NaN is canonicalized when y is stored.
 //
-// Order: the partials are computed one after the other (j = 0..15, blocks b = j, j + 16, ... in
-// order), and each finished p_j enters the tree ((p0 + p1) + (p2 + p3)) + ... through a 4-level stack
-// of pending sums, so an output holds 5 values instead of 16.
+// Work split. A workgroup of 16 waves computes one 32 x 32 tile; wave j computes partial p_j
+// (blocks b = j, j + 16, ... in order: consecutive slots of the weight layout, wlayout.hpp). Each
+// wave issues the loads of up to kMmPre of its blocks at once, then runs their matrix-core steps.
+// The 16 partials meet in LDS and one thread per output adds the tree ((p0 + p1) + (p2 + p3)) + ...
 //
 // Lane layouts (gfx950): an operand lane l supplies row l % 32 of its matrix and k = 16 (l / 32) ..
 // 16 (l / 32) + 15; the result lane l holds column l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4,
 // r = 0..15.
 #include "kernels.hpp"
-#include "tsr_dev.hpp"
+#include "qact.hpp"
 #include "wlayout.hpp"
 
 namespace tsr {
@@ -32,83 +35,100 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-// A workgroup of 4 waves computes 64 weight rows x 64 tokens; wave (wr, wt) the 32 x 32 tile at
-// rows n0 + 32 wr, tokens t0 + 32 wt. Rows and tokens beyond the matrix read clamped (valid)
-// addresses and are not stored.
-__global__ __launch_bounds__(256) void k_mm_q80(MmArgs a) {
-    const WGeom g = wgeom(a.N, a.K >> 5);
-    const uint32_t lane = __lane_id(), wave = threadIdx.x >> 6;
-    const uint32_t nbase = blockIdx.x * 64u + 32u * (wave & 1u), tbase = blockIdx.y * 64u + 32u * (wave >> 1);
-    const uint32_t h = lane >> 5, c = lane & 31u;
-    // operand rows of this lane
-    const uint32_t n = min(nbase + c, a.N - 1u), t = min(tbase + c, a.T - 1u);
-    const uint8_t * xq = a.qa + (size_t)t * a.qa_stride;             // QS of token t
-    const float * xd = (const float *)(a.qa + (size_t)t * a.qa_stride + a.d_off);
+constexpr uint32_t kMmPre = 8;   // blocks whose loads one wave keeps in flight
 
-    v16f p, L0, L1, L2, L3;
-    for (int r = 0; r < 16; ++r) { L0[r] = 0.0f; L1[r] = 0.0f; L2[r] = 0.0f; L3[r] = 0.0f; }
-    for (uint32_t j = 0; j < 16u; ++j) {
-        for (int r = 0; r < 16; ++r) p[r] = 0.0f;
-        const uint32_t cnt = wl_count(g, j);
-        for (uint32_t k = 0; k < cnt; ++k) {
-            const uint32_t b = j + 16u * k, sl = wl_slot(g, j, k);
-            const v4i wa = *(const v4i *)(a.wq + q80_quant_off(g, n >> 4, h, sl, n & 15u));
-            const v4i xb = *(const v4i *)(xq + 32u * b + 16u * h);
-            const float dw = h ? 0.0f : h2f_fast(*(const uint16_t *)(a.wm + q80_meta_off(g, n >> 4, sl, n & 15u)));
-            const float dx = h ? 0.0f : xd[b];
+// QACT A32 of T token rows into the block-major layout: 8 lanes per (token, block), 4 values each
+// (qact_a32_lane: the spec rule, as for the QA image of k_qact).
+__global__ __launch_bounds__(256) void k_qact_mm(const float * x, uint64_t x_stride, uint32_t K, uint32_t T,
+                                                 uint8_t * xq, float * xd) {
+    const uint32_t nb = K >> 5;
+    const uint64_t pair = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;   // (token, block)
+    const uint32_t l8 = threadIdx.x & 7u;
+    const uint64_t npair = (uint64_t)T * nb;
+    const uint64_t pc = pair < npair ? pair : npair - 1u;         // clamped: whole 8-lane groups stay active
+    const uint32_t t = (uint32_t)(pc / nb), b = (uint32_t)(pc % nb);
+    float D;
+    const uint32_t q = qact_a32_lane(*(const float4 *)(x + (size_t)t * x_stride + 32u * b + 4u * l8), &D);
+    if (pair < npair) {
+        *(uint32_t *)(xq + ((size_t)b * T + t) * 32u + 4u * l8) = q;
+        if (l8 == 0u) xd[(size_t)b * T + t] = D;
+    }
+}
+
+__global__ __launch_bounds__(1024) void k_mm_q80(MmArgs a) {
+    __shared__ float s_p[16][1024];                                // partial j of output (lane, r)
+    const WGeom g = wgeom(a.N, a.K >> 5);
+    const uint32_t lane = __lane_id(), j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n0 = blockIdx.x * 32u, t0 = blockIdx.y * 32u;
+    const uint32_t h = lane >> 5, c = lane & 31u;
+    // operand rows of this lane (clamped: rows / tokens beyond the matrix are not stored)
+    const uint32_t n = min(n0 + c, a.N - 1u), t = min(t0 + c, a.T - 1u);
+    const uint8_t * wq = a.wq + q80_quant_off(g, n >> 4, h, 0u, n & 15u);       // + 256 slot
+    const uint8_t * wm = a.wm + q80_meta_off(g, n >> 4, 0u, n & 15u);           // + 32 slot
+    const uint8_t * xq = a.qa + (size_t)t * 32u + 16u * h;                     // + 32 T b
+    const float * xd = (const float *)(a.qa + a.d_off) + t;                      // + T b
+    const uint32_t cnt = wl_count(g, j), sl0 = wl_slot(g, j, 0u);
+
+    v16f p;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = 0.0f;
+    for (uint32_t k0 = 0; k0 < cnt; k0 += kMmPre) {
+        v4i wa[kMmPre], xb[kMmPre];
+        float dw[kMmPre], dx[kMmPre];
+#pragma unroll
+        for (uint32_t i = 0; i < kMmPre; ++i) {                    // clamped: every load is issued
+            const uint32_t k = min(k0 + i, cnt - 1u), sl = sl0 + k, b = j + 16u * k;
+            wa[i] = *(const v4i *)(wq + 256u * sl);
+            xb[i] = *(const v4i *)(xq + (size_t)32u * a.T * b);
+            dw[i] = h2f_fast(*(const uint16_t *)(wm + 32u * sl));
+            dx[i] = xd[(size_t)a.T * b];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kMmPre; ++i) {
+            if (k0 + i >= cnt) break;
             v16i is = {};
-            is = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, xb, is, 0, 0, 0);
+            is = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa[i], xb[i], is, 0, 0, 0);
             v16f P = {};
-            P = __builtin_amdgcn_mfma_f32_32x32x2f32(dw, dx, P, 0, 0, 0);
+            P = __builtin_amdgcn_mfma_f32_32x32x2f32(h ? 0.0f : dw[i], h ? 0.0f : dx[i], P, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 16; ++r) p[r] = p[r] + P[r] * (float)is[r];
         }
-        // p_j into the tree: level 0 holds an even partial, level 1 a pair, level 2 a quad, level 3 an octet
-        if ((j & 1u) == 0u) {
-            L0 = p;
-        } else {
-            v16f s;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[r] = L0[r] + p[r];
-            if ((j & 2u) == 0u) L1 = s;
-            else {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) s[r] = L1[r] + s[r];
-                if ((j & 4u) == 0u) L2 = s;
-                else {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) s[r] = L2[r] + s[r];
-                    if ((j & 8u) == 0u) L3 = s;
-                    else {
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) L0[r] = L3[r] + s[r];   // the full tree (j = 15)
-                    }
-                }
-            }
-        }
     }
-    // result: lane holds token tbase + c, rows nbase + 8 (r / 4) + 4 h + r % 4; L0 = the tree
-    const uint32_t tt = tbase + c;
-    if (tt < a.T) {
-        float * yr = a.y + (size_t)tt * a.y_stride;
-        const float * ar = a.add ? a.add + (size_t)tt * a.add_stride : nullptr;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t nn = nbase + 8u * (uint32_t)(r >> 2) + 4u * h + (uint32_t)(r & 3);
-            if (nn < a.N) {
-                float v = canon(L0[r]);
-                if (ar) v = sadd(ar[nn], v);
-                else if (a.acc) v = sadd(yr[nn], v);
-                yr[nn] = v;
-            }
-        }
+    for (int r = 0; r < 4; ++r)
+        *(float4 *)&s_p[j][16u * lane + 4u * (uint32_t)r] = make_float4(p[4 * r], p[4 * r + 1], p[4 * r + 2], p[4 * r + 3]);
+    lds_barrier();
+
+    // one thread per output: o = 16 lane' + r of the wave layout above
+    const uint32_t o = threadIdx.x, ol = o >> 4, r = o & 15u;
+    const uint32_t tt = t0 + (ol & 31u), nn = n0 + 8u * (r >> 2) + 4u * (ol >> 5) + (r & 3u);
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = s_p[i][o];
+#pragma unroll
+    for (int w = 16; w > 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w / 2; ++i) v[i] = v[2 * i] + v[2 * i + 1];
+    if (tt < a.T && nn < a.N) {
+        float y = canon(v[0]);
+        float * yp = a.y + (size_t)tt * a.y_stride + nn;
+        if (a.add) y = sadd(a.add[(size_t)tt * a.add_stride + nn], y);
+        else if (a.acc) y = sadd(*yp, y);
+        *yp = y;
     }
 }
 
 }  // namespace tsr
 
+int tsr_launch_qact_mm(const float * x, uint64_t x_stride, uint32_t K, uint32_t T, uint8_t * xq, float * xd,
+                       hipStream_t s) {
+    const uint64_t threads = (uint64_t)T * (K / 32u) * 8u;
+    hipLaunchKernelGGL(tsr::k_qact_mm, dim3((uint32_t)((threads + 255u) / 256u)), dim3(256), 0, s, x, x_stride, K, T, xq, xd);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 int tsr_launch_mm_q8_0(const tsr::MmArgs & a, hipStream_t s) {
-    const dim3 grid((a.N + 63u) / 64u, (a.T + 63u) / 64u);
-    hipLaunchKernelGGL(tsr::k_mm_q80, grid, dim3(256), 0, s, a);
+    const dim3 grid((a.N + 31u) / 32u, (a.T + 31u) / 32u);
+    hipLaunchKernelGGL(tsr::k_mm_q80, grid, dim3(1024), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }

@@ -31,8 +31,8 @@ struct MvArgs {
     uint32_t rb;             // rows per workgroup (set by the launcher)
 };
 
-// Prefill MUL_MAT (T >= 16) on the matrix cores: the activations are first quantized into QA
-// images (qa, one per token, qa_stride bytes apart; the f32 scales at d_off).
+// Prefill MUL_MAT (T >= 16) on the matrix cores: the activations are first quantized (k_qact_mm)
+// into block-major quants at qa ([K/32][T][32 B]) and f32 scales at qa + d_off ([K/32][T]).
 struct MmArgs {
     const uint8_t * wm;
     const uint8_t * wq;
@@ -102,6 +102,8 @@ struct FaArgs {
 int tsr_launch_qact(const tsr::QactArgs & a, uint32_t T, hipStream_t s);
 int tsr_launch_mv_q8_0(const tsr::MvArgs & a, uint32_t n_cu, hipStream_t s);
 int tsr_launch_mv_q4_k(const tsr::MvArgs & a, uint32_t n_cu, hipStream_t s);
+int tsr_launch_qact_mm(const float * x, uint64_t x_stride, uint32_t K, uint32_t T, uint8_t * xq, float * xd,
+                       hipStream_t s);
 int tsr_launch_mm_q8_0(const tsr::MmArgs & a, hipStream_t s);
 int tsr_launch_kv_bytes(const tsr::KvArgs & a, uint32_t which, uint64_t off, uint64_t n, uint8_t * stage, int to_dev,
                         hipStream_t s);

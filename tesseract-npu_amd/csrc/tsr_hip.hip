@@ -189,6 +189,7 @@ namespace {
 
 constexpr uint32_t kKMax = 32768u;
 constexpr uint32_t kMmMinTokens = 16u;   // MUL_MAT with at least this many tokens runs on the matrix cores
+constexpr uint32_t kMmChunk = 4096u;     // tokens per prefill launch pair (bounds the scratch)
 
 uint32_t blk_values(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 32u : 256u; }
 uint32_t blk_bytes(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 34u : 144u; }
@@ -417,29 +418,24 @@ static int mul_mat_locked(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
     ctx->ctr.mul_mat_calls++;
     ctx->ctr.mul_mat_rows += (uint64_t)w->N * T;
     ctx->ctr.mul_mat_weight_bytes += (uint64_t)w->N * nb * blk_bytes(w->fmt);
-    // prefill: T >= 16 tokens of Q8_0 on the matrix cores (QACT A32 of every token into scratch)
+    // prefill: T >= 16 tokens of Q8_0 on the matrix cores (QACT A32 of every token into scratch,
+    // block-major), at most kMmChunk tokens per launch pair
     if (T >= kMmMinTokens && w->fmt == TSR_HIP_FMT_Q8_0 && isums == nullptr) {
-        const uint32_t qa_bytes = (uint32_t)tsr_hip_qa_bytes(0u, w->K);
-        int rc = ctx->scratch.reserve((size_t)std::min(T, 65535u) * qa_bytes, s);
+        const uint32_t chunk = std::min(T, kMmChunk), nbx = w->K / 32u;
+        const size_t q_bytes = (size_t)chunk * w->K, d_off = (q_bytes + 255u) & ~(size_t)255u;
+        int rc = ctx->scratch.reserve(d_off + 4u * (size_t)chunk * nbx, s);
         if (rc) return rc;
-        for (uint32_t t0 = 0; t0 < T; t0 += 65535u) {
-            const uint32_t tt = std::min(T - t0, 65535u);
-            tsr::QactArgs q{};
-            q.x = x_dev + (size_t)t0 * x_stride;
-            q.x_stride = x_stride;
-            q.qa = (uint8_t *)ctx->scratch.ptr;
-            q.qa_bytes = qa_bytes;
-            q.K = w->K;
-            q.kind = 0u;
-            q.d_off = (w->K + 63u) / 64u * 64u;
-            q.bs_off = q.d_off + (4u * (w->K / 32u) + 63u) / 64u * 64u;
-            if (tsr_launch_qact(q, tt, s)) return TSR_HIP_E_HIP;
+        for (uint32_t t0 = 0; t0 < T; t0 += chunk) {
+            const uint32_t tt = std::min(T - t0, chunk);
+            uint8_t * xq = (uint8_t *)ctx->scratch.ptr;
+            if (tsr_launch_qact_mm(x_dev + (size_t)t0 * x_stride, x_stride, w->K, tt, xq, (float *)(xq + d_off), s))
+                return TSR_HIP_E_HIP;
             tsr::MmArgs m{};
             m.wm = w->dev;
             m.wq = w->dev + w->quant_off;
-            m.qa = q.qa;
-            m.qa_stride = qa_bytes;
-            m.d_off = q.d_off;
+            m.qa = xq;
+            m.qa_stride = 0u;
+            m.d_off = (uint32_t)d_off;
             m.y = y_dev + (size_t)t0 * y_stride;
             m.y_stride = y_stride;
             m.add = add_dev ? add_dev + (size_t)t0 * add_stride : nullptr;

@@ -23,6 +23,8 @@
 #include "kernels.hpp"
 #include "qact.hpp"
 
+#include <algorithm>
+
 namespace tsr {
 
 constexpr uint32_t kMFloor = 0xF1800000u;   // -2^100 (AT 6.3)
@@ -258,162 +260,207 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// P.V and the merge: block (item * 4 + channel c, KV head g, slice sl), 16 waves.
-// A unit is (segment, head): lane = cell for EXP, the block-float weights and LSUM, then lane =
-// value of the 64-value slice for the exact sum A = sum W q on v_dot4 over the base-256 digits.
-// The per-segment results go to LDS; the f32 segment chain then runs in segment order.
+// P.V: block (item * 4 + channel c, KV head g, group hg of 4 query heads); one wave per segment of
+// the channel (4 of its groups = 64 cells), looping if there are more segments than waves. Each
+// segment's results go to LDS; the f32 segment chain then runs in segment order.
+//
+// Phase A (lane = head row hr = lane / 16, 4 consecutive cells of the segment: group kk = (lane /
+// 4) % 4, cells 4 (lane % 4) .. + 3): EXP of the scores, the weights w = p dV of the value blocks,
+// and, over the 16 lanes of a head row (DPP), the segment's block-float exponent E_S per 64-value
+// slice, the non-finite flags per block and LSUM. The block-float integers W = RNE(w 2^(23 - E_S))
+// (|W| <= 2^24) are split into four balanced base-256 digits d_k in [-128, 127]: the bytes of
+// (W + 0x80808080) ^ 0x80808080 (the offset makes every byte d_k + 128, the xor subtracts 128).
+// The digits go to LDS as [block][head][digit][group][16 cells].
+// Phase B (matrix core): A[h][v] = sum_cells W[h][cell] q[cell][v] = sum_k 256^k sum_cells d_k q is
+// v_mfma_i32_16x16x64_i8 with rows (head, digit), columns 16 values and K the 64 cells; lane l then
+// holds the four digit sums of head l / 16 and value l % 16 and forms A exactly in 64 bits.
 // ---------------------------------------------------------------------------------------------
-constexpr int kHB = 16;                                           // heads per LDS batch
-constexpr int kMaxSeg = 8;                                        // NCG <= 128 -> <= 32 groups per channel
+constexpr uint32_t kPvWaves = 8;                                  // NCG <= 128 -> <= 8 segments per channel
+constexpr uint32_t kPvMaxSeg = 8;
 
 __device__ __forceinline__ float ctree4(float x0, float x1, float x2, float x3) { return sadd(sadd(x0, x1), sadd(x2, x3)); }
+__device__ __forceinline__ int32_t row16_imax(int32_t v) {          // signed max over a 16-lane row
+    return (int32_t)(row16_umax((uint32_t)v ^ 0x80000000u) ^ 0x80000000u);
+}
+__device__ __forceinline__ int32_t row16_isum(int32_t v) {
+    v += dpp_i<kDppXor1>(v);
+    v += dpp_i<kDppXor2>(v);
+    v += dpp_i<kDppRowHalfMirror>(v);
+    return v + dpp_i<kDppRowMirror>(v);
+}
+__device__ __forceinline__ int32_t f_exp(float f) { return (int32_t)((fb(f) >> 23) & 0xFFu) - 127; }
+__device__ __forceinline__ bool f_nonfinite(float f) { return (fb(f) & 0x7F800000u) == 0x7F800000u; }
 
-template <bool INL>
-__global__ __launch_bounds__(1024) void k_fa_pv(FaArgs a, FaPlan p) {
-    __shared__ __align__(16) int8_t s_dig[16][2][4][64];          // wave, block e, digit, cell
-    __shared__ float s_c[kMaxSeg][kHB][64];
-    __shared__ float s_l[kMaxSeg][kHB];
-    __shared__ uint32_t s_t64[64];
-    const uint32_t t64v = a.ex.t64[threadIdx.x & 63u];           // first: the table write waits for it only
-    const uint32_t item = blockIdx.x >> 2, c = blockIdx.x & 3u, g = blockIdx.y, sl = blockIdx.z;
+typedef int v4i_fa __attribute__((ext_vector_type(4)));
+
+template <int D, bool INL>
+__global__ __launch_bounds__(64 * kPvWaves) void k_fa_pv(FaArgs a, FaPlan p) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr uint32_t NBD = D / 32;                              // value blocks of a head
+    constexpr uint32_t BB = NBD < 4 ? NBD : 4;                    // blocks per batch (2 or 4)
+    const uint32_t G = a.G, E = a.E, nh = a.n_head;
+    const uint32_t nbk = E / 32u;                                 // value blocks of a cell
+    uint32_t * s_t64 = (uint32_t *)lds;                           // EXPK table
+    float * s_c = (float *)(lds + 256);                           // [seg][4 heads][D]
+    float * s_l = s_c + kPvMaxSeg * 4u * D;                       // [seg][4 heads]
+    uint8_t * s_dg = (uint8_t *)(s_l + kPvMaxSeg * 4u);          // per wave: [4 blocks][4 heads][4 digits][4 groups][16]
+    const uint32_t t64v = a.ex.t64[threadIdx.x & 63u];            // first: the table write waits for it only
+    const uint32_t item = blockIdx.x >> 2, c = blockIdx.x & 3u, g = blockIdx.y, hg = blockIdx.z;
     const FaItem it = fa_item<INL>(a, p, item);
-    const uint32_t G = a.G, D = a.D, E = a.E, n16 = 16u * it.n, nbk = E / 32u, nh = a.n_head, nsl = D / 64u;
-    const int lane = (int)__lane_id(), wave = (int)(threadIdx.x >> 6), nw = (int)(blockDim.x >> 6);
+    const uint32_t lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nw = blockDim.x >> 6;
+    const uint32_t hr = lane >> 4, kk = (lane >> 2) & 3u, quad = lane & 3u;
+    const uint32_t hi = 4u * hg + hr;                             // query head within the KV head
+    const bool head_ok = hi < G;
+    const uint32_t h = g * G + min(hi, G - 1u);
     const uint32_t u_first = it.u0 + ((c + 4u - (it.u0 & 3u)) & 3u);
     const uint32_t u_end = it.u0 + it.n;
     const uint32_t nu = u_first < u_end ? (u_end - 1u - u_first) / 4u + 1u : 0u;
     const uint32_t nseg = (nu + 3u) / 4u;
-    const uint32_t sa = g * nsl + sl;                             // slice of the cell row
-    const uint32_t d = 64u * sa + (uint32_t)lane;                 // this lane's value in the cell row
-    const int e_l = lane >> 5;
-    const float * S = a.S + (size_t)it.s_off * nh;
+    const uint32_t n16 = 16u * it.n;
+    const float * S = a.S + (size_t)it.s_off * nh + (size_t)h * n16;
     const uint16_t * vmeta = (const uint16_t *)a.vc.base;
     const uint8_t * vq = a.vc.base + a.vc.quant_off;
+    uint8_t * dg = s_dg + (size_t)wave * 4096u;
+    if (threadIdx.x < 64u) s_t64[threadIdx.x] = t64v;
+    lds_barrier();
 
-    // A unit's loads: its V quants (lane = value), score and V scales (lane = cell), and the tile
-    // maxima of its head (lane < ntiles; clamped lanes repeat a tile, which leaves the maximum as it
-    // is). Each wave issues the loads of its next unit before it computes the current one.
-    struct UnitLoads {
-        int4 vqd[4];
-        float sv;
-        uint32_t mv, mkey;
-    };
-    auto load_unit = [&](uint32_t unit, uint32_t hb0, uint32_t hbn) {
-        UnitLoads L;
-        const uint32_t seg = unit / hbn, hi = unit % hbn, h = g * G + hb0 + hi;
-        const uint32_t ngr = min(nu - 4u * seg, 4u);
-#pragma unroll
-        for (uint32_t gi = 0; gi < 4; ++gi) {
-            const uint32_t ug = u_first + 4u * (4u * seg + min(gi, ngr - 1u));
-            L.vqd[gi] = *(const int4 *)(vq + (size_t)ug * 16u * E + (size_t)d * 16u);
-        }
-        const uint32_t grp = 4u * seg + ((uint32_t)lane >> 4);
-        const uint32_t u = u_first + 4u * min(grp, nu - 1u), rr = (uint32_t)lane & 15u;
-        L.sv = S[(size_t)h * n16 + 16u * (u - it.u0) + rr];
-        L.mv = *(const uint32_t *)(vmeta + ((size_t)u * 16u + rr) * nbk + 2u * sa);
-        L.mkey = maxt_key_f(a.Mpart[(size_t)(it.tile0 + min((uint32_t)lane, it.ntiles - 1u)) * nh + h]);
-        return L;
-    };
+    // chunk maximum of head h: MAXOUT of the floor and the tile maxima (row lanes < ntiles read one each)
+    const uint32_t mkey = maxt_key_f(a.Mpart[(size_t)(it.tile0 + min(lane & 15u, it.ntiles - 1u)) * nh + h]);
+    const float m = maxt_unkey(row16_umax(max(mkey, maxt_key_f(bf(kMFloor)))));
 
-    for (uint32_t hb0 = 0; hb0 < G; hb0 += kHB) {
-        const uint32_t hbn = min((uint32_t)kHB, G - hb0), units = nseg * hbn;
-        UnitLoads cur;
-        if ((uint32_t)wave < units) cur = load_unit((uint32_t)wave, hb0, hbn);   // a channel may have no groups
-        if (hb0 == 0u) {
-            if (threadIdx.x < 64u) s_t64[threadIdx.x] = t64v;
-            lds_barrier();                                        // the unit loads stay in flight
+    for (uint32_t seg = wave; seg < nseg; seg += nw) {
+        // ---- phase A: lane = (head row, 4 cells) ----------------------------------------------
+        const uint32_t gi = 4u * seg + kk;                         // the channel's group index
+        const bool cv = gi < nu;
+        const uint32_t u = u_first + 4u * min(gi, nu - 1u);        // clamped: loads stay in the item
+        const uint32_t j0 = 16u * (u - it.u0) + 4u * quad;         // first cell of the lane in the chunk
+        const float4 sv = *(const float4 *)(S + j0);
+        const float ss[4] = { sv.x, sv.y, sv.z, sv.w };
+        float pz[4];
+        bool pnf_any = false;
+        int32_t ep = -1000;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float pe = (cv && head_ok) ? expk(smul(ssub(ss[i], m), a.scale), a.ex, s_t64) : 0.0f;
+            pz[i] = daz(pe);
+            const bool nf = f_nonfinite(pz[i]);
+            pnf_any |= nf;
+            if (!nf && (fb(pz[i]) & 0x7FFFFFFFu)) ep = max(ep, f_exp(pz[i]));
         }
-        for (uint32_t unit = (uint32_t)wave; unit < units; unit += (uint32_t)nw) {
-            const UnitLoads nxt = load_unit(min(unit + (uint32_t)nw, units - 1u), hb0, hbn);
-            const uint32_t seg = unit / hbn, hi = unit % hbn;
-            const uint32_t ngr = min(nu - 4u * seg, 4u);
-            const int4 * vqd = cur.vqd;
-            const float sv = cur.sv;
-            const uint32_t mv = cur.mv;
-            // MAXOUT of the chunk: the floor and the maxima of its tiles (MAXT: a total order)
-            const float m = maxt_unkey(wave_max_u(max(cur.mkey, maxt_key_f(bf(kMFloor)))));
-            const uint32_t grp = 4u * seg + ((uint32_t)lane >> 4);
-            const bool cv = grp < nu;
-            // --- lane = cell k of the segment ---------------------------------------------
-            const float p = cv ? expk(smul(ssub(sv, m), a.scale), a.ex, s_t64) : 0.0f;
-            const float pz = daz(p);
-            const bool live = cv && (fb(pz) & 0x7FFFFFFFu) != 0u;
-            const float w0 = live ? smul(p, h2f_exact(mv & 0xFFFFu)) : 0.0f;
-            const float w1 = live ? smul(p, h2f_exact(mv >> 16)) : 0.0f;
-            const bool nf0 = (fb(w0) & 0x7F800000u) == 0x7F800000u;
-            const bool nf1 = (fb(w1) & 0x7F800000u) == 0x7F800000u;
-            const bool bad0 = __ballot(nf0) != 0ull, bad1 = __ballot(nf1) != 0ull;
-            int ex = -1000;
-            if (!nf0 && (fb(w0) & 0x7FFFFFFFu)) ex = (int)((fb(w0) >> 23) & 0xFFu) - 127;
-            if (!nf1 && (fb(w1) & 0x7FFFFFFFu)) ex = max(ex, (int)((fb(w1) >> 23) & 0xFFu) - 127);
-            const int es = wave_max_i(ex);
-            const bool any = es > -1000;
-            const int32_t W0 = (any && !bad0) ? bf_int(w0, es) : 0;
-            const int32_t W1 = (any && !bad1) ? bf_int(w1, es) : 0;
-            int32_t r0 = W0, r1 = W1;                               // balanced base-256 digits
+        // LSUM of the segment (AT 6.5): block float of its p values
+        const bool badl = row16_umax(pnf_any ? 1u : 0u) != 0u;
+        ep = row16_imax(ep);
+        int32_t lsum = 0;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int32_t d0 = ((r0 + 128) & 255) - 128, d1 = ((r1 + 128) & 255) - 128;
-                s_dig[wave][0][k][lane] = (int8_t)d0;
-                s_dig[wave][1][k][lane] = (int8_t)d1;
-                r0 = (r0 - d0) >> 8;
-                r1 = (r1 - d1) >> 8;
-            }
-            // LSUM of the segment (AT 6.5): block float of its p values
-            const bool pnf = cv && (fb(pz) & 0x7F800000u) == 0x7F800000u;
-            const bool badl = __ballot(pnf) != 0ull;
-            int ep = -1000;
-            if (cv && !pnf && (fb(pz) & 0x7FFFFFFFu)) ep = (int)((fb(pz) >> 23) & 0xFFu) - 127;
-            ep = wave_max_i(ep);
-            float ls;
-            if (badl) ls = bf(kNaN);
-            else if (ep == -1000) ls = 0.0f;
-            else ls = bf_f((int64_t)wave_sum_i((cv && !pnf) ? bf_int(pz, ep) : 0), ep - 23);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            // --- lane = value of the slice ------------------------------------------------
-            int32_t sk[4] = { 0, 0, 0, 0 };
+        for (int i = 0; i < 4; ++i) lsum += f_nonfinite(pz[i]) ? 0 : bf_int(pz[i], ep);
+        lsum = row16_isum(lsum);
+        if ((lane & 15u) == 0u)
+            s_l[seg * 4u + hr] = badl ? bf(kNaN) : (ep == -1000 ? 0.0f : bf_f((int64_t)lsum, ep - 23));
+
+        const uint16_t * vm = vmeta + ((size_t)u * 16u + 4u * quad) * nbk + (size_t)g * NBD;
+#pragma unroll 1
+        for (uint32_t vb = 0; vb < NBD; vb += BB) {                // BB value blocks (32 BB values) at a time
+            // weights of the 4 cells for the BB blocks
+            float w[4][BB];
+            int32_t ex[BB / 2];
+            bool nfb[BB];
 #pragma unroll
-            for (uint32_t gi = 0; gi < 4; ++gi) {
-                if (gi < ngr) {
+            for (uint32_t e = 0; e < BB; ++e) nfb[e] = false;
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const int4 dg = *(const int4 *)&s_dig[wave][e_l][k][16u * gi];
-                        int acc = sk[k];
-                        acc = dot4(dg.x, vqd[gi].x, acc);
-                        acc = dot4(dg.y, vqd[gi].y, acc);
-                        acc = dot4(dg.z, vqd[gi].z, acc);
-                        acc = dot4(dg.w, vqd[gi].w, acc);
-                        sk[k] = acc;
-                    }
+            for (uint32_t sa = 0; sa < BB / 2; ++sa) ex[sa] = -1000;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t dv[BB];
+                if constexpr (BB == 4) {
+                    const uint2 mv = *(const uint2 *)(vm + (size_t)i * nbk + vb);
+                    dv[0] = mv.x & 0xFFFFu; dv[1] = mv.x >> 16; dv[2] = mv.y & 0xFFFFu; dv[3] = mv.y >> 16;
+                } else {
+                    const uint32_t mv = *(const uint32_t *)(vm + (size_t)i * nbk + vb);
+                    dv[0] = mv & 0xFFFFu; dv[1] = mv >> 16;
+                }
+                const bool live = (fb(pz[i]) & 0x7FFFFFFFu) != 0u;
+#pragma unroll
+                for (uint32_t e = 0; e < BB; ++e) {
+                    const float we = live ? smul(pz[i], h2f_exact(dv[e])) : 0.0f;
+                    w[i][e] = we;
+                    const bool nf = f_nonfinite(we);
+                    nfb[e] |= nf;
+                    if (!nf && (fb(we) & 0x7FFFFFFFu)) ex[e >> 1] = max(ex[e >> 1], f_exp(we));
                 }
             }
-            const int64_t A = (int64_t)sk[0] + ((int64_t)sk[1] << 8) + ((int64_t)sk[2] << 16) + ((int64_t)sk[3] << 24);
-            const bool badv = e_l ? bad1 : bad0;
-            s_c[seg][hi][lane] = badv ? bf(kNaN) : (any ? bf_f(A, es - 23) : 0.0f);
-            if (lane == 0) s_l[seg][hi] = ls;
+            int32_t es[BB / 2];
+            bool any[BB / 2], bad[BB];
+#pragma unroll
+            for (uint32_t sa = 0; sa < BB / 2; ++sa) { es[sa] = row16_imax(ex[sa]); any[sa] = es[sa] > -1000; }
+#pragma unroll
+            for (uint32_t e = 0; e < BB; ++e) bad[e] = row16_umax(nfb[e] ? 1u : 0u) != 0u;
+            // digits: for block e and digit k, the 4 cells' digit bytes in one word
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            cur = nxt;
-        }
-        __syncthreads();
-        for (uint32_t idx = threadIdx.x; idx < hbn * 64u; idx += blockDim.x) {   // segment chains in order
-            const uint32_t hi = idx >> 6, L = idx & 63u, h = g * G + hb0 + hi;
-            float O = 0.0f;
-            for (uint32_t seg = 0; seg < nseg; ++seg) O = sadd(O, s_c[seg][hi][L]);
-            const size_t slot = ((size_t)item * 4u + c) * nh + h;
-            a.OP[slot * D + 64u * sl + L] = O;
-            if (L == 0u) {
-                float l = 0.0f;
-                for (uint32_t seg = 0; seg < nseg; ++seg) l = sadd(l, s_l[seg][hi]);
-                a.LP[slot * nsl + sl] = l;
+#pragma unroll
+            for (uint32_t e = 0; e < BB; ++e) {
+                uint32_t P[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int32_t W = (any[e >> 1] && !bad[e]) ? bf_int(w[i][e], es[e >> 1]) : 0;
+                    P[i] = ((uint32_t)W + 0x80808080u) ^ 0x80808080u;     // byte k = digit k of W
+                }
+                // transpose the 4 x 4 bytes: word k = digit k of cells 0..3
+                const uint32_t lo01 = __builtin_amdgcn_perm(P[1], P[0], 0x05010400u);   // d0c0 d0c1 d1c0 d1c1
+                const uint32_t lo23 = __builtin_amdgcn_perm(P[3], P[2], 0x05010400u);
+                const uint32_t hi01 = __builtin_amdgcn_perm(P[1], P[0], 0x07030602u);   // d2c0 d2c1 d3c0 d3c1
+                const uint32_t hi23 = __builtin_amdgcn_perm(P[3], P[2], 0x07030602u);
+                const uint32_t q[4] = { __builtin_amdgcn_perm(lo23, lo01, 0x05040100u), __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                                        __builtin_amdgcn_perm(hi23, hi01, 0x05040100u), __builtin_amdgcn_perm(hi23, hi01, 0x07060302u) };
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    *(uint32_t *)(dg + (((e * 4u + hr) * 4u + (uint32_t)k) * 4u + kk) * 16u + 4u * quad) = q[k];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // ---- phase B: 8 tiles of 16 values; lane = (head row l / 16 of the result, value l % 16)
+            const uint32_t kB = lane >> 4;                          // the operand's 16 cells: group kB
+            const uint32_t uB = u_first + 4u * min(4u * seg + kB, nu - 1u);
+            const uint8_t * vqB = vq + ((size_t)uB * E + (size_t)g * D + 32u * vb + (lane & 15u)) * 16u;
+            int4 Bv[2 * BB];
+#pragma unroll
+            for (uint32_t t8 = 0; t8 < 2 * BB; ++t8) Bv[t8] = *(const int4 *)(vqB + 256u * t8);
+#pragma unroll
+            for (uint32_t e = 0; e < BB; ++e) {
+                // A operand: row l % 16 = (head, digit), K = the 16 cells of group l / 16
+                const v4i_fa Aop = *(const v4i_fa *)(dg + ((e * 16u + (lane & 15u)) * 4u + (lane >> 4)) * 16u);
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const int4 bq = Bv[2 * e + half];
+                    const v4i_fa Bop = { bq.x, bq.y, bq.z, bq.w };
+                    v4i_fa acc = { 0, 0, 0, 0 };
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Aop, Bop, acc, 0, 0, 0);
+                    const int64_t A = (int64_t)acc[0] + ((int64_t)acc[1] << 8) + ((int64_t)acc[2] << 16) + ((int64_t)acc[3] << 24);
+                    const float cval = bad[e] ? bf(kNaN) : (any[e >> 1] ? bf_f(A, es[e >> 1] - 23) : 0.0f);
+                    s_c[(seg * 4u + hr) * D + 32u * (vb + e) + 16u * (uint32_t)half + (lane & 15u)] = cval;
+                }
             }
         }
-        __syncthreads();
     }
-
+    __syncthreads();
+    // segment chains in order (AT 6.4 O, 6.5 l): thread = (head row, value)
+    for (uint32_t idx = threadIdx.x; idx < 4u * D; idx += blockDim.x) {
+        const uint32_t r4 = idx / D, v = idx % D, hi2 = 4u * hg + r4;
+        if (hi2 >= G) continue;
+        const uint32_t h2 = g * G + hi2;
+        float O = 0.0f;
+        for (uint32_t seg = 0; seg < nseg; ++seg) O = sadd(O, s_c[(seg * 4u + r4) * D + v]);
+        const size_t slot = ((size_t)item * 4u + c) * nh + h2;
+        a.OP[slot * D + v] = O;
+        if (v == 0u) {
+            float l = 0.0f;
+            for (uint32_t seg = 0; seg < nseg; ++seg) l = sadd(l, s_l[seg * 4u + r4]);
+            a.LP[slot] = l;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -427,7 +474,7 @@ constexpr uint32_t kMergeHeads = 4;                              // heads per bl
 
 template <bool INL>
 __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
-    const uint32_t G = a.G, D = a.D, nh = a.n_head, nsl = D / 64u;
+    const uint32_t G = a.G, D = a.D, nh = a.n_head;
     const uint32_t ngrp = (G + kMergeHeads - 1u) / kMergeHeads;
     const uint32_t t = blockIdx.x, g = blockIdx.y / ngrp, h0 = g * G + (blockIdx.y % ngrp) * kMergeHeads;
     const uint32_t hn = min(kMergeHeads, g * G + G - h0), sl = blockIdx.z;
@@ -450,7 +497,7 @@ __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
             for (uint32_t c = 0; c < 4u; ++c) {
                 const size_t slot = (kk * 4u + c) * nh + h;
                 op[k][c] = a.OP[slot * D + 64u * sl + L];
-                lp[k][c] = a.LP[slot * nsl + sl];
+                lp[k][c] = a.LP[slot];
             }
         }
         // chunk maxima: lane 8 k + j (k < 4) reads tile j (clamped) of chunk k; MAXOUT over the
@@ -513,7 +560,23 @@ static int launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, h
         default: return -2;
     }
     if (hipGetLastError() != hipSuccess) return -4;
-    hipLaunchKernelGGL(tsr::k_fa_pv<INL>, dim3(4u * p.n_items, a.n_head_kv, a.D / 64u), dim3(1024), 0, s, a, p);
+    // P.V: waves = the most segments of any item (<= 8), LDS = table, segment results, digits
+    uint32_t maxn = 0;
+    if (INL) {
+        for (uint32_t i = 0; i < p.n_items; ++i) maxn = std::max(maxn, p.items[i].n);
+    } else {
+        maxn = a.max_groups;
+    }
+    const uint32_t nwv = std::max(1u, std::min(tsr::kPvWaves, ((maxn + 3u) / 4u + 3u) / 4u));
+    const size_t lds_pv = 256u + 4u * (size_t)tsr::kPvMaxSeg * 4u * a.D + 4u * tsr::kPvMaxSeg * 4u + 4096u * nwv;
+    const dim3 gpv(4u * p.n_items, a.n_head_kv, (a.G + 3u) / 4u);
+    switch (a.D) {
+        case 64: hipLaunchKernelGGL((tsr::k_fa_pv<64, INL>), gpv, dim3(64u * nwv), lds_pv, s, a, p); break;
+        case 128: hipLaunchKernelGGL((tsr::k_fa_pv<128, INL>), gpv, dim3(64u * nwv), lds_pv, s, a, p); break;
+        case 256: hipLaunchKernelGGL((tsr::k_fa_pv<256, INL>), gpv, dim3(64u * nwv), lds_pv, s, a, p); break;
+        case 512: hipLaunchKernelGGL((tsr::k_fa_pv<512, INL>), gpv, dim3(64u * nwv), lds_pv, s, a, p); break;
+        default: return -2;
+    }
     if (hipGetLastError() != hipSuccess) return -4;
     const uint32_t ngrp = (a.G + tsr::kMergeHeads - 1u) / tsr::kMergeHeads;
     hipLaunchKernelGGL(tsr::k_fa_merge<INL>, dim3(T, a.n_head_kv * ngrp, a.D / 64u), dim3(256), 0, s, a, p);

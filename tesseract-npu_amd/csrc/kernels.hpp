@@ -91,7 +91,8 @@ struct FaArgs {
     float * S;               // scores
     float * Mpart;           // [tile][n_head] tile maxima
     float * OP;              // [item][4][n_head][D] channel partials
-    float * LP;              // [item][4][n_head][D / 64] channel row sums (one per slice)
+    float * LP;              // [item][4][n_head] channel row sums
+    uint32_t max_groups;     // the largest item (groups), for a work list in device memory
     float * out;
     uint64_t out_stride;
     ExpkTab ex;

@@ -268,13 +268,12 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     if (cells * n_head > 0xFFFFFFFFull || n_items * 4u > 0x7FFFFFFFull || n_items * maxtiles > 0x7FFFFFFFull)
         return TSR_HIP_E_SHAPE;
     const bool inl = n_items <= tsr::kFaInlItems && T <= tsr::kFaInlTok;
-    const uint32_t nsl = D / 64u;
     size_t off = 0;
     const size_t o_items = off; off = up256(off + (inl ? 0u : n_items * sizeof(tsr::FaItem) + 8u * (size_t)T));
     const size_t o_S = off; off = up256(off + 4u * (size_t)cells * n_head);
     const size_t o_Mp = off; off = up256(off + 4u * (size_t)n_tiles * n_head);
     const size_t o_OP = off; off = up256(off + 4u * n_items * kC * n_head * D);
-    const size_t o_LP = off; off = up256(off + 4u * n_items * kC * n_head * nsl);
+    const size_t o_LP = off; off = up256(off + 4u * n_items * kC * n_head);
 
     tsr::FaPlan p{};
     p.n_items = (uint32_t)n_items;
@@ -325,6 +324,7 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     a.Mpart = (float *)(base + o_Mp);
     a.OP = (float *)(base + o_OP);
     a.LP = (float *)(base + o_LP);
+    for (const tsr::FaItem & i : items) a.max_groups = std::max(a.max_groups, i.n);
     a.out = out_dev;
     a.out_stride = out_stride;
     a.ex = ctx->expk;

@@ -19,7 +19,7 @@
 // Block float (AT 6.4; sw/sim/tsr_ref_at.c:380-488): in a segment every weight w = p dV is scaled
 // to an integer W = RNE(w 2^(23 - E_S)) (|W| <= 2^24) and A = sum W q is exact. W is split into four
 // balanced base-256 digits d_k in [-128, 127] (W = sum d_k 256^k), so A = sum_k 256^k (sum d_k q)
-// runs on v_dot4_i32_i8 with exact int32 partial sums (|sum| <= 64 * 128 * 128).
+// runs on the int8 matrix core with exact int32 digit sums (|sum| <= 64 * 128 * 128).
 #include "kernels.hpp"
 #include "qact.hpp"
 
@@ -104,38 +104,6 @@ __device__ __forceinline__ int wave_sum_i(int v) {
     v += dpp_i<kDppRowMirror>(v);
     v += xor16_i(v);
     return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
-}
-
-// RNE_int(w 2^(23 - es)), exponent(w) <= es; zero / subnormal w -> 0 (sw/sim/tsr_ref_at.c:386-410).
-// Straight-line: a shift of 26 or more leaves 0 after rounding (|m| < 2^24), so it is clamped to 31.
-__device__ __forceinline__ int32_t bf_int(float w, int32_t es) {
-    const uint32_t u = fb(w), e = (u >> 23) & 0xFFu;
-    const uint32_t m = 0x00800000u | (u & 0x007FFFFFu);
-    const int32_t sh0 = es - ((int32_t)e - 127);
-    const uint32_t sh = (uint32_t)min(max(sh0, 0), 31);
-    uint32_t v = m >> sh;
-    const uint32_t r = m & ((1u << sh) - 1u), h = sh ? 1u << (sh - 1u) : 0u;
-    v += (sh && (r > h || (r == h && (v & 1u)))) ? 1u : 0u;
-    const int32_t sv = (u >> 31) ? -(int32_t)v : (int32_t)v;
-    return e == 0u ? 0 : sv;
-}
-// RNE24(A) 2^k; below 2^-126 a signed zero, from 2^128 a signed Inf (sw/sim/tsr_ref_at.c:412-436).
-// Straight-line.
-__device__ __forceinline__ float bf_f(int64_t A, int32_t k) {
-    const uint32_t s = A < 0 ? 0x80000000u : 0u;
-    const uint64_t mag = A < 0 ? (uint64_t)0 - (uint64_t)A : (uint64_t)A;
-    const int32_t msb = 63 - (int32_t)__builtin_clzll(mag | 1ull);
-    const uint32_t shr = (uint32_t)max(msb - 23, 0), shl = (uint32_t)max(23 - msb, 0);
-    uint64_t sig = mag >> shr;
-    const uint64_t r = mag & ((1ull << shr) - 1ull), h = shr ? 1ull << (shr - 1u) : 0ull;
-    sig += (shr && (r > h || (r == h && (sig & 1ull)))) ? 1ull : 0ull;
-    const bool carry = (sig >> 24) != 0ull;
-    sig = carry ? sig >> 1 : sig;
-    sig = sig << shl;
-    const int32_t e = msb + k + (carry ? 1 : 0);
-    uint32_t out = s | ((uint32_t)(e + 127) << 23) | ((uint32_t)sig & 0x007FFFFFu);
-    out = e < -126 ? s : (e > 127 ? (s | 0x7F800000u) : out);
-    return bf(A == 0 ? 0u : out);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -260,9 +228,11 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// P.V: block (item * 4 + channel c, KV head g, group hg of 4 query heads); one wave per segment of
-// the channel (4 of its groups = 64 cells), looping if there are more segments than waves. Each
-// segment's results go to LDS; the f32 segment chain then runs in segment order.
+// P.V: block (item * 4 + channel c, KV head g, group hg of 4 query heads x value part vh of VS); one
+// wave per segment of the channel (4 of its groups = 64 cells), looping if there are more segments
+// than waves. Each segment's results go to LDS; the f32 segment chain then runs in segment order.
+// A block covers D / VS values of its heads (VS > 1 when the grid would not fill the chip: the
+// value-independent EXP and LSUM work is then repeated per part, the value work is split).
 //
 // Phase A (lane = head row hr = lane / 16, 4 consecutive cells of the segment: group kk = (lane /
 // 4) % 4, cells 4 (lane % 4) .. + 3): EXP of the scores, the weights w = p dV of the value blocks,
@@ -273,39 +243,64 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
 // The digits go to LDS as [block][head][digit][group][16 cells].
 // Phase B (matrix core): A[h][v] = sum_cells W[h][cell] q[cell][v] = sum_k 256^k sum_cells d_k q is
 // v_mfma_i32_16x16x64_i8 with rows (head, digit), columns 16 values and K the 64 cells; lane l then
-// holds the four digit sums of head l / 16 and value l % 16 and forms A exactly in 64 bits.
+// holds the four digit sums of head l / 16 and value l % 16 and forms A exactly in f64.
+// Every global load of the first batch is issued before the EXP work, so that a block waits for
+// memory once.
 // ---------------------------------------------------------------------------------------------
 constexpr uint32_t kPvWaves = 8;                                  // NCG <= 128 -> <= 8 segments per channel
 constexpr uint32_t kPvMaxSeg = 8;
 
 __device__ __forceinline__ float ctree4(float x0, float x1, float x2, float x3) { return sadd(sadd(x0, x1), sadd(x2, x3)); }
-__device__ __forceinline__ int32_t row16_imax(int32_t v) {          // signed max over a 16-lane row
-    return (int32_t)(row16_umax((uint32_t)v ^ 0x80000000u) ^ 0x80000000u);
-}
 __device__ __forceinline__ int32_t row16_isum(int32_t v) {
     v += dpp_i<kDppXor1>(v);
     v += dpp_i<kDppXor2>(v);
     v += dpp_i<kDppRowHalfMirror>(v);
     return v + dpp_i<kDppRowMirror>(v);
 }
-__device__ __forceinline__ int32_t f_exp(float f) { return (int32_t)((fb(f) >> 23) & 0xFFu) - 127; }
-__device__ __forceinline__ bool f_nonfinite(float f) { return (fb(f) & 0x7F800000u) == 0x7F800000u; }
+__device__ __forceinline__ uint32_t f_field(float f) { return (fb(f) >> 23) & 0xFFu; }   // biased exponent
+
+// RNE_int(w 2^(23 - es)) of a zero or normal w with exponent(w) <= es (sw/sim/tsr_ref_at.c:386-410):
+// the power-of-two scaling is exact while the scaled value is normal, v_rndne_f32 rounds half to even,
+// and a scaled value below 2^-126 is below 1/2 and rounds to 0 either way. |result| <= 2^24.
+__device__ __forceinline__ int32_t bf_int_n(float w, int32_t es) {
+    return (int32_t)__builtin_rintf(__builtin_ldexpf(w, 23 - es));
+}
+// f = RNE24(A) (zero or normal) scaled by 2^k: below 2^-126 a signed zero, from 2^128 a signed Inf,
+// A == 0 -> +0 (sw/sim/tsr_ref_at.c:412-436). The exponent field of f plus k is the result's.
+__device__ __forceinline__ float bf_scale(float f, int32_t k) {
+    const uint32_t u = fb(f), s = u & 0x80000000u;
+    const int32_t ne = (int32_t)((u >> 23) & 0xFFu) + k;
+    uint32_t out = u + ((uint32_t)k << 23);
+    out = ne < 1 ? s : (ne > 254 ? (s | 0x7F800000u) : out);
+    return bf((u & 0x7FFFFFFFu) == 0u ? 0u : out);
+}
 
 typedef int v4i_fa __attribute__((ext_vector_type(4)));
 
-template <int D, bool INL>
+// A = d0 + 256 d1 + 65536 d2 + 2^24 d3 of four digit sums (|d_k| <= 2^20): every product and partial
+// sum is exact in f64 (|A| < 2^45), and the one conversion to f32 is RNE24(A).
+__device__ __forceinline__ float digits_rne24(const v4i_fa & acc) {
+    const double A = ((double)acc[3] * 16777216.0 + (double)acc[2] * 65536.0) + ((double)acc[1] * 256.0 + (double)acc[0]);
+    return (float)A;
+}
+
+template <int D, bool INL, int VS>
 __global__ __launch_bounds__(64 * kPvWaves) void k_fa_pv(FaArgs a, FaPlan p) {
     extern __shared__ __align__(16) uint8_t lds[];
-    constexpr uint32_t NBD = D / 32;                              // value blocks of a head
-    constexpr uint32_t BB = NBD < 4 ? NBD : 4;                    // blocks per batch (2 or 4)
+    constexpr uint32_t DV = D / VS;                               // values of the block (>= 64)
+    constexpr uint32_t NBV = DV / 32;                             // their value blocks
+    constexpr uint32_t BB = NBV < 4 ? NBV : 4;                    // blocks per batch (2 or 4)
+    constexpr uint32_t NBT = NBV / BB;                            // batches
+    static_assert(DV >= 64 && NBV % BB == 0, "value part");
     const uint32_t G = a.G, E = a.E, nh = a.n_head;
     const uint32_t nbk = E / 32u;                                 // value blocks of a cell
     uint32_t * s_t64 = (uint32_t *)lds;                           // EXPK table
-    float * s_c = (float *)(lds + 256);                           // [seg][4 heads][D]
-    float * s_l = s_c + kPvMaxSeg * 4u * D;                       // [seg][4 heads]
-    uint8_t * s_dg = (uint8_t *)(s_l + kPvMaxSeg * 4u);          // per wave: [4 blocks][4 heads][4 digits][4 groups][16]
+    float * s_c = (float *)(lds + 256);                           // [seg][4 heads][DV]
+    float * s_l = s_c + kPvMaxSeg * 4u * DV;                      // [seg][4 heads]
+    uint8_t * s_dg = (uint8_t *)(s_l + kPvMaxSeg * 4u);          // per wave: [BB blocks][4 heads][4 digits][4 groups][16]
     const uint32_t t64v = a.ex.t64[threadIdx.x & 63u];            // first: the table write waits for it only
-    const uint32_t item = blockIdx.x >> 2, c = blockIdx.x & 3u, g = blockIdx.y, hg = blockIdx.z;
+    const uint32_t item = blockIdx.x >> 2, c = blockIdx.x & 3u, g = blockIdx.y;
+    const uint32_t hg = blockIdx.z / VS, vh = blockIdx.z % VS;
     const FaItem it = fa_item<INL>(a, p, item);
     const uint32_t lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nw = blockDim.x >> 6;
@@ -321,90 +316,114 @@ __global__ __launch_bounds__(64 * kPvWaves) void k_fa_pv(FaArgs a, FaPlan p) {
     const float * S = a.S + (size_t)it.s_off * nh + (size_t)h * n16;
     const uint16_t * vmeta = (const uint16_t *)a.vc.base;
     const uint8_t * vq = a.vc.base + a.vc.quant_off;
-    uint8_t * dg = s_dg + (size_t)wave * 4096u;
+    uint8_t * dg = s_dg + (size_t)wave * (BB * 1024u);
+    const uint32_t vb0 = vh * NBV;                                // first value block of the part (in the head)
+    const uint32_t mkey = maxt_key_f(a.Mpart[(size_t)(it.tile0 + min(lane & 15u, it.ntiles - 1u)) * nh + h]);
+
+    // the loads of one segment: scores, value scales of batch 0 and the value quants of batch 0
+    struct SegLoads {
+        float4 sv;
+        uint32_t mv[4][BB / 2];
+        int4 bq[2 * BB];
+    };
+    auto seg_loads = [&](uint32_t seg, uint32_t vb, SegLoads & L, bool scores) {
+        const uint32_t gi = 4u * seg + kk;
+        const uint32_t u = u_first + 4u * min(gi, nu - 1u);        // clamped: loads stay in the item
+        if (scores) L.sv = *(const float4 *)(S + 16u * (u - it.u0) + 4u * quad);
+        const uint16_t * vm = vmeta + ((size_t)u * 16u + 4u * quad) * nbk + (size_t)g * (D / 32u) + vb;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (BB == 4) {
+                const uint2 m2 = *(const uint2 *)(vm + (size_t)i * nbk);
+                L.mv[i][0] = m2.x; L.mv[i][1] = m2.y;
+            } else {
+                L.mv[i][0] = *(const uint32_t *)(vm + (size_t)i * nbk);
+            }
+        }
+        const uint32_t uB = u_first + 4u * min(4u * seg + (lane >> 4), nu - 1u);
+        const uint8_t * vqB = vq + ((size_t)uB * E + (size_t)g * D + 32u * vb + (lane & 15u)) * 16u;
+#pragma unroll
+        for (uint32_t t8 = 0; t8 < 2 * BB; ++t8) L.bq[t8] = *(const int4 *)(vqB + 256u * t8);
+    };
+
+    SegLoads L;
+    if (wave < nseg) seg_loads(wave, vb0, L, true);
+    __builtin_amdgcn_sched_barrier(0);
     if (threadIdx.x < 64u) s_t64[threadIdx.x] = t64v;
     lds_barrier();
 
     // chunk maximum of head h: MAXOUT of the floor and the tile maxima (row lanes < ntiles read one each)
-    const uint32_t mkey = maxt_key_f(a.Mpart[(size_t)(it.tile0 + min(lane & 15u, it.ntiles - 1u)) * nh + h]);
     const float m = maxt_unkey(row16_umax(max(mkey, maxt_key_f(bf(kMFloor)))));
 
     for (uint32_t seg = wave; seg < nseg; seg += nw) {
+        if (seg != wave) seg_loads(seg, vb0, L, true);
         // ---- phase A: lane = (head row, 4 cells) ----------------------------------------------
-        const uint32_t gi = 4u * seg + kk;                         // the channel's group index
-        const bool cv = gi < nu;
-        const uint32_t u = u_first + 4u * min(gi, nu - 1u);        // clamped: loads stay in the item
-        const uint32_t j0 = 16u * (u - it.u0) + 4u * quad;         // first cell of the lane in the chunk
-        const float4 sv = *(const float4 *)(S + j0);
-        const float ss[4] = { sv.x, sv.y, sv.z, sv.w };
+        const bool cv = 4u * seg + kk < nu;
+        const float ss[4] = { L.sv.x, L.sv.y, L.sv.z, L.sv.w };
         float pz[4];
-        bool pnf_any = false;
-        int32_t ep = -1000;
+        uint32_t pnf = 0u, pe = 0u;                                // non-finite flag; largest exponent field
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float pe = (cv && head_ok) ? expk(smul(ssub(ss[i], m), a.scale), a.ex, s_t64) : 0.0f;
-            pz[i] = daz(pe);
-            const bool nf = f_nonfinite(pz[i]);
-            pnf_any |= nf;
-            if (!nf && (fb(pz[i]) & 0x7FFFFFFFu)) ep = max(ep, f_exp(pz[i]));
+            // EXPK results are zero, normal, Inf or NaN (never subnormal)
+            pz[i] = (cv && head_ok) ? expk(smul(ssub(ss[i], m), a.scale), a.ex, s_t64) : 0.0f;
+            const uint32_t f = f_field(pz[i]);
+            pnf |= f == 255u ? 1u : 0u;
+            pe = max(pe, f == 255u ? 0u : f);
         }
         // LSUM of the segment (AT 6.5): block float of its p values
-        const bool badl = row16_umax(pnf_any ? 1u : 0u) != 0u;
-        ep = row16_imax(ep);
-        int32_t lsum = 0;
+        if (vh == 0u) {
+            const bool badl = row16_or(pnf) != 0u;
+            pe = row16_umax(pe);
+            int32_t lsum = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) lsum += f_nonfinite(pz[i]) ? 0 : bf_int(pz[i], ep);
-        lsum = row16_isum(lsum);
-        if ((lane & 15u) == 0u)
-            s_l[seg * 4u + hr] = badl ? bf(kNaN) : (ep == -1000 ? 0.0f : bf_f((int64_t)lsum, ep - 23));
+            for (int i = 0; i < 4; ++i) lsum += f_field(pz[i]) == 255u ? 0 : bf_int_n(pz[i], (int32_t)pe - 127);
+            lsum = row16_isum(lsum);
+            if ((lane & 15u) == 0u)
+                s_l[seg * 4u + hr] = badl ? bf(kNaN) : (pe == 0u ? 0.0f : bf_scale((float)lsum, (int32_t)pe - 150));
+        }
 
-        const uint16_t * vm = vmeta + ((size_t)u * 16u + 4u * quad) * nbk + (size_t)g * NBD;
-#pragma unroll 1
-        for (uint32_t vb = 0; vb < NBD; vb += BB) {                // BB value blocks (32 BB values) at a time
-            // weights of the 4 cells for the BB blocks
+#pragma unroll
+        for (uint32_t bt = 0; bt < NBT; ++bt) {                    // BB value blocks (32 BB values) at a time
+            const uint32_t vb = vb0 + bt * BB;
+            if (bt > 0u) seg_loads(seg, vb, L, false);
+            // weights of the 4 cells for the BB blocks: w = p dV, a subnormal product flushed to zero
             float w[4][BB];
-            int32_t ex[BB / 2];
-            bool nfb[BB];
+            uint32_t ex[BB / 2], nfm = 0u;
 #pragma unroll
-            for (uint32_t e = 0; e < BB; ++e) nfb[e] = false;
-#pragma unroll
-            for (uint32_t sa = 0; sa < BB / 2; ++sa) ex[sa] = -1000;
+            for (uint32_t sa = 0; sa < BB / 2; ++sa) ex[sa] = 0u;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                uint32_t dv[BB];
-                if constexpr (BB == 4) {
-                    const uint2 mv = *(const uint2 *)(vm + (size_t)i * nbk + vb);
-                    dv[0] = mv.x & 0xFFFFu; dv[1] = mv.x >> 16; dv[2] = mv.y & 0xFFFFu; dv[3] = mv.y >> 16;
-                } else {
-                    const uint32_t mv = *(const uint32_t *)(vm + (size_t)i * nbk + vb);
-                    dv[0] = mv & 0xFFFFu; dv[1] = mv >> 16;
-                }
                 const bool live = (fb(pz[i]) & 0x7FFFFFFFu) != 0u;
 #pragma unroll
                 for (uint32_t e = 0; e < BB; ++e) {
-                    const float we = live ? smul(pz[i], h2f_exact(dv[e])) : 0.0f;
-                    w[i][e] = we;
-                    const bool nf = f_nonfinite(we);
-                    nfb[e] |= nf;
-                    if (!nf && (fb(we) & 0x7FFFFFFFu)) ex[e >> 1] = max(ex[e >> 1], f_exp(we));
+                    const uint32_t dv = (L.mv[i][e >> 1] >> (16u * (e & 1u))) & 0xFFFFu;
+                    const float we = live ? pz[i] * h2f_fast(dv) : 0.0f;
+                    const uint32_t f = f_field(we);
+                    nfm |= (f == 255u ? 1u : 0u) << e;
+                    w[i][e] = f == 0u ? 0.0f : we;
+                    ex[e >> 1] = max(ex[e >> 1], f == 255u ? 0u : f);
                 }
             }
             int32_t es[BB / 2];
-            bool any[BB / 2], bad[BB];
+            bool any[BB / 2];
 #pragma unroll
-            for (uint32_t sa = 0; sa < BB / 2; ++sa) { es[sa] = row16_imax(ex[sa]); any[sa] = es[sa] > -1000; }
-#pragma unroll
-            for (uint32_t e = 0; e < BB; ++e) bad[e] = row16_umax(nfb[e] ? 1u : 0u) != 0u;
+            for (uint32_t sa = 0; sa < BB / 2; ++sa) {
+                const uint32_t ef = row16_umax(ex[sa]);
+                any[sa] = ef != 0u;
+                es[sa] = (int32_t)ef - 127;
+            }
+            const uint32_t badm = row16_or(nfm);
             // digits: for block e and digit k, the 4 cells' digit bytes in one word
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
             for (uint32_t e = 0; e < BB; ++e) {
+                const bool use = any[e >> 1] && ((badm >> e) & 1u) == 0u;
                 uint32_t P[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int32_t W = (any[e >> 1] && !bad[e]) ? bf_int(w[i][e], es[e >> 1]) : 0;
+                    const int32_t W = use ? bf_int_n(w[i][e], es[e >> 1]) : 0;
                     P[i] = ((uint32_t)W + 0x80808080u) ^ 0x80808080u;     // byte k = digit k of W
                 }
                 // transpose the 4 x 4 bytes: word k = digit k of cells 0..3
@@ -421,41 +440,35 @@ __global__ __launch_bounds__(64 * kPvWaves) void k_fa_pv(FaArgs a, FaPlan p) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            // ---- phase B: 8 tiles of 16 values; lane = (head row l / 16 of the result, value l % 16)
-            const uint32_t kB = lane >> 4;                          // the operand's 16 cells: group kB
-            const uint32_t uB = u_first + 4u * min(4u * seg + kB, nu - 1u);
-            const uint8_t * vqB = vq + ((size_t)uB * E + (size_t)g * D + 32u * vb + (lane & 15u)) * 16u;
-            int4 Bv[2 * BB];
-#pragma unroll
-            for (uint32_t t8 = 0; t8 < 2 * BB; ++t8) Bv[t8] = *(const int4 *)(vqB + 256u * t8);
+            // ---- phase B: 2 BB tiles of 16 values; lane = (head row l / 16 of the result, value l % 16)
 #pragma unroll
             for (uint32_t e = 0; e < BB; ++e) {
                 // A operand: row l % 16 = (head, digit), K = the 16 cells of group l / 16
                 const v4i_fa Aop = *(const v4i_fa *)(dg + ((e * 16u + (lane & 15u)) * 4u + (lane >> 4)) * 16u);
+                const bool bad = ((badm >> e) & 1u) != 0u;
 #pragma unroll
                 for (int half = 0; half < 2; ++half) {
-                    const int4 bq = Bv[2 * e + half];
+                    const int4 bq = L.bq[2 * e + half];
                     const v4i_fa Bop = { bq.x, bq.y, bq.z, bq.w };
                     v4i_fa acc = { 0, 0, 0, 0 };
                     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Aop, Bop, acc, 0, 0, 0);
-                    const int64_t A = (int64_t)acc[0] + ((int64_t)acc[1] << 8) + ((int64_t)acc[2] << 16) + ((int64_t)acc[3] << 24);
-                    const float cval = bad[e] ? bf(kNaN) : (any[e >> 1] ? bf_f(A, es[e >> 1] - 23) : 0.0f);
-                    s_c[(seg * 4u + hr) * D + 32u * (vb + e) + 16u * (uint32_t)half + (lane & 15u)] = cval;
+                    const float cval = bad ? bf(kNaN) : (any[e >> 1] ? bf_scale(digits_rne24(acc), es[e >> 1] - 23) : 0.0f);
+                    s_c[(seg * 4u + hr) * DV + 32u * (bt * BB + e) + 16u * (uint32_t)half + (lane & 15u)] = cval;
                 }
             }
         }
     }
     __syncthreads();
-    // segment chains in order (AT 6.4 O, 6.5 l): thread = (head row, value)
-    for (uint32_t idx = threadIdx.x; idx < 4u * D; idx += blockDim.x) {
-        const uint32_t r4 = idx / D, v = idx % D, hi2 = 4u * hg + r4;
+    // segment chains in order (AT 6.4 O, 6.5 l): thread = (head row, value of the part)
+    for (uint32_t idx = threadIdx.x; idx < 4u * DV; idx += blockDim.x) {
+        const uint32_t r4 = idx / DV, v = idx % DV, hi2 = 4u * hg + r4;
         if (hi2 >= G) continue;
         const uint32_t h2 = g * G + hi2;
         float O = 0.0f;
-        for (uint32_t seg = 0; seg < nseg; ++seg) O = sadd(O, s_c[(seg * 4u + r4) * D + v]);
+        for (uint32_t seg = 0; seg < nseg; ++seg) O = sadd(O, s_c[(seg * 4u + r4) * DV + v]);
         const size_t slot = ((size_t)item * 4u + c) * nh + h2;
-        a.OP[slot * D + v] = O;
-        if (v == 0u) {
+        a.OP[slot * D + vh * DV + v] = O;
+        if (vh == 0u && v == 0u) {
             float l = 0.0f;
             for (uint32_t seg = 0; seg < nseg; ++seg) l = sadd(l, s_l[seg * 4u + r4]);
             a.LP[slot] = l;
@@ -465,9 +478,11 @@ __global__ __launch_bounds__(64 * kPvWaves) void k_fa_pv(FaArgs a, FaPlan p) {
 
 // ---------------------------------------------------------------------------------------------
 // merge: block (token, KV head g x group of 4 heads, slice sl), lane = (head of the group, value).
-// Each lane loads the channel partials, row sums and maxima of up to kMergeItems chunks at once,
-// then runs CTREE over the 4 channels, the online merge in chunk order and finally ANORM (AT 5.6,
-// 5.7). No LDS and no barriers.
+// Each lane loads the channel partials, row sums and maxima of up to kMergeItems chunks at once (the
+// first round's before the EXPK table is published), then runs CTREE over the 4 channels, the online
+// merge in chunk order and finally ANORM (AT 5.6, 5.7). The running maxima of a round are
+// wave-uniform, so its 2 kMergeItems merge factors are evaluated by as many lanes at once and read
+// back with readlane.
 // ---------------------------------------------------------------------------------------------
 constexpr uint32_t kMergeItems = 4;                              // chunks loaded per round
 constexpr uint32_t kMergeHeads = 4;                              // heads per block
@@ -480,65 +495,83 @@ __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
     const uint32_t hn = min(kMergeHeads, g * G + G - h0), sl = blockIdx.z;
     const uint32_t i = threadIdx.x >> 6, L = threadIdx.x & 63u;
     __shared__ uint32_t s_t64[64];
-    if (threadIdx.x < 64u) s_t64[threadIdx.x] = a.ex.t64[threadIdx.x];
-    __syncthreads();
-    if (i >= hn) return;                                          // whole waves
+    const uint32_t t64v = a.ex.t64[L];                            // first: the table write waits for it only
     const uint32_t first = INL ? p.tok_first[t] : a.tok_first[t];
-    const uint32_t cnt = INL ? p.tok_count[t] : a.tok_count[t];
-    const uint32_t h = h0 + i;
-    float O = 0.0f, l = 0.0f, mr = 0.0f;
-    for (uint32_t k0 = 0; k0 < cnt; k0 += kMergeItems) {
-        const uint32_t kn = min(kMergeItems, cnt - k0);
+    const uint32_t cnt = INL ? p.tok_count[t] : a.tok_count[t];  // >= 1 (a row without cells has one empty chunk)
+    const uint32_t h = h0 + min(i, hn - 1u);                      // waves past the group load, then leave
+
+    struct Round {
         float op[kMergeItems][4], lp[kMergeItems][4];
+        uint32_t key;                                             // MAXT key of one tile maximum
+    };
+    auto load_round = [&](uint32_t k0, Round & R) {
+        const uint32_t kn = min(kMergeItems, cnt - k0);
 #pragma unroll
         for (uint32_t k = 0; k < kMergeItems; ++k) {                // clamped: every load is issued up front
             const size_t kk = first + k0 + min(k, kn - 1u);
 #pragma unroll
             for (uint32_t c = 0; c < 4u; ++c) {
                 const size_t slot = (kk * 4u + c) * nh + h;
-                op[k][c] = a.OP[slot * D + 64u * sl + L];
-                lp[k][c] = a.LP[slot];
+                R.op[k][c] = a.OP[slot * D + 64u * sl + L];
+                R.lp[k][c] = a.LP[slot];
             }
         }
-        // chunk maxima: lane 8 k + j (k < 4) reads tile j (clamped) of chunk k; MAXOUT over the
-        // 8-lane group (an item has at most 8 tiles: NCG <= 128 groups of 16 cells)
-        uint32_t key;
-        {
-            uint32_t tile = 0;
+        // lane 8 k + j (k < kMergeItems) reads tile j (clamped) of chunk k: an item has at most 8
+        // tiles (NCG <= 128 groups of 16 cells)
+        uint32_t tile = 0;
 #pragma unroll
-            for (uint32_t k = 0; k < kMergeItems; ++k) {            // uniform item reads, per-lane select
-                const FaItem itk = fa_item<INL>(a, p, first + k0 + min(k, kn - 1u));
-                if ((L >> 3) == k) tile = itk.tile0 + min(L & 7u, itk.ntiles - 1u);
-            }
-            key = maxt_key_f(a.Mpart[(size_t)tile * nh + h]);
-            key = max(key, maxt_key_f(bf(kMFloor)));
-            key = umax_u(key, (uint32_t)dpp_i<kDppXor1>((int)key));
-            key = umax_u(key, (uint32_t)dpp_i<kDppXor2>((int)key));
-            key = umax_u(key, (uint32_t)dpp_i<kDppRowHalfMirror>((int)key));
+        for (uint32_t k = 0; k < kMergeItems; ++k) {                // uniform item reads, per-lane select
+            const FaItem itk = fa_item<INL>(a, p, first + k0 + min(k, kn - 1u));
+            if ((L >> 3) == k) tile = itk.tile0 + min(L & 7u, itk.ntiles - 1u);
         }
-        float mk[kMergeItems];
-#pragma unroll
-        for (uint32_t k = 0; k < kMergeItems; ++k) mk[k] = maxt_unkey((uint32_t)__builtin_amdgcn_readlane((int)key, 8 * (int)k));
-        // the running maxima and the merge factors of every chunk are independent of O and l:
-        // computed first, so the EXP evaluations of the chunks can overlap
-        float mrun[kMergeItems], fa[kMergeItems], fbv[kMergeItems];
+        R.key = maxt_key_f(a.Mpart[(size_t)tile * nh + h]);
+    };
+
+    Round R;
+    load_round(0u, R);
+    __builtin_amdgcn_sched_barrier(0);
+    if (threadIdx.x < 64u) s_t64[threadIdx.x] = t64v;
+    lds_barrier();
+    if (i >= hn) return;                                          // whole waves
+
+    float O = 0.0f, l = 0.0f, mr = 0.0f;
+    for (uint32_t k0 = 0; k0 < cnt; k0 += kMergeItems) {
+        if (k0 != 0u) load_round(k0, R);
+        const uint32_t kn = min(kMergeItems, cnt - k0);
+        // chunk maxima: MAXOUT of the floor and the chunk's tile maxima over each 8-lane group
+        uint32_t key = max(R.key, maxt_key_f(bf(kMFloor)));
+        key = umax_u(key, (uint32_t)dpp_i<kDppXor1>((int)key));
+        key = umax_u(key, (uint32_t)dpp_i<kDppXor2>((int)key));
+        key = umax_u(key, (uint32_t)dpp_i<kDppRowHalfMirror>((int)key));
+        float mk[kMergeItems], mrun[kMergeItems];
 #pragma unroll
         for (uint32_t k = 0; k < kMergeItems; ++k) {
+            mk[k] = maxt_unkey((uint32_t)__builtin_amdgcn_readlane((int)key, 8 * (int)k));
             const float prev = k == 0u ? mr : mrun[k - 1u];
-            const bool first_chunk = k0 + k == 0u;
-            mrun[k] = first_chunk ? mk[k] : maxt(prev, mk[k]);
-            fa[k] = first_chunk ? 1.0f : expk(smul(ssub(prev, mrun[k]), a.scale), a.ex, s_t64);
-            fbv[k] = first_chunk ? 1.0f : expk(smul(ssub(mk[k], mrun[k]), a.scale), a.ex, s_t64);
+            mrun[k] = k0 + k == 0u ? mk[k] : maxt(prev, mk[k]);
         }
+        // lane 2 k + b: factor of chunk k, EXP((prev - mrun_k) scale) for b = 0 (the running sums),
+        // EXP((m_k - mrun_k) scale) for b = 1 (the chunk's); the first chunk of a row uses none
+        const uint32_t jk = (L >> 1) & (kMergeItems - 1u);
+        float from = 0.0f, to = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeItems; ++k)
+            if (jk == k) {
+                from = (L & 1u) ? mk[k] : (k == 0u ? mr : mrun[k - 1u]);
+                to = mrun[k];
+            }
+        const float fx = expk(smul(ssub(from, to), a.scale), a.ex, s_t64);
 #pragma unroll
         for (uint32_t k = 0; k < kMergeItems; ++k) {
             if (k >= kn) break;
-            const float ok = ctree4(op[k][0], op[k][1], op[k][2], op[k][3]);
-            const float lk = ctree4(lp[k][0], lp[k][1], lp[k][2], lp[k][3]);
+            const float ok = ctree4(R.op[k][0], R.op[k][1], R.op[k][2], R.op[k][3]);
+            const float lk = ctree4(R.lp[k][0], R.lp[k][1], R.lp[k][2], R.lp[k][3]);
             if (k0 + k == 0u) { O = ok; l = lk; }
             else {
-                l = sadd(smul(l, fa[k]), smul(lk, fbv[k]));
-                O = sadd(smul(O, fa[k]), smul(ok, fbv[k]));
+                const float fa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)k));
+                const float fbv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)k + 1));
+                l = sadd(smul(l, fa), smul(lk, fbv));
+                O = sadd(smul(O, fa), smul(ok, fbv));
             }
             mr = mrun[k];
         }
@@ -549,7 +582,7 @@ __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
 }  // namespace tsr
 
 template <bool INL>
-static int launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, hipStream_t s) {
+static int launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, uint32_t n_cu, hipStream_t s) {
     const size_t lds_qk = (size_t)a.G * a.D + 4u * (size_t)a.G * (a.D / 32u) + 4u * 4u * a.G;
     const dim3 gqk(p.n_items * p.maxtiles, a.n_head_kv);
     switch (a.D) {
@@ -560,7 +593,8 @@ static int launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, h
         default: return -2;
     }
     if (hipGetLastError() != hipSuccess) return -4;
-    // P.V: waves = the most segments of any item (<= 8), LDS = table, segment results, digits
+    // P.V: waves = the most segments of any item (<= 8), LDS = table, segment results, digits; the
+    // values of a head are split over VS blocks while the grid holds fewer than two blocks per CU
     uint32_t maxn = 0;
     if (INL) {
         for (uint32_t i = 0; i < p.n_items; ++i) maxn = std::max(maxn, p.items[i].n);
@@ -568,21 +602,33 @@ static int launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, h
         maxn = a.max_groups;
     }
     const uint32_t nwv = std::max(1u, std::min(tsr::kPvWaves, ((maxn + 3u) / 4u + 3u) / 4u));
-    const size_t lds_pv = 256u + 4u * (size_t)tsr::kPvMaxSeg * 4u * a.D + 4u * tsr::kPvMaxSeg * 4u + 4096u * nwv;
-    const dim3 gpv(4u * p.n_items, a.n_head_kv, (a.G + 3u) / 4u);
-    switch (a.D) {
-        case 64: hipLaunchKernelGGL((tsr::k_fa_pv<64, INL>), gpv, dim3(64u * nwv), lds_pv, s, a, p); break;
-        case 128: hipLaunchKernelGGL((tsr::k_fa_pv<128, INL>), gpv, dim3(64u * nwv), lds_pv, s, a, p); break;
-        case 256: hipLaunchKernelGGL((tsr::k_fa_pv<256, INL>), gpv, dim3(64u * nwv), lds_pv, s, a, p); break;
-        case 512: hipLaunchKernelGGL((tsr::k_fa_pv<512, INL>), gpv, dim3(64u * nwv), lds_pv, s, a, p); break;
+    const uint64_t blocks = 4ull * p.n_items * a.n_head_kv * ((a.G + 3u) / 4u);
+    uint32_t vs = 1;
+    while (vs < 4u && a.D / (2u * vs) >= 64u && blocks * vs < 2ull * n_cu) vs *= 2u;
+    const uint32_t dv = a.D / vs, bb = std::min(4u, dv / 32u);
+    const size_t lds_pv = 256u + 4u * (size_t)tsr::kPvMaxSeg * 4u * dv + 4u * tsr::kPvMaxSeg * 4u + 1024u * bb * nwv;
+    const dim3 gpv(4u * p.n_items, a.n_head_kv, (a.G + 3u) / 4u * vs);
+    const dim3 bpv(64u * nwv);
+#define TSR_PV(DD, VV) hipLaunchKernelGGL((tsr::k_fa_pv<DD, INL, VV>), gpv, bpv, lds_pv, s, a, p)
+    switch (a.D * 8u + vs) {
+        case 64 * 8 + 1: TSR_PV(64, 1); break;
+        case 128 * 8 + 1: TSR_PV(128, 1); break;
+        case 128 * 8 + 2: TSR_PV(128, 2); break;
+        case 256 * 8 + 1: TSR_PV(256, 1); break;
+        case 256 * 8 + 2: TSR_PV(256, 2); break;
+        case 256 * 8 + 4: TSR_PV(256, 4); break;
+        case 512 * 8 + 1: TSR_PV(512, 1); break;
+        case 512 * 8 + 2: TSR_PV(512, 2); break;
+        case 512 * 8 + 4: TSR_PV(512, 4); break;
         default: return -2;
     }
+#undef TSR_PV
     if (hipGetLastError() != hipSuccess) return -4;
     const uint32_t ngrp = (a.G + tsr::kMergeHeads - 1u) / tsr::kMergeHeads;
     hipLaunchKernelGGL(tsr::k_fa_merge<INL>, dim3(T, a.n_head_kv * ngrp, a.D / 64u), dim3(256), 0, s, a, p);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-int tsr_launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, hipStream_t s) {
-    return a.items ? launch_fa<false>(a, p, T, s) : launch_fa<true>(a, p, T, s);
+int tsr_launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, uint32_t n_cu, hipStream_t s) {
+    return a.items ? launch_fa<false>(a, p, T, n_cu, s) : launch_fa<true>(a, p, T, n_cu, s);
 }

@@ -110,4 +110,4 @@ int tsr_launch_kv_bytes(const tsr::KvArgs & a, uint32_t which, uint64_t off, uin
                         hipStream_t s);
 int tsr_launch_kv_set_rows(const tsr::KvArgs & a, uint32_t which, const float * src, uint32_t n_rows,
                            uint64_t src_stride, const int64_t * idx, int32_t * bad, hipStream_t s);
-int tsr_launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, hipStream_t s);
+int tsr_launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, uint32_t n_cu, hipStream_t s);

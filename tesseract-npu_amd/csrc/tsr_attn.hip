@@ -330,5 +330,5 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     a.ex = ctx->expk;
     ctx->ctr.flash_attn_calls++;
     ctx->ctr.flash_attn_kv_bytes += cells * (uint64_t)E / 32u * 34u * 2u;
-    return tsr_launch_fa(a, p, T, s) ? TSR_HIP_E_HIP : TSR_HIP_OK;
+    return tsr_launch_fa(a, p, T, (uint32_t)ctx->n_cu, s) ? TSR_HIP_E_HIP : TSR_HIP_OK;
 }

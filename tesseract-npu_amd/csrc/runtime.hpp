@@ -81,8 +81,8 @@ struct tsr_hip_weight {
     size_t bytes = 0;
 };
 
-// A q8_0 KV cache plane in the device layout: cell-major rows; per row the E/32 fp16 scales
-// ("meta", padded to 16 bytes) and the E int8 quants, in separate regions.
+// A q8_0 KV cache plane in the device layout of k_kv.hip: cells in groups of 16; the fp16 block
+// scales ("meta") and the int8 quants in separate regions.
 struct tsr_hip_kv {
     uint32_t E = 0, kv_size = 0;
     uint8_t * dev = nullptr;

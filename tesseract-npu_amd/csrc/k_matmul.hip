@@ -57,14 +57,15 @@ __global__ __launch_bounds__(256) void k_qact_mm(const float * x, uint64_t x_str
 
 __global__ __launch_bounds__(1024) void k_mm_q80(MmArgs a) {
     __shared__ float s_p[16][1024];                                // partial j of output (lane, r)
-    const WGeom g = wgeom(a.N, a.K >> 5);
+    const WGeom g = wgeom(a.N, a.K >> 5, a.rb, false);
     const uint32_t lane = __lane_id(), j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n0 = blockIdx.x * 32u, t0 = blockIdx.y * 32u;
     const uint32_t h = lane >> 5, c = lane & 31u;
     // operand rows of this lane (clamped: rows / tokens beyond the matrix are not stored)
     const uint32_t n = min(n0 + c, a.N - 1u), t = min(t0 + c, a.T - 1u);
-    const uint8_t * wq = a.wq + q80_quant_off(g, n >> 4, h, 0u, n & 15u);       // + 256 slot
-    const uint8_t * wm = a.wm + q80_meta_off(g, n >> 4, 0u, n & 15u);           // + 32 slot
+    const uint32_t B = n / g.rb, R = wl_rows(g, B), rr = n - B * g.rb;  // row block of the row
+    const uint8_t * wq = a.w + wl_quant_off(g, B, R, h, 0u, rr);         // + 16 R slot
+    const uint8_t * wm = a.w + wl_meta_off(g, B, R, 0u, rr);             // + 2 R slot
     const uint8_t * xq = a.qa + (size_t)t * 32u + 16u * h;                     // + 32 T b
     const float * xd = (const float *)(a.qa + a.d_off) + t;                      // + T b
     const uint32_t cnt = wl_count(g, j), sl0 = wl_slot(g, j, 0u);
@@ -78,9 +79,9 @@ __global__ __launch_bounds__(1024) void k_mm_q80(MmArgs a) {
 #pragma unroll
         for (uint32_t i = 0; i < kMmPre; ++i) {                    // clamped: every load is issued
             const uint32_t k = min(k0 + i, cnt - 1u), sl = sl0 + k, b = j + 16u * k;
-            wa[i] = *(const v4i *)(wq + 256u * sl);
+            wa[i] = *(const v4i *)(wq + (size_t)16u * R * sl);
             xb[i] = *(const v4i *)(xq + (size_t)32u * a.T * b);
-            dw[i] = h2f_fast(*(const uint16_t *)(wm + 32u * sl));
+            dw[i] = h2f_fast(*(const uint16_t *)(wm + (size_t)2u * R * sl));
             dx[i] = xd[(size_t)a.T * b];
         }
 #pragma unroll

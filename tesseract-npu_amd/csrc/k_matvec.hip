@@ -5,10 +5,12 @@
 // (the 16-partial tree). Q8_0 term = (d Dx) f32(isum); Q4_K term = (d Dx) f32(isum) -
 // (dmin Dx) f32(msum) with isum = sum_j sc_j S_j and msum = sum_j m_j (bs[2j] + bs[2j+1]).
 //
-// Work split. A workgroup of 16 waves owns a contiguous range of rows; wave w computes the terms
-// of the blocks s = w + 16 k (the blocks of partial p[w]) of every row in the range. The weight
-// layout (wlayout.hpp) stores exactly these blocks of 16 consecutive rows contiguously, so a wave
-// load of (4 slots x 16 rows) lanes reads 256-byte runs. A lane computes a whole term: the integer
+// Work split. A workgroup of 16 waves owns one row block of the weight layout (wlayout.hpp: rb
+// consecutive rows); wave w computes the terms of the blocks s = w + 16 k (the blocks of partial
+// p[w]) of every row in the block. The layout stores exactly these units (slot, row) of a wave
+// contiguously, so a wave load reads one run of up to 1 KiB and a workgroup reads one contiguous
+// region (measured: the same bytes in runs of 256 bytes 32 KiB apart take ~25 % longer to stream
+// than in contiguous runs of 1 KiB). A lane computes a whole term: the integer
 // sums stay in its registers and need no cross-lane reduction. Each wave quantizes the blocks of x
 // it uses (QACT into its own LDS area), so no workgroup barrier separates the weight stream from
 // the compute. The terms go to LDS; after the only barriers, the partials are summed in the order
@@ -24,6 +26,7 @@
 // partial sums and the tree of the workgroup do too.
 #include "kernels.hpp"
 #include "qact.hpp"
+#include "tsr_hip.h"
 #include "wlayout.hpp"
 
 #include <algorithm>
@@ -85,25 +88,20 @@ __device__ __forceinline__ void mv_tree_store(const MvArgs & a, const float * s_
     }
 }
 
-// The unit of lane `lane` in pass p: unit u = 4 p + lane / 16 of the wave's ngrp * cnt units
-// (group-major), row = 16 G + lane % 16. Rows outside [row_lo, row_hi) load a row of the same group
-// that is inside (the cache lines of a valid lane); units beyond the last, and every unit of a wave
-// without blocks (cnt == 0), load a valid address and are not used.
+// The unit of lane `lane` in pass p: unit u = 64 p + lane of the wave's R cnt units (slot-major:
+// slot k = u / R, row u % R of the block). Units beyond the last, and every unit of a wave without
+// blocks (cnt == 0), load the last unit's address (a valid one) and are not used.
 struct MvUnit {
-    uint32_t G, k, row, rowc;
+    uint32_t k, r;
     bool valid;
 };
-__device__ __forceinline__ MvUnit mv_unit(uint32_t p, int lane, uint32_t cnt, uint32_t nunit, uint32_t G0,
-                                          uint32_t row_lo, uint32_t row_hi) {
-    const uint32_t u = 4u * p + ((uint32_t)lane >> 4);
-    const uint32_t uc = min(u, (nunit ? nunit : 1u) - 1u), cc = cnt ? cnt : 1u;
+__device__ __forceinline__ MvUnit mv_unit(uint32_t p, int lane, uint32_t R, uint32_t nunit) {
+    const uint32_t u = 64u * p + (uint32_t)lane;
+    const uint32_t uc = min(u, (nunit ? nunit : 1u) - 1u);
     MvUnit m;
-    const uint32_t gi = uc / cc;
-    m.k = uc - gi * cc;
-    m.G = G0 + gi;
-    m.row = 16u * m.G + ((uint32_t)lane & 15u);
-    m.valid = u < nunit && m.row >= row_lo && m.row < row_hi;
-    m.rowc = min(max(m.row, row_lo), row_hi - 1u);
+    m.k = uc / R;
+    m.r = uc - m.k * R;
+    m.valid = u < nunit;
     return m;
 }
 
@@ -116,15 +114,14 @@ __device__ __forceinline__ MvUnit mv_unit(uint32_t p, int lane, uint32_t cnt, ui
 template <int P, bool ISUMS>      // P: passes whose loads are in registers at once
 __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const WGeom g = wgeom(a.N, a.K >> 8);
+    const WGeom g = wgeom(a.N, a.K >> 8, a.rb, true);
     const uint32_t nsb = g.nb, kx = g.q + (g.rem ? 1u : 0u);
     const int lane = (int)__lane_id();
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), cnt = wl_count(g, w);
     const uint32_t t = blockIdx.y;
     const float * x = a.x + (size_t)t * a.x_stride;
-    const uint32_t row_lo = blockIdx.x * a.rb, row_hi = min(a.N, row_lo + a.rb), nrow = row_hi - row_lo;
-    const uint32_t G0 = row_lo >> 4, ngrp = ((row_hi - 1u) >> 4) - G0 + 1u;
-    const uint32_t nunit = ngrp * cnt, npass = (nunit + 3u) >> 2;
+    const uint32_t B = blockIdx.x, row_lo = B * g.rb, nrow = wl_rows(g, B);
+    const uint32_t nunit = nrow * cnt, npass = (nunit + 63u) >> 6;
     int8_t * s_xq = (int8_t *)lds;
     int * s_xb = (int *)(lds + kMvWaves * kx * kXq4Stride);
     float * s_xd = (float *)(s_xb + kMvWaves * kx * 8u);
@@ -148,11 +145,11 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     auto load = [&](uint32_t p0) {
 #pragma unroll
         for (int pp = 0; pp < P; ++pp) {
-            const MvUnit m = mv_unit(min(p0 + (uint32_t)pp, npass ? npass - 1u : 0u), lane, cnt, nunit, G0, row_lo, row_hi);
-            const uint32_t sl = min(wl_slot(g, w, m.k), nsb - 1u), r = m.rowc & 15u;
-            mv[pp] = *(const uint4 *)(a.wm + q4k_meta_off(g, m.G, sl, r));
+            const MvUnit m = mv_unit(min(p0 + (uint32_t)pp, npass ? npass - 1u : 0u), lane, nrow, nunit);
+            const uint32_t sl = min(wl_slot(g, w, m.k), nsb - 1u);
+            mv[pp] = *(const uint4 *)(a.w + wl_meta_off(g, B, nrow, sl, m.r));
 #pragma unroll
-            for (uint32_t j = 0; j < 8u; ++j) qv[pp][j] = *(const uint4 *)(a.wq + q4k_quant_off(g, m.G, j, sl, r));
+            for (uint32_t j = 0; j < 8u; ++j) qv[pp][j] = *(const uint4 *)(a.w + wl_quant_off(g, B, nrow, j, sl, m.r));
         }
     };
     // QACT A256 of the wave's blocks s = w + 16 k, four at a time. Round 0 is outside the loop: a
@@ -195,7 +192,7 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
 #pragma unroll
         for (int pp = 0; pp < P; ++pp) {
             if (p0 + (uint32_t)pp >= npass) break;
-            const MvUnit m = mv_unit(p0 + (uint32_t)pp, lane, cnt, nunit, G0, row_lo, row_hi);
+            const MvUnit m = mv_unit(p0 + (uint32_t)pp, lane, nrow, nunit);
             const uint32_t xo = w * kx + m.k;
             const int8_t * xb = s_xq + xo * kXq4Stride;
             int S[8];
@@ -239,10 +236,10 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
             else tt = ssub(smul(smul(d, dx), i2f(isum)), smul(smul(dm, dx), i2f(msum)));
             const uint32_t s = w + 16u * m.k;
             if (m.valid) {
-                s_t[(m.row - row_lo) * nsb + s] = tt;
+                s_t[m.r * nsb + s] = tt;
                 if (ISUMS && t == 0u) {
-                    a.isums[(size_t)m.row * 2u * nsb + 2u * s] = isum;
-                    a.isums[(size_t)m.row * 2u * nsb + 2u * s + 1u] = msum;
+                    a.isums[(size_t)(row_lo + m.r) * 2u * nsb + 2u * s] = isum;
+                    a.isums[(size_t)(row_lo + m.r) * 2u * nsb + 2u * s + 1u] = msum;
                 }
             }
         }
@@ -264,15 +261,14 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
 template <int P, bool ISUMS>
 __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const WGeom g = wgeom(a.N, a.K >> 5);
+    const WGeom g = wgeom(a.N, a.K >> 5, a.rb, false);
     const uint32_t nb = g.nb, kx = g.q + (g.rem ? 1u : 0u);
     const int lane = (int)__lane_id();
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), cnt = wl_count(g, w);
     const uint32_t t = blockIdx.y;
     const float * x = a.x + (size_t)t * a.x_stride;
-    const uint32_t row_lo = blockIdx.x * a.rb, row_hi = min(a.N, row_lo + a.rb), nrow = row_hi - row_lo;
-    const uint32_t G0 = row_lo >> 4, ngrp = ((row_hi - 1u) >> 4) - G0 + 1u;
-    const uint32_t nunit = ngrp * cnt, npass = (nunit + 3u) >> 2;
+    const uint32_t B = blockIdx.x, row_lo = B * g.rb, nrow = wl_rows(g, B);
+    const uint32_t nunit = nrow * cnt, npass = (nunit + 63u) >> 6;
     int8_t * s_xq = (int8_t *)lds;
     float * s_xd = (float *)(lds + kMvWaves * kx * 32u);
     float * s_t = s_xd + kMvWaves * kx;
@@ -294,11 +290,11 @@ __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
     auto load = [&](uint32_t p0) {
 #pragma unroll
         for (int pp = 0; pp < P; ++pp) {
-            const MvUnit m = mv_unit(min(p0 + (uint32_t)pp, npass ? npass - 1u : 0u), lane, cnt, nunit, G0, row_lo, row_hi);
-            const uint32_t sl = min(wl_slot(g, w, m.k), nb - 1u), r = m.rowc & 15u;
-            q0[pp] = *(const uint4 *)(a.wq + q80_quant_off(g, m.G, 0u, sl, r));
-            q1[pp] = *(const uint4 *)(a.wq + q80_quant_off(g, m.G, 1u, sl, r));
-            dv[pp] = *(const uint16_t *)(a.wm + q80_meta_off(g, m.G, sl, r));
+            const MvUnit m = mv_unit(min(p0 + (uint32_t)pp, npass ? npass - 1u : 0u), lane, nrow, nunit);
+            const uint32_t sl = min(wl_slot(g, w, m.k), nb - 1u);
+            q0[pp] = *(const uint4 *)(a.w + wl_quant_off(g, B, nrow, 0u, sl, m.r));
+            q1[pp] = *(const uint4 *)(a.w + wl_quant_off(g, B, nrow, 1u, sl, m.r));
+            dv[pp] = *(const uint16_t *)(a.w + wl_meta_off(g, B, nrow, sl, m.r));
         }
     };
     load(0u);                                                     // unconditional: no join before QACT
@@ -327,7 +323,7 @@ __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
 #pragma unroll
         for (int pp = 0; pp < P; ++pp) {
             if (p0 + (uint32_t)pp >= npass) break;
-            const MvUnit m = mv_unit(p0 + (uint32_t)pp, lane, cnt, nunit, G0, row_lo, row_hi);
+            const MvUnit m = mv_unit(p0 + (uint32_t)pp, lane, nrow, nunit);
             const uint32_t xo = w * kx + m.k;
             const int4 xa = *(const int4 *)(s_xq + xo * 32u), xb = *(const int4 *)(s_xq + xo * 32u + 16u);
             int is = dot4((int)q0[pp].x, xa.x, 0);
@@ -341,8 +337,8 @@ __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
             const float tt = (h2f_fast(dv[pp]) * s_xd[xo]) * (float)is;
             const uint32_t b = w + 16u * m.k;
             if (m.valid) {
-                s_t[(m.row - row_lo) * nb + b] = tt;
-                if (ISUMS && t == 0u) a.isums[(size_t)m.row * nb + b] = is;
+                s_t[m.r * nb + b] = tt;
+                if (ISUMS && t == 0u) a.isums[(size_t)(row_lo + m.r) * nb + b] = is;
             }
         }
     }
@@ -354,29 +350,25 @@ __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
 }  // namespace tsr
 
 // ---- launchers ------------------------------------------------------------------------------------
-// One workgroup of 16 waves per rb consecutive rows, rb = ceil(N / n_cu) (at least 16), so that every
+// One workgroup of 16 waves per row block of rb rows, rb = ceil(N / n_cu) (at least 16), so that every
 // compute unit holds one workgroup with its whole share of the matrix; rb is lowered when the terms
-// would not fit the LDS budget.
+// would not fit the LDS budget. The weight layout is built for this rb at upload.
 static size_t mv_lds_rows(uint32_t rb, uint32_t nb) {   // terms (16-byte padded) and partials
     return 4u * ((((size_t)rb * nb + 3u) & ~(size_t)3u) + 16u * (size_t)rb);
 }
-static uint32_t mv_rows_per_block(uint32_t N, uint32_t nb, uint32_t n_cu, size_t lds_fixed) {
-    uint32_t rb = (N + n_cu - 1u) / n_cu;
-    if (rb < 16u) rb = 16u;
-    while (rb > 1u && lds_fixed + mv_lds_rows(rb, nb) > 120u * 1024u) rb = (rb + 1u) / 2u;
-    return rb;
+static size_t mv_lds_fixed(uint32_t fmt, uint32_t nb) {  // x quants (+ sums) and scales of 16 waves, flags
+    const uint32_t kx = (nb + 15u) / 16u;
+    return fmt == TSR_HIP_FMT_Q4_K ? (size_t)tsr::kMvWaves * kx * (tsr::kXq4Stride + 32u + 4u) + 64u
+                                   : (size_t)tsr::kMvWaves * kx * (32u + 4u);
 }
 
-// The largest number of 4-unit passes of any wave: ngrp * ceil(nb / 16) units for the workgroup
-// whose rows touch the most 16-row groups.
-static uint32_t mv_max_pass(uint32_t N, uint32_t rb, uint32_t nb) {
-    uint32_t ngrp = 0;
-    for (uint32_t lo = 0; lo < N; lo += rb) {
-        const uint32_t hi = std::min(N, lo + rb);
-        ngrp = std::max(ngrp, ((hi - 1u) >> 4) - (lo >> 4) + 1u);
-        if (lo >= 64u * rb) break;                               // the pattern of row_lo mod 16 repeats
-    }
-    return (ngrp * ((nb + 15u) / 16u) + 3u) / 4u;
+uint32_t tsr_wl_rows_per_block(uint32_t fmt, uint32_t N, uint32_t K, uint32_t n_cu) {
+    const uint32_t nb = K / (fmt == TSR_HIP_FMT_Q4_K ? 256u : 32u);
+    const size_t fixed = mv_lds_fixed(fmt, nb);
+    uint32_t rb = (N + n_cu - 1u) / n_cu;
+    if (rb < 16u) rb = 16u;
+    while (rb > 1u && fixed + mv_lds_rows(rb, nb) > 120u * 1024u) rb = (rb + 1u) / 2u;
+    return rb;
 }
 
 template <int P>
@@ -390,25 +382,20 @@ static void launch_q80(const tsr::MvArgs & a, dim3 grid, size_t lds, hipStream_t
     else hipLaunchKernelGGL((tsr::k_mv_q80<P, false>), grid, dim3(1024), lds, s, a);
 }
 
-int tsr_launch_mv_q4_k(const tsr::MvArgs & a0, uint32_t n_cu, hipStream_t s) {
-    tsr::MvArgs a = a0;
-    const uint32_t nsb = a.K / 256u, kx = (nsb + 15u) / 16u;
-    const size_t fixed = (size_t)tsr::kMvWaves * kx * (tsr::kXq4Stride + 32u + 4u) + 64u;
-    a.rb = mv_rows_per_block(a.N, nsb, n_cu, fixed);
-    const size_t lds = fixed + mv_lds_rows(a.rb, nsb);
+int tsr_launch_mv_q4_k(const tsr::MvArgs & a, hipStream_t s) {
+    const uint32_t nsb = a.K / 256u;
+    const size_t lds = mv_lds_fixed(TSR_HIP_FMT_Q4_K, nsb) + mv_lds_rows(a.rb, nsb);
     const dim3 grid((a.N + a.rb - 1u) / a.rb, a.T);
     launch_q4k<1>(a, grid, lds, s);                               // 36 load registers per pass
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-int tsr_launch_mv_q8_0(const tsr::MvArgs & a0, uint32_t n_cu, hipStream_t s) {
-    tsr::MvArgs a = a0;
-    const uint32_t nb = a.K / 32u, kx = (nb + 15u) / 16u;
-    const size_t fixed = (size_t)tsr::kMvWaves * kx * (32u + 4u);
-    a.rb = mv_rows_per_block(a.N, nb, n_cu, fixed);
-    const size_t lds = fixed + mv_lds_rows(a.rb, nb);
+int tsr_launch_mv_q8_0(const tsr::MvArgs & a, hipStream_t s) {
+    const uint32_t nb = a.K / 32u;
+    const size_t lds = mv_lds_fixed(TSR_HIP_FMT_Q8_0, nb) + mv_lds_rows(a.rb, nb);
     const dim3 grid((a.N + a.rb - 1u) / a.rb, a.T);
-    const uint32_t mp = mv_max_pass(a.N, a.rb, nb);
+    // passes of the wave with the most units: rb rows x ceil(nb / 16) slots, 64 units a pass
+    const uint32_t mp = (a.rb * ((nb + 15u) / 16u) + 63u) / 64u;
     if (mp <= 1u) launch_q80<1>(a, grid, lds, s);
     else if (mp <= 2u) launch_q80<2>(a, grid, lds, s);
     else if (mp <= 4u) launch_q80<4>(a, grid, lds, s);

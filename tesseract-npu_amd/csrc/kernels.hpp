@@ -15,10 +15,9 @@ struct QactArgs {
     uint32_t d_off, bs_off;  // byte offsets of the D and BS regions
 };
 
-// MUL_MAT over the device weight layout of wlayout.hpp (meta region wm, quant region wq).
+// MUL_MAT over the device weight layout of wlayout.hpp (row blocks of rb rows at w).
 struct MvArgs {
-    const uint8_t * wm;
-    const uint8_t * wq;
+    const uint8_t * w;
     const float * x;
     uint64_t x_stride;
     float * y;
@@ -28,14 +27,13 @@ struct MvArgs {
     int32_t * isums;         // nullable: per-block integer sums of token 0 (checking)
     uint32_t N, K, T;
     uint32_t acc;            // y = FA(y_old, v)
-    uint32_t rb;             // rows per workgroup (set by the launcher)
+    uint32_t rb;             // rows per row block = per workgroup (the weight's)
 };
 
 // Prefill MUL_MAT (T >= 16) on the matrix cores: the activations are first quantized (k_qact_mm)
 // into block-major quants at qa ([K/32][T][32 B]) and f32 scales at qa + d_off ([K/32][T]).
 struct MmArgs {
-    const uint8_t * wm;
-    const uint8_t * wq;
+    const uint8_t * w;       // weight layout of wlayout.hpp, row blocks of rb rows
     const uint8_t * qa;
     uint32_t qa_stride, d_off;
     float * y;
@@ -44,6 +42,7 @@ struct MmArgs {
     uint64_t add_stride;
     uint32_t N, K, T;
     uint32_t acc;
+    uint32_t rb;
 };
 
 // A KV plane (see k_kv.hip for the layout).
@@ -101,8 +100,10 @@ struct FaArgs {
 }  // namespace tsr
 
 int tsr_launch_qact(const tsr::QactArgs & a, uint32_t T, hipStream_t s);
-int tsr_launch_mv_q8_0(const tsr::MvArgs & a, uint32_t n_cu, hipStream_t s);
-int tsr_launch_mv_q4_k(const tsr::MvArgs & a, uint32_t n_cu, hipStream_t s);
+// Rows per row block of a weight uploaded for a device with n_cu compute units (fmt: TSR_HIP_FMT_*).
+uint32_t tsr_wl_rows_per_block(uint32_t fmt, uint32_t N, uint32_t K, uint32_t n_cu);
+int tsr_launch_mv_q8_0(const tsr::MvArgs & a, hipStream_t s);
+int tsr_launch_mv_q4_k(const tsr::MvArgs & a, hipStream_t s);
 int tsr_launch_qact_mm(const float * x, uint64_t x_stride, uint32_t K, uint32_t T, uint8_t * xq, float * xd,
                        hipStream_t s);
 int tsr_launch_mm_q8_0(const tsr::MmArgs & a, hipStream_t s);

@@ -76,8 +76,8 @@ struct tsr_hip_ctx {
 
 struct tsr_hip_weight {
     uint32_t fmt = 0, N = 0, K = 0;
-    uint8_t * dev = nullptr;     // meta region at 0, quant region at quant_off
-    size_t quant_off = 0;
+    uint32_t rb = 0;             // rows per row block of the layout (wlayout.hpp)
+    uint8_t * dev = nullptr;
     size_t bytes = 0;
 };
 

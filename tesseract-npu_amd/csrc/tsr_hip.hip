@@ -193,8 +193,6 @@ constexpr uint32_t kMmChunk = 4096u;     // tokens per prefill launch pair (boun
 
 uint32_t blk_values(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 32u : 256u; }
 uint32_t blk_bytes(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 34u : 144u; }
-uint32_t blk_meta(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 2u : 16u; }
-uint32_t blk_quant(uint32_t fmt) { return fmt == TSR_HIP_FMT_Q8_0 ? 32u : 128u; }
 
 // Q4_K scales: ggml packs eight 6-bit scales sc_j and mins m_j into 12 bytes (get_scale_min_k4,
 // sw/sim/tsr_ref.c:359-367). The device keeps the same 96 bits re-arranged so that one bit-field
@@ -246,34 +244,32 @@ int tsr_hip_weight_upload(tsr_hip_ctx * ctx, uint32_t fmt, const void * ggml_blo
     if (fmt != TSR_HIP_FMT_Q8_0 && fmt != TSR_HIP_FMT_Q4_K) return TSR_HIP_E_FMT;
     if (N == 0u || K == 0u || K % blk_values(fmt) != 0u || K > kKMax) return TSR_HIP_E_SHAPE;
     const uint32_t nb = K / blk_values(fmt);
-    const tsr::WGeom g = tsr::wgeom(N, nb);
-    const size_t rows = 16u * (size_t)g.ng;                       // padded to whole row groups
-    const size_t meta_bytes = rows * nb * blk_meta(fmt);
-    const size_t quant_off = (meta_bytes + 255u) & ~(size_t)255u;
-    const size_t quant_bytes = rows * nb * blk_quant(fmt);
+    const uint32_t rb = tsr_wl_rows_per_block(fmt, N, K, (uint32_t)ctx->n_cu);
+    const bool q4k = fmt == TSR_HIP_FMT_Q4_K;
+    const tsr::WGeom g = tsr::wgeom(N, nb, rb, q4k);
     std::vector<uint8_t> host;
     try {
-        host.assign(quant_off + quant_bytes, 0u);                 // padding rows stay zero
+        host.assign(tsr::wl_bytes(g), 0u);                      // block padding stays zero
     } catch (...) {
         return TSR_HIP_E_NOMEM;
     }
     const uint8_t * src = (const uint8_t *)ggml_blocks;
-    uint8_t * hm = host.data(), * hq = host.data() + quant_off;
+    uint8_t * hd = host.data();
     const uint32_t bb = blk_bytes(fmt);
     parallel_rows(N, [&](uint32_t lo, uint32_t hi) {
         for (uint32_t n = lo; n < hi; ++n) {
-            const uint32_t G = n >> 4, r = n & 15u;
+            const uint32_t B = n / rb, r = n - B * rb, R = tsr::wl_rows(g, B);
             for (uint32_t s = 0; s < nb; ++s) {
                 const uint8_t * b = src + ((size_t)n * nb + s) * bb;
                 const uint32_t sl = tsr::wl_slot_of(g, s);
-                if (fmt == TSR_HIP_FMT_Q4_K) {
-                    uint8_t * m = hm + tsr::q4k_meta_off(g, G, sl, r);
+                uint8_t * m = hd + tsr::wl_meta_off(g, B, R, sl, r);
+                if (q4k) {
                     memcpy(m, b, 4);
                     q4k_meta_encode(b + 4, m + 4);
-                    for (uint32_t j = 0; j < 8u; ++j) memcpy(hq + tsr::q4k_quant_off(g, G, j, sl, r), b + 16u + 16u * j, 16);
+                    for (uint32_t j = 0; j < 8u; ++j) memcpy(hd + tsr::wl_quant_off(g, B, R, j, sl, r), b + 16u + 16u * j, 16);
                 } else {
-                    memcpy(hm + tsr::q80_meta_off(g, G, sl, r), b, 2);
-                    for (uint32_t h = 0; h < 2u; ++h) memcpy(hq + tsr::q80_quant_off(g, G, h, sl, r), b + 2u + 16u * h, 16);
+                    memcpy(m, b, 2);
+                    for (uint32_t h = 0; h < 2u; ++h) memcpy(hd + tsr::wl_quant_off(g, B, R, h, sl, r), b + 2u + 16u * h, 16);
                 }
             }
         }
@@ -283,7 +279,7 @@ int tsr_hip_weight_upload(tsr_hip_ctx * ctx, uint32_t fmt, const void * ggml_blo
     w->fmt = fmt;
     w->N = N;
     w->K = K;
-    w->quant_off = quant_off;
+    w->rb = rb;
     w->bytes = host.size();
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
@@ -310,23 +306,24 @@ int tsr_hip_weight_read(tsr_hip_ctx * ctx, const tsr_hip_weight * w, void * ggml
         if (rc) return rc;
     }
     const uint32_t nb = w->K / blk_values(w->fmt), bb = blk_bytes(w->fmt);
-    const tsr::WGeom g = tsr::wgeom(w->N, nb);
-    const uint8_t * hm = host.data(), * hq = host.data() + w->quant_off;
+    const bool q4k = w->fmt == TSR_HIP_FMT_Q4_K;
+    const tsr::WGeom g = tsr::wgeom(w->N, nb, w->rb, q4k);
+    const uint8_t * hd = host.data();
     uint8_t * dst = (uint8_t *)ggml_blocks;
     parallel_rows(w->N, [&](uint32_t lo, uint32_t hi) {
         for (uint32_t n = lo; n < hi; ++n) {
-            const uint32_t G = n >> 4, r = n & 15u;
+            const uint32_t B = n / w->rb, r = n - B * w->rb, R = tsr::wl_rows(g, B);
             for (uint32_t s = 0; s < nb; ++s) {
                 uint8_t * b = dst + ((size_t)n * nb + s) * bb;
                 const uint32_t sl = tsr::wl_slot_of(g, s);
-                if (w->fmt == TSR_HIP_FMT_Q4_K) {
-                    const uint8_t * m = hm + tsr::q4k_meta_off(g, G, sl, r);
+                const uint8_t * m = hd + tsr::wl_meta_off(g, B, R, sl, r);
+                if (q4k) {
                     memcpy(b, m, 4);
                     q4k_meta_decode(m + 4, b + 4);
-                    for (uint32_t j = 0; j < 8u; ++j) memcpy(b + 16u + 16u * j, hq + tsr::q4k_quant_off(g, G, j, sl, r), 16);
+                    for (uint32_t j = 0; j < 8u; ++j) memcpy(b + 16u + 16u * j, hd + tsr::wl_quant_off(g, B, R, j, sl, r), 16);
                 } else {
-                    memcpy(b, hm + tsr::q80_meta_off(g, G, sl, r), 2);
-                    for (uint32_t h = 0; h < 2u; ++h) memcpy(b + 2u + 16u * h, hq + tsr::q80_quant_off(g, G, h, sl, r), 16);
+                    memcpy(b, m, 2);
+                    for (uint32_t h = 0; h < 2u; ++h) memcpy(b + 2u + 16u * h, hd + tsr::wl_quant_off(g, B, R, h, sl, r), 16);
                 }
             }
         }
@@ -403,8 +400,8 @@ static int mul_mat_locked(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
     (void)hipSetDevice(ctx->device);
     tsr::MvArgs a{};
     const size_t nb = w->K / blk_values(w->fmt);
-    a.wm = w->dev;
-    a.wq = w->dev + w->quant_off;
+    a.w = w->dev;
+    a.rb = w->rb;
     a.x = x_dev;
     a.x_stride = x_stride;
     a.y = y_dev;
@@ -431,8 +428,8 @@ static int mul_mat_locked(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
             if (tsr_launch_qact_mm(x_dev + (size_t)t0 * x_stride, x_stride, w->K, tt, xq, (float *)(xq + d_off), s))
                 return TSR_HIP_E_HIP;
             tsr::MmArgs m{};
-            m.wm = w->dev;
-            m.wq = w->dev + w->quant_off;
+            m.w = w->dev;
+            m.rb = w->rb;
             m.qa = xq;
             m.qa_stride = 0u;
             m.d_off = (uint32_t)d_off;
@@ -454,8 +451,7 @@ static int mul_mat_locked(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
         a.y = y_dev + (size_t)t0 * y_stride;
         a.add = add_dev ? add_dev + (size_t)t0 * add_stride : nullptr;
         a.T = tt;
-        const uint32_t ncu = (uint32_t)ctx->n_cu;
-        const int rc = w->fmt == TSR_HIP_FMT_Q8_0 ? tsr_launch_mv_q8_0(a, ncu, s) : tsr_launch_mv_q4_k(a, ncu, s);
+        const int rc = w->fmt == TSR_HIP_FMT_Q8_0 ? tsr_launch_mv_q8_0(a, s) : tsr_launch_mv_q4_k(a, s);
         if (rc) return rc == -2 ? TSR_HIP_E_SHAPE : TSR_HIP_E_HIP;
     }
     return TSR_HIP_OK;

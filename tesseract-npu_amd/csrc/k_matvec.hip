@@ -88,6 +88,16 @@ __device__ __forceinline__ void mv_tree_store(const MvArgs & a, const float * s_
     }
 }
 
+// Every wave's x requests enter the compute unit's memory queue before any weight request of the
+// workgroup. The queue serves vector-memory requests in order, so an x load issued behind the
+// weight loads of other waves would return only after them (measured: up to 5 us into a 9 us
+// launch). A bare s_barrier orders the issue without waiting for any load.
+__device__ __forceinline__ void x_first_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 // The unit of lane `lane` in pass p: unit u = 64 p + lane of the wave's R cnt units (slot-major:
 // slot k = u / R, row u % R of the block). Units beyond the last, and every unit of a wave without
 // blocks (cnt == 0), load the last unit's address (a valid one) and are not used.
@@ -139,7 +149,7 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     };
     float4 xv[4];
     load_x(0u, xv);
-    __builtin_amdgcn_sched_barrier(0);
+    x_first_barrier();
 
     uint4 qv[P][8], mv[P];
     auto load = [&](uint32_t p0) {
@@ -171,14 +181,15 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
             tiny_any |= tiny;
         }
     };
-    // Waves 8..15 quantize their first round before they issue their weight loads: the weight
+    // Waves 12..15 quantize their first round before they issue their weight loads: the weight
     // stream of a compute unit is accepted at the rate HBM delivers it, so these waves would wait
-    // to issue anyway, and their QACT is then off the critical path. Waves 0..7 keep the memory
-    // pipe busy from the start and quantize while their loads are in flight.
-    if (w >= 8u && cnt) qact_round(0u, xv);
+    // to issue anyway, and their QACT is then off the critical path. Waves 0..11 keep the memory
+    // pipe busy from the start and quantize while their loads are in flight (a wave blocked on
+    // issuing a load cannot quantize; the split was measured: 12 beats 4, 8 and none).
+    if (w >= 12u && cnt) qact_round(0u, xv);
     load(0u);                                                     // unconditional (clamped)
     __builtin_amdgcn_sched_barrier(0);
-    if (w < 8u && cnt) qact_round(0u, xv);
+    if (w < 12u && cnt) qact_round(0u, xv);
     for (uint32_t i = 1; 4u * i < cnt; ++i) {                     // K > 16384 only
         float4 xr[4];
         load_x(i, xr);
@@ -283,7 +294,7 @@ __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
         const uint32_t b = min(w + 16u * k, nb - 1u);
         xv[i] = *(const float4 *)(x + 32u * b + 4u * ((uint32_t)lane & 7u));
     }
-    __builtin_amdgcn_sched_barrier(0);
+    x_first_barrier();
 
     uint4 q0[P], q1[P];
     uint32_t dv[P];

@@ -141,14 +141,18 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
 
     // x first (vector-memory counters retire in order): the 16-lane row h = lane / 16 of the wave
     // holds block k = 4 i + h of round i, lane i of the row its values 16 i .. 16 i + 15
+    // A wave with one block (cnt == 1) quantizes it with the whole wave instead (lane l: values
+    // 4 l .. 4 l + 3), a quarter of the per-lane work.
     const uint32_t h4 = (uint32_t)lane >> 4, l16 = (uint32_t)lane & 15u;
+    const bool one = cnt <= 1u;                                   // wave-uniform
     auto load_x = [&](uint32_t i, float4 (&xr)[4]) {
         const uint32_t s = min(w + 16u * (4u * i + h4), nsb - 1u);
 #pragma unroll
         for (int c = 0; c < 4; ++c) xr[c] = *(const float4 *)(x + 256u * s + 16u * l16 + 4u * (uint32_t)c);
     };
     float4 xv[4];
-    load_x(0u, xv);
+    if (one) xv[0] = *(const float4 *)(x + 256u * min(w, nsb - 1u) + 4u * (uint32_t)lane);
+    else load_x(0u, xv);
     x_first_barrier();
 
     uint4 qv[P][8], mv[P];
@@ -181,15 +185,28 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
             tiny_any |= tiny;
         }
     };
+    auto qact_first = [&]() {
+        if (!one) { qact_round(0u, xv); return; }
+        float d;
+        int s4;
+        bool tiny;
+        const uint32_t qq = qact_a256_wave(xv[0], &d, &s4, &tiny);
+        const int s32 = sum8_i(s4);                               // the 32 quants of sub-block lane / 8
+        const uint32_t xo = w * kx;
+        *(uint32_t *)(s_xq + xo * kXq4Stride + 4u * (uint32_t)lane) = qq;
+        if ((lane & 7) == 0) s_xb[xo * 8u + ((uint32_t)lane >> 3)] = s32;
+        if (lane == 0) s_xd[xo] = d;
+        tiny_any |= tiny;
+    };
     // Waves 12..15 quantize their first round before they issue their weight loads: the weight
     // stream of a compute unit is accepted at the rate HBM delivers it, so these waves would wait
     // to issue anyway, and their QACT is then off the critical path. Waves 0..11 keep the memory
     // pipe busy from the start and quantize while their loads are in flight (a wave blocked on
     // issuing a load cannot quantize; the split was measured: 12 beats 4, 8 and none).
-    if (w >= 12u && cnt) qact_round(0u, xv);
+    if (w >= 12u && cnt) qact_first();
     load(0u);                                                     // unconditional (clamped)
     __builtin_amdgcn_sched_barrier(0);
-    if (w < 12u && cnt) qact_round(0u, xv);
+    if (w < 12u && cnt) qact_first();
     for (uint32_t i = 1; 4u * i < cnt; ++i) {                     // K > 16384 only
         float4 xr[4];
         load_x(i, xr);

@@ -28,7 +28,8 @@ __global__ __launch_bounds__(256) void k_qact(QactArgs a) {
             const float4 v = *(const float4 *)(x + 256u * unit + 4u * (uint32_t)lane);
             float d;
             int s4;
-            const uint32_t q = qact_a256_lane(v, lane, &d, &s4);
+            bool tiny;
+            const uint32_t q = qact_a256_wave(v, &d, &s4, &tiny);
             *(uint32_t *)(qa + 256u * unit + 4u * (uint32_t)lane) = q;
             if (lane == 0) *(float *)(qa + a.d_off + 4u * unit) = d;
             int s16 = s4 + dpp_i<kDppXor1>(s4);

@@ -59,46 +59,61 @@ __device__ __forceinline__ uint32_t wave_umax(uint32_t m) {
     return umax_u((uint32_t)__builtin_amdgcn_readlane((int)m, 0), (uint32_t)__builtin_amdgcn_readlane((int)m, 32));
 }
 
-// One A256 block held by a whole wave (lane l: values 4l .. 4l+3). Returns this lane's 4 quants
-// packed; *d = the block's d (every lane); *sum4 = the sum of this lane's 4 quants.
-// First largest |x|: the wave maximum of the lane maxima, then the lowest lane holding it (lane l
-// holds indices 4l .. 4l+3, and its own first largest is kept), read with one readlane.
-__device__ __forceinline__ uint32_t qact_a256_lane(const float4 v, int lane, float * d, int * sum4) {
-    (void)lane;
-    const float xs[4] = { v.x, v.y, v.z, v.w };
+// Shared steps of A256 (sw/sim/tsr_ref.c:485-520):
+// - the NaN-excluded magnitude maximum as an integer maximum of |x| bits (a NaN counts as 0). A
+//   subnormal maximum means every value is zero or subnormal, i.e. zero after DAZ, so the DAZ is
+//   applied to the maximum only (normal magnitudes compare above subnormal ones as integers);
+// - the first element of a lane whose magnitude equals the maximum (a reverse select pass);
+// - q = round_half_even(iscale x) saturated to int8: v_rndne, v_cvt_i32 (NaN -> 0, saturating),
+//   integer clamp; four quants packed with v_perm, their sum with v_dot4 against ones.
+__device__ __forceinline__ uint32_t a256_mag_max(const float * xs, int n) {
     uint32_t m = 0;
+    for (int i = 0; i < n; ++i) {
+        const uint32_t a = fb(xs[i]) & 0x7FFFFFFFu;
+        m = umax_u(m, a > 0x7F800000u ? 0u : a);
+    }
+    return m;
+}
+__device__ __forceinline__ float a256_first_of(const float * xs, int n, uint32_t amax) {
     float best = 0.0f;
+    for (int i = n - 1; i >= 0; --i) best = (fb(xs[i]) & 0x7FFFFFFFu) == amax ? xs[i] : best;
+    return best;
+}
+__device__ __forceinline__ uint32_t pack4_i8(int32_t q0, int32_t q1, int32_t q2, int32_t q3) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q1, (uint32_t)q0, 0x0C0C0400u);   // q0.b0 q1.b0 0 0
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q3, (uint32_t)q2, 0x0C0C0400u);   // q2.b0 q3.b0 0 0
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);                                    // lo.b0 lo.b1 hi.b0 hi.b1
+}
+
+// One A256 block held by a whole wave (lane l: values 4l .. 4l+3). Returns this lane's 4 quants
+// packed; *d = the block's d (every lane); *sum4 = the sum of this lane's 4 quants; *tiny =
+// 0 < |d| < 2^-60. First largest |x|: the lowest lane holding the maximum (its own first), read
+// with one readlane. The plain product iscale x rounds like FM(iscale, x) when amax >= 2^-60 (see
+// qact_a32_lane); below that the spec operation is used.
+__device__ __forceinline__ uint32_t qact_a256_wave(const float4 v, float * d, int * sum4, bool * tiny) {
+    const float xs[4] = { v.x, v.y, v.z, v.w };
+    const uint32_t m = a256_mag_max(xs, 4);
+    uint32_t amax = wave_umax(m);
+    amax = amax < 0x00800000u ? 0u : amax;
+    const float best = a256_first_of(xs, 4, amax);
+    const uint64_t hold = __ballot(m == amax && amax != 0u);
+    const float mx = hold ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(best), __builtin_ctzll(hold))) : 0.0f;
+    const bool zero = amax == 0u;
+    const float iscale = zero ? 0.0f : sdiv(-127.0f, mx);
+    int32_t q[4];
+    if (zero || amax >= 0x21800000u) {                            // wave-uniform
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t a = mag_bits(xs[i]);
-        if (a <= 0x7F800000u && a > m) { m = a; best = daz(xs[i]); }
+        for (int i = 0; i < 4; ++i) q[i] = round_even8(iscale * xs[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = round_even8(smul(iscale, xs[i]));
     }
-    const uint32_t amax = wave_umax(m);
-    uint32_t packed = 0;
-    int s = 0;
-    float dd = 0.0f;
-    if (amax != 0u) {
-        const uint64_t hold = __ballot(m == amax);
-        const int win = __builtin_ctzll(hold);
-        const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(best), win));
-        const float iscale = sdiv(-127.0f, mx);
-        int qi[4];
-        if (amax >= 0x21800000u) {                              // wave-uniform; as in qact_a32_lane
-#pragma unroll
-            for (int i = 0; i < 4; ++i) qi[i] = round_even8(iscale * xs[i]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) qi[i] = round_even8(smul(iscale, xs[i]));
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            s += qi[i];
-            packed |= ((uint32_t)qi[i] & 0xFFu) << (8 * i);
-        }
-        dd = srcp(iscale);
-    }
+    const uint32_t packed = pack4_i8(q[0], q[1], q[2], q[3]);
+    const float dd = zero ? 0.0f : srcp(iscale);
+    const uint32_t ad = fb(dd) & 0x7FFFFFFFu;
     *d = dd;
-    *sum4 = s;
+    *sum4 = dot4((int)packed, 0x01010101, 0);
+    *tiny = ad != 0u && ad < 0x21800000u;
     return packed;
 }
 
@@ -134,21 +149,17 @@ __device__ __forceinline__ uint4 qact_a256_row(const float4 (&v)[4], float * d, 
     float xs[16];
 #pragma unroll
     for (int i = 0; i < 4; ++i) { xs[4 * i] = v[i].x; xs[4 * i + 1] = v[i].y; xs[4 * i + 2] = v[i].z; xs[4 * i + 3] = v[i].w; }
-    uint32_t m = 0;
-    float best = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const uint32_t a = mag_bits(xs[i]);
-        if (a <= 0x7F800000u && a > m) { m = a; best = daz(xs[i]); }
-    }
-    const uint32_t amax = row16_umax(m);
+    const uint32_t m = a256_mag_max(xs, 16);
+    uint32_t amax = row16_umax(m);
+    amax = amax < 0x00800000u ? 0u : amax;
+    const float best = a256_first_of(xs, 16, amax);
     const uint32_t l16 = __lane_id() & 15u;
-    const uint32_t win = row16_umin(m == amax ? l16 : 16u);
+    const uint32_t win = row16_umin(m == amax && amax != 0u ? l16 : 16u);
     const float mx = bf(row16_or(l16 == win ? fb(best) : 0u));
     const bool zero = amax == 0u;
     const bool exact = __ballot(!zero && amax < 0x21800000u) != 0ull;   // wave-uniform
     const float iscale = zero ? 0.0f : sdiv(-127.0f, mx);
-    int q[16];
+    int32_t q[16];
     if (!exact) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) q[i] = round_even8(iscale * xs[i]);
@@ -156,12 +167,12 @@ __device__ __forceinline__ uint4 qact_a256_row(const float4 (&v)[4], float * d, 
 #pragma unroll
         for (int i = 0; i < 16; ++i) q[i] = round_even8(smul(iscale, xs[i]));
     }
-    uint32_t pk[4] = { 0u, 0u, 0u, 0u };
+    uint32_t pk[4];
     int s = 0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        s += q[i];
-        pk[i >> 2] |= ((uint32_t)q[i] & 0xFFu) << (8 * (i & 3));
+    for (int i = 0; i < 4; ++i) {
+        pk[i] = pack4_i8(q[4 * i], q[4 * i + 1], q[4 * i + 2], q[4 * i + 3]);
+        s = dot4((int)pk[i], 0x01010101, s);
     }
     const float dd = zero ? 0.0f : srcp(iscale);
     const uint32_t ad = fb(dd) & 0x7FFFFFFFu;

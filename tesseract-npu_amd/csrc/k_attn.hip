@@ -20,6 +20,12 @@
 // to an integer W = RNE(w 2^(23 - E_S)) (|W| <= 2^24) and A = sum W q is exact. W is split into four
 // balanced base-256 digits d_k in [-128, 127] (W = sum d_k 256^k), so A = sum_k 256^k (sum d_k q)
 // runs on the int8 matrix core with exact int32 digit sums (|sum| <= 64 * 128 * 128).
+//
+// Subnormal operands. A score is a tree sum of terms (dK Dx) f32(isum) with fp16 dK and Dx: every
+// term is 0 or a multiple of 2^-48 in magnitude, so is every sum, and a GENERAL mask is added with
+// the full f32 rule: no score is subnormal. Maxima are scores or the floor; EXPK values,
+// block-float values and the results of rule operations are never subnormal either. The f32 steps
+// after the scores therefore use the rule without the input DAZ (sadd_n / smul_n).
 #include "kernels.hpp"
 #include "qact.hpp"
 
@@ -250,7 +256,8 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
 constexpr uint32_t kPvWaves = 8;                                  // NCG <= 128 -> <= 8 segments per channel
 constexpr uint32_t kPvMaxSeg = 8;
 
-__device__ __forceinline__ float ctree4(float x0, float x1, float x2, float x3) { return sadd(sadd(x0, x1), sadd(x2, x3)); }
+// CTREE over 4 channel partials (never subnormal: results of the segment chains).
+__device__ __forceinline__ float ctree4(float x0, float x1, float x2, float x3) { return sadd_n(sadd_n(x0, x1), sadd_n(x2, x3)); }
 __device__ __forceinline__ int32_t row16_isum(int32_t v) {
     v += dpp_i<kDppXor1>(v);
     v += dpp_i<kDppXor2>(v);
@@ -365,7 +372,7 @@ __global__ __launch_bounds__(64 * kPvWaves) void k_fa_pv(FaArgs a, FaPlan p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // EXPK results are zero, normal, Inf or NaN (never subnormal)
-            pz[i] = (cv && head_ok) ? expk(smul(ssub(ss[i], m), a.scale), a.ex, s_t64) : 0.0f;
+            pz[i] = (cv && head_ok) ? expk(smul_n(ssub_n(ss[i], m), a.scale), a.ex, s_t64) : 0.0f;
             const uint32_t f = f_field(pz[i]);
             pnf |= f == 255u ? 1u : 0u;
             pe = max(pe, f == 255u ? 0u : f);
@@ -465,12 +472,12 @@ __global__ __launch_bounds__(64 * kPvWaves) void k_fa_pv(FaArgs a, FaPlan p) {
         if (hi2 >= G) continue;
         const uint32_t h2 = g * G + hi2;
         float O = 0.0f;
-        for (uint32_t seg = 0; seg < nseg; ++seg) O = sadd(O, s_c[(seg * 4u + r4) * DV + v]);
+        for (uint32_t seg = 0; seg < nseg; ++seg) O = sadd_n(O, s_c[(seg * 4u + r4) * DV + v]);
         const size_t slot = ((size_t)item * 4u + c) * nh + h2;
         a.OP[slot * D + vh * DV + v] = O;
         if (vh == 0u && v == 0u) {
             float l = 0.0f;
-            for (uint32_t seg = 0; seg < nseg; ++seg) l = sadd(l, s_l[seg * 4u + r4]);
+            for (uint32_t seg = 0; seg < nseg; ++seg) l = sadd_n(l, s_l[seg * 4u + r4]);
             a.LP[slot] = l;
         }
     }
@@ -560,7 +567,7 @@ __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
                 from = (L & 1u) ? mk[k] : (k == 0u ? mr : mrun[k - 1u]);
                 to = mrun[k];
             }
-        const float fx = expk(smul(ssub(from, to), a.scale), a.ex, s_t64);
+        const float fx = expk(smul_n(ssub_n(from, to), a.scale), a.ex, s_t64);
 #pragma unroll
         for (uint32_t k = 0; k < kMergeItems; ++k) {
             if (k >= kn) break;
@@ -570,13 +577,13 @@ __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
             else {
                 const float fa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)k));
                 const float fbv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)k + 1));
-                l = sadd(smul(l, fa), smul(lk, fbv));
-                O = sadd(smul(O, fa), smul(ok, fbv));
+                l = sadd_n(smul_n(l, fa), smul_n(lk, fbv));
+                O = sadd_n(smul_n(O, fa), smul_n(ok, fbv));
             }
             mr = mrun[k];
         }
     }
-    a.out[(size_t)t * a.out_stride + (size_t)h * D + 64u * sl + L] = smul(O, srcp(maxt(l, bf(kLFloor))));
+    a.out[(size_t)t * a.out_stride + (size_t)h * D + 64u * sl + L] = smul_n(O, srcp(maxt(l, bf(kLFloor))));
 }
 
 }  // namespace tsr

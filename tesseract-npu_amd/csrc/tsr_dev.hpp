@@ -38,6 +38,18 @@ __device__ __forceinline__ float smul(float a, float b) { return fin(daz(a) * da
 __device__ __forceinline__ float sdiv(float a, float b) { return fin(daz(a) / daz(b)); }
 __device__ __forceinline__ float srcp(float a) { return fin(1.0f / daz(a)); }
 
+// The same rule for operands that cannot be subnormal (results of earlier rule operations, EXPK
+// values, block-float values, scores): DAZ is then the identity and only the result needs FTZ and
+// NaN canonicalization, each tested with one v_cmp_class (mask 0x90: -/+ subnormal; 0x3: NaN).
+__device__ __forceinline__ float fin_n(float r) {
+    const uint32_t u = fb(r);
+    const uint32_t o = __builtin_amdgcn_class(r, 0x90) ? (u & 0x80000000u) : u;
+    return bf(__builtin_amdgcn_class(r, 0x3) ? kNaN : o);
+}
+__device__ __forceinline__ float sadd_n(float a, float b) { return fin_n(a + b); }
+__device__ __forceinline__ float ssub_n(float a, float b) { return fin_n(a - b); }
+__device__ __forceinline__ float smul_n(float a, float b) { return fin_n(a * b); }
+
 // int32 -> f32 RNE (v_cvt_f32_i32 rounds to nearest even).
 __device__ __forceinline__ float i2f(int32_t v) { return (float)v; }
 

@@ -50,6 +50,7 @@ float    oc_fsub(float a, float b);
 float    oc_fmul(float a, float b);
 float    oc_fdiv(float a, float b);
 float    oc_frecip(float a);
+float    oc_fsqrt(float a);
 float    oc_i2f(int32_t v);
 float    oc_h2f(uint16_t h);
 uint16_t oc_f2h(float f);
@@ -115,4 +116,21 @@ int oc_flash_attn(const float * q, uint32_t T, uint64_t q_stride, const uint8_t 
 #ifdef __cplusplus
 }
 #endif
+/* ---- decode-layer glue ops (oc_glue.c) ------------------------------------------------------ */
+float oc_rms_scale(const float * x, uint32_t n, float eps, float inv_n);
+void  oc_rms_norm_rows(uint32_t n, uint32_t rows, const float * x, uint64_t x_stride, float eps, float inv_n,
+                       const float * w, uint64_t w_stride, uint32_t w_period, float * y, uint64_t y_stride);
+void  oc_sincos(float t, float * s_out, float * c_out);
+void  oc_rope(uint32_t neox, uint32_t head_dim, uint32_t n_dims, uint32_t n_heads, uint32_t T,
+              const float * x, uint64_t x_stride, float * y, uint64_t y_stride, const int32_t * pos,
+              float ts, float m, float freq_scale, const float * ff);
+float oc_silu(float x);
+void  oc_swiglu_rows(uint32_t n, uint32_t rows, const float * g, uint64_t g_stride, const float * u, uint64_t u_stride,
+                     float * y, uint64_t y_stride);
+void  oc_add_rows(uint32_t n, uint32_t rows, const float * a, uint64_t a_stride, const float * b, uint64_t b_stride,
+                  float * y, uint64_t y_stride);
+void  oc_get_rows(uint32_t n, const float * src, uint64_t src_stride, const int32_t * ids, uint32_t count, float * dst,
+                  uint64_t dst_stride);
+void  oc_argmax_rows(uint32_t n, uint32_t rows, const float * x, uint64_t x_stride, int32_t * out);
+
 #endif

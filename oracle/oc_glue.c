@@ -1,0 +1,192 @@
+/* oc_glue.c -- TEST INFRASTRUCTURE ONLY: the CPU restatement of the decode-layer glue ops on the
+ * vector unit's f32 rules (DAZ inputs, one RNE operation, FTZ, canonical NaN: oc_fadd ... oc_fsqrt):
+ * RMS_NORM (+ MUL), ROPE (NORM / NEOX), SILU / SWIGLU, ADD, GET_ROWS and ARGMAX. Only the tests,
+ * smoke() and bench.py's CPU leg load liboracle.so.
+ *
+ * Reference semantics followed (file:line of the reference tree):
+ *   RMS_NORM  RED.SUMSQ with post RMS, then VOP.MULCB (sw/sim/tsr_ref_vu.c:171-263, 102-133;
+ *             sw/ctrl/ref/rmsnorm_ref.hpp:11-14): s = RC(SQ(FA(FM(tree128(p), inv_n), eps))) with
+ *             p[i % 128] = FA(p[i % 128], FM(x_i, x_i)) from +0, y = FM(FM(x, s), w).
+ *   ROPE      sw/sim/tsr_ref_vu.c:308-376 (angles by the recurrence theta_(i+1) = FM(theta_i, TS)
+ *             from i32_to_f32(pos), optional freq factors FD and freq_scale FM; c = FM(M, cos),
+ *             s = FM(M, sin); y0 = FS(FM(x0, c), FM(x1, s)), y1 = FA(FM(x0, s), FM(x1, c)); dims from
+ *             n_dims on copied raw).
+ *   SIN/COS   sw/sim/tsr_ref_math.c:232-416 (VU 6.6): quadrant reduction with round(2/pi 2^64) in
+ *             128-bit integers, round to the nearest quadrant, r = RNE24(F round(pi/2 2^62) 2^-124),
+ *             then the Cephes sinf / cosf polynomials on the f32 rules.
+ *   SILU      sw/sim/tsr_ref_math.c:165-172: FM(x, RC(FA(1, EXPK(x, N1)))); EXPK(x, N1) is EXPK(-x, P1)
+ *             (same constant LK, the sign of K v flipped). SWIGLU = FM(SILU(g), u); ADD = FA.
+ *   GET_ROWS  rows copied bit for bit by I32 ids (sw/ctrl/ref/elem_ref.hpp:17-20).
+ *   ARGMAX    ggml's f32 ARGMAX: the first index of the largest value, NaN never larger.
+ * Output rows hold exactly n words here (the device image's zero tail up to a 64-byte line is a
+ * property of the NPU's scratchpad, not of the op's values). */
+#include "oc.h"
+
+#include <math.h>
+#include <string.h>
+
+typedef union { float f; uint32_t u; } fu32;
+static inline uint32_t bits_of(float f) { fu32 v; v.f = f; return v.u; }
+static inline float flt_of(uint32_t u) { fu32 v; v.u = u; return v.f; }
+static inline uint32_t daz_bits(uint32_t u) { return (u & 0x7F800000u) ? u : (u & 0x80000000u); }
+static inline float fneg(float x) { return flt_of(bits_of(x) ^ 0x80000000u); }
+
+/* ---- RMS_NORM ------------------------------------------------------------------------------ */
+float oc_rms_scale(const float * x, uint32_t n, float eps, float inv_n) {
+    float p[128];
+    for (int i = 0; i < 128; ++i) p[i] = 0.0f;
+    for (uint32_t i = 0; i < n; ++i) p[i % 128u] = oc_fadd(p[i % 128u], oc_fmul(x[i], x[i]));
+    for (int m = 128; m > 1; m >>= 1)
+        for (int k = 0; k < m / 2; ++k) p[k] = oc_fadd(p[2 * k], p[2 * k + 1]);
+    return oc_frecip(oc_fsqrt(oc_fadd(oc_fmul(p[0], inv_n), eps)));
+}
+
+void oc_rms_norm_rows(uint32_t n, uint32_t rows, const float * x, uint64_t x_stride, float eps, float inv_n,
+                      const float * w, uint64_t w_stride, uint32_t w_period, float * y, uint64_t y_stride) {
+    for (uint32_t r = 0; r < rows; ++r) {
+        const float * xr = x + (size_t)r * x_stride;
+        float * yr = y + (size_t)r * y_stride;
+        const float s = oc_rms_scale(xr, n, eps, inv_n);
+        const float * wr = w ? w + (size_t)(r % (w_period ? w_period : 1u)) * w_stride : NULL;
+        for (uint32_t j = 0; j < n; ++j) yr[j] = wr ? oc_fmul(oc_fmul(xr[j], s), wr[j]) : oc_fmul(xr[j], s);
+    }
+}
+
+/* ---- SIN / COS ----------------------------------------------------------------------------- */
+/* 2/pi = 0.A2F9836E4E441529FC27... (hex): round(2/pi 2^64); pi/2 = 1.921FB54442D18469898C...:
+ * round(pi/2 2^62). Cephes sinf / cosf coefficients (single precision, |r| <= pi/4). */
+static const uint64_t kTwoOverPi64 = 0xA2F9836E4E44152Aull;
+static const uint64_t kPiOver2_62 = 0x6487ED5110B4611Aull;
+#define SN1 (-1.6666654611e-1f)
+#define SN2 (8.3321608736e-3f)
+#define SN3 (-1.9515295891e-4f)
+#define CS1 (4.166664568298827e-2f)
+#define CS2 (-1.388731625493765e-3f)
+#define CS3 (2.443315711809948e-5f)
+
+typedef unsigned __int128 u128;
+
+/* RNE to 24 bits of R 2^-124 (0 < R < 2^124, normal result), with a sign */
+static float u128_to_f32(u128 R, int neg) {
+    const uint64_t hi = (uint64_t)(R >> 64), lo = (uint64_t)R;
+    const int b = hi ? 64 + (63 - __builtin_clzll(hi)) : 63 - __builtin_clzll(lo);
+    const int shift = b - 23;
+    uint64_t sig = (uint64_t)(R >> shift);
+    const u128 rem = R & ((((u128)1) << shift) - 1u), half = ((u128)1) << (shift - 1);
+    uint32_t be = (uint32_t)(b + 3);                              /* b - 124 + 127 */
+    if (rem > half || (rem == half && (sig & 1u))) {
+        if (++sig == (1ull << 24)) { sig >>= 1; ++be; }
+    }
+    return flt_of((neg ? 0x80000000u : 0u) | (be << 23) | ((uint32_t)sig & 0x007FFFFFu));
+}
+
+void oc_sincos(float t, float * s_out, float * c_out) {
+    const uint32_t u = daz_bits(bits_of(t)), a = u & 0x7FFFFFFFu;
+    if (a >= 0x7F800000u) { *s_out = *c_out = flt_of(OC_NAN_BITS); return; }
+    const uint32_t E = a >> 23;
+    if (E < 115u) { *s_out = flt_of(u); *c_out = 1.0f; return; }   /* zero and |t| < 2^-12 */
+    /* t 2/pi = M kTwoOverPi64 2^(E - 214): integer part mod 4 and the fraction in units of 2^-62 */
+    const uint64_t M = 0x00800000u | (a & 0x007FFFFFu);
+    const u128 P = (u128)M * kTwoOverPi64;
+    const int sh = 214 - (int)E;                                  /* -40 .. 99 */
+    uint32_t k4;
+    uint64_t F;
+    const uint64_t mask62 = (1ull << 62) - 1u;
+    if (sh >= 62) { k4 = (uint32_t)(P >> sh) & 3u; F = (uint64_t)(P >> (sh - 62)) & mask62; }
+    else if (sh >= 0) { k4 = (uint32_t)(P >> sh) & 3u; F = (uint64_t)(P << (62 - sh)) & mask62; }
+    else { k4 = (uint32_t)(P << -sh) & 3u; F = 0; }
+    int rneg = 0;
+    uint64_t Fm = F;
+    if (F >= (1ull << 61)) { k4 = (k4 + 1u) & 3u; rneg = 1; Fm = (1ull << 62) - F; }   /* nearest quadrant */
+    const float r = Fm ? u128_to_f32((u128)Fm * kPiOver2_62, rneg) : 0.0f;
+    const float z = oc_fmul(r, r);
+    float p = oc_fmul(SN3, z);
+    p = oc_fadd(p, SN2);
+    p = oc_fmul(p, z);
+    p = oc_fadd(p, SN1);
+    p = oc_fmul(p, z);
+    p = oc_fmul(p, r);
+    const float sn = oc_fadd(p, r);
+    p = oc_fmul(CS3, z);
+    p = oc_fadd(p, CS2);
+    p = oc_fmul(p, z);
+    p = oc_fadd(p, CS1);
+    p = oc_fmul(p, z);
+    p = oc_fmul(p, z);
+    const float cs = oc_fadd(oc_fsub(p, oc_fmul(0.5f, z)), 1.0f);
+    float S, C;
+    switch (k4) {
+        case 0: S = sn; C = cs; break;
+        case 1: S = cs; C = fneg(sn); break;
+        case 2: S = fneg(sn); C = fneg(cs); break;
+        default: S = fneg(cs); C = sn; break;
+    }
+    *s_out = (u >> 31) ? fneg(S) : S;
+    *c_out = C;
+}
+
+/* ---- ROPE ---------------------------------------------------------------------------------- */
+void oc_rope(uint32_t neox, uint32_t head_dim, uint32_t n_dims, uint32_t n_heads, uint32_t T,
+             const float * x, uint64_t x_stride, float * y, uint64_t y_stride, const int32_t * pos,
+             float ts, float m, float freq_scale, const float * ff) {
+    const uint32_t half = n_dims / 2u;
+    const int fs = bits_of(freq_scale) != 0x3F800000u;
+    float c[512], s[512];
+    for (uint32_t t = 0; t < T; ++t) {
+        float theta = oc_i2f(pos[t]);
+        for (uint32_t i = 0; i < half; ++i) {
+            float f = ff ? oc_fdiv(theta, ff[i]) : theta;
+            if (fs) f = oc_fmul(freq_scale, f);
+            float sn, cs;
+            oc_sincos(f, &sn, &cs);
+            c[i] = oc_fmul(m, cs);
+            s[i] = oc_fmul(m, sn);
+            theta = oc_fmul(theta, ts);
+        }
+        for (uint32_t h = 0; h < n_heads; ++h) {
+            const float * xr = x + (size_t)t * x_stride + (size_t)h * head_dim;
+            float * yr = y + (size_t)t * y_stride + (size_t)h * head_dim;
+            for (uint32_t i = 0; i < half; ++i) {
+                const uint32_t j0 = neox ? i : 2u * i, j1 = neox ? i + half : 2u * i + 1u;
+                const float x0 = xr[j0], x1 = xr[j1];
+                yr[j0] = oc_fsub(oc_fmul(x0, c[i]), oc_fmul(x1, s[i]));
+                yr[j1] = oc_fadd(oc_fmul(x0, s[i]), oc_fmul(x1, c[i]));
+            }
+            for (uint32_t j = n_dims; j < head_dim; ++j) yr[j] = xr[j];
+        }
+    }
+}
+
+/* ---- SILU / SWIGLU / ADD -------------------------------------------------------------------- */
+float oc_silu(float x) { return oc_fmul(x, oc_frecip(oc_fadd(1.0f, oc_expk(fneg(x))))); }
+
+void oc_swiglu_rows(uint32_t n, uint32_t rows, const float * g, uint64_t g_stride, const float * u, uint64_t u_stride,
+                    float * y, uint64_t y_stride) {
+    for (uint32_t r = 0; r < rows; ++r)
+        for (uint32_t j = 0; j < n; ++j)
+            y[(size_t)r * y_stride + j] = oc_fmul(oc_silu(g[(size_t)r * g_stride + j]), u[(size_t)r * u_stride + j]);
+}
+
+void oc_add_rows(uint32_t n, uint32_t rows, const float * a, uint64_t a_stride, const float * b, uint64_t b_stride,
+                 float * y, uint64_t y_stride) {
+    for (uint32_t r = 0; r < rows; ++r)
+        for (uint32_t j = 0; j < n; ++j)
+            y[(size_t)r * y_stride + j] = oc_fadd(a[(size_t)r * a_stride + j], b[(size_t)r * b_stride + j]);
+}
+
+/* ---- GET_ROWS / ARGMAX ---------------------------------------------------------------------- */
+void oc_get_rows(uint32_t n, const float * src, uint64_t src_stride, const int32_t * ids, uint32_t count, float * dst,
+                 uint64_t dst_stride) {
+    for (uint32_t i = 0; i < count; ++i) memcpy(dst + (size_t)i * dst_stride, src + (size_t)ids[i] * src_stride, 4u * n);
+}
+
+void oc_argmax_rows(uint32_t n, uint32_t rows, const float * x, uint64_t x_stride, int32_t * out) {
+    for (uint32_t r = 0; r < rows; ++r) {
+        const float * xr = x + (size_t)r * x_stride;
+        float mx = -INFINITY;
+        int32_t idx = 0;
+        for (uint32_t j = 0; j < n; ++j)
+            if (xr[j] > mx) { mx = xr[j]; idx = (int32_t)j; }
+        out[r] = idx;
+    }
+}

@@ -41,6 +41,7 @@ float oc_fsub(float a, float b) { return out_fix(in_daz(a) - in_daz(b)); }
 float oc_fmul(float a, float b) { return out_fix(in_daz(a) * in_daz(b)); }
 float oc_fdiv(float a, float b) { return out_fix(in_daz(a) / in_daz(b)); }
 float oc_frecip(float a)        { return out_fix(1.0f / in_daz(a)); }
+float oc_fsqrt(float a)         { return out_fix(sqrtf(in_daz(a))); }
 
 /* int32 -> f32 with round-to-nearest-even (sw/sim/tsr_ref.c:107-132). The host's conversion
  * instruction rounds with the default (RNE) mode, which the oracle never changes. */

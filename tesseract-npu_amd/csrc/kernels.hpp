@@ -97,6 +97,19 @@ struct FaArgs {
     ExpkTab ex;
 };
 
+// ROPE over T tokens of n_heads heads (head h of token t at x + t * x_stride + h * head_dim).
+struct RopeArgs {
+    const float * x;
+    uint64_t x_stride;
+    float * y;
+    uint64_t y_stride;
+    const int32_t * pos;     // [T] positions
+    const float * ff;        // nullable: [n_dims / 2] freq factors
+    uint32_t head_dim, n_heads, n_dims, neox;
+    float ts, m, freq_scale; // TS = powf(freq_base, -2 / n_dims); M = attn_factor
+    uint32_t fs;             // freq_scale != 1
+};
+
 }  // namespace tsr
 
 int tsr_launch_qact(const tsr::QactArgs & a, uint32_t T, hipStream_t s);
@@ -112,3 +125,13 @@ int tsr_launch_kv_bytes(const tsr::KvArgs & a, uint32_t which, uint64_t off, uin
 int tsr_launch_kv_set_rows(const tsr::KvArgs & a, uint32_t which, const float * src, uint32_t n_rows,
                            uint64_t src_stride, const int64_t * idx, int32_t * bad, hipStream_t s);
 int tsr_launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, uint32_t n_cu, hipStream_t s);
+int tsr_launch_rms_norm(const float * x, uint64_t x_stride, uint32_t n, uint32_t rows, float eps, float inv_n,
+                        const float * w, uint64_t w_stride, uint32_t w_period, float * y, uint64_t y_stride, hipStream_t s);
+int tsr_launch_rope(const tsr::RopeArgs & a, uint32_t T, hipStream_t s);
+int tsr_launch_swiglu(const float * g, uint64_t g_stride, const float * u, uint64_t u_stride, float * y, uint64_t y_stride,
+                      uint32_t n, uint32_t rows, const tsr::ExpkTab & ex, hipStream_t s);
+int tsr_launch_add(const float * a, uint64_t a_stride, const float * b, uint64_t b_stride, uint32_t b_period, float * y,
+                   uint64_t y_stride, uint32_t n, uint32_t rows, hipStream_t s);
+int tsr_launch_get_rows(const float * src, uint64_t src_stride, uint32_t n, uint32_t n_src, const int32_t * ids,
+                        uint32_t count, float * dst, uint64_t dst_stride, int32_t * bad, hipStream_t s);
+int tsr_launch_argmax(const float * x, uint64_t x_stride, uint32_t n, uint32_t rows, int32_t * out, hipStream_t s);

@@ -31,6 +31,7 @@ EXPORTS = (
     "tsr_hip_qa_bytes", "tsr_hip_qact", "tsr_hip_mul_mat", "tsr_hip_mul_mat_isums",
     "tsr_hip_kv_create", "tsr_hip_kv_free", "tsr_hip_kv_set_bytes", "tsr_hip_kv_get_bytes", "tsr_hip_kv_set_rows",
     "tsr_hip_msum_build_f16", "tsr_hip_flash_attn", "tsr_hip_get_counters",
+    "tsr_hip_rms_norm", "tsr_hip_rope", "tsr_hip_swiglu", "tsr_hip_add", "tsr_hip_get_rows", "tsr_hip_argmax",
 )
 
 
@@ -81,6 +82,13 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "tsr_hip_flash_attn": ([vp, vp, u32, u64, vp, vp, u32, u32, u32, C.c_float, vp, vp, vp, u32, vp, u64, vp],
                                C.c_int),
         "tsr_hip_get_counters": ([vp, vp], C.c_int),
+        "tsr_hip_rms_norm": ([vp, vp, u32, u32, u64, C.c_float, vp, u64, u32, vp, u64, vp], C.c_int),
+        "tsr_hip_rope": ([vp, vp, u32, u64, u32, u32, u32, C.c_int, vp, C.c_float, C.c_float, C.c_float, vp, vp, u64,
+                          vp], C.c_int),
+        "tsr_hip_swiglu": ([vp, vp, u64, vp, u64, u32, u32, vp, u64, vp], C.c_int),
+        "tsr_hip_add": ([vp, vp, u64, vp, u64, u32, u32, u32, vp, u64, vp], C.c_int),
+        "tsr_hip_get_rows": ([vp, vp, u64, u32, u32, vp, u32, vp, u64, vp, vp], C.c_int),
+        "tsr_hip_argmax": ([vp, vp, u32, u32, u64, vp, vp], C.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -297,6 +305,36 @@ class Device:
                                          float(scale), words.ctypes.data, self._p(mask_f32),
                                          None if nr is None else nr.ctypes.data, 0 if nr is None else nr.shape[0],
                                          self._p(out), out_stride, stream), "flash_attn")
+
+    # -- decode-layer glue ops (rows of n f32; strides in floats) -------------------------------------
+    def rms_norm(self, x, n: int, rows: int, x_stride: int, eps: float, y, y_stride: int, w=None, w_stride: int = 0,
+                 w_period: int = 1, stream=None) -> None:
+        _check(self.L.tsr_hip_rms_norm(self.ctx, self._p(x), n, rows, x_stride, float(eps), self._p(w), w_stride,
+                                       w_period, self._p(y), y_stride, stream), "rms_norm")
+
+    def rope(self, x, T: int, x_stride: int, head_dim: int, n_heads: int, n_dims: int, mode: int, pos,
+             freq_base: float, y, y_stride: int, freq_scale: float = 1.0, attn_factor: float = 1.0,
+             freq_factors=None, stream=None) -> None:
+        _check(self.L.tsr_hip_rope(self.ctx, self._p(x), T, x_stride, head_dim, n_heads, n_dims, mode, self._p(pos),
+                                   float(freq_base), float(freq_scale), float(attn_factor), self._p(freq_factors),
+                                   self._p(y), y_stride, stream), "rope")
+
+    def swiglu(self, g, g_stride: int, u, u_stride: int, n: int, rows: int, y, y_stride: int, stream=None) -> None:
+        _check(self.L.tsr_hip_swiglu(self.ctx, self._p(g), g_stride, self._p(u), u_stride, n, rows, self._p(y),
+                                     y_stride, stream), "swiglu")
+
+    def add(self, a, a_stride: int, b, b_stride: int, n: int, rows: int, y, y_stride: int, b_period: int = 1,
+            stream=None) -> None:
+        _check(self.L.tsr_hip_add(self.ctx, self._p(a), a_stride, self._p(b), b_stride, b_period, n, rows,
+                                  self._p(y), y_stride, stream), "add")
+
+    def get_rows(self, src, src_stride: int, n: int, n_src: int, ids, count: int, y, y_stride: int, bad=None,
+                 stream=None) -> None:
+        _check(self.L.tsr_hip_get_rows(self.ctx, self._p(src), src_stride, n, n_src, self._p(ids), count, self._p(y),
+                                       y_stride, self._p(bad), stream), "get_rows")
+
+    def argmax(self, x, n: int, rows: int, x_stride: int, out, stream=None) -> None:
+        _check(self.L.tsr_hip_argmax(self.ctx, self._p(x), n, rows, x_stride, self._p(out), stream), "argmax")
 
     def __del__(self):
         try:

@@ -1,0 +1,68 @@
+"""TEST INFRASTRUCTURE ONLY: the decode step of a Llama-architecture model composed from the CPU
+restatement's ops (oracle.Oracle), for checking the GPU decoder end to end. Only tests/, smoke()
+and bench.py's CPU leg import it.
+
+The op order is the reference's decoder-layer op list (sw/ctrl/tests/test_fw_m7_layer.cpp:646-686,
+non-Gemma branch; each record run by its per-kind reference as sw/ctrl/ref/opl_ref.hpp:1-9 runs a
+list): RMS_NORM+MUL, MUL_MAT Q / K / V, ROPE q and k, SET_ROWS_KV K and V, FLASH_ATTN_EXT (the new
+cell's chunk last), MUL_MAT Wo with the residual addend, RMS_NORM+MUL, MUL_MAT gate / up, SWIGLU,
+MUL_MAT down with the residual addend; then the output norm, the output head and the greedy pick.
+Q, K and V are separate MUL_MATs here (the GPU decoder concatenates their rows; each row's value is
+the same), and q and k are rotated by separate ROPEs."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+class OracleLlama:
+    """tensors: {gguf name: quantized blocks or f32 array}; the same names as tsr_llama.layer_tensors,
+    plus blk.<i>.attn_norm.weight, blk.<i>.ffn_norm.weight, output_norm.weight, output.weight and
+    token_embd.weight (f32 [n_vocab, n_embd])."""
+
+    def __init__(self, oc, *, n_layer, n_embd, n_ff, n_head, n_head_kv, head_dim, n_vocab, eps, rope_base,
+                 rope_mode, wfmt, ofmt, tensors, kv_size):
+        self.oc = oc
+        self.n_layer, self.n_embd, self.n_ff = n_layer, n_embd, n_ff
+        self.n_head, self.n_head_kv, self.D, self.n_vocab = n_head, n_head_kv, head_dim, n_vocab
+        self.eps, self.rope_base, self.neox = eps, rope_base, rope_mode != 0
+        self.wfmt, self.ofmt, self.t = wfmt, ofmt, tensors
+        self.E = n_head_kv * head_dim
+        rb = self.E // 32 * 34
+        self.kc = [np.zeros((kv_size, rb), np.uint8) for _ in range(n_layer)]
+        self.vc = [np.zeros((kv_size, rb), np.uint8) for _ in range(n_layer)]
+        self.kv_size = kv_size
+        self.scale = np.float32(1.0 / math.sqrt(head_dim))
+
+    def set_history(self, il: int, which: int, rows) -> None:
+        cache = self.kc[il] if which == 0 else self.vc[il]
+        self.oc.kv_set_rows(cache, rows, np.arange(rows.shape[0], dtype=np.int64))
+
+    def step(self, token: int, pos: int, ts: np.float32, n_kv: int) -> np.ndarray:
+        """Logits [n_vocab] of the token at position pos; ts = powf(rope_base, -2 / head_dim)."""
+        oc, t, D = self.oc, self.t, self.D
+        x = oc.get_rows(t["token_embd.weight"], np.array([token], np.int32))
+        msum = np.zeros(12, np.uint32)
+        msum[0], msum[1], msum[2], msum[9] = 0x4D55534D, 1, n_kv, pos + 1
+        runs = np.array([[pos, pos + 1]], np.uint32)
+        posv = np.array([pos], np.int32)
+        for il in range(self.n_layer):
+            b = f"blk.{il}."
+            xn = oc.rms_norm(x, self.eps, t[b + "attn_norm.weight"])
+            q = oc.mul_mat(self.wfmt, t[b + "attn_q.weight"], self.n_embd, xn)
+            k = oc.mul_mat(self.wfmt, t[b + "attn_k.weight"], self.n_embd, xn)
+            v = oc.mul_mat(self.wfmt, t[b + "attn_v.weight"], self.n_embd, xn)
+            q = oc.rope(q, posv, D, D, self.neox, ts)
+            k = oc.rope(k, posv, D, D, self.neox, ts)
+            oc.kv_set_rows(self.kc[il], k, np.array([pos], np.int64))
+            oc.kv_set_rows(self.vc[il], v, np.array([pos], np.int64))
+            a = oc.flash_attn(q, self.kc[il], self.vc[il], D, self.n_head, self.n_head_kv, float(self.scale), msum,
+                              new_runs=runs)
+            h = oc.mul_mat(self.wfmt, t[b + "attn_output.weight"], self.n_head * D, a, add=x)
+            hn = oc.rms_norm(h, self.eps, t[b + "ffn_norm.weight"])
+            g = oc.mul_mat(self.wfmt, t[b + "ffn_gate.weight"], self.n_embd, hn)
+            u = oc.mul_mat(self.wfmt, t[b + "ffn_up.weight"], self.n_embd, hn)
+            x = oc.mul_mat(self.wfmt, t[b + "ffn_down.weight"], self.n_ff, oc.swiglu(g, u), add=h)
+        xn = oc.rms_norm(x, self.eps, t["output_norm.weight"])
+        return oc.mul_mat(self.ofmt, t["output.weight"], self.n_embd, xn)[0]

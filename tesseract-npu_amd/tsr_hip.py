@@ -22,6 +22,7 @@ FMT_Q8_0, FMT_Q4_K = 0, 1
 QA_A32, QA_A256 = 0, 1
 KV_K, KV_V = 0, 1
 MM_ACC_DST = 1
+ROPE_NORMAL, ROPE_NEOX, ROPE_IMROPE = 0, 2, 40
 
 # the exported symbols of include/tsr_hip.h
 EXPORTS = (

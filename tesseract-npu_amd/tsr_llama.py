@@ -1,0 +1,234 @@
+"""A Llama-architecture decoder built from libtsr_hip's C-ABI ops: the caller side of the hot path,
+in the role llama.cpp's build_llama graph plays for the reference's backend.
+
+One decode step (T = 1) runs the op list of the reference's decoder-layer test
+(sw/ctrl/tests/test_fw_m7_layer.cpp:646-686, the non-Gemma branch), layer by layer:
+
+    Xn  = RMS_NORM(X) * attn_norm                     (RMS_NORM + MUL)
+    Q|K|V = MUL_MAT(Wq|Wk|Wv, Xn)                     (one launch over the concatenated rows)
+    Q, K  = ROPE(Q), ROPE(K)                          (one launch over the q and k heads)
+    SET_ROWS_KV(K cache, K, pos), SET_ROWS_KV(V cache, V, pos)
+    A   = FLASH_ATTN_EXT(Q, K cache, V cache, cells [0, pos], new cell pos), scale 1/sqrt(D)
+    H   = MUL_MAT(Wo, A) + X                          (MUL_MAT with the residual addend)
+    Hn  = RMS_NORM(H) * ffn_norm
+    G|U = MUL_MAT(Wgate|Wup, Hn)                      (one launch over the concatenated rows)
+    X   = MUL_MAT(Wdown, SWIGLU(G, U)) + H
+
+then logits = MUL_MAT(Woutput, RMS_NORM(X) * output_norm) and the greedy token is the ARGMAX.
+The token embedding is a GET_ROWS of an f32 table. Row concatenation leaves every row's result
+unchanged (each output row is its own dot product with the same quantized activation), and ROPE
+of q and k heads in one launch is the same per-head rotation. A residual addend is one FA(add, v),
+the ADD of the reference's fused "attn_out + inpSA" / "ffn_out + ffn_inp" records.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, replace
+
+import numpy as np
+
+import tsr_hip as H
+import tsr_synth as S
+
+
+@dataclass(frozen=True)
+class LlamaConfig:
+    name: str
+    n_layer: int
+    n_embd: int
+    n_ff: int
+    n_head: int
+    n_head_kv: int
+    head_dim: int
+    n_vocab: int
+    eps: float = 1e-5
+    rope_base: float = 500000.0
+    rope_mode: int = H.ROPE_NORMAL
+    wfmt: int = H.FMT_Q4_K           # layer weights
+    ofmt: int = H.FMT_Q4_K           # output head
+    std: float = 0.02
+
+    @property
+    def E(self) -> int:
+        return self.n_head_kv * self.head_dim
+
+    @property
+    def n_q(self) -> int:
+        return self.n_head * self.head_dim
+
+    def weight_bytes_per_token(self) -> int:
+        """Quantized weight bytes one decode token reads (layers + output head), ggml block sizes."""
+        def qb(fmt, N, K):
+            return N * (K // 32 * 34 if fmt == H.FMT_Q8_0 else K // 256 * 144)
+        per_layer = (qb(self.wfmt, self.n_q + 2 * self.E, self.n_embd) + qb(self.wfmt, self.n_embd, self.n_q) +
+                     qb(self.wfmt, 2 * self.n_ff, self.n_embd) + qb(self.wfmt, self.n_embd, self.n_ff))
+        return self.n_layer * per_layer + qb(self.ofmt, self.n_vocab, self.n_embd)
+
+
+LLAMA3_8B = LlamaConfig("llama3-8b", 32, 4096, 14336, 32, 8, 128, 128256)
+
+
+def tensor_seed(cfg: LlamaConfig, name: str) -> int:
+    return S.seed_of(cfg.name, name)
+
+
+def layer_tensors(cfg: LlamaConfig, il: int):
+    """(name, N, K) of the quantized tensors of layer il, in ggml's GGUF names."""
+    d, q, E, ff = cfg.n_embd, cfg.n_q, cfg.E, cfg.n_ff
+    return [(f"blk.{il}.attn_q.weight", q, d), (f"blk.{il}.attn_k.weight", E, d), (f"blk.{il}.attn_v.weight", E, d),
+            (f"blk.{il}.attn_output.weight", d, q), (f"blk.{il}.ffn_gate.weight", ff, d),
+            (f"blk.{il}.ffn_up.weight", ff, d), (f"blk.{il}.ffn_down.weight", d, ff)]
+
+
+class SyntheticWeights:
+    """Seeded random-init weights: every quantized tensor is normal(seed_of(config, name), std) rows
+    quantized to the config's format; norms are f32 N(1, 0.1); the token embedding is f32 N(0, 1)
+    rows (the lookup copies rows bit for bit). Values depend only on (config name, tensor name)."""
+
+    def __init__(self, cfg: LlamaConfig):
+        self.cfg = cfg
+
+    def quant(self, name: str, N: int, K: int, fmt: int) -> np.ndarray:
+        return S.quant_rows(fmt, tensor_seed(self.cfg, name), N, K, self.cfg.std)
+
+    def norm(self, name: str) -> np.ndarray:
+        return (1.0 + S.normal(tensor_seed(self.cfg, name), self.cfg.n_embd, 0.1)).astype(np.float32)
+
+    def embedding(self) -> np.ndarray:
+        c = self.cfg
+        return S.normal(tensor_seed(c, "token_embd.weight"), c.n_vocab * c.n_embd, 1.0).reshape(c.n_vocab, c.n_embd)
+
+    def kv_history(self, il: int, which: int, n: int) -> np.ndarray:
+        """f32 rows [n, E] quantized into cells 0 .. n-1 before decoding (the prefilled context)."""
+        c = self.cfg
+        return S.normal(tensor_seed(c, f"kv_history.{il}.{which}"), n * c.E, 1.0).reshape(n, c.E)
+
+
+def msum_decode(pos: int, n_kv: int) -> np.ndarray:
+    """MSUM words of a one-row decode mask that sees cells [0, pos] of a mask n_kv cells wide (llama.cpp's
+    kq_mask: 0 over the used cells, -inf elsewhere), the form tsr_hip_msum_build_f16 gives."""
+    w = np.zeros(12, np.uint32)
+    w[0], w[1], w[2] = 0x4D55534D, 1, n_kv
+    w[8], w[9] = 0, pos + 1
+    return w
+
+
+class LlamaDecoder:
+    """The model on one device: weights uploaded once, one q8_0 K and V cache per layer of kv_size
+    cells, and the activation buffers of one decode token."""
+
+    def __init__(self, dev: H.Device, cfg: LlamaConfig, weights: SyntheticWeights, kv_size: int):
+        self.dev, self.cfg, self.kv_size = dev, cfg, kv_size
+        c = cfg
+        f4 = 4
+        self.tok_embd = dev.upload(np.ascontiguousarray(weights.embedding(), np.float32))
+        self.layers = []
+        for il in range(c.n_layer):
+            t = {name.split(".")[2]: weights.quant(name, N, K, c.wfmt) for name, N, K in layer_tensors(c, il)}
+            L = {
+                "attn_norm": dev.upload(weights.norm(f"blk.{il}.attn_norm.weight")),
+                "ffn_norm": dev.upload(weights.norm(f"blk.{il}.ffn_norm.weight")),
+                "wqkv": dev.weight(c.wfmt, np.concatenate([t["attn_q"], t["attn_k"], t["attn_v"]]), c.n_q + 2 * c.E,
+                                   c.n_embd),
+                "wo": dev.weight(c.wfmt, t["attn_output"], c.n_embd, c.n_q),
+                "wgu": dev.weight(c.wfmt, np.concatenate([t["ffn_gate"], t["ffn_up"]]), 2 * c.n_ff, c.n_embd),
+                "wd": dev.weight(c.wfmt, t["ffn_down"], c.n_embd, c.n_ff),
+                "kc": dev.kv(c.E, kv_size),
+                "vc": dev.kv(c.E, kv_size),
+            }
+            del t
+            self.layers.append(L)
+        self.out_norm = dev.upload(weights.norm("output_norm.weight"))
+        self.wout = dev.weight(c.ofmt, weights.quant("output.weight", c.n_vocab, c.n_embd, c.ofmt), c.n_vocab, c.n_embd)
+        # activations of one token
+        self.x = dev.alloc(c.n_embd * f4)
+        self.h = dev.alloc(c.n_embd * f4)
+        self.xn = dev.alloc(c.n_embd * f4)
+        self.qkv = dev.alloc((c.n_q + 2 * c.E) * f4)
+        self.att = dev.alloc(c.n_q * f4)
+        self.gu = dev.alloc(2 * c.n_ff * f4)
+        self.glu = dev.alloc(c.n_ff * f4)
+        self.logits = dev.alloc(c.n_vocab * f4)
+        self.tok = dev.alloc(4)            # int32 token id of the step (GET_ROWS ids)
+        self.next = dev.alloc(4)           # int32 greedy token (ARGMAX)
+        self.pos = dev.alloc(4)            # int32 position (ROPE)
+        self.cell = dev.alloc(8)           # int64 cell (SET_ROWS_KV)
+        self.bad = dev.alloc(4).fill(0)
+        self.scale = 1.0 / math.sqrt(c.head_dim)
+
+    def prefill_history(self, weights: SyntheticWeights, n: int) -> None:
+        """Cells 0 .. n-1 of every cache hold QACT'd rows of weights.kv_history (SET_ROWS_KV)."""
+        idx = self.dev.upload(np.arange(n, dtype=np.int64))
+        for il, L in enumerate(self.layers):
+            for which, kv in ((0, L["kc"]), (1, L["vc"])):
+                rows = self.dev.upload(np.ascontiguousarray(weights.kv_history(il, which, n), np.float32))
+                self.dev.kv_set_rows(kv, which, rows, n, self.cfg.E, idx, self.bad)
+                rows.free()
+        self.dev.sync()
+
+    def step(self, token: int | None, pos: int, n_kv: int | None = None, stream=None) -> None:
+        """One decode token at position pos (cell pos). token: the id to embed, or None to embed the
+        previous step's greedy token (left on the device). Logits end in self.logits, the greedy token
+        in self.next. n_kv: the mask width (default: pos + 1 rounded up to 256, at most kv_size)."""
+        c, d = self.cfg, self.dev
+        if not 0 <= pos < self.kv_size:
+            raise ValueError(f"position {pos} outside the cache of {self.kv_size} cells")
+        if token is not None:
+            self.tok.write(np.array([token], np.int32))
+        else:
+            self.tok.write(self.next.read(np.int32, (1,)))
+        self.pos.write(np.array([pos], np.int32))
+        self.cell.write(np.array([pos], np.int64))
+        if n_kv is None:
+            n_kv = min(self.kv_size, (pos + 1 + 255) // 256 * 256)
+        msum = msum_decode(pos, n_kv)
+        runs = np.array([[pos, pos + 1]], np.uint32)
+        nq, E, n = c.n_q, c.E, c.n_embd
+        f4 = 4
+        d.get_rows(self.tok_embd, n, n, c.n_vocab, self.tok, 1, self.x, n, bad=self.bad, stream=stream)
+        for L in self.layers:
+            d.rms_norm(self.x, n, 1, n, c.eps, self.xn, n, w=L["attn_norm"], w_stride=n, stream=stream)
+            d.mul_mat(L["wqkv"], self.xn, 1, n, self.qkv, nq + 2 * E, stream=stream)
+            d.rope(self.qkv, 1, nq + 2 * E, c.head_dim, c.n_head + c.n_head_kv, c.head_dim, c.rope_mode, self.pos,
+                   c.rope_base, self.qkv, nq + 2 * E, stream=stream)
+            d.kv_set_rows(L["kc"], 0, self.qkv.ptr + nq * f4, 1, E, self.cell, self.bad, stream=stream)
+            d.kv_set_rows(L["vc"], 1, self.qkv.ptr + (nq + E) * f4, 1, E, self.cell, self.bad, stream=stream)
+            d.flash_attn(self.qkv, 1, nq + 2 * E, L["kc"], L["vc"], c.head_dim, c.n_head, c.n_head_kv, self.scale,
+                         msum, self.att, nq, new_runs=runs, stream=stream)
+            d.mul_mat(L["wo"], self.att, 1, nq, self.h, n, add=self.x, add_stride=n, stream=stream)
+            d.rms_norm(self.h, n, 1, n, c.eps, self.xn, n, w=L["ffn_norm"], w_stride=n, stream=stream)
+            d.mul_mat(L["wgu"], self.xn, 1, n, self.gu, 2 * c.n_ff, stream=stream)
+            d.swiglu(self.gu, 2 * c.n_ff, self.gu.ptr + c.n_ff * f4, 2 * c.n_ff, c.n_ff, 1, self.glu, c.n_ff,
+                     stream=stream)
+            d.mul_mat(L["wd"], self.glu, 1, c.n_ff, self.x, n, add=self.h, add_stride=n, stream=stream)
+        d.rms_norm(self.x, n, 1, n, c.eps, self.xn, n, w=self.out_norm, w_stride=n, stream=stream)
+        d.mul_mat(self.wout, self.xn, 1, n, self.logits, c.n_vocab, stream=stream)
+        d.argmax(self.logits, c.n_vocab, 1, c.n_vocab, self.next, stream=stream)
+
+    def read_logits(self) -> np.ndarray:
+        self.dev.sync()
+        return self.logits.read(np.float32, (self.cfg.n_vocab,))
+
+    def read_next(self) -> int:
+        self.dev.sync()
+        return int(self.next.read(np.int32, (1,))[0])
+
+    def generate(self, first_token: int, pos0: int, n_tokens: int) -> list[int]:
+        """Greedy decode of n_tokens from first_token at pos0 (the previous token fed back on the device)."""
+        out = []
+        for i in range(n_tokens):
+            self.step(first_token if i == 0 else None, pos0 + i)
+            out.append(self.read_next())
+        return out
+
+    def free(self) -> None:
+        for L in self.layers:
+            for k in ("wqkv", "wo", "wgu", "wd", "kc", "vc"):
+                L[k].free()
+        self.wout.free()
+
+
+def tiny_config(name: str = "tiny-llama", **kw) -> LlamaConfig:
+    """A small model with every shape rule of the 8B one (for parity tests and smoke runs)."""
+    base = LlamaConfig(name, n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, head_dim=64, n_vocab=384)
+    return replace(base, **kw)

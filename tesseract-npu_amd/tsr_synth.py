@@ -32,6 +32,8 @@ def _lib():
             raise FileNotFoundError(f"{path} is not built: run `make -C {_os.path.dirname(path)}`")
         _LIB = _C.CDLL(path)
         _LIB.tsr_synth_normal.argtypes = [_C.c_uint64, _C.c_uint64, _C.c_uint64, _C.c_float, _C.c_void_p]
+        _LIB.tsr_synth_quant.argtypes = [_C.c_int, _C.c_uint64, _C.c_uint64, _C.c_uint64, _C.c_uint64, _C.c_float,
+                                         _C.c_void_p]
     return _LIB
 
 
@@ -40,6 +42,16 @@ def normal(seed: int, n: int, std: float = 1.0, start: int = 0) -> np.ndarray:
     stream (synth/tsr_synth.c). Values depend only on (seed, index)."""
     out = np.empty(n, np.float32)
     _lib().tsr_synth_normal(seed & _M64, start, n, std, out.ctypes.data)
+    return out
+
+
+def quant_rows(fmt: int, seed: int, N: int, K: int, std: float = 0.02, r0: int = 0) -> np.ndarray:
+    """Rows r0 .. r0+N-1 of normal(seed, *, std) as [*, K], quantized to Q8_0 (fmt 0) or Q4_K (fmt 1):
+    bit for bit quantize_q8_0 / quantize_q4_k of normal(seed, ...) rows, computed in C on 16 threads."""
+    bs, bb = (256, 144) if fmt else (32, 34)
+    out = np.empty((N, K // bs * bb), np.uint8)
+    if _lib().tsr_synth_quant(fmt, seed & _M64, K, r0, N, std, out.ctypes.data) != 0:
+        raise ValueError(f"quant_rows: K={K} is not a multiple of {bs} (or > 32768)")
     return out
 
 

@@ -77,3 +77,12 @@ def test_quantizers_round_trip():
     assert q4.shape == (64, 4 * 144)
     err4 = np.abs(S.dequantize_q4_k(q4, 1024) - w).max()
     assert err4 <= 2.0 * np.abs(w).max() / 15.0 * 1.05
+
+
+@pytest.mark.parametrize("fmt,N,K,seed", [(1, 64, 4096, 5), (1, 9, 14336, 9), (0, 100, 896, 3), (0, 7, 4096, 11)])
+def test_c_quantizer_matches_numpy(fmt, N, K, seed):
+    """The threaded C quantizer (synth/tsr_synth.c) writes the bytes of quantize_q4_k / quantize_q8_0."""
+    w = S.normal(seed, N * K, 0.02).reshape(N, K)
+    want = S.quantize_q4_k(w) if fmt else S.quantize_q8_0(w)
+    assert (S.quant_rows(fmt, seed, N, K) == want).all()
+    assert (S.quant_rows(fmt, seed, 3, K, r0=2) == want[2:5]).all()

@@ -1,0 +1,67 @@
+"""End-to-end decode on the GPU (tsr_llama.LlamaDecoder over the C ABI) against the same decode
+composed from the oracle's ops (oracle/oracle_llama.py): logits bit for bit at every step and the
+same greedy tokens, on small models with the 8B model's shape rules."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import tsr_hip as H
+import tsr_llama as LL
+from helpers import assert_bits_equal
+from oracle_llama import OracleLlama
+
+pytestmark = pytest.mark.gpu
+
+_libm = C.CDLL("libm.so.6")
+_libm.powf.argtypes = [C.c_float, C.c_float]
+_libm.powf.restype = C.c_float
+
+
+def oracle_model(oc, cfg, w, kv_size, hist):
+    t = {"token_embd.weight": w.embedding(), "output_norm.weight": w.norm("output_norm.weight")[None],
+         "output.weight": w.quant("output.weight", cfg.n_vocab, cfg.n_embd, cfg.ofmt)}
+    for il in range(cfg.n_layer):
+        for name, N, K in LL.layer_tensors(cfg, il):
+            t[name] = w.quant(name, N, K, cfg.wfmt)
+        for nm in ("attn_norm", "ffn_norm"):
+            t[f"blk.{il}.{nm}.weight"] = w.norm(f"blk.{il}.{nm}.weight")[None]
+    m = OracleLlama(oc, n_layer=cfg.n_layer, n_embd=cfg.n_embd, n_ff=cfg.n_ff, n_head=cfg.n_head,
+                    n_head_kv=cfg.n_head_kv, head_dim=cfg.head_dim, n_vocab=cfg.n_vocab, eps=cfg.eps,
+                    rope_base=cfg.rope_base, rope_mode=cfg.rope_mode, wfmt=cfg.wfmt, ofmt=cfg.ofmt, tensors=t,
+                    kv_size=kv_size)
+    for il in range(cfg.n_layer):
+        for which in (0, 1):
+            m.set_history(il, which, w.kv_history(il, which, hist))
+    return m
+
+
+@pytest.mark.parametrize("cfg,kv_size,hist,n_steps", [
+    (LL.tiny_config(), 512, 100, 5),
+    (LL.tiny_config("tiny-qwen", wfmt=H.FMT_Q8_0, ofmt=H.FMT_Q8_0, rope_mode=H.ROPE_NEOX, eps=1e-6,
+                    rope_base=1000000.0), 640, 300, 4),
+    (LL.tiny_config("tiny-gqa8", n_head=8, n_head_kv=1, head_dim=128, n_embd=512, n_ff=768, n_vocab=1000), 300, 255, 3),
+], ids=["q4k-norm", "q80-neox", "gqa8-d128"])
+def test_decode_matches_oracle(dev, oc, cfg, kv_size, hist, n_steps):
+    w = LL.SyntheticWeights(cfg)
+    print(f"\ndecode parity {cfg.name}: kv {kv_size} history {hist} steps {n_steps}", flush=True)
+    gpu = LL.LlamaDecoder(dev, cfg, w, kv_size)
+    gpu.prefill_history(w, hist)
+    ref = oracle_model(oc, cfg, w, kv_size, hist)
+    ts = np.float32(_libm.powf(float(np.float32(cfg.rope_base)), float(np.float32(-2.0) / np.float32(cfg.head_dim))))
+    tok = 7
+    for i in range(n_steps):
+        pos = hist + i
+        n_kv = min(kv_size, (pos + 1 + 255) // 256 * 256)
+        gpu.step(tok if i == 0 else None, pos)
+        got = gpu.read_logits()
+        want = ref.step(tok, pos, ts, n_kv)
+        assert_bits_equal(got, want, f"{cfg.name} step {i} (pos {pos})")
+        nxt = gpu.read_next()
+        assert nxt == int(oc.argmax(want[None])[0])
+        tok = nxt
+    for il in range(cfg.n_layer):                                 # the caches hold the same bytes
+        assert (gpu.layers[il]["kc"].get_bytes(0).reshape(kv_size, -1) == ref.kc[il]).all()
+        assert (gpu.layers[il]["vc"].get_bytes(1).reshape(kv_size, -1) == ref.vc[il]).all()
+    assert gpu.bad.read(np.int32, (1,))[0] == 0
+    gpu.free()

@@ -147,3 +147,11 @@ def test_mul_mat_errors(dev):
     with pytest.raises(tsr_hip.TsrHipError) as e:
         dev.weight(7, np.zeros(144, np.uint8), 1, 256)
     assert e.value.code == -7
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_mul_mat_vocab_head(dev, oc, fmt):
+    """The output head of a Llama-3-8B-shaped model: 128256 rows x 4096 (the most rows per block)."""
+    N, K = 128256, 4096
+    got, want = _mm_case(dev, oc, fmt, N, K, seed=9, wblocks=S.quant_rows(fmt, 77, N, K))
+    assert_bits_equal(got, want, f"fmt {fmt} {N}x{K}")

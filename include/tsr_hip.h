@@ -78,6 +78,14 @@ int tsr_hip_alloc(tsr_hip_ctx * ctx, size_t bytes, void ** dev_out);
 int tsr_hip_free(tsr_hip_ctx * ctx, void * dev);
 int tsr_hip_write(tsr_hip_ctx * ctx, void * dst_dev, const void * src, size_t bytes);
 int tsr_hip_read(tsr_hip_ctx * ctx, void * dst, const void * src_dev, size_t bytes);
+/* A host-to-device copy ordered on `stream` that does not wait: the bytes are taken at the call (src
+ * may be reused at once) into pinned staging, from which the device copy reads. bytes <= 16384. Not
+ * under graph capture. (The backend's set_tensor for small per-token inputs, positions and ids,
+ * ggml-tesseract.cpp:1905-1945, without a device wait.) */
+int tsr_hip_write_async(tsr_hip_ctx * ctx, void * dst_dev, const void * src, size_t bytes, void * stream);
+/* A device-to-device copy ordered on `stream` (the backend's cpy_tensor between its own buffers,
+ * ggml-tesseract.cpp:2026-2042). */
+int tsr_hip_copy_async(tsr_hip_ctx * ctx, void * dst_dev, const void * src_dev, size_t bytes, void * stream);
 int tsr_hip_memset(tsr_hip_ctx * ctx, void * dst_dev, int value, size_t bytes);
 
 /* ---- weights ---------------------------------------------------------------------------------
@@ -140,6 +148,40 @@ int tsr_hip_kv_get_bytes(tsr_hip_ctx * ctx, const tsr_hip_kv * kv, uint32_t whic
  * out-of-range index stores nothing and sets *bad_dev if bad_dev is not NULL). */
 int tsr_hip_kv_set_rows(tsr_hip_ctx * ctx, tsr_hip_kv * kv, uint32_t which, const float * src_dev, uint32_t n_rows,
                         uint64_t src_stride, const int64_t * idx_dev, int32_t * bad_dev, void * stream);
+
+/* ---- FA plans ------------------------------------------------------------------------------------
+ * The work list of FLASH_ATTN_EXT kept in device memory, so that graphs of planned launches replay
+ * over masks that change between replays (a decode token per replay): the backend's per-graph plan
+ * cache (ggml-tesseract.cpp:3937-3952, 3768-3779) with the FA record's chunk plan refreshed per call.
+ *   create   for T query rows of D / n_head / n_head_kv over caches of at most kv_size cells
+ *   set      plans the MSUM (and new_runs, as tsr_hip_flash_attn) on the host and copies the list to
+ *            the device in stream order (not under capture). *shape_changed = 1 when the list's shape
+ *            (items, tiles per item, groups per item, GENERAL) differs from the previous set: launches
+ *            captured before then must be captured again. mask_f32 != 0: an f32 mask copy will be given.
+ *   flash_attn_plan  FLASH_ATTN_EXT with the plan's current list (capturable; numerics as
+ *            tsr_hip_flash_attn). The plan's partials live in the plan: launches that use one plan run
+ *            in stream order, one at a time. */
+typedef struct tsr_hip_fa_plan tsr_hip_fa_plan;
+int tsr_hip_fa_plan_create(tsr_hip_ctx * ctx, uint32_t D, uint32_t n_head, uint32_t n_head_kv, uint32_t T,
+                           uint32_t kv_size, tsr_hip_fa_plan ** out);
+int tsr_hip_fa_plan_set(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan, const uint32_t * msum, int mask_f32,
+                        const uint32_t (*new_runs)[2], uint32_t n_new, int * shape_changed, void * stream);
+int tsr_hip_flash_attn_plan(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const float * q_dev, uint64_t q_stride,
+                            const tsr_hip_kv * kc, const tsr_hip_kv * vc, float scale, const float * mask_f32_dev,
+                            float * out_dev, uint64_t out_stride, void * stream);
+int tsr_hip_fa_plan_free(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan);
+
+/* ---- graphs -------------------------------------------------------------------------------------
+ * Every launch the library makes on `stream` between begin and end is recorded (stream capture) and
+ * replayed by one launch: one decode token per replay (the backend's one op list per token,
+ * sw/ctrl/ref/opl_ref.hpp:1-9). The stream must not be the null stream. Entry points that copy from
+ * the host or allocate (tsr_hip_write, _write_async, _fa_plan_set, a first FA or prefill call that
+ * grows the scratch) refuse to run under capture. */
+typedef struct tsr_hip_graph tsr_hip_graph;
+int tsr_hip_graph_begin(tsr_hip_ctx * ctx, void * stream);
+int tsr_hip_graph_end(tsr_hip_ctx * ctx, void * stream, tsr_hip_graph ** out);
+int tsr_hip_graph_launch(tsr_hip_ctx * ctx, const tsr_hip_graph * graph, void * stream);
+int tsr_hip_graph_free(tsr_hip_ctx * ctx, tsr_hip_graph * graph);
 
 /* ---- mask summary (the backend's MSUM producer, tsr_msum_build_f16 sw/sim/tsr_ref_at.c:646-693) --
  * words: 8 + 4 * n_q uint32 (host). Returns the flags word (bit 0 GENERAL) or a negative code. */

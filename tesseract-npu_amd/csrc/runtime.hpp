@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstring>
 #include <mutex>
 
 #include "kernels.hpp"
@@ -62,6 +63,53 @@ struct tsr_scratch {
     }
 };
 
+// Pinned host staging for stream-ordered host-to-device copies whose source the caller may reuse at
+// once: the bytes are copied into a slot at the call, and the device copy reads the slot. A slot is
+// reused only after the copy that last read it has run (its event), so the host can run up to kSlots
+// copies ahead of the device. Not usable under graph capture (a slot's contents change per call).
+struct tsr_staging {
+    static constexpr uint32_t kSlots = 64, kSlotBytes = 16384;
+    uint8_t * host = nullptr;
+    hipEvent_t ev[kSlots] = {};
+    bool used[kSlots] = {};
+    uint32_t next = 0;
+    int copy(void * dst_dev, const void * src, size_t bytes, hipStream_t s) {
+        if (bytes > kSlotBytes) return TSR_HIP_E_RANGE;
+        if (host == nullptr) {
+            int rc = tsr::hip_err(hipHostMalloc((void **)&host, (size_t)kSlots * kSlotBytes, hipHostMallocDefault),
+                                  "hipHostMalloc staging");
+            for (uint32_t i = 0; rc == 0 && i < kSlots; ++i)
+                rc = tsr::hip_err(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming), "hipEventCreate");
+            if (rc) { release(); return rc; }
+        }
+        const uint32_t k = next;
+        next = (next + 1u) % kSlots;
+        if (used[k]) {
+            const int rc = tsr::hip_err(hipEventSynchronize(ev[k]), "hipEventSynchronize staging");
+            if (rc) return rc;
+        }
+        uint8_t * slot = host + (size_t)k * kSlotBytes;
+        memcpy(slot, src, bytes);
+        int rc = tsr::hip_err(hipMemcpyAsync(dst_dev, slot, bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync staging");
+        if (rc == 0) rc = tsr::hip_err(hipEventRecord(ev[k], s), "hipEventRecord staging");
+        used[k] = rc == 0;
+        return rc;
+    }
+    void release() {
+        for (uint32_t i = 0; i < kSlots; ++i) {
+            if (ev[i]) (void)hipEventSynchronize(ev[i]);
+        }
+        for (uint32_t i = 0; i < kSlots; ++i) {
+            if (ev[i]) (void)hipEventDestroy(ev[i]);
+            ev[i] = nullptr;
+            used[i] = false;
+        }
+        if (host) (void)hipHostFree(host);
+        host = nullptr;
+        next = 0;
+    }
+};
+
 struct tsr_hip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -70,6 +118,7 @@ struct tsr_hip_ctx {
     char name[128] = {0};
     tsr_hip_counters ctr{};
     tsr_scratch scratch;
+    tsr_staging staging;
     tsr::ExpkTab expk{};
     hipStream_t pick(void * s) const { return s ? (hipStream_t)s : stream; }
 };

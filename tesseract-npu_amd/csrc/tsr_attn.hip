@@ -213,6 +213,85 @@ bool plan_row(uint32_t E, uint32_t D, const uint32_t * words, uint32_t q, const 
 
 size_t up256(size_t x) { return (x + 255u) & ~(size_t)255u; }
 
+// The shape checks FLASH_ATTN_EXT makes on its operands (the planned and the unplanned entry points).
+int fa_check_shape(uint32_t D, uint32_t n_head, uint32_t n_head_kv, float scale) {
+    if (!(D == 64u || D == 128u || D == 256u || D == 512u)) return TSR_HIP_E_SHAPE;
+    if (n_head_kv == 0u || n_head % n_head_kv != 0u || n_head / n_head_kv > 64u) return TSR_HIP_E_SHAPE;
+    const uint32_t E = n_head_kv * D, G = n_head / n_head_kv, K = n_head * D;
+    if (E / 64u > 511u || (uint64_t)G * E > 32768u || K > 32768u) return TSR_HIP_E_SHAPE;
+    uint32_t sb;
+    memcpy(&sb, &scale, 4);
+    if ((sb >> 31) || (sb & 0x7F800000u) == 0u || (sb & 0x7F800000u) == 0x7F800000u) return TSR_HIP_E_SHAPE;
+    return TSR_HIP_OK;
+}
+
+// The work list of one call: every token row planned, flattened into items (chunks) with their
+// 256-cell score tiles; tok = tok_first[T] | tok_count[T].
+struct FaWork {
+    std::vector<tsr::FaItem> items;
+    std::vector<uint32_t> tok;
+    uint64_t cells = 0;
+    uint32_t n_tiles = 0, maxtiles = 1, max_groups = 0;
+};
+
+int fa_plan_rows(uint32_t E, uint32_t D, uint32_t T, const uint32_t * msum, const uint32_t (*new_runs)[2], uint32_t n_new,
+                 bool have_mask, FaWork & w) {
+    w.items.clear();
+    w.tok.assign(2u * (size_t)T, 0u);
+    w.cells = 0;
+    w.n_tiles = 0;
+    w.maxtiles = 1;
+    w.max_groups = 0;
+    std::vector<Chunk> ch;
+    for (uint32_t t = 0; t < T; ++t) {
+        ch.clear();
+        if (!plan_row(E, D, msum, t, new_runs, n_new, ch)) return TSR_HIP_E_MASK;
+        w.tok[t] = (uint32_t)w.items.size();
+        w.tok[T + t] = (uint32_t)ch.size();
+        for (const Chunk & c : ch) {
+            if (c.general && !have_mask) return TSR_HIP_E_MASK;
+            tsr::FaItem it{};
+            it.t = t;
+            it.u0 = c.u0;
+            it.n = c.n;
+            it.c_lo = c.c_lo;
+            it.c_hi = c.c_hi;
+            it.general = c.general;
+            it.s_off = (uint32_t)w.cells;
+            it.tile0 = w.n_tiles;
+            it.ntiles = (16u * c.n + 255u) / 256u;
+            w.n_tiles += it.ntiles;
+            w.maxtiles = std::max(w.maxtiles, it.ntiles);
+            w.max_groups = std::max(w.max_groups, c.n);
+            w.cells += 16u * c.n;
+            w.items.push_back(it);
+        }
+    }
+    return TSR_HIP_OK;
+}
+
+tsr::FaArgs fa_args(tsr_hip_ctx * ctx, const float * q_dev, uint64_t q_stride, const tsr_hip_kv * kc,
+                    const tsr_hip_kv * vc, uint32_t D, uint32_t n_head, uint32_t n_head_kv, float scale,
+                    const float * mask_f32_dev, uint32_t mstride, float * out_dev, uint64_t out_stride) {
+    tsr::FaArgs a{};
+    a.q = q_dev;
+    a.q_stride = q_stride;
+    a.kc = kv_args(kc);
+    a.vc = kv_args(vc);
+    a.D = D;
+    a.G = n_head / n_head_kv;
+    a.n_head = n_head;
+    a.n_head_kv = n_head_kv;
+    a.E = n_head_kv * D;
+    a.scale = scale;
+    a.mask = mask_f32_dev;
+    a.mstride = mstride;
+    a.out = out_dev;
+    a.out_stride = out_stride;
+    a.ex = ctx->expk;
+    return a;
+}
+
 }  // namespace
 
 int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint64_t q_stride, const tsr_hip_kv * kc,
@@ -222,99 +301,56 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     if (ctx == nullptr || q_dev == nullptr || kc == nullptr || vc == nullptr || msum == nullptr || out_dev == nullptr ||
         T == 0u || (n_new && new_runs == nullptr))
         return TSR_HIP_E_ARG;
-    if (!(D == 64u || D == 128u || D == 256u || D == 512u)) return TSR_HIP_E_SHAPE;
-    if (n_head_kv == 0u || n_head % n_head_kv != 0u || n_head / n_head_kv > 64u) return TSR_HIP_E_SHAPE;
-    const uint32_t E = n_head_kv * D, G = n_head / n_head_kv, K = n_head * D;
-    if (kc->E != E || vc->E != E || kc->kv_size != vc->kv_size || E / 64u > 511u || (uint64_t)G * E > 32768u || K > 32768u)
-        return TSR_HIP_E_SHAPE;
-    uint32_t sb;
-    memcpy(&sb, &scale, 4);
-    if ((sb >> 31) || (sb & 0x7F800000u) == 0u || (sb & 0x7F800000u) == 0x7F800000u) return TSR_HIP_E_SHAPE;
+    int rc = fa_check_shape(D, n_head, n_head_kv, scale);
+    if (rc) return rc;
+    const uint32_t E = n_head_kv * D, K = n_head * D;
+    if (kc->E != E || vc->E != E || kc->kv_size != vc->kv_size) return TSR_HIP_E_SHAPE;
     if (msum[0] != 0x4D55534Du || msum[1] != T || msum[2] > kc->kv_size) return TSR_HIP_E_MASK;
     if (((uintptr_t)q_dev & 15u) != 0u || (T > 1u && (q_stride % 4u != 0u || q_stride < K)) ||
         (T > 1u && out_stride < K) || T > 65535u)
         return TSR_HIP_E_ARG;
 
-    // plan every token row; flatten into items (chunks) with their 256-cell score tiles
-    std::vector<tsr::FaItem> items;
-    std::vector<uint32_t> tok(2u * (size_t)T);                    // tok_first [T] | tok_count [T]
-    std::vector<Chunk> ch;
-    uint64_t cells = 0;
-    uint32_t n_tiles = 0, maxtiles = 1;
-    for (uint32_t t = 0; t < T; ++t) {
-        ch.clear();
-        if (!plan_row(E, D, msum, t, new_runs, n_new, ch)) return TSR_HIP_E_MASK;
-        tok[t] = (uint32_t)items.size();
-        tok[T + t] = (uint32_t)ch.size();
-        for (const Chunk & c : ch) {
-            if (c.general && mask_f32_dev == nullptr) return TSR_HIP_E_MASK;
-            tsr::FaItem it{};
-            it.t = t;
-            it.u0 = c.u0;
-            it.n = c.n;
-            it.c_lo = c.c_lo;
-            it.c_hi = c.c_hi;
-            it.general = c.general;
-            it.s_off = (uint32_t)cells;
-            it.tile0 = n_tiles;
-            it.ntiles = (16u * c.n + 255u) / 256u;
-            n_tiles += it.ntiles;
-            maxtiles = std::max(maxtiles, it.ntiles);
-            cells += 16u * c.n;
-            items.push_back(it);
-        }
-    }
-    const size_t n_items = items.size();
-    if (cells * n_head > 0xFFFFFFFFull || n_items * 4u > 0x7FFFFFFFull || n_items * maxtiles > 0x7FFFFFFFull)
+    FaWork w;
+    if ((rc = fa_plan_rows(E, D, T, msum, new_runs, n_new, mask_f32_dev != nullptr, w)) != 0) return rc;
+    const size_t n_items = w.items.size();
+    if (w.cells * n_head > 0xFFFFFFFFull || n_items * 4u > 0x7FFFFFFFull || n_items * w.maxtiles > 0x7FFFFFFFull)
         return TSR_HIP_E_SHAPE;
     const bool inl = n_items <= tsr::kFaInlItems && T <= tsr::kFaInlTok;
     size_t off = 0;
     const size_t o_items = off; off = up256(off + (inl ? 0u : n_items * sizeof(tsr::FaItem) + 8u * (size_t)T));
-    const size_t o_S = off; off = up256(off + 4u * (size_t)cells * n_head);
-    const size_t o_Mp = off; off = up256(off + 4u * (size_t)n_tiles * n_head);
+    const size_t o_S = off; off = up256(off + 4u * (size_t)w.cells * n_head);
+    const size_t o_Mp = off; off = up256(off + 4u * (size_t)w.n_tiles * n_head);
     const size_t o_OP = off; off = up256(off + 4u * n_items * kC * n_head * D);
     const size_t o_LP = off; off = up256(off + 4u * n_items * kC * n_head);
 
     tsr::FaPlan p{};
     p.n_items = (uint32_t)n_items;
-    p.maxtiles = maxtiles;
+    p.maxtiles = w.maxtiles;
     std::vector<uint8_t> packed;
     if (inl) {
-        std::copy(items.begin(), items.end(), p.items);
-        for (uint32_t t = 0; t < T; ++t) { p.tok_first[t] = tok[t]; p.tok_count[t] = tok[T + t]; }
+        std::copy(w.items.begin(), w.items.end(), p.items);
+        for (uint32_t t = 0; t < T; ++t) { p.tok_first[t] = w.tok[t]; p.tok_count[t] = w.tok[T + t]; }
     } else {                                                      // items | tok_first | tok_count, one copy
         packed.resize(n_items * sizeof(tsr::FaItem) + 8u * (size_t)T);
-        memcpy(packed.data(), items.data(), n_items * sizeof(tsr::FaItem));
-        memcpy(packed.data() + n_items * sizeof(tsr::FaItem), tok.data(), 8u * (size_t)T);
+        memcpy(packed.data(), w.items.data(), n_items * sizeof(tsr::FaItem));
+        memcpy(packed.data() + n_items * sizeof(tsr::FaItem), w.tok.data(), 8u * (size_t)T);
     }
 
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
     hipStream_t s = ctx->pick(stream);
-    int rc = ctx->scratch.reserve(off, s);
+    rc = ctx->scratch.reserve(off, s);
     if (rc) return rc;
     uint8_t * base = (uint8_t *)ctx->scratch.ptr;
     if (!inl) {
         // a host-to-device copy of a host vector cannot be recorded into a graph (the vector is gone
-        // when the graph replays): long work lists are for eager calls
+        // when the graph replays): long work lists are for eager calls or a tsr_hip_fa_plan
         if (tsr_capturing(s)) return TSR_HIP_E_ARG;
         rc = hip_err(hipMemcpyAsync(base + o_items, packed.data(), packed.size(), hipMemcpyHostToDevice, s), "fa plan");
         if (rc) return rc;
     }
-
-    tsr::FaArgs a{};
-    a.q = q_dev;
-    a.q_stride = q_stride;
-    a.kc = kv_args(kc);
-    a.vc = kv_args(vc);
-    a.D = D;
-    a.G = G;
-    a.n_head = n_head;
-    a.n_head_kv = n_head_kv;
-    a.E = E;
-    a.scale = scale;
-    a.mask = mask_f32_dev;
-    a.mstride = 16u * ((msum[2] + 15u) / 16u);
+    tsr::FaArgs a = fa_args(ctx, q_dev, q_stride, kc, vc, D, n_head, n_head_kv, scale, mask_f32_dev,
+                            16u * ((msum[2] + 15u) / 16u), out_dev, out_stride);
     if (!inl) {
         a.items = (const tsr::FaItem *)(base + o_items);
         a.tok_first = (const uint32_t *)(base + o_items + n_items * sizeof(tsr::FaItem));
@@ -324,11 +360,145 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     a.Mpart = (float *)(base + o_Mp);
     a.OP = (float *)(base + o_OP);
     a.LP = (float *)(base + o_LP);
-    for (const tsr::FaItem & i : items) a.max_groups = std::max(a.max_groups, i.n);
-    a.out = out_dev;
-    a.out_stride = out_stride;
-    a.ex = ctx->expk;
+    a.max_groups = w.max_groups;
     ctx->ctr.flash_attn_calls++;
-    ctx->ctr.flash_attn_kv_bytes += cells * (uint64_t)E / 32u * 34u * 2u;
+    ctx->ctr.flash_attn_kv_bytes += w.cells * (uint64_t)E / 32u * 34u * 2u;
     return tsr_launch_fa(a, p, T, (uint32_t)ctx->n_cu, s) ? TSR_HIP_E_HIP : TSR_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// FA plans: the work list in device memory, refreshed per call by a stream-ordered copy, so that a
+// captured graph of planned FLASH_ATTN_EXT launches replays over a mask that changes between
+// replays (the per-graph plan cache of ggml-tesseract.cpp:3937-3952 and 3768-3779, as a graph)
+// ---------------------------------------------------------------------------------------------
+struct tsr_hip_fa_plan {
+    uint32_t D = 0, n_head = 0, n_head_kv = 0, T = 0, kv_size = 0;
+    uint32_t items_max = 0, tiles_max = 0;
+    uint64_t cells_max = 0;
+    uint8_t * dev = nullptr;
+    size_t o_items = 0, o_S = 0, o_Mp = 0, o_OP = 0, o_LP = 0, bytes = 0;
+    bool set = false, general = false;
+    uint32_t n_items = 0, maxtiles = 0, max_groups = 0, mstride = 0;   // the shape a launch bakes in
+    uint64_t cells = 0;
+};
+
+int tsr_hip_fa_plan_create(tsr_hip_ctx * ctx, uint32_t D, uint32_t n_head, uint32_t n_head_kv, uint32_t T,
+                           uint32_t kv_size, tsr_hip_fa_plan ** out) {
+    if (ctx == nullptr || out == nullptr || T == 0u || kv_size == 0u) return TSR_HIP_E_ARG;
+    *out = nullptr;
+    int rc = fa_check_shape(D, n_head, n_head_kv, 1.0f);
+    if (rc) return rc;
+    if (T > 65535u) return TSR_HIP_E_SHAPE;
+    const uint32_t E = n_head_kv * D;
+    const uint64_t pc = (uint64_t)kC * (kPcap / (16u * (E / D)));
+    const uint64_t ncg_min = std::max<uint64_t>(1u, std::min<uint64_t>(std::min<uint64_t>(128u, pc), 4u * kC));
+    const uint64_t groups = ((uint64_t)kv_size + 15u) / 16u + 2u;             // two runs, each with a partial group
+    const uint64_t items = (uint64_t)T * ((groups + ncg_min - 1u) / ncg_min + 2u);
+    const uint64_t cells = (uint64_t)T * 16u * groups;
+    const uint64_t tiles = cells / 256u + items;
+    if (items > 0x7FFFFFFFull / 4u || cells * n_head > 0xFFFFFFFFull) return TSR_HIP_E_SHAPE;
+    auto * p = new (std::nothrow) tsr_hip_fa_plan();
+    if (p == nullptr) return TSR_HIP_E_NOMEM;
+    p->D = D;
+    p->n_head = n_head;
+    p->n_head_kv = n_head_kv;
+    p->T = T;
+    p->kv_size = kv_size;
+    p->items_max = (uint32_t)items;
+    p->tiles_max = (uint32_t)tiles;
+    p->cells_max = cells;
+    size_t off = 0;
+    p->o_items = off; off = up256(off + items * sizeof(tsr::FaItem) + 8u * (size_t)T);
+    p->o_S = off; off = up256(off + 4u * (size_t)cells * n_head);
+    p->o_Mp = off; off = up256(off + 4u * (size_t)tiles * n_head);
+    p->o_OP = off; off = up256(off + 4u * (size_t)items * kC * n_head * D);
+    p->o_LP = off; off = up256(off + 4u * (size_t)items * kC * n_head);
+    p->bytes = off;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    if ((rc = hip_err(hipMalloc(&p->dev, off), "hipMalloc fa plan")) != 0) {
+        delete p;
+        return rc;
+    }
+    *out = p;
+    return TSR_HIP_OK;
+}
+
+int tsr_hip_fa_plan_free(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan) {
+    if (ctx == nullptr || plan == nullptr) return TSR_HIP_E_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    (void)hipDeviceSynchronize();                // no queued launch still reads the list
+    (void)hipFree(plan->dev);
+    delete plan;
+    return TSR_HIP_OK;
+}
+
+int tsr_hip_fa_plan_set(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan, const uint32_t * msum, int mask_f32,
+                        const uint32_t (*new_runs)[2], uint32_t n_new, int * shape_changed, void * stream) {
+    if (ctx == nullptr || plan == nullptr || msum == nullptr || (n_new && new_runs == nullptr)) return TSR_HIP_E_ARG;
+    if (msum[0] != 0x4D55534Du || msum[1] != plan->T || msum[2] > plan->kv_size) return TSR_HIP_E_MASK;
+    FaWork w;
+    int rc = fa_plan_rows(plan->n_head_kv * plan->D, plan->D, plan->T, msum, new_runs, n_new, mask_f32 != 0, w);
+    if (rc) return rc;
+    if (w.items.size() > plan->items_max || w.cells > plan->cells_max || w.n_tiles > plan->tiles_max)
+        return TSR_HIP_E_SHAPE;
+    const uint32_t T = plan->T, n_items = (uint32_t)w.items.size();
+    std::vector<uint8_t> packed(n_items * sizeof(tsr::FaItem) + 8u * (size_t)T);
+    memcpy(packed.data(), w.items.data(), n_items * sizeof(tsr::FaItem));
+    memcpy(packed.data() + n_items * sizeof(tsr::FaItem), w.tok.data(), 8u * (size_t)T);
+    bool general = false;
+    for (const tsr::FaItem & it : w.items) general |= it.general != 0u;
+    const uint32_t mstride = 16u * ((msum[2] + 15u) / 16u);
+    const bool changed = !plan->set || n_items != plan->n_items || w.maxtiles != plan->maxtiles ||
+                         w.max_groups != plan->max_groups || (general && mstride != plan->mstride) ||
+                         general != plan->general;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    hipStream_t s = ctx->pick(stream);
+    if (tsr_capturing(s)) return TSR_HIP_E_ARG;      // the copy is made at each call, outside any graph
+    // the tok arrays sit right after the items of this list: a launch baked with another n_items reads
+    // them at another offset, which is why a changed shape asks for a new capture
+    if ((rc = ctx->staging.copy(plan->dev + plan->o_items, packed.data(), packed.size(), s)) != 0) return rc;
+    plan->set = true;
+    plan->n_items = n_items;
+    plan->maxtiles = w.maxtiles;
+    plan->max_groups = w.max_groups;
+    plan->mstride = mstride;
+    plan->general = general;
+    plan->cells = w.cells;
+    if (shape_changed) *shape_changed = changed ? 1 : 0;
+    return TSR_HIP_OK;
+}
+
+int tsr_hip_flash_attn_plan(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const float * q_dev, uint64_t q_stride,
+                            const tsr_hip_kv * kc, const tsr_hip_kv * vc, float scale, const float * mask_f32_dev,
+                            float * out_dev, uint64_t out_stride, void * stream) {
+    if (ctx == nullptr || plan == nullptr || q_dev == nullptr || kc == nullptr || vc == nullptr || out_dev == nullptr)
+        return TSR_HIP_E_ARG;
+    if (!plan->set || (plan->general && mask_f32_dev == nullptr)) return TSR_HIP_E_MASK;
+    int rc = fa_check_shape(plan->D, plan->n_head, plan->n_head_kv, scale);
+    if (rc) return rc;
+    const uint32_t E = plan->n_head_kv * plan->D, K = plan->n_head * plan->D, T = plan->T;
+    if (kc->E != E || vc->E != E || kc->kv_size != vc->kv_size || kc->kv_size < plan->kv_size) return TSR_HIP_E_SHAPE;
+    if (((uintptr_t)q_dev & 15u) != 0u || (T > 1u && (q_stride % 4u != 0u || q_stride < K)) || (T > 1u && out_stride < K))
+        return TSR_HIP_E_ARG;
+    tsr::FaPlan p{};
+    p.n_items = plan->n_items;
+    p.maxtiles = plan->maxtiles;
+    tsr::FaArgs a = fa_args(ctx, q_dev, q_stride, kc, vc, plan->D, plan->n_head, plan->n_head_kv, scale, mask_f32_dev,
+                            plan->mstride, out_dev, out_stride);
+    a.items = (const tsr::FaItem *)(plan->dev + plan->o_items);
+    a.tok_first = (const uint32_t *)(plan->dev + plan->o_items + (size_t)plan->n_items * sizeof(tsr::FaItem));
+    a.tok_count = a.tok_first + T;
+    a.S = (float *)(plan->dev + plan->o_S);
+    a.Mpart = (float *)(plan->dev + plan->o_Mp);
+    a.OP = (float *)(plan->dev + plan->o_OP);
+    a.LP = (float *)(plan->dev + plan->o_LP);
+    a.max_groups = plan->max_groups;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    ctx->ctr.flash_attn_calls++;
+    ctx->ctr.flash_attn_kv_bytes += plan->cells * (uint64_t)E / 32u * 34u * 2u;
+    return tsr_launch_fa(a, p, T, (uint32_t)ctx->n_cu, ctx->pick(stream)) ? TSR_HIP_E_HIP : TSR_HIP_OK;
 }

@@ -93,6 +93,7 @@ int tsr_hip_close(tsr_hip_ctx * ctx) {
         (void)hipSetDevice(ctx->device);
         (void)hipStreamSynchronize(ctx->stream);
         ctx->scratch.release();
+        ctx->staging.release();
         (void)hipStreamDestroy(ctx->stream);
     }
     delete ctx;
@@ -160,6 +161,24 @@ int tsr_hip_write(tsr_hip_ctx * ctx, void * dst_dev, const void * src, size_t by
     int rc = hip_err(hipMemcpyAsync(dst_dev, src, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpy H2D");
     if (rc == 0) rc = hip_err(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     return rc;
+}
+
+int tsr_hip_write_async(tsr_hip_ctx * ctx, void * dst_dev, const void * src, size_t bytes, void * stream) {
+    if (ctx == nullptr || (bytes && (dst_dev == nullptr || src == nullptr))) return TSR_HIP_E_ARG;
+    if (bytes == 0) return TSR_HIP_OK;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    hipStream_t s = ctx->pick(stream);
+    if (tsr_capturing(s)) return TSR_HIP_E_ARG;
+    return ctx->staging.copy(dst_dev, src, bytes, s);
+}
+
+int tsr_hip_copy_async(tsr_hip_ctx * ctx, void * dst_dev, const void * src_dev, size_t bytes, void * stream) {
+    if (ctx == nullptr || (bytes && (dst_dev == nullptr || src_dev == nullptr))) return TSR_HIP_E_ARG;
+    if (bytes == 0) return TSR_HIP_OK;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    return hip_err(hipMemcpyAsync(dst_dev, src_dev, bytes, hipMemcpyDeviceToDevice, ctx->pick(stream)), "hipMemcpyAsync D2D");
 }
 
 int tsr_hip_read(tsr_hip_ctx * ctx, void * dst, const void * src_dev, size_t bytes) {
@@ -476,4 +495,60 @@ int tsr_hip_mul_mat_isums(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
     const int rc = ctx->scratch.reserve((size_t)w->N * sizeof(float), s);
     if (rc) return rc;
     return mul_mat_locked(ctx, w, x_dev, 1u, w->K, (float *)ctx->scratch.ptr, w->N, nullptr, 0u, 0u, isums_dev, s);
+}
+
+// ---------------------------------------------------------------------------------------------
+// graphs: the launches one stream records between begin and end, replayed as one launch
+// ---------------------------------------------------------------------------------------------
+struct tsr_hip_graph {
+    hipGraph_t g = nullptr;
+    hipGraphExec_t x = nullptr;
+};
+
+int tsr_hip_graph_begin(tsr_hip_ctx * ctx, void * stream) {
+    if (ctx == nullptr) return TSR_HIP_E_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    hipStream_t s = ctx->pick(stream);
+    if (tsr_capturing(s)) return TSR_HIP_E_ARG;
+    return hip_err(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+}
+
+int tsr_hip_graph_end(tsr_hip_ctx * ctx, void * stream, tsr_hip_graph ** out) {
+    if (ctx == nullptr || out == nullptr) return TSR_HIP_E_ARG;
+    *out = nullptr;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    hipStream_t s = ctx->pick(stream);
+    hipGraph_t g = nullptr;
+    int rc = hip_err(hipStreamEndCapture(s, &g), "hipStreamEndCapture");
+    if (rc) return rc;
+    auto * gr = new (std::nothrow) tsr_hip_graph();
+    if (gr == nullptr) { (void)hipGraphDestroy(g); return TSR_HIP_E_NOMEM; }
+    gr->g = g;
+    if ((rc = hip_err(hipGraphInstantiate(&gr->x, g, nullptr, nullptr, 0), "hipGraphInstantiate")) != 0) {
+        (void)hipGraphDestroy(g);
+        delete gr;
+        return rc;
+    }
+    *out = gr;
+    return TSR_HIP_OK;
+}
+
+int tsr_hip_graph_launch(tsr_hip_ctx * ctx, const tsr_hip_graph * graph, void * stream) {
+    if (ctx == nullptr || graph == nullptr) return TSR_HIP_E_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    return hip_err(hipGraphLaunch(graph->x, ctx->pick(stream)), "hipGraphLaunch");
+}
+
+int tsr_hip_graph_free(tsr_hip_ctx * ctx, tsr_hip_graph * graph) {
+    if (ctx == nullptr || graph == nullptr) return TSR_HIP_E_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    (void)hipDeviceSynchronize();                // no replay still runs
+    (void)hipGraphExecDestroy(graph->x);
+    (void)hipGraphDestroy(graph->g);
+    delete graph;
+    return TSR_HIP_OK;
 }

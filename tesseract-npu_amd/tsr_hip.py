@@ -33,6 +33,8 @@ EXPORTS = (
     "tsr_hip_kv_create", "tsr_hip_kv_free", "tsr_hip_kv_set_bytes", "tsr_hip_kv_get_bytes", "tsr_hip_kv_set_rows",
     "tsr_hip_msum_build_f16", "tsr_hip_flash_attn", "tsr_hip_get_counters",
     "tsr_hip_rms_norm", "tsr_hip_rope", "tsr_hip_swiglu", "tsr_hip_add", "tsr_hip_get_rows", "tsr_hip_argmax",
+    "tsr_hip_write_async", "tsr_hip_copy_async", "tsr_hip_fa_plan_create", "tsr_hip_fa_plan_set", "tsr_hip_flash_attn_plan",
+    "tsr_hip_fa_plan_free", "tsr_hip_graph_begin", "tsr_hip_graph_end", "tsr_hip_graph_launch", "tsr_hip_graph_free",
 )
 
 
@@ -90,6 +92,16 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "tsr_hip_add": ([vp, vp, u64, vp, u64, u32, u32, u32, vp, u64, vp], C.c_int),
         "tsr_hip_get_rows": ([vp, vp, u64, u32, u32, vp, u32, vp, u64, vp, vp], C.c_int),
         "tsr_hip_argmax": ([vp, vp, u32, u32, u64, vp, vp], C.c_int),
+        "tsr_hip_write_async": ([vp, vp, vp, sz, vp], C.c_int),
+        "tsr_hip_copy_async": ([vp, vp, vp, sz, vp], C.c_int),
+        "tsr_hip_fa_plan_create": ([vp, u32, u32, u32, u32, u32, C.POINTER(vp)], C.c_int),
+        "tsr_hip_fa_plan_set": ([vp, vp, vp, C.c_int, vp, u32, C.POINTER(C.c_int), vp], C.c_int),
+        "tsr_hip_flash_attn_plan": ([vp, vp, vp, u64, vp, vp, C.c_float, vp, vp, u64, vp], C.c_int),
+        "tsr_hip_fa_plan_free": ([vp, vp], C.c_int),
+        "tsr_hip_graph_begin": ([vp, vp], C.c_int),
+        "tsr_hip_graph_end": ([vp, vp, C.POINTER(vp)], C.c_int),
+        "tsr_hip_graph_launch": ([vp, vp, vp], C.c_int),
+        "tsr_hip_graph_free": ([vp, vp], C.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -226,6 +238,58 @@ class KvCache:
             pass
 
 
+class FaPlan:
+    """A FLASH_ATTN_EXT work list in device memory (tsr_hip_fa_plan_*)."""
+
+    def __init__(self, dev: "Device", D: int, n_head: int, n_head_kv: int, T: int, kv_size: int):
+        self.dev = dev
+        h = C.c_void_p()
+        _check(dev.L.tsr_hip_fa_plan_create(dev.ctx, D, n_head, n_head_kv, T, kv_size, C.byref(h)), "fa_plan_create")
+        self.h = h.value
+
+    def set(self, msum, new_runs=None, mask_f32: bool = False, stream=None) -> bool:
+        """Plans the MSUM words; True when the list's shape changed (captured launches are stale)."""
+        words = np.ascontiguousarray(msum, np.uint32)
+        nr = None if new_runs is None else np.ascontiguousarray(new_runs, np.uint32).reshape(-1, 2)
+        ch = C.c_int()
+        _check(self.dev.L.tsr_hip_fa_plan_set(self.dev.ctx, self.h, words.ctypes.data, int(mask_f32),
+                                              None if nr is None else nr.ctypes.data, 0 if nr is None else nr.shape[0],
+                                              C.byref(ch), stream), "fa_plan_set")
+        return bool(ch.value)
+
+    def free(self) -> None:
+        if self.h:
+            self.dev.L.tsr_hip_fa_plan_free(self.dev.ctx, self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Graph:
+    """Launches recorded between Device.graph_begin and graph_end, replayed by launch()."""
+
+    def __init__(self, dev: "Device", h: int):
+        self.dev, self.h = dev, h
+
+    def launch(self, stream=None) -> None:
+        _check(self.dev.L.tsr_hip_graph_launch(self.dev.ctx, self.h, stream), "graph_launch")
+
+    def free(self) -> None:
+        if self.h:
+            self.dev.L.tsr_hip_graph_free(self.dev.ctx, self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class Device:
     """A libtsr_hip context on one GPU."""
 
@@ -306,6 +370,30 @@ class Device:
                                          float(scale), words.ctypes.data, self._p(mask_f32),
                                          None if nr is None else nr.ctypes.data, 0 if nr is None else nr.shape[0],
                                          self._p(out), out_stride, stream), "flash_attn")
+
+    def write_async(self, dst, arr, stream=None) -> None:
+        """Stream-ordered host-to-device copy of arr (<= 16 KiB); arr may be reused at once."""
+        a = np.ascontiguousarray(arr)
+        _check(self.L.tsr_hip_write_async(self.ctx, self._p(dst), a.ctypes.data, a.nbytes, stream), "write_async")
+
+    def copy_async(self, dst, src, nbytes: int, stream=None) -> None:
+        _check(self.L.tsr_hip_copy_async(self.ctx, self._p(dst), self._p(src), nbytes, stream), "copy_async")
+
+    def fa_plan(self, D: int, n_head: int, n_head_kv: int, T: int, kv_size: int) -> "FaPlan":
+        return FaPlan(self, D, n_head, n_head_kv, T, kv_size)
+
+    def flash_attn_plan(self, plan: "FaPlan", q, q_stride: int, kc: KvCache, vc: KvCache, scale: float, out,
+                        out_stride: int, mask_f32=None, stream=None) -> None:
+        _check(self.L.tsr_hip_flash_attn_plan(self.ctx, plan.h, self._p(q), q_stride, kc.h, vc.h, float(scale),
+                                              self._p(mask_f32), self._p(out), out_stride, stream), "flash_attn_plan")
+
+    def graph_begin(self, stream=None) -> None:
+        _check(self.L.tsr_hip_graph_begin(self.ctx, stream), "graph_begin")
+
+    def graph_end(self, stream=None) -> "Graph":
+        h = C.c_void_p()
+        _check(self.L.tsr_hip_graph_end(self.ctx, stream, C.byref(h)), "graph_end")
+        return Graph(self, h.value)
 
     # -- decode-layer glue ops (rows of n f32; strides in floats) -------------------------------------
     def rms_norm(self, x, n: int, rows: int, x_stride: int, eps: float, y, y_stride: int, w=None, w_stride: int = 0,

@@ -150,11 +150,21 @@ class LlamaDecoder:
         self.glu = dev.alloc(c.n_ff * f4)
         self.logits = dev.alloc(c.n_vocab * f4)
         self.tok = dev.alloc(4)            # int32 token id of the step (GET_ROWS ids)
-        self.next = dev.alloc(4)           # int32 greedy token (ARGMAX)
-        self.pos = dev.alloc(4)            # int32 position (ROPE)
-        self.cell = dev.alloc(8)           # int64 cell (SET_ROWS_KV)
+        self.next = dev.alloc(4)           # int32 greedy token (ARGMAX) of an eager step
+        self.params = dev.alloc(16)        # int32 position (ROPE) at 0, int64 cell (SET_ROWS_KV) at 8
         self.bad = dev.alloc(4).fill(0)
         self.scale = 1.0 / math.sqrt(c.head_dim)
+        self.plan = dev.fa_plan(c.head_dim, c.n_head, c.n_head_kv, 1, kv_size)
+        self.graph = None
+        self.captures = 0
+
+    @property
+    def pos_ptr(self) -> int:
+        return self.params.ptr
+
+    @property
+    def cell_ptr(self) -> int:
+        return self.params.ptr + 8
 
     def prefill_history(self, weights: SyntheticWeights, n: int) -> None:
         """Cells 0 .. n-1 of every cache hold QACT'd rows of weights.kv_history (SET_ROWS_KV)."""
@@ -166,35 +176,41 @@ class LlamaDecoder:
                 rows.free()
         self.dev.sync()
 
-    def step(self, token: int | None, pos: int, n_kv: int | None = None, stream=None) -> None:
-        """One decode token at position pos (cell pos). token: the id to embed, or None to embed the
-        previous step's greedy token (left on the device). Logits end in self.logits, the greedy token
-        in self.next. n_kv: the mask width (default: pos + 1 rounded up to 256, at most kv_size)."""
-        c, d = self.cfg, self.dev
+    def _mask(self, pos: int, n_kv: int | None):
         if not 0 <= pos < self.kv_size:
             raise ValueError(f"position {pos} outside the cache of {self.kv_size} cells")
-        if token is not None:
-            self.tok.write(np.array([token], np.int32))
-        else:
-            self.tok.write(self.next.read(np.int32, (1,)))
-        self.pos.write(np.array([pos], np.int32))
-        self.cell.write(np.array([pos], np.int64))
         if n_kv is None:
             n_kv = min(self.kv_size, (pos + 1 + 255) // 256 * 256)
-        msum = msum_decode(pos, n_kv)
-        runs = np.array([[pos, pos + 1]], np.uint32)
+        return msum_decode(pos, n_kv), np.array([[pos, pos + 1]], np.uint32)
+
+    @staticmethod
+    def _params(pos: int) -> np.ndarray:
+        p = np.zeros(2, np.int64)
+        p[1] = pos
+        v = p.view(np.int32)
+        v[0] = pos
+        return p
+
+    def _ops(self, out_tok, msum=None, runs=None, stream=None) -> None:
+        """The launches of one decode token. msum given: FLASH_ATTN_EXT planned on the host per call
+        (eager); else the device-resident plan (capturable)."""
+        c, d = self.cfg, self.dev
         nq, E, n = c.n_q, c.E, c.n_embd
         f4 = 4
         d.get_rows(self.tok_embd, n, n, c.n_vocab, self.tok, 1, self.x, n, bad=self.bad, stream=stream)
         for L in self.layers:
             d.rms_norm(self.x, n, 1, n, c.eps, self.xn, n, w=L["attn_norm"], w_stride=n, stream=stream)
             d.mul_mat(L["wqkv"], self.xn, 1, n, self.qkv, nq + 2 * E, stream=stream)
-            d.rope(self.qkv, 1, nq + 2 * E, c.head_dim, c.n_head + c.n_head_kv, c.head_dim, c.rope_mode, self.pos,
+            d.rope(self.qkv, 1, nq + 2 * E, c.head_dim, c.n_head + c.n_head_kv, c.head_dim, c.rope_mode, self.pos_ptr,
                    c.rope_base, self.qkv, nq + 2 * E, stream=stream)
-            d.kv_set_rows(L["kc"], 0, self.qkv.ptr + nq * f4, 1, E, self.cell, self.bad, stream=stream)
-            d.kv_set_rows(L["vc"], 1, self.qkv.ptr + (nq + E) * f4, 1, E, self.cell, self.bad, stream=stream)
-            d.flash_attn(self.qkv, 1, nq + 2 * E, L["kc"], L["vc"], c.head_dim, c.n_head, c.n_head_kv, self.scale,
-                         msum, self.att, nq, new_runs=runs, stream=stream)
+            d.kv_set_rows(L["kc"], 0, self.qkv.ptr + nq * f4, 1, E, self.cell_ptr, self.bad, stream=stream)
+            d.kv_set_rows(L["vc"], 1, self.qkv.ptr + (nq + E) * f4, 1, E, self.cell_ptr, self.bad, stream=stream)
+            if msum is not None:
+                d.flash_attn(self.qkv, 1, nq + 2 * E, L["kc"], L["vc"], c.head_dim, c.n_head, c.n_head_kv, self.scale,
+                             msum, self.att, nq, new_runs=runs, stream=stream)
+            else:
+                d.flash_attn_plan(self.plan, self.qkv, nq + 2 * E, L["kc"], L["vc"], self.scale, self.att, nq,
+                                  stream=stream)
             d.mul_mat(L["wo"], self.att, 1, nq, self.h, n, add=self.x, add_stride=n, stream=stream)
             d.rms_norm(self.h, n, 1, n, c.eps, self.xn, n, w=L["ffn_norm"], w_stride=n, stream=stream)
             d.mul_mat(L["wgu"], self.xn, 1, n, self.gu, 2 * c.n_ff, stream=stream)
@@ -203,15 +219,62 @@ class LlamaDecoder:
             d.mul_mat(L["wd"], self.glu, 1, c.n_ff, self.x, n, add=self.h, add_stride=n, stream=stream)
         d.rms_norm(self.x, n, 1, n, c.eps, self.xn, n, w=self.out_norm, w_stride=n, stream=stream)
         d.mul_mat(self.wout, self.xn, 1, n, self.logits, c.n_vocab, stream=stream)
-        d.argmax(self.logits, c.n_vocab, 1, c.n_vocab, self.next, stream=stream)
+        d.argmax(self.logits, c.n_vocab, 1, c.n_vocab, out_tok, stream=stream)
+
+    def step(self, token: int | None, pos: int, n_kv: int | None = None) -> None:
+        """One eager decode token at position pos (cell pos): every op a separate call, FLASH_ATTN_EXT
+        planned per call. token: the id to embed, or None for the previous step's greedy token. Logits
+        end in self.logits, the greedy token in self.next. n_kv: the mask width (default pos + 1
+        rounded up to 256, at most kv_size)."""
+        msum, runs = self._mask(pos, n_kv)
+        self.tok.write(np.array([token], np.int32) if token is not None else self.next.read(np.int32, (1,)))
+        self.params.write(self._params(pos))
+        self._ops(self.next, msum, runs)
+
+    def step_graph(self, token: int | None, pos: int, n_kv: int | None = None) -> None:
+        """One decode token as one graph replay. Per token the host only plans the attention chunks and
+        queues two small stream-ordered copies (position / cell and the plan); the greedy token of the
+        previous replay is embedded from the device (token None). The graph is captured on the first
+        call and again whenever the plan's shape changes. Nothing waits for the device."""
+        d = self.dev
+        msum, runs = self._mask(pos, n_kv)
+        if token is not None:
+            d.write_async(self.tok, np.array([token], np.int32))
+        d.write_async(self.params, self._params(pos))
+        changed = self.plan.set(msum, runs)
+        if self.graph is None or changed:
+            if self.graph is not None:
+                self.graph.free()
+            d.graph_begin()
+            try:
+                self._ops(self.tok)
+            finally:
+                g = d.graph_end()
+            self.graph = g
+            self.captures += 1
+        self.graph.launch()
+
+    def generate_graph(self, first_token: int, pos0: int, n_tokens: int, hist=None) -> None:
+        """Greedy decode of n_tokens by graph replays, without waiting for the device; the token
+        generated at step i is copied to hist[i] (a device int32 buffer) when given."""
+        for i in range(n_tokens):
+            self.step_graph(first_token if i == 0 else None, pos0 + i)
+            if hist is not None:
+                self.dev.copy_async(hist.ptr + 4 * i, self.tok, 4)
 
     def read_logits(self) -> np.ndarray:
         self.dev.sync()
         return self.logits.read(np.float32, (self.cfg.n_vocab,))
 
     def read_next(self) -> int:
+        """The greedy token of the last eager step."""
         self.dev.sync()
         return int(self.next.read(np.int32, (1,))[0])
+
+    def read_token(self) -> int:
+        """The greedy token of the last graph replay (it is also the next replay's input)."""
+        self.dev.sync()
+        return int(self.tok.read(np.int32, (1,))[0])
 
     def generate(self, first_token: int, pos0: int, n_tokens: int) -> list[int]:
         """Greedy decode of n_tokens from first_token at pos0 (the previous token fed back on the device)."""
@@ -222,6 +285,10 @@ class LlamaDecoder:
         return out
 
     def free(self) -> None:
+        if self.graph is not None:
+            self.graph.free()
+            self.graph = None
+        self.plan.free()
         for L in self.layers:
             for k in ("wqkv", "wo", "wgu", "wd", "kc", "vc"):
                 L[k].free()

@@ -65,3 +65,52 @@ def test_decode_matches_oracle(dev, oc, cfg, kv_size, hist, n_steps):
         assert (gpu.layers[il]["vc"].get_bytes(1).reshape(kv_size, -1) == ref.vc[il]).all()
     assert gpu.bad.read(np.int32, (1,))[0] == 0
     gpu.free()
+
+
+@pytest.mark.parametrize("cfg,kv_size,hist,n_steps", [
+    (LL.tiny_config(), 300, 254, 5),              # cells 255 .. 259: the plan grows a second chunk at 257
+    (LL.tiny_config("tiny-qwen", wfmt=H.FMT_Q8_0, ofmt=H.FMT_Q8_0, rope_mode=H.ROPE_NEOX, eps=1e-6,
+                    rope_base=1000000.0), 640, 300, 3),
+], ids=["q4k-norm-grow", "q80-neox"])
+def test_decode_graph_matches_oracle(dev, oc, cfg, kv_size, hist, n_steps):
+    """The same decode as one graph replay per token: FLASH_ATTN_EXT from the device-resident plan, the
+    position / cell and the plan copied in stream order, the greedy token fed back on the device."""
+    w = LL.SyntheticWeights(cfg)
+    print(f"\ngraph decode parity {cfg.name}: kv {kv_size} history {hist} steps {n_steps}", flush=True)
+    gpu = LL.LlamaDecoder(dev, cfg, w, kv_size)
+    gpu.prefill_history(w, hist)
+    ref = oracle_model(oc, cfg, w, kv_size, hist)
+    ts = np.float32(_libm.powf(float(np.float32(cfg.rope_base)), float(np.float32(-2.0) / np.float32(cfg.head_dim))))
+    tok = 11
+    for i in range(n_steps):
+        pos = hist + i
+        n_kv = min(kv_size, (pos + 1 + 255) // 256 * 256)
+        gpu.step_graph(tok if i == 0 else None, pos)
+        got = gpu.read_logits()
+        want = ref.step(tok, pos, ts, n_kv)
+        assert_bits_equal(got, want, f"{cfg.name} graph step {i} (pos {pos})")
+        tok = gpu.read_token()
+        assert tok == int(oc.argmax(want[None])[0])
+    assert gpu.captures == (2 if hist < 256 < hist + n_steps else 1)
+    gpu.free()
+
+
+def test_decode_graph_runs_ahead(dev):
+    """Tokens queued without waiting (generate_graph) equal tokens decoded one replay at a time."""
+    cfg = LL.tiny_config()
+    w = LL.SyntheticWeights(cfg)
+    a = LL.LlamaDecoder(dev, cfg, w, 256)
+    a.prefill_history(w, 40)
+    hist = dev.alloc(4 * 12)
+    a.generate_graph(3, 40, 12, hist)
+    dev.sync()
+    fast = hist.read(np.int32, (12,))
+    a.free()
+    b = LL.LlamaDecoder(dev, cfg, w, 256)
+    b.prefill_history(w, 40)
+    slow = []
+    for i in range(12):
+        b.step(3 if i == 0 else None, 40 + i)
+        slow.append(b.read_next())
+    b.free()
+    assert list(fast) == slow

@@ -1,19 +1,23 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized-inference hot path on one MI355X.
 
-Workload: the Llama-3-8B FFN matrix-vector pair at batch 1 --
-Q4_K W_up [14336 x 4096] then Q4_K W_down [4096 x 14336], activation f32 quantized on the fly to
-Q8_K (A256). One step = one up MUL_MAT followed by one down MUL_MAT on its output, i.e. the
-weight stream of one FFN of one decode token. Weights are fp32 N(0, 0.02) from fixed seeds
-quantized to Q4_K; the activation is N(0, 1). Inputs are resident in HBM before timing.
+Headline workload (the configuration the metric is quoted on): greedy
+decode of a random-init Llama-3-8B-architecture model at batch 1 -- 32 layers, hidden 4096, FFN
+14336 SwiGLU, 32 q / 8 KV heads, head_dim 128, vocab 128256, every weight matrix (output head
+included) Q4_K from seeded N(0, 0.02), q8_0 KV caches holding 4096 cells of context. One step is
+one decode token: the whole decoder (embedding row, 32 x [RMS_NORM, MUL_MAT QKV, ROPE, SET_ROWS_KV,
+FLASH_ATTN_EXT, MUL_MAT O + residual, RMS_NORM, MUL_MAT gate|up, SWIGLU, MUL_MAT down + residual],
+output norm, output head, ARGMAX) replayed as one HIP graph, the greedy token fed back on the device.
+Inputs are resident in HBM before the timed region; the 4.2 GB of weights per token exceed the
+256 MB Infinity Cache many times over, so weight reads come from HBM.
 
-Honest HBM numbers: the step rotates through distinct device copies of the weights whose total
-exceeds twice the 256 MB Infinity Cache, so weight reads come from HBM.
-
-Output: one JSON line (metric, value = algorithmic weight+activation bytes per step / time,
-roofline of the dominant kernel measured live with HIP events on the launch stream (the timed
-steps are replayed from a captured HIP graph, as a decode loop runs them), and the CPU
-baseline: this repository's oracle (the reference's numerics restated in C) on the host cores).
+Output: one JSON line with the metric (decode tokens per second), the roofline of the kernel that
+takes the largest share of a token (its launch duration measured live with HIP events on the launch
+stream over the model's own layers), HBM traffic of that kernel from two rocprofv3 --pmc passes, and
+the CPU baseline: this repository's oracle (the reference's numerics restated in C) decoding the same
+model on the host cores -- whose first-token logits are also compared bit for bit with the GPU's.
+The other BASELINE configs (Q4_K FFN pair, Q8_0 matvec, flash-decode at 8192 cells, prefill) are
+reported under "also".
 """
 from __future__ import annotations
 
@@ -35,11 +39,14 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "tesseract-npu_amd"))
 
 import tsr_hip  # noqa: E402
+import tsr_llama as LL  # noqa: E402
 import tsr_synth as S  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
 METRIC = "decode tok/s (8B Q4_K, ctx 4096); matvec/attn HBM GB/s as % of peak"
+CTX = 4096                      # KV cells filled before the first decode token
+FIRST_TOKEN = 128000            # the id of the first decoded token (Llama-3's <|begin_of_text|>)
 
 
 class HipEvents:
@@ -111,37 +118,208 @@ class HipEvents:
             self.h.hipGraphDestroy(g)
 
 
+def q4k_bytes(N: int, K: int) -> int:
+    return N * (K // 256) * 144
+
+
 def mv_bytes(N: int, K: int) -> int:
     """Algorithmic bytes of one Q4_K matvec: weights + f32 x + f32 y."""
-    return N * (K // 256) * 144 + 4 * K + 4 * N
+    return q4k_bytes(N, K) + 4 * K + 4 * N
 
 
-def cpu_baseline(blocks_up, x, seconds: float = 10.0) -> dict:
-    """The oracle's MUL_MAT (the reference numerics restated in C) on the host cores, on whole
-    W_up matvecs, repeated for about `seconds`. Reported in weight GB/s like the GPU value."""
+class CachedWeights(LL.SyntheticWeights):
+    """SyntheticWeights whose tensors are generated once and kept on the host, so that the GPU model
+    and the CPU leg see the same arrays without generating them twice."""
+
+    def __init__(self, cfg):
+        super().__init__(cfg)
+        self.cache = {}
+
+    def quant(self, name, N, K, fmt):
+        key = (name, fmt)
+        if key not in self.cache:
+            self.cache[key] = super().quant(name, N, K, fmt)
+        return self.cache[key]
+
+    def norm(self, name):
+        if name not in self.cache:
+            self.cache[name] = super().norm(name)
+        return self.cache[name]
+
+    def embedding(self):
+        if "token_embd.weight" not in self.cache:
+            self.cache["token_embd.weight"] = super().embedding()
+        return self.cache["token_embd.weight"]
+
+
+def token_bytes(cfg, n_kv_read: int) -> int:
+    """Algorithmic bytes of one decode token: every quantized weight once, the q8_0 K and V of the
+    visible cells of every layer, the embedding row and the norm vectors."""
+    E = cfg.E
+    kv = cfg.n_layer * 2 * n_kv_read * (E // 32) * 34
+    return cfg.weight_bytes_per_token() + kv + 4 * cfg.n_embd * (2 * cfg.n_layer + 2)
+
+
+def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
+    """Llama-3-8B-architecture Q4_K decode with CTX cells of context.
+
+    Cells 0 .. CTX-1 of every layer's caches hold seeded rows (SET_ROWS_KV); token 0 is decoded at
+    position CTX eagerly (its logits are kept for the CPU leg's bit comparison), tokens 1 .. warmup-1
+    by graph replays (the first replay captures), then `steps` timed graph replays at positions
+    CTX+warmup .. CTX+warmup+steps-1. Every greedy token is copied to a device history buffer."""
+    cfg = LL.LLAMA3_8B
+    wts = CachedWeights(cfg)
+    kv_size = CTX + warmup + steps
+    stream = dev.stream
+    t0 = time.perf_counter()
+    m = LL.LlamaDecoder(dev, cfg, wts, kv_size)
+    m.prefill_history(wts, CTX)
+    setup_s = time.perf_counter() - t0
+    hist = dev.alloc(4 * (warmup + steps))
+    m.step(FIRST_TOKEN, CTX)
+    logits0 = m.read_logits().copy()
+    tok1 = m.read_next()
+    hist.write(np.array([tok1], np.int32))
+    for i in range(1, warmup):
+        m.step_graph(tok1 if i == 1 else None, CTX + i)
+        dev.copy_async(hist.ptr + 4 * i, m.tok, 4)
+    dev.sync()
+    captures = m.captures
+    e0, e1 = ev.event(), ev.event()
+    ev.device_sync()
+    h0 = time.perf_counter()
+    ev.record(e0, stream)
+    for i in range(steps):
+        if eager:
+            m.step_async(None, CTX + warmup + i)
+        else:
+            m.step_graph(None, CTX + warmup + i)
+        dev.copy_async(hist.ptr + 4 * (warmup + i), m.tok, 4)
+    ev.record(e1, stream)
+    host_enqueue_s = time.perf_counter() - h0
+    ms = ev.elapsed_ms(e0, e1)
+    wall_s = time.perf_counter() - h0
+    if m.captures != captures:
+        raise RuntimeError("the decode graph was re-captured inside the timed region")
+    toks = hist.read(np.int32, (warmup + steps,))
+    bad = int(m.bad.read(np.int32, (1,))[0])
+    if bad:
+        raise RuntimeError(f"an index went out of range during decode ({bad})")
+    ms_tok = ms / steps
+    mid_kv = CTX + warmup + steps // 2 + 1
+    tb = token_bytes(cfg, mid_kv)
+
+    # each op class alone, launched over the model's own 32 layers (graph replay, HIP events on the
+    # launch stream): what a token spends where
+    n, E, nq, ff, d = cfg.n_embd, cfg.E, cfg.n_q, cfg.n_ff, dev
+    L = m.layers
+    nl = cfg.n_layer
+    f4 = 4
+    w3 = nq + 2 * E
+    ops = {
+        "mul_mat_norm qkv Q4_K 6144x4096": (
+            lambda i: d.mul_mat_norm(L[i % nl]["wqkv"], m.x, 1, n, cfg.eps, L[i % nl]["attn_norm"], m.qkv, w3,
+                                     stream=stream), nl, mv_bytes(w3, n) + 4 * n, "k_mv_q4k<norm>"),
+        "rope_kv": (lambda i: d.rope_kv(m.qkv, 1, w3, cfg.head_dim, cfg.n_head, cfg.n_head_kv, cfg.head_dim,
+                                        cfg.rope_mode, m.pos_ptr, cfg.rope_base, L[i % nl]["kc"], L[i % nl]["vc"],
+                                        m.cell_ptr, m.bad, stream=stream), nl, 8 * (nq + E) + 8 * E, "k_rope_kv"),
+        "flash_attn (3 launches)": (lambda i: d.flash_attn_plan(m.plan, m.qkv, w3, L[i % nl]["kc"], L[i % nl]["vc"],
+                                                                m.scale, m.att, nq, stream=stream),
+                                    nl, 2 * kv_size * (E // 32) * 34 + 8 * nq, "k_fa_*"),
+        "mul_mat o Q4_K 4096x4096 +res": (lambda i: d.mul_mat(L[i % nl]["wo"], m.att, 1, nq, m.h, n, add=m.x, add_stride=n,
+                                                              stream=stream), nl, mv_bytes(n, nq) + 4 * n, "k_mv_q4k"),
+        "mul_mat_norm+glu gate|up Q4_K 28672x4096": (
+            lambda i: d.mul_mat_norm(L[i % nl]["wgu"], m.h, 1, n, cfg.eps, L[i % nl]["ffn_norm"], m.glu, ff,
+                                     flags=tsr_hip.MM_GLU, stream=stream),
+            nl, q4k_bytes(2 * ff, n) + 8 * n + 4 * ff, "k_mv_q4k<norm,glu>"),
+        "mul_mat down Q4_K 4096x14336 +res": (
+            lambda i: d.mul_mat(L[i % nl]["wd"], m.glu, 1, ff, m.x, n, add=m.h, add_stride=n, stream=stream),
+            nl, mv_bytes(n, ff) + 4 * n, "k_mv_q4k"),
+        "mul_mat_norm output Q4_K 128256x4096": (
+            lambda i: d.mul_mat_norm(m.wout, m.x, 1, n, cfg.eps, m.out_norm, m.logits, cfg.n_vocab, stream=stream),
+            1, mv_bytes(cfg.n_vocab, n) + 4 * n, "k_mv_q4k<norm>"),
+        "argmax": (lambda i: d.argmax(m.logits, cfg.n_vocab, 1, cfg.n_vocab, m.next, stream=stream), 1,
+                   4 * cfg.n_vocab, "k_argmax"),
+        "get_rows": (lambda i: d.get_rows(m.tok_embd, n, n, cfg.n_vocab, m.tok, 1, m.h, n, bad=m.bad, stream=stream), 1,
+                     8 * n, "k_get_rows"),
+    }
+    per_op = {}
+    for name, (fn, count, nbytes, kname) in ops.items():
+        for i in range(3):
+            fn(i)
+        ev.device_sync()
+        t, _ = ev.graph_ms(stream, fn, 2 * nl)
+        per_op[name] = {"launch_us": round(t * 1e3, 3), "per_token": count, "us_per_token": round(t * 1e3 * count, 1),
+                        "GB/s": round(nbytes / (t * 1e-3) / 1e9, 1), "algorithmic_bytes": nbytes, "kernel": kname}
+    ev.device_sync()
+    out = {
+        "cfg": cfg, "wts": wts, "model": m, "kv_size": kv_size, "logits0": logits0, "tokens": toks.tolist(),
+        "ms_per_token": ms_tok, "tok_s": 1e3 / ms_tok, "token_bytes": tb,
+        "host_enqueue_ms_per_token": host_enqueue_s * 1e3 / steps, "wall_ms_per_token": wall_s * 1e3 / steps,
+        "setup_s": setup_s, "per_op": per_op, "captures": captures,
+    }
+    return out
+
+
+def cpu_decode(e2e: dict, max_seconds: float = 12.0, max_tokens: int = 4) -> dict:
+    """The oracle's decode of the same model (the reference numerics restated in C, MUL_MAT on all the
+    host cores available, up to 16) from the same cache state: token 0 at position CTX with the same
+    first id, then the oracle's own greedy tokens, for about max_seconds. Its logits of token 0 are
+    compared bit for bit with the GPU's, and its greedy tokens with the GPU's."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle
+    from oracle_llama import OracleLlama
+    cfg, wts = e2e["cfg"], e2e["wts"]
     oc = oracle.Oracle()
     threads = min(16, os.cpu_count() or 1)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        oc.mul_mat(1, blocks_up, 4096, x[None, :], threads=threads)
-        n += 1
-        dt = time.perf_counter() - t0
-        if dt >= seconds:
+    t = {"token_embd.weight": wts.embedding(), "output_norm.weight": wts.norm("output_norm.weight")[None],
+         "output.weight": wts.quant("output.weight", cfg.n_vocab, cfg.n_embd, cfg.ofmt)}
+    for il in range(cfg.n_layer):
+        for name, N, K in LL.layer_tensors(cfg, il):
+            t[name] = wts.quant(name, N, K, cfg.wfmt)
+        for nm in ("attn_norm", "ffn_norm"):
+            t[f"blk.{il}.{nm}.weight"] = wts.norm(f"blk.{il}.{nm}.weight")[None]
+    kv_size = e2e["kv_size"]
+    ref = OracleLlama(oc, n_layer=cfg.n_layer, n_embd=cfg.n_embd, n_ff=cfg.n_ff, n_head=cfg.n_head,
+                      n_head_kv=cfg.n_head_kv, head_dim=cfg.head_dim, n_vocab=cfg.n_vocab, eps=cfg.eps,
+                      rope_base=cfg.rope_base, rope_mode=cfg.rope_mode, wfmt=cfg.wfmt, ofmt=cfg.ofmt, tensors=t,
+                      kv_size=kv_size, threads=threads)
+    for il in range(cfg.n_layer):
+        for which in (0, 1):
+            ref.set_history(il, which, wts.kv_history(il, which, CTX))
+    libm = C.CDLL("libm.so.6")
+    libm.powf.argtypes = [C.c_float, C.c_float]
+    libm.powf.restype = C.c_float
+    ts = np.float32(libm.powf(float(np.float32(cfg.rope_base)), float(np.float32(-2.0) / np.float32(cfg.head_dim))))
+    gpu_toks = e2e["tokens"]
+    tok, n, times, same_tokens, logits_equal = FIRST_TOKEN, 0, [], True, None
+    while n < max_tokens:
+        pos = CTX + n
+        t0 = time.perf_counter()
+        logits = ref.step(tok, pos, ts, min(kv_size, (pos + 1 + 255) // 256 * 256))
+        times.append(time.perf_counter() - t0)
+        nxt = int(oc.argmax(logits[None])[0])
+        if n == 0:
+            logits_equal = bool(np.array_equal(logits.view(np.uint32), e2e["logits0"].view(np.uint32)))
+        same_tokens &= nxt == gpu_toks[n]
+        tok, n = nxt, n + 1
+        if sum(times) >= max_seconds:
             break
-    per = dt / n
-    return {"value": round(mv_bytes(14336, 4096) / per / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{n} x Q4_K matvec 14336x4096 (oracle/oc_num.c, {threads} threads), {per * 1e3:.1f} ms each"}
+    per = float(np.mean(times))
+    return {"value": round(1.0 / per, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": (f"{n} decode tokens of the same Llama-3-8B-arch Q4_K model at positions {CTX}..{CTX + n - 1} "
+                       f"by oracle/oracle_llama.py over oracle/oc_*.c ({threads} threads in MUL_MAT), "
+                       f"{per:.2f} s per token"),
+            "parity": {"token0_logits_bit_equal": logits_equal, "greedy_tokens_equal": bool(same_tokens),
+                       "tokens_compared": n}}
 
 
 def extra_workloads(dev, ev, stream, n: int) -> dict:
     """The other single-GPU BASELINE configs, each timed over rotating device copies (> 2x MALL):
-    configs[0] Q8_0 matvec 4864x896 and configs[2] q8-KV flash-decode (32 q / 8 KV heads, D 128,
-    n_kv 8192, batch 1). Per-call time from HIP events on the launch stream."""
+    configs[1] the Q4_K FFN up/down pair, configs[0] Q8_0 matvec 4864x896, configs[2] q8-KV
+    flash-decode (32 q / 8 KV heads, D 128, n_kv 8192, batch 1), configs[3] the prefill matmuls and
+    the causal prefill attention. Per-call time from HIP events on the launch stream."""
     out = {}
-    n = max(n, 100)
 
     def timed(fn, nn=None):
         for i in range(5):
@@ -159,6 +337,33 @@ def extra_workloads(dev, ev, stream, n: int) -> dict:
             fn(i)
         ev.record(b, stream)
         return ev.elapsed_ms(a, b) / nn
+
+    # the Llama-3-8B FFN up / down Q4_K matvec pair
+    N_up, K_up, N_dn, K_dn = 14336, 4096, 4096, 14336
+    up_blocks = S.quant_rows(1, S.seed_of("cfg2", "w_up"), N_up, K_up)
+    dn_blocks = S.quant_rows(1, S.seed_of("cfg2", "w_down"), N_dn, K_dn)
+    x = S.normal(S.seed_of("cfg2", "x"), K_up)
+    per_copy = up_blocks.nbytes + dn_blocks.nbytes
+    copies = max(2, -(-2 * MALL_BYTES // per_copy))
+    ups = [dev.weight(1, up_blocks, N_up, K_up) for _ in range(copies)]
+    dns = [dev.weight(1, dn_blocks, N_dn, K_dn) for _ in range(copies)]
+    xb, hb, yb = dev.upload(x), dev.alloc(4 * N_up), dev.alloc(4 * N_dn)
+
+    def step(i):
+        dev.mul_mat(ups[i % copies], xb, 1, K_up, hb, N_up, stream=stream)
+        dev.mul_mat(dns[i % copies], hb, 1, K_dn, yb, N_dn, stream=stream)
+
+    ms, ms_eager = timed(step)
+    up_ms, _ = timed(lambda i: dev.mul_mat(ups[i % copies], xb, 1, K_up, hb, N_up, stream=stream))
+    dn_ms, _ = timed(lambda i: dev.mul_mat(dns[i % copies], hb, 1, K_dn, yb, N_dn, stream=stream))
+    sb = mv_bytes(N_up, K_up) + mv_bytes(N_dn, K_dn)
+    out["ffn_pair_q4k_14336x4096_4096x14336"] = {
+        "us_per_step": round(ms * 1e3, 3), "us_per_step_eager": round(ms_eager * 1e3, 3),
+        "GB/s": round(sb / (ms * 1e-3) / 1e9, 1), "frac_of_hbm_peak": round(sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "up_us": round(up_ms * 1e3, 3), "up_GB/s": round(mv_bytes(N_up, K_up) / (up_ms * 1e-3) / 1e9, 1),
+        "down_us": round(dn_ms * 1e3, 3), "down_GB/s": round(mv_bytes(N_dn, K_dn) / (dn_ms * 1e-3) / 1e9, 1),
+        "copies": copies}
+    del ups, dns
 
     # Q8_0 4864 x 896
     N, K = 4864, 896
@@ -214,7 +419,7 @@ def extra_workloads(dev, ev, stream, n: int) -> dict:
     T, K = 512, 4096
     xq = dev.upload(S.normal(S.seed_of("cfg4", "x"), T * K))
     for name, N in (("prefill_q8_0_512x4096x4096", 4096), ("prefill_q8_0_512x14336x4096", 14336)):
-        blocks = S.quantize_q8_0(S.normal(S.seed_of("cfg4", "w_" + str(N)), N * K, 0.02).reshape(N, K))
+        blocks = S.quant_rows(0, S.seed_of("cfg4", "w_" + str(N)), N, K)
         ws = [dev.weight(0, blocks, N, K) for _ in range(2)]
         yb = dev.alloc(4 * T * N)
         ms, ms_eager = timed(lambda i: dev.mul_mat(ws[i % 2], xq, T, K, yb, N, stream=stream), 20)
@@ -249,28 +454,34 @@ def extra_workloads(dev, ev, stream, n: int) -> dict:
 
 
 COPY_BYTES = 256 << 20          # calibration copy (device to device)
+PMC_SHAPES = {"gate|up": ("ffn_gate", "ffn_up"), "down": ("ffn_down",)}
 
 
-def pmc_child(workdir: str, reps: int = 3) -> int:
+def pmc_child(reps: int = 3) -> int:
     """Counter-collection child (run under rocprofv3 --pmc): a device-to-device copy of COPY_BYTES,
-    then the up and down matvecs, `reps` dispatches each, on the weights the parent saved."""
-    up = np.load(os.path.join(workdir, "up.npy"))
-    dn = np.load(os.path.join(workdir, "dn.npy"))
-    x = np.load(os.path.join(workdir, "x.npy"))
+    then the decode model's layer-0 gate|up (28672x4096, RMS_NORM and SWIGLU fused) and down
+    (4096x14336, residual addend) Q4_K matvecs as the decoder launches them, `reps` dispatches each, on
+    the model's seeded weights."""
+    cfg = LL.LLAMA3_8B
+    wts = LL.SyntheticWeights(cfg)
     dev = tsr_hip.Device(0)
     ev = HipEvents()
     ev.h.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
     src, dst = dev.alloc(COPY_BYTES), dev.alloc(COPY_BYTES)
     src.fill(1)
-    w_up, w_dn = dev.weight(1, up, 14336, 4096), dev.weight(1, dn, 4096, 14336)
-    xb, hb, yb = dev.upload(x), dev.alloc(4 * 14336), dev.alloc(4 * 4096)
+    gu = np.stack([wts.quant("blk.0.ffn_gate.weight", cfg.n_ff, cfg.n_embd, cfg.wfmt),
+                   wts.quant("blk.0.ffn_up.weight", cfg.n_ff, cfg.n_embd, cfg.wfmt)], axis=1).reshape(2 * cfg.n_ff, -1)
+    w_gu = dev.weight(cfg.wfmt, gu, 2 * cfg.n_ff, cfg.n_embd)
+    w_dn = dev.weight(cfg.wfmt, wts.quant("blk.0.ffn_down.weight", cfg.n_embd, cfg.n_ff, cfg.wfmt), cfg.n_embd, cfg.n_ff)
+    xb, gb, yb = dev.upload(S.normal(S.seed_of("pmc", "x"), cfg.n_embd)), dev.alloc(8 * cfg.n_ff), dev.alloc(4 * cfg.n_embd)
+    nw = dev.upload(wts.norm("blk.0.ffn_norm.weight"))
     for _ in range(reps):
         assert ev.h.hipMemcpyAsync(dst.ptr, src.ptr, COPY_BYTES, 3, dev.stream) == 0   # 3: device to device
     ev.device_sync()
-    for _ in range(reps):
-        dev.mul_mat(w_up, xb, 1, 4096, hb, 14336, stream=dev.stream)
-    for _ in range(reps):
-        dev.mul_mat(w_dn, hb, 1, 14336, yb, 4096, stream=dev.stream)
+    for _ in range(reps):      # the decoder's gate|up: RMS_NORM + MUL in front, SWIGLU behind
+        dev.mul_mat_norm(w_gu, xb, 1, cfg.n_embd, cfg.eps, nw, gb, cfg.n_ff, flags=tsr_hip.MM_GLU, stream=dev.stream)
+    for _ in range(reps):      # the decoder's down, residual addend
+        dev.mul_mat(w_dn, gb, 1, cfg.n_ff, yb, cfg.n_embd, add=xb, add_stride=cfg.n_embd, stream=dev.stream)
     ev.device_sync()
     dev.close()
     return 0
@@ -281,7 +492,7 @@ def _pmc_pass(counter: str, workdir: str) -> list:
     dispatch order."""
     out = os.path.join(workdir, "pmc_" + counter)
     cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", counter, "--output-format", "csv",
-           "-d", out, "-o", "pmc", "--", sys.executable, os.path.abspath(__file__), "--pmc-child", workdir]
+           "-d", out, "-o", "pmc", "--", sys.executable, os.path.abspath(__file__), "--pmc-child"]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, cwd=workdir)
     files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
     if r.returncode != 0 and not files:
@@ -295,18 +506,14 @@ def _pmc_pass(counter: str, workdir: str) -> list:
     return sorted(rows)
 
 
-def measure_traffic(up_blocks, dn_blocks, x, reps: int = 3) -> dict:
-    """HBM bytes per launch of the two matvecs: FETCH_SIZE and WRITE_SIZE (KiB per dispatch, two
-    separate rocprofv3 passes), each scaled by the same counter's reading for the calibration copy
-    (COPY_BYTES read and COPY_BYTES written). The child dispatches the copies, then `reps` up
-    matvecs, then `reps` down matvecs."""
+def measure_traffic(reps: int = 3) -> dict:
+    """HBM bytes per launch of the gate|up and down matvecs: FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch, two separate rocprofv3 passes), each scaled by the same counter's reading for the
+    calibration copy (COPY_BYTES read and COPY_BYTES written)."""
     if shutil.which("rocprofv3") is None:
         return {"error": "rocprofv3 not found"}
     workdir = tempfile.mkdtemp(prefix="tsr_pmc_")
     try:
-        np.save(os.path.join(workdir, "up.npy"), up_blocks)
-        np.save(os.path.join(workdir, "dn.npy"), dn_blocks)
-        np.save(os.path.join(workdir, "x.npy"), x)
         res = {}
         for counter in ("FETCH_SIZE", "WRITE_SIZE"):
             rows = _pmc_pass(counter, workdir)
@@ -316,7 +523,7 @@ def measure_traffic(up_blocks, dn_blocks, x, reps: int = 3) -> dict:
                 raise RuntimeError(f"{counter}: unexpected dispatches {[(k, v) for _, k, v in rows][:12]}")
             cal = COPY_BYTES / (float(np.median(copy)) * 1024.0)   # true bytes per counted byte
             res[counter] = {"calibration_factor": round(cal, 4), "copy_KiB": float(np.median(copy)),
-                            "up": float(np.median(mv[:reps])) * 1024.0 * cal,
+                            "gate|up": float(np.median(mv[:reps])) * 1024.0 * cal,
                             "down": float(np.median(mv[reps:])) * 1024.0 * cal}
         return res
     finally:
@@ -326,124 +533,87 @@ def measure_traffic(up_blocks, dn_blocks, x, reps: int = 3) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--copies", type=int, default=0, help="distinct weight copies (0: enough for 2x MALL)")
+    ap.add_argument("--steps", type=int, default=128, help="timed decode tokens")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed decode tokens before them (>= 2)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
-    ap.add_argument("--pmc-child", metavar="DIR", help=argparse.SUPPRESS)
+    ap.add_argument("--eager", action="store_true", help="time the decode tokens as direct launches, not graph replays")
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.pmc_child:
-        return pmc_child(args.pmc_child)
+        return pmc_child()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is a "
                                    "design note in DESIGN.md, not measured)"}))
         return 2
+    if args.warmup < 2 or args.steps < 1:
+        print(json.dumps({"error": "--warmup must be >= 2 (an eager token and the capturing replay) and --steps >= 1"}))
+        return 2
+
+    # traffic passes first: child processes under rocprofv3, before this process touches the GPU
+    traffic = None
+    if not args.no_traffic:
+        try:
+            traffic = measure_traffic()
+        except Exception as e:  # reported, not fatal: the timing below does not depend on it
+            traffic = {"error": str(e)[:300]}
 
     dev = tsr_hip.Device(0)
     info = dev.info()
     stream = dev.stream
     ev = HipEvents()
-
-    N_up, K_up, N_dn, K_dn = 14336, 4096, 4096, 14336
-    up_blocks = S.quantize_q4_k(S.normal(S.seed_of("cfg2", "w_up"), N_up * K_up, 0.02).reshape(N_up, K_up))
-    dn_blocks = S.quantize_q4_k(S.normal(S.seed_of("cfg2", "w_down"), N_dn * K_dn, 0.02).reshape(N_dn, K_dn))
-    x = S.normal(S.seed_of("cfg2", "x"), K_up)
-    # traffic passes first: child processes under rocprofv3, before this process touches the GPU
-    traffic = None
-    if not args.no_traffic:
-        try:
-            traffic = measure_traffic(up_blocks, dn_blocks, x)
-        except Exception as e:  # reported, not fatal: the timing below does not depend on it
-            traffic = {"error": str(e)[:300]}
-    per_copy = up_blocks.nbytes + dn_blocks.nbytes
-    copies = args.copies or max(2, -(-2 * MALL_BYTES // per_copy))
-    ups = [dev.weight(1, up_blocks, N_up, K_up) for _ in range(copies)]
-    dns = [dev.weight(1, dn_blocks, N_dn, K_dn) for _ in range(copies)]
-    xb = dev.upload(x)
-    hb = dev.alloc(4 * N_up)
-    yb = dev.alloc(4 * N_dn)
-
-    def step(i):
-        dev.mul_mat(ups[i % copies], xb, 1, K_up, hb, N_up, stream=stream)
-        dev.mul_mat(dns[i % copies], hb, 1, K_dn, yb, N_dn, stream=stream)
-
-    for i in range(args.warmup):
-        step(i)
-    ev.device_sync()
-    # The K timed steps are one captured graph (the launch-bound decode loop as a serving engine
-    # runs it); one untimed replay first, whose output must equal the eager result bit for bit.
-    g, ge = ev.capture(stream, step, args.steps)
-    assert ev.h.hipGraphLaunch(ge, stream) == 0
-    ev.device_sync()
-    y_graph = yb.read(np.float32, (N_dn,))
-    step(args.steps - 1)
-    ev.device_sync()
-    if not np.array_equal(y_graph.view(np.uint32), yb.read(np.float32, (N_dn,)).view(np.uint32)):
-        print(json.dumps({"error": "graph replay differs from the eager step"}))
-        return 1
-    e0, e1 = ev.event(), ev.event()
-    ev.device_sync()
-    ev.record(e0, stream)
-    assert ev.h.hipGraphLaunch(ge, stream) == 0
-    ev.record(e1, stream)
-    ms = ev.elapsed_ms(e0, e1)
-    ev.device_sync()
-    ev.h.hipGraphExecDestroy(ge)
-    ev.h.hipGraphDestroy(g)
-    ms_step = ms / args.steps
-    ev.record(e0, stream)
-    for i in range(args.steps):
-        step(i)
-    ev.record(e1, stream)
-    ms_step_eager = ev.elapsed_ms(e0, e1) / args.steps
-    step_bytes = mv_bytes(N_up, K_up) + mv_bytes(N_dn, K_dn)
-
-    # per-kernel launch durations (HIP events on the launch stream, graph replay), each over
-    # rotating copies
-    n_k = max(50, args.steps)
-    up_ms, _ = ev.graph_ms(stream, lambda i: dev.mul_mat(ups[i % copies], xb, 1, K_up, hb, N_up, stream=stream), n_k)
-    dn_ms, _ = ev.graph_ms(stream, lambda i: dev.mul_mat(dns[i % copies], hb, 1, K_dn, yb, N_dn, stream=stream), n_k)
-    kern = [("k_mv_q4k (up 14336x4096)", up_ms, mv_bytes(N_up, K_up)),
-            ("k_mv_q4k (down 4096x14336)", dn_ms, mv_bytes(N_dn, K_dn))]
-    name, kms, kbytes = max(kern, key=lambda r: r[1])
-    tag = "up" if "(up" in name else "down"
+    print(f"bench: e2e decode, {args.warmup} warmup + {args.steps} timed tokens after {CTX} cells", file=sys.stderr,
+          flush=True)
+    e2e = e2e_decode(dev, ev, args.steps, args.warmup, eager=args.eager)
+    print(f"bench: {e2e['tok_s']:.1f} tok/s", file=sys.stderr, flush=True)
+    per_op = e2e["per_op"]
+    # the roofline kernel: the single-launch op class with the largest share of a token
+    single = {k: v for k, v in per_op.items() if v["kernel"].startswith("k_mv_q4k")}
+    dom = max(single, key=lambda k: single[k]["us_per_token"])
+    dv = single[dom]
+    tag = "gate|up" if "gate|up" in dom else ("down" if "down" in dom else None)
     traffic_bytes = None
-    if traffic and "error" not in traffic and tag in traffic.get("FETCH_SIZE", {}) and tag in traffic.get("WRITE_SIZE", {}):
+    if tag and traffic and "error" not in traffic:
         traffic_bytes = round(traffic["FETCH_SIZE"][tag] + traffic["WRITE_SIZE"][tag])
-    achieved = kbytes / (kms * 1e-3) / 1e9
+    achieved = dv["algorithmic_bytes"] / (dv["launch_us"] * 1e-6) / 1e9
+    m = e2e.pop("model")
+    m.free()
 
-    y = yb.read(np.float32, (N_dn,))
-    if not np.isfinite(y).all():
-        print(json.dumps({"error": "non-finite output"}))
-        return 1
-
-    also = {} if args.no_extra else extra_workloads(dev, ev, stream, args.steps)
-    cpu = None if args.no_cpu else cpu_baseline(up_blocks, x)
+    also = {} if args.no_extra else extra_workloads(dev, ev, stream, 200)
+    cpu = None if args.no_cpu else cpu_decode(e2e)
+    ms_tok = e2e["ms_per_token"]
     out = {
         "metric": METRIC,
-        "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 2),
-        "unit": "GB/s",
+        "value": round(e2e["tok_s"], 2),
+        "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 5),
-        "ms_per_step_eager": round(ms_step_eager, 5),
+        "ms_per_step": round(ms_tok, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k x q8_k -> f32 (int8 dot, f32 accumulate)",
-        "data": "synthetic: seeded N(0,0.02) weights quantized to Q4_K, N(0,1) activation",
-        "config": {"workload": "Llama-3-8B FFN up+down Q4_K matvec pair, batch 1 (BASELINE configs[1])",
-                   "shapes": "W_up 14336x4096, W_down 4096x14336", "weight_copies": copies,
-                   "copy_bytes": per_copy, "device": info["arch"], "n_cu": info["n_cu"]},
-        "roofline": {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_bytes,
-                     "traffic_detail": traffic,
-                     "launch_us": round(kms * 1e3, 3), "algorithmic_bytes": kbytes,
-                     "other_kernels": {n: {"launch_us": round(t * 1e3, 3), "GB/s": round(b / (t * 1e-3) / 1e9, 1)}
-                                       for n, t, b in kern}},
+        "dtype": "q4_k/q8_0 int8 dot products, f32 accumulate (spec f32 rules)",
+        "data": "synthetic: random-init weights N(0,0.02) quantized to Q4_K, seeded KV rows, greedy tokens",
+        "config": {"workload": "Llama-3-8B-arch Q4_K decode, batch 1, ctx 4096 (BASELINE configs[4])",
+                   "layers": 32, "n_embd": 4096, "n_ff": 14336, "heads": "32 q / 8 kv, head_dim 128",
+                   "n_vocab": 128256, "kv": "q8_0", "kv_cells_before_decode": CTX,
+                   "timed_positions": [CTX + args.warmup, CTX + args.warmup + args.steps - 1],
+                   "timing": ("direct launches per token (--eager)" if args.eager else
+                              "one captured HIP graph per token, replayed") + "; HIP events on the launch stream",
+                   "device": info["arch"], "n_cu": info["n_cu"]},
+        "token": {"algorithmic_bytes": e2e["token_bytes"],
+                  "GB/s": round(e2e["token_bytes"] / (ms_tok * 1e-3) / 1e9, 1),
+                  "frac_of_hbm_peak": round(e2e["token_bytes"] / (ms_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                  "host_enqueue_ms": round(e2e["host_enqueue_ms_per_token"], 4),
+                  "wall_ms": round(e2e["wall_ms_per_token"], 4),
+                  "sum_of_ops_us": round(sum(v["us_per_token"] for v in per_op.values()), 1),
+                  "per_op": per_op, "setup_s": round(e2e["setup_s"], 1)},
+        "roofline": {"bound": "hbm", "kernel": f"{dv['kernel']} ({dom})", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_bytes, "traffic_detail": traffic,
+                     "launch_us": dv["launch_us"], "algorithmic_bytes": dv["algorithmic_bytes"]},
         "cpu_baseline": cpu,
         "also": also,
     }

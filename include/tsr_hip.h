@@ -51,6 +51,11 @@ extern "C" {
 #define TSR_HIP_KV_V        1u
 /* tsr_hip_mul_mat flags (the MUL_MAT record's FLAGS word, sw/ctrl/ref/mulmat_ref.hpp:14-16) */
 #define TSR_HIP_MM_ACC_DST  0x1u  /* y = FA(y_old, W.x) */
+/* The weight's rows 2j and 2j + 1 are the gate and up rows of output j, and y[j] = SWIGLU(gate . x,
+ * up . x) for j < N / 2 -- the MUL_MATs of the FFN gate and up weights followed by GGML_GLU_OP_SWIGLU
+ * (tsr_hip_swiglu), bit-identical, in one launch. No addend, no ACC_DST; the matvec path only (not the
+ * Q8_0 T >= 16 prefill shapes); N even (row blocks are always whole pairs). */
+#define TSR_HIP_MM_GLU      0x2u
 
 typedef struct tsr_hip_ctx tsr_hip_ctx;
 typedef struct tsr_hip_weight tsr_hip_weight;
@@ -126,6 +131,16 @@ int tsr_hip_qact(tsr_hip_ctx * ctx, uint32_t kind, const float * x_dev, uint32_t
 int tsr_hip_mul_mat(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T, uint64_t x_stride,
                     float * y_dev, uint64_t y_stride, const float * add_dev, uint64_t add_stride, uint32_t flags,
                     void * stream);
+/* MUL_MAT of RMS_NORM(x) * norm_w in one launch, bit-identical to tsr_hip_rms_norm over n = K with
+ * norm_w_dev (nullable: no MUL) and w_period 1 followed by tsr_hip_mul_mat on its output (the fused
+ * RMS_NORM + MUL record, sw/ggml-tesseract/ggml-tesseract.cpp:33, 426, feeding the Q|K|V and FFN
+ * MUL_MATs of the decoder layer, sw/ctrl/tests/test_fw_m7_layer.cpp:646-686). The reference runs the
+ * norm as its own record before the MUL_MAT; here it runs inside the matvec's activation
+ * quantization. Flags, addend as tsr_hip_mul_mat (TSR_HIP_MM_GLU included). K <= 8192 and not the
+ * Q8_0 T >= 16 prefill shapes, else TSR_HIP_E_SHAPE: run the two ops separately. */
+int tsr_hip_mul_mat_norm(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T,
+                         uint64_t x_stride, float eps, const float * norm_w_dev, float * y_dev, uint64_t y_stride,
+                         const float * add_dev, uint64_t add_stride, uint32_t flags, void * stream);
 /* The exact integer part of MUL_MAT for checking: for token 0, the per-block sums of every row
  * (Q8_0: isum per 32-block, N x K/32; Q4_K: isum and msum per super-block interleaved,
  * N x 2K/256) as the MVM computes them (term_q8_0 / term_q4_K, sw/sim/tsr_ref.c:525-567). */
@@ -148,6 +163,18 @@ int tsr_hip_kv_get_bytes(tsr_hip_ctx * ctx, const tsr_hip_kv * kv, uint32_t whic
  * out-of-range index stores nothing and sets *bad_dev if bad_dev is not NULL). */
 int tsr_hip_kv_set_rows(tsr_hip_ctx * ctx, tsr_hip_kv * kv, uint32_t which, const float * src_dev, uint32_t n_rows,
                         uint64_t src_stride, const int64_t * idx_dev, int32_t * bad_dev, void * stream);
+
+/* The decoder layer's ROPE of q and k followed by SET_ROWS_KV of k and v (the ROPE, SET_ROWS_KV records
+ * of sw/ctrl/tests/test_fw_m7_layer.cpp:646-686) in one launch, bit-identical to tsr_hip_rope over the
+ * n_head + n_head_kv q and k heads (freq_scale 1, no freq factors) in place, then tsr_hip_kv_set_rows of
+ * the rotated k into kc and of v into vc. Token t's row at qkv_dev + t * stride holds n_head q heads,
+ * n_head_kv k heads and n_head_kv v heads of head_dim floats (head_dim % 32 == 0; the row at most 16384
+ * floats); its position is pos_dev[t] (int32) and its cell cell_dev[t] (int64), both on the device. A
+ * cell outside either cache stores nothing and sets *bad_dev (nullable). */
+int tsr_hip_rope_kv(tsr_hip_ctx * ctx, float * qkv_dev, uint32_t T, uint64_t stride, uint32_t head_dim, uint32_t n_head,
+                    uint32_t n_head_kv, uint32_t n_dims, int mode, const int32_t * pos_dev, float freq_base,
+                    float attn_factor, tsr_hip_kv * kc, tsr_hip_kv * vc, const int64_t * cell_dev, int32_t * bad_dev,
+                    void * stream);
 
 /* ---- FA plans ------------------------------------------------------------------------------------
  * The work list of FLASH_ATTN_EXT kept in device memory, so that graphs of planned launches replay

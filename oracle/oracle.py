@@ -336,6 +336,8 @@ def _o_add(self, a, b) -> np.ndarray:
 def _o_get_rows(self, src, ids) -> np.ndarray:
     src = np.ascontiguousarray(np.atleast_2d(src), np.float32)
     ids = np.ascontiguousarray(ids, np.int32)
+    if ids.size and (ids.min() < 0 or ids.max() >= src.shape[0]):
+        raise IndexError(f"get_rows: id outside [0, {src.shape[0]})")
     out = np.empty((ids.size, src.shape[1]), np.float32)
     self.lib.oc_get_rows(src.shape[1], src, src.shape[1], ids, ids.size, out, src.shape[1])
     return out

@@ -22,8 +22,9 @@ class OracleLlama:
     token_embd.weight (f32 [n_vocab, n_embd])."""
 
     def __init__(self, oc, *, n_layer, n_embd, n_ff, n_head, n_head_kv, head_dim, n_vocab, eps, rope_base,
-                 rope_mode, wfmt, ofmt, tensors, kv_size):
+                 rope_mode, wfmt, ofmt, tensors, kv_size, threads=1):
         self.oc = oc
+        self.threads = threads
         self.n_layer, self.n_embd, self.n_ff = n_layer, n_embd, n_ff
         self.n_head, self.n_head_kv, self.D, self.n_vocab = n_head, n_head_kv, head_dim, n_vocab
         self.eps, self.rope_base, self.neox = eps, rope_base, rope_mode != 0
@@ -50,19 +51,19 @@ class OracleLlama:
         for il in range(self.n_layer):
             b = f"blk.{il}."
             xn = oc.rms_norm(x, self.eps, t[b + "attn_norm.weight"])
-            q = oc.mul_mat(self.wfmt, t[b + "attn_q.weight"], self.n_embd, xn)
-            k = oc.mul_mat(self.wfmt, t[b + "attn_k.weight"], self.n_embd, xn)
-            v = oc.mul_mat(self.wfmt, t[b + "attn_v.weight"], self.n_embd, xn)
+            q = oc.mul_mat(self.wfmt, t[b + "attn_q.weight"], self.n_embd, xn, threads=self.threads)
+            k = oc.mul_mat(self.wfmt, t[b + "attn_k.weight"], self.n_embd, xn, threads=self.threads)
+            v = oc.mul_mat(self.wfmt, t[b + "attn_v.weight"], self.n_embd, xn, threads=self.threads)
             q = oc.rope(q, posv, D, D, self.neox, ts)
             k = oc.rope(k, posv, D, D, self.neox, ts)
             oc.kv_set_rows(self.kc[il], k, np.array([pos], np.int64))
             oc.kv_set_rows(self.vc[il], v, np.array([pos], np.int64))
             a = oc.flash_attn(q, self.kc[il], self.vc[il], D, self.n_head, self.n_head_kv, float(self.scale), msum,
                               new_runs=runs)
-            h = oc.mul_mat(self.wfmt, t[b + "attn_output.weight"], self.n_head * D, a, add=x)
+            h = oc.mul_mat(self.wfmt, t[b + "attn_output.weight"], self.n_head * D, a, add=x, threads=self.threads)
             hn = oc.rms_norm(h, self.eps, t[b + "ffn_norm.weight"])
-            g = oc.mul_mat(self.wfmt, t[b + "ffn_gate.weight"], self.n_embd, hn)
-            u = oc.mul_mat(self.wfmt, t[b + "ffn_up.weight"], self.n_embd, hn)
-            x = oc.mul_mat(self.wfmt, t[b + "ffn_down.weight"], self.n_ff, oc.swiglu(g, u), add=h)
+            g = oc.mul_mat(self.wfmt, t[b + "ffn_gate.weight"], self.n_embd, hn, threads=self.threads)
+            u = oc.mul_mat(self.wfmt, t[b + "ffn_up.weight"], self.n_embd, hn, threads=self.threads)
+            x = oc.mul_mat(self.wfmt, t[b + "ffn_down.weight"], self.n_ff, oc.swiglu(g, u), add=h, threads=self.threads)
         xn = oc.rms_norm(x, self.eps, t["output_norm.weight"])
-        return oc.mul_mat(self.ofmt, t["output.weight"], self.n_embd, xn)[0]
+        return oc.mul_mat(self.ofmt, t["output.weight"], self.n_embd, xn, threads=self.threads)[0]

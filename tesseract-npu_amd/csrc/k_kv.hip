@@ -11,6 +11,7 @@
 // The conversion to / from the ggml image (row j = cell j, E/32 blocks of {fp16 d, int8 qs[32]}) is
 // a byte permutation, like the NPU's planes (tsr_kv_set_bytes / get_bytes, sw/sim/tsr_ref_at.c:178-212).
 #include "kernels.hpp"
+#include "kvstore.hpp"
 #include "qact.hpp"
 
 namespace tsr {
@@ -47,24 +48,13 @@ __global__ __launch_bounds__(64) void k_kv_set_rows(KvArgs a, uint32_t which, co
         if (bad != nullptr && lane == 0) *bad = 1;
         return;
     }
-    const uint32_t cell = (uint32_t)cell64, u = cell >> 4, rr = cell & 15u, nbk = a.E / 32u;
+    const uint32_t cell = (uint32_t)cell64;
     const uint32_t slot = blockIdx.x * 64u + lane;            // values 4 slot .. 4 slot + 3
     if (slot >= a.E / 4u) return;
     const float4 v = *(const float4 *)(src + (size_t)r * src_stride + 4u * slot);
     float D;
     const uint32_t q = qact_a32_lane(v, &D);
-    const uint32_t i = 4u * slot;
-    uint8_t * qb = a.base + a.quant_off + (size_t)u * 16u * a.E;
-    if (which == 0u) {
-        *(uint32_t *)(qb + ((size_t)(i >> 4) * 16u + rr) * 16u + (i & 15u)) = q;
-    } else {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) qb[(size_t)(i + k) * 16u + rr] = (uint8_t)(q >> (8 * k));
-    }
-    if ((lane & 7u) == 0u) {
-        uint16_t * meta = (uint16_t *)(a.base + (size_t)u * 16u * nbk * 2u);
-        meta[(size_t)rr * nbk + i / 32u] = (uint16_t)f2h_exact(D);
-    }
+    kv_store_unit(a, which, cell, 4u * slot, q, D, (lane & 7u) == 0u);
 }
 
 }  // namespace tsr

@@ -24,6 +24,8 @@
 // 2^-107, and so is every term and every sum of terms: nothing is ever subnormal. A wave that
 // quantizes a block with 0 < |Dx| < 2^-60 computes its terms with the spec operations, and then the
 // partial sums and the tree of the workgroup do too.
+#include "expk.hpp"
+#include "glue.hpp"
 #include "kernels.hpp"
 #include "qact.hpp"
 #include "tsr_hip.h"
@@ -67,8 +69,13 @@ __device__ __forceinline__ void mv_wave_partials(const WGeom & g, const float * 
 // After a workgroup barrier: the 16-partial tree of each row on an aligned 16-lane row of threads
 // (lane i holds p[i]; the DPP pairs xor 1, xor 2, half mirror, mirror are the tree's pairs, and
 // f32 addition is commutative), then y. Every thread of the workgroup calls it.
+// GLU: weight rows 2j and 2j + 1 are the gate and up rows of output j (the workgroup's row block starts
+// at an even row and holds whole pairs); the pair's two results meet by a swizzle (their 16-lane rows
+// are lanes xor 16 apart) and y[j] = SWIGLU(gate, up) -- the GGML_GLU_OP_SWIGLU that follows the
+// gate and up MUL_MATs, computed once per output. t64: lane j holds the EXPK table entry j.
+template <bool GLU>
 __device__ __forceinline__ void mv_tree_store(const MvArgs & a, const float * s_p, uint32_t nrow, uint32_t row_lo,
-                                              uint32_t t, bool slow) {
+                                              uint32_t t, bool slow, uint32_t t64) {
     for (uint32_t base = 0; base < nrow * 16u; base += blockDim.x) {   // uniform trip count
         const uint32_t idx = base + threadIdx.x, rl = idx >> 4;
         float v = rl < nrow ? s_p[idx] : 0.0f;
@@ -84,7 +91,13 @@ __device__ __forceinline__ void mv_tree_store(const MvArgs & a, const float * s_
             v = sadd(v, dpp_f<kDppRowHalfMirror>(v));
             v = sadd(v, dpp_f<kDppRowMirror>(v));
         }
-        if ((idx & 15u) == 0u && rl < nrow) store_y(a, t, row_lo + rl, v);
+        if constexpr (GLU) {
+            const float u = xor16_f(v);                               // the up row of the pair
+            const float h = swiglu_reg(v, u, a.ex, t64);              // every lane: the table is read by bpermute
+            if ((idx & 31u) == 0u && rl < nrow) a.y[(size_t)t * a.y_stride + ((row_lo + rl) >> 1)] = h;
+        } else {
+            if ((idx & 15u) == 0u && rl < nrow) store_y(a, t, row_lo + rl, v);
+        }
     }
 }
 
@@ -115,13 +128,55 @@ __device__ __forceinline__ MvUnit mv_unit(uint32_t p, int lane, uint32_t R, uint
     return m;
 }
 
+// ---- fused x preparation (MvArgs::prep) and GLU epilogue -------------------------------------------
+// kPrepNorm: every wave squares the x values it loaded (FM(x, x)) into s_sq at their index; after an
+// LDS barrier threads 0 .. 127 run the 128 RED partials in order and the tree (glue.hpp), thread 0
+// forms the scale s, and after another barrier every wave turns its values into FM(FM(x, s), pw) --
+// exactly RMS_NORM + MUL, before QACT. Launched only when every value of x is loaded by some wave in
+// the first round (K <= 8192, the host checks), so s_sq is complete. The loads of x and pw are
+// straight-line with compile-time indices, issued before the weight stream, and the preparation
+// waits only for them.
+__device__ __forceinline__ float4 prep_norm_apply(float4 v, float s, float4 w, bool has_w) {
+    v.x = smul(v.x, s); v.y = smul(v.y, s); v.z = smul(v.z, s); v.w = smul(v.w, s);
+    if (has_w) { v.x = smul(v.x, w.x); v.y = smul(v.y, w.y); v.z = smul(v.z, w.z); v.w = smul(v.w, w.w); }
+    return v;
+}
+__device__ __forceinline__ float4 sq4(float4 v) { return make_float4(smul(v.x, v.x), smul(v.y, v.y), smul(v.z, v.z), smul(v.w, v.w)); }
+// The RMS scale from s_sq[0 .. K): every thread of the workgroup calls it (three LDS barriers inside);
+// returns s in every thread. s_sq[K] and s_sq[K + 1] are the exchange slots.
+__device__ __forceinline__ float prep_norm_scale(float * s_sq, uint32_t K, float inv_n, float eps) {
+    lds_barrier();
+    float p = 0.0f;
+    if (threadIdx.x < 128u) {
+        for (uint32_t j0 = 0; j0 < K; j0 += 1024u) {
+            float v[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k) {
+                const uint32_t j = j0 + threadIdx.x + 128u * k;
+                v[k] = j < K ? s_sq[j] : 0.0f;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 8u; ++k)
+                if (j0 + threadIdx.x + 128u * k < K) p = sadd_n(p, v[k]);
+        }
+        p = rms_tree64(p);
+        if (threadIdx.x == 64u) s_sq[K + 1u] = p;
+    }
+    lds_barrier();
+    if (threadIdx.x == 0u) s_sq[K] = rms_scale(p, s_sq[K + 1u], inv_n, eps);
+    lds_barrier();
+    return s_sq[K];
+}
+
 // ---------------------------------------------------------------------------------------------
 // Q4_K. LDS: x quants [16 waves][kx][272 B] | sub-block sums [16][kx][8] int | d [16][kx] |
 // terms [rb][nsb] | partials [rb][16] | slow flags [16].
 // Lane unit = (row, super-block): 8 quant loads (piece j: group g = j / 2, low nibbles = values
 // 64g + 16 (j % 2) + 0..15, high nibbles = the same + 32) and one meta load.
 // ---------------------------------------------------------------------------------------------
-template <int P, bool ISUMS>      // P: passes whose loads are in registers at once
+// XM: 0 -- each wave picks its x form (one block: the whole-wave form); 1 / 2 -- every wave takes the
+// one-block / four-block form (the fused preparation, whose loads and indices are then compile-time).
+template <int P, bool ISUMS, int PREP, int XM, bool GLU>      // P: passes whose loads are in registers at once
 __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const WGeom g = wgeom(a.N, a.K >> 8, a.rb, true);
@@ -138,21 +193,34 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     float * s_t = s_xd + kMvWaves * kx;
     float * s_p = s_t + ((a.rb * nsb + 3u) & ~3u);                // 16-byte aligned
     int * s_slow = (int *)(s_p + a.rb * 16u);
+    float * s_sq = (float *)(s_slow + 16);                        // kPrepNorm: K squares + 2 slots
 
     // x first (vector-memory counters retire in order): the 16-lane row h = lane / 16 of the wave
     // holds block k = 4 i + h of round i, lane i of the row its values 16 i .. 16 i + 15
     // A wave with one block (cnt == 1) quantizes it with the whole wave instead (lane l: values
     // 4 l .. 4 l + 3), a quarter of the per-lane work.
     const uint32_t h4 = (uint32_t)lane >> 4, l16 = (uint32_t)lane & 15u;
-    const bool one = cnt <= 1u;                                   // wave-uniform
+    const bool one = XM == 0 ? cnt <= 1u : XM == 1;               // wave-uniform
     auto load_x = [&](uint32_t i, float4 (&xr)[4]) {
         const uint32_t s = min(w + 16u * (4u * i + h4), nsb - 1u);
 #pragma unroll
         for (int c = 0; c < 4; ++c) xr[c] = *(const float4 *)(x + 256u * s + 16u * l16 + 4u * (uint32_t)c);
     };
-    float4 xv[4];
-    if (one) xv[0] = *(const float4 *)(x + 256u * min(w, nsb - 1u) + 4u * (uint32_t)lane);
+    auto xoff = [&](uint32_t c) -> uint32_t {                      // offset of float4 c of round 0
+        return one ? 256u * min(w, nsb - 1u) + 4u * (uint32_t)lane
+                   : 256u * min(w + 16u * h4, nsb - 1u) + 16u * l16 + 4u * c;
+    };
+    constexpr int NV = XM == 1 ? 1 : 4;                           // float4s of x per lane (prep forms)
+    float4 xv[4], pv[NV];
+    if (one) xv[0] = *(const float4 *)(x + xoff(0u));
     else load_x(0u, xv);
+    if constexpr (PREP == kPrepNorm) {
+        const float * pl = a.pw ? a.pw : x;                       // without MUL: a valid address, unused
+#pragma unroll
+        for (int c = 0; c < NV; ++c) pv[c] = *(const float4 *)(pl + xoff((uint32_t)c));
+    }
+    uint32_t t64 = 0;
+    if constexpr (GLU) t64 = a.ex.t64[lane];
     x_first_barrier();
 
     uint4 qv[P][8], mv[P];
@@ -203,11 +271,27 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     // to issue anyway, and their QACT is then off the critical path. Waves 0..11 keep the memory
     // pipe busy from the start and quantize while their loads are in flight (a wave blocked on
     // issuing a load cannot quantize; the split was measured: 12 beats 4, 8 and none).
-    if (w >= 12u && cnt) qact_first();
-    load(0u);                                                     // unconditional (clamped)
-    __builtin_amdgcn_sched_barrier(0);
-    if (w < 12u && cnt) qact_first();
-    for (uint32_t i = 1; 4u * i < cnt; ++i) {                     // K > 16384 only
+    if constexpr (PREP == kPrepNone) {
+        if (w >= 12u && cnt) qact_first();
+        load(0u);                                                 // unconditional (clamped)
+        __builtin_amdgcn_sched_barrier(0);
+        if (w < 12u && cnt) qact_first();
+    } else {
+        load(0u);                                                 // the norm runs under the weight stream
+        __builtin_amdgcn_sched_barrier(0);
+        float4 sq[NV];
+#pragma unroll
+        for (int c = 0; c < NV; ++c) sq[c] = sq4(xv[c]);
+        if (XM == 1 ? cnt == 1u : h4 < cnt) {                     // this lane's values are x's (not clamped copies)
+#pragma unroll
+            for (int c = 0; c < NV; ++c) *(float4 *)(s_sq + xoff((uint32_t)c)) = sq[c];
+        }
+        const float sc = prep_norm_scale(s_sq, a.K, a.inv_n, a.eps);
+#pragma unroll
+        for (int c = 0; c < NV; ++c) xv[c] = prep_norm_apply(xv[c], sc, pv[c], a.pw != nullptr);
+        if (cnt) qact_first();
+    }
+    for (uint32_t i = 1; 4u * i < cnt; ++i) {                     // K > 16384 only (never with a prep)
         float4 xr[4];
         load_x(i, xr);
         qact_round(i, xr);
@@ -278,7 +362,7 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     bool any_slow = false;
 #pragma unroll
     for (int i = 0; i < kMvWaves; ++i) any_slow |= s_slow[i] != 0;
-    mv_tree_store(a, s_p, nrow, row_lo, t, any_slow);
+    mv_tree_store<GLU>(a, s_p, nrow, row_lo, t, any_slow, t64);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -286,7 +370,7 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
 // Lane unit = (row, block): two 16-byte quant loads and the fp16 scale. The A32 activation scale is
 // an fp16 value, so every term is exact with plain IEEE operations.
 // ---------------------------------------------------------------------------------------------
-template <int P, bool ISUMS>
+template <int P, bool ISUMS, int PREP, bool GLU>
 __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const WGeom g = wgeom(a.N, a.K >> 5, a.rb, false);
@@ -301,16 +385,24 @@ __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
     float * s_xd = (float *)(lds + kMvWaves * kx * 32u);
     float * s_t = s_xd + kMvWaves * kx;
     float * s_p = s_t + ((a.rb * nb + 3u) & ~3u);                 // 16-byte aligned
+    float * s_sq = s_p + a.rb * 16u;                              // kPrepNorm: K squares + 2 slots
 
     // x: 8 lanes per block; round i covers blocks k = 8 i + lane / 8 of this wave
     constexpr int XP = 2;
-    float4 xv[XP];
+    float4 xv[XP], pv[XP];                                        // pv: norm weights
+    auto xoff = [&](uint32_t i) -> uint32_t {
+        const uint32_t k = 8u * i + ((uint32_t)lane >> 3);
+        return 32u * min(w + 16u * k, nb - 1u) + 4u * ((uint32_t)lane & 7u);
+    };
 #pragma unroll
-    for (int i = 0; i < XP; ++i) {
-        const uint32_t k = 8u * (uint32_t)i + ((uint32_t)lane >> 3);
-        const uint32_t b = min(w + 16u * k, nb - 1u);
-        xv[i] = *(const float4 *)(x + 32u * b + 4u * ((uint32_t)lane & 7u));
+    for (int i = 0; i < XP; ++i) xv[i] = *(const float4 *)(x + xoff((uint32_t)i));
+    if constexpr (PREP == kPrepNorm) {
+        const float * pl = a.pw ? a.pw : x;                       // without MUL: a valid address, unused
+#pragma unroll
+        for (int i = 0; i < XP; ++i) pv[i] = *(const float4 *)(pl + xoff((uint32_t)i));
     }
+    uint32_t t64 = 0;
+    if constexpr (GLU) t64 = a.ex.t64[lane];
     x_first_barrier();
 
     uint4 q0[P], q1[P];
@@ -327,6 +419,17 @@ __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
     };
     load(0u);                                                     // unconditional: no join before QACT
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PREP == kPrepNorm) {
+        float4 sq[XP];
+#pragma unroll
+        for (int i = 0; i < XP; ++i) sq[i] = sq4(xv[i]);
+#pragma unroll
+        for (int i = 0; i < XP; ++i)
+            if (8u * (uint32_t)i + ((uint32_t)lane >> 3) < cnt) *(float4 *)(s_sq + xoff((uint32_t)i)) = sq[i];
+        const float sc = prep_norm_scale(s_sq, a.K, a.inv_n, a.eps);
+#pragma unroll
+        for (int i = 0; i < XP; ++i) xv[i] = prep_norm_apply(xv[i], sc, pv[i], a.pw != nullptr);
+    }
 
     auto qact_round = [&](uint32_t i, const float4 v) {
         const uint32_t k = 8u * i + ((uint32_t)lane >> 3);
@@ -340,11 +443,8 @@ __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
 #pragma unroll
     for (int i = 0; i < XP; ++i)
         if (8u * (uint32_t)i < cnt) qact_round((uint32_t)i, xv[i]);
-    for (uint32_t i = XP; 8u * i < cnt; ++i) {
-        const uint32_t k = 8u * i + ((uint32_t)lane >> 3);
-        const uint32_t b = min(w + 16u * k, nb - 1u);
-        qact_round(i, *(const float4 *)(x + 32u * b + 4u * ((uint32_t)lane & 7u)));
-    }
+    for (uint32_t i = XP; 8u * i < cnt; ++i)                     // K > 8192 only (never with a prep)
+        qact_round(i, *(const float4 *)(x + xoff(i)));
 
     for (uint32_t p0 = 0; p0 < npass; p0 += P) {
         if (p0) load(p0);
@@ -372,7 +472,7 @@ __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
     }
     mv_wave_partials(g, s_t, s_p, nrow, w, false);
     lds_barrier();
-    mv_tree_store(a, s_p, nrow, row_lo, t, false);
+    mv_tree_store<GLU>(a, s_p, nrow, row_lo, t, false, t64);
 }
 
 }  // namespace tsr
@@ -395,38 +495,85 @@ uint32_t tsr_wl_rows_per_block(uint32_t fmt, uint32_t N, uint32_t K, uint32_t n_
     const size_t fixed = mv_lds_fixed(fmt, nb);
     uint32_t rb = (N + n_cu - 1u) / n_cu;
     if (rb < 16u) rb = 16u;
-    while (rb > 1u && fixed + mv_lds_rows(rb, nb) > 120u * 1024u) rb = (rb + 1u) / 2u;
+    rb += rb & 1u;                       // even: whole gate / up pairs per workgroup (GLU)
+    while (rb > 2u && fixed + mv_lds_rows(rb, nb) > 120u * 1024u) rb = (rb / 2u + 1u) & ~1u;
     return rb;
 }
 
-template <int P>
+size_t tsr_mv_prep_lds(uint32_t prep, uint32_t K) {
+    return prep == tsr::kPrepNorm ? (4u * ((size_t)K + 2u) + 15u) & ~(size_t)15u : 0u;
+}
+
+template <int P, int PREP, int XM, bool GLU>
 static void launch_q4k(const tsr::MvArgs & a, dim3 grid, size_t lds, hipStream_t s) {
-    if (a.isums) hipLaunchKernelGGL((tsr::k_mv_q4k<P, true>), grid, dim3(1024), lds, s, a);
-    else hipLaunchKernelGGL((tsr::k_mv_q4k<P, false>), grid, dim3(1024), lds, s, a);
+    if constexpr (PREP == tsr::kPrepNone && XM == 0 && !GLU) {
+        if (a.isums) {
+            hipLaunchKernelGGL((tsr::k_mv_q4k<P, true, PREP, XM, GLU>), grid, dim3(1024), lds, s, a);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((tsr::k_mv_q4k<P, false, PREP, XM, GLU>), grid, dim3(1024), lds, s, a);
+}
+template <int P, int PREP, bool GLU>
+static void launch_q80(const tsr::MvArgs & a, dim3 grid, size_t lds, hipStream_t s) {
+    if constexpr (PREP == tsr::kPrepNone && !GLU) {
+        if (a.isums) {
+            hipLaunchKernelGGL((tsr::k_mv_q80<P, true, PREP, GLU>), grid, dim3(1024), lds, s, a);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((tsr::k_mv_q80<P, false, PREP, GLU>), grid, dim3(1024), lds, s, a);
 }
 template <int P>
-static void launch_q80(const tsr::MvArgs & a, dim3 grid, size_t lds, hipStream_t s) {
-    if (a.isums) hipLaunchKernelGGL((tsr::k_mv_q80<P, true>), grid, dim3(1024), lds, s, a);
-    else hipLaunchKernelGGL((tsr::k_mv_q80<P, false>), grid, dim3(1024), lds, s, a);
+static void launch_q80_v(const tsr::MvArgs & a, dim3 grid, size_t lds, hipStream_t s) {
+    if (a.prep == tsr::kPrepNorm) {
+        if (a.glu) launch_q80<P, tsr::kPrepNorm, true>(a, grid, lds, s);
+        else launch_q80<P, tsr::kPrepNorm, false>(a, grid, lds, s);
+    } else {
+        if (a.glu) launch_q80<P, tsr::kPrepNone, true>(a, grid, lds, s);
+        else launch_q80<P, tsr::kPrepNone, false>(a, grid, lds, s);
+    }
+}
+
+// The fused norm needs every value of x loaded in the kernel's first round: K <= 8192 (Q4_K: at most 4
+// super-blocks per wave, Q8_0 at most 16 blocks), which also bounds its LDS. GLU needs whole pairs of
+// rows in every workgroup (even rb and N) and stores N / 2 outputs (no addend or accumulation).
+static bool variant_ok(const tsr::MvArgs & a) {
+    if (a.prep != tsr::kPrepNone && (a.isums != nullptr || a.K > 8192u)) return false;
+    if (a.glu && (a.isums != nullptr || (a.rb & 1u) || (a.N & 1u) || a.add != nullptr || a.acc)) return false;
+    return true;
 }
 
 int tsr_launch_mv_q4_k(const tsr::MvArgs & a, hipStream_t s) {
+    if (!variant_ok(a)) return -2;
     const uint32_t nsb = a.K / 256u;
-    const size_t lds = mv_lds_fixed(TSR_HIP_FMT_Q4_K, nsb) + mv_lds_rows(a.rb, nsb);
+    const size_t lds = mv_lds_fixed(TSR_HIP_FMT_Q4_K, nsb) + mv_lds_rows(a.rb, nsb) + tsr_mv_prep_lds(a.prep, a.K);
     const dim3 grid((a.N + a.rb - 1u) / a.rb, a.T);
-    launch_q4k<1>(a, grid, lds, s);                               // 36 load registers per pass
+    if (a.prep == tsr::kPrepNorm) {                               // 36 load registers per pass
+        if (nsb <= 16u) {                                         // every wave: one super-block at most
+            if (a.glu) launch_q4k<1, tsr::kPrepNorm, 1, true>(a, grid, lds, s);
+            else launch_q4k<1, tsr::kPrepNorm, 1, false>(a, grid, lds, s);
+        } else {
+            if (a.glu) launch_q4k<1, tsr::kPrepNorm, 2, true>(a, grid, lds, s);
+            else launch_q4k<1, tsr::kPrepNorm, 2, false>(a, grid, lds, s);
+        }
+    } else {
+        if (a.glu) launch_q4k<1, tsr::kPrepNone, 0, true>(a, grid, lds, s);
+        else launch_q4k<1, tsr::kPrepNone, 0, false>(a, grid, lds, s);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 int tsr_launch_mv_q8_0(const tsr::MvArgs & a, hipStream_t s) {
+    if (!variant_ok(a)) return -2;
     const uint32_t nb = a.K / 32u;
-    const size_t lds = mv_lds_fixed(TSR_HIP_FMT_Q8_0, nb) + mv_lds_rows(a.rb, nb);
+    const size_t lds = mv_lds_fixed(TSR_HIP_FMT_Q8_0, nb) + mv_lds_rows(a.rb, nb) + tsr_mv_prep_lds(a.prep, a.K);
     const dim3 grid((a.N + a.rb - 1u) / a.rb, a.T);
     // passes of the wave with the most units: rb rows x ceil(nb / 16) slots, 64 units a pass
     const uint32_t mp = (a.rb * ((nb + 15u) / 16u) + 63u) / 64u;
-    if (mp <= 1u) launch_q80<1>(a, grid, lds, s);
-    else if (mp <= 2u) launch_q80<2>(a, grid, lds, s);
-    else if (mp <= 4u) launch_q80<4>(a, grid, lds, s);
-    else launch_q80<8>(a, grid, lds, s);
+    if (mp <= 1u) launch_q80_v<1>(a, grid, lds, s);
+    else if (mp <= 2u) launch_q80_v<2>(a, grid, lds, s);
+    else if (mp <= 4u) launch_q80_v<4>(a, grid, lds, s);
+    else launch_q80_v<8>(a, grid, lds, s);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }

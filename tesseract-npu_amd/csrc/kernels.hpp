@@ -15,6 +15,19 @@ struct QactArgs {
     uint32_t d_off, bs_off;  // byte offsets of the D and BS regions
 };
 
+// EXPK constants (VU 6.3): LK = round(log2(e) 2^38), c_k = round(ln(2)^k / k! 2^32),
+// t64[j] = round(2^(j/64) 2^30); computed on the host from their definitions.
+struct ExpkTab {
+    uint32_t t64[64];
+    uint64_t lk, c1, c2, c3;
+};
+
+// What the matvec applies to x in front of its activation quantization (MvArgs::prep).
+enum MvPrep : uint32_t {
+    kPrepNone = 0,           // x as given
+    kPrepNorm = 1,           // RMS_NORM of the token row, times pw when pw != 0 (k_rms_norm's rule)
+};
+
 // MUL_MAT over the device weight layout of wlayout.hpp (row blocks of rb rows at w).
 struct MvArgs {
     const uint8_t * w;
@@ -28,6 +41,11 @@ struct MvArgs {
     uint32_t N, K, T;
     uint32_t acc;            // y = FA(y_old, v)
     uint32_t rb;             // rows per row block = per workgroup (the weight's)
+    uint32_t prep;           // MvPrep
+    const float * pw;        // kPrepNorm: the MUL weight [K] (nullable)
+    float eps, inv_n;        // kPrepNorm
+    uint32_t glu;            // rows 2j, 2j + 1 are gate / up of output j: y[j] = SWIGLU(gate, up), N / 2 outputs
+    ExpkTab ex;              // glu
 };
 
 // Prefill MUL_MAT (T >= 16) on the matrix cores: the activations are first quantized (k_qact_mm)
@@ -50,13 +68,6 @@ struct KvArgs {
     uint8_t * base;          // meta region at 0
     size_t quant_off;        // byte offset of the quant region
     uint32_t E, kv_size;
-};
-
-// EXPK constants (VU 6.3): LK = round(log2(e) 2^38), c_k = round(ln(2)^k / k! 2^32),
-// t64[j] = round(2^(j/64) 2^30); computed on the host from their definitions.
-struct ExpkTab {
-    uint32_t t64[64];
-    uint64_t lk, c1, c2, c3;
 };
 
 // One chunk of one query token (the planner's output), in execution order per token.
@@ -110,6 +121,20 @@ struct RopeArgs {
     uint32_t fs;             // freq_scale != 1
 };
 
+// ROPE of the q and k heads of a fused Q|K|V row, then SET_ROWS_KV of the rotated k and of v
+// (one workgroup per token). Token t's row is at qkv + t * stride: n_head q heads, n_head_kv k
+// heads, n_head_kv v heads of head_dim values; q and k are rotated in place.
+struct RopeKvArgs {
+    float * qkv;
+    uint64_t stride;
+    const int32_t * pos;     // [T] positions
+    const int64_t * cell;    // [T] cache cells
+    int32_t * bad;           // nullable: set when a cell is outside the caches
+    KvArgs kc, vc;
+    uint32_t head_dim, n_head, n_head_kv, n_dims, neox;
+    float ts, m;             // TS = powf(freq_base, -2 / n_dims); M = attn_factor
+};
+
 }  // namespace tsr
 
 int tsr_launch_qact(const tsr::QactArgs & a, uint32_t T, hipStream_t s);
@@ -135,3 +160,6 @@ int tsr_launch_add(const float * a, uint64_t a_stride, const float * b, uint64_t
 int tsr_launch_get_rows(const float * src, uint64_t src_stride, uint32_t n, uint32_t n_src, const int32_t * ids,
                         uint32_t count, float * dst, uint64_t dst_stride, int32_t * bad, hipStream_t s);
 int tsr_launch_argmax(const float * x, uint64_t x_stride, uint32_t n, uint32_t rows, int32_t * out, hipStream_t s);
+int tsr_launch_rope_kv(const tsr::RopeKvArgs & a, uint32_t T, hipStream_t s);
+// LDS bytes the fused x preparation adds to a matvec launch (0 when none)
+size_t tsr_mv_prep_lds(uint32_t prep, uint32_t K);

@@ -1,6 +1,8 @@
 // tsr_attn.hip -- host side of the KV cache, the mask summary and FLASH_ATTN_EXT.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
+
 #include <algorithm>
 #include <cstring>
 #include <mutex>
@@ -99,6 +101,43 @@ int tsr_hip_kv_set_rows(tsr_hip_ctx * ctx, tsr_hip_kv * kv, uint32_t which, cons
     return tsr_launch_kv_set_rows(kv_args(kv), which, src_dev, n_rows, src_stride, idx_dev, bad_dev, ctx->pick(stream))
                ? TSR_HIP_E_HIP
                : TSR_HIP_OK;
+}
+
+int tsr_hip_rope_kv(tsr_hip_ctx * ctx, float * qkv_dev, uint32_t T, uint64_t stride, uint32_t head_dim, uint32_t n_head,
+                    uint32_t n_head_kv, uint32_t n_dims, int mode, const int32_t * pos_dev, float freq_base,
+                    float attn_factor, tsr_hip_kv * kc, tsr_hip_kv * vc, const int64_t * cell_dev, int32_t * bad_dev,
+                    void * stream) {
+    if (ctx == nullptr || qkv_dev == nullptr || pos_dev == nullptr || cell_dev == nullptr || kc == nullptr ||
+        vc == nullptr || T == 0u)
+        return TSR_HIP_E_ARG;
+    if (mode != TSR_HIP_ROPE_NORMAL && mode != TSR_HIP_ROPE_NEOX && mode != TSR_HIP_ROPE_IMROPE) return TSR_HIP_E_SHAPE;
+    const uint64_t E = (uint64_t)n_head_kv * head_dim, nrow = (uint64_t)n_head * head_dim + 2u * E;
+    if (head_dim == 0u || head_dim % 32u != 0u || n_head == 0u || n_head_kv == 0u || n_dims < 2u || n_dims % 2u != 0u ||
+        n_dims > head_dim || n_dims > 1024u || nrow > 16384u || T > 0x7FFFFFFFu)
+        return TSR_HIP_E_SHAPE;
+    if (kc->E != E || vc->E != E) return TSR_HIP_E_SHAPE;
+    if (((uintptr_t)qkv_dev & 15u) != 0u || (T > 1u && (stride % 4u != 0u || stride < nrow))) return TSR_HIP_E_ARG;
+    if (!(freq_base > 0.0f) || !std::isfinite(freq_base)) return TSR_HIP_E_ARG;
+    tsr::RopeKvArgs a{};
+    a.qkv = qkv_dev;
+    a.stride = stride;
+    a.pos = pos_dev;
+    a.cell = cell_dev;
+    a.bad = bad_dev;
+    a.kc = kv_args(kc);
+    a.vc = kv_args(vc);
+    a.head_dim = head_dim;
+    a.n_head = n_head;
+    a.n_head_kv = n_head_kv;
+    a.n_dims = n_dims;
+    a.neox = mode != TSR_HIP_ROPE_NORMAL ? 1u : 0u;
+    a.ts = powf(freq_base, -2.0f / (float)n_dims);                  // the host libm, as tsr_hip_rope
+    a.m = attn_factor;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    ctx->ctr.set_rows_calls += 2u;
+    const int rc = tsr_launch_rope_kv(a, T, ctx->pick(stream));
+    return rc == -2 ? TSR_HIP_E_SHAPE : (rc ? TSR_HIP_E_HIP : TSR_HIP_OK);
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -408,14 +408,33 @@ int tsr_hip_qact(tsr_hip_ctx * ctx, uint32_t kind, const float * x_dev, uint32_t
 // ---------------------------------------------------------------------------------------------
 // MUL_MAT
 // ---------------------------------------------------------------------------------------------
+// What a fused MUL_MAT applies to x first (tsr_hip_mul_mat_norm).
+struct MmPrep {
+    uint32_t kind;           // tsr::MvPrep
+    const float * pw;        // kPrepNorm: MUL weight (nullable)
+    float eps, inv_n;
+};
+
 // The caller holds ctx->mtx.
 static int mul_mat_locked(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T,
                           uint64_t x_stride, float * y_dev, uint64_t y_stride, const float * add_dev,
-                          uint64_t add_stride, uint32_t flags, int32_t * isums, hipStream_t s) {
+                          uint64_t add_stride, uint32_t flags, int32_t * isums, hipStream_t s,
+                          const MmPrep * prep = nullptr) {
     if (w == nullptr || x_dev == nullptr || y_dev == nullptr || T == 0u) return TSR_HIP_E_ARG;
-    if ((flags & ~TSR_HIP_MM_ACC_DST) != 0u || (add_dev != nullptr && (flags & TSR_HIP_MM_ACC_DST))) return TSR_HIP_E_ARG;
+    const bool glu = (flags & TSR_HIP_MM_GLU) != 0u;
+    if (prep != nullptr || glu) {
+        // the fused forms run on the matvec kernels (not the matrix-core prefill shapes); the norm needs
+        // the whole row in one round of loads: K <= 8192; GLU pairs whole rows in every row block
+        if ((prep != nullptr && w->K > 8192u) || (T >= kMmMinTokens && w->fmt == TSR_HIP_FMT_Q8_0) ||
+            (glu && ((w->N & 1u) || (w->rb & 1u))))
+            return TSR_HIP_E_SHAPE;
+        if (prep != nullptr && prep->pw != nullptr && !aligned16(prep->pw)) return TSR_HIP_E_ARG;
+        if (glu && (add_dev != nullptr || (flags & TSR_HIP_MM_ACC_DST) || isums != nullptr)) return TSR_HIP_E_ARG;
+    }
+    if ((flags & ~(TSR_HIP_MM_ACC_DST | TSR_HIP_MM_GLU)) != 0u || (add_dev != nullptr && (flags & TSR_HIP_MM_ACC_DST)))
+        return TSR_HIP_E_ARG;
     if (!aligned16(x_dev) || (T > 1u && x_stride % 4u != 0u)) return TSR_HIP_E_ARG;
-    if (T > 1u && (x_stride < w->K || y_stride < w->N)) return TSR_HIP_E_ARG;
+    if (T > 1u && (x_stride < w->K || y_stride < (glu ? w->N / 2u : w->N))) return TSR_HIP_E_ARG;
     (void)hipSetDevice(ctx->device);
     tsr::MvArgs a{};
     const size_t nb = w->K / blk_values(w->fmt);
@@ -431,6 +450,16 @@ static int mul_mat_locked(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
     a.N = w->N;
     a.K = w->K;
     a.acc = (flags & TSR_HIP_MM_ACC_DST) ? 1u : 0u;
+    if (prep != nullptr) {
+        a.prep = prep->kind;
+        a.pw = prep->pw;
+        a.eps = prep->eps;
+        a.inv_n = prep->inv_n;
+    }
+    if (glu) {
+        a.glu = 1u;
+        a.ex = ctx->expk;
+    }
     ctx->ctr.mul_mat_calls++;
     ctx->ctr.mul_mat_rows += (uint64_t)w->N * T;
     ctx->ctr.mul_mat_weight_bytes += (uint64_t)w->N * nb * blk_bytes(w->fmt);
@@ -483,6 +512,20 @@ int tsr_hip_mul_mat(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x
     std::lock_guard<std::mutex> lk(ctx->mtx);
     return mul_mat_locked(ctx, w, x_dev, T, x_stride, y_dev, y_stride, add_dev, add_stride, flags, nullptr,
                           ctx->pick(stream));
+}
+
+int tsr_hip_mul_mat_norm(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T,
+                         uint64_t x_stride, float eps, const float * norm_w_dev, float * y_dev, uint64_t y_stride,
+                         const float * add_dev, uint64_t add_stride, uint32_t flags, void * stream) {
+    if (ctx == nullptr || w == nullptr) return TSR_HIP_E_ARG;
+    MmPrep p{};
+    p.kind = tsr::kPrepNorm;
+    p.pw = norm_w_dev;
+    p.eps = eps;
+    p.inv_n = 1.0f / (float)w->K;                                   // correctly rounded (IEEE division)
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    return mul_mat_locked(ctx, w, x_dev, T, x_stride, y_dev, y_stride, add_dev, add_stride, flags, nullptr,
+                          ctx->pick(stream), &p);
 }
 
 int tsr_hip_mul_mat_isums(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, int32_t * isums_dev,

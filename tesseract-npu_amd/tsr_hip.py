@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(HERE, "libtsr_hip.so")
 FMT_Q8_0, FMT_Q4_K = 0, 1
 QA_A32, QA_A256 = 0, 1
 KV_K, KV_V = 0, 1
-MM_ACC_DST = 1
+MM_ACC_DST, MM_GLU = 1, 2
 ROPE_NORMAL, ROPE_NEOX, ROPE_IMROPE = 0, 2, 40
 
 # the exported symbols of include/tsr_hip.h
@@ -35,6 +35,7 @@ EXPORTS = (
     "tsr_hip_rms_norm", "tsr_hip_rope", "tsr_hip_swiglu", "tsr_hip_add", "tsr_hip_get_rows", "tsr_hip_argmax",
     "tsr_hip_write_async", "tsr_hip_copy_async", "tsr_hip_fa_plan_create", "tsr_hip_fa_plan_set", "tsr_hip_flash_attn_plan",
     "tsr_hip_fa_plan_free", "tsr_hip_graph_begin", "tsr_hip_graph_end", "tsr_hip_graph_launch", "tsr_hip_graph_free",
+    "tsr_hip_mul_mat_norm", "tsr_hip_rope_kv",
 )
 
 
@@ -102,6 +103,9 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "tsr_hip_graph_end": ([vp, vp, C.POINTER(vp)], C.c_int),
         "tsr_hip_graph_launch": ([vp, vp, vp], C.c_int),
         "tsr_hip_graph_free": ([vp, vp], C.c_int),
+        "tsr_hip_mul_mat_norm": ([vp, vp, vp, u32, u64, C.c_float, vp, vp, u64, vp, u64, u32, vp], C.c_int),
+        "tsr_hip_rope_kv": ([vp, vp, u32, u64, u32, u32, u32, u32, C.c_int, vp, C.c_float, C.c_float, vp, vp, vp, vp,
+                             vp], C.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -353,6 +357,22 @@ class Device:
                 flags: int = 0, stream=None) -> None:
         _check(self.L.tsr_hip_mul_mat(self.ctx, w.h, self._p(x), T, x_stride, self._p(y), y_stride, self._p(add),
                                       add_stride, flags, stream), "mul_mat")
+
+    def mul_mat_norm(self, w: Weight, x, T: int, x_stride: int, eps: float, norm_w, y, y_stride: int, add=None,
+                     add_stride: int = 0, flags: int = 0, stream=None) -> None:
+        """MUL_MAT of RMS_NORM(x) * norm_w (norm_w None: no MUL) in one launch; flags as mul_mat (MM_GLU:
+        rows 2j, 2j+1 of w are gate / up of output j, y[j] = SWIGLU(gate, up))."""
+        _check(self.L.tsr_hip_mul_mat_norm(self.ctx, w.h, self._p(x), T, x_stride, float(eps), self._p(norm_w),
+                                           self._p(y), y_stride, self._p(add), add_stride, flags, stream),
+               "mul_mat_norm")
+
+    def rope_kv(self, qkv, T: int, stride: int, head_dim: int, n_head: int, n_head_kv: int, n_dims: int, mode: int,
+                pos, freq_base: float, kc: KvCache, vc: KvCache, cell, bad=None, attn_factor: float = 1.0,
+                stream=None) -> None:
+        """ROPE of the q and k heads of fused Q|K|V rows in place, then SET_ROWS_KV of k and v, in one launch."""
+        _check(self.L.tsr_hip_rope_kv(self.ctx, self._p(qkv), T, stride, head_dim, n_head, n_head_kv, n_dims, mode,
+                                      self._p(pos), float(freq_base), float(attn_factor), kc.h, vc.h, self._p(cell),
+                                      self._p(bad), stream), "rope_kv")
 
     def mul_mat_isums(self, w: Weight, x, isums, stream=None) -> None:
         _check(self.L.tsr_hip_mul_mat_isums(self.ctx, w.h, self._p(x), self._p(isums), stream), "mul_mat_isums")

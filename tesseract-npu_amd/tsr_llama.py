@@ -15,6 +15,12 @@ One decode step (T = 1) runs the op list of the reference's decoder-layer test
     X   = MUL_MAT(Wdown, SWIGLU(G, U)) + H
 
 then logits = MUL_MAT(Woutput, RMS_NORM(X) * output_norm) and the greedy token is the ARGMAX.
+
+With fused=True (the default) a layer is eight launches, three of them FLASH_ATTN_EXT: RMS_NORM + MUL
+runs inside the Q|K|V and gate|up MUL_MATs (tsr_hip_mul_mat_norm), SWIGLU in the epilogue of the
+gate|up MUL_MAT (TSR_HIP_MM_GLU over gate / up rows interleaved), and ROPE with both SET_ROWS_KV in
+one kernel (tsr_hip_rope_kv), each bit-identical to the ops it replaces; fused=False runs every op
+of the list as its own call.
 The token embedding is a GET_ROWS of an f32 table. Row concatenation leaves every row's result
 unchanged (each output row is its own dot product with the same quantized activation), and ROPE
 of q and k heads in one launch is the same per-head rotation. A residual addend is one FA(add, v),
@@ -117,8 +123,9 @@ class LlamaDecoder:
     """The model on one device: weights uploaded once, one q8_0 K and V cache per layer of kv_size
     cells, and the activation buffers of one decode token."""
 
-    def __init__(self, dev: H.Device, cfg: LlamaConfig, weights: SyntheticWeights, kv_size: int):
+    def __init__(self, dev: H.Device, cfg: LlamaConfig, weights: SyntheticWeights, kv_size: int, fused: bool = True):
         self.dev, self.cfg, self.kv_size = dev, cfg, kv_size
+        self.fused = fused
         c = cfg
         f4 = 4
         self.tok_embd = dev.upload(np.ascontiguousarray(weights.embedding(), np.float32))
@@ -131,7 +138,9 @@ class LlamaDecoder:
                 "wqkv": dev.weight(c.wfmt, np.concatenate([t["attn_q"], t["attn_k"], t["attn_v"]]), c.n_q + 2 * c.E,
                                    c.n_embd),
                 "wo": dev.weight(c.wfmt, t["attn_output"], c.n_embd, c.n_q),
-                "wgu": dev.weight(c.wfmt, np.concatenate([t["ffn_gate"], t["ffn_up"]]), 2 * c.n_ff, c.n_embd),
+                # fused: gate / up rows interleaved (row 2j = gate j, 2j + 1 = up j) for the GLU epilogue
+                "wgu": dev.weight(c.wfmt, np.stack([t["ffn_gate"], t["ffn_up"]], axis=1).reshape(2 * c.n_ff, -1)
+                                  if fused else np.concatenate([t["ffn_gate"], t["ffn_up"]]), 2 * c.n_ff, c.n_embd),
                 "wd": dev.weight(c.wfmt, t["ffn_down"], c.n_embd, c.n_ff),
                 "kc": dev.kv(c.E, kv_size),
                 "vc": dev.kv(c.E, kv_size),
@@ -198,27 +207,40 @@ class LlamaDecoder:
         nq, E, n = c.n_q, c.E, c.n_embd
         f4 = 4
         d.get_rows(self.tok_embd, n, n, c.n_vocab, self.tok, 1, self.x, n, bad=self.bad, stream=stream)
+        w3 = nq + 2 * E
         for L in self.layers:
-            d.rms_norm(self.x, n, 1, n, c.eps, self.xn, n, w=L["attn_norm"], w_stride=n, stream=stream)
-            d.mul_mat(L["wqkv"], self.xn, 1, n, self.qkv, nq + 2 * E, stream=stream)
-            d.rope(self.qkv, 1, nq + 2 * E, c.head_dim, c.n_head + c.n_head_kv, c.head_dim, c.rope_mode, self.pos_ptr,
-                   c.rope_base, self.qkv, nq + 2 * E, stream=stream)
-            d.kv_set_rows(L["kc"], 0, self.qkv.ptr + nq * f4, 1, E, self.cell_ptr, self.bad, stream=stream)
-            d.kv_set_rows(L["vc"], 1, self.qkv.ptr + (nq + E) * f4, 1, E, self.cell_ptr, self.bad, stream=stream)
+            if self.fused:
+                d.mul_mat_norm(L["wqkv"], self.x, 1, n, c.eps, L["attn_norm"], self.qkv, w3, stream=stream)
+                d.rope_kv(self.qkv, 1, w3, c.head_dim, c.n_head, c.n_head_kv, c.head_dim, c.rope_mode, self.pos_ptr,
+                          c.rope_base, L["kc"], L["vc"], self.cell_ptr, self.bad, stream=stream)
+            else:
+                d.rms_norm(self.x, n, 1, n, c.eps, self.xn, n, w=L["attn_norm"], w_stride=n, stream=stream)
+                d.mul_mat(L["wqkv"], self.xn, 1, n, self.qkv, w3, stream=stream)
+                d.rope(self.qkv, 1, w3, c.head_dim, c.n_head + c.n_head_kv, c.head_dim, c.rope_mode, self.pos_ptr,
+                       c.rope_base, self.qkv, w3, stream=stream)
+                d.kv_set_rows(L["kc"], 0, self.qkv.ptr + nq * f4, 1, E, self.cell_ptr, self.bad, stream=stream)
+                d.kv_set_rows(L["vc"], 1, self.qkv.ptr + (nq + E) * f4, 1, E, self.cell_ptr, self.bad, stream=stream)
             if msum is not None:
-                d.flash_attn(self.qkv, 1, nq + 2 * E, L["kc"], L["vc"], c.head_dim, c.n_head, c.n_head_kv, self.scale,
+                d.flash_attn(self.qkv, 1, w3, L["kc"], L["vc"], c.head_dim, c.n_head, c.n_head_kv, self.scale,
                              msum, self.att, nq, new_runs=runs, stream=stream)
             else:
-                d.flash_attn_plan(self.plan, self.qkv, nq + 2 * E, L["kc"], L["vc"], self.scale, self.att, nq,
-                                  stream=stream)
+                d.flash_attn_plan(self.plan, self.qkv, w3, L["kc"], L["vc"], self.scale, self.att, nq, stream=stream)
             d.mul_mat(L["wo"], self.att, 1, nq, self.h, n, add=self.x, add_stride=n, stream=stream)
-            d.rms_norm(self.h, n, 1, n, c.eps, self.xn, n, w=L["ffn_norm"], w_stride=n, stream=stream)
-            d.mul_mat(L["wgu"], self.xn, 1, n, self.gu, 2 * c.n_ff, stream=stream)
-            d.swiglu(self.gu, 2 * c.n_ff, self.gu.ptr + c.n_ff * f4, 2 * c.n_ff, c.n_ff, 1, self.glu, c.n_ff,
-                     stream=stream)
-            d.mul_mat(L["wd"], self.glu, 1, c.n_ff, self.x, n, add=self.h, add_stride=n, stream=stream)
-        d.rms_norm(self.x, n, 1, n, c.eps, self.xn, n, w=self.out_norm, w_stride=n, stream=stream)
-        d.mul_mat(self.wout, self.xn, 1, n, self.logits, c.n_vocab, stream=stream)
+            if self.fused:
+                d.mul_mat_norm(L["wgu"], self.h, 1, n, c.eps, L["ffn_norm"], self.glu, c.n_ff, flags=H.MM_GLU,
+                               stream=stream)
+                d.mul_mat(L["wd"], self.glu, 1, c.n_ff, self.x, n, add=self.h, add_stride=n, stream=stream)
+            else:
+                d.rms_norm(self.h, n, 1, n, c.eps, self.xn, n, w=L["ffn_norm"], w_stride=n, stream=stream)
+                d.mul_mat(L["wgu"], self.xn, 1, n, self.gu, 2 * c.n_ff, stream=stream)
+                d.swiglu(self.gu, 2 * c.n_ff, self.gu.ptr + c.n_ff * f4, 2 * c.n_ff, c.n_ff, 1, self.glu, c.n_ff,
+                         stream=stream)
+                d.mul_mat(L["wd"], self.glu, 1, c.n_ff, self.x, n, add=self.h, add_stride=n, stream=stream)
+        if self.fused:
+            d.mul_mat_norm(self.wout, self.x, 1, n, c.eps, self.out_norm, self.logits, c.n_vocab, stream=stream)
+        else:
+            d.rms_norm(self.x, n, 1, n, c.eps, self.xn, n, w=self.out_norm, w_stride=n, stream=stream)
+            d.mul_mat(self.wout, self.xn, 1, n, self.logits, c.n_vocab, stream=stream)
         d.argmax(self.logits, c.n_vocab, 1, c.n_vocab, out_tok, stream=stream)
 
     def step(self, token: int | None, pos: int, n_kv: int | None = None) -> None:
@@ -253,6 +275,18 @@ class LlamaDecoder:
             self.graph = g
             self.captures += 1
         self.graph.launch()
+
+    def step_async(self, token: int | None, pos: int, n_kv: int | None = None) -> None:
+        """The launches of step_graph issued directly (no graph): the device-resident plan, the
+        position / cell and the plan copied in stream order, the greedy token fed back on the device.
+        Nothing waits for the device."""
+        d = self.dev
+        msum, runs = self._mask(pos, n_kv)
+        if token is not None:
+            d.write_async(self.tok, np.array([token], np.int32))
+        d.write_async(self.params, self._params(pos))
+        self.plan.set(msum, runs)
+        self._ops(self.tok)
 
     def generate_graph(self, first_token: int, pos0: int, n_tokens: int, hist=None) -> None:
         """Greedy decode of n_tokens by graph replays, without waiting for the device; the token

@@ -1,0 +1,189 @@
+"""GPU fused decode-layer entry points through the C ABI, bit for bit against the oracle's separate
+ops on the same seeded inputs: MUL_MAT of RMS_NORM(x) * w (tsr_hip_mul_mat_norm), the gate / up
+MUL_MAT with its SWIGLU epilogue (TSR_HIP_MM_GLU) and ROPE + SET_ROWS_KV (tsr_hip_rope_kv)."""
+import numpy as np
+import pytest
+
+import tsr_hip as H
+import tsr_synth as S
+from helpers import assert_bits_equal, special_row
+from test_gpu_glue import SPECIALS, theta_scale
+
+pytestmark = pytest.mark.gpu
+
+
+def _x_rows(K, T, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((T, K)) * rng.uniform(0.05, 20, (T, 1))).astype(np.float32)
+    x[0] = special_row(K, seed)
+    return x
+
+
+@pytest.mark.parametrize("fmt,N,K,T", [
+    (H.FMT_Q4_K, 6144, 4096, 1),        # Llama-3-8B Q|K|V
+    (H.FMT_Q4_K, 28672, 4096, 1),       # Llama-3-8B gate|up
+    (H.FMT_Q4_K, 300, 2048, 3),         # waves without super-blocks
+    (H.FMT_Q4_K, 257, 8192, 2),         # two super-blocks per wave
+    (H.FMT_Q8_0, 4864, 896, 1),         # Qwen2.5-0.5B FFN-up
+    (H.FMT_Q8_0, 1000, 8192, 2),        # sixteen blocks per wave
+    (H.FMT_Q8_0, 70, 4096, 5),
+], ids=lambda v: str(v))
+def test_mul_mat_norm(dev, oc, fmt, N, K, T):
+    print(f"\nmul_mat_norm fmt {fmt} {N}x{K} T {T}", flush=True)
+    blocks = S.quant_rows(fmt, S.seed_of("fused-norm", f"{fmt}-{N}-{K}"), N, K)
+    x = _x_rows(K, T, N + K + T)
+    rng = np.random.default_rng(K)
+    nw = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    nw[:SPECIALS.size] = SPECIALS
+    add = rng.standard_normal((T, N)).astype(np.float32)
+    wt = dev.weight(fmt, blocks, N, K)
+    xb, nb, yb, ab = dev.upload(x), dev.upload(nw), dev.alloc(4 * T * N), dev.upload(add)
+    for eps, w in ((1e-5, nw), (1e-6, None)):
+        xn = oc.rms_norm(x, eps, None if w is None else w[None])
+        dev.mul_mat_norm(wt, xb, T, K, eps, None if w is None else nb, yb, N)
+        assert_bits_equal(yb.read(np.float32, (T, N)), oc.mul_mat(fmt, blocks, K, xn, threads=8),
+                          f"norm eps={eps} w={w is not None}")
+        dev.mul_mat_norm(wt, xb, T, K, eps, None if w is None else nb, yb, N, add=ab, add_stride=N)
+        assert_bits_equal(yb.read(np.float32, (T, N)), oc.mul_mat(fmt, blocks, K, xn, add=add, threads=8),
+                          f"norm + addend eps={eps}")
+    wt.free()
+
+
+def test_mul_mat_norm_specials(dev, oc):
+    """Rows whose squares or scale hit the rule's special cases: zeros, subnormals, an overflowing sum,
+    NaN and Inf, tiny rows whose scaled values quantize with the spec operations."""
+    K, N = 4096, 512
+    blocks = S.quant_rows(H.FMT_Q4_K, S.seed_of("fused-norm", "specials"), N, K)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((7, K)).astype(np.float32)
+    x[0] = 0.0
+    x[1] = np.float32(3e-39)
+    x[2] *= np.float32(1e19)
+    x[3, 17] = np.nan
+    x[4, 99] = np.inf
+    x[5] *= np.float32(1e-30)
+    x[6, :SPECIALS.size] = SPECIALS
+    nw = rng.standard_normal(K).astype(np.float32)
+    nw[5] = np.float32(1e-40)
+    wt = dev.weight(H.FMT_Q4_K, blocks, N, K)
+    yb = dev.alloc(4 * 7 * N)
+    dev.mul_mat_norm(wt, dev.upload(x), 7, K, 1e-5, dev.upload(nw), yb, N)
+    want = oc.mul_mat(H.FMT_Q4_K, blocks, K, oc.rms_norm(x, 1e-5, nw[None]), threads=8)
+    assert_bits_equal(yb.read(np.float32, (7, N)), want, "norm specials")
+    wt.free()
+
+
+@pytest.mark.parametrize("fmt,F,K,T,norm", [
+    (H.FMT_Q4_K, 14336, 4096, 1, True),   # Llama-3-8B gate|up with the ffn norm
+    (H.FMT_Q4_K, 14336, 4096, 1, False),
+    (H.FMT_Q4_K, 300, 2048, 2, True),
+    (H.FMT_Q4_K, 64, 24576, 1, False),    # later rounds of x loads
+    (H.FMT_Q8_0, 4864, 896, 1, True),     # Qwen2.5-0.5B gate|up
+    (H.FMT_Q8_0, 100, 8192, 3, True),
+    (H.FMT_Q8_0, 77, 14336, 2, False),
+], ids=lambda v: str(v))
+def test_mul_mat_glu(dev, oc, fmt, F, K, T, norm):
+    """TSR_HIP_MM_GLU over interleaved gate / up rows: y = SWIGLU(gate . x', up . x') with x' = x or
+    RMS_NORM(x) * w, against the oracle's MUL_MATs of the two weights and its SWIGLU."""
+    print(f"\nmul_mat glu fmt {fmt} F {F} K {K} T {T} norm {norm}", flush=True)
+    gate = S.quant_rows(fmt, S.seed_of("fused-glu", f"g-{fmt}-{F}-{K}"), F, K)
+    up = S.quant_rows(fmt, S.seed_of("fused-glu", f"u-{fmt}-{F}-{K}"), F, K)
+    inter = np.stack([gate, up], axis=1).reshape(2 * F, -1)
+    x = _x_rows(K, T, F + K)
+    nw = (1.0 + 0.1 * np.random.default_rng(F).standard_normal(K)).astype(np.float32)
+    xn = oc.rms_norm(x, 1e-5, nw[None]) if norm else x
+    g = oc.mul_mat(fmt, gate, K, xn, threads=8)
+    u = oc.mul_mat(fmt, up, K, xn, threads=8)
+    want = oc.swiglu(g, u)
+    wt = dev.weight(fmt, inter, 2 * F, K)
+    xb, yb = dev.upload(x), dev.alloc(4 * T * F)
+    if norm:
+        dev.mul_mat_norm(wt, xb, T, K, 1e-5, dev.upload(nw), yb, F, flags=H.MM_GLU)
+    else:
+        dev.mul_mat(wt, xb, T, K, yb, F, flags=H.MM_GLU)
+    assert_bits_equal(yb.read(np.float32, (T, F)), want, "glu")
+    wt.free()
+
+
+def test_fused_shape_refusals(dev):
+    blocks = S.quant_rows(H.FMT_Q4_K, 1, 16, 16384)
+    wt = dev.weight(H.FMT_Q4_K, blocks, 16, 16384)
+    b = dev.alloc(4 * 16384 * 16)
+    with pytest.raises(H.TsrHipError) as e:                              # norm over K > 8192
+        dev.mul_mat_norm(wt, b, 1, 16384, 1e-5, None, b, 16)
+    assert e.value.code == -2
+    w8 = dev.weight(H.FMT_Q8_0, S.quant_rows(H.FMT_Q8_0, 2, 32, 256), 32, 256)
+    with pytest.raises(H.TsrHipError):                                   # the matrix-core prefill shape
+        dev.mul_mat_norm(w8, b, 16, 256, 1e-5, None, b, 32)
+    with pytest.raises(H.TsrHipError):                                   # GLU with an addend
+        dev.mul_mat(w8, b, 1, 256, b, 16, add=b, flags=H.MM_GLU)
+    w7 = dev.weight(H.FMT_Q8_0, S.quant_rows(H.FMT_Q8_0, 3, 31, 256), 31, 256)
+    with pytest.raises(H.TsrHipError) as e:                              # GLU over an odd row count
+        dev.mul_mat(w7, b, 1, 256, b, 15, flags=H.MM_GLU)
+    assert e.value.code == -2
+    for w in (wt, w8, w7):
+        w.free()
+
+
+@pytest.mark.parametrize("mode,hd,nh,nkv,T", [
+    (H.ROPE_NORMAL, 128, 32, 8, 1),     # Llama-3-8B
+    (H.ROPE_NEOX, 128, 32, 8, 1),
+    (H.ROPE_NEOX, 64, 14, 2, 3),        # Qwen2.5-0.5B
+    (H.ROPE_NORMAL, 256, 8, 1, 2),
+    (H.ROPE_IMROPE, 128, 16, 4, 2),
+], ids=lambda v: str(v))
+def test_rope_kv(dev, oc, mode, hd, nh, nkv, T):
+    rng = np.random.default_rng(hd * nh + nkv + T + mode)
+    E, nq = nkv * hd, nh * hd
+    w3 = nq + 2 * E
+    kv_size = 300
+    x = rng.standard_normal((T, w3)).astype(np.float32)
+    x[0, nq:nq + SPECIALS.size] = SPECIALS                              # specials in k
+    x[-1, nq + E + 5:nq + E + 5 + SPECIALS.size] = SPECIALS             # and in v
+    pos = rng.integers(0, 70000, T).astype(np.int32)
+    cells = rng.choice(kv_size, T, replace=False).astype(np.int64)
+    base = 500000.0 if mode == H.ROPE_NORMAL else 1000000.0
+    ts = theta_scale(base, hd)
+    kc, vc = dev.kv(E, kv_size), dev.kv(E, kv_size)
+    k0 = rng.integers(0, 256, (kv_size, E // 32 * 34), dtype=np.uint8)
+    v0 = rng.integers(0, 256, (kv_size, E // 32 * 34), dtype=np.uint8)
+    kc.set_bytes(0, k0)
+    vc.set_bytes(1, v0)
+    xb, bad = dev.upload(x), dev.upload(np.zeros(1, np.int32))
+    dev.rope_kv(xb, T, w3, hd, nh, nkv, hd, mode, dev.upload(pos), base, kc, vc, dev.upload(cells), bad)
+    neox = mode != H.ROPE_NORMAL
+    q = oc.rope(np.ascontiguousarray(x[:, :nq]), pos, hd, hd, neox, ts)
+    k = oc.rope(np.ascontiguousarray(x[:, nq:nq + E]), pos, hd, hd, neox, ts)
+    got = xb.read(np.float32, (T, w3))
+    assert_bits_equal(got[:, :nq], q, "rotated q")
+    assert_bits_equal(got[:, nq:nq + E], k, "rotated k")
+    assert_bits_equal(got[:, nq + E:], x[:, nq + E:], "v untouched")
+    kw, vw = k0.copy(), v0.copy()
+    oc.kv_set_rows(kw, k, cells)
+    oc.kv_set_rows(vw, np.ascontiguousarray(x[:, nq + E:]), cells)
+    assert (kc.get_bytes(0).reshape(kv_size, -1) == kw).all()
+    assert (vc.get_bytes(1).reshape(kv_size, -1) == vw).all()
+    assert bad.read(np.int32, (1,))[0] == 0
+    kc.free()
+    vc.free()
+
+
+def test_rope_kv_bad_cell(dev, oc):
+    """A cell outside the caches stores nothing and raises the flag; q and k are still rotated."""
+    hd, nh, nkv = 64, 4, 2
+    E, nq = nkv * hd, nh * hd
+    x = np.random.default_rng(3).standard_normal((1, nq + 2 * E)).astype(np.float32)
+    kc, vc = dev.kv(E, 32), dev.kv(E, 32)
+    k0 = np.zeros((32, E // 32 * 34), np.uint8)
+    kc.set_bytes(0, k0)
+    vc.set_bytes(1, k0)
+    xb, bad = dev.upload(x), dev.upload(np.zeros(1, np.int32))
+    pos = np.array([9], np.int32)
+    dev.rope_kv(xb, 1, nq + 2 * E, hd, nh, nkv, hd, H.ROPE_NEOX, dev.upload(pos), 10000.0, kc, vc,
+                dev.upload(np.array([32], np.int64)), bad)
+    assert bad.read(np.int32, (1,))[0] == 1
+    assert (kc.get_bytes(0) == 0).all() and (vc.get_bytes(1) == 0).all()
+    q = oc.rope(np.ascontiguousarray(x[:, :nq]), pos, hd, hd, True, theta_scale(10000.0, hd))
+    assert_bits_equal(xb.read(np.float32, (1, nq + 2 * E))[:, :nq], q, "q rotated despite the bad cell")
+    kc.free()
+    vc.free()

@@ -42,10 +42,11 @@ def oracle_model(oc, cfg, w, kv_size, hist):
                     rope_base=1000000.0), 640, 300, 4),
     (LL.tiny_config("tiny-gqa8", n_head=8, n_head_kv=1, head_dim=128, n_embd=512, n_ff=768, n_vocab=1000), 300, 255, 3),
 ], ids=["q4k-norm", "q80-neox", "gqa8-d128"])
-def test_decode_matches_oracle(dev, oc, cfg, kv_size, hist, n_steps):
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "separate"])
+def test_decode_matches_oracle(dev, oc, cfg, kv_size, hist, n_steps, fused):
     w = LL.SyntheticWeights(cfg)
-    print(f"\ndecode parity {cfg.name}: kv {kv_size} history {hist} steps {n_steps}", flush=True)
-    gpu = LL.LlamaDecoder(dev, cfg, w, kv_size)
+    print(f"\ndecode parity {cfg.name} fused={fused}: kv {kv_size} history {hist} steps {n_steps}", flush=True)
+    gpu = LL.LlamaDecoder(dev, cfg, w, kv_size, fused=fused)
     gpu.prefill_history(w, hist)
     ref = oracle_model(oc, cfg, w, kv_size, hist)
     ts = np.float32(_libm.powf(float(np.float32(cfg.rope_base)), float(np.float32(-2.0) / np.float32(cfg.head_dim))))

@@ -220,12 +220,11 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
         "mul_mat_norm qkv Q4_K 6144x4096": (
             lambda i: d.mul_mat_norm(L[i % nl]["wqkv"], m.x, 1, n, cfg.eps, L[i % nl]["attn_norm"], m.qkv, w3,
                                      stream=stream), nl, mv_bytes(w3, n) + 4 * n, "k_mv_q4k<norm>"),
-        "rope_kv": (lambda i: d.rope_kv(m.qkv, 1, w3, cfg.head_dim, cfg.n_head, cfg.n_head_kv, cfg.head_dim,
-                                        cfg.rope_mode, m.pos_ptr, cfg.rope_base, L[i % nl]["kc"], L[i % nl]["vc"],
-                                        m.cell_ptr, m.bad, stream=stream), nl, 8 * (nq + E) + 8 * E, "k_rope_kv"),
-        "flash_attn (3 launches)": (lambda i: d.flash_attn_plan(m.plan, m.qkv, w3, L[i % nl]["kc"], L[i % nl]["vc"],
-                                                                m.scale, m.att, nq, stream=stream),
-                                    nl, 2 * kv_size * (E // 32) * 34 + 8 * nq, "k_fa_*"),
+        "rope+set_rows_kv+flash_attn (3 launches)": (
+            lambda i: d.flash_attn_plan_rope(m.plan, m.qkv, L[i % nl]["kc"], L[i % nl]["vc"], m.scale, cfg.head_dim,
+                                             cfg.rope_mode, m.pos_ptr, cfg.rope_base, m.cell_ptr, m.att, nq, bad=m.bad,
+                                             stream=stream),
+            nl, 2 * kv_size * (E // 32) * 34 + 4 * w3 + 4 * nq, "k_fa_*"),
         "mul_mat o Q4_K 4096x4096 +res": (lambda i: d.mul_mat(L[i % nl]["wo"], m.att, 1, nq, m.h, n, add=m.x, add_stride=n,
                                                               stream=stream), nl, mv_bytes(n, nq) + 4 * n, "k_mv_q4k"),
         "mul_mat_norm+glu gate|up Q4_K 28672x4096": (

@@ -196,6 +196,19 @@ int tsr_hip_fa_plan_set(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan, const uint32_
 int tsr_hip_flash_attn_plan(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const float * q_dev, uint64_t q_stride,
                             const tsr_hip_kv * kc, const tsr_hip_kv * vc, float scale, const float * mask_f32_dev,
                             float * out_dev, uint64_t out_stride, void * stream);
+/* The planned FLASH_ATTN_EXT of one decode token with the layer's ROPE and SET_ROWS_KV folded into its
+ * score kernel: bit-identical to tsr_hip_rope_kv(qkv_dev, T = 1, head_dim = D, n_head, n_head_kv,
+ * n_dims, mode, pos_dev, freq_base, attn_factor, kc, vc, cell_dev, bad_dev) followed by
+ * tsr_hip_flash_attn_plan on the rotated q -- the ROPE / SET_ROWS_KV / FLASH_ATTN_EXT records of
+ * sw/ctrl/tests/test_fw_m7_layer.cpp:646-686 in one call, one launch fewer. qkv_dev holds the token's
+ * unrotated Q|K|V row (n_head q heads, n_head_kv k heads, n_head_kv v heads of D floats); it is read,
+ * not rotated in place. The plan's T is 1; D is 64 or 128 with (n_head / n_head_kv + 2) D <= 1024,
+ * n_dims % 8 == 0 and n_dims <= min(D, 128); otherwise TSR_HIP_E_SHAPE. */
+int tsr_hip_flash_attn_plan_rope(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const float * qkv_dev,
+                                 tsr_hip_kv * kc, tsr_hip_kv * vc, float scale, uint32_t n_dims, int mode,
+                                 const int32_t * pos_dev, float freq_base, float attn_factor, const int64_t * cell_dev,
+                                 int32_t * bad_dev, const float * mask_f32_dev, float * out_dev, uint64_t out_stride,
+                                 void * stream);
 int tsr_hip_fa_plan_free(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan);
 
 /* ---- graphs -------------------------------------------------------------------------------------

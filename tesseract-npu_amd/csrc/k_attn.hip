@@ -27,7 +27,9 @@
 // block-float values and the results of rule operations are never subnormal either. The f32 steps
 // after the scores therefore use the rule without the input DAZ (sadd_n / smul_n).
 #include "expk.hpp"
+#include "glue.hpp"
 #include "kernels.hpp"
+#include "kvstore.hpp"
 #include "qact.hpp"
 
 #include <algorithm>
@@ -90,11 +92,17 @@ __device__ __forceinline__ FaItem fa_item(const FaArgs & a, const FaPlan & p, ui
     else return a.items[i];
 }
 
-template <int D, bool INL>
+// ROPE (T == 1, D <= 128, (G + 2) D <= 1024): the block also rotates the query heads (rope4, angles
+// per lane by rope_cs_lane) before their QACT, rotates and QACTs the token's k row of head g and
+// QACTs its v row (threads after the query slots, A32 as SET_ROWS_KV); the thread of the new cell
+// scores with that fresh k row, and the first block of each KV head stores the k and v rows in the
+// caches -- ROPE, SET_ROWS_KV and the scores in one launch.
+template <int D, bool INL, bool ROPE>
 __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr uint32_t NBD = D / 32u;                             // blocks per head
     constexpr bool KREG = D <= 128;                                // K row of the cell kept in registers
+    static_assert(!ROPE || KREG, "the fused ROPE keeps the K rows in registers");
     const uint32_t tt = blockIdx.x % p.maxtiles;
     const FaItem it = fa_item<INL>(a, p, blockIdx.x / p.maxtiles);
     if (tt >= it.ntiles) return;                                  // the item has fewer tiles (block-uniform)
@@ -102,7 +110,15 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
     int8_t * s_q = (int8_t *)lds;                                 // G*D quants of the KV head's query heads
     float * s_dx = (float *)(lds + G * D);                        // G*D/32 scales
     uint32_t * s_red = (uint32_t *)(s_dx + G * NBD);              // 4 waves x G maxima (keys)
+    int8_t * s_kq = (int8_t *)lds + ((G * D + 4u * G * NBD + 16u * G + 15u) & ~15u);   // ROPE: the new k row of
+    float * s_kd = (float *)(s_kq + D);                           //       head g (D quants) and its D/32 scales
     const int lane = (int)__lane_id(), wave = (int)(threadIdx.x >> 6);
+    int32_t pos = 0;
+    int64_t cell64 = -1;
+    if constexpr (ROPE) {                                         // scalar loads: not behind the vector loads
+        pos = *a.pos;
+        cell64 = *a.cell;
+    }
 
     const uint32_t n16 = 16u * it.n, j = 256u * tt + threadIdx.x;
     const bool in = j < n16;
@@ -119,7 +135,23 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
     // for them only, not for the K rows)
     const float * qrow = a.q + (size_t)it.t * a.q_stride + (size_t)g * G * D;
     const uint32_t nslot = G * D / 4u;                             // 8 lanes per 32-block
-    const float4 qv0 = *(const float4 *)(qrow + 4u * min(threadIdx.x, nslot - 1u));
+    const uint32_t half = a.n_dims / 2u;
+    // ROPE: threads nslot .. nslot + D/4 - 1 hold the k row of head g, the next D/4 its v row
+    const uint32_t kslot = threadIdx.x - nslot, vslot = kslot - D / 4u;
+    const bool is_k = ROPE && threadIdx.x >= nslot && kslot < D / 4u, is_v = ROPE && !is_k && threadIdx.x >= nslot &&
+                                                                             vslot < D / 4u;
+    const float * src = a.q + (size_t)a.n_head * D + (size_t)g * D + (is_v ? E + 4u * vslot : 4u * (is_k ? kslot : 0u));
+    const uint32_t jq = 4u * min(threadIdx.x, nslot - 1u);        // first query value of the thread
+    const float4 qv0 = (ROPE && threadIdx.x >= nslot) ? *(const float4 *)src : *(const float4 *)(qrow + jq);
+    float4 qpart = qv0;                                           // ROPE NEOX: the values half away
+    // value index in the head of a rotated thread (q or k); D for the others (nothing to rotate)
+    const uint32_t jh0 = threadIdx.x < nslot ? jq % D : (is_k ? 4u * kslot : D);
+    if constexpr (ROPE) {
+        if (a.neox && jh0 < a.n_dims) {                           // the partner lies in the same head row
+            const int32_t dj = jh0 < half ? (int32_t)half : -(int32_t)half;
+            qpart = *(const float4 *)((threadIdx.x < nslot ? qrow + jq : src) + dj);
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     int4 kr[KREG ? 2 * NBD : 1];
@@ -140,10 +172,43 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
             if ((lane & 7) == 0) s_dx[slot >> 3] = Dq;
         }
     };
-    qact_slot(threadIdx.x, qv0);
-    for (uint32_t s0 = blockDim.x; s0 < nslot; s0 += blockDim.x)   // G D > 1024 only
-        qact_slot(s0 + threadIdx.x, *(const float4 *)(qrow + 4u * min(s0 + threadIdx.x, nslot - 1u)));
+    if constexpr (ROPE) {
+        float c_l, s_l;
+        rope_cs_lane(pos, half, a.ts, a.m, (uint32_t)lane, &c_l, &s_l);
+        // every lane runs rope4 (its table reads are cross-lane: a lane that skipped it would hide its
+        // entries from the others); v lanes then keep their values (jh0 = D leaves them unrotated anyway)
+        const float4 rot = rope4(qv0, qpart, jh0, a.n_dims, a.neox != 0u, c_l, s_l);
+        const float4 r = is_v ? qv0 : rot;
+        float Dq;
+        const uint32_t qq = qact_a32_lane(r, &Dq);                // every lane (8-lane groups)
+        if (threadIdx.x < nslot) {
+            *(uint32_t *)(s_q + 4u * threadIdx.x) = qq;
+            if ((lane & 7) == 0) s_dx[threadIdx.x >> 3] = Dq;
+        } else if (is_k) {
+            *(uint32_t *)(s_kq + 4u * kslot) = qq;
+            if ((lane & 7) == 0) s_kd[kslot >> 3] = Dq;
+        }
+        const bool cell_ok = cell64 >= 0 && cell64 < (int64_t)a.kc.kv_size && cell64 < (int64_t)a.vc.kv_size;
+        if (blockIdx.x == 0u) {                                   // the caches' copy of the new rows
+            if (cell_ok && (is_k || is_v))
+                kv_store_unit(is_k ? a.kc : a.vc, is_k ? 0u : 1u, (uint32_t)cell64, g * D + 4u * (is_k ? kslot : vslot), qq,
+                              Dq, (lane & 7) == 0);
+            if (!cell_ok && threadIdx.x == 0u && g == 0u && a.bad != nullptr) *a.bad = 1;
+        }
+    } else {
+        qact_slot(threadIdx.x, qv0);
+        for (uint32_t s0 = blockDim.x; s0 < nslot; s0 += blockDim.x)   // G D > 1024 only
+            qact_slot(s0 + threadIdx.x, *(const float4 *)(qrow + 4u * min(s0 + threadIdx.x, nslot - 1u)));
+    }
     lds_barrier();                                                // the K rows stay in flight
+    if constexpr (ROPE) {                                         // the new cell scores with the fresh k row
+        if ((int64_t)cell == cell64 && in) {
+#pragma unroll
+            for (uint32_t c = 0; c < 2 * NBD; ++c) kr[c] = *(const int4 *)(s_kq + 16u * c);
+#pragma unroll
+            for (uint32_t kb = 0; kb < NBD; ++kb) km[kb] = f2h_exact(s_kd[kb]);
+        }
+    }
 
     float * S = a.S + (size_t)it.s_off * a.n_head;
     for (uint32_t i = 0; i < G; ++i) {
@@ -555,14 +620,22 @@ __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
 
 template <bool INL>
 static int launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, uint32_t n_cu, hipStream_t s) {
-    const size_t lds_qk = (size_t)a.G * a.D + 4u * (size_t)a.G * (a.D / 32u) + 4u * 4u * a.G;
+    const size_t lds_qk = (size_t)a.G * a.D + 4u * (size_t)a.G * (a.D / 32u) + 4u * 4u * a.G + (a.pos ? 16u + a.D + a.D / 8u : 0u);
     const dim3 gqk(p.n_items * p.maxtiles, a.n_head_kv);
-    switch (a.D) {
-        case 64: hipLaunchKernelGGL((tsr::k_fa_qk<64, INL>), gqk, dim3(256), lds_qk, s, a, p); break;
-        case 128: hipLaunchKernelGGL((tsr::k_fa_qk<128, INL>), gqk, dim3(256), lds_qk, s, a, p); break;
-        case 256: hipLaunchKernelGGL((tsr::k_fa_qk<256, INL>), gqk, dim3(256), lds_qk, s, a, p); break;
-        case 512: hipLaunchKernelGGL((tsr::k_fa_qk<512, INL>), gqk, dim3(256), lds_qk, s, a, p); break;
-        default: return -2;
+    if (a.pos != nullptr) {                                       // ROPE + SET_ROWS_KV fused (host-checked shape)
+        switch (a.D) {
+            case 64: hipLaunchKernelGGL((tsr::k_fa_qk<64, INL, true>), gqk, dim3(256), lds_qk, s, a, p); break;
+            case 128: hipLaunchKernelGGL((tsr::k_fa_qk<128, INL, true>), gqk, dim3(256), lds_qk, s, a, p); break;
+            default: return -2;
+        }
+    } else {
+        switch (a.D) {
+            case 64: hipLaunchKernelGGL((tsr::k_fa_qk<64, INL, false>), gqk, dim3(256), lds_qk, s, a, p); break;
+            case 128: hipLaunchKernelGGL((tsr::k_fa_qk<128, INL, false>), gqk, dim3(256), lds_qk, s, a, p); break;
+            case 256: hipLaunchKernelGGL((tsr::k_fa_qk<256, INL, false>), gqk, dim3(256), lds_qk, s, a, p); break;
+            case 512: hipLaunchKernelGGL((tsr::k_fa_qk<512, INL, false>), gqk, dim3(256), lds_qk, s, a, p); break;
+            default: return -2;
+        }
     }
     if (hipGetLastError() != hipSuccess) return -4;
     // P.V: waves = the most segments of any item (<= 8), LDS = table, segment results, digits; the

@@ -38,7 +38,7 @@ __global__ __launch_bounds__(128) void k_rms_norm(const float * x, uint64_t x_st
         }
 #pragma unroll
         for (uint32_t k = 0; k < kRmsBatch; ++k)
-            if (j0 + i + 128u * k < n) p = sadd_n(p, smul(v[k], v[k]));
+            if (j0 + i + 128u * k < n) p = p + sq_rule(v[k]);      // = FA(p, FM(v, v)): see rms_tree64
     }
     p = rms_tree64(p);
     if (i == 64u) s_hi = p;                                       // partials 64 .. 127

@@ -141,23 +141,54 @@ __device__ __forceinline__ float4 prep_norm_apply(float4 v, float s, float4 w, b
     if (has_w) { v.x = smul(v.x, w.x); v.y = smul(v.y, w.y); v.z = smul(v.z, w.z); v.w = smul(v.w, w.w); }
     return v;
 }
-__device__ __forceinline__ float4 sq4(float4 v) { return make_float4(smul(v.x, v.x), smul(v.y, v.y), smul(v.z, v.z), smul(v.w, v.w)); }
+__device__ __forceinline__ float4 sq4(float4 v) { return make_float4(sq_rule(v.x), sq_rule(v.y), sq_rule(v.z), sq_rule(v.w)); }
+// LDS flags between the waves of one workgroup (all resident together). A writer makes its earlier LDS
+// writes complete (lgkmcnt(0)) before it writes the flag; a reader polls the flag with volatile LDS
+// loads, then reads the data (the LDS executes one wave's operations in order). The polls are bounded
+// (every wait ends): a flag that never comes lets the kernel finish with wrong values, never hang.
+constexpr uint32_t kLdsSpinMax = 1u << 22;
+__device__ __forceinline__ void lds_wait_writes() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);                           // lgkmcnt(0); vmcnt and expcnt untouched
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// (Relaxed workgroup-scope atomics on a static __shared__ array: plain ds_read / ds_write, which count
+// on lgkmcnt only. A volatile access through a generic pointer would be a flat load that also waits
+// for every outstanding vector-memory load.)
+__device__ __forceinline__ uint32_t lds_ld(const uint32_t * p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_st(uint32_t * p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_flag_set(uint32_t * f, uint32_t v) {
+    lds_wait_writes();
+    lds_st(f, v);
+}
+__device__ __forceinline__ void lds_flag_wait(const uint32_t * f, uint32_t want) {
+    for (uint32_t n = 0; n < kLdsSpinMax; ++n) {
+        if (lds_ld(f) >= want) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // The RMS scale from s_sq[0 .. K): every thread of the workgroup calls it (three LDS barriers inside);
 // returns s in every thread. s_sq[K] and s_sq[K + 1] are the exchange slots.
 __device__ __forceinline__ float prep_norm_scale(float * s_sq, uint32_t K, float inv_n, float eps) {
     lds_barrier();
     float p = 0.0f;
-    if (threadIdx.x < 128u) {
-        for (uint32_t j0 = 0; j0 < K; j0 += 1024u) {
-            float v[8];
+    if (threadIdx.x < 128u) {                                     // plain additions: see rms_tree64
+        // every partial has ceil((K - i) / 128) terms; reads at clamped indices, selects on the count
+        for (uint32_t j0 = 0; j0 < K; j0 += 128u * 32u) {
+            float v[32];
 #pragma unroll
-            for (uint32_t k = 0; k < 8u; ++k) {
-                const uint32_t j = j0 + threadIdx.x + 128u * k;
-                v[k] = j < K ? s_sq[j] : 0.0f;
+            for (uint32_t k = 0; k < 32u; ++k) v[k] = s_sq[min(j0 + threadIdx.x + 128u * k, K - 1u)];
+#pragma unroll
+            for (uint32_t k = 0; k < 32u; ++k) {
+                const float q = p + v[k];
+                p = j0 + threadIdx.x + 128u * k < K ? q : p;
             }
-#pragma unroll
-            for (uint32_t k = 0; k < 8u; ++k)
-                if (j0 + threadIdx.x + 128u * k < K) p = sadd_n(p, v[k]);
         }
         p = rms_tree64(p);
         if (threadIdx.x == 64u) s_sq[K + 1u] = p;
@@ -219,6 +250,21 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
 #pragma unroll
         for (int c = 0; c < NV; ++c) pv[c] = *(const float4 *)(pl + xoff((uint32_t)c));
     }
+    // kPrepNorm with one block per wave (K <= 4096): waves 12..15, which quantize before they issue
+    // their weight loads, also load the whole row (lane L = 64 (w - 12) + l: values 16 L .. 16 L + 15)
+    // and compute the scale alone, so that no wave waits for another that is held issuing its loads
+    constexpr bool SPLIT = PREP == kPrepNorm && XM == 1;
+    __shared__ uint32_t s_ctl[8];                                 // squares done, hi ready, s ready, hi, s
+    const uint32_t L = 64u * (w - 12u) + (uint32_t)lane;
+    float4 nv[4];
+    if constexpr (SPLIT) {
+        if (threadIdx.x == 0u) { lds_st(s_ctl, 0u); lds_st(s_ctl + 1, 0u); lds_st(s_ctl + 2, 0u); }
+        if (w >= 12u) {
+#pragma unroll
+            for (uint32_t c = 0; c < 4u; ++c) nv[c] = *(const float4 *)(x + min(16u * L + 4u * c, a.K - 4u));
+        }
+        lds_wait_writes();                                        // the cleared flags before the barrier
+    }
     uint32_t t64 = 0;
     if constexpr (GLU) t64 = a.ex.t64[lane];
     x_first_barrier();
@@ -276,6 +322,57 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
         load(0u);                                                 // unconditional (clamped)
         __builtin_amdgcn_sched_barrier(0);
         if (w < 12u && cnt) qact_first();
+    } else if constexpr (SPLIT) {
+        if (w < 12u) {
+            load(0u);
+            __builtin_amdgcn_sched_barrier(0);
+            lds_flag_wait(s_ctl + 2, 1u);
+            const float sc = __uint_as_float(lds_ld(s_ctl + 4));
+            xv[0] = prep_norm_apply(xv[0], sc, pv[0], a.pw != nullptr);
+            if (cnt) qact_first();
+        } else {
+            // the squares of the row (strided layout: partial i reads i, i + 128, ...), then count the wave
+#pragma unroll
+            for (uint32_t c = 0; c < 4u; ++c) {
+                const uint32_t j = 16u * L + 4u * c;
+                if (j < a.K) *(float4 *)(s_sq + j) = sq4(nv[c]);
+            }
+            lds_wait_writes();
+            if (lane == 0) __hip_atomic_fetch_add(s_ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (w >= 14u) {                                       // no part in the chain: stream now
+                load(0u);
+                __builtin_amdgcn_sched_barrier(0);
+            } else {                                              // partials 0..63 (wave 12), 64..127 (wave 13)
+                lds_flag_wait(s_ctl, 4u);
+                // every partial has K / 128 terms (K % 256 == 0): branch-free reads (clamped index) and a
+                // select on the wave-uniform count, so that the 32 reads are in flight together
+                const uint32_t i = 64u * (w - 12u) + (uint32_t)lane, nk = a.K >> 7;
+                float v[32], p = 0.0f;
+#pragma unroll
+                for (uint32_t k = 0; k < 32u; ++k) v[k] = s_sq[min(i + 128u * k, a.K - 1u)];
+#pragma unroll
+                for (uint32_t k = 0; k < 32u; ++k) {
+                    const float q = p + v[k];                     // plain additions: see rms_tree64
+                    p = k < nk ? q : p;
+                }
+                p = rms_tree64(p);
+                if (w == 13u) {
+                    if (lane == 0) lds_st(s_ctl + 3, __float_as_uint(p));
+                    if (lane == 0) lds_flag_set(s_ctl + 1, 1u);
+                } else {
+                    lds_flag_wait(s_ctl + 1, 1u);
+                    const float sc = rms_scale(p, __uint_as_float(lds_ld(s_ctl + 3)), a.inv_n, a.eps);
+                    if (lane == 0) lds_st(s_ctl + 4, __float_as_uint(sc));
+                    if (lane == 0) lds_flag_set(s_ctl + 2, 1u);
+                }
+                load(0u);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            lds_flag_wait(s_ctl + 2, 1u);
+            const float sc = __uint_as_float(lds_ld(s_ctl + 4));
+            xv[0] = prep_norm_apply(xv[0], sc, pv[0], a.pw != nullptr);
+            if (cnt) qact_first();
+        }
     } else {
         load(0u);                                                 // the norm runs under the weight stream
         __builtin_amdgcn_sched_barrier(0);
@@ -500,8 +597,8 @@ uint32_t tsr_wl_rows_per_block(uint32_t fmt, uint32_t N, uint32_t K, uint32_t n_
     return rb;
 }
 
-size_t tsr_mv_prep_lds(uint32_t prep, uint32_t K) {
-    return prep == tsr::kPrepNorm ? (4u * ((size_t)K + 2u) + 15u) & ~(size_t)15u : 0u;
+size_t tsr_mv_prep_lds(uint32_t prep, uint32_t K) {   // K squares (16-byte padded) + 8 control words
+    return prep == tsr::kPrepNorm ? 4u * (((size_t)K + 3u) & ~(size_t)3u) + 32u : 0u;
 }
 
 template <int P, int PREP, int XM, bool GLU>

@@ -106,6 +106,14 @@ struct FaArgs {
     float * out;
     uint64_t out_stride;
     ExpkTab ex;
+    // ROPE + SET_ROWS_KV fused into the score kernel (T == 1): q is then the token's unrotated Q|K|V
+    // row (k at q + n_head D, v at q + n_head D + E), rotated by position *pos; the new k and v rows
+    // go to cell *cell (a cell outside the caches stores nothing and sets *bad)
+    const int32_t * pos;
+    const int64_t * cell;
+    int32_t * bad;
+    uint32_t n_dims, neox;
+    float ts, m;
 };
 
 // ROPE over T tokens of n_heads heads (head h of token t at x + t * x_stride + h * head_dim).

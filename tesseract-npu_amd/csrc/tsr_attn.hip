@@ -510,9 +510,10 @@ int tsr_hip_fa_plan_set(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan, const uint32_
     return TSR_HIP_OK;
 }
 
-int tsr_hip_flash_attn_plan(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const float * q_dev, uint64_t q_stride,
-                            const tsr_hip_kv * kc, const tsr_hip_kv * vc, float scale, const float * mask_f32_dev,
-                            float * out_dev, uint64_t out_stride, void * stream) {
+// The planned FLASH_ATTN_EXT launch (optionally with ROPE + SET_ROWS_KV in the score kernel).
+static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const float * q_dev, uint64_t q_stride,
+                          const tsr_hip_kv * kc, const tsr_hip_kv * vc, float scale, const float * mask_f32_dev,
+                          float * out_dev, uint64_t out_stride, const tsr::FaArgs * rope, void * stream) {
     if (ctx == nullptr || plan == nullptr || q_dev == nullptr || kc == nullptr || vc == nullptr || out_dev == nullptr)
         return TSR_HIP_E_ARG;
     if (!plan->set || (plan->general && mask_f32_dev == nullptr)) return TSR_HIP_E_MASK;
@@ -535,9 +536,50 @@ int tsr_hip_flash_attn_plan(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, con
     a.OP = (float *)(plan->dev + plan->o_OP);
     a.LP = (float *)(plan->dev + plan->o_LP);
     a.max_groups = plan->max_groups;
+    if (rope != nullptr) {
+        a.pos = rope->pos;
+        a.cell = rope->cell;
+        a.bad = rope->bad;
+        a.n_dims = rope->n_dims;
+        a.neox = rope->neox;
+        a.ts = rope->ts;
+        a.m = rope->m;
+    }
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
     ctx->ctr.flash_attn_calls++;
     ctx->ctr.flash_attn_kv_bytes += plan->cells * (uint64_t)E / 32u * 34u * 2u;
+    if (rope != nullptr) ctx->ctr.set_rows_calls += 2u;
     return tsr_launch_fa(a, p, T, (uint32_t)ctx->n_cu, ctx->pick(stream)) ? TSR_HIP_E_HIP : TSR_HIP_OK;
+}
+
+int tsr_hip_flash_attn_plan(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const float * q_dev, uint64_t q_stride,
+                            const tsr_hip_kv * kc, const tsr_hip_kv * vc, float scale, const float * mask_f32_dev,
+                            float * out_dev, uint64_t out_stride, void * stream) {
+    return fa_plan_launch(ctx, plan, q_dev, q_stride, kc, vc, scale, mask_f32_dev, out_dev, out_stride, nullptr, stream);
+}
+
+int tsr_hip_flash_attn_plan_rope(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const float * qkv_dev,
+                                 tsr_hip_kv * kc, tsr_hip_kv * vc, float scale, uint32_t n_dims, int mode,
+                                 const int32_t * pos_dev, float freq_base, float attn_factor, const int64_t * cell_dev,
+                                 int32_t * bad_dev, const float * mask_f32_dev, float * out_dev, uint64_t out_stride,
+                                 void * stream) {
+    if (ctx == nullptr || plan == nullptr || pos_dev == nullptr || cell_dev == nullptr) return TSR_HIP_E_ARG;
+    if (mode != TSR_HIP_ROPE_NORMAL && mode != TSR_HIP_ROPE_NEOX && mode != TSR_HIP_ROPE_IMROPE) return TSR_HIP_E_SHAPE;
+    const uint32_t D = plan->D, G = plan->n_head_kv ? plan->n_head / plan->n_head_kv : 0u;
+    // one token; the score kernel keeps K rows in registers (D <= 128) and holds the query slots and
+    // the k and v rows of its KV head in one pass of its 256 threads; one angle per lane
+    if (plan->T != 1u || (D != 64u && D != 128u) || (G + 2u) * D > 1024u || n_dims < 8u || n_dims % 8u != 0u ||
+        n_dims > D || n_dims / 2u > 64u)
+        return TSR_HIP_E_SHAPE;
+    if (!(freq_base > 0.0f) || !std::isfinite(freq_base)) return TSR_HIP_E_ARG;
+    tsr::FaArgs r{};
+    r.pos = pos_dev;
+    r.cell = cell_dev;
+    r.bad = bad_dev;
+    r.n_dims = n_dims;
+    r.neox = mode != TSR_HIP_ROPE_NORMAL ? 1u : 0u;
+    r.ts = powf(freq_base, -2.0f / (float)n_dims);                  // the host libm, as tsr_hip_rope
+    r.m = attn_factor;
+    return fa_plan_launch(ctx, plan, qkv_dev, 0u, kc, vc, scale, mask_f32_dev, out_dev, out_stride, &r, stream);
 }

@@ -35,7 +35,7 @@ EXPORTS = (
     "tsr_hip_rms_norm", "tsr_hip_rope", "tsr_hip_swiglu", "tsr_hip_add", "tsr_hip_get_rows", "tsr_hip_argmax",
     "tsr_hip_write_async", "tsr_hip_copy_async", "tsr_hip_fa_plan_create", "tsr_hip_fa_plan_set", "tsr_hip_flash_attn_plan",
     "tsr_hip_fa_plan_free", "tsr_hip_graph_begin", "tsr_hip_graph_end", "tsr_hip_graph_launch", "tsr_hip_graph_free",
-    "tsr_hip_mul_mat_norm", "tsr_hip_rope_kv",
+    "tsr_hip_mul_mat_norm", "tsr_hip_rope_kv", "tsr_hip_flash_attn_plan_rope",
 )
 
 
@@ -106,6 +106,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "tsr_hip_mul_mat_norm": ([vp, vp, vp, u32, u64, C.c_float, vp, vp, u64, vp, u64, u32, vp], C.c_int),
         "tsr_hip_rope_kv": ([vp, vp, u32, u64, u32, u32, u32, u32, C.c_int, vp, C.c_float, C.c_float, vp, vp, vp, vp,
                              vp], C.c_int),
+        "tsr_hip_flash_attn_plan_rope": ([vp, vp, vp, vp, vp, C.c_float, u32, C.c_int, vp, C.c_float, C.c_float, vp, vp,
+                                          vp, vp, u64, vp], C.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -406,6 +408,15 @@ class Device:
                         out_stride: int, mask_f32=None, stream=None) -> None:
         _check(self.L.tsr_hip_flash_attn_plan(self.ctx, plan.h, self._p(q), q_stride, kc.h, vc.h, float(scale),
                                               self._p(mask_f32), self._p(out), out_stride, stream), "flash_attn_plan")
+
+    def flash_attn_plan_rope(self, plan: "FaPlan", qkv, kc: KvCache, vc: KvCache, scale: float, n_dims: int, mode: int,
+                             pos, freq_base: float, cell, out, out_stride: int, bad=None, attn_factor: float = 1.0,
+                             mask_f32=None, stream=None) -> None:
+        """One decode token's ROPE + SET_ROWS_KV + planned FLASH_ATTN_EXT (qkv: the unrotated Q|K|V row)."""
+        _check(self.L.tsr_hip_flash_attn_plan_rope(self.ctx, plan.h, self._p(qkv), kc.h, vc.h, float(scale), n_dims, mode,
+                                                   self._p(pos), float(freq_base), float(attn_factor), self._p(cell),
+                                                   self._p(bad), self._p(mask_f32), self._p(out), out_stride, stream),
+               "flash_attn_plan_rope")
 
     def graph_begin(self, stream=None) -> None:
         _check(self.L.tsr_hip_graph_begin(self.ctx, stream), "graph_begin")

@@ -16,11 +16,12 @@ One decode step (T = 1) runs the op list of the reference's decoder-layer test
 
 then logits = MUL_MAT(Woutput, RMS_NORM(X) * output_norm) and the greedy token is the ARGMAX.
 
-With fused=True (the default) a layer is eight launches, three of them FLASH_ATTN_EXT: RMS_NORM + MUL
-runs inside the Q|K|V and gate|up MUL_MATs (tsr_hip_mul_mat_norm), SWIGLU in the epilogue of the
-gate|up MUL_MAT (TSR_HIP_MM_GLU over gate / up rows interleaved), and ROPE with both SET_ROWS_KV in
-one kernel (tsr_hip_rope_kv), each bit-identical to the ops it replaces; fused=False runs every op
-of the list as its own call.
+With fused=True (the default) RMS_NORM + MUL runs inside the Q|K|V and gate|up MUL_MATs
+(tsr_hip_mul_mat_norm), SWIGLU in the epilogue of the gate|up MUL_MAT (TSR_HIP_MM_GLU over gate / up
+rows interleaved), and ROPE with both SET_ROWS_KV inside the score kernel of the planned
+FLASH_ATTN_EXT (tsr_hip_flash_attn_plan_rope; eager steps, planned on the host, use tsr_hip_rope_kv):
+a layer is seven launches, three of them FLASH_ATTN_EXT, each fusion bit-identical to the ops it
+replaces. fused=False runs every op of the list as its own call.
 The token embedding is a GET_ROWS of an f32 table. Row concatenation leaves every row's result
 unchanged (each output row is its own dot product with the same quantized activation), and ROPE
 of q and k heads in one launch is the same per-head rotation. A residual addend is one FA(add, v),
@@ -164,6 +165,9 @@ class LlamaDecoder:
         self.bad = dev.alloc(4).fill(0)
         self.scale = 1.0 / math.sqrt(c.head_dim)
         self.plan = dev.fa_plan(c.head_dim, c.n_head, c.n_head_kv, 1, kv_size)
+        # the planned FLASH_ATTN_EXT can take the ROPE + SET_ROWS_KV (tsr_hip_flash_attn_plan_rope) at these shapes
+        self.fa_rope = (c.head_dim in (64, 128) and (c.n_head // c.n_head_kv + 2) * c.head_dim <= 1024 and
+                        c.head_dim % 8 == 0)
         self.graph = None
         self.captures = 0
 
@@ -209,10 +213,17 @@ class LlamaDecoder:
         d.get_rows(self.tok_embd, n, n, c.n_vocab, self.tok, 1, self.x, n, bad=self.bad, stream=stream)
         w3 = nq + 2 * E
         for L in self.layers:
+            fa_done = False
             if self.fused:
                 d.mul_mat_norm(L["wqkv"], self.x, 1, n, c.eps, L["attn_norm"], self.qkv, w3, stream=stream)
-                d.rope_kv(self.qkv, 1, w3, c.head_dim, c.n_head, c.n_head_kv, c.head_dim, c.rope_mode, self.pos_ptr,
-                          c.rope_base, L["kc"], L["vc"], self.cell_ptr, self.bad, stream=stream)
+                if msum is None and self.fa_rope:                 # ROPE + SET_ROWS_KV inside the FA launch
+                    d.flash_attn_plan_rope(self.plan, self.qkv, L["kc"], L["vc"], self.scale, c.head_dim, c.rope_mode,
+                                           self.pos_ptr, c.rope_base, self.cell_ptr, self.att, nq, bad=self.bad,
+                                           stream=stream)
+                    fa_done = True
+                else:
+                    d.rope_kv(self.qkv, 1, w3, c.head_dim, c.n_head, c.n_head_kv, c.head_dim, c.rope_mode,
+                              self.pos_ptr, c.rope_base, L["kc"], L["vc"], self.cell_ptr, self.bad, stream=stream)
             else:
                 d.rms_norm(self.x, n, 1, n, c.eps, self.xn, n, w=L["attn_norm"], w_stride=n, stream=stream)
                 d.mul_mat(L["wqkv"], self.xn, 1, n, self.qkv, w3, stream=stream)
@@ -220,7 +231,9 @@ class LlamaDecoder:
                        c.rope_base, self.qkv, w3, stream=stream)
                 d.kv_set_rows(L["kc"], 0, self.qkv.ptr + nq * f4, 1, E, self.cell_ptr, self.bad, stream=stream)
                 d.kv_set_rows(L["vc"], 1, self.qkv.ptr + (nq + E) * f4, 1, E, self.cell_ptr, self.bad, stream=stream)
-            if msum is not None:
+            if fa_done:
+                pass
+            elif msum is not None:
                 d.flash_attn(self.qkv, 1, w3, L["kc"], L["vc"], c.head_dim, c.n_head, c.n_head_kv, self.scale,
                              msum, self.att, nq, new_runs=runs, stream=stream)
             else:

@@ -187,3 +187,72 @@ def test_rope_kv_bad_cell(dev, oc):
     assert_bits_equal(xb.read(np.float32, (1, nq + 2 * E))[:, :nq], q, "q rotated despite the bad cell")
     kc.free()
     vc.free()
+
+
+@pytest.mark.parametrize("n_kv,pos,cell,n_head,n_head_kv,D,mode", [
+    (4232, 4200, 4200, 32, 8, 128, H.ROPE_NORMAL),    # Llama-3-8B decode (three chunks)
+    (4232, 4231, 4231, 32, 8, 128, H.ROPE_NEOX),
+    (300, 257, 257, 14, 2, 64, H.ROPE_NEOX),          # Qwen2.5-0.5B heads; a second chunk of one cell
+    (700, 513, 100, 8, 2, 128, H.ROPE_IMROPE),        # the new row lands in a cell other than its position
+    (96, 0, 0, 4, 4, 64, H.ROPE_NORMAL),              # position 0: the first cell of an empty cache
+], ids=lambda v: str(v))
+def test_flash_attn_plan_rope(dev, oc, n_kv, pos, cell, n_head, n_head_kv, D, mode):
+    """tsr_hip_flash_attn_plan_rope against the oracle's ROPE of q and k, SET_ROWS_KV of k and v and
+    FLASH_ATTN_EXT (one decode token seeing cells [0, max(pos, cell)] of a mask n_kv wide)."""
+    import math
+    print(f"\nflash_attn_plan_rope n_kv {n_kv} pos {pos} cell {cell} heads {n_head}/{n_head_kv} D {D} mode {mode}",
+          flush=True)
+    rng = np.random.default_rng(n_kv + pos + D)
+    E, nq = n_head_kv * D, n_head * D
+    kv_size = n_kv
+    k0 = np.zeros((kv_size, E // 32 * 34), np.uint8)
+    v0 = np.zeros_like(k0)
+    hist = max(pos, cell)
+    oc.kv_set_rows(k0, S.normal(11 + D, hist * E).reshape(hist, E), np.arange(hist))
+    oc.kv_set_rows(v0, S.normal(12 + D, hist * E).reshape(hist, E), np.arange(hist))
+    row = rng.standard_normal((1, nq + 2 * E)).astype(np.float32)
+    row[0, :SPECIALS.size] = SPECIALS
+    base = 500000.0
+    ts = theta_scale(base, D)
+    neox = mode != H.ROPE_NORMAL
+    q = oc.rope(np.ascontiguousarray(row[:, :nq]), np.array([pos], np.int32), D, D, neox, ts)
+    k = oc.rope(np.ascontiguousarray(row[:, nq:nq + E]), np.array([pos], np.int32), D, D, neox, ts)
+    kw, vw = k0.copy(), v0.copy()
+    oc.kv_set_rows(kw, k, np.array([cell], np.int64))
+    oc.kv_set_rows(vw, np.ascontiguousarray(row[:, nq + E:]), np.array([cell], np.int64))
+    msum = np.zeros(12, np.uint32)
+    msum[0], msum[1], msum[2], msum[9] = 0x4D55534D, 1, n_kv, hist + 1
+    runs = np.array([[cell, cell + 1]], np.uint32)
+    scale = np.float32(1.0 / math.sqrt(D))
+    want = oc.flash_attn(q, kw, vw, D, n_head, n_head_kv, scale, msum, new_runs=runs)
+    kc, vc = dev.kv(E, kv_size), dev.kv(E, kv_size)
+    kc.set_bytes(0, k0)
+    vc.set_bytes(1, v0)
+    plan = dev.fa_plan(D, n_head, n_head_kv, 1, kv_size)
+    plan.set(msum, runs)
+    rb, out, bad = dev.upload(row), dev.alloc(4 * nq), dev.upload(np.zeros(1, np.int32))
+    dev.flash_attn_plan_rope(plan, rb, kc, vc, scale, D, mode, dev.upload(np.array([pos], np.int32)), base,
+                             dev.upload(np.array([cell], np.int64)), out, nq, bad=bad)
+    assert_bits_equal(out.read(np.float32, (1, nq)), want, "fa + rope")
+    assert (kc.get_bytes(0).reshape(kv_size, -1) == kw).all()
+    assert (vc.get_bytes(1).reshape(kv_size, -1) == vw).all()
+    assert bad.read(np.int32, (1,))[0] == 0
+    assert_bits_equal(rb.read(np.float32, (1, nq + 2 * E)), row, "the Q|K|V row is read, not rotated")
+    plan.free()
+    kc.free()
+    vc.free()
+
+
+def test_flash_attn_plan_rope_refusals(dev):
+    plan = dev.fa_plan(128, 64, 8, 1, 64)                 # G = 8: (8 + 2) 128 > 1024
+    kc, vc = dev.kv(1024, 64), dev.kv(1024, 64)
+    b = dev.alloc(4 * 16384)
+    msum = np.zeros(12, np.uint32)
+    msum[0], msum[1], msum[2], msum[9] = 0x4D55534D, 1, 64, 10
+    plan.set(msum)
+    with pytest.raises(H.TsrHipError) as e:
+        dev.flash_attn_plan_rope(plan, b, kc, vc, 0.1, 128, H.ROPE_NORMAL, b, 10000.0, b, b, 8192)
+    assert e.value.code == -2
+    plan.free()
+    kc.free()
+    vc.free()

@@ -93,6 +93,21 @@ class HipEvents:
         assert self.h.hipGraphInstantiate(C.byref(ge), g, None, None, 0) == 0
         return g, ge
 
+    def eager_ms(self, stream, fn, n: int, replays: int = 3) -> float:
+        """Milliseconds per call of fn over n direct launches: the median of `replays` timed rounds
+        after one untimed round."""
+        a, b = self.event(), self.event()
+        for i in range(n):
+            fn(i)
+        times = []
+        for _ in range(replays):
+            self.record(a, stream)
+            for i in range(n):
+                fn(i)
+            self.record(b, stream)
+            times.append(self.elapsed_ms(a, b) / n)
+        return float(np.median(times))
+
     def graph_ms(self, stream, fn, n: int, replays: int = 3) -> tuple:
         """Milliseconds per call of fn over n calls replayed from one graph: the median of `replays`
         timed replays after one untimed replay; also the eager (host-launched) time of n calls."""
@@ -166,7 +181,8 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
     Cells 0 .. CTX-1 of every layer's caches hold seeded rows (SET_ROWS_KV); token 0 is decoded at
     position CTX eagerly (its logits are kept for the CPU leg's bit comparison), tokens 1 .. warmup-1
     by graph replays (the first replay captures), then `steps` timed graph replays at positions
-    CTX+warmup .. CTX+warmup+steps-1. Every greedy token is copied to a device history buffer."""
+    CTX+warmup .. CTX+warmup+steps-1; with `eager`, direct launches instead of every replay. Every
+    greedy token is copied to a device history buffer."""
     cfg = LL.LLAMA3_8B
     wts = CachedWeights(cfg)
     kv_size = CTX + warmup + steps
@@ -181,7 +197,10 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
     tok1 = m.read_next()
     hist.write(np.array([tok1], np.int32))
     for i in range(1, warmup):
-        m.step_graph(tok1 if i == 1 else None, CTX + i)
+        if eager:   # no decode graph at all (the profiler's kernel trace of this process)
+            m.step_async(tok1 if i == 1 else None, CTX + i)
+        else:
+            m.step_graph(tok1 if i == 1 else None, CTX + i)
         dev.copy_async(hist.ptr + 4 * i, m.tok, 4)
     dev.sync()
     captures = m.captures
@@ -209,8 +228,8 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
     mid_kv = CTX + warmup + steps // 2 + 1
     tb = token_bytes(cfg, mid_kv)
 
-    # each op class alone, launched over the model's own 32 layers (graph replay, HIP events on the
-    # launch stream): what a token spends where
+    # each op class alone, launched over the model's own 32 layers (graph replay, or direct launches
+    # with `eager`; HIP events on the launch stream): what a token spends where
     n, E, nq, ff, d = cfg.n_embd, cfg.E, cfg.n_q, cfg.n_ff, dev
     L = m.layers
     nl = cfg.n_layer
@@ -220,11 +239,10 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
         "mul_mat_norm qkv Q4_K 6144x4096": (
             lambda i: d.mul_mat_norm(L[i % nl]["wqkv"], m.x, 1, n, cfg.eps, L[i % nl]["attn_norm"], m.qkv, w3,
                                      stream=stream), nl, mv_bytes(w3, n) + 4 * n, "k_mv_q4k<norm>"),
-        "rope+set_rows_kv+flash_attn (3 launches)": (
-            lambda i: d.flash_attn_plan_rope(m.plan, m.qkv, L[i % nl]["kc"], L[i % nl]["vc"], m.scale, cfg.head_dim,
-                                             cfg.rope_mode, m.pos_ptr, cfg.rope_base, m.cell_ptr, m.att, nq, bad=m.bad,
-                                             stream=stream),
-            nl, 2 * kv_size * (E // 32) * 34 + 4 * w3 + 4 * nq, "k_fa_*"),
+        "rope+set_rows_kv+flash_attn": (
+            lambda i: d.flash_attn_plan_rope_tab(m.plan, m.qkv, L[i % nl]["kc"], L[i % nl]["vc"], m.scale, cfg.head_dim,
+                                                 cfg.rope_mode, m.rtab, m.cell_ptr, m.att, nq, bad=m.bad, stream=stream),
+            nl, 2 * kv_size * (E // 32) * 34 + 4 * w3 + 4 * nq, "k_fa_qk<fused>"),
         "mul_mat o Q4_K 4096x4096 +res": (lambda i: d.mul_mat(L[i % nl]["wo"], m.att, 1, nq, m.h, n, add=m.x, add_stride=n,
                                                               stream=stream), nl, mv_bytes(n, nq) + 4 * n, "k_mv_q4k"),
         "mul_mat_norm+glu gate|up Q4_K 28672x4096": (
@@ -237,6 +255,8 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
         "mul_mat_norm output Q4_K 128256x4096": (
             lambda i: d.mul_mat_norm(m.wout, m.x, 1, n, cfg.eps, m.out_norm, m.logits, cfg.n_vocab, stream=stream),
             1, mv_bytes(cfg.n_vocab, n) + 4 * n, "k_mv_q4k<norm>"),
+        "rope_table": (lambda i: d.rope_table(m.pos_ptr, cfg.head_dim, cfg.rope_base, m.rtab, stream=stream), 1,
+                       4 * cfg.head_dim, "k_rope_table"),
         "argmax": (lambda i: d.argmax(m.logits, cfg.n_vocab, 1, cfg.n_vocab, m.next, stream=stream), 1,
                    4 * cfg.n_vocab, "k_argmax"),
         "get_rows": (lambda i: d.get_rows(m.tok_embd, n, n, cfg.n_vocab, m.tok, 1, m.h, n, bad=m.bad, stream=stream), 1,
@@ -247,7 +267,7 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
         for i in range(3):
             fn(i)
         ev.device_sync()
-        t, _ = ev.graph_ms(stream, fn, 2 * nl)
+        t = ev.eager_ms(stream, fn, 2 * nl) if eager else ev.graph_ms(stream, fn, 2 * nl)[0]
         per_op[name] = {"launch_us": round(t * 1e3, 3), "per_token": count, "us_per_token": round(t * 1e3 * count, 1),
                         "GB/s": round(nbytes / (t * 1e-3) / 1e9, 1), "algorithmic_bytes": nbytes, "kernel": kname}
     ev.device_sync()

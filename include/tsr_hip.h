@@ -209,6 +209,14 @@ int tsr_hip_flash_attn_plan_rope(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan
                                  const int32_t * pos_dev, float freq_base, float attn_factor, const int64_t * cell_dev,
                                  int32_t * bad_dev, const float * mask_f32_dev, float * out_dev, uint64_t out_stride,
                                  void * stream);
+/* The same with the ROPE angles of the token's position read from a table made by tsr_hip_rope_table
+ * (pos_dev, n_dims, freq_base, attn_factor of that call) instead of computed per launch: the layers of
+ * one token share the table, so the per-layer launch spends no time on the angle recurrence. tab_dev:
+ * n_dims floats, 8-byte aligned. Same shapes and results as tsr_hip_flash_attn_plan_rope. */
+int tsr_hip_flash_attn_plan_rope_tab(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const float * qkv_dev,
+                                     tsr_hip_kv * kc, tsr_hip_kv * vc, float scale, uint32_t n_dims, int mode,
+                                     const float * tab_dev, const int64_t * cell_dev, int32_t * bad_dev,
+                                     const float * mask_f32_dev, float * out_dev, uint64_t out_stride, void * stream);
 int tsr_hip_fa_plan_free(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan);
 
 /* ---- graphs -------------------------------------------------------------------------------------
@@ -270,6 +278,14 @@ int tsr_hip_rms_norm(tsr_hip_ctx * ctx, const float * x_dev, uint32_t n, uint32_
 int tsr_hip_rope(tsr_hip_ctx * ctx, const float * x_dev, uint32_t T, uint64_t x_stride, uint32_t head_dim,
                  uint32_t n_heads, uint32_t n_dims, int mode, const int32_t * pos_dev, float freq_base, float freq_scale,
                  float attn_factor, const float * freq_factors_dev, float * y_dev, uint64_t y_stride, void * stream);
+/* The ROPE angles of one position (*pos_dev) as tsr_hip_rope computes them without freq factors and
+ * with freq_scale 1 (theta_0 = pos, theta_i = theta_(i-1) TS, tsr_ref_rope sw/sim/tsr_ref_vu.c:
+ * 308-376): tab_dev[2 i] = FM(attn_factor, cos theta_i), tab_dev[2 i + 1] = FM(attn_factor,
+ * sin theta_i) for i < n_dims / 2; n_dims even, 2 <= n_dims <= 128; tab_dev 8-byte aligned. The table
+ * of tsr_hip_flash_attn_plan_rope_tab (no counterpart in the reference, which derives the angles in
+ * every ROPE record: a decode token's layers share one position). */
+int tsr_hip_rope_table(tsr_hip_ctx * ctx, const int32_t * pos_dev, uint32_t n_dims, float freq_base, float attn_factor,
+                       float * tab_dev, void * stream);
 
 /* GGML_GLU_OP_SWIGLU, split form (tsr_lower_glu, sw/ggml-tesseract/tsr-build.cpp:423-490; VOP.SWIGLU
  * sw/sim/tsr_ref_vu.c:102-133): y = SILU(g) u, SILU(g) = g / (1 + EXPK(-g)). */

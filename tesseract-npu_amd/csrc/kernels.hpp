@@ -102,6 +102,16 @@ struct FaArgs {
     float * Mpart;           // [tile][n_head] tile maxima
     float * OP;              // [item][4][n_head][D] channel partials
     float * LP;              // [item][4][n_head] channel row sums
+    // the fused decode form (a plan's buffers): per score tile the segment results of its channels
+    // [tile][4][n_head][D] and row sums [tile][4][n_head]; zero between launches: the tile maxima as
+    // MAXT keys [n_head_kv][n_items * maxtiles][4] (0: not yet published) and the counters
+    // [item][n_head_kv] tiles that stored their segments, [n_head_kv] items whose channel partials
+    // are stored
+    float * seg_o;
+    float * seg_l;
+    float * m_item;          // [item][n_head] chunk maxima
+    uint32_t * tkeys;
+    uint32_t * sync;
     uint32_t max_groups;     // the largest item (groups), for a work list in device memory
     float * out;
     uint64_t out_stride;
@@ -114,6 +124,7 @@ struct FaArgs {
     int32_t * bad;
     uint32_t n_dims, neox;
     float ts, m;
+    const float * rtab;      // or the angles of *pos from tsr_hip_rope_table: [n_dims / 2] (M cos, M sin)
 };
 
 // ROPE over T tokens of n_heads heads (head h of token t at x + t * x_stride + h * head_dim).
@@ -161,6 +172,7 @@ int tsr_launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, uint
 int tsr_launch_rms_norm(const float * x, uint64_t x_stride, uint32_t n, uint32_t rows, float eps, float inv_n,
                         const float * w, uint64_t w_stride, uint32_t w_period, float * y, uint64_t y_stride, hipStream_t s);
 int tsr_launch_rope(const tsr::RopeArgs & a, uint32_t T, hipStream_t s);
+int tsr_launch_rope_table(const int32_t * pos, uint32_t half, float ts, float m, float * tab, hipStream_t s);
 int tsr_launch_swiglu(const float * g, uint64_t g_stride, const float * u, uint64_t u_stride, float * y, uint64_t y_stride,
                       uint32_t n, uint32_t rows, const tsr::ExpkTab & ex, hipStream_t s);
 int tsr_launch_add(const float * a, uint64_t a_stride, const float * b, uint64_t b_stride, uint32_t b_period, float * y,

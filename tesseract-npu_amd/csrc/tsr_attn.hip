@@ -415,7 +415,8 @@ struct tsr_hip_fa_plan {
     uint32_t items_max = 0, tiles_max = 0;
     uint64_t cells_max = 0;
     uint8_t * dev = nullptr;
-    size_t o_items = 0, o_S = 0, o_Mp = 0, o_OP = 0, o_LP = 0, bytes = 0;
+    size_t o_items = 0, o_S = 0, o_Mp = 0, o_OP = 0, o_LP = 0, o_SO = 0, o_SL = 0, o_MI = 0, o_TK = 0, o_sync = 0,
+           bytes = 0;
     bool set = false, general = false;
     uint32_t n_items = 0, maxtiles = 0, max_groups = 0, mstride = 0;   // the shape a launch bakes in
     uint64_t cells = 0;
@@ -452,10 +453,25 @@ int tsr_hip_fa_plan_create(tsr_hip_ctx * ctx, uint32_t D, uint32_t n_head, uint3
     p->o_Mp = off; off = up256(off + 4u * (size_t)tiles * n_head);
     p->o_OP = off; off = up256(off + 4u * (size_t)items * kC * n_head * D);
     p->o_LP = off; off = up256(off + 4u * (size_t)items * kC * n_head);
+    // the fused decode form (T == 1): per-tile segment results and row sums, and its counters
+    const uint64_t ftiles = T == 1u ? tiles : 0u;
+    p->o_SO = off; off = up256(off + 4u * (size_t)ftiles * kC * n_head * D);
+    p->o_SL = off; off = up256(off + 4u * (size_t)ftiles * kC * n_head);
+    p->o_MI = off; off = up256(off + (T == 1u ? 4u * (size_t)items * n_head : 0u));
+    // zero between launches: the tile keys (an item has <= 8 tiles: NCG <= 128 groups) and the counters
+    p->o_TK = off; off = up256(off + (T == 1u ? 4u * 4u * 8u * (size_t)items * n_head_kv : 0u));
+    p->o_sync = off; off = up256(off + (T == 1u ? 4u * ((size_t)items + 1u) * n_head_kv : 0u));
     p->bytes = off;
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
     if ((rc = hip_err(hipMalloc(&p->dev, off), "hipMalloc fa plan")) != 0) {
+        delete p;
+        return rc;
+    }
+    // the counters start at zero; every fused launch leaves them at zero
+    if ((rc = hip_err(hipMemset(p->dev + p->o_TK, 0, off - p->o_TK), "hipMemset fa plan counters")) != 0 ||
+        (rc = hip_err(hipDeviceSynchronize(), "fa plan counters")) != 0) {
+        (void)hipFree(p->dev);
         delete p;
         return rc;
     }
@@ -536,7 +552,15 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
     a.OP = (float *)(plan->dev + plan->o_OP);
     a.LP = (float *)(plan->dev + plan->o_LP);
     a.max_groups = plan->max_groups;
+    if (T == 1u) {                                                // the fused decode form's buffers
+        a.seg_o = (float *)(plan->dev + plan->o_SO);
+        a.seg_l = (float *)(plan->dev + plan->o_SL);
+        a.m_item = (float *)(plan->dev + plan->o_MI);
+        a.tkeys = (uint32_t *)(plan->dev + plan->o_TK);
+        a.sync = (uint32_t *)(plan->dev + plan->o_sync);
+    }
     if (rope != nullptr) {
+        a.rtab = rope->rtab;
         a.pos = rope->pos;
         a.cell = rope->cell;
         a.bad = rope->bad;
@@ -559,27 +583,48 @@ int tsr_hip_flash_attn_plan(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, con
     return fa_plan_launch(ctx, plan, q_dev, q_stride, kc, vc, scale, mask_f32_dev, out_dev, out_stride, nullptr, stream);
 }
 
+// The shape the score kernel's ROPE form takes: one token, K rows in registers (D <= 128), the query
+// slots and the k and v rows of a KV head in one pass of its 256 threads, one angle per lane.
+static int fa_rope_args(const tsr_hip_fa_plan * plan, uint32_t n_dims, int mode, const int64_t * cell_dev,
+                        int32_t * bad_dev, tsr::FaArgs & r) {
+    if (plan == nullptr || cell_dev == nullptr) return TSR_HIP_E_ARG;
+    if (mode != TSR_HIP_ROPE_NORMAL && mode != TSR_HIP_ROPE_NEOX && mode != TSR_HIP_ROPE_IMROPE) return TSR_HIP_E_SHAPE;
+    const uint32_t D = plan->D, G = plan->n_head_kv ? plan->n_head / plan->n_head_kv : 0u;
+    if (plan->T != 1u || (D != 64u && D != 128u) || (G + 2u) * D > 1024u || n_dims < 8u || n_dims % 8u != 0u ||
+        n_dims > D || n_dims / 2u > 64u)
+        return TSR_HIP_E_SHAPE;
+    r = tsr::FaArgs{};
+    r.cell = cell_dev;
+    r.bad = bad_dev;
+    r.n_dims = n_dims;
+    r.neox = mode != TSR_HIP_ROPE_NORMAL ? 1u : 0u;
+    return TSR_HIP_OK;
+}
+
 int tsr_hip_flash_attn_plan_rope(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const float * qkv_dev,
                                  tsr_hip_kv * kc, tsr_hip_kv * vc, float scale, uint32_t n_dims, int mode,
                                  const int32_t * pos_dev, float freq_base, float attn_factor, const int64_t * cell_dev,
                                  int32_t * bad_dev, const float * mask_f32_dev, float * out_dev, uint64_t out_stride,
                                  void * stream) {
-    if (ctx == nullptr || plan == nullptr || pos_dev == nullptr || cell_dev == nullptr) return TSR_HIP_E_ARG;
-    if (mode != TSR_HIP_ROPE_NORMAL && mode != TSR_HIP_ROPE_NEOX && mode != TSR_HIP_ROPE_IMROPE) return TSR_HIP_E_SHAPE;
-    const uint32_t D = plan->D, G = plan->n_head_kv ? plan->n_head / plan->n_head_kv : 0u;
-    // one token; the score kernel keeps K rows in registers (D <= 128) and holds the query slots and
-    // the k and v rows of its KV head in one pass of its 256 threads; one angle per lane
-    if (plan->T != 1u || (D != 64u && D != 128u) || (G + 2u) * D > 1024u || n_dims < 8u || n_dims % 8u != 0u ||
-        n_dims > D || n_dims / 2u > 64u)
-        return TSR_HIP_E_SHAPE;
+    if (ctx == nullptr || pos_dev == nullptr) return TSR_HIP_E_ARG;
+    tsr::FaArgs r;
+    const int rc = fa_rope_args(plan, n_dims, mode, cell_dev, bad_dev, r);
+    if (rc) return rc;
     if (!(freq_base > 0.0f) || !std::isfinite(freq_base)) return TSR_HIP_E_ARG;
-    tsr::FaArgs r{};
     r.pos = pos_dev;
-    r.cell = cell_dev;
-    r.bad = bad_dev;
-    r.n_dims = n_dims;
-    r.neox = mode != TSR_HIP_ROPE_NORMAL ? 1u : 0u;
     r.ts = powf(freq_base, -2.0f / (float)n_dims);                  // the host libm, as tsr_hip_rope
     r.m = attn_factor;
+    return fa_plan_launch(ctx, plan, qkv_dev, 0u, kc, vc, scale, mask_f32_dev, out_dev, out_stride, &r, stream);
+}
+
+int tsr_hip_flash_attn_plan_rope_tab(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const float * qkv_dev,
+                                     tsr_hip_kv * kc, tsr_hip_kv * vc, float scale, uint32_t n_dims, int mode,
+                                     const float * tab_dev, const int64_t * cell_dev, int32_t * bad_dev,
+                                     const float * mask_f32_dev, float * out_dev, uint64_t out_stride, void * stream) {
+    if (ctx == nullptr || tab_dev == nullptr || ((uintptr_t)tab_dev & 7u) != 0u) return TSR_HIP_E_ARG;
+    tsr::FaArgs r;
+    const int rc = fa_rope_args(plan, n_dims, mode, cell_dev, bad_dev, r);
+    if (rc) return rc;
+    r.rtab = tab_dev;
     return fa_plan_launch(ctx, plan, qkv_dev, 0u, kc, vc, scale, mask_f32_dev, out_dev, out_stride, &r, stream);
 }

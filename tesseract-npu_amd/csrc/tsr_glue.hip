@@ -68,6 +68,17 @@ int tsr_hip_rope(tsr_hip_ctx * ctx, const float * x_dev, uint32_t T, uint64_t x_
     return tsr_launch_rope(a, T, s);
 }
 
+int tsr_hip_rope_table(tsr_hip_ctx * ctx, const int32_t * pos_dev, uint32_t n_dims, float freq_base, float attn_factor,
+                       float * tab_dev, void * stream) {
+    if (ctx == nullptr || pos_dev == nullptr || tab_dev == nullptr || ((uintptr_t)tab_dev & 7u) != 0u) return TSR_HIP_E_ARG;
+    if (n_dims < 2u || n_dims % 2u != 0u || n_dims > 128u) return TSR_HIP_E_SHAPE;
+    if (!(freq_base > 0.0f) || !std::isfinite(freq_base)) return TSR_HIP_E_ARG;
+    const float ts = powf(freq_base, -2.0f / (float)n_dims);       // the host libm, as tsr_hip_rope
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    const hipStream_t s = enter(ctx, stream);
+    return tsr_launch_rope_table(pos_dev, n_dims / 2u, ts, attn_factor, tab_dev, s);
+}
+
 int tsr_hip_swiglu(tsr_hip_ctx * ctx, const float * g_dev, uint64_t g_stride, const float * u_dev, uint64_t u_stride,
                    uint32_t n, uint32_t rows, float * y_dev, uint64_t y_stride, void * stream) {
     if (ctx == nullptr || g_dev == nullptr || u_dev == nullptr || y_dev == nullptr || n == 0u || rows == 0u)

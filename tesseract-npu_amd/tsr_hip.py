@@ -35,7 +35,8 @@ EXPORTS = (
     "tsr_hip_rms_norm", "tsr_hip_rope", "tsr_hip_swiglu", "tsr_hip_add", "tsr_hip_get_rows", "tsr_hip_argmax",
     "tsr_hip_write_async", "tsr_hip_copy_async", "tsr_hip_fa_plan_create", "tsr_hip_fa_plan_set", "tsr_hip_flash_attn_plan",
     "tsr_hip_fa_plan_free", "tsr_hip_graph_begin", "tsr_hip_graph_end", "tsr_hip_graph_launch", "tsr_hip_graph_free",
-    "tsr_hip_mul_mat_norm", "tsr_hip_rope_kv", "tsr_hip_flash_attn_plan_rope",
+    "tsr_hip_mul_mat_norm", "tsr_hip_rope_kv", "tsr_hip_flash_attn_plan_rope", "tsr_hip_rope_table",
+    "tsr_hip_flash_attn_plan_rope_tab",
 )
 
 
@@ -108,6 +109,9 @@ def load(path: str = LIB_PATH) -> C.CDLL:
                              vp], C.c_int),
         "tsr_hip_flash_attn_plan_rope": ([vp, vp, vp, vp, vp, C.c_float, u32, C.c_int, vp, C.c_float, C.c_float, vp, vp,
                                           vp, vp, u64, vp], C.c_int),
+        "tsr_hip_rope_table": ([vp, vp, u32, C.c_float, C.c_float, vp, vp], C.c_int),
+        "tsr_hip_flash_attn_plan_rope_tab": ([vp, vp, vp, vp, vp, C.c_float, u32, C.c_int, vp, vp, vp, vp, vp, u64, vp],
+                                             C.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -417,6 +421,19 @@ class Device:
                                                    self._p(pos), float(freq_base), float(attn_factor), self._p(cell),
                                                    self._p(bad), self._p(mask_f32), self._p(out), out_stride, stream),
                "flash_attn_plan_rope")
+
+    def rope_table(self, pos, n_dims: int, freq_base: float, tab, attn_factor: float = 1.0, stream=None) -> None:
+        """The ROPE angles of position *pos: tab[2 i], tab[2 i + 1] = M cos, M sin of theta_i, i < n_dims / 2."""
+        _check(self.L.tsr_hip_rope_table(self.ctx, self._p(pos), n_dims, float(freq_base), float(attn_factor),
+                                         self._p(tab), stream), "rope_table")
+
+    def flash_attn_plan_rope_tab(self, plan: "FaPlan", qkv, kc: KvCache, vc: KvCache, scale: float, n_dims: int,
+                                 mode: int, tab, cell, out, out_stride: int, bad=None, mask_f32=None, stream=None) -> None:
+        """flash_attn_plan_rope with the angles from a rope_table of the token's position."""
+        _check(self.L.tsr_hip_flash_attn_plan_rope_tab(self.ctx, plan.h, self._p(qkv), kc.h, vc.h, float(scale), n_dims,
+                                                       mode, self._p(tab), self._p(cell), self._p(bad),
+                                                       self._p(mask_f32), self._p(out), out_stride, stream),
+               "flash_attn_plan_rope_tab")
 
     def graph_begin(self, stream=None) -> None:
         _check(self.L.tsr_hip_graph_begin(self.ctx, stream), "graph_begin")

@@ -18,10 +18,11 @@ then logits = MUL_MAT(Woutput, RMS_NORM(X) * output_norm) and the greedy token i
 
 With fused=True (the default) RMS_NORM + MUL runs inside the Q|K|V and gate|up MUL_MATs
 (tsr_hip_mul_mat_norm), SWIGLU in the epilogue of the gate|up MUL_MAT (TSR_HIP_MM_GLU over gate / up
-rows interleaved), and ROPE with both SET_ROWS_KV inside the score kernel of the planned
-FLASH_ATTN_EXT (tsr_hip_flash_attn_plan_rope; eager steps, planned on the host, use tsr_hip_rope_kv):
-a layer is seven launches, three of them FLASH_ATTN_EXT, each fusion bit-identical to the ops it
-replaces. fused=False runs every op of the list as its own call.
+rows interleaved), and ROPE with both SET_ROWS_KV inside the planned FLASH_ATTN_EXT
+(tsr_hip_flash_attn_plan_rope_tab, the angles of the token's position made once per token by
+tsr_hip_rope_table; eager steps, planned on the host, use tsr_hip_rope_kv): at the Llama-3-8B shape a
+layer is five launches (the planned decode FLASH_ATTN_EXT is one), each fusion bit-identical to the ops
+it replaces. fused=False runs every op of the list as its own call.
 The token embedding is a GET_ROWS of an f32 table. Row concatenation leaves every row's result
 unchanged (each output row is its own dot product with the same quantized activation), and ROPE
 of q and k heads in one launch is the same per-head rotation. A residual addend is one FA(add, v),
@@ -163,6 +164,7 @@ class LlamaDecoder:
         self.next = dev.alloc(4)           # int32 greedy token (ARGMAX) of an eager step
         self.params = dev.alloc(16)        # int32 position (ROPE) at 0, int64 cell (SET_ROWS_KV) at 8
         self.bad = dev.alloc(4).fill(0)
+        self.rtab = dev.alloc(4 * c.head_dim)  # ROPE angles of the token's position (tsr_hip_rope_table)
         self.scale = 1.0 / math.sqrt(c.head_dim)
         self.plan = dev.fa_plan(c.head_dim, c.n_head, c.n_head_kv, 1, kv_size)
         # the planned FLASH_ATTN_EXT can take the ROPE + SET_ROWS_KV (tsr_hip_flash_attn_plan_rope) at these shapes
@@ -212,14 +214,17 @@ class LlamaDecoder:
         f4 = 4
         d.get_rows(self.tok_embd, n, n, c.n_vocab, self.tok, 1, self.x, n, bad=self.bad, stream=stream)
         w3 = nq + 2 * E
+        fa_tab = self.fused and msum is None and self.fa_rope
+        if fa_tab:                                                # the position's angles, once per token
+            d.rope_table(self.pos_ptr, c.head_dim, c.rope_base, self.rtab, stream=stream)
         for L in self.layers:
             fa_done = False
             if self.fused:
                 d.mul_mat_norm(L["wqkv"], self.x, 1, n, c.eps, L["attn_norm"], self.qkv, w3, stream=stream)
-                if msum is None and self.fa_rope:                 # ROPE + SET_ROWS_KV inside the FA launch
-                    d.flash_attn_plan_rope(self.plan, self.qkv, L["kc"], L["vc"], self.scale, c.head_dim, c.rope_mode,
-                                           self.pos_ptr, c.rope_base, self.cell_ptr, self.att, nq, bad=self.bad,
-                                           stream=stream)
+                if fa_tab:                                        # ROPE + SET_ROWS_KV inside the FA launch
+                    d.flash_attn_plan_rope_tab(self.plan, self.qkv, L["kc"], L["vc"], self.scale, c.head_dim,
+                                               c.rope_mode, self.rtab, self.cell_ptr, self.att, nq, bad=self.bad,
+                                               stream=stream)
                     fa_done = True
                 else:
                     d.rope_kv(self.qkv, 1, w3, c.head_dim, c.n_head, c.n_head_kv, c.head_dim, c.rope_mode,

@@ -189,22 +189,28 @@ def test_rope_kv_bad_cell(dev, oc):
     vc.free()
 
 
-@pytest.mark.parametrize("n_kv,pos,cell,n_head,n_head_kv,D,mode", [
-    (4232, 4200, 4200, 32, 8, 128, H.ROPE_NORMAL),    # Llama-3-8B decode (three chunks)
-    (4232, 4231, 4231, 32, 8, 128, H.ROPE_NEOX),
-    (300, 257, 257, 14, 2, 64, H.ROPE_NEOX),          # Qwen2.5-0.5B heads; a second chunk of one cell
-    (700, 513, 100, 8, 2, 128, H.ROPE_IMROPE),        # the new row lands in a cell other than its position
-    (96, 0, 0, 4, 4, 64, H.ROPE_NORMAL),              # position 0: the first cell of an empty cache
+@pytest.mark.parametrize("n_kv,pos,cell,n_head,n_head_kv,D,mode,n_dims,general", [
+    (4232, 4200, 4200, 32, 8, 128, H.ROPE_NORMAL, 128, False),    # Llama-3-8B decode (three chunks)
+    (4232, 4231, 4231, 32, 8, 128, H.ROPE_NEOX, 128, False),
+    (4232, 4215, 4215, 32, 8, 128, H.ROPE_NORMAL, 128, False),    # the new cell's group in channel 3
+    (2100, 2090, 2068, 16, 8, 128, H.ROPE_NEOX, 64, False),       # G = 2, half the dims rotated, channel 1
+    (1500, 1400, 1400, 12, 4, 64, H.ROPE_NORMAL, 32, True),       # G = 3, a GENERAL mask
+    (4232, 4100, 4100, 32, 8, 128, H.ROPE_NEOX, 128, True),       # GENERAL mask at the decode shape
+    (300, 257, 257, 14, 2, 64, H.ROPE_NEOX, 64, False),           # Qwen2.5-0.5B heads; a second chunk of one cell
+    (700, 513, 100, 8, 2, 128, H.ROPE_IMROPE, 128, False),        # the new row lands in a cell other than its position
+    (96, 0, 0, 4, 4, 64, H.ROPE_NORMAL, 64, False),               # position 0: the first cell of an empty cache
+    (640, 600, 600, 64, 8, 64, H.ROPE_NORMAL, 64, False),         # G = 8: the three-launch form
 ], ids=lambda v: str(v))
-def test_flash_attn_plan_rope(dev, oc, n_kv, pos, cell, n_head, n_head_kv, D, mode):
+def test_flash_attn_plan_rope(dev, oc, n_kv, pos, cell, n_head, n_head_kv, D, mode, n_dims, general):
     """tsr_hip_flash_attn_plan_rope against the oracle's ROPE of q and k, SET_ROWS_KV of k and v and
-    FLASH_ATTN_EXT (one decode token seeing cells [0, max(pos, cell)] of a mask n_kv wide)."""
+    FLASH_ATTN_EXT (one decode token seeing cells [0, max(pos, cell)] of a mask n_kv wide; with
+    `general`, some of those cells carry finite biases and some are masked out)."""
     import math
-    print(f"\nflash_attn_plan_rope n_kv {n_kv} pos {pos} cell {cell} heads {n_head}/{n_head_kv} D {D} mode {mode}",
-          flush=True)
+    print(f"\nflash_attn_plan_rope n_kv {n_kv} pos {pos} cell {cell} heads {n_head}/{n_head_kv} D {D} mode {mode} "
+          f"n_dims {n_dims} general {general}", flush=True)
     rng = np.random.default_rng(n_kv + pos + D)
     E, nq = n_head_kv * D, n_head * D
-    kv_size = n_kv
+    kv_size = 16 * -(-n_kv // 16) if general else n_kv   # a GENERAL mask covers whole groups of the cache
     k0 = np.zeros((kv_size, E // 32 * 34), np.uint8)
     v0 = np.zeros_like(k0)
     hist = max(pos, cell)
@@ -213,31 +219,115 @@ def test_flash_attn_plan_rope(dev, oc, n_kv, pos, cell, n_head, n_head_kv, D, mo
     row = rng.standard_normal((1, nq + 2 * E)).astype(np.float32)
     row[0, :SPECIALS.size] = SPECIALS
     base = 500000.0
-    ts = theta_scale(base, D)
+    ts = theta_scale(base, n_dims)
     neox = mode != H.ROPE_NORMAL
-    q = oc.rope(np.ascontiguousarray(row[:, :nq]), np.array([pos], np.int32), D, D, neox, ts)
-    k = oc.rope(np.ascontiguousarray(row[:, nq:nq + E]), np.array([pos], np.int32), D, D, neox, ts)
+    q = oc.rope(np.ascontiguousarray(row[:, :nq]), np.array([pos], np.int32), D, n_dims, neox, ts)
+    k = oc.rope(np.ascontiguousarray(row[:, nq:nq + E]), np.array([pos], np.int32), D, n_dims, neox, ts)
     kw, vw = k0.copy(), v0.copy()
     oc.kv_set_rows(kw, k, np.array([cell], np.int64))
     oc.kv_set_rows(vw, np.ascontiguousarray(row[:, nq + E:]), np.array([cell], np.int64))
-    msum = np.zeros(12, np.uint32)
-    msum[0], msum[1], msum[2], msum[9] = 0x4D55534D, 1, n_kv, hist + 1
-    runs = np.array([[cell, cell + 1]], np.uint32)
     scale = np.float32(1.0 / math.sqrt(D))
-    want = oc.flash_attn(q, kw, vw, D, n_head, n_head_kv, scale, msum, new_runs=runs)
+    mf = None
+    if general:
+        mask = np.full((1, n_kv), -np.inf, np.float16)
+        mask[0, :hist + 1] = 0
+        mask[0, rng.integers(0, hist + 1, hist // 7)] = -1.75
+        mask[0, rng.integers(0, hist + 1, hist // 11)] = -np.inf
+        mask[0, cell] = 0.5
+        msum = oc.msum(mask)
+        assert msum[3], "the mask must plan as GENERAL"
+        mf = oc.mask_f32(mask, scale)
+    else:
+        msum = np.zeros(12, np.uint32)
+        msum[0], msum[1], msum[2], msum[9] = 0x4D55534D, 1, n_kv, hist + 1
+    runs = np.array([[cell, cell + 1]], np.uint32)
+    want = oc.flash_attn(q, kw, vw, D, n_head, n_head_kv, scale, msum, mf, new_runs=runs)
     kc, vc = dev.kv(E, kv_size), dev.kv(E, kv_size)
     kc.set_bytes(0, k0)
     vc.set_bytes(1, v0)
     plan = dev.fa_plan(D, n_head, n_head_kv, 1, kv_size)
-    plan.set(msum, runs)
+    plan.set(msum, runs, mask_f32=general)
     rb, out, bad = dev.upload(row), dev.alloc(4 * nq), dev.upload(np.zeros(1, np.int32))
-    dev.flash_attn_plan_rope(plan, rb, kc, vc, scale, D, mode, dev.upload(np.array([pos], np.int32)), base,
-                             dev.upload(np.array([cell], np.int64)), out, nq, bad=bad)
+    pb, cb = dev.upload(np.array([pos], np.int32)), dev.upload(np.array([cell], np.int64))
+    mb = None if mf is None else dev.upload(mf)
+    dev.flash_attn_plan_rope(plan, rb, kc, vc, scale, n_dims, mode, pb, base, cb, out, nq, bad=bad, mask_f32=mb)
     assert_bits_equal(out.read(np.float32, (1, nq)), want, "fa + rope")
     assert (kc.get_bytes(0).reshape(kv_size, -1) == kw).all()
     assert (vc.get_bytes(1).reshape(kv_size, -1) == vw).all()
     assert bad.read(np.int32, (1,))[0] == 0
     assert_bits_equal(rb.read(np.float32, (1, nq + 2 * E)), row, "the Q|K|V row is read, not rotated")
+    # the same with the angles from a table of the position, over fresh caches
+    kc.set_bytes(0, k0)
+    vc.set_bytes(1, v0)
+    tab, out2 = dev.alloc(4 * n_dims), dev.alloc(4 * nq)
+    dev.rope_table(pb, n_dims, base, tab)
+    dev.flash_attn_plan_rope_tab(plan, rb, kc, vc, scale, n_dims, mode, tab, cb, out2, nq, bad=bad, mask_f32=mb)
+    assert_bits_equal(out2.read(np.float32, (1, nq)), want, "fa + rope (table)")
+    assert (kc.get_bytes(0).reshape(kv_size, -1) == kw).all()
+    assert (vc.get_bytes(1).reshape(kv_size, -1) == vw).all()
+    assert bad.read(np.int32, (1,))[0] == 0
+    plan.free()
+    kc.free()
+    vc.free()
+
+
+@pytest.mark.parametrize("pos,n_dims,m", [(0, 128, 1.0), (7, 64, 1.0), (4231, 128, 1.0), (131071, 128, 0.75),
+                                          (-5, 8, 1.0), (1000, 2, 1.25)])
+def test_rope_table(dev, oc, pos, n_dims, m):
+    """tsr_hip_rope_table against the oracle's ROPE of a row of (1, 0) pairs (NORMAL): y_2i =
+    FS(FM(1, c), FM(0, s)) = c and y_2i+1 = FA(FM(1, s), FM(0, c)) = s, c = FM(M, cos theta_i) and
+    s = FM(M, sin theta_i), for every i < n_dims / 2."""
+    base = 500000.0
+    x = np.zeros((1, n_dims), np.float32)
+    x[0, 0::2] = 1.0
+    want = oc.rope(x, np.array([pos], np.int32), n_dims, n_dims, False, theta_scale(base, n_dims), m)
+    tab = dev.alloc(4 * n_dims)
+    dev.rope_table(dev.upload(np.array([pos], np.int32)), n_dims, base, tab, attn_factor=m)
+    assert_bits_equal(tab.read(np.float32, (1, n_dims)), want, f"rope table pos {pos}")
+
+
+def test_rope_table_refusals(dev):
+    b = dev.alloc(4096)
+    for n_dims in (0, 3, 130):
+        with pytest.raises(H.TsrHipError) as e:
+            dev.rope_table(b, n_dims, 10000.0, b)
+        assert e.value.code == -2
+    with pytest.raises(H.TsrHipError) as e:
+        dev.rope_table(b, 64, 10000.0, b.ptr + 4)                 # the table 8-byte aligned
+    assert e.value.code == -1
+    with pytest.raises(H.TsrHipError) as e:
+        dev.rope_table(b, 64, -1.0, b)
+    assert e.value.code == -1
+
+
+def test_flash_attn_plan_rope_bad_cell(dev, oc):
+    """A cell outside the caches: the flag is raised, the caches are left alone, and the attention
+    runs over the cached cells with the rotated query."""
+    import math
+    n_kv, pos, n_head, n_head_kv, D = 600, 520, 32, 8, 128
+    E, nq = n_head_kv * D, n_head * D
+    k0 = np.zeros((n_kv, E // 32 * 34), np.uint8)
+    v0 = np.zeros_like(k0)
+    oc.kv_set_rows(k0, S.normal(5, n_kv * E).reshape(n_kv, E), np.arange(n_kv))
+    oc.kv_set_rows(v0, S.normal(6, n_kv * E).reshape(n_kv, E), np.arange(n_kv))
+    row = np.random.default_rng(4).standard_normal((1, nq + 2 * E)).astype(np.float32)
+    base = 10000.0
+    q = oc.rope(np.ascontiguousarray(row[:, :nq]), np.array([pos], np.int32), D, D, False, theta_scale(base, D))
+    msum = np.zeros(12, np.uint32)
+    msum[0], msum[1], msum[2], msum[9] = 0x4D55534D, 1, n_kv, pos + 1
+    scale = np.float32(1.0 / math.sqrt(D))
+    want = oc.flash_attn(q, k0, v0, D, n_head, n_head_kv, scale, msum)
+    kc, vc = dev.kv(E, n_kv), dev.kv(E, n_kv)
+    kc.set_bytes(0, k0)
+    vc.set_bytes(1, v0)
+    plan = dev.fa_plan(D, n_head, n_head_kv, 1, n_kv)
+    plan.set(msum)
+    out, bad = dev.alloc(4 * nq), dev.upload(np.zeros(1, np.int32))
+    dev.flash_attn_plan_rope(plan, dev.upload(row), kc, vc, scale, D, H.ROPE_NORMAL, dev.upload(np.array([pos], np.int32)),
+                             base, dev.upload(np.array([n_kv], np.int64)), out, nq, bad=bad)
+    assert bad.read(np.int32, (1,))[0] == 1
+    assert (kc.get_bytes(0).reshape(n_kv, -1) == k0).all() and (vc.get_bytes(1).reshape(n_kv, -1) == v0).all()
+    assert_bits_equal(out.read(np.float32, (1, nq)), want, "fa + rope, bad cell")
     plan.free()
     kc.free()
     vc.free()

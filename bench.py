@@ -333,17 +333,21 @@ def cpu_decode(e2e: dict, max_seconds: float = 12.0, max_tokens: int = 4) -> dic
                        "tokens_compared": n}}
 
 
-def extra_workloads(dev, ev, stream, n: int) -> dict:
+def extra_workloads(dev, ev, stream, n: int, eager: bool = False) -> dict:
     """The other single-GPU BASELINE configs, each timed over rotating device copies (> 2x MALL):
     configs[1] the Q4_K FFN up/down pair, configs[0] Q8_0 matvec 4864x896, configs[2] q8-KV
     flash-decode (32 q / 8 KV heads, D 128, n_kv 8192, batch 1), configs[3] the prefill matmuls and
-    the causal prefill attention. Per-call time from HIP events on the launch stream."""
+    the causal prefill attention. Per-call time from HIP events on the launch stream (graph replay
+    and direct launches; with `eager`, direct launches only)."""
     out = {}
 
     def timed(fn, nn=None):
         for i in range(5):
             fn(i)
         ev.device_sync()
+        if eager:
+            t = ev.eager_ms(stream, fn, nn or n)
+            return t, t
         return ev.graph_ms(stream, fn, nn or n)
 
     def timed_eager(fn, nn):
@@ -557,7 +561,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
-    ap.add_argument("--eager", action="store_true", help="time the decode tokens as direct launches, not graph replays")
+    ap.add_argument("--eager", action="store_true", help="time everything as direct launches: no HIP graph is built")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.pmc_child:
@@ -599,7 +603,7 @@ def main() -> int:
     m = e2e.pop("model")
     m.free()
 
-    also = {} if args.no_extra else extra_workloads(dev, ev, stream, 200)
+    also = {} if args.no_extra else extra_workloads(dev, ev, stream, 200, eager=args.eager)
     cpu = None if args.no_cpu else cpu_decode(e2e)
     ms_tok = e2e["ms_per_token"]
     out = {

@@ -56,6 +56,12 @@ extern "C" {
  * (tsr_hip_swiglu), bit-identical, in one launch. No addend, no ACC_DST; the matvec path only (not the
  * Q8_0 T >= 16 prefill shapes); N even (row blocks are always whole pairs). */
 #define TSR_HIP_MM_GLU      0x2u
+/* tsr_hip_mul_mat_epi: the MVM record's local scale applied to y after the addend / ACC
+ * (TSR_MVM_LOCAL_SCALE / _SOFTCAP, sw/sim/tsr_sim.c:1648-1667; GGML MUL_MAT followed by SCALE, or the
+ * logit softcap tanh(y fs) sc): SCALE y = FM(y, scale); SOFTCAP y = FM(TANH(FM(y, first_scale)), scale)
+ * with the VU's TANH (sw/sim/tsr_ref_math.c:182-199). Not with TSR_HIP_MM_GLU; not both. */
+#define TSR_HIP_MM_SCALE    0x4u
+#define TSR_HIP_MM_SOFTCAP  0x8u
 
 typedef struct tsr_hip_ctx tsr_hip_ctx;
 typedef struct tsr_hip_weight tsr_hip_weight;
@@ -141,6 +147,11 @@ int tsr_hip_mul_mat(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x
 int tsr_hip_mul_mat_norm(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T,
                          uint64_t x_stride, float eps, const float * norm_w_dev, float * y_dev, uint64_t y_stride,
                          const float * add_dev, uint64_t add_stride, uint32_t flags, void * stream);
+/* tsr_hip_mul_mat with the SCALE / SOFTCAP epilogue of its flags (TSR_HIP_MM_SCALE, TSR_HIP_MM_SOFTCAP,
+ * the words 6 and 7 of the MVM record: first_scale, scale). Every MUL_MAT shape, the prefill path too. */
+int tsr_hip_mul_mat_epi(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T, uint64_t x_stride,
+                        float * y_dev, uint64_t y_stride, const float * add_dev, uint64_t add_stride, uint32_t flags,
+                        float first_scale, float scale, void * stream);
 /* The exact integer part of MUL_MAT for checking: for token 0, the per-block sums of every row
  * (Q8_0: isum per 32-block, N x K/32; Q4_K: isum and msum per super-block interleaved,
  * N x 2K/256) as the MVM computes them (term_q8_0 / term_q4_K, sw/sim/tsr_ref.c:525-567). */

@@ -125,6 +125,8 @@ void  oc_rope(uint32_t neox, uint32_t head_dim, uint32_t n_dims, uint32_t n_head
               const float * x, uint64_t x_stride, float * y, uint64_t y_stride, const int32_t * pos,
               float ts, float m, float freq_scale, const float * ff);
 float oc_silu(float x);
+float oc_tanh(float x);
+void  oc_mm_epilogue(float * y, uint64_t n, uint32_t mode, float fs, float sc);
 void  oc_swiglu_rows(uint32_t n, uint32_t rows, const float * g, uint64_t g_stride, const float * u, uint64_t u_stride,
                      float * y, uint64_t y_stride);
 void  oc_add_rows(uint32_t n, uint32_t rows, const float * a, uint64_t a_stride, const float * b, uint64_t b_stride,

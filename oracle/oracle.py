@@ -99,6 +99,9 @@ class Oracle:
                               C.c_uint64, _i32p, C.c_float, C.c_float, C.c_float, C.c_void_p]
         L.oc_silu.argtypes = [C.c_float]
         L.oc_silu.restype = C.c_float
+        L.oc_tanh.argtypes = [C.c_float]
+        L.oc_tanh.restype = C.c_float
+        L.oc_mm_epilogue.argtypes = [_f32p, C.c_uint64, C.c_uint32, C.c_float, C.c_float]
         L.oc_swiglu_rows.argtypes = [C.c_uint32, C.c_uint32, _f32p, C.c_uint64, _f32p, C.c_uint64, _f32p, C.c_uint64]
         L.oc_add_rows.argtypes = [C.c_uint32, C.c_uint32, _f32p, C.c_uint64, _f32p, C.c_uint64, _f32p, C.c_uint64]
         L.oc_get_rows.argtypes = [C.c_uint32, _f32p, C.c_uint64, _i32p, C.c_uint32, _f32p, C.c_uint64]
@@ -184,8 +187,9 @@ class Oracle:
         self.lib.oc_isums_n(fmt, w, N, K, np.ascontiguousarray(qa, np.uint8).ravel(), out)
         return out
 
-    def mul_mat(self, fmt: int, w, K: int, x, add=None, threads: int = 1) -> np.ndarray:
-        """y[T][N] = MUL_MAT(w [N][row_bytes], x [T][K]); add: [T][N] addend (or [1][N])."""
+    def mul_mat(self, fmt: int, w, K: int, x, add=None, threads: int = 1, epi=None) -> np.ndarray:
+        """y[T][N] = MUL_MAT(w [N][row_bytes], x [T][K]); add: [T][N] addend (or [1][N]); epi:
+        (1, _, scale) SCALE or (2, first_scale, scale) SOFTCAP after the addend."""
         w = np.ascontiguousarray(w, np.uint8)
         x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
         N, T = w.shape[0], x.shape[0]
@@ -195,6 +199,8 @@ class Oracle:
             add = np.ascontiguousarray(np.atleast_2d(add), np.float32)
             add_p, add_s = add.ctypes.data, (N if add.shape[0] > 1 else 0)
         self.lib.oc_mul_mat(fmt, w, N, K, x, T, K, add_p, add_s, y, N, threads)
+        if epi is not None:
+            self.lib.oc_mm_epilogue(y, y.size, int(epi[0]), float(epi[1]), float(epi[2]))
         return y
 
     # -- attention -------------------------------------------------------------------------------
@@ -315,6 +321,11 @@ def _o_silu(self, x) -> np.ndarray:
     return np.array([self.lib.oc_silu(float(v)) for v in x], np.float32)
 
 
+def _o_tanh(self, x) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    return np.array([self.lib.oc_tanh(float(v)) for v in x], np.float32)
+
+
 def _o_swiglu(self, g, u) -> np.ndarray:
     g = np.ascontiguousarray(np.atleast_2d(g), np.float32)
     u = np.ascontiguousarray(np.atleast_2d(u), np.float32)
@@ -354,6 +365,7 @@ Oracle.rms_norm = _o_rms_norm
 Oracle.sincos = _o_sincos
 Oracle.rope = _o_rope
 Oracle.silu = _o_silu
+Oracle.tanh = _o_tanh
 Oracle.swiglu = _o_swiglu
 Oracle.add = _o_add
 Oracle.get_rows = _o_get_rows
@@ -434,6 +446,8 @@ class Ref:
         L.tsr_m_sincos.argtypes = [C.c_float, C.POINTER(C.c_float), C.POINTER(C.c_float)]
         L.tsr_m_silu.argtypes = [C.c_float]
         L.tsr_m_silu.restype = C.c_float
+        L.tsr_m_tanh.argtypes = [C.c_float]
+        L.tsr_m_tanh.restype = C.c_float
         L.tsr_ref_rope.argtypes = [C.POINTER(_RopeCfg), _u32p, C.c_uint32, _u32p, C.c_uint32, _u32p, C.c_void_p]
 
     def scalar(self, fn: str, *args):
@@ -579,6 +593,12 @@ def _r_vop(self, func: int, a, b=None, c=0.0) -> np.ndarray:
     return out.view(np.float32)
 
 
+def _r_tanh(self, x) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    return np.array([self.lib.tsr_m_tanh(float(v)) for v in x], np.float32)
+
+
+Ref.tanh = _r_tanh
 Ref.rms_norm = _r_rms_norm
 Ref.sincos = _r_sincos
 Ref.rope = _r_rope

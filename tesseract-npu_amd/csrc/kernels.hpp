@@ -28,6 +28,13 @@ enum MvPrep : uint32_t {
     kPrepNorm = 1,           // RMS_NORM of the token row, times pw when pw != 0 (k_rms_norm's rule)
 };
 
+// What tsr_hip_mul_mat_epi applies to y after the addend / ACC (the MVM record's local scale).
+enum MmEpi : uint32_t {
+    kEpiNone = 0,
+    kEpiScale = 1,           // y = FM(y, sc)
+    kEpiSoftcap = 2,         // y = FM(TANH(FM(y, fs)), sc)
+};
+
 // MUL_MAT over the device weight layout of wlayout.hpp (row blocks of rb rows at w).
 struct MvArgs {
     const uint8_t * w;
@@ -173,6 +180,8 @@ int tsr_launch_rms_norm(const float * x, uint64_t x_stride, uint32_t n, uint32_t
                         const float * w, uint64_t w_stride, uint32_t w_period, float * y, uint64_t y_stride, hipStream_t s);
 int tsr_launch_rope(const tsr::RopeArgs & a, uint32_t T, hipStream_t s);
 int tsr_launch_rope_table(const int32_t * pos, uint32_t half, float ts, float m, float * tab, hipStream_t s);
+int tsr_launch_mm_epilogue(float * y, uint64_t y_stride, uint32_t N, uint32_t T, uint32_t mode, float fs, float sc,
+                           const tsr::ExpkTab & ex, hipStream_t s);
 int tsr_launch_swiglu(const float * g, uint64_t g_stride, const float * u, uint64_t u_stride, float * y, uint64_t y_stride,
                       uint32_t n, uint32_t rows, const tsr::ExpkTab & ex, hipStream_t s);
 int tsr_launch_add(const float * a, uint64_t a_stride, const float * b, uint64_t b_stride, uint32_t b_period, float * y,

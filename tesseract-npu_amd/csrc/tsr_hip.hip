@@ -460,6 +460,7 @@ static int mul_mat_locked(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
         a.glu = 1u;
         a.ex = ctx->expk;
     }
+
     ctx->ctr.mul_mat_calls++;
     ctx->ctr.mul_mat_rows += (uint64_t)w->N * T;
     ctx->ctr.mul_mat_weight_bytes += (uint64_t)w->N * nb * blk_bytes(w->fmt);
@@ -489,6 +490,7 @@ static int mul_mat_locked(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
             m.K = w->K;
             m.T = tt;
             m.acc = a.acc;
+
             if (tsr_launch_mm_q8_0(m, s)) return TSR_HIP_E_HIP;
         }
         return TSR_HIP_OK;
@@ -508,16 +510,38 @@ static int mul_mat_locked(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
 int tsr_hip_mul_mat(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T, uint64_t x_stride,
                     float * y_dev, uint64_t y_stride, const float * add_dev, uint64_t add_stride, uint32_t flags,
                     void * stream) {
-    if (ctx == nullptr) return TSR_HIP_E_ARG;
+    if (ctx == nullptr || (flags & (TSR_HIP_MM_SCALE | TSR_HIP_MM_SOFTCAP))) return TSR_HIP_E_ARG;   // _epi has the scales
     std::lock_guard<std::mutex> lk(ctx->mtx);
     return mul_mat_locked(ctx, w, x_dev, T, x_stride, y_dev, y_stride, add_dev, add_stride, flags, nullptr,
                           ctx->pick(stream));
 }
 
+int tsr_hip_mul_mat_epi(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T, uint64_t x_stride,
+                        float * y_dev, uint64_t y_stride, const float * add_dev, uint64_t add_stride, uint32_t flags,
+                        float first_scale, float scale, void * stream) {
+    // the MUL_MAT, then one elementwise launch over its T x N result: the MUL_MAT kernels carry no
+    // epilogue code (their store tail is on the critical path of every decode launch)
+    const uint32_t ef = flags & (TSR_HIP_MM_SCALE | TSR_HIP_MM_SOFTCAP);
+    if (ctx == nullptr || w == nullptr || ef == 0u || ef == (TSR_HIP_MM_SCALE | TSR_HIP_MM_SOFTCAP) ||
+        (flags & TSR_HIP_MM_GLU))
+        return TSR_HIP_E_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    const hipStream_t s = ctx->pick(stream);
+    int rc = mul_mat_locked(ctx, w, x_dev, T, x_stride, y_dev, y_stride, add_dev, add_stride, flags & ~ef, nullptr, s);
+    if (rc) return rc;
+    const uint32_t mode = ef == TSR_HIP_MM_SOFTCAP ? tsr::kEpiSoftcap : tsr::kEpiScale;
+    for (uint32_t t0 = 0; t0 < T; t0 += 65535u) {
+        rc = tsr_launch_mm_epilogue(y_dev + (size_t)t0 * y_stride, y_stride, w->N, std::min(T - t0, 65535u), mode,
+                                    first_scale, scale, ctx->expk, s);
+        if (rc) return TSR_HIP_E_HIP;
+    }
+    return TSR_HIP_OK;
+}
+
 int tsr_hip_mul_mat_norm(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T,
                          uint64_t x_stride, float eps, const float * norm_w_dev, float * y_dev, uint64_t y_stride,
                          const float * add_dev, uint64_t add_stride, uint32_t flags, void * stream) {
-    if (ctx == nullptr || w == nullptr) return TSR_HIP_E_ARG;
+    if (ctx == nullptr || w == nullptr || (flags & (TSR_HIP_MM_SCALE | TSR_HIP_MM_SOFTCAP))) return TSR_HIP_E_ARG;
     MmPrep p{};
     p.kind = tsr::kPrepNorm;
     p.pw = norm_w_dev;

@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(HERE, "libtsr_hip.so")
 FMT_Q8_0, FMT_Q4_K = 0, 1
 QA_A32, QA_A256 = 0, 1
 KV_K, KV_V = 0, 1
-MM_ACC_DST, MM_GLU = 1, 2
+MM_ACC_DST, MM_GLU, MM_SCALE, MM_SOFTCAP = 1, 2, 4, 8
 ROPE_NORMAL, ROPE_NEOX, ROPE_IMROPE = 0, 2, 40
 
 # the exported symbols of include/tsr_hip.h
@@ -36,7 +36,7 @@ EXPORTS = (
     "tsr_hip_write_async", "tsr_hip_copy_async", "tsr_hip_fa_plan_create", "tsr_hip_fa_plan_set", "tsr_hip_flash_attn_plan",
     "tsr_hip_fa_plan_free", "tsr_hip_graph_begin", "tsr_hip_graph_end", "tsr_hip_graph_launch", "tsr_hip_graph_free",
     "tsr_hip_mul_mat_norm", "tsr_hip_rope_kv", "tsr_hip_flash_attn_plan_rope", "tsr_hip_rope_table",
-    "tsr_hip_flash_attn_plan_rope_tab",
+    "tsr_hip_flash_attn_plan_rope_tab", "tsr_hip_mul_mat_epi",
 )
 
 
@@ -110,6 +110,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "tsr_hip_flash_attn_plan_rope": ([vp, vp, vp, vp, vp, C.c_float, u32, C.c_int, vp, C.c_float, C.c_float, vp, vp,
                                           vp, vp, u64, vp], C.c_int),
         "tsr_hip_rope_table": ([vp, vp, u32, C.c_float, C.c_float, vp, vp], C.c_int),
+        "tsr_hip_mul_mat_epi": ([vp, vp, vp, u32, u64, vp, u64, vp, u64, u32, C.c_float, C.c_float, vp], C.c_int),
         "tsr_hip_flash_attn_plan_rope_tab": ([vp, vp, vp, vp, vp, C.c_float, u32, C.c_int, vp, vp, vp, vp, vp, u64, vp],
                                              C.c_int),
     }
@@ -363,6 +364,12 @@ class Device:
                 flags: int = 0, stream=None) -> None:
         _check(self.L.tsr_hip_mul_mat(self.ctx, w.h, self._p(x), T, x_stride, self._p(y), y_stride, self._p(add),
                                       add_stride, flags, stream), "mul_mat")
+
+    def mul_mat_epi(self, w: "Weight", x, T: int, x_stride: int, y, y_stride: int, flags: int, first_scale: float,
+                    scale: float, add=None, add_stride: int = 0, stream=None) -> None:
+        """mul_mat with the SCALE / SOFTCAP epilogue of flags (MM_SCALE, MM_SOFTCAP) after the addend / ACC."""
+        _check(self.L.tsr_hip_mul_mat_epi(self.ctx, w.h, self._p(x), T, x_stride, self._p(y), y_stride, self._p(add),
+                                          add_stride, flags, float(first_scale), float(scale), stream), "mul_mat_epi")
 
     def mul_mat_norm(self, w: Weight, x, T: int, x_stride: int, eps: float, norm_w, y, y_stride: int, add=None,
                      add_stride: int = 0, flags: int = 0, stream=None) -> None:

@@ -155,3 +155,50 @@ def test_mul_mat_vocab_head(dev, oc, fmt):
     N, K = 128256, 4096
     got, want = _mm_case(dev, oc, fmt, N, K, seed=9, wblocks=S.quant_rows(fmt, 77, N, K))
     assert_bits_equal(got, want, f"fmt {fmt} {N}x{K}")
+
+
+@pytest.mark.parametrize("fmt,N,K,T,mode,extra", [
+    (1, 4096, 4096, 1, 2, "add"),          # Q4_K matvec, SOFTCAP after the residual addend
+    (0, 4864, 896, 1, 1, "acc"),           # Q8_0 matvec, SCALE after ACC
+    (1, 512, 4096, 3, 2, None),            # Q4_K, several tokens (the matvec per token)
+    (0, 300, 896, 40, 2, "add"),           # Q8_0 T >= 16: the matrix-core prefill path
+    (0, 130, 1024, 33, 1, None),           # prefill, SCALE, ragged tiles
+    (0, 48, 1024, 4, 2, "special"),        # special activations: NaN / Inf dots through TANH
+])
+def test_mul_mat_scale_softcap(dev, oc, fmt, N, K, T, mode, extra):
+    """tsr_hip_mul_mat_epi (the MVM record's local SCALE / SOFTCAP after ACC, sw/sim/tsr_sim.c:1648-1667)
+    against the oracle's MUL_MAT with the same epilogue, bit for bit."""
+    print(f"\nmul_mat_epi fmt {fmt} {N}x{K} T {T} mode {mode} {extra}", flush=True)
+    seed = N + K + T
+    blocks = weights(fmt, N, K, seed)
+    w = dev.weight(fmt, blocks, N, K)
+    if extra == "special":
+        x = np.stack([special_row(K, 1), S.normal(2, K, 1e-25), S.normal(3, K, 30.0), np.zeros(K, np.float32)])
+    else:
+        x = S.normal(seed + 100, T * K).reshape(T, K)
+    y0 = S.normal(seed + 200, T * N).reshape(T, N)
+    a = S.normal(seed + 300, T * N).reshape(T, N) if extra == "add" else None
+    yb = dev.upload(y0)
+    fs, sc = (np.float32(1.0 / 30.0), np.float32(30.0)) if mode == 2 else (np.float32(0.0), np.float32(0.125))
+    flags = (tsr_hip.MM_SOFTCAP if mode == 2 else tsr_hip.MM_SCALE) | (tsr_hip.MM_ACC_DST if extra == "acc" else 0)
+    dev.mul_mat_epi(w, dev.upload(x), T, K, yb, N, flags, fs, sc, add=None if a is None else dev.upload(a),
+                    add_stride=N if a is not None else 0)
+    got = yb.read(np.float32, (T, N))
+    want = oc.mul_mat(fmt, blocks, K, x, add=(a if a is not None else (y0 if extra == "acc" else None)), threads=8,
+                      epi=(mode, fs, sc))
+    assert_bits_equal(got, want, f"epilogue {mode} fmt {fmt} {N}x{K} T {T}")
+    w.free()
+
+
+def test_mul_mat_scale_softcap_refusals(dev):
+    w = dev.weight(0, weights(0, 64, 256, 1), 64, 256)
+    b = dev.alloc(4 * 4096)
+    for call, code in [
+        (lambda: dev.mul_mat(w, b, 1, 256, b.ptr + 4096, 64, flags=tsr_hip.MM_SCALE), -1),     # no scales here
+        (lambda: dev.mul_mat_epi(w, b, 1, 256, b.ptr + 4096, 64, tsr_hip.MM_SCALE | tsr_hip.MM_SOFTCAP, 1.0, 1.0), -1),
+        (lambda: dev.mul_mat_epi(w, b, 1, 256, b.ptr + 4096, 32, tsr_hip.MM_GLU | tsr_hip.MM_SCALE, 1.0, 1.0), -1),
+    ]:
+        with pytest.raises(tsr_hip.TsrHipError) as e:
+            call()
+        assert e.value.code == code
+    w.free()

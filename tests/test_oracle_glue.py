@@ -145,3 +145,45 @@ def test_get_rows_argmax(o):
     x[1, 10] = x[1, 500] = 9.0                                         # first maximum wins
     x[2, 3] = np.nan
     assert np.array_equal(o.argmax(x), np.array([np.argmax(x[0]), 10, np.nanargmax(x[2]), np.argmax(x[3])]))
+
+
+def test_tanh_bitwise_vs_ref(o, r):
+    """oc_tanh (the MUL_MAT softcap's TANH) bit for bit against tsr_m_tanh: random values across both
+    branches (|x| < 2^-6 and above), the branch boundary, subnormals, specials and random bit patterns."""
+    rng = np.random.default_rng(11)
+    edge = np.array([0x3C800000, 0x3C7FFFFF, 0xBC800000, 0xBC7FFFFF, 0x41200000, 0x42000000, 0x00400000,
+                     0x80400000, 0x7F000000, 0x7E800000], np.uint32).view(np.float32)
+    x = np.concatenate([SPECIALS, edge, rng.uniform(-12, 12, 20000).astype(np.float32),
+                        (rng.standard_normal(10000) * 0.01).astype(np.float32),
+                        rng.integers(0, 2 ** 32, 40000, dtype=np.uint64).astype(np.uint32).view(np.float32)])
+    assert (bits(o.tanh(x)) == bits(r.tanh(x))).all()
+
+
+def test_tanh_closed_form(o):
+    """Against float64 tanh (the EXPK error, < 4 ulp, grows by the 1 - e cancellation below |x| ~ 0.1),
+    odd symmetry bit for bit, the limits, zeros, DAZ and the canonical NaN."""
+    x = np.linspace(-9, 9, 20001, dtype=np.float32)
+    got = o.tanh(x).astype(np.float64)
+    want = np.tanh(x.astype(np.float64))
+    assert (np.abs(got - want) <= 2e-5 * np.abs(want) + 1e-7).all()
+    assert (bits(o.tanh(-x)) == (bits(o.tanh(x)) ^ 0x80000000)).all()
+    sp = np.array([0x7F800000, 0xFF800000, 0x00000000, 0x80000000, 0x00000001, 0x80000001, 0x7FC00000, 0xFFC00001],
+                  np.uint32).view(np.float32)
+    assert bits(o.tanh(sp)).tolist() == [0x3F800000, 0xBF800000, 0, 0x80000000, 0, 0x80000000, 0x7FC00000, 0x7FC00000]
+
+
+def test_mul_mat_epilogue_wiring(o):
+    """oc_mul_mat's SCALE / SOFTCAP epilogue is applied after the addend, with the scales in their
+    places: SCALE y = (dot + add) * sc, SOFTCAP y = TANH((dot + add) * fs) * sc (float32 products of
+    normal values: the rule's FM)."""
+    import tsr_synth as S
+    N, K = 64, 256
+    w = S.quant_rows(0, 5, N, K)
+    x = S.normal(6, 2 * K).reshape(2, K)
+    add = S.normal(7, 2 * N).reshape(2, N)
+    y = o.mul_mat(0, w, K, x, add=add)
+    fs, sc = np.float32(0.0333), np.float32(30.0)
+    assert (bits(o.mul_mat(0, w, K, x, add=add, epi=(1, 0.0, sc))) == bits(y * sc)).all()
+    soft = o.mul_mat(0, w, K, x, add=add, epi=(2, fs, sc))
+    assert (bits(soft) == bits(o.tanh(y * fs).reshape(y.shape) * sc)).all()
+    assert np.abs(soft).max() <= sc

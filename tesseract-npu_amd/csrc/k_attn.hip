@@ -356,7 +356,6 @@ __host__ __device__ inline uint32_t fa_fuse_lds(uint32_t D) {
     const uint32_t bb = D / 32u < 4u ? D / 32u : 4u;
     return 256u + 4u * 4u * 256u + 4u * 4u * 4u * D + 4u * 16u + 4u * bb * 1024u + 32u;
 }
-constexpr uint32_t kFaSpinMax = 1u << 20;                        // polls of the tile barrier (s_sleep 1 each)
 
 // Data that blocks on other XCDs read after a counter moves only through accesses coherent at agent
 // scope (relaxed atomics: sc1 stores write through to the coherence point, sc1 loads bypass stale
@@ -440,7 +439,7 @@ __device__ __forceinline__ void fa_fused_tail(const FaArgs & a, const FaPlan & p
         for (;;) {
             v = lane < nk ? ld_co_u(kp) : 1u;
             if (__all(v != 0u)) break;
-            if (++spins >= kFaSpinMax) {
+            if (++spins >= a.spin_max) {
                 if (lane == 0u && a.bad != nullptr)
                     __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;

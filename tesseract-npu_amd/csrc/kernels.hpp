@@ -119,6 +119,7 @@ struct FaArgs {
     float * m_item;          // [item][n_head] chunk maxima
     uint32_t * tkeys;
     uint32_t * sync;
+    uint32_t spin_max;       // polls of the tile-key wait before it gives up (*bad = 2)
     uint32_t max_groups;     // the largest item (groups), for a work list in device memory
     float * out;
     uint64_t out_stride;

@@ -120,6 +120,7 @@ struct tsr_hip_ctx {
     tsr_scratch scratch;
     tsr_staging staging;
     tsr::ExpkTab expk{};
+    uint32_t fa_spin_max = 1u << 20;    // polls of the fused decode FA's tile-key wait (s_sleep 1 each)
     hipStream_t pick(void * s) const { return s ? (hipStream_t)s : stream; }
 };
 

@@ -479,6 +479,13 @@ int tsr_hip_fa_plan_create(tsr_hip_ctx * ctx, uint32_t D, uint32_t n_head, uint3
     return TSR_HIP_OK;
 }
 
+int tsr_hip_set_fa_wait_limit(tsr_hip_ctx * ctx, uint32_t polls) {
+    if (ctx == nullptr) return TSR_HIP_E_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    ctx->fa_spin_max = polls ? polls : (1u << 20);
+    return TSR_HIP_OK;
+}
+
 int tsr_hip_fa_plan_free(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan) {
     if (ctx == nullptr || plan == nullptr) return TSR_HIP_E_ARG;
     std::lock_guard<std::mutex> lk(ctx->mtx);
@@ -557,6 +564,7 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
         a.seg_l = (float *)(plan->dev + plan->o_SL);
         a.m_item = (float *)(plan->dev + plan->o_MI);
         a.tkeys = (uint32_t *)(plan->dev + plan->o_TK);
+        a.spin_max = ctx->fa_spin_max;
         a.sync = (uint32_t *)(plan->dev + plan->o_sync);
     }
     if (rope != nullptr) {

@@ -36,7 +36,7 @@ EXPORTS = (
     "tsr_hip_write_async", "tsr_hip_copy_async", "tsr_hip_fa_plan_create", "tsr_hip_fa_plan_set", "tsr_hip_flash_attn_plan",
     "tsr_hip_fa_plan_free", "tsr_hip_graph_begin", "tsr_hip_graph_end", "tsr_hip_graph_launch", "tsr_hip_graph_free",
     "tsr_hip_mul_mat_norm", "tsr_hip_rope_kv", "tsr_hip_flash_attn_plan_rope", "tsr_hip_rope_table",
-    "tsr_hip_flash_attn_plan_rope_tab", "tsr_hip_mul_mat_epi",
+    "tsr_hip_flash_attn_plan_rope_tab", "tsr_hip_mul_mat_epi", "tsr_hip_set_fa_wait_limit",
 )
 
 
@@ -111,6 +111,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
                                           vp, vp, u64, vp], C.c_int),
         "tsr_hip_rope_table": ([vp, vp, u32, C.c_float, C.c_float, vp, vp], C.c_int),
         "tsr_hip_mul_mat_epi": ([vp, vp, vp, u32, u64, vp, u64, vp, u64, u32, C.c_float, C.c_float, vp], C.c_int),
+        "tsr_hip_set_fa_wait_limit": ([vp, u32], C.c_int),
         "tsr_hip_flash_attn_plan_rope_tab": ([vp, vp, vp, vp, vp, C.c_float, u32, C.c_int, vp, vp, vp, vp, vp, u64, vp],
                                              C.c_int),
     }
@@ -428,6 +429,10 @@ class Device:
                                                    self._p(pos), float(freq_base), float(attn_factor), self._p(cell),
                                                    self._p(bad), self._p(mask_f32), self._p(out), out_stride, stream),
                "flash_attn_plan_rope")
+
+    def set_fa_wait_limit(self, polls: int) -> None:
+        """Polls of the fused decode FA's bounded wait (0: the default)."""
+        _check(self.L.tsr_hip_set_fa_wait_limit(self.ctx, polls), "set_fa_wait_limit")
 
     def rope_table(self, pos, n_dims: int, freq_base: float, tab, attn_factor: float = 1.0, stream=None) -> None:
         """The ROPE angles of position *pos: tab[2 i], tab[2 i + 1] = M cos, M sin of theta_i, i < n_dims / 2."""

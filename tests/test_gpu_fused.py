@@ -346,3 +346,59 @@ def test_flash_attn_plan_rope_refusals(dev):
     plan.free()
     kc.free()
     vc.free()
+
+
+def test_flash_attn_plan_rope_wait_expires(dev, oc):
+    """The one-launch decode form's bounded wait forced to expire from the host (a poll limit of 1): the
+    launch still ends, raises *bad = 2, and leaves the plan's keys and counters clear, so that the next
+    launch with the default limit is bit-exact again."""
+    import math
+    n_kv, pos, n_head, n_head_kv, D = 4232, 4100, 32, 8, 128
+    E, nq = n_head_kv * D, n_head * D
+    k0 = np.zeros((n_kv, E // 32 * 34), np.uint8)
+    v0 = np.zeros_like(k0)
+    oc.kv_set_rows(k0, S.normal(21, n_kv * E).reshape(n_kv, E), np.arange(n_kv))
+    oc.kv_set_rows(v0, S.normal(22, n_kv * E).reshape(n_kv, E), np.arange(n_kv))
+    row = np.random.default_rng(5).standard_normal((1, nq + 2 * E)).astype(np.float32)
+    base = 500000.0
+    ts = theta_scale(base, D)
+    q = oc.rope(np.ascontiguousarray(row[:, :nq]), np.array([pos], np.int32), D, D, False, ts)
+    k = oc.rope(np.ascontiguousarray(row[:, nq:nq + E]), np.array([pos], np.int32), D, D, False, ts)
+    kw, vw = k0.copy(), v0.copy()
+    oc.kv_set_rows(kw, k, np.array([pos], np.int64))
+    oc.kv_set_rows(vw, np.ascontiguousarray(row[:, nq + E:]), np.array([pos], np.int64))
+    msum = np.zeros(12, np.uint32)
+    msum[0], msum[1], msum[2], msum[9] = 0x4D55534D, 1, n_kv, pos + 1
+    runs = np.array([[pos, pos + 1]], np.uint32)
+    scale = np.float32(1.0 / math.sqrt(D))
+    want = oc.flash_attn(q, kw, vw, D, n_head, n_head_kv, scale, msum, new_runs=runs)
+    kc, vc = dev.kv(E, n_kv), dev.kv(E, n_kv)
+    plan = dev.fa_plan(D, n_head, n_head_kv, 1, n_kv)
+    plan.set(msum, runs)
+    rb, pb, cb = dev.upload(row), dev.upload(np.array([pos], np.int32)), dev.upload(np.array([pos], np.int64))
+    tab = dev.alloc(4 * D)
+    dev.rope_table(pb, D, base, tab)
+    expired = 0
+    try:
+        # a workgroup gives up when its first poll finds a tile of its chunk unpublished: the tiles of
+        # a chunk publish microseconds apart, so with 16 chunks x KV heads per launch some always do
+        for limit in (1, 0, 1, 0):
+            kc.set_bytes(0, k0)
+            vc.set_bytes(1, v0)
+            bad, out = dev.upload(np.zeros(1, np.int32)), dev.alloc(4 * nq)
+            dev.set_fa_wait_limit(limit)
+            dev.flash_attn_plan_rope_tab(plan, rb, kc, vc, scale, D, H.ROPE_NORMAL, tab, cb, out, nq, bad=bad)
+            dev.sync()
+            got_bad = int(bad.read(np.int32, (1,))[0])
+            assert got_bad in (0, 2), got_bad
+            if limit:
+                expired |= got_bad
+            else:
+                assert got_bad == 0
+                assert_bits_equal(out.read(np.float32, (1, nq)), want, "after an expired wait")
+        assert expired == 2, "a poll limit of 1 never expired"
+    finally:
+        dev.set_fa_wait_limit(0)
+    plan.free()
+    kc.free()
+    vc.free()

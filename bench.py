@@ -4,7 +4,8 @@
 Headline workload (the configuration the metric is quoted on): greedy
 decode of a random-init Llama-3-8B-architecture model at batch 1 -- 32 layers, hidden 4096, FFN
 14336 SwiGLU, 32 q / 8 KV heads, head_dim 128, vocab 128256, every weight matrix (output head
-included) Q4_K from seeded N(0, 0.02), q8_0 KV caches holding 4096 cells of context. One step is
+included) Q4_K from seeded N(0, 0.02), q8_0 KV caches prefilled through the model with 4096 seeded
+random token ids (8 ubatches of 512 tokens, every layer's ops over the ubatch rows). One step is
 one decode token: the whole decoder (embedding row, 32 x [RMS_NORM, MUL_MAT QKV, ROPE, SET_ROWS_KV,
 FLASH_ATTN_EXT, MUL_MAT O + residual, RMS_NORM, MUL_MAT gate|up, SWIGLU, MUL_MAT down + residual],
 output norm, output head, ARGMAX) replayed as one HIP graph, the greedy token fed back on the device.
@@ -46,7 +47,8 @@ HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
 METRIC = "decode tok/s (8B Q4_K, ctx 4096); matvec/attn HBM GB/s as % of peak"
 CTX = 4096                      # KV cells filled before the first decode token
-FIRST_TOKEN = 128000            # the id of the first decoded token (Llama-3's <|begin_of_text|>)
+UBATCH = 512                    # prefill tokens per pass of the layers (llama.cpp's default n_ubatch)
+PROMPT_SEED = 4096              # numpy seed of the random prompt token ids
 
 
 class HipEvents:
@@ -178,8 +180,9 @@ def token_bytes(cfg, n_kv_read: int) -> int:
 def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
     """Llama-3-8B-architecture Q4_K decode with CTX cells of context.
 
-    Cells 0 .. CTX-1 of every layer's caches hold seeded rows (SET_ROWS_KV); token 0 is decoded at
-    position CTX eagerly (its logits are kept for the CPU leg's bit comparison), tokens 1 .. warmup-1
+    Cells 0 .. CTX-1 of every layer's caches are filled by the prefill of CTX random token ids in
+    ubatches of UBATCH (untimed; its rate is reported); token 0, the prompt's greedy token, is decoded
+    at position CTX eagerly (its logits are kept for the CPU leg's bit comparison), tokens 1 .. warmup-1
     by graph replays (the first replay captures), then `steps` timed graph replays at positions
     CTX+warmup .. CTX+warmup+steps-1; with `eager`, direct launches instead of every replay. Every
     greedy token is copied to a device history buffer."""
@@ -189,10 +192,15 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
     stream = dev.stream
     t0 = time.perf_counter()
     m = LL.LlamaDecoder(dev, cfg, wts, kv_size)
-    m.prefill_history(wts, CTX)
     setup_s = time.perf_counter() - t0
+    prompt = np.random.default_rng(PROMPT_SEED).integers(0, cfg.n_vocab, CTX).astype(np.int32)
+    t0 = time.perf_counter()
+    m.prefill(prompt, 0, UBATCH)
+    prefill_s = time.perf_counter() - t0
+    tok0 = m.read_next()
+    print(f"[bench] prefill of {CTX} random ids in ubatches of {UBATCH}: {prefill_s:.2f} s", flush=True)
     hist = dev.alloc(4 * (warmup + steps))
-    m.step(FIRST_TOKEN, CTX)
+    m.step(tok0, CTX)
     logits0 = m.read_logits().copy()
     tok1 = m.read_next()
     hist.write(np.array([tok1], np.int32))
@@ -275,16 +283,18 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
         "cfg": cfg, "wts": wts, "model": m, "kv_size": kv_size, "logits0": logits0, "tokens": toks.tolist(),
         "ms_per_token": ms_tok, "tok_s": 1e3 / ms_tok, "token_bytes": tb,
         "host_enqueue_ms_per_token": host_enqueue_s * 1e3 / steps, "wall_ms_per_token": wall_s * 1e3 / steps,
-        "setup_s": setup_s, "per_op": per_op, "captures": captures,
+        "setup_s": setup_s, "per_op": per_op, "captures": captures, "tok0": tok0, "prefill_s": prefill_s,
     }
     return out
 
 
 def cpu_decode(e2e: dict, max_seconds: float = 12.0, max_tokens: int = 4) -> dict:
     """The oracle's decode of the same model (the reference numerics restated in C, MUL_MAT on all the
-    host cores available, up to 16) from the same cache state: token 0 at position CTX with the same
-    first id, then the oracle's own greedy tokens, for about max_seconds. Its logits of token 0 are
-    compared bit for bit with the GPU's, and its greedy tokens with the GPU's."""
+    host cores available, up to 16) from the same cache state (the GPU's prefilled cache bytes, read
+    back): token 0 at position CTX with the same first id, then the oracle's own greedy tokens, for
+    about max_seconds. Its logits of token 0 are compared bit for bit with the GPU's, and its greedy
+    tokens with the GPU's. (The prefill itself is checked against the oracle on small models by the
+    tests; at 8B it would take the oracle hours.)"""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle
     from oracle_llama import OracleLlama
@@ -303,15 +313,16 @@ def cpu_decode(e2e: dict, max_seconds: float = 12.0, max_tokens: int = 4) -> dic
                       n_head_kv=cfg.n_head_kv, head_dim=cfg.head_dim, n_vocab=cfg.n_vocab, eps=cfg.eps,
                       rope_base=cfg.rope_base, rope_mode=cfg.rope_mode, wfmt=cfg.wfmt, ofmt=cfg.ofmt, tensors=t,
                       kv_size=kv_size, threads=threads)
-    for il in range(cfg.n_layer):
+    for il, caches in enumerate(e2e["caches"]):
         for which in (0, 1):
-            ref.set_history(il, which, wts.kv_history(il, which, CTX))
+            ref.set_cache_bytes(il, which, caches[which])
+    e2e["caches"] = None
     libm = C.CDLL("libm.so.6")
     libm.powf.argtypes = [C.c_float, C.c_float]
     libm.powf.restype = C.c_float
     ts = np.float32(libm.powf(float(np.float32(cfg.rope_base)), float(np.float32(-2.0) / np.float32(cfg.head_dim))))
     gpu_toks = e2e["tokens"]
-    tok, n, times, same_tokens, logits_equal = FIRST_TOKEN, 0, [], True, None
+    tok, n, times, same_tokens, logits_equal = e2e["tok0"], 0, [], True, None
     while n < max_tokens:
         pos = CTX + n
         t0 = time.perf_counter()
@@ -601,6 +612,8 @@ def main() -> int:
         traffic_bytes = round(traffic["FETCH_SIZE"][tag] + traffic["WRITE_SIZE"][tag])
     achieved = dv["algorithmic_bytes"] / (dv["launch_us"] * 1e-6) / 1e9
     m = e2e.pop("model")
+    # the CPU leg decodes from the GPU's prefilled caches (the ggml q8_0 images, read back)
+    e2e["caches"] = None if args.no_cpu else [(L["kc"].get_bytes(0), L["vc"].get_bytes(1)) for L in m.layers]
     m.free()
 
     also = {} if args.no_extra else extra_workloads(dev, ev, stream, 200, eager=args.eager)
@@ -618,7 +631,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4_k/q8_0 int8 dot products, f32 accumulate (spec f32 rules)",
-        "data": "synthetic: random-init weights N(0,0.02) quantized to Q4_K, seeded KV rows, greedy tokens",
+        "data": ("synthetic: random-init weights N(0,0.02) quantized to Q4_K, KV prefilled from seeded random "
+                 "token ids, greedy tokens"),
         "config": {"workload": "Llama-3-8B-arch Q4_K decode, batch 1, ctx 4096 (BASELINE configs[4])",
                    "layers": 32, "n_embd": 4096, "n_ff": 14336, "heads": "32 q / 8 kv, head_dim 128",
                    "n_vocab": 128256, "kv": "q8_0", "kv_cells_before_decode": CTX,
@@ -633,6 +647,9 @@ def main() -> int:
                   "wall_ms": round(e2e["wall_ms_per_token"], 4),
                   "sum_of_ops_us": round(sum(v["us_per_token"] for v in per_op.values()), 1),
                   "per_op": per_op, "setup_s": round(e2e["setup_s"], 1)},
+        "prefill": {"tokens": CTX, "ubatch": UBATCH, "seconds": round(e2e["prefill_s"], 3),
+                    "tok_s": round(CTX / e2e["prefill_s"], 1),
+                    "note": "untimed setup of the decode workload, wall clock including host planning"},
         "roofline": {"bound": "hbm", "kernel": f"{dv['kernel']} ({dom})", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_bytes, "traffic_detail": traffic,

@@ -40,14 +40,29 @@ class OracleLlama:
         cache = self.kc[il] if which == 0 else self.vc[il]
         self.oc.kv_set_rows(cache, rows, np.arange(rows.shape[0], dtype=np.int64))
 
+    def set_cache_bytes(self, il: int, which: int, image) -> None:
+        """A layer's K (0) or V (1) cache as the ggml q8_0 image [kv_size][E / 32 * 34] (a copy)."""
+        cache = self.kc[il] if which == 0 else self.vc[il]
+        cache[:] = np.asarray(image, np.uint8).reshape(cache.shape)
+
     def step(self, token: int, pos: int, ts: np.float32, n_kv: int) -> np.ndarray:
         """Logits [n_vocab] of the token at position pos; ts = powf(rope_base, -2 / head_dim)."""
+        return self.forward(np.array([token], np.int32), pos, ts, n_kv)
+
+    def forward(self, tokens, pos0: int, ts: np.float32, n_kv: int) -> np.ndarray:
+        """T tokens at positions pos0 .. pos0 + T - 1 (cells the same), one ubatch: row t attends to
+        cells [0, pos0 + t] (llama.cpp's causal kq_mask over a cache), the ubatch's cells planned
+        newest last. Returns the logits [n_vocab] of the last token."""
         oc, t, D = self.oc, self.t, self.D
-        x = oc.get_rows(t["token_embd.weight"], np.array([token], np.int32))
-        msum = np.zeros(12, np.uint32)
-        msum[0], msum[1], msum[2], msum[9] = 0x4D55534D, 1, n_kv, pos + 1
-        runs = np.array([[pos, pos + 1]], np.uint32)
-        posv = np.array([pos], np.int32)
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        T = tokens.size
+        x = oc.get_rows(t["token_embd.weight"], tokens)
+        msum = np.zeros(8 + 4 * T, np.uint32)
+        msum[0], msum[1], msum[2] = 0x4D55534D, T, n_kv
+        msum[9::4] = pos0 + 1 + np.arange(T, dtype=np.uint32)        # row r: cells [0, pos0 + r + 1)
+        runs = np.array([[pos0, pos0 + T]], np.uint32)
+        posv = pos0 + np.arange(T, dtype=np.int32)
+        cells = posv.astype(np.int64)
         for il in range(self.n_layer):
             b = f"blk.{il}."
             xn = oc.rms_norm(x, self.eps, t[b + "attn_norm.weight"])
@@ -56,8 +71,8 @@ class OracleLlama:
             v = oc.mul_mat(self.wfmt, t[b + "attn_v.weight"], self.n_embd, xn, threads=self.threads)
             q = oc.rope(q, posv, D, D, self.neox, ts)
             k = oc.rope(k, posv, D, D, self.neox, ts)
-            oc.kv_set_rows(self.kc[il], k, np.array([pos], np.int64))
-            oc.kv_set_rows(self.vc[il], v, np.array([pos], np.int64))
+            oc.kv_set_rows(self.kc[il], k, cells)
+            oc.kv_set_rows(self.vc[il], v, cells)
             a = oc.flash_attn(q, self.kc[il], self.vc[il], D, self.n_head, self.n_head_kv, float(self.scale), msum,
                               new_runs=runs)
             h = oc.mul_mat(self.wfmt, t[b + "attn_output.weight"], self.n_head * D, a, add=x, threads=self.threads)
@@ -65,5 +80,5 @@ class OracleLlama:
             g = oc.mul_mat(self.wfmt, t[b + "ffn_gate.weight"], self.n_embd, hn, threads=self.threads)
             u = oc.mul_mat(self.wfmt, t[b + "ffn_up.weight"], self.n_embd, hn, threads=self.threads)
             x = oc.mul_mat(self.wfmt, t[b + "ffn_down.weight"], self.n_ff, oc.swiglu(g, u), add=h, threads=self.threads)
-        xn = oc.rms_norm(x, self.eps, t["output_norm.weight"])
+        xn = oc.rms_norm(x[T - 1:T], self.eps, t["output_norm.weight"])
         return oc.mul_mat(self.ofmt, t["output.weight"], self.n_embd, xn, threads=self.threads)[0]

@@ -115,9 +115,16 @@ class SyntheticWeights:
 def msum_decode(pos: int, n_kv: int) -> np.ndarray:
     """MSUM words of a one-row decode mask that sees cells [0, pos] of a mask n_kv cells wide (llama.cpp's
     kq_mask: 0 over the used cells, -inf elsewhere), the form tsr_hip_msum_build_f16 gives."""
-    w = np.zeros(12, np.uint32)
-    w[0], w[1], w[2] = 0x4D55534D, 1, n_kv
-    w[8], w[9] = 0, pos + 1
+    return msum_causal(pos, 1, n_kv)
+
+
+def msum_causal(pos0: int, T: int, n_kv: int) -> np.ndarray:
+    """MSUM words of the causal mask of a ubatch of T tokens at cells pos0 .. pos0 + T - 1: row t sees
+    cells [0, pos0 + t] (one FAST run per row, the form tsr_hip_msum_build_f16 gives for llama.cpp's
+    kq_mask over a cache)."""
+    w = np.zeros(8 + 4 * T, np.uint32)
+    w[0], w[1], w[2] = 0x4D55534D, T, n_kv
+    w[9::4] = pos0 + 1 + np.arange(T, dtype=np.uint32)
     return w
 
 
@@ -172,6 +179,7 @@ class LlamaDecoder:
                         c.head_dim % 8 == 0)
         self.graph = None
         self.captures = 0
+        self._pf = None                    # activations of a prefill ubatch (prefill)
 
     @property
     def pos_ptr(self) -> int:
@@ -190,6 +198,94 @@ class LlamaDecoder:
                 self.dev.kv_set_rows(kv, which, rows, n, self.cfg.E, idx, self.bad)
                 rows.free()
         self.dev.sync()
+
+    def _prefill_buffers(self, U: int) -> dict:
+        """Activations of a ubatch of U tokens (allocated on first use, grown when a larger one comes)."""
+        if self._pf is not None and self._pf["U"] >= U:
+            return self._pf
+        if self._pf is not None:
+            for k, b in self._pf.items():
+                if k != "U":
+                    b.free()
+        c, d, f4 = self.cfg, self.dev, 4
+        self._pf = {"U": U, "x": d.alloc(U * c.n_embd * f4), "h": d.alloc(U * c.n_embd * f4),
+                    "xn": d.alloc(U * c.n_embd * f4), "qkv": d.alloc(U * (c.n_q + 2 * c.E) * f4),
+                    "att": d.alloc(U * c.n_q * f4), "gu": d.alloc(U * 2 * c.n_ff * f4),
+                    "glu": d.alloc(U * c.n_ff * f4), "ids": d.alloc(U * 4), "pos": d.alloc(U * 4),
+                    "cell": d.alloc(U * 8)}
+        return self._pf
+
+    def prefill(self, tokens, pos0: int = 0, ubatch: int = 512) -> None:
+        """The prompt tokens at positions (= cells) pos0, pos0 + 1, ... in ubatches of at most `ubatch`
+        tokens, each ubatch one pass of the layers over all its tokens (llama.cpp's llama_decode of a
+        ubatch): every MUL_MAT over the ubatch's rows, ROPE + SET_ROWS_KV of its cells, FLASH_ATTN_EXT
+        with the causal mask (row t sees cells [0, pos0 + t]; the ubatch's cells planned newest last).
+        The last token's logits end in self.logits and its greedy token in self.next and self.tok (the
+        input of a following step_graph(None, ...))."""
+        toks = np.ascontiguousarray(tokens, np.int32).reshape(-1)
+        if toks.size == 0:
+            raise ValueError("prefill of no tokens")
+        if pos0 < 0 or pos0 + toks.size > self.kv_size:
+            raise ValueError(f"positions {pos0} .. {pos0 + toks.size - 1} outside the cache of {self.kv_size} cells")
+        for u0 in range(0, toks.size, ubatch):
+            self._prefill_ubatch(toks[u0:u0 + ubatch], pos0 + u0)
+        c, d = self.cfg, self.dev
+        pf, n = self._pf, c.n_embd
+        last = pf["x"].ptr + ((toks.size - 1) % ubatch) * n * 4
+        if self.fused:
+            d.mul_mat_norm(self.wout, last, 1, n, c.eps, self.out_norm, self.logits, c.n_vocab)
+        else:
+            d.rms_norm(last, n, 1, n, c.eps, self.xn, n, w=self.out_norm, w_stride=n)
+            d.mul_mat(self.wout, self.xn, 1, n, self.logits, c.n_vocab)
+        d.argmax(self.logits, c.n_vocab, 1, c.n_vocab, self.next)
+        d.copy_async(self.tok, self.next, 4)
+        d.sync()
+
+    def _prefill_ubatch(self, toks: np.ndarray, pos0: int) -> None:
+        c, d = self.cfg, self.dev
+        T, nq, E, n, ff = toks.size, c.n_q, c.E, c.n_embd, c.n_ff
+        w3, f4 = nq + 2 * E, 4
+        pf = self._prefill_buffers(T)
+        x, h, xn, qkv, att, gu, glu = (pf[k] for k in ("x", "h", "xn", "qkv", "att", "gu", "glu"))
+        pos = pos0 + np.arange(T, dtype=np.int64)
+        pf["ids"].write(toks)
+        pf["pos"].write(pos.astype(np.int32))
+        pf["cell"].write(pos)
+        n_kv = min(self.kv_size, (pos0 + T + 255) // 256 * 256)
+        msum, runs = msum_causal(pos0, T, n_kv), np.array([[pos0, pos0 + T]], np.uint32)
+        # the fused norm / GLU forms run on the matvec kernels: Q8_0 takes them 15 tokens at a time (16 or
+        # more Q8_0 tokens belong to the matrix-core path, which has no fused prologue / epilogue)
+        step = 15 if c.wfmt == H.FMT_Q8_0 else T
+
+        def fused_rows(fn):
+            for t0 in range(0, T, step):
+                fn(t0, min(step, T - t0))
+
+        d.get_rows(self.tok_embd, n, n, c.n_vocab, pf["ids"], T, x, n, bad=self.bad)
+        for L in self.layers:
+            if self.fused:
+                fused_rows(lambda t0, tt: d.mul_mat_norm(L["wqkv"], x.ptr + t0 * n * f4, tt, n, c.eps, L["attn_norm"],
+                                                         qkv.ptr + t0 * w3 * f4, w3))
+                d.rope_kv(qkv, T, w3, c.head_dim, c.n_head, c.n_head_kv, c.head_dim, c.rope_mode, pf["pos"],
+                          c.rope_base, L["kc"], L["vc"], pf["cell"], self.bad)
+            else:
+                d.rms_norm(x, n, T, n, c.eps, xn, n, w=L["attn_norm"], w_stride=n)
+                d.mul_mat(L["wqkv"], xn, T, n, qkv, w3)
+                d.rope(qkv, T, w3, c.head_dim, c.n_head + c.n_head_kv, c.head_dim, c.rope_mode, pf["pos"],
+                       c.rope_base, qkv, w3)
+                d.kv_set_rows(L["kc"], 0, qkv.ptr + nq * f4, T, w3, pf["cell"], self.bad)
+                d.kv_set_rows(L["vc"], 1, qkv.ptr + (nq + E) * f4, T, w3, pf["cell"], self.bad)
+            d.flash_attn(qkv, T, w3, L["kc"], L["vc"], c.head_dim, c.n_head, c.n_head_kv, self.scale, msum, att, nq,
+                         new_runs=runs)
+            d.mul_mat(L["wo"], att, T, nq, h, n, add=x, add_stride=n)
+            if self.fused:
+                fused_rows(lambda t0, tt: d.mul_mat_norm(L["wgu"], h.ptr + t0 * n * f4, tt, n, c.eps, L["ffn_norm"],
+                                                         glu.ptr + t0 * ff * f4, ff, flags=H.MM_GLU))
+            else:
+                d.rms_norm(h, n, T, n, c.eps, xn, n, w=L["ffn_norm"], w_stride=n)
+                d.mul_mat(L["wgu"], xn, T, n, gu, 2 * ff)
+                d.swiglu(gu, 2 * ff, gu.ptr + ff * f4, 2 * ff, ff, T, glu, ff)
+            d.mul_mat(L["wd"], glu, T, ff, x, n, add=h, add_stride=n)
 
     def _mask(self, pos: int, n_kv: int | None):
         if not 0 <= pos < self.kv_size:
@@ -341,6 +437,11 @@ class LlamaDecoder:
             self.graph.free()
             self.graph = None
         self.plan.free()
+        if self._pf is not None:
+            for k, b in self._pf.items():
+                if k != "U":
+                    b.free()
+            self._pf = None
         for L in self.layers:
             for k in ("wqkv", "wo", "wgu", "wd", "kc", "vc"):
                 L[k].free()

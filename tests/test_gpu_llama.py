@@ -115,3 +115,52 @@ def test_decode_graph_runs_ahead(dev):
         slow.append(b.read_next())
     b.free()
     assert list(fast) == slow
+
+
+@pytest.mark.parametrize("cfg,kv_size,hist,n_prompt,ubatch,fused", [
+    (LL.tiny_config(), 512, 0, 70, 32, True),                  # ubatches of 32, 32, 6 from cell 0
+    (LL.tiny_config(), 400, 40, 50, 512, False),               # one ubatch after a history, separate ops
+    (LL.tiny_config("tiny-qwen", wfmt=H.FMT_Q8_0, ofmt=H.FMT_Q8_0, rope_mode=H.ROPE_NEOX, eps=1e-6,
+                    rope_base=1000000.0), 640, 200, 90, 40, True),   # Q8_0: the matrix-core MUL_MATs
+    (LL.tiny_config("tiny-gqa8", n_head=8, n_head_kv=1, head_dim=128, n_embd=512, n_ff=768, n_vocab=1000),
+     300, 0, 260, 256, True),                                  # a second chunk of the causal rows
+], ids=["q4k-3ub", "q4k-separate-hist", "q80-neox-hist", "gqa8-d128-2ub"])
+def test_prefill_matches_oracle(dev, oc, cfg, kv_size, hist, n_prompt, ubatch, fused):
+    """Prefill of a prompt in ubatches (every op over the ubatch's rows, the causal mask) against the
+    oracle's forward of the same ubatches: the last token's logits bit for bit, the same cache bytes, the
+    same greedy token; then one graph-replayed decode token from the prefilled caches."""
+    w = LL.SyntheticWeights(cfg)
+    print(f"\nprefill parity {cfg.name} fused={fused}: kv {kv_size} history {hist} prompt {n_prompt} "
+          f"ubatch {ubatch}", flush=True)
+    gpu = LL.LlamaDecoder(dev, cfg, w, kv_size, fused=fused)
+    if hist:
+        gpu.prefill_history(w, hist)
+    ref = oracle_model(oc, cfg, w, kv_size, hist)
+    ts = np.float32(_libm.powf(float(np.float32(cfg.rope_base)), float(np.float32(-2.0) / np.float32(cfg.head_dim))))
+    toks = np.random.default_rng(n_prompt).integers(0, cfg.n_vocab, n_prompt).astype(np.int32)
+    gpu.prefill(toks, hist, ubatch=ubatch)
+    for u0 in range(0, n_prompt, ubatch):
+        T = min(ubatch, n_prompt - u0)
+        want = ref.forward(toks[u0:u0 + T], hist + u0, ts, min(kv_size, (hist + u0 + T + 255) // 256 * 256))
+    assert_bits_equal(gpu.read_logits(), want, f"{cfg.name} prefill logits")
+    nxt = int(oc.argmax(want[None])[0])
+    assert gpu.read_next() == nxt and gpu.read_token() == nxt
+    for il in range(cfg.n_layer):
+        assert (gpu.layers[il]["kc"].get_bytes(0).reshape(kv_size, -1) == ref.kc[il]).all(), f"K cache, layer {il}"
+        assert (gpu.layers[il]["vc"].get_bytes(1).reshape(kv_size, -1) == ref.vc[il]).all(), f"V cache, layer {il}"
+    pos = hist + n_prompt
+    gpu.step_graph(None, pos)
+    want = ref.step(nxt, pos, ts, min(kv_size, (pos + 1 + 255) // 256 * 256))
+    assert_bits_equal(gpu.read_logits(), want, f"{cfg.name} decode after prefill")
+    assert gpu.bad.read(np.int32, (1,))[0] == 0
+    gpu.free()
+
+
+def test_prefill_refusals(dev):
+    cfg = LL.tiny_config()
+    gpu = LL.LlamaDecoder(dev, cfg, LL.SyntheticWeights(cfg), 64)
+    with pytest.raises(ValueError):
+        gpu.prefill(np.zeros(0, np.int32))
+    with pytest.raises(ValueError):
+        gpu.prefill(np.zeros(10, np.int32), 60)
+    gpu.free()

@@ -25,6 +25,7 @@
 // Lane layouts (gfx950): an operand lane l supplies row l % 32 of its matrix and k = 16 (l / 32) ..
 // 16 (l / 32) + 15; the result lane l holds column l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4,
 // r = 0..15.
+#include "expk.hpp"
 #include "kernels.hpp"
 #include "qact.hpp"
 #include "wlayout.hpp"
@@ -119,7 +120,211 @@ __global__ __launch_bounds__(1024) void k_mm_q80(MmArgs a) {
     }
 }
 
+// ---- Q4_K -----------------------------------------------------------------------------------
+//
+// Numerics (sw/sim/tsr_ref.c:543-567, 580-635): the term of super-block s is (d Dx) f32(isum) -
+// (dmin Dx) f32(msum), isum = sum_j sc_j S_j, msum = sum_j m_j (BS[2j] + BS[2j+1]), S_j the int8
+// dot of sub-block j; the activation is quantized by QACT A256 (k_qact_mm4). Terms go to partial
+// s mod 16 in order of s, then the 16-partial tree, as for Q8_0.
+//
+// Per super-block s and 32 x 32 tile the tokens are the A operand and the weight rows the B operand,
+// so that a result lane holds one weight row (whose scales the lane decoded itself) and 16 tokens:
+//   S_j  = v_mfma_i32_32x32x32_i8(X sub-block j, W sub-block j), j = 0..7: the lane's 16-byte
+//          piece 2g + h of the weight row holds values 16 h .. 16 h + 15 of sub-block 2g in its low
+//          nibbles and of sub-block 2g + 1 in its high nibbles;
+//   isum = sum_j sc_j S_j (one v_mad_i32_i24 per output and sub-block);
+//   msum = four v_mfma_f32_32x32x2f32 over k = j of bs_j[token] m_j[row]: every product and every
+//          partial sum is an integer below 2^24 in magnitude (|bs_j| <= 32 * 128, m_j < 64), so the
+//          matrix core's f32 sum is the exact integer;
+//   term and partial sum on the VALU. Dx is an A256 scale (any f32): while every Dx a wave has met
+//   is 0 or >= 2^-60 in magnitude the plain IEEE operations are the spec operations (see
+//   k_matvec.hip); from the first super-block with a smaller nonzero Dx on, the wave uses the spec
+//   operations, and the tree of a workgroup with such a wave does too.
+
+// QACT A256 of T token rows, block-major: one aligned 16-lane row per (token, super-block)
+// (qact_a256_row: lane i holds values 16 i .. 16 i + 15, half i & 1 of sub-block i / 2). Writes
+// the quants xq [K/32][T][32 B], the sub-block sums xs [K/32][T] and the scales xd [K/256][tp]
+// (tp >= T, a multiple of 32; tokens T .. tp - 1 get d = 0). Every lane of a wave stays active
+// (the row operations need them): lanes past the last pair quantize a copy and store nothing.
+__global__ __launch_bounds__(256) void k_qact_mm4(const float * x, uint64_t x_stride, uint32_t K, uint32_t T,
+                                                  uint32_t tp, uint8_t * xq, int32_t * xs, float * xd) {
+    const uint32_t nsb = K >> 8;
+    const uint64_t pair = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;   // (token < tp, super-block)
+    const uint32_t l16 = threadIdx.x & 15u;
+    const uint64_t npair = (uint64_t)tp * nsb;
+    const uint64_t pc = pair < npair ? pair : npair - 1u;
+    const uint32_t t = (uint32_t)(pc / nsb), sb = (uint32_t)(pc % nsb);
+    const uint32_t tc = t < T ? t : T - 1u;
+    const float * xp = x + (size_t)tc * x_stride + 256u * sb + 16u * l16;
+    float4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = *(const float4 *)(xp + 4 * i);
+    float d;
+    int s16;
+    bool tiny;
+    const uint4 q = qact_a256_row(v, &d, &s16, &tiny);
+    const int bs = s16 + dpp_i<kDppXor1>(s16);                     // the two halves of sub-block l16 / 2
+    if (pair < npair) {
+        if (t < T) {
+            const uint32_t j = 8u * sb + (l16 >> 1);
+            *(uint4 *)(xq + ((size_t)j * T + t) * 32u + 16u * (l16 & 1u)) = q;
+            if ((l16 & 1u) == 0u) xs[(size_t)j * T + t] = bs;
+        }
+        if (l16 == 0u) xd[(size_t)sb * tp + t] = t < T ? d : 0.0f;
+    }
+}
+
+__device__ __forceinline__ uint32_t q4k_sc(const uint4 mt, uint32_t j) {
+    // meta bytes 4 + j: sc_j | (m_j & 3) << 6; nibble j of bytes 12..15: m_j >> 2 (wlayout.hpp)
+    return __builtin_amdgcn_ubfe(j < 4u ? mt.y : mt.z, 8u * (j & 3u), 6);
+}
+__device__ __forceinline__ uint32_t q4k_m(const uint4 mt, uint32_t j) {
+    return __builtin_amdgcn_ubfe(j < 4u ? mt.y : mt.z, 8u * (j & 3u) + 6u, 2) | (__builtin_amdgcn_ubfe(mt.w, 4u * j, 4) << 2);
+}
+
+// GLU: weight rows 2j and 2j + 1 are the gate and up rows of output j; their results are in adjacent
+// lanes of the output phase and y[j] = SWIGLU(gate, up) (as the matvec's GLU epilogue).
+template <bool GLU>
+__global__ __launch_bounds__(512) void k_mm_q4k(MmArgs a) {
+    __shared__ float s_p[16][1024];                                // partial pj of output (r, lane)
+    __shared__ int s_slow[8];
+    const WGeom g = wgeom(a.N, a.K >> 8, a.rb, true);
+    const uint32_t lane = __lane_id(), j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n0 = blockIdx.x * 32u, t0 = blockIdx.y * 32u;
+    const uint32_t h = lane >> 5, c = lane & 31u;
+    // operand rows of this lane (clamped: rows / tokens beyond the matrix are not stored)
+    const uint32_t n = min(n0 + c, a.N - 1u), t = min(t0 + c, a.T - 1u);
+    const uint32_t B = n / g.rb, R = wl_rows(g, B), rr = n - B * g.rb;
+    const uint8_t * wq = a.w + wl_quant_off(g, B, R, h, 0u, rr);  // piece 2 gg + h, slot sl: + 16 R (2 gg nb + sl)
+    const uint8_t * wm = a.w + wl_meta_off(g, B, R, 0u, rr);      // + 16 R sl
+    const uint8_t * xq = a.qa + (size_t)t * 32u + 16u * h;         // sub-block jb: + 32 T jb
+    const int32_t * xs = (const int32_t *)(a.qa + a.s_off) + t;    // + T jb
+    const float * xd = (const float *)(a.qa + a.d_off) + t0 + 4u * h;   // + tp s + 8 q: tokens of result r = 4 q + i
+    const uint32_t m4 = 0x0F0F0F0Fu;
+    bool slow = false;
+    // wave j computes partials j and j + 8 (8 waves of up to 256 VGPRs: one wave per partial at 16
+    // waves would leave 128 and spill)
+    for (uint32_t half = 0; half < 2u; ++half) {
+    const uint32_t pj = j + 8u * half, cnt = wl_count(g, pj), sl0 = wl_slot(g, pj, 0u);
+    v16f p;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = 0.0f;
+    for (uint32_t k = 0; k < cnt; ++k) {
+        const uint32_t sl = sl0 + k, s = pj + 16u * k;
+        v4i wv[4], xv[8];
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) wv[gg] = *(const v4i *)(wq + (size_t)16u * R * (2u * gg * g.nb + sl));
+        const uint4 mt = *(const uint4 *)(wm + (size_t)16u * R * sl);
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) xv[jb] = *(const v4i *)(xq + (size_t)32u * a.T * (8u * s + jb));
+        float bsf[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bsf[q] = (float)xs[(size_t)a.T * (8u * s + 2u * q + h)];
+        float4 dx4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dx4[q] = *(const float4 *)(xd + (size_t)a.tp * s + 8u * q);
+
+        v16f ms = {};
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q)
+            ms = __builtin_amdgcn_mfma_f32_32x32x2f32(bsf[q], (float)q4k_m(mt, 2u * q + h), ms, 0, 0, 0);
+        v16i isum = {};
+#pragma unroll
+        for (uint32_t gg = 0; gg < 4u; ++gg) {
+            const v4i lo = { wv[gg][0] & (int)m4, wv[gg][1] & (int)m4, wv[gg][2] & (int)m4, wv[gg][3] & (int)m4 };
+            const v4i hi = { (wv[gg][0] >> 4) & (int)m4, (wv[gg][1] >> 4) & (int)m4, (wv[gg][2] >> 4) & (int)m4,
+                             (wv[gg][3] >> 4) & (int)m4 };
+            v16i s0 = {}, s1 = {};
+            s0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xv[2 * gg], lo, s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xv[2 * gg + 1], hi, s1, 0, 0, 0);
+            const int sc0 = (int)q4k_sc(mt, 2u * gg), sc1 = (int)q4k_sc(mt, 2u * gg + 1u);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) isum[r] += __mul24(sc0, s0[r]) + __mul24(sc1, s1[r]);
+        }
+        const float d = h2f_fast(mt.x & 0xFFFFu), dm = h2f_fast(mt.x >> 16);
+        const float dxs[16] = { dx4[0].x, dx4[0].y, dx4[0].z, dx4[0].w, dx4[1].x, dx4[1].y, dx4[1].z, dx4[1].w,
+                                dx4[2].x, dx4[2].y, dx4[2].z, dx4[2].w, dx4[3].x, dx4[3].y, dx4[3].z, dx4[3].w };
+        bool tiny = false;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t ad = fb(dxs[r]) & 0x7FFFFFFFu;
+            tiny |= ad != 0u && ad < 0x21800000u;
+        }
+        slow = slow || __ballot(tiny) != 0ull;                       // wave-uniform, sticky
+        if (!slow) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float tt = (d * dxs[r]) * (float)isum[r] - (dm * dxs[r]) * (float)(int)ms[r];
+                p[r] = p[r] + tt;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float tt = ssub(smul(smul(d, dxs[r]), i2f(isum[r])), smul(smul(dm, dxs[r]), i2f((int)ms[r])));
+                p[r] = sadd(p[r], tt);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s_p[pj][64u * (uint32_t)r + lane] = p[r];
+    }
+    if (lane == 0u) s_slow[j] = slow ? 1 : 0;
+    lds_barrier();
+
+    bool any_slow = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) any_slow |= s_slow[i] != 0;
+    uint32_t t64 = 0;
+    if constexpr (GLU) t64 = a.ex.t64[lane];
+    // two outputs per thread, o = 64 r + lane of the wave layout above: weight row n0 + lane % 32,
+    // token t0 + 8 (r / 4) + 4 (lane / 32) + r % 4 (a wave stores 32 consecutive rows of 2 tokens)
+    for (uint32_t o = threadIdx.x; o < 1024u; o += 512u) {
+    const uint32_t ol = o & 63u, r = o >> 6;
+    const uint32_t nn = n0 + (ol & 31u), tt = t0 + 8u * (r >> 2) + 4u * (ol >> 5) + (r & 3u);
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = s_p[i][o];
+    if (!any_slow) {
+#pragma unroll
+        for (int w = 16; w > 1; w >>= 1)
+#pragma unroll
+            for (int i = 0; i < w / 2; ++i) v[i] = v[2 * i] + v[2 * i + 1];
+    } else {
+#pragma unroll
+        for (int w = 16; w > 1; w >>= 1)
+#pragma unroll
+            for (int i = 0; i < w / 2; ++i) v[i] = sadd(v[2 * i], v[2 * i + 1]);
+    }
+    if constexpr (GLU) {
+        const float gt = canon(v[0]);
+        const float h = swiglu_reg(gt, dpp_f<kDppXor1>(gt), a.ex, t64);   // every lane: the table is read by bpermute
+        if ((ol & 1u) == 0u && tt < a.T && nn < a.N) a.y[(size_t)tt * a.y_stride + (nn >> 1)] = h;
+    } else if (tt < a.T && nn < a.N) {
+        float y = canon(v[0]);
+        float * yp = a.y + (size_t)tt * a.y_stride + nn;
+        if (a.add) y = sadd(a.add[(size_t)tt * a.add_stride + nn], y);
+        else if (a.acc) y = sadd(*yp, y);
+        *yp = y;
+    }
+    }
+}
+
 }  // namespace tsr
+
+int tsr_launch_qact_mm4(const float * x, uint64_t x_stride, uint32_t K, uint32_t T, uint32_t tp, uint8_t * xq,
+                        int32_t * xs, float * xd, hipStream_t s) {
+    const uint64_t threads = (uint64_t)tp * (K / 256u) * 16u;
+    hipLaunchKernelGGL(tsr::k_qact_mm4, dim3((uint32_t)((threads + 255u) / 256u)), dim3(256), 0, s, x, x_stride, K, T,
+                       tp, xq, xs, xd);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int tsr_launch_mm_q4_k(const tsr::MmArgs & a, hipStream_t s) {
+    const dim3 grid((a.N + 31u) / 32u, (a.T + 31u) / 32u);
+    if (a.glu) hipLaunchKernelGGL(tsr::k_mm_q4k<true>, grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL(tsr::k_mm_q4k<false>, grid, dim3(512), 0, s, a);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
 
 int tsr_launch_qact_mm(const float * x, uint64_t x_stride, uint32_t K, uint32_t T, uint8_t * xq, float * xd,
                        hipStream_t s) {

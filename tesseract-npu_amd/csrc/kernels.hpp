@@ -68,6 +68,11 @@ struct MmArgs {
     uint32_t N, K, T;
     uint32_t acc;
     uint32_t rb;
+    // Q4_K (k_qact_mm4's A256 form): sub-block sums int32 [K/32][T] at qa + s_off, the super-block
+    // scales f32 [K/256][tp] at qa + d_off (tp: T rounded up to 32, padding tokens d = 0)
+    uint32_t s_off, tp;
+    uint32_t glu;            // Q4_K: rows 2j, 2j + 1 are gate / up of output j: y[j] = SWIGLU(gate, up)
+    ExpkTab ex;              // glu
 };
 
 // A KV plane (see k_kv.hip for the layout).
@@ -172,6 +177,9 @@ int tsr_launch_mv_q4_k(const tsr::MvArgs & a, hipStream_t s);
 int tsr_launch_qact_mm(const float * x, uint64_t x_stride, uint32_t K, uint32_t T, uint8_t * xq, float * xd,
                        hipStream_t s);
 int tsr_launch_mm_q8_0(const tsr::MmArgs & a, hipStream_t s);
+int tsr_launch_qact_mm4(const float * x, uint64_t x_stride, uint32_t K, uint32_t T, uint32_t tp, uint8_t * xq,
+                        int32_t * xs, float * xd, hipStream_t s);
+int tsr_launch_mm_q4_k(const tsr::MmArgs & a, hipStream_t s);
 int tsr_launch_kv_bytes(const tsr::KvArgs & a, uint32_t which, uint64_t off, uint64_t n, uint8_t * stage, int to_dev,
                         hipStream_t s);
 int tsr_launch_kv_set_rows(const tsr::KvArgs & a, uint32_t which, const float * src, uint32_t n_rows,

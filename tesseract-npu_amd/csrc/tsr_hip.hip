@@ -495,6 +495,41 @@ static int mul_mat_locked(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
         }
         return TSR_HIP_OK;
     }
+    // prefill: T >= 16 tokens of Q4_K on the matrix cores (QACT A256 of every token into scratch,
+    // block-major), with the GLU epilogue when asked; the fused norm form stays on the matvec kernels
+    if (T >= kMmMinTokens && w->fmt == TSR_HIP_FMT_Q4_K && isums == nullptr && prep == nullptr) {
+        const uint32_t chunk = std::min(T, kMmChunk), tpc = (chunk + 31u) & ~31u;
+        const size_t s_off = ((size_t)chunk * w->K + 255u) & ~(size_t)255u;
+        const size_t d_off = (s_off + 4u * (size_t)chunk * (w->K / 32u) + 255u) & ~(size_t)255u;
+        int rc = ctx->scratch.reserve(d_off + 4u * (size_t)tpc * (w->K / 256u), s);
+        if (rc) return rc;
+        for (uint32_t t0 = 0; t0 < T; t0 += chunk) {
+            const uint32_t tt = std::min(T - t0, chunk), tp = (tt + 31u) & ~31u;
+            uint8_t * xq = (uint8_t *)ctx->scratch.ptr;
+            if (tsr_launch_qact_mm4(x_dev + (size_t)t0 * x_stride, x_stride, w->K, tt, tp, xq, (int32_t *)(xq + s_off),
+                                    (float *)(xq + d_off), s))
+                return TSR_HIP_E_HIP;
+            tsr::MmArgs m{};
+            m.w = w->dev;
+            m.rb = w->rb;
+            m.qa = xq;
+            m.s_off = (uint32_t)s_off;
+            m.d_off = (uint32_t)d_off;
+            m.tp = tp;
+            m.y = y_dev + (size_t)t0 * y_stride;
+            m.y_stride = y_stride;
+            m.add = add_dev ? add_dev + (size_t)t0 * add_stride : nullptr;
+            m.add_stride = add_stride;
+            m.N = w->N;
+            m.K = w->K;
+            m.T = tt;
+            m.acc = a.acc;
+            m.glu = a.glu;
+            m.ex = a.ex;
+            if (tsr_launch_mm_q4_k(m, s)) return TSR_HIP_E_HIP;
+        }
+        return TSR_HIP_OK;
+    }
     for (uint32_t t0 = 0; t0 < T; t0 += 65535u) {
         const uint32_t tt = std::min(T - t0, 65535u);
         a.x = x_dev + (size_t)t0 * x_stride;

@@ -253,8 +253,10 @@ class LlamaDecoder:
         pf["cell"].write(pos)
         n_kv = min(self.kv_size, (pos0 + T + 255) // 256 * 256)
         msum, runs = msum_causal(pos0, T, n_kv), np.array([[pos0, pos0 + T]], np.uint32)
-        # the fused norm / GLU forms run on the matvec kernels: Q8_0 takes them 15 tokens at a time (16 or
-        # more Q8_0 tokens belong to the matrix-core path, which has no fused prologue / epilogue)
+        # 16 or more tokens run the MUL_MATs on the matrix cores, which take no fused RMS_NORM: there the
+        # norm is its own launch (the same operations); Q4_K's matrix-core path has the GLU epilogue,
+        # Q8_0's has none, so a fused Q8_0 model takes its norm / GLU matvecs 15 tokens at a time
+        mma = c.wfmt == H.FMT_Q4_K and T >= 16
         step = 15 if c.wfmt == H.FMT_Q8_0 else T
 
         def fused_rows(fn):
@@ -264,8 +266,12 @@ class LlamaDecoder:
         d.get_rows(self.tok_embd, n, n, c.n_vocab, pf["ids"], T, x, n, bad=self.bad)
         for L in self.layers:
             if self.fused:
-                fused_rows(lambda t0, tt: d.mul_mat_norm(L["wqkv"], x.ptr + t0 * n * f4, tt, n, c.eps, L["attn_norm"],
-                                                         qkv.ptr + t0 * w3 * f4, w3))
+                if mma:
+                    d.rms_norm(x, n, T, n, c.eps, xn, n, w=L["attn_norm"], w_stride=n)
+                    d.mul_mat(L["wqkv"], xn, T, n, qkv, w3)
+                else:
+                    fused_rows(lambda t0, tt: d.mul_mat_norm(L["wqkv"], x.ptr + t0 * n * f4, tt, n, c.eps,
+                                                             L["attn_norm"], qkv.ptr + t0 * w3 * f4, w3))
                 d.rope_kv(qkv, T, w3, c.head_dim, c.n_head, c.n_head_kv, c.head_dim, c.rope_mode, pf["pos"],
                           c.rope_base, L["kc"], L["vc"], pf["cell"], self.bad)
             else:
@@ -278,7 +284,10 @@ class LlamaDecoder:
             d.flash_attn(qkv, T, w3, L["kc"], L["vc"], c.head_dim, c.n_head, c.n_head_kv, self.scale, msum, att, nq,
                          new_runs=runs)
             d.mul_mat(L["wo"], att, T, nq, h, n, add=x, add_stride=n)
-            if self.fused:
+            if self.fused and mma:
+                d.rms_norm(h, n, T, n, c.eps, xn, n, w=L["ffn_norm"], w_stride=n)
+                d.mul_mat(L["wgu"], xn, T, n, glu, ff, flags=H.MM_GLU)
+            elif self.fused:
                 fused_rows(lambda t0, tt: d.mul_mat_norm(L["wgu"], h.ptr + t0 * n * f4, tt, n, c.eps, L["ffn_norm"],
                                                          glu.ptr + t0 * ff * f4, ff, flags=H.MM_GLU))
             else:

@@ -16,9 +16,9 @@ from helpers import assert_bits_equal, special_row, weights
 pytestmark = pytest.mark.gpu
 
 
-def _mm(dev, oc, N, K, T, seed=1, x=None, add=False, acc=False, wblocks=None):
-    blocks = weights(0, N, K, seed) if wblocks is None else wblocks
-    w = dev.weight(0, blocks, N, K)
+def _mm(dev, oc, N, K, T, seed=1, x=None, add=False, acc=False, wblocks=None, fmt=0):
+    blocks = weights(fmt, N, K, seed) if wblocks is None else wblocks
+    w = dev.weight(fmt, blocks, N, K)
     if x is None:
         x = S.normal(seed + 100, T * K).reshape(T, K)
     y0 = S.normal(seed + 200, T * N).reshape(T, N)
@@ -27,7 +27,8 @@ def _mm(dev, oc, N, K, T, seed=1, x=None, add=False, acc=False, wblocks=None):
     dev.mul_mat(w, dev.upload(x), T, K, yb, N, dev.upload(a) if add else None, N if add else 0,
                 tsr_hip.MM_ACC_DST if acc else 0)
     got = yb.read(np.float32, (T, N))
-    want = oc.mul_mat(0, blocks, K, x, add=(a if add else (y0 if acc else None)), threads=8)
+    want = oc.mul_mat(fmt, blocks, K, x, add=(a if add else (y0 if acc else None)), threads=8)
+    w.free()
     return got, want
 
 
@@ -73,3 +74,83 @@ def test_mm_q8_0_baseline_prefill_shape(dev, oc):
     assert_bits_equal(got[toks], oc.mul_mat(0, blocks, K, x[toks], threads=8), "token sample")
     rows = np.r_[0:40, 2040:2056, 4060:4096]
     assert_bits_equal(got[:, rows], oc.mul_mat(0, blocks[rows], K, x, threads=8), "row sample")
+
+
+# ---- Q4_K (QACT A256, i8 matrix core per sub-block, exact f32 matrix-core msum) ----
+
+@pytest.mark.parametrize("T,N,K", [(16, 64, 256), (17, 100, 4096), (64, 256, 14336), (100, 33, 4096),
+                                   (16, 1, 512), (130, 200, 1024), (33, 47, 3840), (40, 96, 32768)])
+def test_mm_q4_k_shapes(dev, oc, T, N, K):
+    print(f"\nmm Q4_K T {T} {N}x{K}", flush=True)
+    got, want = _mm(dev, oc, N, K, T, seed=T + N + 1, fmt=1)
+    assert_bits_equal(got, want, f"Q4_K T {T} {N}x{K}")
+
+
+def test_mm_q4_k_add_acc(dev, oc):
+    got, want = _mm(dev, oc, 96, 2048, 40, seed=13, add=True, fmt=1)
+    assert_bits_equal(got, want, "add")
+    got, want = _mm(dev, oc, 96, 2048, 40, seed=14, acc=True, fmt=1)
+    assert_bits_equal(got, want, "acc")
+
+
+@pytest.mark.parametrize("tiny_rows", [False, True], ids=["specials", "tiny-scales"])
+def test_mm_q4_k_specials(dev, oc, tiny_rows):
+    """Special activations (NaN, Inf, subnormal, zero rows) and special weight scales; with tiny_rows,
+    token rows whose A256 scale is below 2^-60 (the spec-operation path of their waves and trees)."""
+    N, K, T = 48, 1024, 40
+    rows = []
+    for t in range(T):
+        if t % 4 == 0:
+            rows.append(special_row(K, t))
+        elif tiny_rows and t % 4 == 1:
+            rows.append(S.normal(60 + t, K, 1e-25))
+        elif t % 4 == 2:
+            rows.append(S.normal(60 + t, K, 3e-18))
+        else:
+            rows.append(S.normal(60 + t, K))
+    x = np.stack(rows)
+    blocks = weights(1, N, K, 19).copy()
+    v = blocks.reshape(N, -1, 144)
+    rng = np.random.default_rng(5)
+    specials = np.array([0x0001, 0x03FF, 0x8005, 0x7C00, 0xFC00, 0x7E01, 0x0000], np.uint16).view(np.uint8).reshape(-1, 2)
+    for r in range(0, N, 3):
+        b = rng.integers(0, v.shape[1])
+        v[r, b, 0:2] = specials[r % len(specials)]
+        v[r, b, 2:4] = specials[(r + 3) % len(specials)]
+    got, want = _mm(dev, oc, N, K, T, x=x, wblocks=blocks, fmt=1)
+    assert_bits_equal(got, want, "Q4_K specials")
+
+
+def test_mm_q4_k_llama_prefill_shape(dev, oc):
+    """A Llama-3-8B ubatch: 512 tokens x W[4096 x 14336] Q4_K (the FFN down projection): every output
+    of a sample of tokens, and every token of a sample of rows."""
+    T, N, K = 512, 4096, 14336
+    blocks = S.quant_rows(1, 91, N, K)
+    x = S.normal(92, T * K).reshape(T, K)
+    w = dev.weight(1, blocks, N, K)
+    yb = dev.alloc(4 * T * N)
+    dev.mul_mat(w, dev.upload(x), T, K, yb, N)
+    got = yb.read(np.float32, (T, N))
+    toks = [0, 1, 31, 32, 63, 64, 255, 510, 511]
+    assert_bits_equal(got[toks], oc.mul_mat(1, blocks, K, x[toks], threads=8), "token sample")
+    rows = np.r_[0:40, 2040:2056, 4060:4096]
+    assert_bits_equal(got[:, rows], oc.mul_mat(1, blocks[rows], K, x, threads=8), "row sample")
+    w.free()
+
+
+@pytest.mark.parametrize("T,N,K", [(16, 64, 256), (40, 512, 4096), (100, 130, 1024)])
+def test_mm_q4_k_glu(dev, oc, T, N, K):
+    """The GLU epilogue of the Q4_K matrix-core path: rows 2j, 2j + 1 are gate / up of output j, y[j] =
+    SWIGLU(gate, up), against the oracle's MUL_MAT of the gate and up rows then SWIGLU."""
+    print(f"\nmm Q4_K GLU T {T} {N}x{K}", flush=True)
+    blocks = weights(1, N, K, T + N + 7)
+    x = S.normal(T + 8, T * K).reshape(T, K)
+    x[T // 2] = special_row(K, 3)
+    w = dev.weight(1, blocks, N, K)
+    yb = dev.alloc(4 * T * (N // 2))
+    dev.mul_mat(w, dev.upload(x), T, K, yb, N // 2, flags=tsr_hip.MM_GLU)
+    got = yb.read(np.float32, (T, N // 2))
+    g = oc.mul_mat(1, blocks[0::2], K, x, threads=8)
+    u = oc.mul_mat(1, blocks[1::2], K, x, threads=8)
+    assert_bits_equal(got, oc.swiglu(g, u), f"GLU T {T} {N}x{K}")
+    w.free()

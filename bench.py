@@ -463,6 +463,23 @@ def extra_workloads(dev, ev, stream, n: int, eager: bool = False) -> dict:
                      "frac_of_int8_mfma_peak": round(ops / (ms * 1e-3) / 5.0e15, 4),
                      "launches_per_call": 2, "note": "QACT of the 512 rows + the matrix-core kernel"}
         del ws, yb
+    # the same on Q4_K weights (the headline model's format): QACT A256 + the Q4_K matrix-core kernel;
+    # 512 x 14336 x 4096 with the GLU epilogue is the 8B ubatch's gate|up (28672 interleaved rows)
+    for name, N, K4, flags in (("prefill_q4_k_512x4096x4096", 4096, 4096, 0),
+                               ("prefill_q4_k_512x4096x14336", 4096, 14336, 0),
+                               ("prefill_q4_k_glu_512x28672x4096", 28672, 4096, tsr_hip.MM_GLU)):
+        blocks = S.quant_rows(1, S.seed_of("cfg4", "w4_" + name), N, K4)
+        ws = [dev.weight(1, blocks, N, K4) for _ in range(2)]
+        x4 = dev.upload(S.normal(S.seed_of("cfg4", "x4"), T * K4))
+        ny = N // 2 if flags else N
+        yb = dev.alloc(4 * T * ny)
+        ms, ms_eager = timed(lambda i: dev.mul_mat(ws[i % 2], x4, T, K4, yb, ny, flags=flags, stream=stream), 20)
+        ops = 2 * T * N * K4
+        out[name] = {"us_per_call": round(ms * 1e3, 2), "us_per_call_eager": round(ms_eager * 1e3, 2),
+                     "int8_TOPS": round(ops / (ms * 1e-3) / 1e12, 1),
+                     "frac_of_int8_mfma_peak": round(ops / (ms * 1e-3) / 5.0e15, 4),
+                     "launches_per_call": 2, "note": "QACT A256 of the 512 rows + the Q4_K matrix-core kernel"}
+        del ws, yb, x4
 
     # causal flash attention over 512 tokens (32 q / 8 KV heads, D 128, q8_0 KV); the
     # work list of 512 rows is copied to the device per call, so this one is timed eagerly

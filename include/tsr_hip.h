@@ -53,8 +53,8 @@ extern "C" {
 #define TSR_HIP_MM_ACC_DST  0x1u  /* y = FA(y_old, W.x) */
 /* The weight's rows 2j and 2j + 1 are the gate and up rows of output j, and y[j] = SWIGLU(gate . x,
  * up . x) for j < N / 2 -- the MUL_MATs of the FFN gate and up weights followed by GGML_GLU_OP_SWIGLU
- * (tsr_hip_swiglu), bit-identical, in one launch. No addend, no ACC_DST; the matvec path only (not the
- * Q8_0 T >= 16 prefill shapes); N even (row blocks are always whole pairs). */
+ * (tsr_hip_swiglu), bit-identical, in one launch. No addend, no ACC_DST; Q4_K at any T (matvec, or the
+ * matrix-core path at T >= 16), Q8_0 at T < 16 (not its matrix-core prefill shapes); N even. */
 #define TSR_HIP_MM_GLU      0x2u
 /* tsr_hip_mul_mat_epi: the MVM record's local scale applied to y after the addend / ACC
  * (TSR_MVM_LOCAL_SCALE / _SOFTCAP, sw/sim/tsr_sim.c:1648-1667; GGML MUL_MAT followed by SCALE, or the
@@ -133,7 +133,9 @@ int tsr_hip_qact(tsr_hip_ctx * ctx, uint32_t kind, const float * x_dev, uint32_t
  *                           = FA(add_dev[t * add_stride + n], v)   with an addend (add_stride 0: row 0)
  *                           = FA(y_old, v)                          with TSR_HIP_MM_ACC_DST
  * for t < T, n < N. An addend together with ACC_DST is refused (TSR_HIP_E_ARG), as the kernel's record
- * check does. x, y and add must not overlap. T >= 1. */
+ * check does. x, y and add must not overlap. T >= 1. T < 16 runs the matvec kernels; T >= 16 the int8
+ * matrix cores (both formats; the activations are quantized into the context's scratch first), with
+ * the same bits. */
 int tsr_hip_mul_mat(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const float * x_dev, uint32_t T, uint64_t x_stride,
                     float * y_dev, uint64_t y_stride, const float * add_dev, uint64_t add_stride, uint32_t flags,
                     void * stream);

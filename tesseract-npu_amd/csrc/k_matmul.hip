@@ -135,7 +135,9 @@ __global__ __launch_bounds__(1024) void k_mm_q80(MmArgs a) {
 //   isum = sum_j sc_j S_j (one v_mad_i32_i24 per output and sub-block);
 //   msum = four v_mfma_f32_32x32x2f32 over k = j of bs_j[token] m_j[row]: every product and every
 //          partial sum is an integer below 2^24 in magnitude (|bs_j| <= 32 * 128, m_j < 64), so the
-//          matrix core's f32 sum is the exact integer;
+//          matrix core's f32 sum is the exact integer (an exact zero may come out as -0 where the
+//          spec's f32(msum) is +0: that can only change the sign of a zero product or term, and a
+//          zero term added to a partial that starts at +0 never changes it);
 //   term and partial sum on the VALU. Dx is an A256 scale (any f32): while every Dx a wave has met
 //   is 0 or >= 2^-60 in magnitude the plain IEEE operations are the spec operations (see
 //   k_matvec.hip); from the first super-block with a smaller nonzero Dx on, the wave uses the spec
@@ -254,13 +256,13 @@ __global__ __launch_bounds__(512) void k_mm_q4k(MmArgs a) {
         if (!slow) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float tt = (d * dxs[r]) * (float)isum[r] - (dm * dxs[r]) * (float)(int)ms[r];
+                const float tt = (d * dxs[r]) * (float)isum[r] - (dm * dxs[r]) * ms[r];
                 p[r] = p[r] + tt;
             }
         } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float tt = ssub(smul(smul(d, dxs[r]), i2f(isum[r])), smul(smul(dm, dxs[r]), i2f((int)ms[r])));
+                const float tt = ssub(smul(smul(d, dxs[r]), i2f(isum[r])), smul(smul(dm, dxs[r]), ms[r]));
                 p[r] = sadd(p[r], tt);
             }
         }

@@ -200,20 +200,26 @@ def test_rope_kv_bad_cell(dev, oc):
     (700, 513, 100, 8, 2, 128, H.ROPE_IMROPE, 128, False),        # the new row lands in a cell other than its position
     (96, 0, 0, 4, 4, 64, H.ROPE_NORMAL, 64, False),               # position 0: the first cell of an empty cache
     (640, 600, 600, 64, 8, 64, H.ROPE_NORMAL, 64, False),         # G = 8: the three-launch form
+    (4232, 5000, 100, 32, 8, 128, H.ROPE_NORMAL, 128, "swa"),     # wrapped sliding window over a full ring:
+    (1500, 3000, 700, 12, 4, 64, H.ROPE_NEOX, 64, "swa"),         #   runs [0, cell] and [lo, n_kv), two FAST runs
 ], ids=lambda v: str(v))
 def test_flash_attn_plan_rope(dev, oc, n_kv, pos, cell, n_head, n_head_kv, D, mode, n_dims, general):
     """tsr_hip_flash_attn_plan_rope against the oracle's ROPE of q and k, SET_ROWS_KV of k and v and
     FLASH_ATTN_EXT (one decode token seeing cells [0, max(pos, cell)] of a mask n_kv wide; with
-    `general`, some of those cells carry finite biases and some are masked out)."""
+    `general`, some of those cells carry finite biases and some are masked out; with "swa", a full
+    ring cache whose sliding window wraps: cells [0, cell] and [cell + 1000 or n_kv - 300, n_kv), the
+    new cell in the first run)."""
     import math
     print(f"\nflash_attn_plan_rope n_kv {n_kv} pos {pos} cell {cell} heads {n_head}/{n_head_kv} D {D} mode {mode} "
           f"n_dims {n_dims} general {general}", flush=True)
     rng = np.random.default_rng(n_kv + pos + D)
     E, nq = n_head_kv * D, n_head * D
+    swa = general == "swa"
+    general = general is True
     kv_size = 16 * -(-n_kv // 16) if general else n_kv   # a GENERAL mask covers whole groups of the cache
     k0 = np.zeros((kv_size, E // 32 * 34), np.uint8)
     v0 = np.zeros_like(k0)
-    hist = max(pos, cell)
+    hist = n_kv if swa else max(pos, cell)
     oc.kv_set_rows(k0, S.normal(11 + D, hist * E).reshape(hist, E), np.arange(hist))
     oc.kv_set_rows(v0, S.normal(12 + D, hist * E).reshape(hist, E), np.arange(hist))
     row = rng.standard_normal((1, nq + 2 * E)).astype(np.float32)
@@ -237,6 +243,10 @@ def test_flash_attn_plan_rope(dev, oc, n_kv, pos, cell, n_head, n_head_kv, D, mo
         msum = oc.msum(mask)
         assert msum[3], "the mask must plan as GENERAL"
         mf = oc.mask_f32(mask, scale)
+    elif swa:
+        msum = np.zeros(12, np.uint32)
+        msum[0], msum[1], msum[2] = 0x4D55534D, 1, n_kv
+        msum[8], msum[9], msum[10], msum[11] = 0, cell + 1, min(cell + 1000, n_kv - 300), n_kv
     else:
         msum = np.zeros(12, np.uint32)
         msum[0], msum[1], msum[2], msum[9] = 0x4D55534D, 1, n_kv, hist + 1

@@ -47,6 +47,8 @@ HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
 METRIC = "decode tok/s (8B Q4_K, ctx 4096); matvec/attn HBM GB/s as % of peak"
 CTX = 4096                      # KV cells filled before the first decode token
+PMC_KV_SIZE = CTX + 8 + 128     # the counter child's cache (the default bench's kv_size)
+PMC_POS = CTX + 8 + 64          # and its token's cell: the timed region's middle
 UBATCH = 512                    # prefill tokens per pass of the layers (llama.cpp's default n_ubatch)
 PROMPT_SEED = 4096              # numpy seed of the random prompt token ids
 
@@ -144,31 +146,6 @@ def mv_bytes(N: int, K: int) -> int:
     return q4k_bytes(N, K) + 4 * K + 4 * N
 
 
-class CachedWeights(LL.SyntheticWeights):
-    """SyntheticWeights whose tensors are generated once and kept on the host, so that the GPU model
-    and the CPU leg see the same arrays without generating them twice."""
-
-    def __init__(self, cfg):
-        super().__init__(cfg)
-        self.cache = {}
-
-    def quant(self, name, N, K, fmt):
-        key = (name, fmt)
-        if key not in self.cache:
-            self.cache[key] = super().quant(name, N, K, fmt)
-        return self.cache[key]
-
-    def norm(self, name):
-        if name not in self.cache:
-            self.cache[name] = super().norm(name)
-        return self.cache[name]
-
-    def embedding(self):
-        if "token_embd.weight" not in self.cache:
-            self.cache["token_embd.weight"] = super().embedding()
-        return self.cache["token_embd.weight"]
-
-
 def token_bytes(cfg, n_kv_read: int) -> int:
     """Algorithmic bytes of one decode token: every quantized weight once, the q8_0 K and V of the
     visible cells of every layer, the embedding row and the norm vectors."""
@@ -187,7 +164,7 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
     CTX+warmup .. CTX+warmup+steps-1; with `eager`, direct launches instead of every replay. Every
     greedy token is copied to a device history buffer."""
     cfg = LL.LLAMA3_8B
-    wts = CachedWeights(cfg)
+    wts = LL.SyntheticWeights(cfg, cache=True)
     kv_size = CTX + warmup + steps
     stream = dev.stream
     t0 = time.perf_counter()
@@ -228,10 +205,8 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
     wall_s = time.perf_counter() - h0
     if m.captures != captures:
         raise RuntimeError("the decode graph was re-captured inside the timed region")
+    m.check()                   # DecodeError: an index out of range (1) or an expired FA wait (2)
     toks = hist.read(np.int32, (warmup + steps,))
-    bad = int(m.bad.read(np.int32, (1,))[0])
-    if bad:
-        raise RuntimeError(f"an index went out of range during decode ({bad})")
     ms_tok = ms / steps
     mid_kv = CTX + warmup + steps // 2 + 1
     tb = token_bytes(cfg, mid_kv)
@@ -300,7 +275,7 @@ def cpu_decode(e2e: dict, max_seconds: float = 12.0, max_tokens: int = 4) -> dic
     from oracle_llama import OracleLlama
     cfg, wts = e2e["cfg"], e2e["wts"]
     oc = oracle.Oracle()
-    threads = min(16, os.cpu_count() or 1)
+    threads = min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1))
     t = {"token_embd.weight": wts.embedding(), "output_norm.weight": wts.norm("output_norm.weight")[None],
          "output.weight": wts.quant("output.weight", cfg.n_vocab, cfg.n_embd, cfg.ofmt)}
     for il in range(cfg.n_layer):
@@ -336,12 +311,38 @@ def cpu_decode(e2e: dict, max_seconds: float = 12.0, max_tokens: int = 4) -> dic
         if sum(times) >= max_seconds:
             break
     per = float(np.mean(times))
+    # the same first token on one thread (position CTX again: it rewrites its cell with the same rows)
+    ref.threads = 1
+    t0 = time.perf_counter()
+    logits1 = ref.step(e2e["tok0"], CTX, ts, min(kv_size, (CTX + 1 + 255) // 256 * 256))
+    one_s = time.perf_counter() - t0
+    one_equal = bool(np.array_equal(logits1.view(np.uint32), e2e["logits0"].view(np.uint32)))
     return {"value": round(1.0 / per, 4), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": (f"{n} decode tokens of the same Llama-3-8B-arch Q4_K model at positions {CTX}..{CTX + n - 1} "
                        f"by oracle/oracle_llama.py over oracle/oc_*.c ({threads} threads in MUL_MAT), "
                        f"{per:.2f} s per token"),
+            "single_thread": {"value": round(1.0 / one_s, 4), "unit": "tok/s", "cores": 1,
+                              "sample": f"token 0 again at position {CTX} on one thread, {one_s:.2f} s",
+                              "token0_logits_bit_equal": one_equal},
+            "host": host_info(),
+            "ggml_cpu": "not measured (unavailable offline: llama.cpp/ggml is an un-vendored submodule)",
             "parity": {"token0_logits_bit_equal": logits_equal, "greedy_tokens_equal": bool(same_tokens),
                        "tokens_compared": n}}
+
+
+def host_info() -> dict:
+    """The CPU the baseline ran on: model name, online CPUs and the CPUs this process may use."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc_online": os.cpu_count(),
+            "nproc_affinity": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
 
 
 def extra_workloads(dev, ev, stream, n: int, eager: bool = False) -> dict:
@@ -505,14 +506,16 @@ def extra_workloads(dev, ev, stream, n: int, eager: bool = False) -> dict:
 
 
 COPY_BYTES = 256 << 20          # calibration copy (device to device)
-PMC_SHAPES = {"gate|up": ("ffn_gate", "ffn_up"), "down": ("ffn_down",)}
+# the launches of the counter child, in dispatch order, and the per_op entry each one stands for
+PMC_TAGS = {"gate|up": "gate|up", "down": "mul_mat down", "fa": "flash_attn"}
 
 
 def pmc_child(reps: int = 3) -> int:
     """Counter-collection child (run under rocprofv3 --pmc): a device-to-device copy of COPY_BYTES,
-    then the decode model's layer-0 gate|up (28672x4096, RMS_NORM and SWIGLU fused) and down
-    (4096x14336, residual addend) Q4_K matvecs as the decoder launches them, `reps` dispatches each, on
-    the model's seeded weights."""
+    then, `reps` dispatches each, the decode model's layer-0 gate|up (28672x4096, RMS_NORM and SWIGLU
+    fused) and down (4096x14336, residual addend) Q4_K matvecs as the decoder launches them, and the
+    planned one-launch ROPE + SET_ROWS_KV + FLASH_ATTN_EXT of one layer at the bench's mid-run context
+    (cells [0, pos] visible, the new cell pos), on the model's seeded weights and seeded cache rows."""
     cfg = LL.LLAMA3_8B
     wts = LL.SyntheticWeights(cfg)
     dev = tsr_hip.Device(0)
@@ -526,6 +529,22 @@ def pmc_child(reps: int = 3) -> int:
     w_dn = dev.weight(cfg.wfmt, wts.quant("blk.0.ffn_down.weight", cfg.n_embd, cfg.n_ff, cfg.wfmt), cfg.n_embd, cfg.n_ff)
     xb, gb, yb = dev.upload(S.normal(S.seed_of("pmc", "x"), cfg.n_embd)), dev.alloc(8 * cfg.n_ff), dev.alloc(4 * cfg.n_embd)
     nw = dev.upload(wts.norm("blk.0.ffn_norm.weight"))
+    # one layer's caches at the e2e shape, cells [0, pos) filled, the token at cell pos
+    kv_size, pos = PMC_KV_SIZE, PMC_POS
+    E, nq, w3 = cfg.E, cfg.n_q, cfg.n_q + 2 * cfg.E
+    kc, vc = dev.kv(E, kv_size), dev.kv(E, kv_size)
+    idx = dev.upload(np.arange(pos, dtype=np.int64))
+    for which, kv in ((0, kc), (1, vc)):
+        rows = dev.upload(S.normal(S.seed_of("pmc", f"kv{which}"), pos * E))
+        dev.kv_set_rows(kv, which, rows, pos, E, idx)
+        rows.free()
+    qkv = dev.upload(S.normal(S.seed_of("pmc", "qkv"), w3))
+    params = dev.upload(LL.LlamaDecoder._params(pos))
+    rtab, att, bad = dev.alloc(4 * cfg.head_dim), dev.alloc(4 * nq), dev.alloc(4).fill(0)
+    plan = dev.fa_plan(cfg.head_dim, cfg.n_head, cfg.n_head_kv, 1, kv_size)
+    plan.set(LL.msum_decode(pos, min(kv_size, (pos + 1 + 255) // 256 * 256)), np.array([[pos, pos + 1]], np.uint32))
+    dev.rope_table(params.ptr, cfg.head_dim, cfg.rope_base, rtab)
+    dev.sync()
     for _ in range(reps):
         assert ev.h.hipMemcpyAsync(dst.ptr, src.ptr, COPY_BYTES, 3, dev.stream) == 0   # 3: device to device
     ev.device_sync()
@@ -533,7 +552,12 @@ def pmc_child(reps: int = 3) -> int:
         dev.mul_mat_norm(w_gu, xb, 1, cfg.n_embd, cfg.eps, nw, gb, cfg.n_ff, flags=tsr_hip.MM_GLU, stream=dev.stream)
     for _ in range(reps):      # the decoder's down, residual addend
         dev.mul_mat(w_dn, gb, 1, cfg.n_ff, yb, cfg.n_embd, add=xb, add_stride=cfg.n_embd, stream=dev.stream)
+    for _ in range(reps):      # the decoder's attention launch
+        dev.flash_attn_plan_rope_tab(plan, qkv, kc, vc, np.float32(1.0 / np.sqrt(cfg.head_dim)), cfg.head_dim,
+                                     cfg.rope_mode, rtab, params.ptr + 8, att, nq, bad=bad, stream=dev.stream)
     ev.device_sync()
+    assert int(bad.read(np.int32, (1,))[0]) == 0
+    plan.free()
     dev.close()
     return 0
 
@@ -558,9 +582,9 @@ def _pmc_pass(counter: str, workdir: str) -> list:
 
 
 def measure_traffic(reps: int = 3) -> dict:
-    """HBM bytes per launch of the gate|up and down matvecs: FETCH_SIZE and WRITE_SIZE (KiB per
-    dispatch, two separate rocprofv3 passes), each scaled by the same counter's reading for the
-    calibration copy (COPY_BYTES read and COPY_BYTES written)."""
+    """HBM bytes per launch of the gate|up and down matvecs and of the decode attention launch:
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch, two separate rocprofv3 passes), each scaled by the
+    same counter's reading for the calibration copy (COPY_BYTES read and COPY_BYTES written)."""
     if shutil.which("rocprofv3") is None:
         return {"error": "rocprofv3 not found"}
     workdir = tempfile.mkdtemp(prefix="tsr_pmc_")
@@ -570,12 +594,14 @@ def measure_traffic(reps: int = 3) -> dict:
             rows = _pmc_pass(counter, workdir)
             copy = [v for _, k, v in rows if "copyBuffer" in k]
             mv = [v for _, k, v in rows if "k_mv_q4k" in k]
-            if not copy or len(mv) != 2 * reps:
+            fa = [v for _, k, v in rows if "k_fa" in k]
+            if not copy or len(mv) != 2 * reps or len(fa) != reps:
                 raise RuntimeError(f"{counter}: unexpected dispatches {[(k, v) for _, k, v in rows][:12]}")
             cal = COPY_BYTES / (float(np.median(copy)) * 1024.0)   # true bytes per counted byte
             res[counter] = {"calibration_factor": round(cal, 4), "copy_KiB": float(np.median(copy)),
                             "gate|up": float(np.median(mv[:reps])) * 1024.0 * cal,
-                            "down": float(np.median(mv[reps:])) * 1024.0 * cal}
+                            "down": float(np.median(mv[reps:])) * 1024.0 * cal,
+                            "fa": float(np.median(fa)) * 1024.0 * cal}
         return res
     finally:
         shutil.rmtree(workdir, ignore_errors=True)
@@ -619,11 +645,10 @@ def main() -> int:
     e2e = e2e_decode(dev, ev, args.steps, args.warmup, eager=args.eager)
     print(f"bench: {e2e['tok_s']:.1f} tok/s", file=sys.stderr, flush=True)
     per_op = e2e["per_op"]
-    # the roofline kernel: the single-launch op class with the largest share of a token
-    single = {k: v for k, v in per_op.items() if v["kernel"].startswith("k_mv_q4k")}
-    dom = max(single, key=lambda k: single[k]["us_per_token"])
-    dv = single[dom]
-    tag = "gate|up" if "gate|up" in dom else ("down" if "down" in dom else None)
+    # the roofline kernel: the op class (one kernel each) with the largest share of a token
+    dom = max(per_op, key=lambda k: per_op[k]["us_per_token"])
+    dv = per_op[dom]
+    tag = next((t for t, key in PMC_TAGS.items() if key in dom), None)
     traffic_bytes = None
     if tag and traffic and "error" not in traffic:
         traffic_bytes = round(traffic["FETCH_SIZE"][tag] + traffic["WRITE_SIZE"][tag])

@@ -242,7 +242,10 @@ int tsr_hip_set_fa_wait_limit(tsr_hip_ctx * ctx, uint32_t polls);
  * replayed by one launch: one decode token per replay (the backend's one op list per token,
  * sw/ctrl/ref/opl_ref.hpp:1-9). The stream must not be the null stream. Entry points that copy from
  * the host or allocate (tsr_hip_write, _write_async, _fa_plan_set, a first FA or prefill call that
- * grows the scratch) refuse to run under capture. */
+ * grows the scratch) refuse to run under capture. A graph whose captured launches use the context's
+ * scratch (tsr_hip_flash_attn, MUL_MAT at T >= 16, tsr_hip_mul_mat_isums) holds its address: once a
+ * later call has grown the scratch (and freed the old block), tsr_hip_graph_launch refuses that graph
+ * with TSR_HIP_E_ARG; capture it again. Graphs of planned FA launches and matvecs use no scratch. */
 typedef struct tsr_hip_graph tsr_hip_graph;
 int tsr_hip_graph_begin(tsr_hip_ctx * ctx, void * stream);
 int tsr_hip_graph_end(tsr_hip_ctx * ctx, void * stream, tsr_hip_graph ** out);

@@ -20,7 +20,9 @@ void tsr_expk_table(tsr::ExpkTab * t);
 // user first waits (hipStreamWaitEvent) for the work queued on that stream, so two calls never use
 // the block at once; growing waits for the whole device first, so no queued kernel still uses the
 // old block. Under graph capture neither a growth nor a wait on another stream can be recorded:
-// reserve() then fails with TSR_HIP_E_ARG (warm the context up outside the capture).
+// reserve() then fails with TSR_HIP_E_ARG (warm the context up outside the capture). A graph whose
+// capture used the scratch holds its address: `gen` counts the reallocations, and a replay after one
+// is refused (tsr_hip_graph_launch) instead of writing freed memory.
 inline bool tsr_capturing(hipStream_t s) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     return hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
@@ -30,7 +32,10 @@ struct tsr_scratch {
     size_t bytes = 0;
     hipStream_t last = nullptr;
     hipEvent_t ev = nullptr;
+    uint64_t gen = 0;                            // reallocations so far
+    bool captured = false;                       // a capture in progress used the block
     int reserve(size_t need, hipStream_t s) {
+        if (tsr_capturing(s)) captured = true;
         if (last != nullptr && last != s) {
             if (tsr_capturing(s)) return TSR_HIP_E_ARG;
             if (ev == nullptr) {
@@ -49,6 +54,7 @@ struct tsr_scratch {
         ptr = nullptr;
         bytes = 0;
         const size_t n = (need + (1u << 20) - 1u) & ~(size_t)((1u << 20) - 1u);
+        ++gen;
         const int rc = tsr::hip_err(hipMalloc(&ptr, n), "hipMalloc scratch");
         if (rc == 0) bytes = n;
         return rc;

@@ -605,6 +605,8 @@ int tsr_hip_mul_mat_isums(tsr_hip_ctx * ctx, const tsr_hip_weight * w, const flo
 struct tsr_hip_graph {
     hipGraph_t g = nullptr;
     hipGraphExec_t x = nullptr;
+    bool uses_scratch = false;                   // a captured launch holds the scratch's address
+    uint64_t scratch_gen = 0;                    // the scratch's generation at capture
 };
 
 int tsr_hip_graph_begin(tsr_hip_ctx * ctx, void * stream) {
@@ -613,6 +615,7 @@ int tsr_hip_graph_begin(tsr_hip_ctx * ctx, void * stream) {
     (void)hipSetDevice(ctx->device);
     hipStream_t s = ctx->pick(stream);
     if (tsr_capturing(s)) return TSR_HIP_E_ARG;
+    ctx->scratch.captured = false;
     return hip_err(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
 }
 
@@ -628,6 +631,9 @@ int tsr_hip_graph_end(tsr_hip_ctx * ctx, void * stream, tsr_hip_graph ** out) {
     auto * gr = new (std::nothrow) tsr_hip_graph();
     if (gr == nullptr) { (void)hipGraphDestroy(g); return TSR_HIP_E_NOMEM; }
     gr->g = g;
+    gr->uses_scratch = ctx->scratch.captured;
+    gr->scratch_gen = ctx->scratch.gen;
+    ctx->scratch.captured = false;
     if ((rc = hip_err(hipGraphInstantiate(&gr->x, g, nullptr, nullptr, 0), "hipGraphInstantiate")) != 0) {
         (void)hipGraphDestroy(g);
         delete gr;
@@ -640,6 +646,8 @@ int tsr_hip_graph_end(tsr_hip_ctx * ctx, void * stream, tsr_hip_graph ** out) {
 int tsr_hip_graph_launch(tsr_hip_ctx * ctx, const tsr_hip_graph * graph, void * stream) {
     if (ctx == nullptr || graph == nullptr) return TSR_HIP_E_ARG;
     std::lock_guard<std::mutex> lk(ctx->mtx);
+    // the scratch block the capture used was freed by a later growth: capture again
+    if (graph->uses_scratch && graph->scratch_gen != ctx->scratch.gen) return TSR_HIP_E_ARG;
     (void)hipSetDevice(ctx->device);
     return hip_err(hipGraphLaunch(graph->x, ctx->pick(stream)), "hipGraphLaunch");
 }

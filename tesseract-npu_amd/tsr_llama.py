@@ -39,6 +39,10 @@ import tsr_hip as H
 import tsr_synth as S
 
 
+class DecodeError(RuntimeError):
+    """A decode launch raised the decoder's index / wait flag (LlamaDecoder.check)."""
+
+
 @dataclass(frozen=True)
 class LlamaConfig:
     name: str
@@ -91,20 +95,32 @@ def layer_tensors(cfg: LlamaConfig, il: int):
 class SyntheticWeights:
     """Seeded random-init weights: every quantized tensor is normal(seed_of(config, name), std) rows
     quantized to the config's format; norms are f32 N(1, 0.1); the token embedding is f32 N(0, 1)
-    rows (the lookup copies rows bit for bit). Values depend only on (config name, tensor name)."""
+    rows (the lookup copies rows bit for bit). Values depend only on (config name, tensor name).
+    cache=True keeps every generated tensor on the host, so that a GPU model and a CPU checker built
+    from the same object see the same arrays without generating them twice."""
 
-    def __init__(self, cfg: LlamaConfig):
+    def __init__(self, cfg: LlamaConfig, cache: bool = False):
         self.cfg = cfg
+        self.cache = {} if cache else None
+
+    def _kept(self, key, make):
+        if self.cache is None:
+            return make()
+        if key not in self.cache:
+            self.cache[key] = make()
+        return self.cache[key]
 
     def quant(self, name: str, N: int, K: int, fmt: int) -> np.ndarray:
-        return S.quant_rows(fmt, tensor_seed(self.cfg, name), N, K, self.cfg.std)
+        return self._kept((name, fmt), lambda: S.quant_rows(fmt, tensor_seed(self.cfg, name), N, K, self.cfg.std))
 
     def norm(self, name: str) -> np.ndarray:
-        return (1.0 + S.normal(tensor_seed(self.cfg, name), self.cfg.n_embd, 0.1)).astype(np.float32)
+        return self._kept(name, lambda: (1.0 + S.normal(tensor_seed(self.cfg, name), self.cfg.n_embd, 0.1))
+                          .astype(np.float32))
 
     def embedding(self) -> np.ndarray:
         c = self.cfg
-        return S.normal(tensor_seed(c, "token_embd.weight"), c.n_vocab * c.n_embd, 1.0).reshape(c.n_vocab, c.n_embd)
+        return self._kept("token_embd.weight", lambda: S.normal(tensor_seed(c, "token_embd.weight"), c.n_vocab * c.n_embd,
+                                                                1.0).reshape(c.n_vocab, c.n_embd))
 
     def kv_history(self, il: int, which: int, n: int) -> np.ndarray:
         """f32 rows [n, E] quantized into cells 0 .. n-1 before decoding (the prefilled context)."""
@@ -411,26 +427,49 @@ class LlamaDecoder:
         self.plan.set(msum, runs)
         self._ops(self.tok)
 
-    def generate_graph(self, first_token: int, pos0: int, n_tokens: int, hist=None) -> None:
-        """Greedy decode of n_tokens by graph replays, without waiting for the device; the token
-        generated at step i is copied to hist[i] (a device int32 buffer) when given."""
+    def generate_graph(self, first_token: int, pos0: int, n_tokens: int, hist=None, check: bool = True) -> None:
+        """Greedy decode of n_tokens by graph replays, queued without waiting for the device; the token
+        generated at step i is copied to hist[i] (a device int32 buffer) when given. With check, the
+        batch ends with check() (one wait for the device, DecodeError on a raised flag)."""
         for i in range(n_tokens):
             self.step_graph(first_token if i == 0 else None, pos0 + i)
             if hist is not None:
                 self.dev.copy_async(hist.ptr + 4 * i, self.tok, 4)
+        if check:
+            self.check()
+
+    BAD_RANGE, BAD_WAIT = 1, 2
+
+    def check(self) -> None:
+        """Wait for the device, then raise DecodeError if a launch since the last check raised the
+        decoder's flag: bit 0, a token id or cache cell was out of range (GET_ROWS / SET_ROWS_KV stored
+        nothing); bit 1, the one-launch FLASH_ATTN_EXT's bounded wait for its chunk maxima expired (its
+        attention output is not valid). The flag is cleared when it is reported."""
+        self.dev.sync()
+        bad = int(self.bad.read(np.int32, (1,))[0])
+        if bad == 0:
+            return
+        self.bad.fill(0)
+        why = []
+        if bad & self.BAD_RANGE:
+            why.append("a token id or cache cell was out of range")
+        if bad & self.BAD_WAIT:
+            why.append("the one-launch FLASH_ATTN_EXT's wait for its chunk maxima expired (attention not valid)")
+        raise DecodeError(f"decode flag {bad}: " + "; ".join(why or ["unknown code"]))
 
     def read_logits(self) -> np.ndarray:
-        self.dev.sync()
+        """The logits of the last step (checked: raises DecodeError on a raised flag)."""
+        self.check()
         return self.logits.read(np.float32, (self.cfg.n_vocab,))
 
     def read_next(self) -> int:
-        """The greedy token of the last eager step."""
-        self.dev.sync()
+        """The greedy token of the last eager step (checked)."""
+        self.check()
         return int(self.next.read(np.int32, (1,))[0])
 
     def read_token(self) -> int:
-        """The greedy token of the last graph replay (it is also the next replay's input)."""
-        self.dev.sync()
+        """The greedy token of the last graph replay (it is also the next replay's input; checked)."""
+        self.check()
         return int(self.tok.read(np.int32, (1,))[0])
 
     def generate(self, first_token: int, pos0: int, n_tokens: int) -> list[int]:

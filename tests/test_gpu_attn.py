@@ -71,6 +71,18 @@ def test_fa_causal_prefill(dev, oc):
     assert_bits_equal(got, want, "causal prefill")
 
 
+def test_fa_causal_prefill_baseline_512(dev, oc):
+    """causal flash attention over a 512-token ubatch at cells 0 .. 511, 32 q / 8 KV
+    heads, D 128, q8_0 K / V, Q drawn f16 N(0, 1): row t sees cells [0, t], the ubatch's cells newest
+    last. Every output of every row bit-exact (the contract allows 2e-3 absolute, asserted too)."""
+    T = 512
+    mask = np.full((T, T), -np.inf, np.float16)
+    mask[np.tril_indices(T)] = 0
+    got, want = _fa(dev, oc, T, T, 32, 8, 128, T=T, mask=mask, new_runs=[[0, T]], seed=512)
+    assert np.abs(got - want).max() <= 2e-3
+    assert_bits_equal(got, want, "causal prefill 512")
+
+
 def test_fa_general_and_two_run_masks(dev, oc):
     m2 = np.zeros((3, 100), np.float16); m2[:, 10:20] = -2.5; m2[1, 50:] = -np.inf
     got, want = _fa(dev, oc, 100, 112, 8, 2, 64, T=3, mask=m2)
@@ -184,3 +196,39 @@ def test_fa_decode_graph_replays(dev, oc):
     finally:
         hip.h.hipGraphExecDestroy(ge)
         hip.h.hipGraphDestroy(g)
+
+
+def test_graph_refused_after_scratch_growth(oc):
+    """A graph whose capture used the context's scratch (the unplanned FLASH_ATTN_EXT's partials) replays
+    while the scratch block stays; after a larger call has grown (reallocated) it, the launch is refused
+    and the stale graph never runs; a new capture replays exactly. A fresh context, so that the scratch
+    starts empty."""
+    d2 = tsr_hip.Device(0)
+    try:
+        a = _decode_case(oc, d2, 1024, 41)
+        _run(d2, a)                                     # warm: the scratch holds a's partials
+        d2.sync()
+        d2.graph_begin()
+        _run(d2, a)
+        g = d2.graph_end()
+        a["out"].fill(0)
+        g.launch()
+        d2.sync()
+        assert_bits_equal(a["out"].read(np.float32, a["want"].shape), a["want"], "replay before growth")
+        big = _decode_case(oc, d2, 8192, 42)            # its byte upload and partials grow the scratch
+        _run(d2, big)
+        d2.sync()
+        assert_bits_equal(big["out"].read(np.float32, big["want"].shape), big["want"], "the growing call")
+        with pytest.raises(tsr_hip.TsrHipError):
+            g.launch()
+        g.free()
+        d2.graph_begin()
+        _run(d2, a)
+        g2 = d2.graph_end()
+        a["out"].fill(0)
+        g2.launch()
+        d2.sync()
+        assert_bits_equal(a["out"].read(np.float32, a["want"].shape), a["want"], "replay of the new capture")
+        g2.free()
+    finally:
+        d2.close()

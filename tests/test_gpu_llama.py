@@ -18,7 +18,7 @@ _libm.powf.argtypes = [C.c_float, C.c_float]
 _libm.powf.restype = C.c_float
 
 
-def oracle_model(oc, cfg, w, kv_size, hist):
+def oracle_model(oc, cfg, w, kv_size, hist, threads=1):
     t = {"token_embd.weight": w.embedding(), "output_norm.weight": w.norm("output_norm.weight")[None],
          "output.weight": w.quant("output.weight", cfg.n_vocab, cfg.n_embd, cfg.ofmt)}
     for il in range(cfg.n_layer):
@@ -29,7 +29,7 @@ def oracle_model(oc, cfg, w, kv_size, hist):
     m = OracleLlama(oc, n_layer=cfg.n_layer, n_embd=cfg.n_embd, n_ff=cfg.n_ff, n_head=cfg.n_head,
                     n_head_kv=cfg.n_head_kv, head_dim=cfg.head_dim, n_vocab=cfg.n_vocab, eps=cfg.eps,
                     rope_base=cfg.rope_base, rope_mode=cfg.rope_mode, wfmt=cfg.wfmt, ofmt=cfg.ofmt, tensors=t,
-                    kv_size=kv_size)
+                    kv_size=kv_size, threads=threads)
     for il in range(cfg.n_layer):
         for which in (0, 1):
             m.set_history(il, which, w.kv_history(il, which, hist))
@@ -163,4 +163,47 @@ def test_prefill_refusals(dev):
         gpu.prefill(np.zeros(0, np.int32))
     with pytest.raises(ValueError):
         gpu.prefill(np.zeros(10, np.int32), 60)
+    gpu.free()
+
+
+def test_decode_llama3_8b_token_matches_oracle(dev, oc):
+    """BASELINE configs[4] at its full shape: the Llama-3-8B-architecture Q4_K model (32 layers, n_embd
+    4096, n_ff 14336, 32 q / 8 KV heads of 128, vocabulary 128256), q8_0 caches holding a short history,
+    one decode token eagerly and the same token by graph replay (the form the bench times): all 128256
+    logits bit-equal to the oracle composition's step, and the same greedy token."""
+    cfg = LL.LLAMA3_8B
+    hist, kv_size = 100, 256
+    w = LL.SyntheticWeights(cfg, cache=True)        # one generation of the 4.5 GB of blocks for both sides
+    print(f"\n8B decode parity: history {hist}, kv {kv_size}", flush=True)
+    gpu = LL.LlamaDecoder(dev, cfg, w, kv_size)
+    gpu.prefill_history(w, hist)
+    ref = oracle_model(oc, cfg, w, kv_size, hist, threads=16)
+    ts = np.float32(_libm.powf(float(np.float32(cfg.rope_base)), float(np.float32(-2.0) / np.float32(cfg.head_dim))))
+    tok, pos = 1234, hist
+    n_kv = min(kv_size, (pos + 1 + 255) // 256 * 256)
+    want = ref.step(tok, pos, ts, n_kv)
+    print("8B decode parity: oracle token done", flush=True)
+    gpu.step(tok, pos)
+    assert_bits_equal(gpu.read_logits(), want, "8B eager step")
+    assert gpu.read_next() == int(oc.argmax(want[None])[0])
+    gpu.step_graph(tok, pos)                        # rewrites cell pos with the same rows
+    assert_bits_equal(gpu.read_logits(), want, "8B graph step")
+    assert gpu.read_token() == int(oc.argmax(want[None])[0])
+    for il in (0, cfg.n_layer - 1):                 # the new cell's K / V bytes
+        assert (gpu.layers[il]["kc"].get_bytes(0).reshape(kv_size, -1)[pos] == ref.kc[il][pos]).all()
+        assert (gpu.layers[il]["vc"].get_bytes(1).reshape(kv_size, -1)[pos] == ref.vc[il][pos]).all()
+    gpu.free()
+    w.cache.clear()
+
+
+def test_decode_flag_raises(dev):
+    """A token id outside the embedding table raises the decoder's flag (GET_ROWS stores nothing): the
+    next read raises DecodeError naming it, and the flag is cleared for the steps after it."""
+    cfg = LL.tiny_config()
+    gpu = LL.LlamaDecoder(dev, cfg, LL.SyntheticWeights(cfg), 64)
+    gpu.step_graph(cfg.n_vocab + 5, 3)
+    with pytest.raises(LL.DecodeError, match="out of range"):
+        gpu.read_token()
+    gpu.step_graph(5, 4)
+    gpu.read_token()
     gpu.free()

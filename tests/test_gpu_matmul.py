@@ -76,6 +76,24 @@ def test_mm_q8_0_baseline_prefill_shape(dev, oc):
     assert_bits_equal(got[:, rows], oc.mul_mat(0, blocks[rows], K, x, threads=8), "row sample")
 
 
+def test_mm_q8_0_baseline_prefill_ffn_shape(dev, oc):
+    """BASELINE configs[3] (512 tokens x W[14336 x 4096] Q8_0, the FFN up shape): every output of a
+    sample of tokens, and every token of a sample of rows (first, middle and last row blocks)."""
+    T, N, K = 512, 14336, 4096
+    blocks = S.quantize_q8_0(S.normal(S.seed_of("cfg4", "w_14336"), N * K, 0.02).reshape(N, K))
+    x = S.normal(S.seed_of("cfg4", "x"), T * K).reshape(T, K)
+    w = dev.weight(0, blocks, N, K)
+    yb = dev.alloc(4 * T * N)
+    dev.mul_mat(w, dev.upload(x), T, K, yb, N)
+    got = yb.read(np.float32, (T, N))
+    toks = [0, 1, 31, 32, 95, 96, 257, 510, 511]
+    assert_bits_equal(got[toks], oc.mul_mat(0, blocks, K, x[toks], threads=8), "token sample")
+    rows = np.r_[0:40, 7160:7176, 14300:14336]
+    assert_bits_equal(got[:, rows], oc.mul_mat(0, blocks[rows], K, x, threads=8), "row sample")
+    w.free()
+    yb.free()
+
+
 # ---- Q4_K (QACT A256, i8 matrix core per sub-block, exact f32 matrix-core msum) ----
 
 @pytest.mark.parametrize("T,N,K", [(16, 64, 256), (17, 100, 4096), (64, 256, 14336), (100, 33, 4096),

@@ -273,6 +273,21 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
                        const uint32_t (*new_runs)[2], uint32_t n_new, float * out_dev, uint64_t out_stride,
                        void * stream);
 
+/* FLASH_ATTN_EXT exactly as tsr_hip_flash_attn (same arguments, same bits), allocating nothing: no
+ * hipMalloc / hipFree / pinned staging / host-to-device copy, no wait on another stream. No counterpart
+ * in the reference; it is for callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Its partials live in a fixed device array of 16 MiB that each
+ * GPU holds from the library's load until the process ends; the work list travels in the kernel
+ * arguments. Limits: T <= 8 query rows, at most 48 planned chunks (about 98 K visible cells per row), and
+ * partials (scores 4 n_head B per visible cell and row, 2 KiB-per-head chunk partials) within the 16 MiB;
+ * beyond them TSR_HIP_E_RANGE, before anything runs. Every call on one GPU shares that GPU's array
+ * (from every context): calls that overlap on one GPU (two streams, two threads, two contexts) race. */
+int tsr_hip_flash_attn_noalloc(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint64_t q_stride,
+                               const tsr_hip_kv * kc, const tsr_hip_kv * vc, uint32_t D, uint32_t n_head,
+                               uint32_t n_head_kv, float scale, const uint32_t * msum, const float * mask_f32_dev,
+                               const uint32_t (*new_runs)[2], uint32_t n_new, float * out_dev, uint64_t out_stride,
+                               void * stream);
+
 /* ---- decode-layer glue ops ----------------------------------------------------------------------
  * The f32 ops around MUL_MAT and FLASH_ATTN in a decoder layer, on the vector unit's f32 rules
  * (every input denormal-as-zero, one IEEE round-to-nearest-even operation, result flushed to zero,

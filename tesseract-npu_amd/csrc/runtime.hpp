@@ -14,6 +14,11 @@ namespace tsr {
 int hip_err(hipError_t e, const char * what);
 }
 void tsr_expk_table(tsr::ExpkTab * t);
+struct tsr_hip_ctx;
+// The fixed device array of tsr_hip_flash_attn_noalloc (bytes) and the lookup of its device address,
+// made once per context with the context's device current.
+constexpr size_t kFaNoAllocBytes = (size_t)16 << 20;
+int tsr_fa_fixed_init(tsr_hip_ctx * ctx);
 
 // Device scratch owned by a context (FA partials and work lists, prefill QA images, the isums y
 // sink). It only grows. reserve() orders its users: a call on another stream than the previous
@@ -127,6 +132,7 @@ struct tsr_hip_ctx {
     tsr_staging staging;
     tsr::ExpkTab expk{};
     uint32_t fa_spin_max = 1u << 20;    // polls of the fused decode FA's tile-key wait (s_sleep 1 each)
+    uint8_t * fa_fixed = nullptr;       // device address of this device's fixed FA array (tsr_fa_fixed_init)
     hipStream_t pick(void * s) const { return s ? (hipStream_t)s : stream; }
 };
 

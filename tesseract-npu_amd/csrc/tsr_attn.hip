@@ -7,6 +7,7 @@
 #include <cstring>
 #include <mutex>
 #include <new>
+#include <type_traits>
 #include <vector>
 
 #include "kernels.hpp"
@@ -204,8 +205,36 @@ uint32_t ncg_of(uint32_t E, uint32_t D, uint32_t n_total) {
 
 // The chunks of one query row in execution order (one-row tiles: rules 1, 2, 4, 7, 8 of the planner,
 // sw/sim/include/tsr_fa_plan.h:16-42). Returns false for a malformed MSUM row.
+// A fixed-capacity stand-in for std::vector in the planner of the entry point that allocates nothing:
+// push_back past the capacity records an overflow instead of growing.
+template <class T, size_t N>
+struct FixedVec {
+    T v[N];
+    size_t n = 0;
+    bool overflow = false;
+    void clear() { n = 0; overflow = false; }
+    void push_back(const T & x) {
+        if (n < N) v[n++] = x;
+        else overflow = true;
+    }
+    void assign(size_t k, const T & x) {
+        if (k > N) { overflow = true; k = N; }
+        n = k;
+        for (size_t i = 0; i < k; ++i) v[i] = x;
+    }
+    size_t size() const { return n; }
+    T & operator[](size_t i) { return v[i]; }
+    const T & operator[](size_t i) const { return v[i]; }
+    T * data() { return v; }
+    const T * begin() const { return v; }
+    const T * end() const { return v + n; }
+};
+template <class V> bool overflowed(const V &) { return false; }
+template <class T, size_t N> bool overflowed(const FixedVec<T, N> & v) { return v.overflow; }
+
+template <class Out>
 bool plan_row(uint32_t E, uint32_t D, const uint32_t * words, uint32_t q, const uint32_t (*new_runs)[2],
-              uint32_t n_new, std::vector<Chunk> & out) {
+              uint32_t n_new, Out & out) {
     const uint32_t n_kv = words[2];
     const bool general = (words[3] & 1u) != 0u;
     struct Sub { uint32_t ulo, uhi; uint64_t lo, hi; } sub[2];
@@ -265,26 +294,36 @@ int fa_check_shape(uint32_t D, uint32_t n_head, uint32_t n_head_kv, float scale)
 }
 
 // The work list of one call: every token row planned, flattened into items (chunks) with their
-// 256-cell score tiles; tok = tok_first[T] | tok_count[T].
-struct FaWork {
-    std::vector<tsr::FaItem> items;
-    std::vector<uint32_t> tok;
+// 256-cell score tiles; tok = tok_first[T] | tok_count[T]. FaWorkFixed holds at most the inline list
+// (kFaInlItems items of at most kFaInlTok tokens) in fixed arrays: planning it allocates nothing.
+template <class Items, class Tok, class Chunks>
+struct FaWorkT {
+    Items items;
+    Tok tok;
+    Chunks ch;               // one row's chunks (planner temporary)
     uint64_t cells = 0;
     uint32_t n_tiles = 0, maxtiles = 1, max_groups = 0;
 };
+using FaWork = FaWorkT<std::vector<tsr::FaItem>, std::vector<uint32_t>, std::vector<Chunk>>;
+using FaWorkFixed = FaWorkT<FixedVec<tsr::FaItem, tsr::kFaInlItems>, FixedVec<uint32_t, 2u * tsr::kFaInlTok>,
+                            FixedVec<Chunk, tsr::kFaInlItems>>;
 
+// Returns TSR_HIP_E_RANGE when a fixed-capacity work list overflows.
+template <class W>
 int fa_plan_rows(uint32_t E, uint32_t D, uint32_t T, const uint32_t * msum, const uint32_t (*new_runs)[2], uint32_t n_new,
-                 bool have_mask, FaWork & w) {
+                 bool have_mask, W & w) {
     w.items.clear();
     w.tok.assign(2u * (size_t)T, 0u);
+    if (overflowed(w.tok)) return TSR_HIP_E_RANGE;
     w.cells = 0;
     w.n_tiles = 0;
     w.maxtiles = 1;
     w.max_groups = 0;
-    std::vector<Chunk> ch;
+    auto & ch = w.ch;
     for (uint32_t t = 0; t < T; ++t) {
         ch.clear();
         if (!plan_row(E, D, msum, t, new_runs, n_new, ch)) return TSR_HIP_E_MASK;
+        if (overflowed(ch)) return TSR_HIP_E_RANGE;
         w.tok[t] = (uint32_t)w.items.size();
         w.tok[T + t] = (uint32_t)ch.size();
         for (const Chunk & c : ch) {
@@ -305,6 +344,7 @@ int fa_plan_rows(uint32_t E, uint32_t D, uint32_t T, const uint32_t * msum, cons
             w.cells += 16u * c.n;
             w.items.push_back(it);
         }
+        if (overflowed(w.items)) return TSR_HIP_E_RANGE;
     }
     return TSR_HIP_OK;
 }
@@ -333,10 +373,14 @@ tsr::FaArgs fa_args(tsr_hip_ctx * ctx, const float * q_dev, uint64_t q_stride, c
 
 }  // namespace
 
-int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint64_t q_stride, const tsr_hip_kv * kc,
-                       const tsr_hip_kv * vc, uint32_t D, uint32_t n_head, uint32_t n_head_kv, float scale,
-                       const uint32_t * msum, const float * mask_f32_dev, const uint32_t (*new_runs)[2], uint32_t n_new,
-                       float * out_dev, uint64_t out_stride, void * stream) {
+// The unplanned FLASH_ATTN_EXT: the host plans the rows, the partials go to the context's scratch
+// (NOALLOC false: grown by hipMalloc on demand, ordered across streams) or to the fixed device array of
+// this file (NOALLOC true: the inline work list only, nothing allocated, nothing waited for).
+template <bool NOALLOC>
+static int fa_unplanned(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint64_t q_stride, const tsr_hip_kv * kc,
+                        const tsr_hip_kv * vc, uint32_t D, uint32_t n_head, uint32_t n_head_kv, float scale,
+                        const uint32_t * msum, const float * mask_f32_dev, const uint32_t (*new_runs)[2], uint32_t n_new,
+                        float * out_dev, uint64_t out_stride, void * stream) {
     if (ctx == nullptr || q_dev == nullptr || kc == nullptr || vc == nullptr || msum == nullptr || out_dev == nullptr ||
         T == 0u || (n_new && new_runs == nullptr))
         return TSR_HIP_E_ARG;
@@ -348,8 +392,9 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     if (((uintptr_t)q_dev & 15u) != 0u || (T > 1u && (q_stride % 4u != 0u || q_stride < K)) ||
         (T > 1u && out_stride < K) || T > 65535u)
         return TSR_HIP_E_ARG;
+    if (NOALLOC && T > tsr::kFaInlTok) return TSR_HIP_E_RANGE;
 
-    FaWork w;
+    typename std::conditional<NOALLOC, FaWorkFixed, FaWork>::type w;
     if ((rc = fa_plan_rows(E, D, T, msum, new_runs, n_new, mask_f32_dev != nullptr, w)) != 0) return rc;
     const size_t n_items = w.items.size();
     if (w.cells * n_head > 0xFFFFFFFFull || n_items * 4u > 0x7FFFFFFFull || n_items * w.maxtiles > 0x7FFFFFFFull)
@@ -361,6 +406,7 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     const size_t o_Mp = off; off = up256(off + 4u * (size_t)w.n_tiles * n_head);
     const size_t o_OP = off; off = up256(off + 4u * n_items * kC * n_head * D);
     const size_t o_LP = off; off = up256(off + 4u * n_items * kC * n_head);
+    if (NOALLOC && off > kFaNoAllocBytes) return TSR_HIP_E_RANGE;
 
     tsr::FaPlan p{};
     p.n_items = (uint32_t)n_items;
@@ -369,7 +415,7 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     if (inl) {
         std::copy(w.items.begin(), w.items.end(), p.items);
         for (uint32_t t = 0; t < T; ++t) { p.tok_first[t] = w.tok[t]; p.tok_count[t] = w.tok[T + t]; }
-    } else {                                                      // items | tok_first | tok_count, one copy
+    } else if constexpr (!NOALLOC) {                              // items | tok_first | tok_count, one copy
         packed.resize(n_items * sizeof(tsr::FaItem) + 8u * (size_t)T);
         memcpy(packed.data(), w.items.data(), n_items * sizeof(tsr::FaItem));
         memcpy(packed.data() + n_items * sizeof(tsr::FaItem), w.tok.data(), 8u * (size_t)T);
@@ -378,15 +424,21 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
     hipStream_t s = ctx->pick(stream);
-    rc = ctx->scratch.reserve(off, s);
-    if (rc) return rc;
-    uint8_t * base = (uint8_t *)ctx->scratch.ptr;
-    if (!inl) {
-        // a host-to-device copy of a host vector cannot be recorded into a graph (the vector is gone
-        // when the graph replays): long work lists are for eager calls or a tsr_hip_fa_plan
-        if (tsr_capturing(s)) return TSR_HIP_E_ARG;
-        rc = hip_err(hipMemcpyAsync(base + o_items, packed.data(), packed.size(), hipMemcpyHostToDevice, s), "fa plan");
+    uint8_t * base;
+    if constexpr (NOALLOC) {
+        if (ctx->fa_fixed == nullptr) return TSR_HIP_E_HIP;       // the array's address was not found at open
+        base = ctx->fa_fixed;
+    } else {
+        rc = ctx->scratch.reserve(off, s);
         if (rc) return rc;
+        base = (uint8_t *)ctx->scratch.ptr;
+        if (!inl) {
+            // a host-to-device copy of a host vector cannot be recorded into a graph (the vector is gone
+            // when the graph replays): long work lists are for eager calls or a tsr_hip_fa_plan
+            if (tsr_capturing(s)) return TSR_HIP_E_ARG;
+            rc = hip_err(hipMemcpyAsync(base + o_items, packed.data(), packed.size(), hipMemcpyHostToDevice, s), "fa plan");
+            if (rc) return rc;
+        }
     }
     tsr::FaArgs a = fa_args(ctx, q_dev, q_stride, kc, vc, D, n_head, n_head_kv, scale, mask_f32_dev,
                             16u * ((msum[2] + 15u) / 16u), out_dev, out_stride);
@@ -403,6 +455,42 @@ int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint6
     ctx->ctr.flash_attn_calls++;
     ctx->ctr.flash_attn_kv_bytes += w.cells * (uint64_t)E / 32u * 34u * 2u;
     return tsr_launch_fa(a, p, T, (uint32_t)ctx->n_cu, s) ? TSR_HIP_E_HIP : TSR_HIP_OK;
+}
+
+int tsr_hip_flash_attn(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint64_t q_stride, const tsr_hip_kv * kc,
+                       const tsr_hip_kv * vc, uint32_t D, uint32_t n_head, uint32_t n_head_kv, float scale,
+                       const uint32_t * msum, const float * mask_f32_dev, const uint32_t (*new_runs)[2], uint32_t n_new,
+                       float * out_dev, uint64_t out_stride, void * stream) {
+    return fa_unplanned<false>(ctx, q_dev, T, q_stride, kc, vc, D, n_head, n_head_kv, scale, msum, mask_f32_dev,
+                               new_runs, n_new, out_dev, out_stride, stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The FLASH_ATTN_EXT entry point that allocates nothing (for callers that cannot call hipMalloc: code
+// under graph capture, tight serving loops). Its partials live in fa_fixed_scratch, a file-scope device
+// array of kFaNoAllocBytes that every GPU the library runs on holds until the process ends. On the host
+// the array's name is a stand-in, not a device address: tsr_fa_fixed_init (run by tsr_hip_open with the
+// context's device current) looks the device address up once, and launches use only that address. All
+// calls on one GPU share its array (every context on that device): calls that overlap on one GPU race.
+// Nothing in the array has to start at zero (every partial is written before it is read).
+// ---------------------------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t fa_fixed_scratch[kFaNoAllocBytes];
+
+int tsr_fa_fixed_init(tsr_hip_ctx * ctx) {
+    void * p = nullptr;
+    const int rc = hip_err(hipGetSymbolAddress(&p, HIP_SYMBOL(fa_fixed_scratch)), "hipGetSymbolAddress fa_fixed_scratch");
+    if (rc) return rc;
+    ctx->fa_fixed = (uint8_t *)p;
+    return TSR_HIP_OK;
+}
+
+int tsr_hip_flash_attn_noalloc(tsr_hip_ctx * ctx, const float * q_dev, uint32_t T, uint64_t q_stride,
+                               const tsr_hip_kv * kc, const tsr_hip_kv * vc, uint32_t D, uint32_t n_head,
+                               uint32_t n_head_kv, float scale, const uint32_t * msum, const float * mask_f32_dev,
+                               const uint32_t (*new_runs)[2], uint32_t n_new, float * out_dev, uint64_t out_stride,
+                               void * stream) {
+    return fa_unplanned<true>(ctx, q_dev, T, q_stride, kc, vc, D, n_head, n_head_kv, scale, msum, mask_f32_dev,
+                              new_runs, n_new, out_dev, out_stride, stream);
 }
 
 // ---------------------------------------------------------------------------------------------

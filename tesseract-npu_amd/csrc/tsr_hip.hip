@@ -82,6 +82,11 @@ int tsr_hip_open(int device, tsr_hip_ctx ** out) {
         delete c;
         return rc;
     }
+    if ((rc = tsr_fa_fixed_init(c)) != 0) {                       // the device address of the fixed FA array
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return rc;
+    }
     *out = c;
     return TSR_HIP_OK;
 }

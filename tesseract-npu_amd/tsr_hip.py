@@ -37,6 +37,7 @@ EXPORTS = (
     "tsr_hip_fa_plan_free", "tsr_hip_graph_begin", "tsr_hip_graph_end", "tsr_hip_graph_launch", "tsr_hip_graph_free",
     "tsr_hip_mul_mat_norm", "tsr_hip_rope_kv", "tsr_hip_flash_attn_plan_rope", "tsr_hip_rope_table",
     "tsr_hip_flash_attn_plan_rope_tab", "tsr_hip_mul_mat_epi", "tsr_hip_set_fa_wait_limit",
+    "tsr_hip_flash_attn_noalloc",
 )
 
 
@@ -86,6 +87,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "tsr_hip_msum_build_f16": ([vp, sz, u32, u32, vp], C.c_int),
         "tsr_hip_flash_attn": ([vp, vp, u32, u64, vp, vp, u32, u32, u32, C.c_float, vp, vp, vp, u32, vp, u64, vp],
                                C.c_int),
+        "tsr_hip_flash_attn_noalloc": ([vp, vp, u32, u64, vp, vp, u32, u32, u32, C.c_float, vp, vp, vp, u32, vp, u64,
+                                        vp], C.c_int),
         "tsr_hip_get_counters": ([vp, vp], C.c_int),
         "tsr_hip_rms_norm": ([vp, vp, u32, u32, u64, C.c_float, vp, u64, u32, vp, u64, vp], C.c_int),
         "tsr_hip_rope": ([vp, vp, u32, u64, u32, u32, u32, C.c_int, vp, C.c_float, C.c_float, C.c_float, vp, vp, u64,
@@ -404,6 +407,19 @@ class Device:
                                          float(scale), words.ctypes.data, self._p(mask_f32),
                                          None if nr is None else nr.ctypes.data, 0 if nr is None else nr.shape[0],
                                          self._p(out), out_stride, stream), "flash_attn")
+
+    def flash_attn_noalloc(self, q, T: int, q_stride: int, kc: KvCache, vc: KvCache, D: int, n_head: int,
+                           n_head_kv: int, scale: float, msum, out, out_stride: int, mask_f32=None, new_runs=None,
+                           stream=None) -> None:
+        """flash_attn through the entry point that allocates nothing (its partials in the library's fixed
+        device array: T <= 8, <= 48 chunks, <= 16 MiB of partials)."""
+        words = np.ascontiguousarray(msum, np.uint32)
+        nr = None if new_runs is None else np.ascontiguousarray(new_runs, np.uint32).reshape(-1, 2)
+        _check(self.L.tsr_hip_flash_attn_noalloc(self.ctx, self._p(q), T, q_stride, kc.h, vc.h, D, n_head, n_head_kv,
+                                                 float(scale), words.ctypes.data, self._p(mask_f32),
+                                                 None if nr is None else nr.ctypes.data,
+                                                 0 if nr is None else nr.shape[0], self._p(out), out_stride, stream),
+               "flash_attn_noalloc")
 
     def write_async(self, dst, arr, stream=None) -> None:
         """Stream-ordered host-to-device copy of arr (<= 16 KiB); arr may be reused at once."""

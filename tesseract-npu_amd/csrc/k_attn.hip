@@ -31,53 +31,11 @@
 #include "kernels.hpp"
 #include "kvstore.hpp"
 #include "qact.hpp"
+#include "fa_common.hpp"
 
 #include <algorithm>
 
 namespace tsr {
-
-constexpr uint32_t kMFloor = 0xF1800000u;   // -2^100 (AT 6.3)
-constexpr uint32_t kLFloor = 0x00800000u;   // 2^-126 (AT 5.7)
-
-
-// MAXT (AT 5.4, sw/sim/tsr_ref_at.c:286-292): NaN wins as the canonical NaN; -0 < +0.
-__device__ __forceinline__ uint32_t maxt_key(uint32_t u) { return (u >> 31) ? ~u : (u | 0x80000000u); }
-__device__ __forceinline__ float maxt(float a, float b) {
-    const uint32_t ua = fb(daz(a)), ub = fb(daz(b));
-    if ((ua & 0x7FFFFFFFu) > 0x7F800000u || (ub & 0x7FFFFFFFu) > 0x7F800000u) return bf(kNaN);
-    return maxt_key(ua) >= maxt_key(ub) ? bf(ua) : bf(ub);
-}
-// Order-preserving key of MAXT's total order (DAZ applied; NaN above everything; -0 < +0).
-__device__ __forceinline__ uint32_t maxt_key_f(float v) {
-    const uint32_t u = fb(daz(v));
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0xFFFFFFFFu;
-    return (u >> 31) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float maxt_unkey(uint32_t k) {
-    if (k == 0xFFFFFFFFu) return bf(kNaN);
-    return bf((k >> 31) ? (k & 0x7FFFFFFFu) : ~k);
-}
-// Wave-wide max / sum with DPP inside rows, a swizzle across the halves and two readlanes (every
-// lane of the wave must be active).
-__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
-    v = umax_u(v, (uint32_t)dpp_i<kDppXor1>((int)v));
-    v = umax_u(v, (uint32_t)dpp_i<kDppXor2>((int)v));
-    v = umax_u(v, (uint32_t)dpp_i<kDppRowHalfMirror>((int)v));
-    v = umax_u(v, (uint32_t)dpp_i<kDppRowMirror>((int)v));
-    v = umax_u(v, (uint32_t)xor16_i((int)v));
-    return umax_u((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 32));
-}
-__device__ __forceinline__ int wave_max_i(int v) {   // via the order-preserving unsigned map
-    return (int)(wave_max_u((uint32_t)v ^ 0x80000000u) ^ 0x80000000u);
-}
-__device__ __forceinline__ int wave_sum_i(int v) {
-    v += dpp_i<kDppXor1>(v);
-    v += dpp_i<kDppXor2>(v);
-    v += dpp_i<kDppRowHalfMirror>(v);
-    v += dpp_i<kDppRowMirror>(v);
-    v += xor16_i(v);
-    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
-}
 
 // ---------------------------------------------------------------------------------------------
 // P.V: block (item * 4 + channel c, KV head g, group hg of 4 query heads x value part vh of VS); one
@@ -102,44 +60,9 @@ __device__ __forceinline__ int wave_sum_i(int v) {
 constexpr uint32_t kPvWaves = 8;                                  // NCG <= 128 -> <= 8 segments per channel
 constexpr uint32_t kPvMaxSeg = 8;
 
-// CTREE over 4 channel partials (never subnormal: results of the segment chains).
-__device__ __forceinline__ float ctree4(float x0, float x1, float x2, float x3) { return sadd_n(sadd_n(x0, x1), sadd_n(x2, x3)); }
-__device__ __forceinline__ int32_t row16_isum(int32_t v) {
-    v += dpp_i<kDppXor1>(v);
-    v += dpp_i<kDppXor2>(v);
-    v += dpp_i<kDppRowHalfMirror>(v);
-    return v + dpp_i<kDppRowMirror>(v);
-}
-__device__ __forceinline__ uint32_t f_field(float f) { return (fb(f) >> 23) & 0xFFu; }   // biased exponent
-
-// RNE_int(w 2^(23 - es)) of a zero or normal w with exponent(w) <= es (sw/sim/tsr_ref_at.c:386-410):
-// the power-of-two scaling is exact while the scaled value is normal, v_rndne_f32 rounds half to even,
-// and a scaled value below 2^-126 is below 1/2 and rounds to 0 either way. |result| <= 2^24.
-__device__ __forceinline__ int32_t bf_int_n(float w, int32_t es) {
-    return (int32_t)__builtin_rintf(__builtin_ldexpf(w, 23 - es));
-}
-// f = RNE24(A) (zero or normal) scaled by 2^k: below 2^-126 a signed zero, from 2^128 a signed Inf,
-// A == 0 -> +0 (sw/sim/tsr_ref_at.c:412-436). The exponent field of f plus k is the result's.
-__device__ __forceinline__ float bf_scale(float f, int32_t k) {
-    const uint32_t u = fb(f), s = u & 0x80000000u;
-    const int32_t ne = (int32_t)((u >> 23) & 0xFFu) + k;
-    uint32_t out = u + ((uint32_t)k << 23);
-    out = ne < 1 ? s : (ne > 254 ? (s | 0x7F800000u) : out);
-    return bf((u & 0x7FFFFFFFu) == 0u ? 0u : out);
-}
-
-typedef int v4i_fa __attribute__((ext_vector_type(4)));
-
-// A = d0 + 256 d1 + 65536 d2 + 2^24 d3 of four digit sums (|d_k| <= 2^20): every product and partial
-// sum is exact in f64 (|A| < 2^45), and the one conversion to f32 is RNE24(A).
-__device__ __forceinline__ float digits_rne24(const v4i_fa & acc) {
-    const double A = ((double)acc[3] * 16777216.0 + (double)acc[2] * 65536.0) + ((double)acc[1] * 256.0 + (double)acc[0]);
-    return (float)A;
-}
-
 // The P.V work of one block (chunk item, channel c, KV head g, head group hg, value part vh), shared by
-// k_fa_pv (the item's scores in global memory) and the fused decode form of k_fa_qk (one tile's scores
-// in LDS). Lane = (head row hr, group kk of the segment, cell quad); one wave per segment.
+// k_fa_pv (the item's scores in global memory). Lane = (head row hr, group kk of the segment, cell quad);
+// one wave per segment.
 template <int D, int VS>
 struct PvBlock {
     static constexpr uint32_t DV = D / VS;                        // values of the block (>= 64)
@@ -150,7 +73,7 @@ struct PvBlock {
     // the loads of one segment: scores, value scales and the value quants of a batch
     struct Loads {
         float4 sv;
-        uint32_t mv[4][BB / 2];
+        uint32_t mb[BB][2];                                       // block e: scales of cells 0, 1 | 2, 3
         int4 bq[2 * BB];
     };
     const FaArgs & a;
@@ -188,15 +111,12 @@ struct PvBlock {
         const uint32_t gi = 4u * seg + kk;
         const uint32_t u = u_first + 4u * min(gi, nu - 1u);        // clamped: loads stay in the item
         if (scores) load_scores(seg, L);
-        const uint16_t * vm = vmeta + ((size_t)u * 16u + 4u * quad) * nbk + (size_t)g * (D / 32u) + vb;
+        const uint16_t * vm = vmeta + ((size_t)u * nbk + (size_t)g * (D / 32u) + vb) * 16u + 4u * quad;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if constexpr (BB == 4) {
-                const uint2 m2 = *(const uint2 *)(vm + (size_t)i * nbk);
-                L.mv[i][0] = m2.x; L.mv[i][1] = m2.y;
-            } else {
-                L.mv[i][0] = *(const uint32_t *)(vm + (size_t)i * nbk);
-            }
+        for (uint32_t e = 0; e < BB; ++e) {                       // the 4 cells' scales of block e: 8 bytes
+            const uint2 m2 = *(const uint2 *)(vm + (size_t)e * 16u);
+            L.mb[e][0] = m2.x;
+            L.mb[e][1] = m2.y;
         }
         const uint32_t uB = u_first + 4u * min(4u * seg + (lane >> 4), nu - 1u);
         const uint8_t * vqB = vq + ((size_t)uB * a.E + (size_t)g * D + 32u * vb + (lane & 15u)) * 16u;
@@ -247,7 +167,7 @@ struct PvBlock {
                 const bool live = (fb(pz[i]) & 0x7FFFFFFFu) != 0u;
 #pragma unroll
                 for (uint32_t e = 0; e < BB; ++e) {
-                    const uint32_t dv = (L.mv[i][e >> 1] >> (16u * (e & 1u))) & 0xFFFFu;
+                    const uint32_t dv = (L.mb[e][i >> 1] >> (16u * (i & 1u))) & 0xFFFFu;
                     const float we = live ? pz[i] * h2f_fast(dv) : 0.0f;
                     const uint32_t f = f_field(we);
                     nfm |= (f == 255u ? 1u : 0u) << e;
@@ -349,250 +269,17 @@ __host__ __device__ inline uint32_t fa_qk_lds(uint32_t G, uint32_t D, bool rope)
     const uint32_t b = G * D + 4u * G * (D / 32u) + 16u * G;
     return rope ? ((b + 15u) & ~15u) + D + D / 8u : b;
 }
-// The fused decode tail's LDS after it (16-aligned): EXPK table, the tile's scores [4 heads][256],
-// segment results [4 waves][4 heads][D], row sums [4 waves][4 heads], digits [4 waves][BB][1024], two
-// flags and 4 chunk maxima.
-__host__ __device__ inline uint32_t fa_fuse_lds(uint32_t D) {
-    const uint32_t bb = D / 32u < 4u ? D / 32u : 4u;
-    return 256u + 4u * 4u * 256u + 4u * 4u * 4u * D + 4u * 16u + 4u * bb * 1024u + 32u;
-}
-
-// Data that blocks on other XCDs read after a counter moves only through accesses coherent at agent
-// scope (relaxed atomics: sc1 stores write through to the coherence point, sc1 loads bypass stale
-// L1 / L2 lines), so the counters need no L2-wide write-back or invalidation: a wave waits for its
-// coherent stores to complete (vm_wait) before the block's barrier and the counter increment, and a
-// reader issues its loads after it has seen the counter (program order behind the barrier).
-__device__ __forceinline__ void st_co(float * p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ void st_co4(float * p, float4 v) {     // 8-byte aligned p: two 8-byte stores
-    uint64_t * q = (uint64_t *)p;
-    __hip_atomic_store(q, ((uint64_t)fb(v.y) << 32) | fb(v.x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(q + 1, ((uint64_t)fb(v.w) << 32) | fb(v.z), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_co(const float * p) {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float4 ld_co4(const float * p) {
-    uint64_t * q = (uint64_t *)const_cast<float *>(p);
-    const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return make_float4(bf((uint32_t)lo), bf((uint32_t)(lo >> 32)), bf((uint32_t)hi), bf((uint32_t)(hi >> 32)));
-}
-__device__ __forceinline__ uint32_t ld_co_u(const uint32_t * p) {
-    return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_co_u(uint32_t * p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ void vm_wait() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);                           // vmcnt(0); expcnt and lgkmcnt untouched
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-// Counter increment by thread 0 after every wave's vm_wait and a barrier; the previous value.
-__device__ __forceinline__ uint32_t count_up(uint32_t * ctr) {
-    return __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The fused decode form (T == 1, G <= 4, D <= 128, a plan's work list): after its scores and tile
-// maxima, the block (item, tile tt, KV head g) goes on with P.V. Segment s of a channel is the 4 of
-// its groups in tile s of the item (tiles are 16 groups), so the block's 4 waves take the segments
-// in its tile of channels 0..3.
-//   1. The block has published its maxima as MAXT keys (never 0: a NaN keys to ~0, every other value
-//      to at least 0x007FFFFF) in slots that are 0 until then; its first wave reads the item's slots
-//      until none is 0 (blocks of one item are consecutive in dispatch order, so they all run: the
-//      wait is bounded all the same, and an expired wait raises *bad = 2). What it read gives the
-//      chunk maxima.
-//   2. Each wave: the chunk maximum of its heads, the segment (PvBlock, scores from LDS), its results
-//      to seg_o / seg_l.
-//   3. The last tile block of the item (a counter, no wait) chains the segments of each channel in
-//      order into the item's channel partials (as k_fa_pv) and records the chunk maxima; the last
-//      item of the KV head (a counter) merges the items in order and normalizes (as k_fa_merge), then
-//      clears the counters for the next launch.
-constexpr uint32_t kFuseSegMax = 8;                              // segments per channel (NCG <= 128)
-constexpr uint32_t kFuseItems = 4;                               // items loaded per round of the merge
-
-template <int D>
-__device__ __forceinline__ void fa_fused_tail(const FaArgs & a, const FaPlan & p, const FaItem & it, uint32_t item,
-                                              uint32_t tt, uint32_t g, uint8_t * ft, const PvBlock<D, 1> & pb,
-                                              typename PvBlock<D, 1>::Loads & L) {
-    using PB = PvBlock<D, 1>;
-    constexpr uint32_t BB = PB::BB, D4 = D / 4u;
-    const uint32_t G = a.G, nh = a.n_head, nkv = a.n_head_kv, ni = p.n_items;
-    const uint32_t * s_t64 = (const uint32_t *)ft;
-    const float * s_S = (const float *)(ft + 256);
-    float * s_c = (float *)(ft + 256 + 4096);                     // [wave][4 heads][D]
-    float * s_l = s_c + 16u * D;                                  // [wave][4 heads]
-    uint8_t * s_dg = (uint8_t *)(s_l + 16);                       // [wave][BB][1024]
-    uint32_t * s_flag = (uint32_t *)(s_dg + 4u * BB * 1024u);
-    uint32_t * segdone = a.sync + (size_t)item * nkv + g;
-    uint32_t * done = a.sync + (size_t)ni * nkv + g;
-    uint32_t * s_mk = s_flag + 2;                                 // chunk maxima (keys) of the G heads
-    const uint32_t lane = __lane_id(), c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave = channel
-    const uint32_t hrow = min(lane >> 4, G - 1u), h = g * G + hrow;
-    const bool has = tt < pb.nseg;                                // wave-uniform (the V rows are loading)
-    (void)s_S;
-
-    // 1. wait for the item's tile maxima; the chunk maxima: MAXOUT of the floor and the tile maxima
-    const uint32_t floor_key = maxt_key_f(bf(kMFloor));
-    if (c == 0u) {                                                // wave 0, every lane
-        const uint32_t nk = it.ntiles * G;                        // lane l < nk: tile l / G, head l % G
-        const uint32_t * kp = a.tkeys + ((size_t)g * p.n_items * p.maxtiles + it.tile0) * 4u + (lane / G) * 4u + lane % G;
-        uint32_t v = 1u, spins = 0;
-        for (;;) {
-            v = lane < nk ? ld_co_u(kp) : 1u;
-            if (__all(v != 0u)) break;
-            if (++spins >= a.spin_max) {
-                if (lane == 0u && a.bad != nullptr)
-                    __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < 4u; ++i) {
-            const uint32_t k = wave_max_u(lane < nk && lane % G == i ? v : floor_key);
-            if (lane == 0u && i < G) s_mk[i] = k;
-        }
-    }
-    __syncthreads();
-    const float m = maxt_unkey(s_mk[hrow]);
-
-    // 2. the segment and its results
-    const size_t tile = (size_t)it.tile0 + tt;
-    if (has) {
-        pb.load_scores(tt, L);
-        pb.segment(tt, c, L, m, s_t64, s_c, s_l, s_dg + (size_t)c * (BB * 1024u));
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        for (uint32_t idx = lane; idx < G * D4; idx += 64u) {
-            const uint32_t r = idx / D4, v4 = idx % D4;
-            st_co4(a.seg_o + ((tile * 4u + c) * nh + g * G + r) * D + 4u * v4, *(const float4 *)(s_c + (c * 4u + r) * D + 4u * v4));
-        }
-        if (lane < G) st_co(a.seg_l + (tile * 4u + c) * nh + g * G + lane, s_l[c * 4u + lane]);
-    }
-    vm_wait();
-    __syncthreads();
-    if (threadIdx.x == 0u) s_flag[0] = count_up(segdone) == it.ntiles - 1u;
-    __syncthreads();
-    if (s_flag[0] == 0u) return;                                  // block-uniform
-
-    // 3a. the item's last tile: each channel's segment chain in segment order (AT 6.4 O, 6.5 l), all
-    // of its loads first; and the chunk maxima of the KV head's heads
-    if (c == 0u && (lane & 15u) == 0u && (lane >> 4) < G) st_co(a.m_item + (size_t)item * nh + h, m);
-    constexpr uint32_t kPer = 2;                                  // 4 G D / 4 <= 512 entries: 2 per thread
-    const uint32_t ne = 4u * G * D4;
-    float4 x[kPer][kFuseSegMax];
-    float xl[kPer][kFuseSegMax];
-    uint32_t nsg[kPer], ent[kPer];
-#pragma unroll
-    for (uint32_t e = 0; e < kPer; ++e) {                         // every load first
-        ent[e] = threadIdx.x + 256u * e;
-        const uint32_t idx = min(ent[e], ne - 1u);
-        const uint32_t cc = idx / (G * D4), r = (idx / D4) % G, v4 = idx % D4, hh = g * G + r;
-        const uint32_t u_first = it.u0 + ((cc + 4u - (it.u0 & 3u)) & 3u), u_end = it.u0 + it.n;
-        const uint32_t nu = u_first < u_end ? (u_end - 1u - u_first) / 4u + 1u : 0u;
-        nsg[e] = (nu + 3u) / 4u;
-#pragma unroll
-        for (uint32_t sg = 0; sg < kFuseSegMax; ++sg) {
-            const size_t row = ((size_t)(it.tile0 + min(sg, max(nsg[e], 1u) - 1u)) * 4u + cc) * nh + hh;
-            x[e][sg] = ld_co4(a.seg_o + row * D + 4u * v4);
-            xl[e][sg] = ld_co(a.seg_l + row);
-        }
-    }
-#pragma unroll
-    for (uint32_t e = 0; e < kPer; ++e) {
-        if (ent[e] >= ne) continue;
-        const uint32_t idx = ent[e];
-        const uint32_t cc = idx / (G * D4), r = (idx / D4) % G, v4 = idx % D4, hh = g * G + r;
-        float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float l = 0.0f;
-#pragma unroll
-        for (uint32_t sg = 0; sg < kFuseSegMax; ++sg) {
-            if (sg < nsg[e]) {
-                O.x = sadd_n(O.x, x[e][sg].x);
-                O.y = sadd_n(O.y, x[e][sg].y);
-                O.z = sadd_n(O.z, x[e][sg].z);
-                O.w = sadd_n(O.w, x[e][sg].w);
-                l = sadd_n(l, xl[e][sg]);
-            }
-        }
-        const size_t slot = ((size_t)item * 4u + cc) * nh + hh;
-        st_co4(a.OP + slot * D + 4u * v4, O);
-        if (v4 == 0u) st_co(a.LP + slot, l);
-    }
-    vm_wait();
-    __syncthreads();
-    if (threadIdx.x == 0u) s_flag[1] = count_up(done) == ni - 1u;
-    __syncthreads();
-    if (s_flag[1] == 0u) return;
-
-    // 3b. the KV head's last item: CTREE of the channels, the online merge in item (chunk) order and
-    // ANORM (AT 5.6, 5.7), as k_fa_merge; the items' loads a round of kFuseItems at a time
-    for (uint32_t idx = threadIdx.x; idx < G * D4; idx += blockDim.x) {
-        const uint32_t r = idx / D4, v4 = idx % D4, hh = g * G + r;
-        float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float l = 0.0f, mr = 0.0f;
-        for (uint32_t k0 = 0; k0 < ni; k0 += kFuseItems) {
-            float4 op[kFuseItems][4];
-            float lp[kFuseItems][4], mk[kFuseItems];
-#pragma unroll
-            for (uint32_t k = 0; k < kFuseItems; ++k) {
-                const uint32_t kk = min(k0 + k, ni - 1u);
-                mk[k] = ld_co(a.m_item + (size_t)kk * nh + hh);
-#pragma unroll
-                for (uint32_t cc = 0; cc < 4u; ++cc) {
-                    const size_t slot = ((size_t)kk * 4u + cc) * nh + hh;
-                    op[k][cc] = ld_co4(a.OP + slot * D + 4u * v4);
-                    lp[k][cc] = ld_co(a.LP + slot);
-                }
-            }
-#pragma unroll
-            for (uint32_t k = 0; k < kFuseItems; ++k) {
-                if (k0 + k >= ni) break;
-                const float4 ok = make_float4(ctree4(op[k][0].x, op[k][1].x, op[k][2].x, op[k][3].x),
-                                              ctree4(op[k][0].y, op[k][1].y, op[k][2].y, op[k][3].y),
-                                              ctree4(op[k][0].z, op[k][1].z, op[k][2].z, op[k][3].z),
-                                              ctree4(op[k][0].w, op[k][1].w, op[k][2].w, op[k][3].w));
-                const float lk = ctree4(lp[k][0], lp[k][1], lp[k][2], lp[k][3]);
-                if (k0 + k == 0u) {
-                    O = ok;
-                    l = lk;
-                    mr = mk[k];
-                } else {
-                    const float mrun = maxt(mr, mk[k]);
-                    const float fa = expk(smul_n(ssub_n(mr, mrun), a.scale), a.ex, s_t64);
-                    const float fbv = expk(smul_n(ssub_n(mk[k], mrun), a.scale), a.ex, s_t64);
-                    l = sadd_n(smul_n(l, fa), smul_n(lk, fbv));
-                    O.x = sadd_n(smul_n(O.x, fa), smul_n(ok.x, fbv));
-                    O.y = sadd_n(smul_n(O.y, fa), smul_n(ok.y, fbv));
-                    O.z = sadd_n(smul_n(O.z, fa), smul_n(ok.z, fbv));
-                    O.w = sadd_n(smul_n(O.w, fa), smul_n(ok.w, fbv));
-                    mr = mrun;
-                }
-            }
-        }
-        const float rl = srcp(maxt(l, bf(kLFloor)));
-        *(float4 *)(a.out + (size_t)hh * D + 4u * v4) = make_float4(smul_n(O.x, rl), smul_n(O.y, rl), smul_n(O.z, rl), smul_n(O.w, rl));
-    }
-    // every block of the KV head is past its waits: clear its counters for the next launch
-    for (uint32_t k = threadIdx.x; k < ni; k += blockDim.x) a.sync[(size_t)k * nkv + g] = 0u;
-    for (uint32_t t = threadIdx.x; t < 4u * ni * p.maxtiles; t += blockDim.x)
-        a.tkeys[(size_t)g * 4u * ni * p.maxtiles + t] = 0u;
-    if (threadIdx.x == 0u) *done = 0u;
-}
-
 // ROPE (T == 1, D <= 128, (G + 2) D <= 1024): the block also rotates the query heads (rope4, angles
 // per lane by rope_cs_lane) before their QACT, rotates and QACTs the token's k row of head g and
 // QACTs its v row (threads after the query slots, A32 as SET_ROWS_KV); the thread of the new cell
 // scores with that fresh k row, and the first block of each KV head stores the k and v rows in the
 // caches -- ROPE, SET_ROWS_KV and the scores in one launch.
-// FUSE: the decode form that goes on with P.V and the merge (fa_fused_tail).
-template <int D, bool INL, bool ROPE, bool FUSE = false>
+template <int D, bool INL, bool ROPE>
 __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr uint32_t NBD = D / 32u;                             // blocks per head
     constexpr bool KREG = D <= 128;                                // K row of the cell kept in registers
     static_assert(!ROPE || KREG, "the fused ROPE keeps the K rows in registers");
-    static_assert(!FUSE || (KREG && !INL), "the fused decode form: D <= 128, a plan's work list");
     const uint32_t tt = blockIdx.x % p.maxtiles;
     const FaItem it = fa_item<INL>(a, p, blockIdx.x / p.maxtiles);
     if (tt >= it.ntiles) return;                                  // the item has fewer tiles (block-uniform)
@@ -609,8 +296,6 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
         if (a.rtab == nullptr) pos = *a.pos;
         cell64 = *a.cell;
     }
-    uint8_t * ft = lds + ((fa_qk_lds(G, D, ROPE) + 15u) & ~15u);  // FUSE: the tail's LDS
-    const uint32_t t64v = FUSE ? a.ex.t64[threadIdx.x & 63u] : 0u;
 
     const uint32_t n16 = 16u * it.n, j = 256u * tt + threadIdx.x;
     const bool in = j < n16;
@@ -619,7 +304,7 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
     const uint32_t u = min(cell >> 4, ng - 1u), rr = cell & 15u;  // clamped: loads stay inside the plane
     const bool vis = in && (it.general || (j >= it.c_lo && j < it.c_hi));
     const uint32_t E = a.E, nbk = E / 32u;
-    const uint16_t * kmeta = (const uint16_t *)a.kc.base + ((size_t)u * 16u + rr) * nbk + (size_t)g * NBD;
+    const uint16_t * kmeta = (const uint16_t *)a.kc.base + ((size_t)u * nbk + (size_t)g * NBD) * 16u + rr;
     const uint8_t * kq = a.kc.base + a.kc.quant_off + (size_t)u * 16u * E + (size_t)rr * 16u;
     const uint32_t ci0 = g * D / 16u;                             // first 16-byte chunk of the head
 
@@ -649,17 +334,12 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
     int4 kr[KREG ? 2 * NBD : 1];
     uint32_t km[NBD];
 #pragma unroll
-    for (uint32_t kb = 0; kb < NBD; ++kb) km[kb] = kmeta[kb];
+    for (uint32_t kb = 0; kb < NBD; ++kb) km[kb] = kmeta[(size_t)kb * 16u];
     if constexpr (KREG) {
 #pragma unroll
         for (uint32_t c = 0; c < 2 * NBD; ++c) kr[c] = *(const int4 *)(kq + (size_t)(ci0 + c) * 256u);
     }
-    // FUSE: the P.V segments of the block (wave = channel); their V rows load after the QACT below
-    const PvBlock<D, 1> pb(a, it, (uint32_t)__builtin_amdgcn_readfirstlane(wave), g, 0u, 0u,
-                           (const float *)(ft + 256) + (size_t)min((uint32_t)lane >> 4, G - 1u) * 256u, 256u * tt);
-    typename PvBlock<D, 1>::Loads pl;
     __builtin_amdgcn_sched_barrier(0);
-    bool holds = false;                                           // FUSE + ROPE: the tile holds the new cell's group
 
     auto qact_slot = [&](uint32_t slot, const float4 v) {
         float Dq;
@@ -692,27 +372,24 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
             if ((lane & 7) == 0) s_kd[kslot >> 3] = Dq;
         }
         const bool cell_ok = cell64 >= 0 && cell64 < (int64_t)a.kc.kv_size && cell64 < (int64_t)a.vc.kv_size;
-        // FUSE: a tile holding the new cell's group reads its v row, so its block stores it too
-        const uint32_t ug = (uint32_t)((uint64_t)cell64 >> 4), ut = it.u0 + 16u * tt;
-        holds = FUSE && cell_ok && ug >= ut && ug < min(ut + 16u, it.u0 + it.n);
-        if (blockIdx.x == 0u || holds) {                          // the caches' copy of the new rows
-            if (cell_ok && (is_k || is_v))
-                kv_store_unit(is_k ? a.kc : a.vc, is_k ? 0u : 1u, (uint32_t)cell64, g * D + 4u * (is_k ? kslot : vslot), qq,
-                              Dq, (lane & 7) == 0);
-            if (!cell_ok && blockIdx.x == 0u && threadIdx.x == 0u && g == 0u && a.bad != nullptr) *a.bad = 1;
+        if (blockIdx.x == 0u) {                                   // the caches' copy of the new rows
+            if (cell_ok && (is_k || is_v)) {
+                KvArgs kv;                                        // per-lane choice of the plane, field by field
+                kv.base = is_k ? a.kc.base : a.vc.base;
+                kv.quant_off = is_k ? a.kc.quant_off : a.vc.quant_off;
+                kv.E = a.kc.E;
+                kv.kv_size = is_k ? a.kc.kv_size : a.vc.kv_size;
+                kv_store_unit(kv, is_k ? 0u : 1u, (uint32_t)cell64, g * D + 4u * (is_k ? kslot : vslot), qq, Dq,
+                              (lane & 7) == 0);
+            }
+            if (!cell_ok && threadIdx.x == 0u && g == 0u && a.bad != nullptr) *a.bad = 1;
         }
     } else {
         qact_slot(threadIdx.x, qv0);
         for (uint32_t s0 = blockDim.x; s0 < nslot; s0 += blockDim.x)   // G D > 1024 only
             qact_slot(s0 + threadIdx.x, *(const float4 *)(qrow + 4u * min(s0 + threadIdx.x, nslot - 1u)));
     }
-    if constexpr (FUSE) {
-        if (threadIdx.x < 64u) ((uint32_t *)ft)[threadIdx.x] = t64v;
-    }
     lds_barrier();                                                // the K rows stay in flight
-    if constexpr (FUSE) {                                         // the V rows (the new v row is stored now)
-        if (tt < pb.nseg) pb.loads(tt, pb.vb0, pl, false);
-    }
     if constexpr (ROPE) {                                         // the new cell scores with the fresh k row
         if ((int64_t)cell == cell64 && in) {
 #pragma unroll
@@ -763,10 +440,7 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
                 s = fb(m) == kNegInf ? bf(kNegInf) : sadd(s, m);
             }
         }
-        if (in) {
-            if constexpr (FUSE) ((float *)(ft + 256))[i * 256u + threadIdx.x] = s;
-            else S[(size_t)h * n16 + j] = s;
-        }
+        if (in) S[(size_t)h * n16 + j] = s;
         const uint32_t mk = wave_max_u(in ? maxt_key_f(s) : maxt_key_f(bf(kMFloor)));
         if (lane == 0) s_red[wave * G + i] = mk;
     }
@@ -774,10 +448,8 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
     for (uint32_t i = threadIdx.x; i < G; i += blockDim.x) {
         uint32_t m = s_red[i];
         for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = umax_u(m, s_red[w * G + i]);
-        if constexpr (FUSE) st_co_u(a.tkeys + ((size_t)g * p.n_items * p.maxtiles + it.tile0 + tt) * 4u + i, m);
-        else a.Mpart[(size_t)(it.tile0 + tt) * a.n_head + g * G + i] = maxt_unkey(m);
+        a.Mpart[(size_t)(it.tile0 + tt) * a.n_head + g * G + i] = maxt_unkey(m);
     }
-    if constexpr (FUSE) fa_fused_tail<D>(a, p, it, blockIdx.x / p.maxtiles, tt, g, ft, pb, pl);
 }
 
 template <int D, bool INL, int VS>
@@ -927,18 +599,6 @@ static int launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, u
     const bool rope = a.cell != nullptr;                          // ROPE + SET_ROWS_KV fused (host-checked shape)
     const size_t lds_qk = tsr::fa_qk_lds(a.G, a.D, rope);
     const dim3 gqk(p.n_items * p.maxtiles, a.n_head_kv);
-    if (!INL && a.sync != nullptr && T == 1u && a.G <= 4u && (a.D == 64u || a.D == 128u)) {
-        // decode over a plan's work list: scores, P.V and the merge in one launch
-        const size_t lds = ((lds_qk + 15u) & ~(size_t)15u) + tsr::fa_fuse_lds(a.D);
-        switch (a.D * 2u + (rope ? 1u : 0u)) {
-            case 128: hipLaunchKernelGGL((tsr::k_fa_qk<64, false, false, true>), gqk, dim3(256), lds, s, a, p); break;
-            case 129: hipLaunchKernelGGL((tsr::k_fa_qk<64, false, true, true>), gqk, dim3(256), lds, s, a, p); break;
-            case 256: hipLaunchKernelGGL((tsr::k_fa_qk<128, false, false, true>), gqk, dim3(256), lds, s, a, p); break;
-            case 257: hipLaunchKernelGGL((tsr::k_fa_qk<128, false, true, true>), gqk, dim3(256), lds, s, a, p); break;
-            default: return -2;
-        }
-        return hipGetLastError() == hipSuccess ? 0 : -4;
-    }
     if (rope) {
         switch (a.D) {
             case 64: hipLaunchKernelGGL((tsr::k_fa_qk<64, INL, true>), gqk, dim3(256), lds_qk, s, a, p); break;

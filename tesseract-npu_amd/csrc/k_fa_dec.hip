@@ -1,0 +1,572 @@
+// k_fa_dec.hip -- the one-launch decode FLASH_ATTN_EXT (one query row, a plan's device work list),
+// bit-exact to the reference's composite flash attention (tsr_ref_fa, sw/sim/tsr_ref_at.c:774-860) in
+// its fixed configuration C = 4 channels, PCAP = 9344, T_MAX = 1.
+//
+// Work unit: one segment of ATTPV (AT 6.4) = 4 groups of one channel (groups u = c mod 4) of one chunk
+// item, i.e. 64 cells, for the G <= 4 query heads of one KV head g. Segment s of channel c is the 4 of
+// its groups in tile s (16 groups) of the item. One workgroup of 4 waves per segment:
+//   scores     wave b = K block b (32 values) of the 64 cells: the block's term for every query head;
+//              then wave h = head h: the tree16 of the 64 scores (SEG, AT 6.2) and their MAXT
+//   publish    the segment's 4 maxima as MAXT keys in a slot tagged with the launch's epoch
+//   wait       wave 0 reads the item's slots until every segment has published (bounded: an expired
+//              wait raises *bad = 2): the chunk maxima, MAXOUT with the floor (AT 6.3)
+//   EXP        wave h = head h: p = EXPK((s - m) scale) of its 64 cells and the segment's LSUM (AT 6.5)
+//   P.V        wave b = value block b: the block-float weights of its 32 values (E_S over the 64-value
+//              slice: both blocks of the slice), their base-256 digits and two int8 matrix-core
+//              products for the 4 heads (16 values each)
+//   results    the segment's O (G x D) and l (G) to the plan, agent-coherent, then its flag
+//   reduce     G x D/64 reducer workgroups per KV head, after every segment in dispatch order: each
+//              waits for every flag, then chains, in order, the segments of every channel of every item
+//              for its 64 values of one head, CTREE over the channels, merges the items in chunk order
+//              (AMERGE) and normalizes (ANORM); no atomic operation, nothing to clear (tags)
+// The chunk maximum needs every score of the chunk before any P.V of it (p depends on it bit for bit),
+// and the segment chains need every segment: two exchanges between workgroups, the least the reference's
+// order allows. Segments of one item are consecutive in dispatch order, so every segment an item's
+// wait needs has been dispatched before or is dispatched next (no wait can starve).
+//
+// ROPE (the layer's ROPE + SET_ROWS_KV folded in): q is then the token's unrotated Q|K|V row. Every
+// workgroup rotates and quantizes its KV head's query heads, the new k row (and quantizes the new v
+// row) into LDS; the workgroup of the new cell's segment scores and weighs the new cell from those LDS
+// rows (the caches may not hold them yet), and the workgroup of the item's first segment stores them
+// into the caches (SET_ROWS_KV, sw/ctrl/ref/kv_ref.cpp:20-45).
+#include "expk.hpp"
+#include "fa_common.hpp"
+#include "glue.hpp"
+#include "kernels.hpp"
+#include "kvstore.hpp"
+#include "qact.hpp"
+
+namespace tsr {
+
+// A buffer resource over [p, p + bytes) (gfx9 descriptor word 3): loads beyond it return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t fa_rsrc(const void * p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+constexpr int kSc1 = 16;                                           // cache policy: agent-coherent (sc1)
+typedef unsigned v4u_fa __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ld_co16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1));
+}
+__device__ __forceinline__ void st_co16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_fa, v), r, off, 0, kSc1);
+}
+
+// Byte r (0..15) of a 16-byte value replaced by b (selects only: the value stays in registers).
+__device__ __forceinline__ int4 put_byte(int4 v, uint32_t r, uint32_t b) {
+    const uint32_t sh = 8u * (r & 3u), m = ~(0xFFu << sh), x = (b & 0xFFu) << sh, w = r >> 2;
+    v.x = w == 0u ? (int)(((uint32_t)v.x & m) | x) : v.x;
+    v.y = w == 1u ? (int)(((uint32_t)v.y & m) | x) : v.y;
+    v.z = w == 2u ? (int)(((uint32_t)v.z & m) | x) : v.z;
+    v.w = w == 3u ? (int)(((uint32_t)v.w & m) | x) : v.w;
+    return v;
+}
+
+// Segments of channel c in an item: its groups u = c (mod 4) in [u0, u0 + n), 4 per segment.
+struct FaSeg {
+    uint32_t u_first, nu, nseg;
+    __device__ __forceinline__ FaSeg(const FaItem & it, uint32_t c) {
+        u_first = it.u0 + ((c + 4u - (it.u0 & 3u)) & 3u);
+        const uint32_t u_end = it.u0 + it.n;
+        nu = u_first < u_end ? (u_end - 1u - u_first) / 4u + 1u : 0u;
+        nseg = (nu + 3u) / 4u;
+    }
+};
+
+// LDS of one workgroup (bytes): table 256 | q quants 512 | q scales 64 | new k quants 128, scales 16 |
+// new v quants 128, scales 16 | terms [4 heads][4 blocks][64] f32 4096 | scores [4][64] 1024 |
+// p [4][64] 1024 | digits [4 waves][1024] | keys 16 | maxima 16 | flag 16.
+constexpr uint32_t kDecLds = 256 + 512 + 64 + 128 + 16 + 128 + 16 + 4096 + 1024 + 1024 + 4096 + 48;
+
+template <int D, bool ROPE>
+__global__ __launch_bounds__(256, 6) void k_fa_dec(FaDecArgs a) {
+    constexpr uint32_t NBD = D / 32u;                             // K / V blocks of a head
+    __shared__ __align__(16) uint8_t lds[kDecLds];
+    uint32_t * s_t64 = (uint32_t *)lds;
+    int8_t * s_q = (int8_t *)(lds + 256);                         // [G][D]
+    float * s_dx = (float *)(lds + 768);                          // [G][NBD]
+    int8_t * s_kq = (int8_t *)(lds + 832);                        // new k row of head g [D], scales [NBD]
+    float * s_kd = (float *)(lds + 960);
+    int8_t * s_vq = (int8_t *)(lds + 976);                        // new v row [D], scales [NBD]
+    float * s_vd = (float *)(lds + 1104);
+    float * s_t = (float *)(lds + 1120);                          // [h][b][64] block terms
+    float * s_S = (float *)(lds + 5216);                          // [h][64] scores
+    float * s_P = (float *)(lds + 6240);                          // [h][64] p
+    uint8_t * s_dg = lds + 7264;                                  // [wave][1024] digits
+    uint32_t * s_key = (uint32_t *)(lds + 11360);                 // [4] segment maxima (keys)
+    float * s_m = (float *)(lds + 11376);                         // [4] chunk maxima
+
+    const uint32_t per_item = 4u * a.maxtiles;
+    if (blockIdx.x >= a.n_items * per_item) {                     // the KV head's reducers
+        fa_dec_reduce<D>(a, lds, blockIdx.x - a.n_items * per_item);
+        return;
+    }
+    const uint32_t item = blockIdx.x / per_item, tt = (blockIdx.x / 4u) % a.maxtiles, c = blockIdx.x & 3u;
+    const uint32_t g = blockIdx.y, G = a.G, nh = a.n_head, E = a.E, nbk = E / 32u;
+    const FaItem it = a.items[item];
+    const FaSeg sg(it, c);
+    if (tt >= sg.nseg) return;                                    // no such segment (block-uniform)
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t ng = (a.kc.kv_size + 15u) / 16u;
+    // the segment's groups (clamped: loads of a missing group stay inside the item)
+    uint32_t ug[4];
+    bool gv[4];
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; ++k) {
+        const uint32_t gi = 4u * tt + k;
+        gv[k] = gi < sg.nu;
+        ug[k] = min(sg.u_first + 4u * min(gi, sg.nu - 1u), ng - 1u);
+    }
+    int64_t cell_new = -1;
+    int32_t pos = 0;
+    if constexpr (ROPE) {
+        cell_new = *a.cell;
+        if (a.rtab == nullptr) pos = *a.pos;
+    }
+    const uint32_t t64v = a.ex.t64[lane];
+    // the launch's tag: reducer 0's epoch of the KV head + 1 (the epochs advance at the end of a launch)
+    const uint32_t tag = a.ep[(size_t)g * G * (D / 64u)] + 1u;
+    // ROPE angles of the token (table): first, so that waiting for them is not waiting for K and V
+    float2 cs_tab = make_float2(0.0f, 0.0f);
+    if constexpr (ROPE) {
+        if (a.rtab != nullptr) cs_tab = *(const float2 *)(a.rtab + 2u * min(lane, a.n_dims / 2u - 1u));
+    }
+
+    // ---- loads: the query values, the K rows of the thread's (cell, block), the V of its wave ----
+    const uint32_t nslot = G * D / 4u;                            // 8 lanes per 32-value block
+    const float * qrow = a.q + (size_t)g * G * D;
+    const uint32_t kslot = tid - nslot, vslot = kslot - D / 4u;
+    const bool is_k = ROPE && tid >= nslot && kslot < D / 4u;
+    const bool is_v = ROPE && !is_k && tid >= nslot && vslot < D / 4u;
+    const float * src = a.q + (size_t)nh * D + (size_t)g * D + (is_v ? E + 4u * vslot : 4u * (is_k ? kslot : 0u));
+    const uint32_t jq = 4u * min(tid, nslot - 1u);
+    const float * qsrc = (ROPE && tid >= nslot) ? src : qrow + jq;
+    const float4 qv0 = *(const float4 *)qsrc;
+    const uint32_t half = a.n_dims / 2u;
+    const uint32_t jh0 = tid < nslot ? jq % D : (is_k ? 4u * kslot : D);
+    // ROPE NEOX: the 4 values half a rotation away (their own address otherwise: no load waits on a branch)
+    const int32_t dj = (ROPE && a.neox && jh0 < a.n_dims) ? (jh0 < half ? (int32_t)half : -(int32_t)half) : 0;
+    const float4 qpart = ROPE ? *(const float4 *)(qsrc + dj) : qv0;
+    __builtin_amdgcn_sched_barrier(0);
+    // K: thread = (cell j, block b = wave)
+    const uint32_t j = lane, kkj = j >> 4, rrj = j & 15u;
+    const uint32_t bk = wave < NBD ? wave : 0u;
+    const uint8_t * kbase = a.kc.base + a.kc.quant_off + ((size_t)ug[kkj] * (E / 16u) + (size_t)g * (D / 16u) + 2u * bk) * 256u +
+                            (size_t)rrj * 16u;
+    int4 kr0 = *(const int4 *)kbase, kr1 = *(const int4 *)(kbase + 256u);
+    uint32_t km = ((const uint16_t *)a.kc.base)[((size_t)ug[kkj] * nbk + (size_t)g * NBD + bk) * 16u + rrj];
+    // V: wave b = value block b; lane (head row hr, group kk, cell quad) for the weights, lane
+    // (value l % 16, group l / 16) for the matrix-core operand
+    const uint32_t hr = lane >> 4, kk = (lane >> 2) & 3u, quad = lane & 3u;
+    const uint32_t bv = wave < NBD ? wave : 0u, b0 = bv & ~1u;    // the 64-value slice: blocks b0, b0 + 1
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- QACT of the query heads (ROPE: rotated first), the new k and v rows ----
+    if constexpr (ROPE) {
+        float c_l, s_l;
+        if (a.rtab != nullptr) {
+            c_l = cs_tab.x;
+            s_l = cs_tab.y;
+        } else {
+            rope_cs_lane(pos, half, a.ts, a.m, lane, &c_l, &s_l);
+        }
+        const float4 rot = rope4(qv0, qpart, jh0, a.n_dims, a.neox != 0u, c_l, s_l);   // every lane (bpermute)
+        const float4 r = is_v ? qv0 : rot;
+        float Dq;
+        const uint32_t qq = qact_a32_lane(r, &Dq);                // every lane (8-lane groups)
+        if (tid < nslot) {
+            *(uint32_t *)(s_q + 4u * tid) = qq;
+            if ((lane & 7u) == 0u) s_dx[tid >> 3] = Dq;
+        } else if (is_k) {
+            *(uint32_t *)(s_kq + 4u * kslot) = qq;
+            if ((lane & 7u) == 0u) s_kd[kslot >> 3] = Dq;
+        } else if (is_v) {
+            *(uint32_t *)(s_vq + 4u * vslot) = qq;
+            if ((lane & 7u) == 0u) s_vd[vslot >> 3] = Dq;
+        }
+        const bool cell_ok = cell_new >= 0 && cell_new < (int64_t)a.kc.kv_size && cell_new < (int64_t)a.vc.kv_size;
+        if (item == 0u && tt == 0u && c == (it.u0 & 3u)) {       // the caches' copy of the new rows
+            if (cell_ok && (is_k || is_v))
+            {
+                KvArgs kv;                                        // per-lane choice of the plane, field by field
+                kv.base = is_k ? a.kc.base : a.vc.base;
+                kv.quant_off = is_k ? a.kc.quant_off : a.vc.quant_off;
+                kv.E = a.kc.E;
+                kv.kv_size = is_k ? a.kc.kv_size : a.vc.kv_size;
+                kv_store_unit(kv, is_k ? 0u : 1u, (uint32_t)cell_new, g * D + 4u * (is_k ? kslot : vslot), qq, Dq,
+                              (lane & 7u) == 0u);
+            }
+            if (!cell_ok && tid == 0u && g == 0u && a.bad != nullptr) *a.bad = 1;
+        }
+    } else {
+        float Dq;
+        const uint32_t qq = qact_a32_lane(qv0, &Dq);
+        if (tid < nslot) {
+            *(uint32_t *)(s_q + 4u * tid) = qq;
+            if ((lane & 7u) == 0u) s_dx[tid >> 3] = Dq;
+        }
+    }
+    if (tid < 64u) s_t64[tid] = t64v;
+    lds_barrier();                                                // K and V stay in flight
+
+    // ---- scores: the block terms of (cell j, block b) for every head ----
+    const uint32_t u_j = ug[kkj];
+    const int64_t cell_j = 16 * (int64_t)u_j + rrj;
+    if (wave < NBD) {
+        if (ROPE && cell_j == cell_new) {                         // the new cell: the fresh k row
+            kr0 = *(const int4 *)(s_kq + 32u * wave);
+            kr1 = *(const int4 *)(s_kq + 32u * wave + 16u);
+            km = f2h_exact(s_kd[wave]);
+        }
+        const float dk = h2f_fast(km);
+        for (uint32_t h = 0; h < G; ++h) {
+            const int4 * xq = (const int4 *)(s_q + (size_t)h * D + 32u * wave);
+            const int4 x0 = xq[0], x1 = xq[1];
+            int is = dot4(kr0.x, x0.x, 0);
+            is = dot4(kr0.y, x0.y, is);
+            is = dot4(kr0.z, x0.z, is);
+            is = dot4(kr0.w, x0.w, is);
+            is = dot4(kr1.x, x1.x, is);
+            is = dot4(kr1.y, x1.y, is);
+            is = dot4(kr1.z, x1.z, is);
+            is = dot4(kr1.w, x1.w, is);
+            // SEG (AT 6.2): p_k = +0 + (dK Dx) f32(isum); |terms| >= 2^-48 or 0 (fp16 scales)
+            const float t = (dk * s_dx[h * NBD + wave]) * (float)is;
+            s_t[(h * 4u + wave) * 64u + j] = 0.0f + t;
+        }
+    }
+    // the V rows load now: K first across the whole launch, V during the exchange of the maxima
+    // the scales of the lane's 4 cells in the slice's two blocks (8 contiguous bytes each)
+    uint2 mvb[2];
+#pragma unroll
+    for (uint32_t e = 0; e < 2u; ++e)
+        mvb[e] = *(const uint2 *)((const uint16_t *)a.vc.base + ((size_t)ug[kk] * nbk + (size_t)g * NBD + b0 + e) * 16u +
+                                  4u * quad);
+    const uint8_t * vq = a.vc.base + a.vc.quant_off + ((size_t)ug[lane >> 4] * E + (size_t)g * D + 32u * bv + (lane & 15u)) * 16u;
+    int4 bq0 = *(const int4 *)vq, bq1 = *(const int4 *)(vq + 256u);
+    __syncthreads();
+    // wave h = head h: tree16 over the block terms, the mask, the segment maximum
+    const uint32_t floor_key = maxt_key_f(bf(kMFloor));
+    const uint32_t jc = 16u * (u_j - it.u0) + rrj;                // cell index in the chunk
+    const bool in = gv[kkj];
+    const bool vis = in && (it.general || (jc >= it.c_lo && jc < it.c_hi));
+    if (wave < G) {
+        const uint32_t h = wave;
+        float s = bf(kNegInf);
+        if (vis) {
+            float p[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) p[k] = (uint32_t)k < NBD ? s_t[(h * 4u + (uint32_t)k) * 64u + j] : 0.0f;
+#pragma unroll
+            for (int w = 16; w > 1; w >>= 1)
+#pragma unroll
+                for (int k = 0; k < w / 2; ++k) p[k] = p[2 * k] + p[2 * k + 1];
+            s = canon(p[0]);
+            if (it.general) {
+                const float mval = a.mask[(size_t)it.t * a.mstride + (uint32_t)cell_j];
+                s = fb(mval) == kNegInf ? bf(kNegInf) : sadd(s, mval);
+            }
+        }
+        s_S[h * 64u + j] = s;
+        const uint32_t key = wave_max_u(in ? maxt_key_f(s) : floor_key);
+        if (lane == 0u) s_key[h] = key;
+    } else if (wave < 4u && lane == 0u) {
+        s_key[wave] = floor_key;
+    }
+    __syncthreads();
+
+    // ---- publish the segment maxima; wait for the item's segments ----
+    // A slot holds (key, tag) for each of 4 heads (32 bytes, written as two 16-byte stores: a reader
+    // sees whole 8-byte pairs); tag = the launch's epoch + 1, so slots of earlier launches never match.
+    const uint32_t nslots = a.n_items * a.maxtiles * 4u;          // segment slots per KV head
+    const __amdgpu_buffer_rsrc_t rk = fa_rsrc(a.keys + (size_t)g * nslots * 8u, nslots * 32u);
+    const uint32_t my_slot = (item * a.maxtiles + tt) * 4u + c;
+    if (tid == 0u) {
+        st_co16(rk, my_slot * 32u, make_uint4(s_key[0], tag, s_key[1], tag));
+        st_co16(rk, my_slot * 32u + 16u, make_uint4(s_key[2], tag, s_key[3], tag));
+    }
+    if (wave == 0u) {
+        // lane: half (lane & 1: heads 2 hf, 2 hf + 1) of segment sl = lane / 2 (tile sl / 4, channel sl % 4)
+        const uint32_t sl = lane >> 1, hf = lane & 1u, tl = sl >> 2, cl = sl & 3u;
+        const FaSeg fs(it, cl);
+        const bool want = tl < a.maxtiles && tl < fs.nseg;
+        const uint32_t off = ((item * a.maxtiles + min(tl, a.maxtiles - 1u)) * 4u + cl) * 32u + 16u * hf;
+        uint4 v = make_uint4(floor_key, tag, floor_key, tag);
+        uint32_t spins = 0;
+        for (;;) {
+            if (want) v = ld_co16(rk, off);
+            if (__all(v.y == tag && v.w == tag)) break;
+            if (++spins >= a.spin_max) {
+                if (lane == 0u && a.bad != nullptr)
+                    __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        // chunk maxima: MAXOUT of the floor and the segment maxima (AT 6.3)
+        const uint32_t a0 = want && hf == 0u ? v.x : floor_key, a1 = want && hf == 0u ? v.z : floor_key;
+        const uint32_t a2 = want && hf == 1u ? v.x : floor_key, a3 = want && hf == 1u ? v.z : floor_key;
+        const uint32_t k0 = wave_max_u(umax_u(a0, floor_key)), k1 = wave_max_u(umax_u(a1, floor_key));
+        const uint32_t k2 = wave_max_u(umax_u(a2, floor_key)), k3 = wave_max_u(umax_u(a3, floor_key));
+        if (lane < 4u) s_m[lane] = maxt_unkey(lane == 0u ? k0 : lane == 1u ? k1 : lane == 2u ? k2 : k3);
+    }
+    __syncthreads();
+    if (item < a.n_items && tt == 0u && c == (it.u0 & 3u) && tid < G)   // the item's first segment records them
+        st_co(a.m_item + (size_t)item * nh + g * G + tid, s_m[tid]);
+
+    // ---- EXP (wave h = head h) and the segment's LSUM ----
+    const size_t segrow = ((size_t)(it.tile0 + tt) * 4u + c) * nh + (size_t)g * G;   // + head
+    if (wave < G) {
+        const uint32_t h = wave;
+        // EXPK results are zero, normal, Inf or NaN (never subnormal)
+        const float p = in ? expk(smul_n(ssub_n(s_S[h * 64u + j], s_m[h]), a.scale), a.ex, s_t64) : 0.0f;
+        s_P[h * 64u + j] = p;
+        const uint32_t f = f_field(p);
+        const bool badl = __any(f == 255u);
+        const uint32_t pe = wave_max_u(f == 255u ? 0u : f);
+        const int32_t w = f == 255u ? 0 : bf_int_n(p, (int32_t)pe - 127);
+        const int32_t lsum = wave_sum_i(w);
+        if (lane == 0u)
+            st_co(a.seg_l + segrow + h, badl ? bf(kNaN) : (pe == 0u ? 0.0f : bf_scale((float)lsum, (int32_t)pe - 150)));
+    }
+    __syncthreads();
+
+    // ---- P.V: wave b = value block b ----
+    if (wave < NBD) {
+        const bool head_ok = hr < G;
+        const float4 pv = *(const float4 *)(s_P + min(hr, G - 1u) * 64u + 16u * kk + 4u * quad);
+        const float pz[4] = { head_ok ? pv.x : 0.0f, head_ok ? pv.y : 0.0f, head_ok ? pv.z : 0.0f, head_ok ? pv.w : 0.0f };
+        const uint32_t own = bv - b0;                             // the wave's block in the slice
+        if constexpr (ROPE) {                                     // the new cell: the fresh v scales
+            const int64_t base = 16 * (int64_t)ug[kk] + 4u * quad;
+            if (cell_new >= base && cell_new < base + 4) {
+                const uint32_t i = (uint32_t)(cell_new - base), sh = 16u * (i & 1u), keep = ~(0xFFFFu << sh);
+#pragma unroll
+                for (uint32_t e = 0; e < 2u; ++e) {
+                    const uint32_t h16 = f2h_exact(s_vd[b0 + e]) << sh;
+                    if (i < 2u) mvb[e].x = (mvb[e].x & keep) | h16;
+                    else mvb[e].y = (mvb[e].y & keep) | h16;
+                }
+            }
+        }
+        // weights w = p dV of the slice's two blocks, a subnormal product flushed to zero
+        float w[4][2];
+        uint32_t ex = 0u, nfm = 0u;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const bool live = (fb(pz[i]) & 0x7FFFFFFFu) != 0u;
+#pragma unroll
+            for (uint32_t e = 0; e < 2u; ++e) {
+                const float we = live ? pz[i] * h2f_fast(((i < 2u ? mvb[e].x : mvb[e].y) >> (16u * (i & 1u))) & 0xFFFFu) : 0.0f;
+                const uint32_t f = f_field(we);
+                nfm |= (f == 255u ? 1u : 0u) << e;
+                w[i][e] = f == 0u ? 0.0f : we;
+                ex = max(ex, f == 255u ? 0u : f);
+            }
+        }
+        const uint32_t ef = row16_umax(ex);                        // E_S over the head's 64 cells and the slice
+        const bool any = ef != 0u;
+        const int32_t es = (int32_t)ef - 127;
+        const bool bad = ((row16_or(nfm) >> own) & 1u) != 0u;
+        const bool use = any && !bad;
+        uint32_t P[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const int32_t W = use ? bf_int_n(w[i][own], es) : 0;
+            P[i] = ((uint32_t)W + 0x80808080u) ^ 0x80808080u;      // byte k = digit k of W
+        }
+        uint8_t * dg = s_dg + wave * 1024u;
+        const uint32_t lo01 = __builtin_amdgcn_perm(P[1], P[0], 0x05010400u);
+        const uint32_t lo23 = __builtin_amdgcn_perm(P[3], P[2], 0x05010400u);
+        const uint32_t hi01 = __builtin_amdgcn_perm(P[1], P[0], 0x07030602u);
+        const uint32_t hi23 = __builtin_amdgcn_perm(P[3], P[2], 0x07030602u);
+        const uint32_t q4[4] = { __builtin_amdgcn_perm(lo23, lo01, 0x05040100u), __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                                 __builtin_amdgcn_perm(hi23, hi01, 0x05040100u), __builtin_amdgcn_perm(hi23, hi01, 0x07060302u) };
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; ++k) *(uint32_t *)(dg + ((hr * 4u + k) * 4u + kk) * 16u + 4u * quad) = q4[k];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // matrix core: rows (head, digit), K = the 16 cells of group l / 16, columns 16 values
+        const v4i_fa Aop = *(const v4i_fa *)(dg + ((lane & 15u) * 4u + (lane >> 4)) * 16u);
+        if constexpr (ROPE) {                                     // the new cell's v quants
+            const int64_t base = 16 * (int64_t)ug[lane >> 4];
+            if (cell_new >= base && cell_new < base + 16) {
+                const uint32_t r = (uint32_t)(cell_new - base);
+                bq0 = put_byte(bq0, r, (uint8_t)s_vq[32u * bv + (lane & 15u)]);
+                bq1 = put_byte(bq1, r, (uint8_t)s_vq[32u * bv + 16u + (lane & 15u)]);
+            }
+        }
+        const uint32_t hres = lane >> 4;
+        const bool store = hres < G;
+        float * orow = a.seg_o + (segrow + min(hres, G - 1u)) * D + 32u * bv + (lane & 15u);
+#pragma unroll
+        for (uint32_t hf = 0; hf < 2u; ++hf) {
+            const int4 bq = hf ? bq1 : bq0;
+            const v4i_fa Bop = { bq.x, bq.y, bq.z, bq.w };
+            v4i_fa acc = { 0, 0, 0, 0 };
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Aop, Bop, acc, 0, 0, 0);
+            const float cval = bad ? bf(kNaN) : (any ? bf_scale(digits_rne24(acc), es - 23) : 0.0f);
+            if (store) st_co(orow + 16u * hf, cval);
+        }
+    }
+
+    // ---- the segment's results are stored: its flag (the launch's tag) ----
+    vm_wait();
+    __syncthreads();
+    if (tid == 0u) st_co_u(a.flags + (size_t)g * nslots + my_slot, tag);
+}
+
+// The reducers of a KV head: workgroup (head r, 64-value part vp) waits until every segment of the list
+// has stored its results (their flags), then, thread = (value, channel c): the chain of channel c's
+// segments in order (AT 6.4 O, 6.5 l), CTREE over the channels (AT 5.6), the merge of the items in
+// chunk order (AMERGE) and ANORM (AT 5.7). Slots and flags carry the launch's tag (an epoch + 1, one
+// epoch word per reducer, each advanced by its reducer at its end): nothing is cleared, and a store that
+// lands after an expired wait carries a tag no later launch expects. Reducers come after every segment
+// in dispatch order.
+constexpr uint32_t kRedItems = 3;                                 // items loaded per round
+
+template <int D>
+__device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds, uint32_t ri) {
+    uint32_t * s_t64 = (uint32_t *)lds;
+    uint32_t * s_it = (uint32_t *)(lds + 256);                    // [item] u0, n, tile0 (<= 256 items)
+    float * s_x = (float *)(lds + 256 + 3072);                    // [item][channel][64] O, then [item][channel] l
+    const uint32_t g = blockIdx.y, G = a.G, nh = a.n_head, ni = a.n_items;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    constexpr uint32_t NVP = D / 64u;                             // 64-value parts of a head
+    const uint32_t r = ri / NVP, vp = ri % NVP, hh = g * G + r;
+    const uint32_t c = tid >> 6, v = 64u * vp + lane;             // channel c, value v
+    const uint32_t nslots = ni * a.maxtiles * 4u;
+    uint32_t * ep = a.ep + (size_t)g * G * NVP + ri;              // this reducer's epoch of the KV head
+    const uint32_t tag = *ep + 1u;
+    s_t64[lane] = a.ex.t64[lane];
+    for (uint32_t k = tid; k < ni; k += blockDim.x) {
+        const FaItem ik = a.items[k];
+        s_it[3u * k] = ik.u0;
+        s_it[3u * k + 1u] = ik.n;
+        s_it[3u * k + 2u] = ik.tile0;
+    }
+    __syncthreads();
+    // every segment's flag (wave 0; slots of segments that do not exist are not waited for)
+    if (c == 0u) {
+        const uint32_t * fl = a.flags + (size_t)g * nslots;
+        uint32_t spins = 0;
+        for (uint32_t s0 = 0; s0 < nslots; s0 += 64u) {
+            const uint32_t sl = s0 + lane;
+            bool want = false;
+            if (sl < nslots) {
+                const uint32_t k = sl / (4u * a.maxtiles), tt = (sl / 4u) % a.maxtiles, cc = sl & 3u;
+                FaItem ik{};
+                ik.u0 = s_it[3u * k];
+                ik.n = s_it[3u * k + 1u];
+                want = tt < FaSeg(ik, cc).nseg;
+            }
+            for (;;) {
+                const uint32_t f = want ? ld_co_u(fl + sl) : tag;
+                if (__all(f == tag)) break;
+                if (++spins >= a.spin_max) {
+                    if (lane == 0u && a.bad != nullptr)
+                        __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+    }
+    __syncthreads();
+    float O = 0.0f, l = 0.0f, mr = 0.0f;
+    for (uint32_t k0 = 0; k0 < ni; k0 += kRedItems) {
+        float xo[kRedItems][8], xl[kRedItems][8], mkr[kRedItems];
+        uint32_t ns[kRedItems];
+#pragma unroll
+        for (uint32_t kq = 0; kq < kRedItems; ++kq) {             // every load of the round first
+            const uint32_t k = min(k0 + kq, ni - 1u);
+            FaItem ik{};
+            ik.u0 = s_it[3u * k];
+            ik.n = s_it[3u * k + 1u];
+            const uint32_t tile0 = s_it[3u * k + 2u];
+            const FaSeg sc(ik, c);
+            ns[kq] = sc.nseg;
+            mkr[kq] = ld_co(a.m_item + (size_t)k * nh + hh);
+#pragma unroll
+            for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
+                const size_t row = ((size_t)(tile0 + min(sgi, max(sc.nseg, 1u) - 1u)) * 4u + c) * nh + hh;
+                xo[kq][sgi] = ld_co(a.seg_o + row * D + v);
+                xl[kq][sgi] = ld_co(a.seg_l + row);
+            }
+        }
+#pragma unroll
+        for (uint32_t kq = 0; kq < kRedItems; ++kq) {             // channel c's segments in order
+            float Oc = 0.0f, Lc = 0.0f;
+#pragma unroll
+            for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
+                if (sgi < ns[kq]) {
+                    Oc = sadd_n(Oc, xo[kq][sgi]);
+                    Lc = sadd_n(Lc, xl[kq][sgi]);
+                }
+            }
+            s_x[(kq * 4u + c) * 64u + lane] = Oc;
+            if (lane == 0u) s_x[1024u + kq * 4u + c] = Lc;
+        }
+        __syncthreads();
+        if (c == 0u) {                                            // CTREE, then AMERGE, in chunk order
+            // the running maxima are a MAXT scan of the chunk maxima, so every merge factor of the round is
+            // known before the merge: lane 2 kq + b evaluates EXP((prev - mrun_kq) scale) for b = 0 (the
+            // running sums) or EXP((m_kq - mrun_kq) scale) for b = 1 (the chunk's), all at once
+            float mrun[kRedItems], prev[kRedItems];
+            float m = mr;
+#pragma unroll
+            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+                prev[kq] = m;
+                mrun[kq] = k0 + kq == 0u ? mkr[kq] : maxt(m, mkr[kq]);
+                m = mrun[kq];
+            }
+            const uint32_t jk = min(lane >> 1, kRedItems - 1u);  // lanes 2 kq, 2 kq + 1 hold item kq's factors
+            float from = 0.0f, to = 0.0f;
+#pragma unroll
+            for (uint32_t kq = 0; kq < kRedItems; ++kq)
+                if (jk == kq) {
+                    from = (lane & 1u) ? mkr[kq] : prev[kq];
+                    to = mrun[kq];
+                }
+            const float fx = expk(smul_n(ssub_n(from, to), a.scale), a.ex, s_t64);
+#pragma unroll
+            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+                if (k0 + kq >= ni) break;
+                const float * x = s_x + kq * 256u + lane;
+                const float ok = ctree4(x[0], x[64], x[128], x[192]);
+                const float * xl4 = s_x + 1024u + kq * 4u;
+                const float lk = ctree4(xl4[0], xl4[1], xl4[2], xl4[3]);
+                if (k0 + kq == 0u) {
+                    O = ok;
+                    l = lk;
+                } else {
+                    const float fa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq));
+                    const float fbv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq + 1));
+                    l = sadd_n(smul_n(l, fa), smul_n(lk, fbv));
+                    O = sadd_n(smul_n(O, fa), smul_n(ok, fbv));
+                }
+                mr = mrun[kq];
+            }
+        }
+        __syncthreads();
+    }
+    if (c == 0u) a.out[(size_t)hh * D + v] = smul_n(O, srcp(maxt(l, bf(kLFloor))));   // ANORM
+    // every segment of the KV head has read the epochs (its flag is in): the next launch's tags
+    if (tid == 0u) st_co_u(ep, tag);
+}
+
+}  // namespace tsr
+
+int tsr_launch_fa_dec(const tsr::FaDecArgs & a, hipStream_t s) {
+    const dim3 grid(a.n_items * a.maxtiles * 4u + a.G * (a.D / 64u), a.n_head_kv);   // segments, then reducers
+    const bool rope = a.cell != nullptr;
+    switch (a.D * 2u + (rope ? 1u : 0u)) {
+        case 128: hipLaunchKernelGGL((tsr::k_fa_dec<64, false>), grid, dim3(256), 0, s, a); break;
+        case 129: hipLaunchKernelGGL((tsr::k_fa_dec<64, true>), grid, dim3(256), 0, s, a); break;
+        case 256: hipLaunchKernelGGL((tsr::k_fa_dec<128, false>), grid, dim3(256), 0, s, a); break;
+        case 257: hipLaunchKernelGGL((tsr::k_fa_dec<128, true>), grid, dim3(256), 0, s, a); break;
+        default: return -2;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}

@@ -3,7 +3,8 @@
 //
 // Device layout of one plane (K or V), E = n_head_kv * D values per cell, cells in groups of 16
 // (AT's group, docs/design/03-attention-kv.md:141-205), ng = ceil(kv_size / 16) groups:
-//   meta  [ng][16 cells][E/32]   fp16 block scales
+//   meta  [ng][E/32 blocks][16 cells]  fp16 block scales (block-major: the scales of one block of a
+//                                      group's 16 cells are 32 contiguous bytes)
 //   quant K: [ng][E/16 chunks][16 cells][16 bytes]  (chunk-major: a wave load of chunk i over 64
 //                                                   cells is 4 runs of 256 contiguous bytes)
 //         V: [ng][E dims][16 cells]                 (dim-major: 16 cells of one value contiguous,
@@ -19,7 +20,7 @@ namespace tsr {
 // Device byte offset of byte k (0..33) of ggml block b of cell `cell`.
 __device__ __forceinline__ size_t kv_dev_off(const KvArgs & a, uint32_t which, uint32_t cell, uint32_t b, uint32_t k) {
     const uint32_t u = cell >> 4, rr = cell & 15u, nbk = a.E / 32u;
-    if (k < 2u) return (size_t)u * 16u * nbk * 2u + ((size_t)rr * nbk + b) * 2u + k;
+    if (k < 2u) return (((size_t)u * nbk + b) * 16u + rr) * 2u + k;
     const uint32_t i = 32u * b + (k - 2u);                  // value index in the row
     size_t q = a.quant_off + (size_t)u * 16u * a.E;
     if (which == 0u) q += ((size_t)(i >> 4) * 16u + rr) * 16u + (i & 15u);

@@ -114,17 +114,6 @@ struct FaArgs {
     float * Mpart;           // [tile][n_head] tile maxima
     float * OP;              // [item][4][n_head][D] channel partials
     float * LP;              // [item][4][n_head] channel row sums
-    // the fused decode form (a plan's buffers): per score tile the segment results of its channels
-    // [tile][4][n_head][D] and row sums [tile][4][n_head]; zero between launches: the tile maxima as
-    // MAXT keys [n_head_kv][n_items * maxtiles][4] (0: not yet published) and the counters
-    // [item][n_head_kv] tiles that stored their segments, [n_head_kv] items whose channel partials
-    // are stored
-    float * seg_o;
-    float * seg_l;
-    float * m_item;          // [item][n_head] chunk maxima
-    uint32_t * tkeys;
-    uint32_t * sync;
-    uint32_t spin_max;       // polls of the tile-key wait before it gives up (*bad = 2)
     uint32_t max_groups;     // the largest item (groups), for a work list in device memory
     float * out;
     uint64_t out_stride;
@@ -138,6 +127,35 @@ struct FaArgs {
     uint32_t n_dims, neox;
     float ts, m;
     const float * rtab;      // or the angles of *pos from tsr_hip_rope_table: [n_dims / 2] (M cos, M sin)
+};
+
+// The one-launch decode FLASH_ATTN_EXT (k_fa_dec.hip): one query row over a plan's device work list,
+// one workgroup per ATTPV segment (64 cells of one channel of one chunk, one KV head).
+struct FaDecArgs {
+    const float * q;         // the query row [n_head][D]; with ROPE the token's unrotated Q|K|V row
+    KvArgs kc, vc;
+    uint32_t D, G, n_head, n_head_kv, E;
+    float scale;
+    const float * mask;      // GENERAL: the f32 mask row (mstride floats)
+    uint32_t mstride;
+    const FaItem * items;    // the plan's work list (n_items items, chunk order)
+    uint32_t n_items, maxtiles;
+    float * seg_o;           // [tile][4][n_head][D] segment results
+    float * seg_l;           // [tile][4][n_head] segment row sums
+    float * m_item;          // [item][n_head] chunk maxima
+    uint32_t * keys;         // [n_head_kv][n_items][maxtiles][4] 32-byte slots: (MAXT key, tag) of 4 heads
+    uint32_t * flags;        // [n_head_kv][n_items][maxtiles][4] the launch's tag once the segment's results are stored
+    uint32_t * ep;           // [n_head_kv][reducer] epochs (zero at creation); a launch's tag is epoch + 1
+    uint32_t spin_max;       // polls of the maxima wait before it gives up (*bad = 2)
+    float * out;             // [n_head][D]
+    ExpkTab ex;
+    // ROPE + SET_ROWS_KV folded in (cell != 0): position *pos or the angle table rtab, new cell *cell
+    const int32_t * pos;
+    const int64_t * cell;
+    int32_t * bad;
+    uint32_t n_dims, neox;
+    float ts, m;
+    const float * rtab;
 };
 
 // ROPE over T tokens of n_heads heads (head h of token t at x + t * x_stride + h * head_dim).
@@ -185,6 +203,7 @@ int tsr_launch_kv_bytes(const tsr::KvArgs & a, uint32_t which, uint64_t off, uin
 int tsr_launch_kv_set_rows(const tsr::KvArgs & a, uint32_t which, const float * src, uint32_t n_rows,
                            uint64_t src_stride, const int64_t * idx, int32_t * bad, hipStream_t s);
 int tsr_launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, uint32_t n_cu, hipStream_t s);
+int tsr_launch_fa_dec(const tsr::FaDecArgs & a, hipStream_t s);
 int tsr_launch_rms_norm(const float * x, uint64_t x_stride, uint32_t n, uint32_t rows, float eps, float inv_n,
                         const float * w, uint64_t w_stride, uint32_t w_period, float * y, uint64_t y_stride, hipStream_t s);
 int tsr_launch_rope(const tsr::RopeArgs & a, uint32_t T, hipStream_t s);

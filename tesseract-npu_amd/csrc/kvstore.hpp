@@ -21,8 +21,7 @@ __device__ __forceinline__ void kv_store_unit(const KvArgs & a, uint32_t which, 
         for (int k = 0; k < 4; ++k) qb[(size_t)(i + k) * 16u + rr] = (uint8_t)(q >> (8 * k));
     }
     if (lead) {
-        uint16_t * meta = (uint16_t *)(a.base + (size_t)u * 16u * nbk * 2u);
-        meta[(size_t)rr * nbk + i / 32u] = (uint16_t)f2h_exact(D);
+        ((uint16_t *)a.base)[((size_t)u * nbk + i / 32u) * 16u + rr] = (uint16_t)f2h_exact(D);
     }
 }
 

@@ -503,7 +503,7 @@ struct tsr_hip_fa_plan {
     uint32_t items_max = 0, tiles_max = 0;
     uint64_t cells_max = 0;
     uint8_t * dev = nullptr;
-    size_t o_items = 0, o_S = 0, o_Mp = 0, o_OP = 0, o_LP = 0, o_SO = 0, o_SL = 0, o_MI = 0, o_TK = 0, o_sync = 0,
+    size_t o_items = 0, o_S = 0, o_Mp = 0, o_OP = 0, o_LP = 0, o_SO = 0, o_SL = 0, o_MI = 0, o_TK = 0, o_FL = 0, o_EP = 0,
            bytes = 0;
     bool set = false, general = false;
     uint32_t n_items = 0, maxtiles = 0, max_groups = 0, mstride = 0;   // the shape a launch bakes in
@@ -546,9 +546,12 @@ int tsr_hip_fa_plan_create(tsr_hip_ctx * ctx, uint32_t D, uint32_t n_head, uint3
     p->o_SO = off; off = up256(off + 4u * (size_t)ftiles * kC * n_head * D);
     p->o_SL = off; off = up256(off + 4u * (size_t)ftiles * kC * n_head);
     p->o_MI = off; off = up256(off + (T == 1u ? 4u * (size_t)items * n_head : 0u));
-    // zero between launches: the tile keys (an item has <= 8 tiles: NCG <= 128 groups) and the counters
-    p->o_TK = off; off = up256(off + (T == 1u ? 4u * 4u * 8u * (size_t)items * n_head_kv : 0u));
-    p->o_sync = off; off = up256(off + (T == 1u ? 4u * ((size_t)items + 1u) * n_head_kv : 0u));
+    // zero between launches: the 16-byte slots of segment maxima (an item has <= 8 tiles of 4 channels:
+    // NCG <= 128 groups) and the counters
+    // the decode form's segment slots (32 bytes), flags and per-reducer epochs (<= 4 heads x 2 value parts)
+    p->o_TK = off; off = up256(off + (T == 1u ? 32u * 8u * 4u * (size_t)items * n_head_kv : 0u));
+    p->o_FL = off; off = up256(off + (T == 1u ? 4u * 8u * 4u * (size_t)items * n_head_kv : 0u));
+    p->o_EP = off; off = up256(off + (T == 1u ? 4u * 8u * (size_t)n_head_kv : 0u));
     p->bytes = off;
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
@@ -634,6 +637,50 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
     if (kc->E != E || vc->E != E || kc->kv_size != vc->kv_size || kc->kv_size < plan->kv_size) return TSR_HIP_E_SHAPE;
     if (((uintptr_t)q_dev & 15u) != 0u || (T > 1u && (q_stride % 4u != 0u || q_stride < K)) || (T > 1u && out_stride < K))
         return TSR_HIP_E_ARG;
+    const uint32_t G = plan->n_head / plan->n_head_kv;
+    if (T == 1u && G <= 4u && (plan->D == 64u || plan->D == 128u) && plan->n_items <= 256u) {
+        // one decode row: the one-launch form, one workgroup per ATTPV segment (k_fa_dec.hip)
+        tsr::FaDecArgs d{};
+        d.q = q_dev;
+        d.kc = kv_args(kc);
+        d.vc = kv_args(vc);
+        d.D = plan->D;
+        d.G = G;
+        d.n_head = plan->n_head;
+        d.n_head_kv = plan->n_head_kv;
+        d.E = E;
+        d.scale = scale;
+        d.mask = mask_f32_dev;
+        d.mstride = plan->mstride;
+        d.items = (const tsr::FaItem *)(plan->dev + plan->o_items);
+        d.n_items = plan->n_items;
+        d.maxtiles = plan->maxtiles;
+        d.seg_o = (float *)(plan->dev + plan->o_SO);
+        d.seg_l = (float *)(plan->dev + plan->o_SL);
+        d.m_item = (float *)(plan->dev + plan->o_MI);
+        d.keys = (uint32_t *)(plan->dev + plan->o_TK);
+        d.flags = (uint32_t *)(plan->dev + plan->o_FL);
+        d.ep = (uint32_t *)(plan->dev + plan->o_EP);
+        d.spin_max = ctx->fa_spin_max;
+        d.out = out_dev;
+        d.ex = ctx->expk;
+        if (rope != nullptr) {
+            d.rtab = rope->rtab;
+            d.pos = rope->pos;
+            d.cell = rope->cell;
+            d.bad = rope->bad;
+            d.n_dims = rope->n_dims;
+            d.neox = rope->neox;
+            d.ts = rope->ts;
+            d.m = rope->m;
+        }
+        std::lock_guard<std::mutex> lk(ctx->mtx);
+        (void)hipSetDevice(ctx->device);
+        ctx->ctr.flash_attn_calls++;
+        ctx->ctr.flash_attn_kv_bytes += plan->cells * (uint64_t)E / 32u * 34u * 2u;
+        if (rope != nullptr) ctx->ctr.set_rows_calls += 2u;
+        return tsr_launch_fa_dec(d, ctx->pick(stream)) ? TSR_HIP_E_HIP : TSR_HIP_OK;
+    }
     tsr::FaPlan p{};
     p.n_items = plan->n_items;
     p.maxtiles = plan->maxtiles;
@@ -647,14 +694,6 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
     a.OP = (float *)(plan->dev + plan->o_OP);
     a.LP = (float *)(plan->dev + plan->o_LP);
     a.max_groups = plan->max_groups;
-    if (T == 1u) {                                                // the fused decode form's buffers
-        a.seg_o = (float *)(plan->dev + plan->o_SO);
-        a.seg_l = (float *)(plan->dev + plan->o_SL);
-        a.m_item = (float *)(plan->dev + plan->o_MI);
-        a.tkeys = (uint32_t *)(plan->dev + plan->o_TK);
-        a.spin_max = ctx->fa_spin_max;
-        a.sync = (uint32_t *)(plan->dev + plan->o_sync);
-    }
     if (rope != nullptr) {
         a.rtab = rope->rtab;
         a.pos = rope->pos;

@@ -231,10 +231,14 @@ int tsr_hip_flash_attn_plan_rope_tab(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * 
                                      const float * tab_dev, const int64_t * cell_dev, int32_t * bad_dev,
                                      const float * mask_f32_dev, float * out_dev, uint64_t out_stride, void * stream);
 int tsr_hip_fa_plan_free(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan);
-/* The one-launch decode form of the planned FLASH_ATTN_EXT waits, bounded, for the tile maxima of its
- * chunk (no counterpart in the reference, whose chunks run in order on one engine): polls of that
- * wait before it gives up and raises *bad_dev = 2 (its results are then not valid). 0 restores the
- * default (2^20 polls, tens of milliseconds); a small limit forces the expired path (tests of it). */
+/* The one-launch decode form of the planned FLASH_ATTN_EXT (one query row) runs a workgroup per ATTPV
+ * segment and exchanges the chunk maxima and the segment results between its workgroups (no
+ * counterpart in the reference, whose chunks run in order on one engine). Its waits are bounded: polls
+ * of a wait before it gives up and raises *bad_dev |= 2 (the results are then not valid). 0 restores the
+ * default (2^20 polls, tens of milliseconds); a small limit forces the expired path (tests of it).
+ * When n_head_kv is a multiple of the device's XCD count, all workgroups of a KV head are placed on one
+ * XCD (the dispatcher's round-robin) and exchange through its L2; a workgroup found on another XCD
+ * raises *bad_dev |= 4 (results not valid). bad_dev is the argument of the _rope entry points. */
 int tsr_hip_set_fa_wait_limit(tsr_hip_ctx * ctx, uint32_t polls);
 
 /* ---- graphs -------------------------------------------------------------------------------------

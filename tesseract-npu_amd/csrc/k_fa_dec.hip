@@ -14,9 +14,11 @@
 //   P.V        wave b = value block b: the block-float weights of its 32 values (E_S over the 64-value
 //              slice: both blocks of the slice), their base-256 digits and two int8 matrix-core
 //              products for the 4 heads (16 values each)
-//   results    the segment's O (G x D) and l (G) to the plan, agent-coherent, then its flag
+//   results    the segment's O (G x D) and l (G) to the plan, each value with the launch's tag in one
+//              8-byte agent-coherent store
 //   reduce     G x D/64 reducer workgroups per KV head, after every segment in dispatch order: each
-//              waits for every flag, then chains, in order, the segments of every channel of every item
+//              polls the results until all carry the tag, then chains, in order, the segments of every
+//              channel of every item
 //              for its 64 values of one head, CTREE over the channels, merges the items in chunk order
 //              (AMERGE) and normalizes (ANORM); no atomic operation, nothing to clear (tags)
 // The chunk maximum needs every score of the chunk before any P.V of it (p depends on it bit for bit),
@@ -48,8 +50,29 @@ typedef unsigned v4u_fa __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_co16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1));
 }
+// Stores of the exchanged slots and results: agent-coherent (write-through, sc1) when the workgroups of
+// a KV head may sit on different XCDs; plain (into the XCD's L2, where the readers' agent-coherent
+// loads find them) when they all sit on one (LOCAL).
+template <bool LOCAL>
 __device__ __forceinline__ void st_co16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_fa, v), r, off, 0, kSc1);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_fa, v), r, off, 0, LOCAL ? 0 : kSc1);
+}
+
+// Tags: the low 28 bits are the launch's epoch + 1 (mod 2^28), the high 4 bits the writer's XCD, so a
+// reader checks in the same word that a value is this launch's and, in the LOCAL form, that its writer
+// shared its XCD (and so its L2).
+constexpr uint32_t kTagMask = 0x0FFFFFFFu;
+__device__ __forceinline__ bool tag_is(uint32_t t, uint32_t tag) { return (t & kTagMask) == tag; }
+
+// A result with the launch's tag in one 8-byte agent-coherent store (a reader sees both or neither) and
+// its load.
+template <bool LOCAL>
+__device__ __forceinline__ void st_tag(uint64_t * p, float v, uint32_t tag) {
+    if constexpr (LOCAL) __hip_atomic_store(p, ((uint64_t)tag << 32) | fb(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else __hip_atomic_store(p, ((uint64_t)tag << 32) | fb(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_tag(const uint64_t * p) {
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Byte r (0..15) of a 16-byte value replaced by b (selects only: the value stays in registers).
@@ -73,12 +96,35 @@ struct FaSeg {
     }
 };
 
+// The workgroup's work: index x among its KV head's workgroups (segments, then reducers) and the head g.
+// LOCAL: a 1-D grid with g = blockIdx.x mod n_head_kv, so that under the dispatcher's round-robin of
+// workgroups over the XCDs (consecutive workgroups on consecutive XCDs, n_head_kv a multiple of n_xcd)
+// every workgroup of a head runs on one XCD: their exchanges stay in that XCD's L2. Every exchanged
+// word carries its writer's XCD; a reader that finds another XCD than its own raises *bad |= 4 (the
+// exchange is then not guaranteed: a wait that misses it expires and raises 2 as well), never silently.
+struct FaDecBlock {
+    uint32_t x, g;
+};
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & 0xFu;
+}
+template <bool LOCAL>
+__device__ __forceinline__ FaDecBlock fa_dec_block(const FaDecArgs & a) {
+    if constexpr (LOCAL) {
+        return { blockIdx.x / a.n_head_kv, blockIdx.x % a.n_head_kv };
+    } else {
+        return { blockIdx.x, blockIdx.y };
+    }
+}
+
 // LDS of one workgroup (bytes): table 256 | q quants 512 | q scales 64 | new k quants 128, scales 16 |
 // new v quants 128, scales 16 | terms [4 heads][4 blocks][64] f32 4096 | scores [4][64] 1024 |
 // p [4][64] 1024 | digits [4 waves][1024] | keys 16 | maxima 16 | flag 16.
 constexpr uint32_t kDecLds = 256 + 512 + 64 + 128 + 16 + 128 + 16 + 4096 + 1024 + 1024 + 4096 + 48;
 
-template <int D, bool ROPE>
+template <int D, bool ROPE, bool LOCAL>
 __global__ __launch_bounds__(256, 6) void k_fa_dec(FaDecArgs a) {
     constexpr uint32_t NBD = D / 32u;                             // K / V blocks of a head
     __shared__ __align__(16) uint8_t lds[kDecLds];
@@ -97,12 +143,13 @@ __global__ __launch_bounds__(256, 6) void k_fa_dec(FaDecArgs a) {
     float * s_m = (float *)(lds + 11376);                         // [4] chunk maxima
 
     const uint32_t per_item = 4u * a.maxtiles;
-    if (blockIdx.x >= a.n_items * per_item) {                     // the KV head's reducers
-        fa_dec_reduce<D>(a, lds, blockIdx.x - a.n_items * per_item);
+    const FaDecBlock blk = fa_dec_block<LOCAL>(a);
+    if (blk.x >= a.n_items * per_item) {                          // the KV head's reducers
+        fa_dec_reduce<D, LOCAL>(a, lds, blk.x - a.n_items * per_item, blk.g);
         return;
     }
-    const uint32_t item = blockIdx.x / per_item, tt = (blockIdx.x / 4u) % a.maxtiles, c = blockIdx.x & 3u;
-    const uint32_t g = blockIdx.y, G = a.G, nh = a.n_head, E = a.E, nbk = E / 32u;
+    const uint32_t item = blk.x / per_item, tt = (blk.x / 4u) % a.maxtiles, c = blk.x & 3u;
+    const uint32_t g = blk.g, G = a.G, nh = a.n_head, E = a.E, nbk = E / 32u;
     const FaItem it = a.items[item];
     const FaSeg sg(it, c);
     if (tt >= sg.nseg) return;                                    // no such segment (block-uniform)
@@ -124,8 +171,10 @@ __global__ __launch_bounds__(256, 6) void k_fa_dec(FaDecArgs a) {
         if (a.rtab == nullptr) pos = *a.pos;
     }
     const uint32_t t64v = a.ex.t64[lane];
-    // the launch's tag: reducer 0's epoch of the KV head + 1 (the epochs advance at the end of a launch)
-    const uint32_t tag = a.ep[(size_t)g * G * (D / 64u)] + 1u;
+    // the launch's tag: reducer 0's epoch of the KV head + 1 (the epochs advance at the end of a launch);
+    // what this workgroup writes carries its XCD too
+    const uint32_t xcc = xcc_id();
+    const uint32_t tag = (a.ep[(size_t)g * G * (D / 64u)] + 1u) & kTagMask, tagw = tag | (xcc << 28);
     // ROPE angles of the token (table): first, so that waiting for them is not waiting for K and V
     float2 cs_tab = make_float2(0.0f, 0.0f);
     if constexpr (ROPE) {
@@ -282,8 +331,8 @@ __global__ __launch_bounds__(256, 6) void k_fa_dec(FaDecArgs a) {
     const __amdgpu_buffer_rsrc_t rk = fa_rsrc(a.keys + (size_t)g * nslots * 8u, nslots * 32u);
     const uint32_t my_slot = (item * a.maxtiles + tt) * 4u + c;
     if (tid == 0u) {
-        st_co16(rk, my_slot * 32u, make_uint4(s_key[0], tag, s_key[1], tag));
-        st_co16(rk, my_slot * 32u + 16u, make_uint4(s_key[2], tag, s_key[3], tag));
+        st_co16<LOCAL>(rk, my_slot * 32u, make_uint4(s_key[0], tagw, s_key[1], tagw));
+        st_co16<LOCAL>(rk, my_slot * 32u + 16u, make_uint4(s_key[2], tagw, s_key[3], tagw));
     }
     if (wave == 0u) {
         // lane: half (lane & 1: heads 2 hf, 2 hf + 1) of segment sl = lane / 2 (tile sl / 4, channel sl % 4)
@@ -291,11 +340,11 @@ __global__ __launch_bounds__(256, 6) void k_fa_dec(FaDecArgs a) {
         const FaSeg fs(it, cl);
         const bool want = tl < a.maxtiles && tl < fs.nseg;
         const uint32_t off = ((item * a.maxtiles + min(tl, a.maxtiles - 1u)) * 4u + cl) * 32u + 16u * hf;
-        uint4 v = make_uint4(floor_key, tag, floor_key, tag);
+        uint4 v = make_uint4(floor_key, tagw, floor_key, tagw);
         uint32_t spins = 0;
         for (;;) {
             if (want) v = ld_co16(rk, off);
-            if (__all(v.y == tag && v.w == tag)) break;
+            if (__all(tag_is(v.y, tag) && tag_is(v.w, tag))) break;
             if (++spins >= a.spin_max) {
                 if (lane == 0u && a.bad != nullptr)
                     __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -303,6 +352,10 @@ __global__ __launch_bounds__(256, 6) void k_fa_dec(FaDecArgs a) {
             }
             __builtin_amdgcn_s_sleep(1);
         }
+        // (a word the wait gave up on may be another launch's: only this launch's words count here)
+        if (LOCAL && __any((tag_is(v.y, tag) && (v.y >> 28) != xcc) || (tag_is(v.w, tag) && (v.w >> 28) != xcc)) &&
+            lane == 0u && a.bad != nullptr)
+            __hip_atomic_fetch_or(a.bad, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // chunk maxima: MAXOUT of the floor and the segment maxima (AT 6.3)
         const uint32_t a0 = want && hf == 0u ? v.x : floor_key, a1 = want && hf == 0u ? v.z : floor_key;
         const uint32_t a2 = want && hf == 1u ? v.x : floor_key, a3 = want && hf == 1u ? v.z : floor_key;
@@ -312,7 +365,7 @@ __global__ __launch_bounds__(256, 6) void k_fa_dec(FaDecArgs a) {
     }
     __syncthreads();
     if (item < a.n_items && tt == 0u && c == (it.u0 & 3u) && tid < G)   // the item's first segment records them
-        st_co(a.m_item + (size_t)item * nh + g * G + tid, s_m[tid]);
+        st_tag<LOCAL>(a.m_item + (size_t)item * nh + g * G + tid, s_m[tid], tagw);
 
     // ---- EXP (wave h = head h) and the segment's LSUM ----
     const size_t segrow = ((size_t)(it.tile0 + tt) * 4u + c) * nh + (size_t)g * G;   // + head
@@ -327,7 +380,7 @@ __global__ __launch_bounds__(256, 6) void k_fa_dec(FaDecArgs a) {
         const int32_t w = f == 255u ? 0 : bf_int_n(p, (int32_t)pe - 127);
         const int32_t lsum = wave_sum_i(w);
         if (lane == 0u)
-            st_co(a.seg_l + segrow + h, badl ? bf(kNaN) : (pe == 0u ? 0.0f : bf_scale((float)lsum, (int32_t)pe - 150)));
+            st_tag<LOCAL>(a.seg_l + segrow + h, badl ? bf(kNaN) : (pe == 0u ? 0.0f : bf_scale((float)lsum, (int32_t)pe - 150)), tagw);
     }
     __syncthreads();
 
@@ -399,7 +452,7 @@ __global__ __launch_bounds__(256, 6) void k_fa_dec(FaDecArgs a) {
         }
         const uint32_t hres = lane >> 4;
         const bool store = hres < G;
-        float * orow = a.seg_o + (segrow + min(hres, G - 1u)) * D + 32u * bv + (lane & 15u);
+        uint64_t * orow = a.seg_o + (segrow + min(hres, G - 1u)) * D + 32u * bv + (lane & 15u);
 #pragma unroll
         for (uint32_t hf = 0; hf < 2u; ++hf) {
             const int4 bq = hf ? bq1 : bq0;
@@ -407,38 +460,32 @@ __global__ __launch_bounds__(256, 6) void k_fa_dec(FaDecArgs a) {
             v4i_fa acc = { 0, 0, 0, 0 };
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(Aop, Bop, acc, 0, 0, 0);
             const float cval = bad ? bf(kNaN) : (any ? bf_scale(digits_rne24(acc), es - 23) : 0.0f);
-            if (store) st_co(orow + 16u * hf, cval);
+            if (store) st_tag<LOCAL>(orow + 16u * hf, cval, tagw);
         }
     }
-
-    // ---- the segment's results are stored: its flag (the launch's tag) ----
-    vm_wait();
-    __syncthreads();
-    if (tid == 0u) st_co_u(a.flags + (size_t)g * nslots + my_slot, tag);
 }
 
-// The reducers of a KV head: workgroup (head r, 64-value part vp) waits until every segment of the list
-// has stored its results (their flags), then, thread = (value, channel c): the chain of channel c's
-// segments in order (AT 6.4 O, 6.5 l), CTREE over the channels (AT 5.6), the merge of the items in
-// chunk order (AMERGE) and ANORM (AT 5.7). Slots and flags carry the launch's tag (an epoch + 1, one
-// epoch word per reducer, each advanced by its reducer at its end): nothing is cleared, and a store that
-// lands after an expired wait carries a tag no later launch expects. Reducers come after every segment
-// in dispatch order.
+// The reducers of a KV head: workgroup (head r, 64-value part vp), thread = (value, channel c), polls the
+// segments' results of its head until every one carries the launch's tag, then chains channel c's
+// segments in order (AT 6.4 O, 6.5 l), CTREE over the channels (AT 5.6), merges the items in chunk
+// order (AMERGE) and normalizes (ANORM, AT 5.7). Slots and results carry the launch's tag (an epoch + 1,
+// one epoch word per reducer, each advanced by its reducer at its end): nothing is cleared, and a store
+// that lands after an expired wait carries a tag no later launch expects. A reducer only waits for
+// segments, which come before it in dispatch order.
 constexpr uint32_t kRedItems = 3;                                 // items loaded per round
 
-template <int D>
-__device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds, uint32_t ri) {
+template <int D, bool LOCAL>
+__device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds, uint32_t ri, uint32_t g) {
     uint32_t * s_t64 = (uint32_t *)lds;
     uint32_t * s_it = (uint32_t *)(lds + 256);                    // [item] u0, n, tile0 (<= 256 items)
     float * s_x = (float *)(lds + 256 + 3072);                    // [item][channel][64] O, then [item][channel] l
-    const uint32_t g = blockIdx.y, G = a.G, nh = a.n_head, ni = a.n_items;
+    const uint32_t G = a.G, nh = a.n_head, ni = a.n_items;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     constexpr uint32_t NVP = D / 64u;                             // 64-value parts of a head
     const uint32_t r = ri / NVP, vp = ri % NVP, hh = g * G + r;
     const uint32_t c = tid >> 6, v = 64u * vp + lane;             // channel c, value v
-    const uint32_t nslots = ni * a.maxtiles * 4u;
     uint32_t * ep = a.ep + (size_t)g * G * NVP + ri;              // this reducer's epoch of the KV head
-    const uint32_t tag = *ep + 1u;
+    const uint32_t tag = (*ep + 1u) & kTagMask, xcc = xcc_id();
     s_t64[lane] = a.ex.t64[lane];
     for (uint32_t k = tid; k < ni; k += blockDim.x) {
         const FaItem ik = a.items[k];
@@ -447,53 +494,65 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
         s_it[3u * k + 2u] = ik.tile0;
     }
     __syncthreads();
-    // every segment's flag (wave 0; slots of segments that do not exist are not waited for)
-    if (c == 0u) {
-        const uint32_t * fl = a.flags + (size_t)g * nslots;
+    float O = 0.0f, l = 0.0f, mr = 0.0f;
+    for (uint32_t k0 = 0; k0 < ni; k0 += kRedItems) {
+        // wave c polls its round's results until every one carries the launch's tag: lane v's value of
+        // channel c in each segment, lane s's row sum of segment s, lane kq's chunk maximum of item kq
+        uint64_t po[kRedItems][8], pl[kRedItems], pm;
+        uint32_t ns[kRedItems];
         uint32_t spins = 0;
-        for (uint32_t s0 = 0; s0 < nslots; s0 += 64u) {
-            const uint32_t sl = s0 + lane;
-            bool want = false;
-            if (sl < nslots) {
-                const uint32_t k = sl / (4u * a.maxtiles), tt = (sl / 4u) % a.maxtiles, cc = sl & 3u;
+        for (;;) {
+            bool ok = true;
+#pragma unroll
+            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+                const uint32_t k = min(k0 + kq, ni - 1u);
                 FaItem ik{};
                 ik.u0 = s_it[3u * k];
                 ik.n = s_it[3u * k + 1u];
-                want = tt < FaSeg(ik, cc).nseg;
-            }
-            for (;;) {
-                const uint32_t f = want ? ld_co_u(fl + sl) : tag;
-                if (__all(f == tag)) break;
-                if (++spins >= a.spin_max) {
-                    if (lane == 0u && a.bad != nullptr)
-                        __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
-    }
-    __syncthreads();
-    float O = 0.0f, l = 0.0f, mr = 0.0f;
-    for (uint32_t k0 = 0; k0 < ni; k0 += kRedItems) {
-        float xo[kRedItems][8], xl[kRedItems][8], mkr[kRedItems];
-        uint32_t ns[kRedItems];
+                const uint32_t tile0 = s_it[3u * k + 2u];
+                const FaSeg sc(ik, c);
+                ns[kq] = sc.nseg;
 #pragma unroll
-        for (uint32_t kq = 0; kq < kRedItems; ++kq) {             // every load of the round first
-            const uint32_t k = min(k0 + kq, ni - 1u);
-            FaItem ik{};
-            ik.u0 = s_it[3u * k];
-            ik.n = s_it[3u * k + 1u];
-            const uint32_t tile0 = s_it[3u * k + 2u];
-            const FaSeg sc(ik, c);
-            ns[kq] = sc.nseg;
-            mkr[kq] = ld_co(a.m_item + (size_t)k * nh + hh);
+                for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
+                    const size_t row = ((size_t)(tile0 + min(sgi, max(sc.nseg, 1u) - 1u)) * 4u + c) * nh + hh;
+                    po[kq][sgi] = ld_tag(a.seg_o + row * D + v);
+                }
+                const size_t lrow = ((size_t)(tile0 + min(lane, max(sc.nseg, 1u) - 1u)) * 4u + c) * nh + hh;
+                pl[kq] = ld_tag(a.seg_l + lrow);
+            }
+            pm = ld_tag(a.m_item + (size_t)min(k0 + min(lane, kRedItems - 1u), ni - 1u) * nh + hh);
+            bool near = true;                                     // every writer shared this XCD
+#pragma unroll
+            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+#pragma unroll
+                for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
+                    ok &= sgi >= ns[kq] || tag_is((uint32_t)(po[kq][sgi] >> 32), tag);
+                    near &= sgi >= ns[kq] || (uint32_t)(po[kq][sgi] >> 60) == xcc;
+                }
+                ok &= lane >= ns[kq] || tag_is((uint32_t)(pl[kq] >> 32), tag);
+            }
+            ok &= tag_is((uint32_t)(pm >> 32), tag);
+            if (__all(ok)) {
+                if (LOCAL && __any(!near) && lane == 0u && a.bad != nullptr)
+                    __hip_atomic_fetch_or(a.bad, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            if (++spins >= a.spin_max) {
+                if (lane == 0u && a.bad != nullptr)
+                    __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        float xo[kRedItems][8], xl[kRedItems][8], mkr[kRedItems];
+#pragma unroll
+        for (uint32_t kq = 0; kq < kRedItems; ++kq) {
 #pragma unroll
             for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
-                const size_t row = ((size_t)(tile0 + min(sgi, max(sc.nseg, 1u) - 1u)) * 4u + c) * nh + hh;
-                xo[kq][sgi] = ld_co(a.seg_o + row * D + v);
-                xl[kq][sgi] = ld_co(a.seg_l + row);
+                xo[kq][sgi] = bf((uint32_t)po[kq][sgi]);
+                xl[kq][sgi] = bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pl[kq], (int)sgi));
             }
+            mkr[kq] = bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pm, (int)kq));
         }
 #pragma unroll
         for (uint32_t kq = 0; kq < kRedItems; ++kq) {             // channel c's segments in order
@@ -559,14 +618,32 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
 }  // namespace tsr
 
 int tsr_launch_fa_dec(const tsr::FaDecArgs & a, hipStream_t s) {
-    const dim3 grid(a.n_items * a.maxtiles * 4u + a.G * (a.D / 64u), a.n_head_kv);   // segments, then reducers
+    const uint32_t per_head = a.n_items * a.maxtiles * 4u + a.G * (a.D / 64u);   // segments, then reducers
+    const bool local = a.n_xcd != 0u && a.n_head_kv % a.n_xcd == 0u;
+    const dim3 grid = local ? dim3(per_head * a.n_head_kv, 1) : dim3(per_head, a.n_head_kv);
     const bool rope = a.cell != nullptr;
-    switch (a.D * 2u + (rope ? 1u : 0u)) {
-        case 128: hipLaunchKernelGGL((tsr::k_fa_dec<64, false>), grid, dim3(256), 0, s, a); break;
-        case 129: hipLaunchKernelGGL((tsr::k_fa_dec<64, true>), grid, dim3(256), 0, s, a); break;
-        case 256: hipLaunchKernelGGL((tsr::k_fa_dec<128, false>), grid, dim3(256), 0, s, a); break;
-        case 257: hipLaunchKernelGGL((tsr::k_fa_dec<128, true>), grid, dim3(256), 0, s, a); break;
+#define TSR_DEC(DD, RR, LL) hipLaunchKernelGGL((tsr::k_fa_dec<DD, RR, LL>), grid, dim3(256), 0, s, a)
+    switch (a.D * 4u + (rope ? 2u : 0u) + (local ? 1u : 0u)) {
+        case 256: TSR_DEC(64, false, false); break;
+        case 257: TSR_DEC(64, false, true); break;
+        case 258: TSR_DEC(64, true, false); break;
+        case 259: TSR_DEC(64, true, true); break;
+        case 512: TSR_DEC(128, false, false); break;
+        case 513: TSR_DEC(128, false, true); break;
+        case 514: TSR_DEC(128, true, false); break;
+        case 515: TSR_DEC(128, true, true); break;
         default: return -2;
     }
+#undef TSR_DEC
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+// The XCD of each of the first 64 workgroups of a launch (the context's check of the dispatcher's
+// round-robin over the XCDs).
+__global__ void k_xcd_probe(uint32_t * out) {
+    if (threadIdx.x == 0u) out[blockIdx.x] = tsr::xcc_id();
+}
+int tsr_launch_xcd_probe(uint32_t * out64, hipStream_t s) {
+    hipLaunchKernelGGL(k_xcd_probe, dim3(64), dim3(64), 0, s, out64);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }

@@ -140,13 +140,15 @@ struct FaDecArgs {
     uint32_t mstride;
     const FaItem * items;    // the plan's work list (n_items items, chunk order)
     uint32_t n_items, maxtiles;
-    float * seg_o;           // [tile][4][n_head][D] segment results
-    float * seg_l;           // [tile][4][n_head] segment row sums
-    float * m_item;          // [item][n_head] chunk maxima
+    // results as (f32 bits | tag << 32): segment results [tile][4][n_head][D], segment row sums
+    // [tile][4][n_head], chunk maxima [item][n_head]
+    uint64_t * seg_o;
+    uint64_t * seg_l;
+    uint64_t * m_item;
     uint32_t * keys;         // [n_head_kv][n_items][maxtiles][4] 32-byte slots: (MAXT key, tag) of 4 heads
-    uint32_t * flags;        // [n_head_kv][n_items][maxtiles][4] the launch's tag once the segment's results are stored
     uint32_t * ep;           // [n_head_kv][reducer] epochs (zero at creation); a launch's tag is epoch + 1
-    uint32_t spin_max;       // polls of the maxima wait before it gives up (*bad = 2)
+    uint32_t spin_max;       // polls of a wait before it gives up (*bad |= 2)
+    uint32_t n_xcd;          // XCDs of the device (workgroups go to them round-robin); 0: unknown
     float * out;             // [n_head][D]
     ExpkTab ex;
     // ROPE + SET_ROWS_KV folded in (cell != 0): position *pos or the angle table rtab, new cell *cell
@@ -204,6 +206,7 @@ int tsr_launch_kv_set_rows(const tsr::KvArgs & a, uint32_t which, const float * 
                            uint64_t src_stride, const int64_t * idx, int32_t * bad, hipStream_t s);
 int tsr_launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, uint32_t n_cu, hipStream_t s);
 int tsr_launch_fa_dec(const tsr::FaDecArgs & a, hipStream_t s);
+int tsr_launch_xcd_probe(uint32_t * out64, hipStream_t s);
 int tsr_launch_rms_norm(const float * x, uint64_t x_stride, uint32_t n, uint32_t rows, float eps, float inv_n,
                         const float * w, uint64_t w_stride, uint32_t w_period, float * y, uint64_t y_stride, hipStream_t s);
 int tsr_launch_rope(const tsr::RopeArgs & a, uint32_t T, hipStream_t s);

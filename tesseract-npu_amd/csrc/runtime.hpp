@@ -126,6 +126,7 @@ struct tsr_hip_ctx {
     hipStream_t stream = nullptr;
     std::mutex mtx;
     int n_cu = 0;
+    uint32_t n_xcd = 0;                 // XCDs whose round-robin of workgroups was verified at open (0: none)
     char name[128] = {0};
     tsr_hip_counters ctr{};
     tsr_scratch scratch;

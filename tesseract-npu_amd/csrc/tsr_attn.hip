@@ -503,7 +503,7 @@ struct tsr_hip_fa_plan {
     uint32_t items_max = 0, tiles_max = 0;
     uint64_t cells_max = 0;
     uint8_t * dev = nullptr;
-    size_t o_items = 0, o_S = 0, o_Mp = 0, o_OP = 0, o_LP = 0, o_SO = 0, o_SL = 0, o_MI = 0, o_TK = 0, o_FL = 0, o_EP = 0,
+    size_t o_items = 0, o_S = 0, o_Mp = 0, o_OP = 0, o_LP = 0, o_SO = 0, o_SL = 0, o_MI = 0, o_TK = 0, o_EP = 0,
            bytes = 0;
     bool set = false, general = false;
     uint32_t n_items = 0, maxtiles = 0, max_groups = 0, mstride = 0;   // the shape a launch bakes in
@@ -543,14 +543,14 @@ int tsr_hip_fa_plan_create(tsr_hip_ctx * ctx, uint32_t D, uint32_t n_head, uint3
     p->o_LP = off; off = up256(off + 4u * (size_t)items * kC * n_head);
     // the fused decode form (T == 1): per-tile segment results and row sums, and its counters
     const uint64_t ftiles = T == 1u ? tiles : 0u;
-    p->o_SO = off; off = up256(off + 4u * (size_t)ftiles * kC * n_head * D);
-    p->o_SL = off; off = up256(off + 4u * (size_t)ftiles * kC * n_head);
-    p->o_MI = off; off = up256(off + (T == 1u ? 4u * (size_t)items * n_head : 0u));
+    // (value, tag) pairs of the decode form: segment results, row sums, chunk maxima
+    p->o_SO = off; off = up256(off + 8u * (size_t)ftiles * kC * n_head * D);
+    p->o_SL = off; off = up256(off + 8u * (size_t)ftiles * kC * n_head);
+    p->o_MI = off; off = up256(off + (T == 1u ? 8u * (size_t)items * n_head : 0u));
     // zero between launches: the 16-byte slots of segment maxima (an item has <= 8 tiles of 4 channels:
     // NCG <= 128 groups) and the counters
-    // the decode form's segment slots (32 bytes), flags and per-reducer epochs (<= 4 heads x 2 value parts)
+    // the decode form's segment slots (32 bytes) and per-reducer epochs (<= 4 heads x 2 value parts)
     p->o_TK = off; off = up256(off + (T == 1u ? 32u * 8u * 4u * (size_t)items * n_head_kv : 0u));
-    p->o_FL = off; off = up256(off + (T == 1u ? 4u * 8u * 4u * (size_t)items * n_head_kv : 0u));
     p->o_EP = off; off = up256(off + (T == 1u ? 4u * 8u * (size_t)n_head_kv : 0u));
     p->bytes = off;
     std::lock_guard<std::mutex> lk(ctx->mtx);
@@ -559,8 +559,8 @@ int tsr_hip_fa_plan_create(tsr_hip_ctx * ctx, uint32_t D, uint32_t n_head, uint3
         delete p;
         return rc;
     }
-    // the counters start at zero; every fused launch leaves them at zero
-    if ((rc = hip_err(hipMemset(p->dev + p->o_TK, 0, off - p->o_TK), "hipMemset fa plan counters")) != 0 ||
+    // tags and epochs start at zero (the decode form's first launch tags with 1)
+    if ((rc = hip_err(hipMemset(p->dev, 0, off), "hipMemset fa plan")) != 0 ||
         (rc = hip_err(hipDeviceSynchronize(), "fa plan counters")) != 0) {
         (void)hipFree(p->dev);
         delete p;
@@ -655,13 +655,13 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
         d.items = (const tsr::FaItem *)(plan->dev + plan->o_items);
         d.n_items = plan->n_items;
         d.maxtiles = plan->maxtiles;
-        d.seg_o = (float *)(plan->dev + plan->o_SO);
-        d.seg_l = (float *)(plan->dev + plan->o_SL);
-        d.m_item = (float *)(plan->dev + plan->o_MI);
+        d.seg_o = (uint64_t *)(plan->dev + plan->o_SO);
+        d.seg_l = (uint64_t *)(plan->dev + plan->o_SL);
+        d.m_item = (uint64_t *)(plan->dev + plan->o_MI);
         d.keys = (uint32_t *)(plan->dev + plan->o_TK);
-        d.flags = (uint32_t *)(plan->dev + plan->o_FL);
         d.ep = (uint32_t *)(plan->dev + plan->o_EP);
         d.spin_max = ctx->fa_spin_max;
+        d.n_xcd = ctx->n_xcd;
         d.out = out_dev;
         d.ex = ctx->expk;
         if (rope != nullptr) {

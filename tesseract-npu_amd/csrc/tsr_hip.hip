@@ -63,6 +63,34 @@ void tsr_expk_table(tsr::ExpkTab * t) {
 // ---------------------------------------------------------------------------------------------
 // context
 // ---------------------------------------------------------------------------------------------
+// The dispatcher places consecutive workgroups of a launch on consecutive XCDs (round-robin); the
+// one-launch decode FLASH_ATTN_EXT relies on it to keep a KV head's workgroups on one XCD. At open, 64
+// workgroups record their XCD: n_xcd is the period of that sequence (gfx950: 32 compute units per XCD,
+// so n_cu / 32 XCDs when the whole device is visible). Any other pattern leaves n_xcd = 0 and the
+// FLASH_ATTN_EXT on the agent-coherent exchange.
+static int xcd_calibrate(tsr_hip_ctx * c) {
+    c->n_xcd = 0;
+    const uint32_t n = (c->n_cu % 32 == 0 && c->n_cu > 0 && c->n_cu <= 8 * 32) ? (uint32_t)(c->n_cu / 32) : 0u;
+    if (n == 0u) return TSR_HIP_OK;
+    uint32_t * d = nullptr;
+    int rc = hip_err(hipMalloc(&d, 64 * sizeof(uint32_t)), "hipMalloc xcd probe");
+    if (rc) return rc;
+    uint32_t h[64] = {};
+    rc = tsr_launch_xcd_probe(d, c->stream) ? TSR_HIP_E_HIP : 0;
+    if (rc == 0) rc = hip_err(hipMemcpyAsync(h, d, sizeof h, hipMemcpyDeviceToHost, c->stream), "xcd probe copy");
+    if (rc == 0) rc = hip_err(hipStreamSynchronize(c->stream), "xcd probe sync");
+    (void)hipFree(d);
+    if (rc) return rc;
+    bool ok = true;
+    uint32_t seen = 0;
+    for (uint32_t i = 0; i < 64; ++i) ok &= h[i] == h[i % n] && h[i] < 16u;
+    for (uint32_t i = 0; ok && i < n; ++i) {
+        ok &= ((seen >> h[i]) & 1u) == 0u;                        // n distinct XCDs
+        seen |= 1u << h[i];
+    }
+    if (ok) c->n_xcd = n;
+    return TSR_HIP_OK;
+}
 int tsr_hip_open(int device, tsr_hip_ctx ** out) {
     if (out == nullptr) return TSR_HIP_E_ARG;
     *out = nullptr;
@@ -82,7 +110,8 @@ int tsr_hip_open(int device, tsr_hip_ctx ** out) {
         delete c;
         return rc;
     }
-    if ((rc = tsr_fa_fixed_init(c)) != 0) {                       // the device address of the fixed FA array
+    if ((rc = tsr_fa_fixed_init(c)) != 0 ||                       // the device address of the fixed FA array
+        (rc = xcd_calibrate(c)) != 0) {
         (void)hipStreamDestroy(c->stream);
         delete c;
         return rc;

@@ -438,13 +438,14 @@ class LlamaDecoder:
         if check:
             self.check()
 
-    BAD_RANGE, BAD_WAIT = 1, 2
+    BAD_RANGE, BAD_WAIT, BAD_XCD = 1, 2, 4
 
     def check(self) -> None:
         """Wait for the device, then raise DecodeError if a launch since the last check raised the
         decoder's flag: bit 0, a token id or cache cell was out of range (GET_ROWS / SET_ROWS_KV stored
-        nothing); bit 1, the one-launch FLASH_ATTN_EXT's bounded wait for its chunk maxima expired (its
-        attention output is not valid). The flag is cleared when it is reported."""
+        nothing); bit 1, a bounded wait of the one-launch FLASH_ATTN_EXT expired; bit 2, one of its
+        workgroups ran on another XCD than its KV head's (for bits 1 and 2 the attention output is not
+        valid). The flag is cleared when it is reported."""
         self.dev.sync()
         bad = int(self.bad.read(np.int32, (1,))[0])
         if bad == 0:
@@ -454,7 +455,10 @@ class LlamaDecoder:
         if bad & self.BAD_RANGE:
             why.append("a token id or cache cell was out of range")
         if bad & self.BAD_WAIT:
-            why.append("the one-launch FLASH_ATTN_EXT's wait for its chunk maxima expired (attention not valid)")
+            why.append("a wait of the one-launch FLASH_ATTN_EXT expired (attention not valid)")
+        if bad & self.BAD_XCD:
+            why.append("a workgroup of the one-launch FLASH_ATTN_EXT ran on another XCD than its KV head's "
+                       "(attention not valid)")
         raise DecodeError(f"decode flag {bad}: " + "; ".join(why or ["unknown code"]))
 
     def read_logits(self) -> np.ndarray:

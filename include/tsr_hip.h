@@ -259,6 +259,11 @@ int tsr_hip_graph_free(tsr_hip_ctx * ctx, tsr_hip_graph * graph);
 /* ---- mask summary (the backend's MSUM producer, tsr_msum_build_f16 sw/sim/tsr_ref_at.c:646-693) --
  * words: 8 + 4 * n_q uint32 (host). Returns the flags word (bit 0 GENERAL) or a negative code. */
 int tsr_hip_msum_build_f16(const uint16_t * mask, size_t row_stride, uint32_t n_kv, uint32_t n_q, uint32_t * words);
+/* The f32 mask copy a GENERAL summary needs (tsr_msum_mask_f32, sw/sim/tsr_ref_at.c:704-715): row q of
+ * dst (16 ceil(n_kv / 16) floats) holds fdiv(f32(mask[q][j]), scale) under the f32 rule for j < n_kv and
+ * -inf after. Host only. scale must be finite, normal and > 0 (else TSR_HIP_E_ARG). */
+int tsr_hip_msum_mask_f32(const uint16_t * mask, size_t row_stride, uint32_t n_kv, uint32_t n_q, float scale,
+                          float * dst);
 
 /* ---- FLASH_ATTN_EXT ----------------------------------------------------------------------------
  * GGML_OP_FLASH_ATTN_EXT with f32 q and a q8_0 K / V cache (the FLASH_ATTN kind, lowered by
@@ -349,6 +354,16 @@ int tsr_hip_get_rows(tsr_hip_ctx * ctx, const float * src_dev, uint64_t src_stri
  * of row r; NaN is never the largest; a row with no value above -inf gives 0. */
 int tsr_hip_argmax(tsr_hip_ctx * ctx, const float * x_dev, uint32_t n, uint32_t rows, uint64_t x_stride,
                    int32_t * out_dev, void * stream);
+
+/* ---- device flags --------------------------------------------------------------------------------
+ * Kernels that find a bad input or give up a bounded wait raise a flag word: the bad_dev argument of
+ * their entry point, or the context's own word when bad_dev is NULL (and for the entry points that
+ * take none, such as tsr_hip_flash_attn_plan): bit 0 an index outside its range (SET_ROWS_KV cell,
+ * GET_ROWS id), bit 1 an expired FLASH_ATTN_EXT wait, bit 2 a workgroup on another XCD than its KV
+ * head's (results of the launch not valid in every case). Reads the context's word, waiting for the
+ * context's stream, and clears it when clear != 0 (the backend's device-failure check after a
+ * graph_compute, ggml-tesseract.cpp:2260-2271). Not under capture. */
+int tsr_hip_get_flags(tsr_hip_ctx * ctx, int32_t * flags, int clear);
 
 /* ---- counters (the backend's TSR_STATS report, ggml-tesseract.cpp:3799-3866) --------------------- */
 typedef struct tsr_hip_counters {

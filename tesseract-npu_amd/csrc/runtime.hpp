@@ -135,6 +135,9 @@ struct tsr_hip_ctx {
     uint32_t fa_spin_max = 1u << 20;    // polls of the fused decode FA's tile-key wait (s_sleep 1 each)
     uint8_t * fa_fixed = nullptr;       // device address of this device's fixed FA array (tsr_fa_fixed_init)
     hipStream_t pick(void * s) const { return s ? (hipStream_t)s : stream; }
+    // The device flag word raised by a kernel given no flag word of its own (tsr_hip_get_flags).
+    int32_t * flags_dev = nullptr;
+    int32_t * flag(int32_t * p) const { return p ? p : flags_dev; }
 };
 
 struct tsr_hip_weight {

@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <limits>
 #include <mutex>
 #include <new>
 #include <type_traits>
@@ -99,7 +100,7 @@ int tsr_hip_kv_set_rows(tsr_hip_ctx * ctx, tsr_hip_kv * kv, uint32_t which, cons
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
     ctx->ctr.set_rows_calls++;
-    return tsr_launch_kv_set_rows(kv_args(kv), which, src_dev, n_rows, src_stride, idx_dev, bad_dev, ctx->pick(stream))
+    return tsr_launch_kv_set_rows(kv_args(kv), which, src_dev, n_rows, src_stride, idx_dev, ctx->flag(bad_dev), ctx->pick(stream))
                ? TSR_HIP_E_HIP
                : TSR_HIP_OK;
 }
@@ -124,7 +125,7 @@ int tsr_hip_rope_kv(tsr_hip_ctx * ctx, float * qkv_dev, uint32_t T, uint64_t str
     a.stride = stride;
     a.pos = pos_dev;
     a.cell = cell_dev;
-    a.bad = bad_dev;
+    a.bad = ctx->flag(bad_dev);
     a.kc = kv_args(kc);
     a.vc = kv_args(vc);
     a.head_dim = head_dim;
@@ -181,6 +182,58 @@ int tsr_hip_msum_build_f16(const uint16_t * mask, size_t row_stride, uint32_t n_
     words[3] = general ? 1u : 0u;
     words[4] = words[5] = words[6] = words[7] = 0u;
     return (int)words[3];
+}
+
+// The f32 mask copy of a GENERAL mask (tsr_msum_mask_f32, sw/sim/tsr_ref_at.c:704-715): cell j of row q
+// is fdiv(f32(mask[q][j]), scale) under the f32 rule (DAZ operands, one IEEE division, FTZ result,
+// canonical NaN), rows of 16 ceil(n_kv / 16) floats padded with -inf.
+static float host_h2f(uint16_t h) {
+    const uint32_t s = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u;
+    uint32_t u;
+    if (e == 31u) u = s | 0x7F800000u | (m ? (0x00400000u | (m << 13)) : 0u);
+    else if (e != 0u) u = s | ((e + 112u) << 23) | (m << 13);
+    else if (m == 0u) u = s;
+    else {                                                         // subnormal fp16: a normal f32
+        uint32_t k = 0, mm = m;
+        while ((mm & 0x400u) == 0u) { mm <<= 1; ++k; }
+        u = s | ((113u - k) << 23) | ((mm & 0x3FFu) << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+static float host_rule(float r) {
+    uint32_t u;
+    memcpy(&u, &r, 4);
+    const uint32_t e = u & 0x7F800000u;
+    if (e == 0u) u &= 0x80000000u;
+    else if (e == 0x7F800000u && (u & 0x007FFFFFu)) u = 0x7FC00000u;
+    memcpy(&r, &u, 4);
+    return r;
+}
+static float host_daz(float x) { return host_rule(x) == 0.0f ? std::copysign(0.0f, x) : x; }
+
+int tsr_hip_msum_mask_f32(const uint16_t * mask, size_t row_stride, uint32_t n_kv, uint32_t n_q, float scale,
+                          float * dst) {
+    if (dst == nullptr || (n_q && n_kv && mask == nullptr)) return TSR_HIP_E_ARG;
+    uint32_t sb;
+    memcpy(&sb, &scale, 4);
+    const uint32_t e = (sb >> 23) & 0xFFu;
+    if ((sb & 0x80000000u) || e == 0u || e == 0xFFu) return TSR_HIP_E_ARG;   // finite, normal and > 0
+    const size_t w = 16u * (((size_t)n_kv + 15u) / 16u);
+    const float ninf = -std::numeric_limits<float>::infinity();
+    for (uint32_t q = 0; q < n_q; ++q) {
+        const uint16_t * m = mask + (size_t)q * row_stride;
+        float * d = dst + (size_t)q * w;
+        for (uint32_t j = 0; j < n_kv; ++j) {
+            const float x = host_daz(host_h2f(m[j]));
+            if (std::isnan(x)) { d[j] = host_rule(std::numeric_limits<float>::quiet_NaN()); continue; }
+            volatile float num = x, den = scale;                   // one IEEE binary32 division
+            d[j] = host_rule(num / den);
+        }
+        for (size_t j = n_kv; j < w; ++j) d[j] = ninf;
+    }
+    return TSR_HIP_OK;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -664,11 +717,12 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
         d.n_xcd = ctx->n_xcd;
         d.out = out_dev;
         d.ex = ctx->expk;
+        d.bad = ctx->flags_dev;                              // the rope form below names its own
         if (rope != nullptr) {
             d.rtab = rope->rtab;
             d.pos = rope->pos;
             d.cell = rope->cell;
-            d.bad = rope->bad;
+            d.bad = ctx->flag(rope->bad);
             d.n_dims = rope->n_dims;
             d.neox = rope->neox;
             d.ts = rope->ts;
@@ -698,7 +752,7 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
         a.rtab = rope->rtab;
         a.pos = rope->pos;
         a.cell = rope->cell;
-        a.bad = rope->bad;
+        a.bad = ctx->flag(rope->bad);
         a.n_dims = rope->n_dims;
         a.neox = rope->neox;
         a.ts = rope->ts;

@@ -110,7 +110,7 @@ int tsr_hip_get_rows(tsr_hip_ctx * ctx, const float * src_dev, uint64_t src_stri
     if (!rows_ok(n, n_src, src_stride) || !rows_ok(n, count, y_stride)) return TSR_HIP_E_ARG;
     std::lock_guard<std::mutex> lk(ctx->mtx);
     const hipStream_t s = enter(ctx, stream);
-    return tsr_launch_get_rows(src_dev, src_stride, n, n_src, ids_dev, count, y_dev, y_stride, bad_dev, s);
+    return tsr_launch_get_rows(src_dev, src_stride, n, n_src, ids_dev, count, y_dev, y_stride, ctx->flag(bad_dev), s);
 }
 
 int tsr_hip_argmax(tsr_hip_ctx * ctx, const float * x_dev, uint32_t n, uint32_t rows, uint64_t x_stride,

@@ -111,7 +111,11 @@ int tsr_hip_open(int device, tsr_hip_ctx ** out) {
         return rc;
     }
     if ((rc = tsr_fa_fixed_init(c)) != 0 ||                       // the device address of the fixed FA array
+        (rc = hip_err(hipMalloc((void **)&c->flags_dev, 256), "hipMalloc flags")) != 0 ||
+        (rc = hip_err(hipMemsetAsync(c->flags_dev, 0, 256, c->stream), "hipMemset flags")) != 0 ||
+        (rc = hip_err(hipStreamSynchronize(c->stream), "hipStreamSynchronize")) != 0 ||
         (rc = xcd_calibrate(c)) != 0) {
+        if (c->flags_dev) (void)hipFree(c->flags_dev);
         (void)hipStreamDestroy(c->stream);
         delete c;
         return rc;
@@ -128,6 +132,7 @@ int tsr_hip_close(tsr_hip_ctx * ctx) {
         (void)hipStreamSynchronize(ctx->stream);
         ctx->scratch.release();
         ctx->staging.release();
+        if (ctx->flags_dev) (void)hipFree(ctx->flags_dev);
         (void)hipStreamDestroy(ctx->stream);
     }
     delete ctx;
@@ -141,6 +146,19 @@ int tsr_hip_sync(tsr_hip_ctx * ctx, void * stream) {
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
     return hip_err(hipStreamSynchronize(ctx->pick(stream)), "hipStreamSynchronize");
+}
+
+int tsr_hip_get_flags(tsr_hip_ctx * ctx, int32_t * flags, int clear) {
+    if (ctx == nullptr || flags == nullptr) return TSR_HIP_E_ARG;
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    if (tsr_capturing(ctx->stream)) return TSR_HIP_E_ARG;
+    int32_t v = 0;
+    int rc = hip_err(hipMemcpyAsync(&v, ctx->flags_dev, 4, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpy flags");
+    if (rc == 0 && clear && (rc = hip_err(hipMemsetAsync(ctx->flags_dev, 0, 4, ctx->stream), "hipMemset flags")) != 0) return rc;
+    if (rc == 0) rc = hip_err(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (rc == 0) *flags = v;
+    return rc;
 }
 
 int tsr_hip_device_info(tsr_hip_ctx * ctx, int * n_cu, char * name, size_t name_len, size_t * mem_free,

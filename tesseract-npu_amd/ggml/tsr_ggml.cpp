@@ -1,0 +1,1736 @@
+// tsr_ggml.cpp -- the ggml-backend adapter over libtsr_hip (include/tsr_ggml.h): buffers, supports_op,
+// lowering of a ggml graph onto the C ABI of include/tsr_hip.h, and the per-graph plan cache with HIP
+// graph replay. Host code only (C++20); it reaches the device through libtsr_hip alone.
+//
+// What it restates from the reference backend (sw/ggml-tesseract), in its own structure:
+//   - supports_op's rules (ggml-tesseract.cpp:4126-4300, tsr-build.cpp tsr_build_supports and the
+//     lowering functions it probes: tsr_lower_fa :673-773, tsr_lower_rms, tsr_lower_glu, tsr_lower_rope,
+//     tsr_lower_get_rows, tsr_lower_ew);
+//   - the MUL_MAT lowering (ggml-tesseract.cpp:2790-2928) with its ADD / SCALE / softcap fusions
+//     (tsr-build.h tsr_build_fusion: the fused node is the MUL_MAT's only user);
+//   - KV-cache buffers recognized by tensor name and shape (tsr-kvbuf.h:61-63), the mask summary built
+//     when the mask is written (tsr-msum.h), load-time conversion of other weight types to Q8_0
+//     (tsr-weights.cpp:33-49);
+//   - the plan cache keyed by graph identity (ggml-tesseract.cpp:3929-3966, 3768-3779).
+// What differs by design: there is no op list to encode; a graph lowers to a list of library calls,
+// and a graph that is met again replays its calls as one HIP graph (the MI355X form of the reference's
+// one launch per decode token), with only the FLASH_ATTN_EXT chunk lists re-planned on the host from
+// the masks of the run.
+#include "tsr_ggml.h"
+#include "tsr_hip.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+namespace {
+
+constexpr uint64_t kVBase = 0x4000000000000000ull;   // buffer addresses: never dereferenced by ggml
+constexpr uint64_t kVSpan = 1ull << 40;               // address space per buffer
+constexpr size_t kAlign = 64;
+constexpr uint32_t kKMax = 32768;                      // K_MAX (sw/sim/include/tsr_isa.h:64-67)
+constexpr uint32_t kFaTMax = 680;                      // FLASH_ATTN_EXT rows per call (tsr-build.cpp:760)
+constexpr size_t kShadowMax = 1u << 20;                // host copies of small index inputs
+constexpr size_t kMaxPlans = 16;
+
+enum Mode { kUndecided = 0, kLinear = 1, kWeights = 2, kKv = 3 };
+
+struct TypeInfo {
+    uint32_t blck = 0, size = 0;
+    tsr_gg_to_float_fn to_float = nullptr;
+    std::string name;
+};
+
+struct TInfo {                                         // a tensor init_tensor announced
+    std::string name;
+    uint64_t vaddr = 0;
+    size_t nbytes = 0;
+    int32_t type = 0;
+    int64_t ne[4] = {0, 0, 0, 0};
+    uint64_t nb[4] = {0, 0, 0, 0};
+};
+
+struct KvTensor {                                      // one KV-cache tensor of a KV buffer
+    std::string name;
+    uint64_t vaddr = 0;
+    size_t nbytes = 0, row_bytes = 0;
+    uint32_t which = 0, E = 0, kv_size = 0;
+    int layer = -1;
+    tsr_hip_kv * kv = nullptr;
+};
+
+struct Weight {                                        // a MUL_MAT weight in the library's layout
+    tsr_hip_weight * w = nullptr;
+    uint64_t vaddr = 0;
+    size_t nbytes = 0;
+    uint32_t N = 0, K = 0;
+};
+
+struct Mask {                                          // a summarized KQ mask (written by the host)
+    uint32_t n_kv = 0, n_q = 0;
+    std::vector<uint16_t> f16;                         // the mask, rows of n_kv values
+    std::vector<uint32_t> words;                       // its MSUM
+};
+
+struct FaSlot {                                        // one FLASH_ATTN_EXT of a plan
+    tsr_hip_fa_plan * plan = nullptr;
+    uint64_t mask = 0;                                 // mask data address (0: no mask)
+    uint64_t kidx = 0;                                 // the K SET_ROWS indices of the same graph (0: none)
+    uint32_t kidx_n = 0, T = 0, n_kv = 0;
+    float scale = 0.0f;
+    float * mf32 = nullptr;                            // device f32 mask copy (GENERAL summaries)
+    size_t mf32_floats = 0;
+    bool general = false;
+};
+
+struct Plan;
+struct Call {
+    tsr_gg_call info{};
+    bool capturable = true;
+    std::function<int(const Plan &)> run;
+};
+
+struct Plan {
+    std::vector<Call> calls;
+    std::vector<FaSlot> fa;
+    bool capturable = true;
+    tsr_hip_graph * graph = nullptr;
+    uint64_t used = 0, runs = 0;
+};
+
+bool is_noop(int op) {
+    return op == TSR_GG_OP_NONE || op == TSR_GG_OP_RESHAPE || op == TSR_GG_OP_VIEW || op == TSR_GG_OP_PERMUTE ||
+           op == TSR_GG_OP_TRANSPOSE;
+}
+
+float param_f32(const tsr_gg_tensor * t, int i) {
+    float f;
+    memcpy(&f, &t->op_params[i], 4);
+    return f;
+}
+
+int64_t nrows(const tsr_gg_tensor * t) { return t->ne[1] * t->ne[2] * t->ne[3]; }
+
+bool same_shape(const tsr_gg_tensor * a, const tsr_gg_tensor * b) {
+    return a->ne[0] == b->ne[0] && a->ne[1] == b->ne[1] && a->ne[2] == b->ne[2] && a->ne[3] == b->ne[3];
+}
+
+const tsr_gg_tensor * base_of(const tsr_gg_tensor * t) {
+    while (t->view_src != nullptr) t = t->view_src;
+    return t;
+}
+
+// fp32 -> fp16, round to nearest even (ggml's GGML_FP32_TO_FP16 on every host it supports).
+uint16_t f2h(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? 0x200u : 0u));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);            // rounds to infinity
+    if (ax < 0x38800000u) {                                               // fp16 subnormal or zero
+        if (ax < 0x33000000u) return (uint16_t)sign;                      // below half the smallest
+        const uint32_t e = ax >> 23, m = (ax & 0x7FFFFFu) | 0x800000u;
+        const uint32_t shift = 126u - e;                                  // 14 .. 24
+        uint32_t r = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (r & 1u))) ++r;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = ((ax >> 13) - (112u << 10));
+    const uint32_t rem = ax & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
+    return (uint16_t)(sign | r);
+}
+
+float h2f(uint16_t h) {
+    const uint32_t s = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u;
+    uint32_t u;
+    if (e == 31u) u = s | 0x7F800000u | (m << 13);
+    else if (e != 0u) u = s | ((e + 112u) << 23) | (m << 13);
+    else if (m == 0u) u = s;
+    else {
+        uint32_t k = 0, mm = m;
+        while ((mm & 0x400u) == 0u) { mm <<= 1; ++k; }
+        u = s | ((113u - k) << 23) | ((mm & 0x3FFu) << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+float bf16f(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+// ggml's quantize_row_q8_0_ref: per 32 values d = amax / 127, id = 1/d (0 if d is 0), q = roundf(x id).
+void quantize_q8_0(const float * x, int64_t K, uint8_t * out) {
+    for (int64_t b = 0; b < K / 32; ++b) {
+        const float * v = x + 32 * b;
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) amax = std::max(amax, std::fabs(v[j]));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint8_t * blk = out + 34 * b;
+        const uint16_t dh = f2h(d);
+        memcpy(blk, &dh, 2);
+        for (int j = 0; j < 32; ++j) blk[2 + j] = (uint8_t)(int8_t)std::roundf(v[j] * id);
+    }
+}
+
+uint64_t mix(uint64_t h, uint64_t v) {
+    h ^= v + 0x9E3779B97F4A7C15ull + (h << 6) + (h >> 2);
+    return h * 0xFF51AFD7ED558CCDull;
+}
+
+uint64_t key_tensor(uint64_t h, const tsr_gg_tensor * t) {
+    h = mix(h, (uint64_t)(uint32_t)t->op << 32 | (uint32_t)t->type);
+    for (int i = 0; i < 4; ++i) h = mix(mix(h, (uint64_t)t->ne[i]), t->nb[i]);
+    h = mix(h, t->data);
+    h = mix(h, (uint64_t)(uint32_t)t->flags);
+    return h;
+}
+
+// "cache_<tag>k_l<n>" / "cache_<tag>v_l<n>" (llama.cpp's KV-cache tensor names).
+bool kv_parse_name(const char * name, uint32_t * which, int * layer) {
+    if (name == nullptr || strncmp(name, "cache_", 6) != 0) return false;
+    const char * l = strrchr(name, '_');
+    if (l == nullptr || l - name < 7 || l[1] != 'l' || l[2] == '\0') return false;
+    for (const char * p = l + 2; *p; ++p)
+        if (*p < '0' || *p > '9') return false;
+    const char kv = l[-1];
+    if (kv != 'k' && kv != 'v') return false;
+    if (which) *which = kv == 'k' ? TSR_HIP_KV_K : TSR_HIP_KV_V;
+    if (layer) *layer = atoi(l + 2);
+    return true;
+}
+
+}  // namespace
+
+struct tsr_gg_buffer {
+    tsr_gg_dev * dev = nullptr;
+    uint64_t vbase = 0;
+    size_t size = 0;
+    int usage = TSR_GG_USAGE_ANY;
+    int mode = kUndecided;
+    uint8_t * mem = nullptr;                           // device memory (kLinear, kWeights)
+    std::vector<TInfo> tensors;
+    std::vector<KvTensor> kv;                          // kKv, by address
+};
+
+struct tsr_gg_dev {
+    int device = -1;
+    tsr_hip_ctx * ctx = nullptr;
+    void * stream = nullptr;
+    std::recursive_mutex mtx;
+    std::string err;
+    std::vector<TypeInfo> foreign;
+    std::vector<tsr_gg_buffer *> buffers;
+    uint64_t next_vbase = kVBase;
+    std::map<uint64_t, Weight> weights;                // by data address
+    std::map<uint64_t, Mask> masks;                    // by data address
+    std::map<uint64_t, std::vector<uint8_t>> shadows;  // host copies of I32 / I64 inputs, by data address
+    std::map<uint64_t, Plan> plans;
+    uint64_t stamp = 0, epoch = 0;
+    tsr_gg_stats st{};
+
+    int fail(int code, const char * fmt, ...) {
+        char b[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(b, sizeof b, fmt, ap);
+        va_end(ap);
+        err = b;
+        return code;
+    }
+    int hip(int rc, const char * what) {
+        return rc == TSR_HIP_OK ? TSR_GG_OK : fail(rc == TSR_HIP_E_NOMEM ? TSR_GG_E_NOMEM : TSR_GG_E_DEVICE,
+                                                   "%s: %s", what, tsr_hip_strerror(rc));
+    }
+};
+
+namespace {
+
+bool type_info(const tsr_gg_dev * d, int32_t type, TypeInfo * out) {
+    switch (type) {
+        case TSR_GG_TYPE_F32: *out = {1, 4, nullptr, "f32"}; return true;
+        case TSR_GG_TYPE_F16: *out = {1, 2, nullptr, "f16"}; return true;
+        case TSR_GG_TYPE_BF16: *out = {1, 2, nullptr, "bf16"}; return true;
+        case TSR_GG_TYPE_Q8_0: *out = {32, 34, nullptr, "q8_0"}; return true;
+        case TSR_GG_TYPE_Q4_K: *out = {256, 144, nullptr, "q4_K"}; return true;
+        case TSR_GG_TYPE_I32: *out = {1, 4, nullptr, "i32"}; return true;
+        case TSR_GG_TYPE_I64: *out = {1, 8, nullptr, "i64"}; return true;
+        default: break;
+    }
+    const int k = type - TSR_GG_TYPE_FOREIGN;
+    if (d != nullptr && k >= 0 && k < (int)d->foreign.size()) {
+        *out = d->foreign[k];
+        return true;
+    }
+    return false;
+}
+
+size_t nbytes_of(const tsr_gg_dev * d, const tsr_gg_tensor * t) {
+    TypeInfo ti;
+    if (!type_info(d, t->type, &ti) || ti.blck == 0) return 0;
+    size_t n = (size_t)t->ne[0] / ti.blck * ti.size;
+    for (int i = 1; i < 4; ++i) n += (size_t)(t->ne[i] - 1) * t->nb[i];
+    return n;
+}
+
+bool contiguous(const tsr_gg_dev * d, const tsr_gg_tensor * t) {
+    TypeInfo ti;
+    if (!type_info(d, t->type, &ti) || ti.blck == 0 || t->ne[0] % ti.blck != 0) return false;
+    uint64_t s = ti.size;
+    if (t->nb[0] != s) return false;
+    s = (uint64_t)t->ne[0] / ti.blck * ti.size;
+    for (int i = 1; i < 4; ++i) {
+        if (t->ne[i] > 1 && t->nb[i] != s) return false;
+        s *= (uint64_t)t->ne[i];
+    }
+    return true;
+}
+
+// A weight type the device can hold: Q8_0 / Q4_K natively, F32 / F16 / BF16 and registered types by
+// conversion to Q8_0 (tsr_type_loadable, tsr-weights.cpp).
+bool loadable(const tsr_gg_dev * d, int32_t type) {
+    TypeInfo ti;
+    if (!type_info(d, type, &ti)) return false;
+    return type == TSR_GG_TYPE_Q8_0 || type == TSR_GG_TYPE_Q4_K || type == TSR_GG_TYPE_F32 || type == TSR_GG_TYPE_F16 ||
+           type == TSR_GG_TYPE_BF16 || ti.to_float != nullptr;
+}
+
+tsr_gg_buffer * find_buffer(tsr_gg_dev * d, uint64_t a) {
+    for (tsr_gg_buffer * b : d->buffers)
+        if (a >= b->vbase && a < b->vbase + std::max<size_t>(b->size, 1)) return b;
+    return nullptr;
+}
+
+bool kv_identify(const tsr_gg_dev * d, const TInfo & t, KvTensor * out, std::string * why) {
+    uint32_t which = 0;
+    int layer = -1;
+    if (!kv_parse_name(t.name.c_str(), &which, &layer)) {
+        if (why) *why = "not named cache_<tag>k_l<n> / cache_<tag>v_l<n>";
+        return false;
+    }
+    const int64_t E = t.ne[0], cells = t.ne[1];
+    if (t.type != TSR_GG_TYPE_Q8_0 || t.ne[2] != 1 || t.ne[3] != 1 || E % 64 != 0 || E < 64 || E > (int64_t)kKMax ||
+        cells < 1 || cells > 0x7FFFFFFF) {
+        if (why) *why = "a KV cache the device holds is q8_0 [E, kv_size, 1] with E % 64 == 0 and 64 <= E <= 32768 (one stream)";
+        return false;
+    }
+    const size_t row = (size_t)E / 32 * 34;
+    if (t.nb[0] != 34 || t.nb[1] != row) {
+        if (why) *why = "the KV cache tensor is not contiguous";
+        return false;
+    }
+    (void)d;
+    out->name = t.name;
+    out->vaddr = t.vaddr;
+    out->nbytes = row * (size_t)cells;
+    out->row_bytes = row;
+    out->which = which;
+    out->layer = layer;
+    out->E = (uint32_t)E;
+    out->kv_size = (uint32_t)cells;
+    return true;
+}
+
+// The storage of a buffer, decided at its first data access: KV planes when every tensor announced is
+// a KV-cache tensor, else device memory.
+int decide(tsr_gg_dev * d, tsr_gg_buffer * b) {
+    if (b->mode != kUndecided) return TSR_GG_OK;
+    if (b->usage != TSR_GG_USAGE_WEIGHTS && !b->tensors.empty()) {
+        std::vector<KvTensor> kv;
+        bool all = true;
+        for (const TInfo & t : b->tensors) {
+            KvTensor k;
+            if (!kv_identify(d, t, &k, nullptr)) { all = false; break; }
+            kv.push_back(k);
+        }
+        if (all) {
+            std::sort(kv.begin(), kv.end(), [](const KvTensor & a, const KvTensor & c) { return a.vaddr < c.vaddr; });
+            for (size_t i = 1; i < kv.size(); ++i)
+                if (kv[i].vaddr < kv[i - 1].vaddr + kv[i - 1].nbytes)
+                    return d->fail(TSR_GG_E_ARG, "KV buffer: tensors '%s' and '%s' overlap", kv[i - 1].name.c_str(),
+                                   kv[i].name.c_str());
+            if (d->ctx != nullptr) {
+                for (KvTensor & k : kv) {
+                    const int rc = tsr_hip_kv_create(d->ctx, k.E, k.kv_size, &k.kv);
+                    if (rc) {
+                        for (KvTensor & f : kv) if (f.kv) tsr_hip_kv_free(d->ctx, f.kv);
+                        return d->hip(rc, "KV planes");
+                    }
+                }
+            }
+            b->kv = std::move(kv);
+            b->mode = kKv;
+            return TSR_GG_OK;
+        }
+    }
+    if (d->ctx != nullptr && b->size > 0) {
+        void * p = nullptr;
+        const int rc = tsr_hip_alloc(d->ctx, b->size, &p);
+        if (rc) return d->hip(rc, "buffer memory");
+        b->mem = (uint8_t *)p;
+    }
+    b->mode = b->usage == TSR_GG_USAGE_WEIGHTS ? kWeights : kLinear;
+    return TSR_GG_OK;
+}
+
+// Plans hold device pointers of weights, planes and buffers: a change to any of them empties the cache.
+void drop_plans(tsr_gg_dev * d) {
+    for (auto & [k, p] : d->plans) {
+        if (p.graph) tsr_hip_graph_free(d->ctx, p.graph);
+        for (FaSlot & f : p.fa) {
+            if (f.plan) tsr_hip_fa_plan_free(d->ctx, f.plan);
+            if (f.mf32) tsr_hip_free(d->ctx, f.mf32);
+        }
+    }
+    d->plans.clear();
+    ++d->epoch;
+}
+
+void drop_weights_in(tsr_gg_dev * d, uint64_t lo, uint64_t hi) {
+    bool any = false;
+    for (auto it = d->weights.begin(); it != d->weights.end();) {
+        const Weight & w = it->second;
+        if (w.vaddr < hi && w.vaddr + w.nbytes > lo) {
+            if (!any) drop_plans(d);
+            any = true;
+            if (d->ctx && w.w) tsr_hip_weight_free(d->ctx, w.w);
+            it = d->weights.erase(it);
+        } else {
+            ++it;
+        }
+    }
+}
+
+// KV buffers: byte ranges of the ggml images, across tensors.
+int kv_access(tsr_gg_dev * d, tsr_gg_buffer * b, uint64_t addr, size_t n, const uint8_t * src, uint8_t * dst,
+              int value) {
+    uint64_t a = addr;
+    const uint64_t end = addr + n;
+    std::vector<uint8_t> fill;
+    for (const KvTensor & k : b->kv) {
+        if (a >= end) break;
+        if (k.vaddr + k.nbytes <= a) continue;
+        if (k.vaddr > a)
+            return d->fail(TSR_GG_E_ARG, "KV buffer: bytes at 0x%llx lie between tensors", (unsigned long long)a);
+        const uint64_t e = std::min<uint64_t>(end, k.vaddr + k.nbytes);
+        const size_t off = a - k.vaddr, len = e - a;
+        int rc;
+        if (src) rc = tsr_hip_kv_set_bytes(d->ctx, k.kv, k.which, off, src + (a - addr), len);
+        else if (dst) rc = tsr_hip_kv_get_bytes(d->ctx, k.kv, k.which, off, dst + (a - addr), len);
+        else {
+            constexpr size_t kChunk = 8u << 20;
+            fill.assign(std::min(len, kChunk), (uint8_t)value);
+            rc = TSR_HIP_OK;
+            for (size_t o = 0; o < len && rc == TSR_HIP_OK; o += kChunk)
+                rc = tsr_hip_kv_set_bytes(d->ctx, k.kv, k.which, off + o, fill.data(), std::min(kChunk, len - o));
+        }
+        if (rc) return d->hip(rc, k.name.c_str());
+        a = e;
+    }
+    if (a < end) return d->fail(TSR_GG_E_ARG, "KV buffer: bytes at 0x%llx lie outside its tensors", (unsigned long long)a);
+    return TSR_GG_OK;
+}
+
+// The KV tensor an address of a KV buffer falls in, with the cell.
+const KvTensor * kv_at(tsr_gg_dev * d, uint64_t a, uint32_t * cell, uint32_t * byte_in_row) {
+    tsr_gg_buffer * b = find_buffer(d, a);
+    if (b == nullptr || decide(d, b) != TSR_GG_OK || b->mode != kKv) return nullptr;
+    for (const KvTensor & k : b->kv)
+        if (a >= k.vaddr && a < k.vaddr + k.nbytes) {
+            *cell = (uint32_t)((a - k.vaddr) / k.row_bytes);
+            *byte_in_row = (uint32_t)((a - k.vaddr) % k.row_bytes);
+            return &k;
+        }
+    return nullptr;
+}
+
+// The KV-cache tensor a (view of a) tensor names, for supports_op before placement: its base tensor's
+// announced shape (the buffer may still be undecided).
+bool kv_probe(tsr_gg_dev * d, const tsr_gg_tensor * t, KvTensor * out, std::string * why) {
+    const tsr_gg_tensor * bt = base_of(t);
+    TInfo ti;
+    ti.name = bt->name;
+    ti.vaddr = bt->data;
+    ti.type = bt->type;
+    memcpy(ti.ne, bt->ne, sizeof ti.ne);
+    memcpy(ti.nb, bt->nb, sizeof ti.nb);
+    if (bt->buffer == nullptr || bt->buffer->usage == TSR_GG_USAGE_WEIGHTS) {
+        if (why) *why = "not a KV-cache tensor in a buffer of this device";
+        return false;
+    }
+    if (bt->buffer->mode != kUndecided && bt->buffer->mode != kKv) {
+        if (why) *why = "its buffer holds other tensors than KV caches (device memory, not KV planes)";
+        return false;
+    }
+    return kv_identify(d, ti, out, why);
+}
+
+// Device address of [a, a + n) in a device-memory buffer (a probe device answers the address itself).
+bool dev_ptr(tsr_gg_dev * d, uint64_t a, size_t n, void ** p, std::string * why) {
+    tsr_gg_buffer * b = find_buffer(d, a);
+    if (b == nullptr) {
+        if (why) *why = "not in a buffer of this device";
+        return false;
+    }
+    if (decide(d, b) != TSR_GG_OK) {
+        if (why) *why = d->err;
+        return false;
+    }
+    if (b->mode != kLinear && b->mode != kWeights) {
+        if (why) *why = "in a KV buffer (planes, not rows)";
+        return false;
+    }
+    if (a + n > b->vbase + b->size) {
+        if (why) *why = "extends past its buffer";
+        return false;
+    }
+    *p = d->ctx ? (void *)(b->mem + (a - b->vbase)) : (void *)(uintptr_t)a;
+    return true;
+}
+
+// Rows of f32 values: n per row, rows equally strided (floats).
+struct Rows {
+    uint64_t a = 0;
+    void * p = nullptr;
+    uint32_t n = 0, rows = 0;
+    uint64_t stride = 0;
+};
+
+bool f32_rows(tsr_gg_dev * d, const tsr_gg_tensor * t, const char * what, Rows * r, std::string * why) {
+    char b[256];
+    if (t->type != TSR_GG_TYPE_F32 || t->nb[0] != 4 || t->nb[1] % 4 != 0) {
+        snprintf(b, sizeof b, "%s '%s' is not f32 rows", what, t->name);
+        *why = b;
+        return false;
+    }
+    if ((t->ne[2] > 1 && t->nb[2] != t->nb[1] * (uint64_t)t->ne[1]) ||
+        (t->ne[3] > 1 && t->nb[3] != t->nb[2] * (uint64_t)t->ne[2])) {
+        snprintf(b, sizeof b, "%s '%s': its rows are not equally spaced", what, t->name);
+        *why = b;
+        return false;
+    }
+    const int64_t rr = nrows(t);
+    if (t->ne[0] < 1 || rr < 1 || t->ne[0] > 0x7FFFFFFF || rr > 0x7FFFFFFF) {
+        snprintf(b, sizeof b, "%s '%s' is empty or too large", what, t->name);
+        *why = b;
+        return false;
+    }
+    r->a = t->data;
+    r->n = (uint32_t)t->ne[0];
+    r->rows = (uint32_t)rr;
+    r->stride = rr > 1 ? t->nb[1] / 4 : (uint64_t)t->ne[0];
+    if (rr > 1 && r->stride < r->n) {
+        snprintf(b, sizeof b, "%s '%s': rows overlap", what, t->name);
+        *why = b;
+        return false;
+    }
+    const size_t bytes = ((size_t)(r->rows - 1) * r->stride + r->n) * 4;
+    std::string w2;
+    if (!dev_ptr(d, r->a, bytes, &r->p, &w2)) {
+        snprintf(b, sizeof b, "%s '%s' %s", what, t->name, w2.c_str());
+        *why = b;
+        return false;
+    }
+    return true;
+}
+
+// [lo, hi) of the bytes rows span
+void span(const Rows & r, uint64_t * lo, uint64_t * hi) {
+    *lo = r.a;
+    *hi = r.a + ((uint64_t)(r.rows - 1) * r.stride + r.n) * 4;
+}
+bool overlap(const Rows & a, const Rows & b) {
+    uint64_t l0, h0, l1, h1;
+    span(a, &l0, &h0);
+    span(b, &l1, &h1);
+    return l0 < h1 && l1 < h0;
+}
+bool same_rows(const Rows & a, const Rows & b) { return a.a == b.a && a.stride == b.stride && a.n == b.n && a.rows == b.rows; }
+
+// The weight of a MUL_MAT: converted from the buffer's ggml bytes when first used.
+int weight_of(tsr_gg_dev * d, const tsr_gg_tensor * t, bool build, Weight ** out, std::string * why) {
+    const uint64_t a = t->data;
+    auto it = d->weights.find(a);
+    if (it != d->weights.end()) {
+        if (it->second.N != (uint32_t)t->ne[1] || it->second.K != (uint32_t)t->ne[0]) {
+            *why = "a view of a converted weight with another shape";
+            return TSR_GG_E_UNSUPPORTED;
+        }
+        *out = &it->second;
+        return TSR_GG_OK;
+    }
+    const size_t nb = nbytes_of(d, t);
+    void * p = nullptr;
+    if (!dev_ptr(d, a, nb, &p, why)) return TSR_GG_E_UNSUPPORTED;
+    Weight w;
+    w.vaddr = a;
+    w.nbytes = nb;
+    w.N = (uint32_t)t->ne[1];
+    w.K = (uint32_t)t->ne[0];
+    if (!build || d->ctx == nullptr) {
+        static Weight probe;
+        probe = w;
+        *out = &probe;
+        return TSR_GG_OK;
+    }
+    std::vector<uint8_t> raw(nb);
+    int rc = tsr_hip_read(d->ctx, raw.data(), p, nb);
+    if (rc) return d->hip(rc, "weight read");
+    uint32_t fmt = TSR_HIP_FMT_Q8_0;
+    const void * blocks = raw.data();
+    std::vector<uint8_t> conv;
+    if (t->type == TSR_GG_TYPE_Q4_K) fmt = TSR_HIP_FMT_Q4_K;
+    else if (t->type != TSR_GG_TYPE_Q8_0) {
+        TypeInfo ti;
+        type_info(d, t->type, &ti);
+        const size_t K = w.K, row_in = K / ti.blck * ti.size;
+        conv.resize((size_t)w.N * (K / 32) * 34);
+        std::vector<float> f(K);
+        for (uint32_t n = 0; n < w.N; ++n) {
+            const uint8_t * src = raw.data() + (size_t)n * row_in;
+            switch (t->type) {
+                case TSR_GG_TYPE_F32: memcpy(f.data(), src, K * 4); break;
+                case TSR_GG_TYPE_F16:
+                    for (size_t k = 0; k < K; ++k) { uint16_t h; memcpy(&h, src + 2 * k, 2); f[k] = h2f(h); }
+                    break;
+                case TSR_GG_TYPE_BF16:
+                    for (size_t k = 0; k < K; ++k) { uint16_t h; memcpy(&h, src + 2 * k, 2); f[k] = bf16f(h); }
+                    break;
+                default: ti.to_float(src, f.data(), (int64_t)K); break;
+            }
+            quantize_q8_0(f.data(), (int64_t)K, conv.data() + (size_t)n * (K / 32) * 34);
+        }
+        blocks = conv.data();
+    }
+    rc = tsr_hip_weight_upload(d->ctx, fmt, blocks, w.N, w.K, &w.w);
+    if (rc) return d->hip(rc, "weight upload");
+    d->st.weights_converted++;
+    auto [ins, ok] = d->weights.emplace(a, w);
+    *out = &ins->second;
+    return TSR_GG_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Lowering
+// ---------------------------------------------------------------------------------------------
+
+struct Graph {
+    const tsr_gg_tensor * const * nodes;
+    int n;
+    std::vector<int> uses;                              // uses of node i by later nodes
+    int index_of(const tsr_gg_tensor * t) const {
+        for (int i = 0; i < n; ++i) if (nodes[i] == t) return i;
+        return -1;
+    }
+    int next_real(int i) const {                        // the next node that is not a no-op
+        for (int j = i + 1; j < n; ++j) if (!is_noop(nodes[j]->op)) return j;
+        return -1;
+    }
+    bool only_user(int i, int j) const {                // node j is node i's only user, i not an output
+        if (j < 0 || uses[i] != 1 || (nodes[i]->flags & TSR_GG_FLAG_OUTPUT)) return false;
+        for (int s = 0; s < 10; ++s) if (nodes[j]->src[s] == nodes[i]) return true;
+        return false;
+    }
+};
+
+struct Lowerer {
+    tsr_gg_dev * d;
+    bool build;                                         // false: describe only (no device resources)
+    Plan * plan;
+    std::string why;
+
+    void * stream() const { return d->stream; }
+
+    Call & add(int kind, int node) {
+        plan->calls.emplace_back();
+        Call & c = plan->calls.back();
+        c.info.kind = kind;
+        c.info.node = node;
+        c.info.node2 = c.info.node3 = -1;
+        return c;
+    }
+    bool refuse(const char * fmt, ...) {
+        char b[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(b, sizeof b, fmt, ap);
+        va_end(ap);
+        why = b;
+        return false;
+    }
+
+    // MUL_MAT, with the ADD / SCALE / softcap behind it when it is their only source of this value.
+    bool mul_mat(const Graph & g, int i, int * consumed) {
+        const tsr_gg_tensor * node = g.nodes[i];
+        const tsr_gg_tensor * w = node->src[0];
+        const tsr_gg_tensor * x = node->src[1];
+        if (w == nullptr || x == nullptr) return refuse("MUL_MAT without both sources");
+        if (node->type != TSR_GG_TYPE_F32 || x->type != TSR_GG_TYPE_F32) return refuse("MUL_MAT: the result and src1 must be f32");
+        if (w->ne[2] != 1 || w->ne[3] != 1) return refuse("MUL_MAT: src0 is a batch of matrices (ne2 or ne3 not 1)");
+        if (!contiguous(d, w) || !contiguous(d, x) || !contiguous(d, node)) return refuse("MUL_MAT: an operand is not contiguous");
+        if (!loadable(d, w->type)) return refuse("MUL_MAT: the weight type has no device format (not loadable)");
+        const int64_t K = w->ne[0], N = w->ne[1];
+        if (K < 32 || K % 32 != 0 || K > (int64_t)kKMax || (w->type == TSR_GG_TYPE_Q4_K && K % 256 != 0) || N < 1 ||
+            N > 0x7FFFFFFF)
+            return refuse("MUL_MAT: K > K_MAX, K %% 32 != 0 or N out of range");
+        if (x->ne[0] != K || node->ne[0] != N || nrows(x) != nrows(node)) return refuse("MUL_MAT: shapes do not match");
+        const tsr_gg_tensor * wb = base_of(w);
+        if (wb->buffer == nullptr || wb->buffer->dev != d || wb->buffer->usage == TSR_GG_USAGE_COMPUTE)
+            return refuse("MUL_MAT: src0 is not a weight in a weights buffer of this device");
+        if (w->view_src != nullptr && (w->data != wb->data || !same_shape(w, wb)))
+            return refuse("MUL_MAT: src0 is a slice of a weight");
+        if (x->data % kAlign != 0) return refuse("MUL_MAT: src1 is not 64-byte aligned");
+        Rows X, Y;
+        if (!f32_rows(d, x, "src1", &X, &why)) return false;
+        Weight * wt = nullptr;
+        int rc = weight_of(d, w, build, &wt, &why);
+        if (rc) {
+            if (rc != TSR_GG_E_UNSUPPORTED) why = d->err;
+            return false;
+        }
+        const uint32_t T = X.rows;
+        // the fused consumer: ADD of an f32 addend (same shape, or one row), SCALE, or SCALE-TANH-SCALE
+        const tsr_gg_tensor * out = node;
+        const tsr_gg_tensor * addend = nullptr;
+        uint32_t flags = 0;
+        float s1 = 0.0f, s2 = 0.0f;
+        int n2 = -1, n3 = -1, last = i;
+        const int u = g.next_real(i);
+        if (u >= 0 && g.only_user(i, u)) {
+            const tsr_gg_tensor * un = g.nodes[u];
+            if (un->op == TSR_GG_OP_ADD && same_shape(un, node) && un->type == TSR_GG_TYPE_F32) {
+                const tsr_gg_tensor * o = un->src[0] == node ? un->src[1] : un->src[0];
+                if (o != nullptr && o != node && o->type == TSR_GG_TYPE_F32 && o->ne[0] == N &&
+                    (nrows(o) == 1 || same_shape(o, node))) {
+                    out = un;
+                    addend = o;
+                    n2 = last = u;
+                }
+            } else if (un->op == TSR_GG_OP_SCALE && param_f32(un, 1) == 0.0f && same_shape(un, node)) {
+                const int v = g.next_real(u);
+                const tsr_gg_tensor * vn = v >= 0 ? g.nodes[v] : nullptr;
+                const int z = v >= 0 ? g.next_real(v) : -1;
+                const tsr_gg_tensor * zn = z >= 0 ? g.nodes[z] : nullptr;
+                if (vn && zn && vn->op == TSR_GG_OP_UNARY && vn->op_params[0] == TSR_GG_UNARY_TANH && g.only_user(u, v) &&
+                    zn->op == TSR_GG_OP_SCALE && param_f32(zn, 1) == 0.0f && g.only_user(v, z) && same_shape(zn, node)) {
+                    out = zn;
+                    flags = TSR_HIP_MM_SOFTCAP;
+                    s1 = param_f32(un, 0);
+                    s2 = param_f32(zn, 0);
+                    n2 = u;
+                    n3 = z;
+                    last = z;
+                } else {
+                    out = un;
+                    flags = TSR_HIP_MM_SCALE;
+                    s2 = param_f32(un, 0);
+                    n2 = last = u;
+                }
+            }
+        }
+        if (!f32_rows(d, out, "dst", &Y, &why)) return false;
+        Rows A;
+        if (addend != nullptr) {
+            if (!f32_rows(d, addend, "addend", &A, &why)) return false;
+            if (overlap(A, Y) && !same_rows(A, Y)) { addend = nullptr; out = node; n2 = -1; last = i; }
+            else if (overlap(X, Y)) { addend = nullptr; out = node; n2 = -1; last = i; }
+            if (addend == nullptr && !f32_rows(d, node, "dst", &Y, &why)) return false;
+        } else if (out != node && overlap(X, Y)) {
+            out = node;
+            flags = 0;
+            n2 = n3 = -1;
+            last = i;
+            if (!f32_rows(d, node, "dst", &Y, &why)) return false;
+        }
+        if (overlap(X, Y)) return refuse("MUL_MAT: src1 and the result overlap");
+        Call & c = add(TSR_GG_CALL_MUL_MAT, i);
+        c.info.node2 = n2;
+        c.info.node3 = n3;
+        c.info.N = (uint32_t)N;
+        c.info.K = (uint32_t)K;
+        c.info.T = T;
+        c.info.flags = flags;
+        c.info.x = X.a;
+        c.info.y = Y.a;
+        c.info.add = addend ? A.a : 0;
+        c.info.w = w->data;
+        c.info.x_stride = X.stride;
+        c.info.y_stride = Y.stride;
+        c.info.add_stride = addend ? (A.rows == 1 ? 0 : A.stride) : 0;
+        c.info.scale = s1;
+        c.info.scale2 = s2;
+        c.capturable = T < 16;
+        if (build) {
+            tsr_hip_ctx * ctx = d->ctx;
+            const tsr_hip_weight * hw = wt->w;
+            const float * xp = (const float *)X.p;
+            float * yp = (float *)Y.p;
+            const float * ap = addend ? (const float *)A.p : nullptr;
+            const uint64_t xs = X.stride, ys = Y.stride, as = c.info.add_stride;
+            void * s = stream();
+            if (flags)
+                c.run = [=](const Plan &) { return tsr_hip_mul_mat_epi(ctx, hw, xp, T, xs, yp, ys, ap, as, flags, s1, s2, s); };
+            else
+                c.run = [=](const Plan &) { return tsr_hip_mul_mat(ctx, hw, xp, T, xs, yp, ys, ap, as, 0u, s); };
+        }
+        *consumed = last;
+        return true;
+    }
+
+    // RMS_NORM, with the MUL by a weight row behind it when it is the norm's only user.
+    bool rms_norm(const Graph & g, int i, int * consumed) {
+        const tsr_gg_tensor * node = g.nodes[i];
+        const tsr_gg_tensor * x = node->src[0];
+        if (x == nullptr || !same_shape(x, node) || node->type != TSR_GG_TYPE_F32) return refuse("RMS_NORM: source and result differ in shape");
+        Rows X, Y, W;
+        if (!f32_rows(d, x, "source", &X, &why)) return false;
+        const tsr_gg_tensor * out = node;
+        const tsr_gg_tensor * wt = nullptr;
+        int n2 = -1;
+        const int u = g.next_real(i);
+        if (u >= 0 && g.only_user(i, u) && g.nodes[u]->op == TSR_GG_OP_MUL && same_shape(g.nodes[u], node)) {
+            const tsr_gg_tensor * un = g.nodes[u];
+            const tsr_gg_tensor * o = un->src[0] == node ? un->src[1] : un->src[0];
+            if (o && o->type == TSR_GG_TYPE_F32 && o->ne[0] == node->ne[0] && (nrows(o) == 1 || nrows(o) == nrows(node))) {
+                out = un;
+                wt = o;
+                n2 = u;
+            }
+        }
+        if (!f32_rows(d, out, "result", &Y, &why)) return false;
+        if (wt && !f32_rows(d, wt, "weight", &W, &why)) return false;
+        if (overlap(X, Y) && !same_rows(X, Y)) return refuse("RMS_NORM: source and result overlap");
+        Call & c = add(TSR_GG_CALL_RMS_NORM, i);
+        c.info.node2 = n2;
+        c.info.N = X.n;
+        c.info.T = X.rows;
+        c.info.x = X.a;
+        c.info.y = Y.a;
+        c.info.w = wt ? W.a : 0;
+        c.info.x_stride = X.stride;
+        c.info.y_stride = Y.stride;
+        c.info.add_stride = wt ? W.stride : 0;
+        c.info.scale = param_f32(node, 0);
+        if (build) {
+            tsr_hip_ctx * ctx = d->ctx;
+            const float * xp = (const float *)X.p;
+            float * yp = (float *)Y.p;
+            const float * wp = wt ? (const float *)W.p : nullptr;
+            const uint32_t n = X.n, rows = X.rows, wper = wt ? W.rows : 1;
+            const uint64_t xs = X.stride, ys = Y.stride, ws = wt ? W.stride : 0;
+            const float eps = c.info.scale;
+            void * s = stream();
+            c.run = [=](const Plan &) { return tsr_hip_rms_norm(ctx, xp, n, rows, xs, eps, wp, ws, wper, yp, ys, s); };
+        }
+        *consumed = n2 >= 0 ? n2 : i;
+        return true;
+    }
+
+    bool add_op(const Graph & g, int i) {
+        const tsr_gg_tensor * node = g.nodes[i];
+        const tsr_gg_tensor * a = node->src[0];
+        const tsr_gg_tensor * b = node->src[1];
+        if (a == nullptr || b == nullptr || !same_shape(a, node)) return refuse("ADD: a and the result differ in shape");
+        Rows A, B, Y;
+        if (!f32_rows(d, a, "a", &A, &why) || !f32_rows(d, b, "b", &B, &why) || !f32_rows(d, node, "result", &Y, &why))
+            return false;
+        if (B.n != Y.n || (B.rows != 1 && (B.rows > Y.rows || Y.rows % B.rows != 0)) ||
+            (B.rows != 1 && B.rows != Y.rows && (node->ne[2] > 1 || node->ne[3] > 1)))
+            return refuse("ADD: b '%s' is not broadcast by whole rows", b->name);
+        if ((overlap(A, Y) && !same_rows(A, Y)) || (overlap(B, Y) && !same_rows(B, Y)))
+            return refuse("ADD: an operand and the result overlap");
+        Call & c = add(TSR_GG_CALL_ADD, i);
+        c.info.N = Y.n;
+        c.info.T = Y.rows;
+        c.info.x = A.a;
+        c.info.add = B.a;
+        c.info.y = Y.a;
+        c.info.x_stride = A.stride;
+        c.info.add_stride = B.stride;
+        c.info.y_stride = Y.stride;
+        if (build) {
+            tsr_hip_ctx * ctx = d->ctx;
+            const float * ap = (const float *)A.p;
+            const float * bp = (const float *)B.p;
+            float * yp = (float *)Y.p;
+            const uint64_t as = A.stride, bs = B.stride, ys = Y.stride;
+            const uint32_t per = B.rows, n = Y.n, rows = Y.rows;
+            void * s = stream();
+            c.run = [=](const Plan &) { return tsr_hip_add(ctx, ap, as, bp, bs, per, n, rows, yp, ys, s); };
+        }
+        return true;
+    }
+
+    bool rope(const Graph & g, int i) {
+        const tsr_gg_tensor * node = g.nodes[i];
+        const tsr_gg_tensor * x = node->src[0];
+        const tsr_gg_tensor * pos = node->src[1];
+        const tsr_gg_tensor * ff = node->src[2];
+        const int32_t n_dims = node->op_params[1], mode = node->op_params[2];
+        const float freq_base = param_f32(node, 5), freq_scale = param_f32(node, 6), ext = param_f32(node, 7),
+                    attn = param_f32(node, 8);
+        if (mode != TSR_HIP_ROPE_NORMAL && mode != TSR_HIP_ROPE_NEOX && mode != TSR_HIP_ROPE_IMROPE)
+            return refuse("ROPE mode %d (multi-section / vision) is not on the device", mode);
+        if (ext != 0.0f) return refuse("ROPE with YaRN ext_factor %g", ext);
+        if (node->op_params[15] != 0) return refuse("ROPE with a position offset");
+        if (x == nullptr || pos == nullptr || !same_shape(x, node)) return refuse("ROPE: source and result differ in shape");
+        const uint32_t hd = (uint32_t)node->ne[0], nh = (uint32_t)node->ne[1], T = (uint32_t)node->ne[2];
+        for (const tsr_gg_tensor * t : {x, node})
+            if (t->type != TSR_GG_TYPE_F32 || t->nb[0] != 4 || t->nb[1] != 4ull * hd || t->ne[3] != 1 || (T > 1 && t->nb[2] % 4))
+                return refuse("ROPE '%s' is not f32 [head_dim, n_heads, n_tokens] with contiguous heads", t->name);
+        if (n_dims < 2 || n_dims % 2 || (uint32_t)n_dims > hd || n_dims > 1024) return refuse("ROPE: n_dims %d", n_dims);
+        if (pos->type != TSR_GG_TYPE_I32 || pos->ne[0] < (mode == TSR_HIP_ROPE_IMROPE ? 4 * (int64_t)T : (int64_t)T))
+            return refuse("ROPE: positions are not I32 of n_tokens");
+        if (mode == TSR_HIP_ROPE_IMROPE && strstr(pos->name, "inp_pos") == nullptr)
+            return refuse("IMROPE: the positions '%s' are not llama.cpp's inp_pos input", pos->name);
+        if (!(freq_base > 0.0f) || !std::isfinite(freq_base)) return refuse("ROPE: freq_base %g", freq_base);
+        const uint64_t xs = T > 1 ? x->nb[2] / 4 : (uint64_t)hd * nh, ys = T > 1 ? node->nb[2] / 4 : (uint64_t)hd * nh;
+        void *xp, *yp, *pp, *fp = nullptr;
+        const size_t xb = ((size_t)(T - 1) * xs + (size_t)hd * nh) * 4, yb = ((size_t)(T - 1) * ys + (size_t)hd * nh) * 4;
+        std::string w2;
+        if (!dev_ptr(d, x->data, xb, &xp, &w2) || !dev_ptr(d, node->data, yb, &yp, &w2) ||
+            !dev_ptr(d, pos->data, 4 * (size_t)pos->ne[0], &pp, &w2))
+            return refuse("ROPE: %s", w2.c_str());
+        if (ff != nullptr) {
+            if (ff->type != TSR_GG_TYPE_F32 || ff->ne[0] < n_dims / 2 || !contiguous(d, ff))
+                return refuse("ROPE freq_factors '%s' is not an f32 vector of n_dims/2", ff->name);
+            if (!dev_ptr(d, ff->data, 4 * (size_t)ff->ne[0], &fp, &w2)) return refuse("ROPE freq_factors: %s", w2.c_str());
+        }
+        if (x->data != node->data && x->data < node->data + yb && node->data < x->data + xb)
+            return refuse("ROPE: source and result overlap");
+        Call & c = add(TSR_GG_CALL_ROPE, i);
+        c.info.N = hd;
+        c.info.K = nh;
+        c.info.T = T;
+        c.info.x = x->data;
+        c.info.y = node->data;
+        c.info.add = pos->data;
+        c.info.w = ff ? ff->data : 0;
+        c.info.x_stride = xs;
+        c.info.y_stride = ys;
+        c.info.mode = (uint32_t)mode;
+        c.info.n_dims = (uint32_t)n_dims;
+        c.info.scale = freq_base;
+        c.info.scale2 = attn;
+        if (build) {
+            tsr_hip_ctx * ctx = d->ctx;
+            void * s = stream();
+            const uint32_t nd = (uint32_t)n_dims;
+            c.run = [=](const Plan &) {
+                return tsr_hip_rope(ctx, (const float *)xp, T, xs, hd, nh, nd, mode, (const int32_t *)pp, freq_base, freq_scale,
+                                    attn, (const float *)fp, (float *)yp, ys, s);
+            };
+        }
+        return true;
+    }
+
+    bool glu(const Graph & g, int i) {
+        const tsr_gg_tensor * node = g.nodes[i];
+        if (node->op_params[0] != TSR_GG_GLU_SWIGLU) return refuse("GLU %d is not on the device (SWIGLU)", node->op_params[0]);
+        const tsr_gg_tensor * gt = node->src[0];
+        const tsr_gg_tensor * ut = node->src[1];
+        Rows G, U, Y;
+        if (!f32_rows(d, node, "result", &Y, &why)) return false;
+        if (ut != nullptr) {
+            if (!same_shape(gt, node) || !same_shape(ut, node)) return refuse("GLU: gate, up and the result differ in shape");
+            if (!f32_rows(d, gt, "gate", &G, &why) || !f32_rows(d, ut, "up", &U, &why)) return false;
+        } else {
+            if (node->op_params[1] != 0) return refuse("GLU: the swapped single form is not supported");
+            if (gt == nullptr || gt->ne[0] != 2 * node->ne[0] || nrows(gt) != nrows(node))
+                return refuse("GLU: the single form's source is not [2n, rows]");
+            if (!f32_rows(d, gt, "gate|up", &G, &why)) return false;
+            U = G;
+            U.a += 4ull * (uint64_t)node->ne[0];
+            U.p = d->ctx ? (void *)((uint8_t *)G.p + 4 * node->ne[0]) : (void *)(uintptr_t)U.a;
+            G.n = U.n = (uint32_t)node->ne[0];
+        }
+        if ((overlap(G, Y) && !same_rows(G, Y)) || (overlap(U, Y) && !same_rows(U, Y)))
+            return refuse("GLU: an operand and the result overlap");
+        Call & c = add(TSR_GG_CALL_SWIGLU, i);
+        c.info.N = Y.n;
+        c.info.T = Y.rows;
+        c.info.x = G.a;
+        c.info.add = U.a;
+        c.info.y = Y.a;
+        c.info.x_stride = G.stride;
+        c.info.add_stride = U.stride;
+        c.info.y_stride = Y.stride;
+        if (build) {
+            tsr_hip_ctx * ctx = d->ctx;
+            const float * gp = (const float *)G.p;
+            const float * up = (const float *)U.p;
+            float * yp = (float *)Y.p;
+            const uint64_t gs = G.stride, us = U.stride, ys = Y.stride;
+            const uint32_t n = Y.n, rows = Y.rows;
+            void * s = stream();
+            c.run = [=](const Plan &) { return tsr_hip_swiglu(ctx, gp, gs, up, us, n, rows, yp, ys, s); };
+        }
+        return true;
+    }
+
+    bool get_rows(const Graph & g, int i) {
+        const tsr_gg_tensor * node = g.nodes[i];
+        const tsr_gg_tensor * src = node->src[0];
+        const tsr_gg_tensor * ids = node->src[1];
+        if (src == nullptr || ids == nullptr || src->ne[2] != 1 || src->ne[3] != 1 || ids->ne[1] != 1 || ids->ne[2] != 1 ||
+            src->ne[0] != node->ne[0])
+            return refuse("GET_ROWS: only 2D sources with one id vector");
+        if (ids->type != TSR_GG_TYPE_I32) return refuse("GET_ROWS: ids are not I32");
+        Rows S, Y;
+        if (!f32_rows(d, src, "source", &S, &why) || !f32_rows(d, node, "result", &Y, &why)) return false;
+        void * ip = nullptr;
+        std::string w2;
+        if (!dev_ptr(d, ids->data, 4 * (size_t)ids->ne[0], &ip, &w2)) return refuse("GET_ROWS ids: %s", w2.c_str());
+        if (overlap(S, Y)) return refuse("GET_ROWS: source and result overlap");
+        Call & c = add(TSR_GG_CALL_GET_ROWS, i);
+        c.info.N = S.n;
+        c.info.K = S.rows;
+        c.info.T = (uint32_t)ids->ne[0];
+        c.info.w = S.a;
+        c.info.x = ids->data;
+        c.info.y = Y.a;
+        c.info.x_stride = S.stride;
+        c.info.y_stride = Y.stride;
+        if (build) {
+            tsr_hip_ctx * ctx = d->ctx;
+            const float * sp = (const float *)S.p;
+            float * yp = (float *)Y.p;
+            const uint64_t ss = S.stride, ys = Y.stride;
+            const uint32_t n = S.n, n_src = S.rows, cnt = c.info.T;
+            void * s = stream();
+            c.run = [=](const Plan &) { return tsr_hip_get_rows(ctx, sp, ss, n, n_src, (const int32_t *)ip, cnt, yp, ys, nullptr, s); };
+        }
+        return true;
+    }
+
+    bool argmax(const Graph & g, int i) {
+        const tsr_gg_tensor * node = g.nodes[i];
+        const tsr_gg_tensor * x = node->src[0];
+        Rows X;
+        if (x == nullptr || !f32_rows(d, x, "source", &X, &why)) return x ? false : refuse("ARGMAX without a source");
+        if (node->type != TSR_GG_TYPE_I32 || node->ne[0] != (int64_t)X.rows || !contiguous(d, node))
+            return refuse("ARGMAX: the result is not I32 [rows]");
+        void * yp = nullptr;
+        std::string w2;
+        if (!dev_ptr(d, node->data, 4ull * X.rows, &yp, &w2)) return refuse("ARGMAX: %s", w2.c_str());
+        Call & c = add(TSR_GG_CALL_ARGMAX, i);
+        c.info.N = X.n;
+        c.info.T = X.rows;
+        c.info.x = X.a;
+        c.info.y = node->data;
+        c.info.x_stride = X.stride;
+        if (build) {
+            tsr_hip_ctx * ctx = d->ctx;
+            const float * xp = (const float *)X.p;
+            const uint32_t n = X.n, rows = X.rows;
+            const uint64_t xs = X.stride;
+            void * s = stream();
+            c.run = [=](const Plan &) { return tsr_hip_argmax(ctx, xp, n, rows, xs, (int32_t *)yp, s); };
+        }
+        return true;
+    }
+
+    // SET_ROWS into a KV-cache tensor (the SET_ROWS_KV kind).
+    bool set_rows(const Graph & g, int i) {
+        const tsr_gg_tensor * node = g.nodes[i];
+        const tsr_gg_tensor * src = node->src[0];
+        const tsr_gg_tensor * idx = node->src[1];
+        if (src == nullptr || idx == nullptr) return refuse("SET_ROWS without both sources");
+        KvTensor kp;
+        std::string w2;
+        if (!kv_probe(d, node, &kp, &w2)) return refuse("SET_ROWS does not write a KV cache of this device: %s", w2.c_str());
+        if (node->data != base_of(node)->data) return refuse("SET_ROWS: the destination view does not start at cell 0");
+        if (idx->type != TSR_GG_TYPE_I64 || idx->ne[1] != 1 || idx->ne[2] != 1 || idx->ne[3] != 1 || !contiguous(d, idx))
+            return refuse("SET_ROWS: the indices are not one I64 vector");
+        Rows S;
+        if (!f32_rows(d, src, "rows", &S, &why)) return false;
+        if (S.n != kp.E || (int64_t)S.rows != idx->ne[0]) return refuse("SET_ROWS: rows of %u values, the cache has E = %u", S.n, kp.E);
+        void * ip = nullptr;
+        if (!dev_ptr(d, idx->data, 8 * (size_t)idx->ne[0], &ip, &w2)) return refuse("SET_ROWS indices: %s", w2.c_str());
+        Call & c = add(TSR_GG_CALL_SET_ROWS, i);
+        c.info.N = S.n;
+        c.info.T = S.rows;
+        c.info.x = S.a;
+        c.info.add = idx->data;
+        c.info.y = node->data;
+        c.info.x_stride = S.stride;
+        c.info.which = kp.which;
+        c.info.kv_size = kp.kv_size;
+        if (build) {
+            uint32_t cell, bir;
+            const KvTensor * k = kv_at(d, base_of(node)->data, &cell, &bir);
+            if (k == nullptr) return refuse("SET_ROWS: the KV cache is not placed");
+            tsr_hip_ctx * ctx = d->ctx;
+            tsr_hip_kv * kv = k->kv;
+            const uint32_t which = k->which, n_rows = S.rows;
+            const float * sp = (const float *)S.p;
+            const uint64_t ss = S.stride;
+            void * s = stream();
+            c.run = [=](const Plan &) { return tsr_hip_kv_set_rows(ctx, kv, which, sp, n_rows, ss, (const int64_t *)ip, nullptr, s); };
+        }
+        return true;
+    }
+
+    // FLASH_ATTN_EXT over one layer's K and V planes (tsr_lower_fa, tsr-build.cpp:673-773).
+    bool flash_attn(const Graph & g, int i) {
+        const tsr_gg_tensor * node = g.nodes[i];
+        const tsr_gg_tensor * q = node->src[0];
+        const tsr_gg_tensor * k = node->src[1];
+        const tsr_gg_tensor * v = node->src[2];
+        const tsr_gg_tensor * mask = node->src[3];
+        if (q == nullptr || k == nullptr || v == nullptr) return refuse("FLASH_ATTN_EXT without q / k / v");
+        if (node->src[4] != nullptr) return refuse("FLASH_ATTN_EXT with attention sinks");
+        const float scale = param_f32(node, 0), max_bias = param_f32(node, 1), softcap = param_f32(node, 2);
+        const int32_t prec = node->op_params[3], n_kv_max = node->op_params[4];
+        if (max_bias != 0.0f || softcap != 0.0f || n_kv_max != 0 || (prec != 0 && prec != 10))
+            return refuse("FLASH_ATTN_EXT with ALiBi, a softcap, n_kv_max or a precision other than F32");
+        const uint32_t D = (uint32_t)q->ne[0], T = (uint32_t)q->ne[1], H = (uint32_t)q->ne[2];
+        const uint32_t n_kv = (uint32_t)k->ne[1], Hk = (uint32_t)k->ne[2];
+        if (q->type != TSR_GG_TYPE_F32 || k->type != TSR_GG_TYPE_Q8_0 || v->type != TSR_GG_TYPE_Q8_0 || node->type != TSR_GG_TYPE_F32)
+            return refuse("FLASH_ATTN_EXT: q F32, K / V q8_0 only");
+        if ((D != 64 && D != 128 && D != 256 && D != 512) || k->ne[0] != D || v->ne[0] != D || v->ne[1] != n_kv ||
+            v->ne[2] != Hk || Hk == 0 || H % Hk != 0 || H / Hk > 64 || q->ne[3] != 1 || k->ne[3] != 1 || v->ne[3] != 1 ||
+            T < 1 || n_kv < 1)
+            return refuse("FLASH_ATTN_EXT shape: D = DK = DV in {64, 128, 256, 512}, n_head %% n_head_kv = 0, one stream");
+        if (q->nb[0] != 4 || q->nb[2] != 4ull * D || (T > 1 && q->nb[1] % 4 != 0))
+            return refuse("FLASH_ATTN_EXT: q's heads are not contiguous per token");
+        if (node->nb[0] != 4 || node->nb[1] != 4ull * D || (T > 1 && node->nb[2] % 4 != 0) || node->ne[0] != D ||
+            node->ne[1] != H || node->ne[2] != T)
+            return refuse("FLASH_ATTN_EXT: the result's layout");
+        if (T > kFaTMax) return refuse("FLASH_ATTN_EXT of %u tokens (at most %u)", T, kFaTMax);
+        if (mask != nullptr && (mask->type != TSR_GG_TYPE_F16 || mask->ne[0] != n_kv || mask->ne[1] != T || mask->ne[2] != 1 ||
+                                mask->ne[3] != 1 || mask->nb[0] != 2))
+            return refuse("FLASH_ATTN_EXT: the mask is not F16 [n_kv, n_tokens]");
+        KvTensor kk, vk;
+        std::string w2;
+        if (!kv_probe(d, k, &kk, &w2)) return refuse("FLASH_ATTN_EXT: K '%s' is not a KV cache view: %s", k->name, w2.c_str());
+        if (!kv_probe(d, v, &vk, &w2)) return refuse("FLASH_ATTN_EXT: V '%s' is not a KV cache view: %s", v->name, w2.c_str());
+        if (kk.which != TSR_HIP_KV_K || vk.which != TSR_HIP_KV_V || kk.E != Hk * D || vk.E != kk.E || vk.kv_size != kk.kv_size)
+            return refuse("FLASH_ATTN_EXT: K / V are not the K and V planes of one layer with E = n_head_kv D");
+        const size_t cell_b = (size_t)kk.E / 32 * 34, head_b = (size_t)D / 32 * 34;
+        for (const tsr_gg_tensor * t : {k, v})
+            if (t->nb[0] != 34 || (n_kv > 1 && t->nb[1] != cell_b) || (Hk > 1 && t->nb[2] != head_b) ||
+                t->data != base_of(t)->data)
+                return refuse("FLASH_ATTN_EXT: '%s' is not the cache's cells from cell 0 with heads %zu bytes apart", t->name, head_b);
+        if (n_kv > kk.kv_size) return refuse("FLASH_ATTN_EXT: %u cells of a cache of %u", n_kv, kk.kv_size);
+        const uint64_t qs = T > 1 ? q->nb[1] / 4 : (uint64_t)H * D, os = T > 1 ? node->nb[2] / 4 : (uint64_t)H * D;
+        void *qp = nullptr, *op = nullptr;
+        if (!dev_ptr(d, q->data, ((size_t)(T - 1) * qs + (size_t)H * D) * 4, &qp, &w2) ||
+            !dev_ptr(d, node->data, ((size_t)(T - 1) * os + (size_t)H * D) * 4, &op, &w2))
+            return refuse("FLASH_ATTN_EXT: %s", w2.c_str());
+        if (!(scale > 0.0f) || !std::isfinite(scale)) return refuse("FLASH_ATTN_EXT: scale %g", scale);
+        // the new cells: a SET_ROWS of this graph into the same K cache, earlier, with indices from the host
+        uint64_t kidx = 0;
+        uint32_t kidx_n = 0;
+        for (int j = 0; j < i; ++j) {
+            const tsr_gg_tensor * sj = g.nodes[j];
+            if (sj->op != TSR_GG_OP_SET_ROWS || base_of(sj)->data != base_of(k)->data || sj->src[1] == nullptr) continue;
+            const tsr_gg_tensor * ix = sj->src[1];
+            if (ix->op != TSR_GG_OP_NONE || g.index_of(ix) >= 0)
+                return refuse("FLASH_ATTN_EXT: the new-cell indices '%s' are computed by the graph, not written by the host", ix->name);
+            kidx = ix->data;
+            kidx_n = (uint32_t)ix->ne[0];
+        }
+        Call & c = add(TSR_GG_CALL_FLASH_ATTN, i);
+        c.info.D = D;
+        c.info.n_head = H;
+        c.info.n_head_kv = Hk;
+        c.info.n_kv = n_kv;
+        c.info.kv_size = kk.kv_size;
+        c.info.T = T;
+        c.info.x = q->data;
+        c.info.y = node->data;
+        c.info.add = mask ? mask->data : 0;
+        c.info.w = kidx;
+        c.info.x_stride = qs;
+        c.info.y_stride = os;
+        c.info.scale = scale;
+        c.info.K = kidx_n;
+        if (build) {
+            uint32_t cell, bir;
+            const KvTensor * kt = kv_at(d, base_of(k)->data, &cell, &bir);
+            const KvTensor * vt = kv_at(d, base_of(v)->data, &cell, &bir);
+            if (kt == nullptr || vt == nullptr) return refuse("FLASH_ATTN_EXT: the KV caches are not placed");
+            FaSlot f;
+            int rc = tsr_hip_fa_plan_create(d->ctx, D, H, Hk, T, kk.kv_size, &f.plan);
+            if (rc) { why = std::string("FA plan: ") + tsr_hip_strerror(rc); return false; }
+            f.mask = mask ? mask->data : 0;
+            f.kidx = kidx;
+            f.kidx_n = kidx_n;
+            f.T = T;
+            f.n_kv = n_kv;
+            f.scale = scale;
+            f.mf32_floats = (size_t)T * 16u * ((n_kv + 15u) / 16u);
+            plan->fa.push_back(f);
+            const size_t slot = plan->fa.size() - 1;
+            tsr_hip_ctx * ctx = d->ctx;
+            const tsr_hip_kv * kc = kt->kv;
+            const tsr_hip_kv * vc = vt->kv;
+            void * s = stream();
+            c.run = [=](const Plan & pl) {
+                const FaSlot & fs = pl.fa[slot];
+                return tsr_hip_flash_attn_plan(ctx, fs.plan, (const float *)qp, qs, kc, vc, scale,
+                                               fs.general ? fs.mf32 : nullptr, (float *)op, os, s);
+            };
+        }
+        return true;
+    }
+
+    // Every node of the graph in order; the nodes a call absorbed are skipped.
+    bool lower(const Graph & g, int * bad_node) {
+        for (int i = 0; i < g.n; ++i) {
+            const tsr_gg_tensor * node = g.nodes[i];
+            if (is_noop(node->op)) continue;
+            int consumed = i;
+            bool ok;
+            switch (node->op) {
+                case TSR_GG_OP_MUL_MAT: ok = mul_mat(g, i, &consumed); break;
+                case TSR_GG_OP_RMS_NORM: ok = rms_norm(g, i, &consumed); break;
+                case TSR_GG_OP_ADD: ok = add_op(g, i); break;
+                case TSR_GG_OP_ROPE: ok = rope(g, i); break;
+                case TSR_GG_OP_GLU: ok = glu(g, i); break;
+                case TSR_GG_OP_GET_ROWS: ok = get_rows(g, i); break;
+                case TSR_GG_OP_ARGMAX: ok = argmax(g, i); break;
+                case TSR_GG_OP_SET_ROWS: ok = set_rows(g, i); break;
+                case TSR_GG_OP_FLASH_ATTN_EXT: ok = flash_attn(g, i); break;
+                case TSR_GG_OP_MUL: ok = refuse("MUL is on the device only behind an RMS_NORM whose only user it is"); break;
+                case TSR_GG_OP_SCALE: ok = refuse("SCALE is on the device only behind a MUL_MAT (its epilogue)"); break;
+                case TSR_GG_OP_UNARY: ok = refuse("TANH is on the device only inside a MUL_MAT's softcap"); break;
+                default: ok = refuse("op %d is not on the device", node->op); break;
+            }
+            if (!ok) {
+                *bad_node = i;
+                return false;
+            }
+            // the nodes between i and the last fused one are no-ops (next_real): skip to it
+            i = consumed;
+        }
+        for (const Call & c : plan->calls) plan->capturable &= c.capturable;
+        return true;
+    }
+};
+
+Graph make_graph(const tsr_gg_tensor * const * nodes, int n) {
+    Graph g{nodes, n, std::vector<int>(n, 0)};
+    for (int j = 0; j < n; ++j)
+        for (int s = 0; s < 10; ++s) {
+            const tsr_gg_tensor * t = nodes[j]->src[s];
+            if (t == nullptr) continue;
+            for (int i = 0; i < j; ++i) if (nodes[i] == t) ++g.uses[i];
+        }
+    for (int j = 0; j < n; ++j)              // a view of node i is a user of i
+        if (nodes[j]->view_src)
+            for (int i = 0; i < j; ++i) if (nodes[i] == nodes[j]->view_src && nodes[j]->src[0] != nodes[i]) ++g.uses[i];
+    return g;
+}
+
+void free_plan(tsr_gg_dev * d, Plan & p) {
+    if (p.graph) tsr_hip_graph_free(d->ctx, p.graph);
+    p.graph = nullptr;
+    for (FaSlot & f : p.fa) {
+        if (f.plan) tsr_hip_fa_plan_free(d->ctx, f.plan);
+        if (f.mf32) tsr_hip_free(d->ctx, f.mf32);
+        f.plan = nullptr;
+        f.mf32 = nullptr;
+    }
+}
+
+// The FLASH_ATTN_EXT chunk lists of a plan from the masks and new cells of this run.
+int refresh_fa(tsr_gg_dev * d, Plan & p, bool * changed) {
+    *changed = false;
+    for (FaSlot & f : p.fa) {
+        std::vector<uint32_t> words;
+        const Mask * m = nullptr;
+        if (f.mask) {
+            auto it = d->masks.find(f.mask);
+            if (it == d->masks.end())
+                return d->fail(TSR_GG_E_UNSUPPORTED, "FLASH_ATTN_EXT: its mask was not written by the host (no summary)");
+            m = &it->second;
+            if (m->n_q != f.T || m->n_kv != f.n_kv)
+                return d->fail(TSR_GG_E_UNSUPPORTED, "FLASH_ATTN_EXT: the mask summary is %u x %u, the op %u x %u", m->n_q, m->n_kv,
+                               f.T, f.n_kv);
+            words = m->words;
+        } else {                                        // no mask: every cell visible
+            words.assign(8 + 4 * (size_t)f.T, 0u);
+            words[0] = 0x4D55534Du;
+            words[1] = f.T;
+            words[2] = f.n_kv;
+            for (uint32_t q = 0; q < f.T; ++q) words[8 + 4 * q + 1] = f.n_kv;
+        }
+        std::vector<uint32_t> runs;                     // runs of consecutive new cells
+        if (f.kidx) {
+            auto it = d->shadows.find(f.kidx);
+            if (it == d->shadows.end() || it->second.size() < 8 * (size_t)f.kidx_n)
+                return d->fail(TSR_GG_E_UNSUPPORTED, "FLASH_ATTN_EXT: the new-cell indices were not written by the host");
+            const int64_t * ix = (const int64_t *)it->second.data();
+            for (uint32_t j = 0; j < f.kidx_n; ++j) {
+                if (ix[j] < 0 || ix[j] > 0xFFFFFFFFll) return d->fail(TSR_GG_E_ARG, "FLASH_ATTN_EXT: new cell %lld", (long long)ix[j]);
+                const uint32_t c = (uint32_t)ix[j];
+                if (!runs.empty() && runs.back() == c) runs.back() = c + 1;
+                else { runs.push_back(c); runs.push_back(c + 1); }
+            }
+        }
+        f.general = (words[3] & 1u) != 0;
+        if (f.general) {
+            if (f.mf32 == nullptr) {
+                void * pm = nullptr;
+                const int rc = tsr_hip_alloc(d->ctx, f.mf32_floats * 4, &pm);
+                if (rc) return d->hip(rc, "FA mask copy");
+                f.mf32 = (float *)pm;
+            }
+            std::vector<float> mf(f.mf32_floats);
+            int rc = tsr_hip_msum_mask_f32(m->f16.data(), m->n_kv, m->n_kv, m->n_q, f.scale, mf.data());
+            if (rc == 0) rc = tsr_hip_write(d->ctx, f.mf32, mf.data(), mf.size() * 4);
+            if (rc) return d->hip(rc, "FA mask copy");
+        }
+        int ch = 0;
+        const int rc = tsr_hip_fa_plan_set(d->ctx, f.plan, words.data(), f.general ? 1 : 0,
+                                           runs.empty() ? nullptr : (const uint32_t (*)[2])runs.data(),
+                                           (uint32_t)(runs.size() / 2), &ch, d->stream);
+        if (rc) return d->hip(rc, "FA plan");
+        *changed |= ch != 0;
+    }
+    return TSR_GG_OK;
+}
+
+int run_calls(tsr_gg_dev * d, Plan & p, const tsr_gg_tensor * const * nodes) {
+    for (Call & c : p.calls) {
+        const int rc = c.run(p);
+        if (rc) return d->fail(rc == TSR_HIP_E_NOMEM ? TSR_GG_E_NOMEM : TSR_GG_E_DEVICE, "node '%s': %s",
+                               nodes ? nodes[c.info.node]->name : "?", tsr_hip_strerror(rc));
+    }
+    return TSR_GG_OK;
+}
+
+int capture(tsr_gg_dev * d, Plan & p) {
+    if (p.graph) tsr_hip_graph_free(d->ctx, p.graph);
+    p.graph = nullptr;
+    int rc = tsr_hip_graph_begin(d->ctx, d->stream);
+    if (rc) return d->hip(rc, "graph capture");
+    const int rr = run_calls(d, p, nullptr);
+    tsr_hip_graph * gr = nullptr;
+    rc = tsr_hip_graph_end(d->ctx, d->stream, &gr);
+    if (rr) {
+        if (gr) tsr_hip_graph_free(d->ctx, gr);
+        return rr;
+    }
+    if (rc) return d->hip(rc, "graph capture");
+    p.graph = gr;
+    d->st.captures++;
+    return TSR_GG_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------------------------
+extern "C" {
+
+int tsr_gg_open(int device, tsr_gg_dev ** out) {
+    if (out == nullptr || device < -1) return TSR_GG_E_ARG;
+    *out = nullptr;
+    auto * d = new (std::nothrow) tsr_gg_dev();
+    if (d == nullptr) return TSR_GG_E_NOMEM;
+    d->device = device;
+    if (device >= 0) {
+        const int rc = tsr_hip_open(device, &d->ctx);
+        if (rc) {
+            delete d;
+            return rc == TSR_HIP_E_NODEV ? TSR_GG_E_NODEV : TSR_GG_E_DEVICE;
+        }
+        d->stream = tsr_hip_stream(d->ctx);
+    }
+    *out = d;
+    return TSR_GG_OK;
+}
+
+int tsr_gg_close(tsr_gg_dev * d) {
+    if (d == nullptr) return TSR_GG_E_ARG;
+    {
+        std::lock_guard<std::recursive_mutex> lk(d->mtx);
+        drop_plans(d);
+        for (auto & [a, w] : d->weights) if (d->ctx && w.w) tsr_hip_weight_free(d->ctx, w.w);
+        d->weights.clear();
+        while (!d->buffers.empty()) tsr_gg_buffer_free(d->buffers.back());
+        if (d->ctx) tsr_hip_close(d->ctx);
+        d->ctx = nullptr;
+    }
+    delete d;
+    return TSR_GG_OK;
+}
+
+const char * tsr_gg_last_error(const tsr_gg_dev * d) { return d ? d->err.c_str() : "no device"; }
+void * tsr_gg_hip_ctx(tsr_gg_dev * d) { return d ? (void *)d->ctx : nullptr; }
+
+int tsr_gg_register_type(tsr_gg_dev * d, const char * name, uint32_t blck_size, uint32_t type_size, tsr_gg_to_float_fn to_float,
+                         int32_t * id) {
+    if (d == nullptr || id == nullptr || to_float == nullptr || blck_size == 0 || type_size == 0 || blck_size % 32 != 0)
+        return TSR_GG_E_ARG;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    if (d->foreign.size() >= 64) return TSR_GG_E_ARG;
+    d->foreign.push_back({blck_size, type_size, to_float, name ? name : "foreign"});
+    *id = TSR_GG_TYPE_FOREIGN + (int32_t)d->foreign.size() - 1;
+    return TSR_GG_OK;
+}
+
+size_t tsr_gg_alignment(void) { return kAlign; }
+
+size_t tsr_gg_alloc_size(const tsr_gg_dev * d, const tsr_gg_tensor * t) {
+    if (t == nullptr) return 0;
+    const size_t n = nbytes_of(d, t);
+    return (n + kAlign - 1) / kAlign * kAlign;
+}
+
+int tsr_gg_buffer_alloc(tsr_gg_dev * d, size_t size, int usage, tsr_gg_buffer ** out) {
+    if (d == nullptr || out == nullptr || size >= kVSpan) return TSR_GG_E_ARG;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    auto * b = new (std::nothrow) tsr_gg_buffer();
+    if (b == nullptr) return TSR_GG_E_NOMEM;
+    b->dev = d;
+    b->vbase = d->next_vbase;
+    d->next_vbase += kVSpan;
+    b->size = (size + kAlign - 1) / kAlign * kAlign;
+    b->usage = usage;
+    d->buffers.push_back(b);
+    *out = b;
+    return TSR_GG_OK;
+}
+
+int tsr_gg_buffer_set_usage(tsr_gg_buffer * b, int usage) {
+    if (b == nullptr) return TSR_GG_E_ARG;
+    std::lock_guard<std::recursive_mutex> lk(b->dev->mtx);
+    if (b->mode != kUndecided && (usage == TSR_GG_USAGE_WEIGHTS) != (b->mode == kWeights) && b->mode != kKv)
+        b->mode = usage == TSR_GG_USAGE_WEIGHTS ? kWeights : kLinear;
+    b->usage = usage;
+    return TSR_GG_OK;
+}
+
+uint64_t tsr_gg_buffer_base(const tsr_gg_buffer * b) { return b ? b->vbase : 0; }
+size_t tsr_gg_buffer_size(const tsr_gg_buffer * b) { return b ? b->size : 0; }
+int tsr_gg_buffer_mode(const tsr_gg_buffer * b) { return b ? b->mode : -1; }
+
+int tsr_gg_buffer_init_tensor(tsr_gg_buffer * b, const tsr_gg_tensor * t) {
+    if (b == nullptr || t == nullptr) return TSR_GG_E_ARG;
+    tsr_gg_dev * d = b->dev;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    if (t->view_src != nullptr) return TSR_GG_OK;                // views add nothing
+    const size_t n = nbytes_of(d, t);
+    if (t->data < b->vbase || t->data + n > b->vbase + b->size)
+        return d->fail(TSR_GG_E_ARG, "init_tensor: '%s' lies outside its buffer", t->name);
+    if (b->mode != kUndecided)
+        return TSR_GG_OK;                                          // late tensors keep the decided storage
+    TInfo ti;
+    ti.name = t->name;
+    ti.vaddr = t->data;
+    ti.nbytes = n;
+    ti.type = t->type;
+    memcpy(ti.ne, t->ne, sizeof ti.ne);
+    memcpy(ti.nb, t->nb, sizeof ti.nb);
+    b->tensors.push_back(ti);
+    return TSR_GG_OK;
+}
+
+static int buf_enter(tsr_gg_buffer * b, const tsr_gg_tensor * t, size_t offset, size_t size, uint64_t * addr) {
+    tsr_gg_dev * d = b->dev;
+    if (d->ctx == nullptr) return d->fail(TSR_GG_E_NODEV, "a probe device has no memory");
+    const int rc = decide(d, b);
+    if (rc) return rc;
+    const uint64_t a = t ? t->data + offset : b->vbase + offset;
+    if (a < b->vbase || a + size > b->vbase + b->size)
+        return d->fail(TSR_GG_E_ARG, "bytes [0x%llx, +%zu) outside the buffer", (unsigned long long)a, size);
+    *addr = a;
+    return TSR_GG_OK;
+}
+
+int tsr_gg_buffer_set_tensor(tsr_gg_buffer * b, const tsr_gg_tensor * t, const void * data, size_t offset, size_t size) {
+    if (b == nullptr || t == nullptr || (size && data == nullptr)) return TSR_GG_E_ARG;
+    tsr_gg_dev * d = b->dev;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    uint64_t a;
+    int rc = buf_enter(b, t, offset, size, &a);
+    if (rc || size == 0) return rc;
+    if (b->mode == kKv) return kv_access(d, b, a, size, (const uint8_t *)data, nullptr, 0);
+    drop_weights_in(d, a, a + size);
+    // stream-ordered: small inputs through the library's pinned staging, the rest synchronously
+    rc = size <= 16384 ? tsr_hip_write_async(d->ctx, b->mem + (a - b->vbase), data, size, d->stream)
+                       : tsr_hip_write(d->ctx, b->mem + (a - b->vbase), data, size);
+    if (rc) return d->hip(rc, t->name);
+    // host copies: index inputs (new-cell runs) and KQ masks (their summaries)
+    const uint64_t t0 = t->data;
+    const size_t tn = nbytes_of(d, t);
+    if ((t->type == TSR_GG_TYPE_I64 || t->type == TSR_GG_TYPE_I32) && tn <= kShadowMax) {
+        std::vector<uint8_t> & sh = d->shadows[t0];
+        sh.resize(tn);
+        memcpy(sh.data() + offset, data, std::min(size, tn - offset));
+    }
+    if (t->type == TSR_GG_TYPE_F16 && strstr(t->name, "kq_mask") != nullptr && t->ne[2] == 1 && t->ne[3] == 1 &&
+        t->ne[0] >= 1 && t->ne[1] >= 1 && t->nb[0] == 2) {
+        Mask & m = d->masks[t0];
+        const uint32_t n_kv = (uint32_t)t->ne[0], n_q = (uint32_t)t->ne[1];
+        const size_t rs = t->nb[1] / 2;
+        if (m.n_kv != n_kv || m.n_q != n_q) {
+            m = Mask{};
+            m.n_kv = n_kv;
+            m.n_q = n_q;
+            m.f16.assign((size_t)n_kv * n_q, 0xFC00u);
+        }
+        // the written bytes into the dense host copy (rows of n_kv)
+        const uint8_t * src = (const uint8_t *)data;
+        for (size_t o = 0; o < size; o += 2) {
+            const size_t e = (offset + o) / 2, r = e / rs, c = e % rs;
+            if (r < n_q && c < n_kv) memcpy(&m.f16[r * n_kv + c], src + o, 2);
+        }
+        m.words.assign(8 + 4 * (size_t)n_q, 0u);
+        rc = tsr_hip_msum_build_f16(m.f16.data(), n_kv, n_kv, n_q, m.words.data());
+        if (rc < 0) return d->hip(rc, "mask summary");
+        d->st.masks_summarized++;
+    }
+    return TSR_GG_OK;
+}
+
+int tsr_gg_buffer_get_tensor(tsr_gg_buffer * b, const tsr_gg_tensor * t, void * data, size_t offset, size_t size) {
+    if (b == nullptr || t == nullptr || (size && data == nullptr)) return TSR_GG_E_ARG;
+    tsr_gg_dev * d = b->dev;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    uint64_t a;
+    int rc = buf_enter(b, t, offset, size, &a);
+    if (rc || size == 0) return rc;
+    if (b->mode == kKv) rc = kv_access(d, b, a, size, nullptr, (uint8_t *)data, 0);
+    else rc = d->hip(tsr_hip_read(d->ctx, data, b->mem + (a - b->vbase), size), t->name);
+    if (rc) return rc;
+    int32_t fl = 0;
+    rc = tsr_hip_get_flags(d->ctx, &fl, 1);
+    if (rc) return d->hip(rc, "device flags");
+    if (fl) return d->fail(TSR_GG_E_FLAG, "a kernel raised device flags 0x%x (1: an index out of range, 2: an expired "
+                                          "FLASH_ATTN_EXT wait, 4: an XCD placement check): the results are not valid", fl);
+    return TSR_GG_OK;
+}
+
+int tsr_gg_buffer_memset_tensor(tsr_gg_buffer * b, const tsr_gg_tensor * t, uint8_t value, size_t offset, size_t size) {
+    if (b == nullptr || t == nullptr) return TSR_GG_E_ARG;
+    tsr_gg_dev * d = b->dev;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    uint64_t a;
+    int rc = buf_enter(b, t, offset, size, &a);
+    if (rc || size == 0) return rc;
+    if (b->mode == kKv) return kv_access(d, b, a, size, nullptr, nullptr, value);
+    drop_weights_in(d, a, a + size);
+    auto it = d->shadows.find(t->data);
+    if (it != d->shadows.end() && offset < it->second.size())
+        memset(it->second.data() + offset, value, std::min(size, it->second.size() - offset));
+    return d->hip(tsr_hip_memset(d->ctx, b->mem + (a - b->vbase), value, size), t->name);
+}
+
+int tsr_gg_buffer_clear(tsr_gg_buffer * b, uint8_t value) {
+    if (b == nullptr) return TSR_GG_E_ARG;
+    tsr_gg_dev * d = b->dev;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    uint64_t a;
+    int rc = buf_enter(b, nullptr, 0, 0, &a);
+    if (rc) return rc;
+    if (b->mode == kKv) {
+        for (const KvTensor & k : b->kv)
+            if ((rc = kv_access(d, b, k.vaddr, k.nbytes, nullptr, nullptr, value)) != 0) return rc;
+        return TSR_GG_OK;
+    }
+    drop_weights_in(d, b->vbase, b->vbase + b->size);
+    return b->size ? d->hip(tsr_hip_memset(d->ctx, b->mem, value, b->size), "buffer clear") : TSR_GG_OK;
+}
+
+int tsr_gg_buffer_free(tsr_gg_buffer * b) {
+    if (b == nullptr) return TSR_GG_E_ARG;
+    tsr_gg_dev * d = b->dev;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    drop_plans(d);
+    const uint64_t lo = b->vbase, hi = b->vbase + kVSpan;
+    drop_weights_in(d, lo, hi);
+    for (auto it = d->masks.begin(); it != d->masks.end();) it = it->first >= lo && it->first < hi ? d->masks.erase(it) : ++it;
+    for (auto it = d->shadows.begin(); it != d->shadows.end();)
+        it = it->first >= lo && it->first < hi ? d->shadows.erase(it) : ++it;
+    if (d->ctx) {
+        if (d->stream) tsr_hip_sync(d->ctx, d->stream);
+        for (KvTensor & k : b->kv) if (k.kv) tsr_hip_kv_free(d->ctx, k.kv);
+        if (b->mem) tsr_hip_free(d->ctx, b->mem);
+    }
+    d->buffers.erase(std::remove(d->buffers.begin(), d->buffers.end(), b), d->buffers.end());
+    delete b;
+    return TSR_GG_OK;
+}
+
+int tsr_gg_supports_op(tsr_gg_dev * d, const tsr_gg_tensor * op, char * why, size_t why_len) {
+    if (d == nullptr || op == nullptr) return TSR_GG_E_ARG;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    if (is_noop(op->op)) return 1;
+    // the node alone, lowered as a one-node graph in describe mode; the fusion partners are judged by
+    // the rules of their own position (MUL behind RMS_NORM, SCALE / TANH behind MUL_MAT)
+    std::string w;
+    bool ok = true;
+    const tsr_gg_tensor * s0 = op->src[0];
+    if (op->op == TSR_GG_OP_MUL) {
+        const tsr_gg_tensor * o = s0 && s0->op == TSR_GG_OP_RMS_NORM ? op->src[1] : (op->src[1] && op->src[1]->op == TSR_GG_OP_RMS_NORM ? s0 : nullptr);
+        if (o == nullptr) { ok = false; w = "MUL is on the device only behind an RMS_NORM (its weight)"; }
+        else if (o->type != TSR_GG_TYPE_F32 || o->ne[0] != op->ne[0] || !same_shape(op, op->src[0] == o ? op->src[1] : s0)) {
+            ok = false;
+            w = "RMS_NORM + MUL: the weight is not an f32 row of the norm's width";
+        }
+    } else if (op->op == TSR_GG_OP_SCALE || op->op == TSR_GG_OP_UNARY) {
+        const bool tanh_ok = op->op == TSR_GG_OP_SCALE || op->op_params[0] == TSR_GG_UNARY_TANH;
+        const tsr_gg_tensor * up = s0;
+        while (up && (up->op == TSR_GG_OP_SCALE || up->op == TSR_GG_OP_UNARY)) up = up->src[0];
+        if (!tanh_ok || up == nullptr || up->op != TSR_GG_OP_MUL_MAT || (op->op == TSR_GG_OP_SCALE && param_f32(op, 1) != 0.0f)) {
+            ok = false;
+            w = "SCALE / TANH are on the device only as a MUL_MAT's epilogue (SCALE, or SCALE TANH SCALE)";
+        }
+    } else {
+        Plan p;
+        Lowerer L{d, false, &p, {}};
+        const tsr_gg_tensor * one[1] = {op};
+        Graph g = make_graph(one, 1);
+        int bad = -1;
+        ok = L.lower(g, &bad);
+        w = L.why;
+    }
+    if (!ok && why && why_len) snprintf(why, why_len, "%s", w.c_str());
+    return ok ? 1 : 0;
+}
+
+int tsr_gg_lower(tsr_gg_dev * d, const tsr_gg_tensor * const * nodes, int n, tsr_gg_call * out, int cap, int * n_out) {
+    if (d == nullptr || (n && nodes == nullptr) || n < 0 || n_out == nullptr || cap < 0) return TSR_GG_E_ARG;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    Plan p;
+    Lowerer L{d, false, &p, {}};
+    Graph g = make_graph(nodes, n);
+    int bad = -1;
+    const tsr_gg_stats saved = d->st;
+    const bool ok = L.lower(g, &bad);
+    d->st = saved;
+    if (!ok) return d->fail(TSR_GG_E_UNSUPPORTED, "node %d '%s': %s", bad, bad >= 0 ? nodes[bad]->name : "?", L.why.c_str());
+    *n_out = (int)p.calls.size();
+    for (int i = 0; i < (int)p.calls.size() && i < cap; ++i) out[i] = p.calls[i].info;
+    return TSR_GG_OK;
+}
+
+int tsr_gg_graph_compute(tsr_gg_dev * d, const tsr_gg_tensor * const * nodes, int n) {
+    if (d == nullptr || (n && nodes == nullptr) || n < 0) return TSR_GG_E_ARG;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    if (d->ctx == nullptr) return d->fail(TSR_GG_E_NODEV, "a probe device runs no graph");
+    d->st.graphs++;
+    const uint64_t key = tsr_gg_graph_key(nodes, n, d->epoch);
+    auto it = d->plans.find(key);
+    if (it == d->plans.end()) {
+        d->st.plan_misses++;
+        if (d->plans.size() >= kMaxPlans) {
+            auto lru = d->plans.begin();
+            for (auto j = d->plans.begin(); j != d->plans.end(); ++j) if (j->second.used < lru->second.used) lru = j;
+            free_plan(d, lru->second);
+            d->plans.erase(lru);
+        }
+        Plan p;
+        Lowerer L{d, true, &p, {}};
+        Graph g = make_graph(nodes, n);
+        int bad = -1;
+        if (!L.lower(g, &bad)) {
+            free_plan(d, p);
+            return d->fail(TSR_GG_E_UNSUPPORTED, "node %d '%s': %s", bad, bad >= 0 ? nodes[bad]->name : "?", L.why.c_str());
+        }
+        bool changed = false;
+        int rc = refresh_fa(d, p, &changed);
+        if (rc == 0) rc = run_calls(d, p, nodes);
+        d->st.calls += p.calls.size();
+        d->st.eager_runs++;
+        for (const Call & c : p.calls) d->st.fused += c.info.node2 >= 0;
+        if (rc) {
+            free_plan(d, p);
+            return rc;
+        }
+        p.used = ++d->stamp;
+        p.runs = 1;
+        d->plans.emplace(key, std::move(p));
+        return TSR_GG_OK;
+    }
+    Plan & p = it->second;
+    d->st.plan_hits++;
+    p.used = ++d->stamp;
+    bool changed = false;
+    int rc = refresh_fa(d, p, &changed);
+    if (rc) return rc;
+    d->st.calls += p.calls.size();
+    if (!p.capturable) {
+        d->st.eager_runs++;
+        return run_calls(d, p, nodes);
+    }
+    if (p.graph == nullptr || changed) {
+        if ((rc = capture(d, p)) != 0) return rc;
+    }
+    rc = tsr_hip_graph_launch(d->ctx, p.graph, d->stream);
+    if (rc == TSR_HIP_E_ARG) {                          // the scratch moved since the capture
+        if ((rc = capture(d, p)) != 0) return rc;
+        rc = tsr_hip_graph_launch(d->ctx, p.graph, d->stream);
+    }
+    if (rc) return d->hip(rc, "graph launch");
+    d->st.replays++;
+    ++p.runs;
+    return TSR_GG_OK;
+}
+
+int tsr_gg_synchronize(tsr_gg_dev * d) {
+    if (d == nullptr) return TSR_GG_E_ARG;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    if (d->ctx == nullptr) return TSR_GG_OK;
+    int rc = tsr_hip_sync(d->ctx, d->stream);
+    if (rc) return d->hip(rc, "synchronize");
+    int32_t fl = 0;
+    if ((rc = tsr_hip_get_flags(d->ctx, &fl, 1)) != 0) return d->hip(rc, "device flags");
+    if (fl) return d->fail(TSR_GG_E_FLAG, "a kernel raised device flags 0x%x (1: an index out of range, 2: an expired "
+                                          "FLASH_ATTN_EXT wait, 4: an XCD placement check): the results are not valid", fl);
+    return TSR_GG_OK;
+}
+
+int tsr_gg_get_stats(tsr_gg_dev * d, tsr_gg_stats * out) {
+    if (d == nullptr || out == nullptr) return TSR_GG_E_ARG;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    *out = d->st;
+    return TSR_GG_OK;
+}
+
+int tsr_gg_kv_parse_name(const char * name, uint32_t * which, int * layer) { return kv_parse_name(name, which, layer) ? 1 : 0; }
+
+uint64_t tsr_gg_graph_key(const tsr_gg_tensor * const * nodes, int n, uint64_t salt) {
+    uint64_t h = mix(0x243F6A8885A308D3ull, salt);
+    for (int i = 0; i < n; ++i) {
+        const tsr_gg_tensor * t = nodes[i];
+        h = key_tensor(h, t);
+        for (int p = 0; p < 16; ++p) h = mix(h, (uint64_t)(uint32_t)t->op_params[p]);
+        for (int s = 0; s < 10; ++s) {
+            if (t->src[s] == nullptr) { h = mix(h, 0x5A5Aull + (uint64_t)s); continue; }
+            h = key_tensor(h, t->src[s]);
+        }
+        h = mix(h, t->view_src ? t->view_src->data : 0);
+    }
+    return h;
+}
+
+int tsr_gg_quantize_q8_0(const float * x, int64_t K, void * blocks) {
+    if (x == nullptr || blocks == nullptr || K < 0 || K % 32 != 0) return TSR_GG_E_ARG;
+    quantize_q8_0(x, K, (uint8_t *)blocks);
+    return TSR_GG_OK;
+}
+
+}  // extern "C"

@@ -37,7 +37,7 @@ EXPORTS = (
     "tsr_hip_fa_plan_free", "tsr_hip_graph_begin", "tsr_hip_graph_end", "tsr_hip_graph_launch", "tsr_hip_graph_free",
     "tsr_hip_mul_mat_norm", "tsr_hip_rope_kv", "tsr_hip_flash_attn_plan_rope", "tsr_hip_rope_table",
     "tsr_hip_flash_attn_plan_rope_tab", "tsr_hip_mul_mat_epi", "tsr_hip_set_fa_wait_limit",
-    "tsr_hip_flash_attn_noalloc",
+    "tsr_hip_flash_attn_noalloc", "tsr_hip_get_flags", "tsr_hip_msum_mask_f32",
 )
 
 
@@ -85,6 +85,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "tsr_hip_kv_get_bytes": ([vp, vp, u32, sz, vp, sz], C.c_int),
         "tsr_hip_kv_set_rows": ([vp, vp, u32, vp, u32, u64, vp, vp, vp], C.c_int),
         "tsr_hip_msum_build_f16": ([vp, sz, u32, u32, vp], C.c_int),
+        "tsr_hip_msum_mask_f32": ([vp, sz, u32, u32, C.c_float, vp], C.c_int),
+        "tsr_hip_get_flags": ([vp, C.POINTER(C.c_int32), C.c_int], C.c_int),
         "tsr_hip_flash_attn": ([vp, vp, u32, u64, vp, vp, u32, u32, u32, C.c_float, vp, vp, vp, u32, vp, u64, vp],
                                C.c_int),
         "tsr_hip_flash_attn_noalloc": ([vp, vp, u32, u64, vp, vp, u32, u32, u32, C.c_float, vp, vp, vp, u32, vp, u64,
@@ -148,6 +150,17 @@ def msum_build_f16(mask_f16) -> np.ndarray:
     if rc < 0:
         raise TsrHipError(rc, "msum_build_f16")
     return words
+
+
+def msum_mask_f32(mask_f16, scale: float) -> np.ndarray:
+    """The f32 mask copy of a GENERAL summary (host): [n_q, 16 ceil(n_kv / 16)] f32."""
+    m = np.ascontiguousarray(mask_f16, np.float16)
+    n_q, n_kv = m.shape
+    out = np.empty((n_q, 16 * ((n_kv + 15) // 16)), np.float32)
+    rc = load().tsr_hip_msum_mask_f32(m.ctypes.data, n_kv, n_kv, n_q, float(scale), out.ctypes.data)
+    if rc < 0:
+        raise TsrHipError(rc, "msum_mask_f32")
+    return out
 
 
 class Buffer:
@@ -325,6 +338,12 @@ class Device:
 
     def sync(self, stream=None) -> None:
         _check(self.L.tsr_hip_sync(self.ctx, stream), "sync")
+
+    def get_flags(self, clear: bool = True) -> int:
+        """The context's device flag word (kernels given no flag word of their own raise it)."""
+        v = C.c_int32()
+        _check(self.L.tsr_hip_get_flags(self.ctx, C.byref(v), int(clear)), "get_flags")
+        return int(v.value)
 
     def info(self) -> dict:
         n = C.c_int()

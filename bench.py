@@ -440,14 +440,23 @@ def extra_workloads(dev, ev, stream, n: int, eager: bool = False) -> dict:
     ob = dev.alloc(4 * n_head * D)
     msum = tsr_hip.msum_build_f16(np.zeros((1, n_kv), np.float16))
     scale = np.float32(1.0 / np.sqrt(D))
-    ms, ms_eager = timed(lambda i: dev.flash_attn(qb, 1, n_head * D, caches[i % copies][0], caches[i % copies][1], D,
-                                                  n_head, n_kv_head, scale, msum, ob, n_head * D, stream=stream))
     nbytes = 2 * n_kv * E // 32 * 34 + 2 * n_head * D + 4 * n_head * D
+    # the planned entry point (the decode form: one launch, k_fa_dec), the plan set once for the mask
+    plan = dev.fa_plan(D, n_head, n_kv_head, 1, n_kv)
+    plan.set(msum)
+    ms, ms_eager = timed(lambda i: dev.flash_attn_plan(plan, qb, n_head * D, caches[i % copies][0], caches[i % copies][1],
+                                                       scale, ob, n_head * D, stream=stream))
+    # the unplanned entry point (work list planned per call on the host: QK, P.V and merge launches)
+    ms3, ms3_eager = timed(lambda i: dev.flash_attn(qb, 1, n_head * D, caches[i % copies][0], caches[i % copies][1], D,
+                                                    n_head, n_kv_head, scale, msum, ob, n_head * D, stream=stream))
     out["fa_decode_q8kv_8192_32q8kv_d128"] = {"us_per_call": round(ms * 1e3, 3), "us_per_call_eager": round(ms_eager * 1e3, 3),
                                               "algorithmic_bytes": nbytes,
                                               "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
                                               "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                              "copies": copies, "launches_per_call": 3}
+                                              "copies": copies, "launches_per_call": 1, "kernel": "k_fa_dec",
+                                              "unplanned_us_per_call": round(ms3 * 1e3, 3),
+                                              "unplanned_launches_per_call": 3}
+    plan.free()
     del caches
 
     # prefill at Llama-3-8B shapes, 512 tokens: Q8_0 MUL_MAT on the int8 matrix cores
@@ -562,12 +571,14 @@ def pmc_child(reps: int = 3) -> int:
     return 0
 
 
-def _pmc_pass(counter: str, workdir: str) -> list:
-    """One rocprofv3 --pmc pass over the child; returns [(dispatch id, kernel name, KiB)] in
-    dispatch order."""
-    out = os.path.join(workdir, "pmc_" + counter)
-    cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", counter, "--output-format", "csv",
-           "-d", out, "-o", "pmc", "--", sys.executable, os.path.abspath(__file__), "--pmc-child"]
+def _pmc_pass(counter: str, workdir: str, child: str = "--pmc-child") -> list:
+    """One rocprofv3 --pmc pass over a child; returns [(dispatch id, kernel name, value)] of the
+    counter in dispatch order. counter may name several counters (space separated): the rows then
+    carry the counter's name as a fourth field."""
+    names = counter.split()
+    out = os.path.join(workdir, "pmc_" + "_".join(names))
+    cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", *names, "--output-format", "csv",
+           "-d", out, "-o", "pmc", "--", sys.executable, os.path.abspath(__file__), child]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, cwd=workdir)
     files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
     if r.returncode != 0 and not files:
@@ -576,9 +587,62 @@ def _pmc_pass(counter: str, workdir: str) -> list:
     for f in files:
         with open(f, newline="") as fh:
             for row in csv.DictReader(fh):
-                if row.get("Counter_Name") == counter:
-                    rows.append((int(row["Dispatch_Id"]), row["Kernel_Name"], float(row["Counter_Value"])))
+                if row.get("Counter_Name") in names:
+                    rec = (int(row["Dispatch_Id"]), row["Kernel_Name"], float(row["Counter_Value"]))
+                    rows.append(rec if len(names) == 1 else rec + (row["Counter_Name"],))
     return sorted(rows)
+
+
+PREFILL_PMC = [("q8_0 512x4096x4096", 0, 4096, 4096, 0), ("q4_K 512x4096x14336", 1, 4096, 14336, 0),
+               ("q4_K+GLU 512x28672x4096", 1, 28672, 4096, tsr_hip.MM_GLU)]
+
+
+def pmc_prefill_child(reps: int = 2) -> int:
+    """Counter child for the prefill matmuls of BASELINE configs[3]: `reps` launches each of the Q8_0
+    512x4096x4096, Q4_K 512x4096x14336 and Q4_K + GLU 512x28672x4096 MUL_MATs (activation QACT kernel +
+    matrix-core kernel), in that order."""
+    dev = tsr_hip.Device(0)
+    T = 512
+    for name, fmt, N, K, flags in PREFILL_PMC:
+        w = dev.weight(fmt, S.quant_rows(fmt, S.seed_of("pmc-prefill", name), N, K), N, K)
+        x = dev.upload(S.normal(S.seed_of("pmc-prefill", "x" + name), T * K))
+        ny = N // 2 if flags else N
+        y = dev.alloc(4 * T * ny)
+        for _ in range(reps):
+            dev.mul_mat(w, x, T, K, y, ny, flags=flags)
+        dev.sync()
+        del w, x, y
+    dev.close()
+    return 0
+
+
+def measure_prefill_counters(reps: int = 2) -> dict:
+    """MFMA and VALU use of the prefill matrix-core kernels (one rocprofv3 --pmc pass: rocprofv3's
+    derived MfmaUtil = MFMA-busy cycles / (GPU-active cycles x SIMDs) and VALUBusy = active VALU
+    instruction cycles / CUs / GPU-active cycles, plus the MFMA and VALU instruction counts)."""
+    if shutil.which("rocprofv3") is None:
+        return {"error": "rocprofv3 not found"}
+    workdir = tempfile.mkdtemp(prefix="tsr_pmc_")
+    try:
+        rows = _pmc_pass("MfmaUtil VALUBusy SQ_INSTS_MFMA SQ_INSTS_VALU", workdir, "--pmc-prefill-child")
+        by = {}
+        for did, k, v, name in rows:
+            if "k_mm_" in k:
+                by.setdefault(did, {"kernel": k.split("(")[0].replace("void ", "")})[name] = v
+        disp = [by[d] for d in sorted(by)]
+        if len(disp) != reps * len(PREFILL_PMC):
+            raise RuntimeError(f"unexpected matrix-core dispatches: {len(disp)}")
+        out = {}
+        for i, (name, *_r) in enumerate(PREFILL_PMC):
+            ds = disp[reps * i:reps * (i + 1)]
+            out[name] = {"kernel": ds[-1]["kernel"],
+                         "MfmaUtil_pct": round(float(np.median([d["MfmaUtil"] for d in ds])), 2),
+                         "VALUBusy_pct": round(float(np.median([d["VALUBusy"] for d in ds])), 2),
+                         "SQ_INSTS_MFMA": int(np.median([d["SQ_INSTS_MFMA"] for d in ds])),
+                         "SQ_INSTS_VALU": int(np.median([d["SQ_INSTS_VALU"] for d in ds]))}
+        return out
+    finally:
+        shutil.rmtree(workdir, ignore_errors=True)
 
 
 def measure_traffic(reps: int = 3) -> dict:
@@ -619,9 +683,12 @@ def main() -> int:
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
     ap.add_argument("--eager", action="store_true", help="time everything as direct launches: no HIP graph is built")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--pmc-prefill-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.pmc_child:
         return pmc_child()
+    if args.pmc_prefill_child:
+        return pmc_prefill_child()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is a "
                                    "design note in DESIGN.md, not measured)"}))
@@ -631,12 +698,17 @@ def main() -> int:
         return 2
 
     # traffic passes first: child processes under rocprofv3, before this process touches the GPU
-    traffic = None
+    traffic = prefill_counters = None
     if not args.no_traffic:
         try:
             traffic = measure_traffic()
         except Exception as e:  # reported, not fatal: the timing below does not depend on it
             traffic = {"error": str(e)[:300]}
+        if not args.no_extra:
+            try:
+                prefill_counters = measure_prefill_counters()
+            except Exception as e:
+                prefill_counters = {"error": str(e)[:300]}
 
     dev = tsr_hip.Device(0)
     info = dev.info()
@@ -661,6 +733,8 @@ def main() -> int:
     m.free()
 
     also = {} if args.no_extra else extra_workloads(dev, ev, stream, 200, eager=args.eager)
+    if prefill_counters is not None:
+        also["prefill_counters"] = prefill_counters
     cpu = None if args.no_cpu else cpu_decode(e2e)
     ms_tok = e2e["ms_per_token"]
     out = {

@@ -345,6 +345,67 @@ def host_info() -> dict:
             "nproc_affinity": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
 
 
+def adapter_decode(ev, e2e, caches, steps: int) -> dict:
+    """The same decode through the ggml-backend adapter (libtsr_ggml): llama.cpp's graph of the
+    Llama-3-8B-architecture model (tsr_ggml_graph.LlamaGraph: separate Q / K / V MUL_MATs, ROPE,
+    SET_ROWS into cache tensors recognized by name, permuted FLASH_ATTN_EXT views, inp_out_ids), the
+    weights set as ggml blocks into a weights buffer, the caches as the decoder's q8_0 images into a KV
+    buffer. Token 0 is decoded at position CTX (its logits compared bit for bit with the decoder's), then
+    `steps` timed tokens at CTX + 1 .., one graph_compute each: the adapter replays its captured graph,
+    the greedy token fed back on the device (cpy_tensor from the ARGMAX result to inp_tokens)."""
+    import tsr_ggml as G
+    import tsr_ggml_graph as GL
+    cfg, wts, kv_size = e2e["cfg"], e2e["wts"], e2e["kv_size"]
+    gd = G.Device(0)
+    t0 = time.perf_counter()
+    images = {}
+    for il, (k, v) in enumerate(caches):
+        images[(il, 0)], images[(il, 1)] = k, v
+    _, W, kvt, wbuf, kvbuf = GL.load_model(gd, cfg, wts, kv_size, images)
+    g = GL.LlamaGraph(gd, cfg, W, kvt, kv_size, 1, kv_size, argmax=True)
+    nodes = gd.prepare(g.ctx.nodes)
+    g.set_inputs([e2e["tok0"]], CTX)
+    gd.graph_compute(nodes)                                # lowers, converts the weights, runs
+    logits0 = g.logits_host()
+    setup_s = time.perf_counter() - t0
+    same = bool((logits0.view(np.uint32) == e2e["logits0"].view(np.uint32)).all())
+    hstream = C.c_void_p(tsr_hip.load().tsr_hip_stream(gd.L.tsr_gg_hip_ctx(gd.h)))
+    pos = CTX + 1
+    for i in range(2):                                     # the capture, one replay
+        g.buf.cpy_tensor(g.next, g.inp_tokens)
+        g.set_position(pos)
+        gd.graph_compute(nodes)
+        pos += 1
+    gd.synchronize()
+    e0, e1 = ev.event(), ev.event()
+    s0 = gd.stats()
+    ev.record(e0, hstream)
+    h0 = time.perf_counter()
+    for i in range(steps):
+        g.buf.cpy_tensor(g.next, g.inp_tokens)
+        g.set_position(pos)
+        gd.graph_compute(nodes)
+        pos += 1
+    ev.record(e1, hstream)
+    host_ms = (time.perf_counter() - h0) * 1e3 / steps
+    ms = ev.elapsed_ms(e0, e1)
+    gd.synchronize()                                       # TSR_GG_E_FLAG if a kernel raised a flag
+    s1 = gd.stats()
+    calls = [c["name"] for c in gd.lower(g.ctx.nodes)]
+    out = {"tok_s": round(steps / (ms * 1e-3), 2), "ms_per_token": round(ms / steps, 5),
+           "host_ms_per_token": round(host_ms, 4), "replays": s1["replays"] - s0["replays"],
+           "plan_hits": s1["plan_hits"] - s0["plan_hits"], "launches_per_token": len(calls),
+           "graph_nodes": len(g.ctx.nodes), "token0_logits_bit_equal_to_decoder": same,
+           "setup_s": round(setup_s, 2),
+           "path": "tsr_gg_graph_compute over llama.cpp's graph (fused: Q|K|V + norm, ROPE+SET_ROWS+FA, "
+                   "gate|up + norm + GLU), captured once, replayed per token"}
+    g.free()
+    kvbuf.free()
+    wbuf.free()
+    gd.close()
+    return out
+
+
 def extra_workloads(dev, ev, stream, n: int, eager: bool = False) -> dict:
     """The other single-GPU BASELINE configs, each timed over rotating device copies (> 2x MALL):
     configs[1] the Q4_K FFN up/down pair, configs[0] Q8_0 matvec 4864x896, configs[2] q8-KV
@@ -682,6 +743,7 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
     ap.add_argument("--eager", action="store_true", help="time everything as direct launches: no HIP graph is built")
+    ap.add_argument("--no-adapter", action="store_true", help="skip the decode through the ggml-backend adapter")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--pmc-prefill-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -729,12 +791,17 @@ def main() -> int:
     achieved = dv["algorithmic_bytes"] / (dv["launch_us"] * 1e-6) / 1e9
     m = e2e.pop("model")
     # the CPU leg decodes from the GPU's prefilled caches (the ggml q8_0 images, read back)
-    e2e["caches"] = None if args.no_cpu else [(L["kc"].get_bytes(0), L["vc"].get_bytes(1)) for L in m.layers]
+    caches = [(L["kc"].get_bytes(0), L["vc"].get_bytes(1)) for L in m.layers]
+    e2e["caches"] = None if args.no_cpu else caches
     m.free()
+    adapter = None if args.no_adapter else adapter_decode(ev, e2e, caches, args.steps)
+    del caches
 
     also = {} if args.no_extra else extra_workloads(dev, ev, stream, 200, eager=args.eager)
     if prefill_counters is not None:
         also["prefill_counters"] = prefill_counters
+    if adapter is not None:
+        also["adapter_decode_llama3_8b_q4k"] = adapter
     cpu = None if args.no_cpu else cpu_decode(e2e)
     ms_tok = e2e["ms_per_token"]
     out = {

@@ -148,6 +148,10 @@ int tsr_gg_buffer_set_tensor(tsr_gg_buffer * buf, const tsr_gg_tensor * t, const
 int tsr_gg_buffer_get_tensor(tsr_gg_buffer * buf, const tsr_gg_tensor * t, void * data, size_t offset, size_t size);
 int tsr_gg_buffer_memset_tensor(tsr_gg_buffer * buf, const tsr_gg_tensor * t, uint8_t value, size_t offset, size_t size);
 int tsr_gg_buffer_clear(tsr_gg_buffer * buf, uint8_t value);
+/* buffer_i.cpy_tensor (ggml-tesseract.cpp:2026-2042): dst = src in the device's stream order, both in
+ * device memory of this device and of the same byte size. Returns 1 when copied, 0 when it cannot copy
+ * (ggml then copies through the host), or a negative code. */
+int tsr_gg_buffer_cpy_tensor(tsr_gg_buffer * buf, const tsr_gg_tensor * src, const tsr_gg_tensor * dst);
 int tsr_gg_buffer_free(tsr_gg_buffer * buf);
 /* The storage the buffer got: 0 undecided, 1 device memory, 2 weights, 3 KV planes. */
 int tsr_gg_buffer_mode(const tsr_gg_buffer * buf);
@@ -177,6 +181,11 @@ int tsr_gg_supports_op(tsr_gg_dev * dev, const tsr_gg_tensor * op, char * why, s
 int tsr_gg_graph_compute(tsr_gg_dev * dev, const tsr_gg_tensor * const * nodes, int n_nodes);
 int tsr_gg_synchronize(tsr_gg_dev * dev);
 
+/* Options of a device: TSR_GG_OPT_NO_FUSION lowers every node on its own (no fold, group or epilogue
+ * fusion; the results are the same bits). Plans made under other options are not reused. */
+#define TSR_GG_OPT_NO_FUSION  1u
+int tsr_gg_set_options(tsr_gg_dev * dev, uint32_t options);
+
 typedef struct tsr_gg_stats {
     uint64_t graphs, plan_hits, plan_misses, captures, replays, eager_runs;
     uint64_t calls, fused, weights_converted, masks_summarized;
@@ -185,8 +194,18 @@ int tsr_gg_get_stats(tsr_gg_dev * dev, tsr_gg_stats * out);
 
 /* ---- lowering, for inspection ---------------------------------------------------------------------
  * The calls graph_compute would make for the nodes, without running them (also on a probe device).
- * kind: one of TSR_GG_CALL_*; node / node2: the graph indices of the node and of the node fused into
- * it (-1 for none); the other fields as each call reads them (addresses are ggml data addresses). */
+ * kind: one of TSR_GG_CALL_*; node / node2 / node3: the graph indices of the node and of the nodes fused
+ * into it (-1 for none; for a MUL_MAT node3 is the RMS_NORM folded into it); the other fields as each
+ * call reads them (addresses are ggml data addresses; 0 for a plan's own buffer).
+ * graph_compute fuses llama.cpp's layer pattern into the decoder's launch list:
+ *   - RMS_NORM * w read only by MUL_MATs of fewer than 16 tokens: the norm inside each matvec;
+ *   - the Q, K, V MUL_MATs of one input, whose results only reach the ROPEs, the K / V SET_ROWS and
+ *     the FLASH_ATTN_EXT: one MUL_MAT over their rows into a plan buffer, then for one token one
+ *     ROPE + SET_ROWS_KV + FLASH_ATTN_EXT launch (TSR_GG_CALL_ROPE_TABLE once per graph), for more
+ *     tokens TSR_GG_CALL_ROPE_KV and the planned FLASH_ATTN_EXT; the K and V SET_ROWS must then write
+ *     the same cells (else graph_compute fails: TSR_GG_E_UNSUPPORTED);
+ *   - the gate and up MUL_MATs read only by a SWIGLU: one MUL_MAT with the GLU epilogue.
+ * Each fusion leaves the results bit-identical to the unfused calls. */
 #define TSR_GG_CALL_MUL_MAT     1
 #define TSR_GG_CALL_FLASH_ATTN  2
 #define TSR_GG_CALL_SET_ROWS    3
@@ -196,6 +215,8 @@ int tsr_gg_get_stats(tsr_gg_dev * dev, tsr_gg_stats * out);
 #define TSR_GG_CALL_SWIGLU      7
 #define TSR_GG_CALL_GET_ROWS    8
 #define TSR_GG_CALL_ARGMAX      9
+#define TSR_GG_CALL_ROPE_TABLE 10   /* the ROPE angles of a decode token, once per graph */
+#define TSR_GG_CALL_ROPE_KV    11   /* ROPE of q and k + SET_ROWS of k and v over a ubatch's Q|K|V rows */
 typedef struct tsr_gg_call {
     int32_t kind, node, node2, node3;
     uint32_t N, K, T, flags;            /* MUL_MAT: rows, K, tokens, TSR_HIP_MM_* ; elementwise: n, rows */

@@ -72,6 +72,7 @@ struct Weight {                                        // a MUL_MAT weight in th
     uint64_t vaddr = 0;
     size_t nbytes = 0;
     uint32_t N = 0, K = 0;
+    std::vector<std::pair<uint64_t, size_t>> parts;    // a fused weight: the ggml tensors it was made of
 };
 
 struct Mask {                                          // a summarized KQ mask (written by the host)
@@ -89,6 +90,8 @@ struct FaSlot {                                        // one FLASH_ATTN_EXT of 
     float * mf32 = nullptr;                            // device f32 mask copy (GENERAL summaries)
     size_t mf32_floats = 0;
     bool general = false;
+    uint64_t vidx = 0;                                 // the fused form: the V SET_ROWS indices (the same cells)
+    uint32_t D = 0, H = 0, Hk = 0, kv_size = 0;
 };
 
 struct Plan;
@@ -101,6 +104,7 @@ struct Call {
 struct Plan {
     std::vector<Call> calls;
     std::vector<FaSlot> fa;
+    std::vector<void *> bufs;                          // device buffers of the plan (Q|K|V rows, ROPE tables)
     bool capturable = true;
     tsr_hip_graph * graph = nullptr;
     uint64_t used = 0, runs = 0;
@@ -239,10 +243,12 @@ struct tsr_gg_dev {
     std::vector<tsr_gg_buffer *> buffers;
     uint64_t next_vbase = kVBase;
     std::map<uint64_t, Weight> weights;                // by data address
+    std::map<std::vector<uint64_t>, Weight> fused;     // concatenated / interleaved weights, by their parts
     std::map<uint64_t, Mask> masks;                    // by data address
     std::map<uint64_t, std::vector<uint8_t>> shadows;  // host copies of I32 / I64 inputs, by data address
     std::map<uint64_t, Plan> plans;
     uint64_t stamp = 0, epoch = 0;
+    uint32_t options = 0;
     tsr_gg_stats st{};
 
     int fail(int code, const char * fmt, ...) {
@@ -389,32 +395,48 @@ int decide(tsr_gg_dev * d, tsr_gg_buffer * b) {
     return TSR_GG_OK;
 }
 
+void free_plan(tsr_gg_dev * d, Plan & p) {
+    if (p.graph) tsr_hip_graph_free(d->ctx, p.graph);
+    p.graph = nullptr;
+    for (FaSlot & f : p.fa) {
+        if (f.plan) tsr_hip_fa_plan_free(d->ctx, f.plan);
+        if (f.mf32) tsr_hip_free(d->ctx, f.mf32);
+        f.plan = nullptr;
+        f.mf32 = nullptr;
+    }
+    for (void * b : p.bufs) tsr_hip_free(d->ctx, b);
+    p.bufs.clear();
+}
+
 // Plans hold device pointers of weights, planes and buffers: a change to any of them empties the cache.
 void drop_plans(tsr_gg_dev * d) {
-    for (auto & [k, p] : d->plans) {
-        if (p.graph) tsr_hip_graph_free(d->ctx, p.graph);
-        for (FaSlot & f : p.fa) {
-            if (f.plan) tsr_hip_fa_plan_free(d->ctx, f.plan);
-            if (f.mf32) tsr_hip_free(d->ctx, f.mf32);
-        }
-    }
+    for (auto & [k, p] : d->plans) free_plan(d, p);
     d->plans.clear();
     ++d->epoch;
 }
 
 void drop_weights_in(tsr_gg_dev * d, uint64_t lo, uint64_t hi) {
     bool any = false;
-    for (auto it = d->weights.begin(); it != d->weights.end();) {
-        const Weight & w = it->second;
-        if (w.vaddr < hi && w.vaddr + w.nbytes > lo) {
-            if (!any) drop_plans(d);
-            any = true;
-            if (d->ctx && w.w) tsr_hip_weight_free(d->ctx, w.w);
-            it = d->weights.erase(it);
-        } else {
-            ++it;
+    auto hit = [&](const Weight & w) {
+        if (w.parts.empty()) return w.vaddr < hi && w.vaddr + w.nbytes > lo;
+        for (const auto & [a, n] : w.parts)
+            if (a < hi && a + n > lo) return true;
+        return false;
+    };
+    auto sweep = [&](auto & m) {
+        for (auto it = m.begin(); it != m.end();) {
+            if (hit(it->second)) {
+                if (!any) drop_plans(d);
+                any = true;
+                if (d->ctx && it->second.w) tsr_hip_weight_free(d->ctx, it->second.w);
+                it = m.erase(it);
+            } else {
+                ++it;
+            }
         }
-    }
+    };
+    sweep(d->weights);
+    sweep(d->fused);
 }
 
 // KV buffers: byte ranges of the ggml images, across tensors.
@@ -563,6 +585,42 @@ bool overlap(const Rows & a, const Rows & b) {
 }
 bool same_rows(const Rows & a, const Rows & b) { return a.a == b.a && a.stride == b.stride && a.n == b.n && a.rows == b.rows; }
 
+// The ggml rows of a weight read back from its buffer, as blocks of its device format: Q8_0 / Q4_K
+// unchanged, other types to f32 and quantized to Q8_0 (ggml's quantize_row_q8_0_ref).
+int weight_blocks(tsr_gg_dev * d, const tsr_gg_tensor * t, const void * p, uint32_t * fmt, std::vector<uint8_t> * out) {
+    const size_t nb = nbytes_of(d, t);
+    std::vector<uint8_t> raw(nb);
+    const int rc = tsr_hip_read(d->ctx, raw.data(), p, nb);
+    if (rc) return d->hip(rc, "weight read");
+    const size_t K = (size_t)t->ne[0], N = (size_t)t->ne[1];
+    if (t->type == TSR_GG_TYPE_Q4_K || t->type == TSR_GG_TYPE_Q8_0) {
+        *fmt = t->type == TSR_GG_TYPE_Q4_K ? TSR_HIP_FMT_Q4_K : TSR_HIP_FMT_Q8_0;
+        *out = std::move(raw);
+        return TSR_GG_OK;
+    }
+    *fmt = TSR_HIP_FMT_Q8_0;
+    TypeInfo ti;
+    type_info(d, t->type, &ti);
+    const size_t row_in = K / ti.blck * ti.size;
+    out->assign(N * (K / 32) * 34, 0);
+    std::vector<float> f(K);
+    for (size_t n = 0; n < N; ++n) {
+        const uint8_t * src = raw.data() + n * row_in;
+        switch (t->type) {
+            case TSR_GG_TYPE_F32: memcpy(f.data(), src, K * 4); break;
+            case TSR_GG_TYPE_F16:
+                for (size_t k = 0; k < K; ++k) { uint16_t h; memcpy(&h, src + 2 * k, 2); f[k] = h2f(h); }
+                break;
+            case TSR_GG_TYPE_BF16:
+                for (size_t k = 0; k < K; ++k) { uint16_t h; memcpy(&h, src + 2 * k, 2); f[k] = bf16f(h); }
+                break;
+            default: ti.to_float(src, f.data(), (int64_t)K); break;
+        }
+        quantize_q8_0(f.data(), (int64_t)K, out->data() + n * (K / 32) * 34);
+    }
+    return TSR_GG_OK;
+}
+
 // The weight of a MUL_MAT: converted from the buffer's ggml bytes when first used.
 int weight_of(tsr_gg_dev * d, const tsr_gg_tensor * t, bool build, Weight ** out, std::string * why) {
     const uint64_t a = t->data;
@@ -589,39 +647,74 @@ int weight_of(tsr_gg_dev * d, const tsr_gg_tensor * t, bool build, Weight ** out
         *out = &probe;
         return TSR_GG_OK;
     }
-    std::vector<uint8_t> raw(nb);
-    int rc = tsr_hip_read(d->ctx, raw.data(), p, nb);
-    if (rc) return d->hip(rc, "weight read");
-    uint32_t fmt = TSR_HIP_FMT_Q8_0;
-    const void * blocks = raw.data();
-    std::vector<uint8_t> conv;
-    if (t->type == TSR_GG_TYPE_Q4_K) fmt = TSR_HIP_FMT_Q4_K;
-    else if (t->type != TSR_GG_TYPE_Q8_0) {
-        TypeInfo ti;
-        type_info(d, t->type, &ti);
-        const size_t K = w.K, row_in = K / ti.blck * ti.size;
-        conv.resize((size_t)w.N * (K / 32) * 34);
-        std::vector<float> f(K);
-        for (uint32_t n = 0; n < w.N; ++n) {
-            const uint8_t * src = raw.data() + (size_t)n * row_in;
-            switch (t->type) {
-                case TSR_GG_TYPE_F32: memcpy(f.data(), src, K * 4); break;
-                case TSR_GG_TYPE_F16:
-                    for (size_t k = 0; k < K; ++k) { uint16_t h; memcpy(&h, src + 2 * k, 2); f[k] = h2f(h); }
-                    break;
-                case TSR_GG_TYPE_BF16:
-                    for (size_t k = 0; k < K; ++k) { uint16_t h; memcpy(&h, src + 2 * k, 2); f[k] = bf16f(h); }
-                    break;
-                default: ti.to_float(src, f.data(), (int64_t)K); break;
-            }
-            quantize_q8_0(f.data(), (int64_t)K, conv.data() + (size_t)n * (K / 32) * 34);
-        }
-        blocks = conv.data();
-    }
-    rc = tsr_hip_weight_upload(d->ctx, fmt, blocks, w.N, w.K, &w.w);
+    uint32_t fmt;
+    std::vector<uint8_t> blocks;
+    int rc = weight_blocks(d, t, p, &fmt, &blocks);
+    if (rc) return rc;
+    rc = tsr_hip_weight_upload(d->ctx, fmt, blocks.data(), w.N, w.K, &w.w);
     if (rc) return d->hip(rc, "weight upload");
     d->st.weights_converted++;
     auto [ins, ok] = d->weights.emplace(a, w);
+    *out = &ins->second;
+    return TSR_GG_OK;
+}
+
+// The device format of a weight type: Q4_K stays Q4_K, every other type is Q8_0.
+uint32_t dev_fmt(int32_t type) { return type == TSR_GG_TYPE_Q4_K ? TSR_HIP_FMT_Q4_K : TSR_HIP_FMT_Q8_0; }
+size_t dev_row_bytes(uint32_t fmt, uint32_t K) { return fmt == TSR_HIP_FMT_Q4_K ? (size_t)K / 256 * 144 : (size_t)K / 32 * 34; }
+
+// A weight made of several 2-D ggml weights of one device format and K: their rows one after another
+// (Q|K|V) or, with interleave, row j of each in turn (gate / up: the library's GLU layout).
+int fused_weight_of(tsr_gg_dev * d, const std::vector<const tsr_gg_tensor *> & ts, bool interleave, bool build,
+                    Weight ** out, std::string * why) {
+    std::vector<uint64_t> key{interleave ? 1u : 0u};
+    for (const tsr_gg_tensor * t : ts) key.push_back(t->data);
+    auto it = d->fused.find(key);
+    if (it != d->fused.end()) {
+        *out = &it->second;
+        return TSR_GG_OK;
+    }
+    Weight w;
+    w.K = (uint32_t)ts[0]->ne[0];
+    const uint32_t fmt = dev_fmt(ts[0]->type);
+    std::vector<void *> ps;
+    for (const tsr_gg_tensor * t : ts) {
+        void * p = nullptr;
+        const size_t nb = nbytes_of(d, t);
+        if (!dev_ptr(d, t->data, nb, &p, why)) return TSR_GG_E_UNSUPPORTED;
+        ps.push_back(p);
+        w.N += (uint32_t)t->ne[1];
+        w.parts.emplace_back(t->data, nb);
+    }
+    if (!build || d->ctx == nullptr) {
+        static Weight probe;
+        probe = w;
+        *out = &probe;
+        return TSR_GG_OK;
+    }
+    const size_t rb = dev_row_bytes(fmt, w.K);
+    std::vector<std::vector<uint8_t>> parts(ts.size());
+    for (size_t i = 0; i < ts.size(); ++i) {
+        uint32_t f;
+        const int rc = weight_blocks(d, ts[i], ps[i], &f, &parts[i]);
+        if (rc) return rc;
+    }
+    std::vector<uint8_t> all((size_t)w.N * rb);
+    if (interleave) {
+        const size_t rows = (size_t)ts[0]->ne[1], np = ts.size();
+        for (size_t r = 0; r < rows; ++r)
+            for (size_t i = 0; i < np; ++i) memcpy(all.data() + (r * np + i) * rb, parts[i].data() + r * rb, rb);
+    } else {
+        size_t o = 0;
+        for (const auto & pb : parts) {
+            memcpy(all.data() + o, pb.data(), pb.size());
+            o += pb.size();
+        }
+    }
+    const int rc = tsr_hip_weight_upload(d->ctx, fmt, all.data(), w.N, w.K, &w.w);
+    if (rc) return d->hip(rc, "weight upload");
+    d->st.weights_converted++;
+    auto [ins, ok] = d->fused.emplace(key, std::move(w));
     *out = &ins->second;
     return TSR_GG_OK;
 }
@@ -634,6 +727,14 @@ struct Graph {
     const tsr_gg_tensor * const * nodes;
     int n;
     std::vector<int> uses;                              // uses of node i by later nodes
+    std::vector<std::vector<int>> users;                // the later nodes that name node i as a source
+    std::vector<std::pair<uint64_t, uint64_t>> out;     // bytes each node writes ([0, 0) for views)
+    // some node strictly between i and j writes bytes of [lo, hi)
+    bool written_between(int i, int j, uint64_t lo, uint64_t hi) const {
+        for (int k = i + 1; k < j; ++k)
+            if (out[k].first < hi && lo < out[k].second) return true;
+        return false;
+    }
     int index_of(const tsr_gg_tensor * t) const {
         for (int i = 0; i < n; ++i) if (nodes[i] == t) return i;
         return -1;
@@ -654,6 +755,8 @@ struct Lowerer {
     bool build;                                         // false: describe only (no device resources)
     Plan * plan;
     std::string why;
+    Lowerer(tsr_gg_dev * dev, bool b, Plan * p) : d(dev), build(b), plan(p) {}
+    bool fuse = true;
 
     void * stream() const { return d->stream; }
 
@@ -696,8 +799,12 @@ struct Lowerer {
         if (w->view_src != nullptr && (w->data != wb->data || !same_shape(w, wb)))
             return refuse("MUL_MAT: src0 is a slice of a weight");
         if (x->data % kAlign != 0) return refuse("MUL_MAT: src1 is not 64-byte aligned");
-        Rows X, Y;
-        if (!f32_rows(d, x, "src1", &X, &why)) return false;
+        // src1 = RMS_NORM(x') * w folded into this matvec: the norm runs on x' inside it
+        const int xi = g.index_of(x);
+        const Fold * fo = xi >= 0 && xi < (int)fold_of.size() && fold_of[xi] >= 0 ? &folds[fold_of[xi]] : nullptr;
+        Rows X, Y, NW;
+        if (!f32_rows(d, fo ? fo->x : x, "src1", &X, &why)) return false;
+        if (fo && !f32_rows(d, fo->w, "norm weight", &NW, &why)) return false;
         Weight * wt = nullptr;
         int rc = weight_of(d, w, build, &wt, &why);
         if (rc) {
@@ -711,10 +818,12 @@ struct Lowerer {
         uint32_t flags = 0;
         float s1 = 0.0f, s2 = 0.0f;
         int n2 = -1, n3 = -1, last = i;
-        const int u = g.next_real(i);
-        if (u >= 0 && g.only_user(i, u)) {
+        const int u = fuse ? g.next_real(i) : -1;
+        if (u >= 0 && g.only_user(i, u) && !skip[u]) {
             const tsr_gg_tensor * un = g.nodes[u];
-            if (un->op == TSR_GG_OP_ADD && same_shape(un, node) && un->type == TSR_GG_TYPE_F32) {
+            if (fo && un->op == TSR_GG_OP_SCALE) {
+                // the norm form has no epilogue: never reached (a fold is refused for such readers)
+            } else if (un->op == TSR_GG_OP_ADD && same_shape(un, node) && un->type == TSR_GG_TYPE_F32) {
                 const tsr_gg_tensor * o = un->src[0] == node ? un->src[1] : un->src[0];
                 if (o != nullptr && o != node && o->type == TSR_GG_TYPE_F32 && o->ne[0] == N &&
                     (nrows(o) == 1 || same_shape(o, node))) {
@@ -775,6 +884,10 @@ struct Lowerer {
         c.info.add_stride = addend ? (A.rows == 1 ? 0 : A.stride) : 0;
         c.info.scale = s1;
         c.info.scale2 = s2;
+        if (fo) {
+            c.info.node3 = fo->norm;
+            c.info.scale = fo->eps;
+        }
         c.capturable = T < 16;
         if (build) {
             tsr_hip_ctx * ctx = d->ctx;
@@ -784,10 +897,15 @@ struct Lowerer {
             const float * ap = addend ? (const float *)A.p : nullptr;
             const uint64_t xs = X.stride, ys = Y.stride, as = c.info.add_stride;
             void * s = stream();
-            if (flags)
+            if (fo) {
+                const float eps = fo->eps;
+                const float * nw = (const float *)NW.p;
+                c.run = [=](const Plan &) { return tsr_hip_mul_mat_norm(ctx, hw, xp, T, xs, eps, nw, yp, ys, ap, as, 0u, s); };
+            } else if (flags) {
                 c.run = [=](const Plan &) { return tsr_hip_mul_mat_epi(ctx, hw, xp, T, xs, yp, ys, ap, as, flags, s1, s2, s); };
-            else
+            } else {
                 c.run = [=](const Plan &) { return tsr_hip_mul_mat(ctx, hw, xp, T, xs, yp, ys, ap, as, 0u, s); };
+            }
         }
         *consumed = last;
         return true;
@@ -805,6 +923,7 @@ struct Lowerer {
         int n2 = -1;
         const int u = g.next_real(i);
         if (u >= 0 && g.only_user(i, u) && g.nodes[u]->op == TSR_GG_OP_MUL && same_shape(g.nodes[u], node)) {
+            // RMS_NORM + MUL is one record in every lowering (a MUL by a weight has no call of its own)
             const tsr_gg_tensor * un = g.nodes[u];
             const tsr_gg_tensor * o = un->src[0] == node ? un->src[1] : un->src[0];
             if (o && o->type == TSR_GG_TYPE_F32 && o->ne[0] == node->ne[0] && (nrows(o) == 1 || nrows(o) == nrows(node))) {
@@ -1087,8 +1206,17 @@ struct Lowerer {
         return true;
     }
 
-    // FLASH_ATTN_EXT over one layer's K and V planes (tsr_lower_fa, tsr-build.cpp:673-773).
-    bool flash_attn(const Graph & g, int i) {
+    // FLASH_ATTN_EXT over one layer's K and V planes (tsr_lower_fa, tsr-build.cpp:673-773): the rules of
+    // everything but q, the result and the new cells.
+    struct FaInfo {
+        uint32_t D = 0, T = 0, H = 0, Hk = 0, n_kv = 0, kv_size = 0;
+        float scale = 0.0f;
+        uint64_t mask = 0, kidx = 0, kbase = 0, vbase = 0;
+        uint32_t kidx_n = 0;
+        void * op = nullptr;
+        uint64_t os = 0;
+    };
+    bool fa_info(const Graph & g, int i, FaInfo * f) {
         const tsr_gg_tensor * node = g.nodes[i];
         const tsr_gg_tensor * q = node->src[0];
         const tsr_gg_tensor * k = node->src[1];
@@ -1108,8 +1236,6 @@ struct Lowerer {
             v->ne[2] != Hk || Hk == 0 || H % Hk != 0 || H / Hk > 64 || q->ne[3] != 1 || k->ne[3] != 1 || v->ne[3] != 1 ||
             T < 1 || n_kv < 1)
             return refuse("FLASH_ATTN_EXT shape: D = DK = DV in {64, 128, 256, 512}, n_head %% n_head_kv = 0, one stream");
-        if (q->nb[0] != 4 || q->nb[2] != 4ull * D || (T > 1 && q->nb[1] % 4 != 0))
-            return refuse("FLASH_ATTN_EXT: q's heads are not contiguous per token");
         if (node->nb[0] != 4 || node->nb[1] != 4ull * D || (T > 1 && node->nb[2] % 4 != 0) || node->ne[0] != D ||
             node->ne[1] != H || node->ne[2] != T)
             return refuse("FLASH_ATTN_EXT: the result's layout");
@@ -1129,60 +1255,105 @@ struct Lowerer {
                 t->data != base_of(t)->data)
                 return refuse("FLASH_ATTN_EXT: '%s' is not the cache's cells from cell 0 with heads %zu bytes apart", t->name, head_b);
         if (n_kv > kk.kv_size) return refuse("FLASH_ATTN_EXT: %u cells of a cache of %u", n_kv, kk.kv_size);
-        const uint64_t qs = T > 1 ? q->nb[1] / 4 : (uint64_t)H * D, os = T > 1 ? node->nb[2] / 4 : (uint64_t)H * D;
-        void *qp = nullptr, *op = nullptr;
-        if (!dev_ptr(d, q->data, ((size_t)(T - 1) * qs + (size_t)H * D) * 4, &qp, &w2) ||
-            !dev_ptr(d, node->data, ((size_t)(T - 1) * os + (size_t)H * D) * 4, &op, &w2))
+        f->os = T > 1 ? node->nb[2] / 4 : (uint64_t)H * D;
+        if (!dev_ptr(d, node->data, ((size_t)(T - 1) * f->os + (size_t)H * D) * 4, &f->op, &w2))
             return refuse("FLASH_ATTN_EXT: %s", w2.c_str());
         if (!(scale > 0.0f) || !std::isfinite(scale)) return refuse("FLASH_ATTN_EXT: scale %g", scale);
         // the new cells: a SET_ROWS of this graph into the same K cache, earlier, with indices from the host
-        uint64_t kidx = 0;
-        uint32_t kidx_n = 0;
         for (int j = 0; j < i; ++j) {
             const tsr_gg_tensor * sj = g.nodes[j];
             if (sj->op != TSR_GG_OP_SET_ROWS || base_of(sj)->data != base_of(k)->data || sj->src[1] == nullptr) continue;
             const tsr_gg_tensor * ix = sj->src[1];
             if (ix->op != TSR_GG_OP_NONE || g.index_of(ix) >= 0)
                 return refuse("FLASH_ATTN_EXT: the new-cell indices '%s' are computed by the graph, not written by the host", ix->name);
-            kidx = ix->data;
-            kidx_n = (uint32_t)ix->ne[0];
+            f->kidx = ix->data;
+            f->kidx_n = (uint32_t)ix->ne[0];
         }
-        Call & c = add(TSR_GG_CALL_FLASH_ATTN, i);
-        c.info.D = D;
-        c.info.n_head = H;
-        c.info.n_head_kv = Hk;
-        c.info.n_kv = n_kv;
-        c.info.kv_size = kk.kv_size;
-        c.info.T = T;
-        c.info.x = q->data;
-        c.info.y = node->data;
-        c.info.add = mask ? mask->data : 0;
-        c.info.w = kidx;
+        f->D = D;
+        f->T = T;
+        f->H = H;
+        f->Hk = Hk;
+        f->n_kv = n_kv;
+        f->kv_size = kk.kv_size;
+        f->scale = scale;
+        f->mask = mask ? mask->data : 0;
+        f->kbase = base_of(k)->data;
+        f->vbase = base_of(v)->data;
+        return true;
+    }
+    void fa_call_info(Call & c, const FaInfo & f, uint64_t q, uint64_t qs, uint64_t y) {
+        c.info.D = f.D;
+        c.info.n_head = f.H;
+        c.info.n_head_kv = f.Hk;
+        c.info.n_kv = f.n_kv;
+        c.info.kv_size = f.kv_size;
+        c.info.T = f.T;
+        c.info.x = q;
+        c.info.y = y;
+        c.info.add = f.mask;
+        c.info.w = f.kidx;
         c.info.x_stride = qs;
-        c.info.y_stride = os;
-        c.info.scale = scale;
-        c.info.K = kidx_n;
+        c.info.y_stride = f.os;
+        c.info.scale = f.scale;
+        c.info.K = f.kidx_n;
+    }
+    // The plan of a FLASH_ATTN_EXT (build mode): one per shape, mask and new cells, shared by the layers
+    // of a graph (their launches run one after another on one stream). -1 on failure (why set).
+    int fa_slot(const FaInfo & f, uint64_t vidx) {
+        for (size_t i = 0; i < plan->fa.size(); ++i) {
+            const FaSlot & s = plan->fa[i];
+            if (s.mask == f.mask && s.kidx == f.kidx && s.vidx == vidx && s.kidx_n == f.kidx_n && s.T == f.T &&
+                s.n_kv == f.n_kv && s.scale == f.scale && s.D == f.D && s.H == f.H && s.Hk == f.Hk && s.kv_size == f.kv_size)
+                return (int)i;
+        }
+        FaSlot s;
+        const int rc = tsr_hip_fa_plan_create(d->ctx, f.D, f.H, f.Hk, f.T, f.kv_size, &s.plan);
+        if (rc) {
+            why = std::string("FA plan: ") + tsr_hip_strerror(rc);
+            return -1;
+        }
+        s.mask = f.mask;
+        s.kidx = f.kidx;
+        s.vidx = vidx;
+        s.kidx_n = f.kidx_n;
+        s.T = f.T;
+        s.n_kv = f.n_kv;
+        s.scale = f.scale;
+        s.D = f.D;
+        s.H = f.H;
+        s.Hk = f.Hk;
+        s.kv_size = f.kv_size;
+        s.mf32_floats = (size_t)f.T * 16u * ((f.n_kv + 15u) / 16u);
+        plan->fa.push_back(s);
+        return (int)plan->fa.size() - 1;
+    }
+    bool flash_attn(const Graph & g, int i) {
+        FaInfo f;
+        if (!fa_info(g, i, &f)) return false;
+        const tsr_gg_tensor * q = g.nodes[i]->src[0];
+        if (q->nb[0] != 4 || q->nb[2] != 4ull * f.D || (f.T > 1 && q->nb[1] % 4 != 0))
+            return refuse("FLASH_ATTN_EXT: q's heads are not contiguous per token");
+        const uint64_t qs = f.T > 1 ? q->nb[1] / 4 : (uint64_t)f.H * f.D;
+        void * qp = nullptr;
+        std::string w2;
+        if (!dev_ptr(d, q->data, ((size_t)(f.T - 1) * qs + (size_t)f.H * f.D) * 4, &qp, &w2))
+            return refuse("FLASH_ATTN_EXT: %s", w2.c_str());
+        Call & c = add(TSR_GG_CALL_FLASH_ATTN, i);
+        fa_call_info(c, f, q->data, qs, g.nodes[i]->data);
         if (build) {
             uint32_t cell, bir;
-            const KvTensor * kt = kv_at(d, base_of(k)->data, &cell, &bir);
-            const KvTensor * vt = kv_at(d, base_of(v)->data, &cell, &bir);
+            const KvTensor * kt = kv_at(d, f.kbase, &cell, &bir);
+            const KvTensor * vt = kv_at(d, f.vbase, &cell, &bir);
             if (kt == nullptr || vt == nullptr) return refuse("FLASH_ATTN_EXT: the KV caches are not placed");
-            FaSlot f;
-            int rc = tsr_hip_fa_plan_create(d->ctx, D, H, Hk, T, kk.kv_size, &f.plan);
-            if (rc) { why = std::string("FA plan: ") + tsr_hip_strerror(rc); return false; }
-            f.mask = mask ? mask->data : 0;
-            f.kidx = kidx;
-            f.kidx_n = kidx_n;
-            f.T = T;
-            f.n_kv = n_kv;
-            f.scale = scale;
-            f.mf32_floats = (size_t)T * 16u * ((n_kv + 15u) / 16u);
-            plan->fa.push_back(f);
-            const size_t slot = plan->fa.size() - 1;
+            const int slot = fa_slot(f, 0);
+            if (slot < 0) return false;
             tsr_hip_ctx * ctx = d->ctx;
             const tsr_hip_kv * kc = kt->kv;
             const tsr_hip_kv * vc = vt->kv;
             void * s = stream();
+            void * op = f.op;
+            const uint64_t os = f.os;
+            const float scale = f.scale;
             c.run = [=](const Plan & pl) {
                 const FaSlot & fs = pl.fa[slot];
                 return tsr_hip_flash_attn_plan(ctx, fs.plan, (const float *)qp, qs, kc, vc, scale,
@@ -1192,11 +1363,408 @@ struct Lowerer {
         return true;
     }
 
+    // ---- fusions of llama.cpp's layer pattern (the decoder's launch list) ---------------------------
+    // A fold: MUL m = RMS_NORM(x) * w read only by MUL_MATs of fewer than 16 tokens: the norm runs inside
+    // each of their matvecs (tsr_hip_mul_mat_norm), not as a launch of its own.
+    struct Fold {
+        int norm = -1, mul = -1;
+        const tsr_gg_tensor * x = nullptr;
+        const tsr_gg_tensor * w = nullptr;
+        float eps = 0.0f;
+    };
+    // A group: the Q / K / V MUL_MATs (one matvec over their rows concatenated into a plan buffer) with
+    // the ROPEs, SET_ROWS and FLASH_ATTN_EXT that read them (one ROPE + SET_ROWS_KV + FA launch for a
+    // decode token; ROPE_KV then the planned FA for more tokens); or the gate / up MUL_MATs and their
+    // SWIGLU (one matvec with the GLU epilogue over their rows interleaved).
+    struct Group {
+        bool attn = false;
+        int mm_last = -1, fa = -1;
+        const tsr_gg_tensor * src1 = nullptr;                  // the MUL_MATs' input
+        std::vector<const tsr_gg_tensor *> ws;                 // q, k, v or gate, up
+        const tsr_gg_tensor * out = nullptr;                   // GLU: the SWIGLU node
+        const tsr_gg_tensor * rq = nullptr;                    // attention: q's ROPE (its parameters)
+        const tsr_gg_tensor * kidx = nullptr, * vidx = nullptr;
+        uint32_t T = 0;
+    };
+    std::vector<char> skip;
+    std::vector<int> fold_of, group_mm, group_fa;
+    std::vector<Fold> folds;
+    std::vector<Group> groups;
+    std::vector<std::pair<std::vector<uint64_t>, float *>> tables;   // ROPE angle tables of the plan
+    std::vector<std::pair<size_t, float *>> rows_bufs;                // Q|K|V row buffers of the plan
+
+    static bool is_(const tsr_gg_tensor * t, int op) { return t != nullptr && t->op == op; }
+    bool single(const Graph & g, const tsr_gg_tensor * t) const {   // a node of the graph with one user, not an output
+        const int i = g.index_of(t);
+        return i >= 0 && g.uses[i] == 1 && !(t->flags & TSR_GG_FLAG_OUTPUT);
+    }
+    // The weights of MUL_MATs that can share one launch: one device format, one K, in weights buffers.
+    bool same_weights(const std::vector<const tsr_gg_tensor *> & mm) const {
+        const tsr_gg_tensor * w0 = mm[0]->src[0];
+        for (const tsr_gg_tensor * m : mm) {
+            const tsr_gg_tensor * w = m->src[0];
+            const tsr_gg_tensor * b = w ? base_of(w) : nullptr;
+            if (w == nullptr || m->src[1] != mm[0]->src[1] || w->ne[0] != w0->ne[0] || dev_fmt(w->type) != dev_fmt(w0->type) ||
+                !loadable(d, w->type) || w->ne[2] != 1 || w->ne[3] != 1 || !contiguous(d, w) || b->buffer == nullptr ||
+                b->buffer->usage == TSR_GG_USAGE_COMPUTE || w->view_src != nullptr || m->type != TSR_GG_TYPE_F32)
+                return false;
+        }
+        const int64_t K = w0->ne[0];
+        return K >= 32 && K % 32 == 0 && K <= (int64_t)kKMax && (w0->type != TSR_GG_TYPE_Q4_K || K % 256 == 0);
+    }
+
+    void find_fusions(const Graph & g) {
+        const int n = g.n;
+        skip.assign(n, 0);
+        fold_of.assign(n, -1);
+        group_mm.assign(n, -1);
+        group_fa.assign(n, -1);
+        // Q / K / V + ROPE + SET_ROWS + FLASH_ATTN_EXT
+        for (int i = 0; i < n; ++i) {
+            const tsr_gg_tensor * fa = g.nodes[i];
+            if (fa->op != TSR_GG_OP_FLASH_ATTN_EXT) continue;
+            const tsr_gg_tensor * qp = fa->src[0];
+            if (!is_(qp, TSR_GG_OP_PERMUTE) || qp->op_params[0] != 0 || qp->op_params[1] != 2 || qp->op_params[2] != 1 ||
+                !single(g, qp))
+                continue;
+            const tsr_gg_tensor * rq = qp->src[0];
+            if (!is_(rq, TSR_GG_OP_ROPE) || !single(g, rq) || rq->src[2] != nullptr) continue;
+            const tsr_gg_tensor * shq = rq->src[0];
+            if (!is_(shq, TSR_GG_OP_RESHAPE) || !single(g, shq) || !is_(shq->src[0], TSR_GG_OP_MUL_MAT) || !single(g, shq->src[0]))
+                continue;
+            const tsr_gg_tensor * mq = shq->src[0];
+            const tsr_gg_tensor * srk = nullptr, * srv = nullptr;
+            for (int j = 0; j < i; ++j) {
+                const tsr_gg_tensor * t = g.nodes[j];
+                if (t->op != TSR_GG_OP_SET_ROWS) continue;
+                if (base_of(t)->data == base_of(fa->src[1])->data) srk = t;
+                if (base_of(t)->data == base_of(fa->src[2])->data) srv = t;
+            }
+            if (srk == nullptr || srv == nullptr || g.uses[g.index_of(srk)] || g.uses[g.index_of(srv)]) continue;
+            // K: SET_ROWS(cache_k, VIEW(ROPE(RESHAPE(MUL_MAT)))), V: SET_ROWS(cache_v, VIEW(RESHAPE(MUL_MAT)))
+            const tsr_gg_tensor * vk = srk->src[0], * vv = srv->src[0];
+            if (!is_(vk, TSR_GG_OP_VIEW) || !single(g, vk) || !is_(vv, TSR_GG_OP_VIEW) || !single(g, vv)) continue;
+            const tsr_gg_tensor * rk = vk->src[0], * shv = vv->src[0];
+            if (!is_(rk, TSR_GG_OP_ROPE) || !single(g, rk) || rk->src[1] != rq->src[1] || rk->src[2] != nullptr) continue;
+            if (memcmp(rk->op_params + 1, rq->op_params + 1, 15 * 4) != 0) continue;
+            const tsr_gg_tensor * shk = rk->src[0];
+            if (!is_(shk, TSR_GG_OP_RESHAPE) || !single(g, shk) || !is_(shk->src[0], TSR_GG_OP_MUL_MAT) || !single(g, shk->src[0]))
+                continue;
+            if (!is_(shv, TSR_GG_OP_RESHAPE) || !single(g, shv) || !is_(shv->src[0], TSR_GG_OP_MUL_MAT) || !single(g, shv->src[0]))
+                continue;
+            const tsr_gg_tensor * mk = shk->src[0], * mv = shv->src[0];
+            if (!same_weights({mq, mk, mv})) continue;
+            const uint32_t D = (uint32_t)rq->ne[0], H = (uint32_t)rq->ne[1], T = (uint32_t)rq->ne[2];
+            const uint32_t Hk = (uint32_t)rk->ne[1], E = Hk * D;
+            const int32_t n_dims = rq->op_params[1], mode = rq->op_params[2];
+            if (mq->ne[0] != (int64_t)H * D || mk->ne[0] != E || mv->ne[0] != E || nrows(mq) != T || nrows(mk) != T ||
+                nrows(mv) != T || rk->ne[0] != D || rk->ne[2] != T || vk->ne[0] != E || vv->ne[0] != E || vk->ne[1] != T ||
+                vv->ne[1] != T || vk->nb[1] != 4ull * E || vv->nb[1] != 4ull * E || !same_shape(rq, shq) || !same_shape(rk, shk))
+                continue;
+            if (mode != TSR_HIP_ROPE_NORMAL && mode != TSR_HIP_ROPE_NEOX && mode != TSR_HIP_ROPE_IMROPE) continue;
+            if (param_f32(rq, 6) != 1.0f || param_f32(rq, 7) != 0.0f || rq->op_params[15] != 0 || n_dims < 2 || n_dims % 2 ||
+                (uint32_t)n_dims > D)
+                continue;
+            const uint32_t G = Hk ? H / Hk : 0;
+            const uint32_t row = H * D + 2 * E;
+            if (Hk == 0 || H % Hk || D % 32 || row > 16384) continue;
+            if (T == 1 && ((D != 64 && D != 128) || (G + 2) * D > 1024 || n_dims % 8 || (uint32_t)n_dims > std::min(D, 128u)))
+                continue;
+            const tsr_gg_tensor * kidx = srk->src[1], * vidx = srv->src[1];
+            if (kidx == nullptr || vidx == nullptr || kidx->type != TSR_GG_TYPE_I64 || vidx->type != TSR_GG_TYPE_I64 ||
+                kidx->ne[0] != T || vidx->ne[0] != T || kidx->op != TSR_GG_OP_NONE || vidx->op != TSR_GG_OP_NONE ||
+                g.index_of(kidx) >= 0 || g.index_of(vidx) >= 0)
+                continue;
+            const tsr_gg_tensor * pos = rq->src[1];
+            if (pos == nullptr || pos->type != TSR_GG_TYPE_I32) continue;
+            Group gr;
+            gr.attn = true;
+            gr.fa = i;
+            gr.mm_last = std::max({g.index_of(mq), g.index_of(mk), g.index_of(mv)});
+            gr.src1 = mq->src[1];
+            gr.ws = {mq->src[0], mk->src[0], mv->src[0]};
+            gr.rq = rq;
+            gr.kidx = kidx;
+            gr.vidx = vidx;
+            gr.T = T;
+            // the input must be intact when the fused matvec reads it, at the last of the three
+            const int first = std::min({g.index_of(mq), g.index_of(mk), g.index_of(mv)});
+            if (g.written_between(first, gr.mm_last, gr.src1->data, gr.src1->data + nbytes_of(d, gr.src1))) continue;
+            groups.push_back(gr);
+            const int gi = (int)groups.size() - 1;
+            group_mm[gr.mm_last] = gi;
+            group_fa[i] = gi;
+            for (const tsr_gg_tensor * t : {mq, mk, mv, shq, shk, shv, rq, rk, vk, vv, srk, srv, qp}) skip[g.index_of(t)] = 1;
+        }
+        // gate / up + SWIGLU
+        for (int i = 0; i < n; ++i) {
+            const tsr_gg_tensor * u = g.nodes[i];
+            if (u->op != TSR_GG_OP_GLU || u->op_params[0] != TSR_GG_GLU_SWIGLU || u->op_params[1] != 0 || u->src[1] == nullptr)
+                continue;
+            const tsr_gg_tensor * mg = u->src[0], * mu = u->src[1];
+            if (!is_(mg, TSR_GG_OP_MUL_MAT) || !is_(mu, TSR_GG_OP_MUL_MAT) || !single(g, mg) || !single(g, mu) || mg == mu ||
+                !same_weights({mg, mu}) || mg->src[0]->ne[1] != mu->src[0]->ne[1] || !same_shape(u, mg) ||
+                !same_shape(mg, mu) || u->type != TSR_GG_TYPE_F32)
+                continue;
+            const uint32_t T = (uint32_t)nrows(mg);
+            if (dev_fmt(mg->src[0]->type) == TSR_HIP_FMT_Q8_0 && T >= 16) continue;   // GLU: Q8_0 on the matvec kernels only
+            const int a = g.index_of(mg), b = g.index_of(mu);
+            const tsr_gg_tensor * x = mg->src[1];
+            const uint64_t xl = x->data, xh = x->data + nbytes_of(d, x);
+            const uint64_t ul = u->data, uh = u->data + nbytes_of(d, u);
+            if (g.written_between(std::min(a, b), i, xl, xh) || (ul < xh && xl < uh)) continue;
+            Group gr;
+            gr.mm_last = i;
+            gr.src1 = x;
+            gr.ws = {mg->src[0], mu->src[0]};
+            gr.out = u;
+            gr.T = T;
+            groups.push_back(gr);
+            group_mm[i] = (int)groups.size() - 1;
+            skip[a] = skip[b] = 1;
+        }
+        // RMS_NORM * w folded into the MUL_MATs (and groups) that read it
+        for (int m = 0; m < n; ++m) {
+            const tsr_gg_tensor * mt = g.nodes[m];
+            if (mt->op != TSR_GG_OP_MUL || mt->type != TSR_GG_TYPE_F32 || (mt->flags & TSR_GG_FLAG_OUTPUT) || g.users[m].empty())
+                continue;
+            const tsr_gg_tensor * nt = is_(mt->src[0], TSR_GG_OP_RMS_NORM) ? mt->src[0] : mt->src[1];
+            const tsr_gg_tensor * w = nt == mt->src[0] ? mt->src[1] : mt->src[0];
+            if (!is_(nt, TSR_GG_OP_RMS_NORM) || !single(g, nt) || w == nullptr || w->type != TSR_GG_TYPE_F32 ||
+                w->ne[0] != mt->ne[0] || nrows(w) != 1 || !contiguous(d, w) || !same_shape(nt, mt))
+                continue;
+            const tsr_gg_tensor * x = nt->src[0];
+            const int64_t K = mt->ne[0], T = nrows(mt);
+            if (x == nullptr || !same_shape(x, nt) || K > 8192 || T >= 16 || mt->ne[2] != 1 || mt->ne[3] != 1) continue;
+            bool ok = true;
+            int last = m;
+            for (int u : g.users[m]) {
+                const tsr_gg_tensor * ut = g.nodes[u];
+                // a reader: a MUL_MAT of m (alone, or in a group), not one whose result gets an epilogue
+                ok &= ut->op == TSR_GG_OP_MUL_MAT && ut->src[1] == mt && ut->src[0] != mt;
+                const int nx = g.next_real(u);
+                ok &= !(nx >= 0 && g.nodes[nx]->op == TSR_GG_OP_SCALE && g.only_user(u, nx));
+                const int gm = ok ? (skip[u] ? -1 : u) : -1;
+                (void)gm;
+                last = std::max(last, u);
+            }
+            for (const Group & gr : groups) if (gr.src1 == mt) last = std::max(last, gr.mm_last);
+            const int ni = g.index_of(nt);
+            if (!ok || ni < 0 || g.written_between(ni, last + 1, x->data, x->data + nbytes_of(d, x))) continue;
+            Fold f;
+            f.norm = ni;
+            f.mul = m;
+            f.x = x;
+            f.w = w;
+            f.eps = param_f32(nt, 0);
+            folds.push_back(f);
+            fold_of[m] = (int)folds.size() - 1;
+            skip[ni] = skip[m] = 1;
+        }
+    }
+
+    // A device buffer owned by the plan (build mode).
+    void * plan_buf(size_t bytes) {
+        void * p = nullptr;
+        if (tsr_hip_alloc(d->ctx, bytes, &p) != TSR_HIP_OK) return nullptr;
+        plan->bufs.push_back(p);
+        return p;
+    }
+
+    // The matvec of a group (or of a MUL_MAT with a folded norm): y = W x (the norm applied to x first).
+    bool group_matvec(const Graph & g, const Group & gr, int at) {
+        const tsr_gg_tensor * x = gr.src1;
+        const int fi = g.index_of(x) >= 0 ? fold_of[g.index_of(x)] : -1;
+        const Fold * fo = fi >= 0 ? &folds[fi] : nullptr;
+        Rows X, Y, NW;
+        if (!f32_rows(d, fo ? fo->x : x, "src1", &X, &why)) return false;
+        if (fo && !f32_rows(d, fo->w, "norm weight", &NW, &why)) return false;
+        Weight * wt = nullptr;
+        const int rc = fused_weight_of(d, gr.ws, !gr.attn, build, &wt, &why);
+        if (rc) {
+            if (rc != TSR_GG_E_UNSUPPORTED) why = d->err;
+            return false;
+        }
+        const uint32_t T = X.rows, N = wt->N, K = wt->K;
+        uint32_t flags = 0;
+        uint64_t ys;
+        if (gr.attn) {
+            ys = N;
+            Y.a = 0;
+            if (build) {
+                Y.p = nullptr;
+                for (auto & rb : rows_bufs)
+                    if (rb.first >= (size_t)T * N * 4) Y.p = rb.second;
+                if (Y.p == nullptr) {
+                    Y.p = plan_buf((size_t)T * N * 4);
+                    if (Y.p == nullptr) return refuse("no device memory for the Q|K|V rows");
+                    rows_bufs.emplace_back((size_t)T * N * 4, (float *)Y.p);
+                }
+            }
+        } else {
+            if (!f32_rows(d, gr.out, "SWIGLU result", &Y, &why)) return false;
+            ys = Y.stride;
+            flags = TSR_HIP_MM_GLU;
+        }
+        Call & c = add(TSR_GG_CALL_MUL_MAT, at);
+        c.info.N = N;
+        c.info.K = K;
+        c.info.T = T;
+        c.info.flags = flags;
+        c.info.x = X.a;
+        c.info.y = Y.a;
+        c.info.w = gr.ws[0]->data;
+        c.info.x_stride = X.stride;
+        c.info.y_stride = ys;
+        c.info.node2 = fo ? fo->norm : -1;
+        c.info.scale = fo ? fo->eps : 0.0f;
+        c.info.add = fo ? NW.a : 0;
+        c.capturable = T < 16;
+        if (build) {
+            tsr_hip_ctx * ctx = d->ctx;
+            const tsr_hip_weight * hw = wt->w;
+            const float * xp = (const float *)X.p;
+            float * yp = (float *)Y.p;
+            const uint64_t xs = X.stride;
+            void * s = stream();
+            if (fo) {
+                const float eps = fo->eps;
+                const float * nw = (const float *)NW.p;
+                c.run = [=](const Plan &) { return tsr_hip_mul_mat_norm(ctx, hw, xp, T, xs, eps, nw, yp, ys, nullptr, 0, flags, s); };
+            } else {
+                c.run = [=](const Plan &) { return tsr_hip_mul_mat(ctx, hw, xp, T, xs, yp, ys, nullptr, 0, flags, s); };
+            }
+            if (gr.attn) qkv_rows = yp;
+        }
+        return true;
+    }
+    float * qkv_rows = nullptr;                            // the Q|K|V rows of the group being emitted
+
+    // The attention of a group: ROPE of q and k, SET_ROWS of k and v, FLASH_ATTN_EXT.
+    bool group_attn(const Graph & g, const Group & gr) {
+        FaInfo f;
+        if (!fa_info(g, gr.fa, &f)) return false;
+        const tsr_gg_tensor * rq = gr.rq;
+        const int32_t n_dims = rq->op_params[1], mode = rq->op_params[2];
+        const float base = param_f32(rq, 5), attn = param_f32(rq, 8);
+        if (!(base > 0.0f) || !std::isfinite(base)) return refuse("ROPE: freq_base %g", base);
+        const tsr_gg_tensor * pos = rq->src[1];
+        if (mode == TSR_HIP_ROPE_IMROPE && strstr(pos->name, "inp_pos") == nullptr)
+            return refuse("IMROPE: the positions '%s' are not llama.cpp's inp_pos input", pos->name);
+        void *pp = nullptr, *kp = nullptr;
+        std::string w2;
+        if (!dev_ptr(d, pos->data, 4 * (size_t)pos->ne[0], &pp, &w2) || !dev_ptr(d, gr.kidx->data, 8 * (size_t)gr.T, &kp, &w2))
+            return refuse("attention: %s", w2.c_str());
+        const uint32_t T = gr.T, row = f.H * f.D + 2 * f.Hk * f.D;
+        float * tab = nullptr;
+        if (T == 1) {                                        // the token's angle table, once per graph
+            const std::vector<uint64_t> key{pos->data, (uint64_t)(uint32_t)n_dims, (uint64_t)(uint32_t)rq->op_params[5],
+                                            (uint64_t)(uint32_t)rq->op_params[8]};
+            for (auto & t : tables) if (t.first == key) tab = t.second;
+            if (tab == nullptr) {
+                Call & tc = add(TSR_GG_CALL_ROPE_TABLE, gr.fa);
+                tc.info.x = pos->data;
+                tc.info.n_dims = (uint32_t)n_dims;
+                tc.info.scale = base;
+                tc.info.scale2 = attn;
+                if (build) {
+                    tab = (float *)plan_buf(4 * (size_t)n_dims + 64);
+                    if (tab == nullptr) return refuse("no device memory for the ROPE table");
+                    tsr_hip_ctx * ctx = d->ctx;
+                    void * s = stream();
+                    float * tb = tab;
+                    const uint32_t nd = (uint32_t)n_dims;
+                    tc.run = [=](const Plan &) { return tsr_hip_rope_table(ctx, (const int32_t *)pp, nd, base, attn, tb, s); };
+                } else {
+                    tab = (float *)(uintptr_t)(0x1000 + 64 * tables.size());     // describe mode: a marker
+                }
+                tables.emplace_back(key, tab);
+            }
+        } else {
+            Call & rc = add(TSR_GG_CALL_ROPE_KV, gr.fa);
+            rc.info.T = T;
+            rc.info.x_stride = row;
+            rc.info.n_dims = (uint32_t)n_dims;
+            rc.info.mode = (uint32_t)mode;
+            rc.info.scale = base;
+            rc.info.add = gr.kidx->data;
+        }
+        Call & c = add(TSR_GG_CALL_FLASH_ATTN, gr.fa);
+        fa_call_info(c, f, 0, row, g.nodes[gr.fa]->data);
+        c.info.n_dims = (uint32_t)n_dims;
+        c.info.mode = (uint32_t)mode;
+        c.info.node2 = gr.mm_last;
+        if (build) {
+            uint32_t cell, bir;
+            const KvTensor * kt = kv_at(d, f.kbase, &cell, &bir);
+            const KvTensor * vt = kv_at(d, f.vbase, &cell, &bir);
+            if (kt == nullptr || vt == nullptr) return refuse("FLASH_ATTN_EXT: the KV caches are not placed");
+            if (f.kidx != gr.kidx->data) return refuse("attention: the new cells are not the K SET_ROWS' indices");
+            const int slot = fa_slot(f, gr.vidx->data);
+            if (slot < 0) return false;
+            tsr_hip_ctx * ctx = d->ctx;
+            tsr_hip_kv * kc = kt->kv;
+            tsr_hip_kv * vc = vt->kv;
+            void * s = stream();
+            void * op = f.op;
+            const uint64_t os = f.os;
+            const float scale = f.scale;
+            float * qkv = qkv_rows;
+            const uint32_t nd = (uint32_t)n_dims, D = f.D, H = f.H, Hk = f.Hk;
+            const int64_t * cells = (const int64_t *)kp;
+            if (T == 1) {
+                const float * tb = tab;
+                c.run = [=](const Plan & pl) {
+                    const FaSlot & fs = pl.fa[slot];
+                    return tsr_hip_flash_attn_plan_rope_tab(ctx, fs.plan, qkv, kc, vc, scale, nd, mode, tb, cells, nullptr,
+                                                            fs.general ? fs.mf32 : nullptr, (float *)op, os, s);
+                };
+            } else {
+                Call & rc = plan->calls[plan->calls.size() - 2];
+                const int32_t * pv = (const int32_t *)pp;
+                rc.run = [=](const Plan &) {
+                    return tsr_hip_rope_kv(ctx, qkv, T, row, D, H, Hk, nd, mode, pv, base, attn, kc, vc, cells, nullptr, s);
+                };
+                c.run = [=](const Plan & pl) {
+                    const FaSlot & fs = pl.fa[slot];
+                    return tsr_hip_flash_attn_plan(ctx, fs.plan, qkv, row, kc, vc, scale, fs.general ? fs.mf32 : nullptr,
+                                                   (float *)op, os, s);
+                };
+            }
+        }
+        return true;
+    }
+
     // Every node of the graph in order; the nodes a call absorbed are skipped.
     bool lower(const Graph & g, int * bad_node) {
+        fuse = (d->options & TSR_GG_OPT_NO_FUSION) == 0u;
+        if (fuse) find_fusions(g);
+        else {
+            skip.assign(g.n, 0);
+            fold_of.assign(g.n, -1);
+            group_mm.assign(g.n, -1);
+            group_fa.assign(g.n, -1);
+        }
         for (int i = 0; i < g.n; ++i) {
             const tsr_gg_tensor * node = g.nodes[i];
-            if (is_noop(node->op)) continue;
+            if (group_mm[i] >= 0) {
+                const Group & gr = groups[group_mm[i]];
+                if (!group_matvec(g, gr, i)) {
+                    *bad_node = i;
+                    return false;
+                }
+                if (gr.attn) pending_qkv[group_mm[i]] = qkv_rows;
+                if (!gr.attn) continue;                        // the SWIGLU node is this call
+            }
+            if (group_fa[i] >= 0) {
+                qkv_rows = pending_qkv[group_fa[i]];
+                if (!group_attn(g, groups[group_fa[i]])) {
+                    *bad_node = i;
+                    return false;
+                }
+                continue;
+            }
+            if (is_noop(node->op) || skip[i]) continue;
             int consumed = i;
             bool ok;
             switch (node->op) {
@@ -1224,31 +1792,31 @@ struct Lowerer {
         for (const Call & c : plan->calls) plan->capturable &= c.capturable;
         return true;
     }
+    std::map<int, float *> pending_qkv;                     // group -> its Q|K|V rows (between the two emissions)
 };
 
-Graph make_graph(const tsr_gg_tensor * const * nodes, int n) {
-    Graph g{nodes, n, std::vector<int>(n, 0)};
-    for (int j = 0; j < n; ++j)
+Graph make_graph(const tsr_gg_dev * d, const tsr_gg_tensor * const * nodes, int n) {
+    Graph g{nodes, n, std::vector<int>(n, 0), std::vector<std::vector<int>>(n), {}};
+    std::map<const tsr_gg_tensor *, int> at;
+    for (int i = 0; i < n; ++i) at.emplace(nodes[i], i);
+    for (int j = 0; j < n; ++j) {
         for (int s = 0; s < 10; ++s) {
-            const tsr_gg_tensor * t = nodes[j]->src[s];
-            if (t == nullptr) continue;
-            for (int i = 0; i < j; ++i) if (nodes[i] == t) ++g.uses[i];
+            auto it = nodes[j]->src[s] ? at.find(nodes[j]->src[s]) : at.end();
+            if (it != at.end() && it->second < j) {
+                ++g.uses[it->second];
+                g.users[it->second].push_back(j);
+            }
         }
-    for (int j = 0; j < n; ++j)              // a view of node i is a user of i
-        if (nodes[j]->view_src)
-            for (int i = 0; i < j; ++i) if (nodes[i] == nodes[j]->view_src && nodes[j]->src[0] != nodes[i]) ++g.uses[i];
-    return g;
-}
-
-void free_plan(tsr_gg_dev * d, Plan & p) {
-    if (p.graph) tsr_hip_graph_free(d->ctx, p.graph);
-    p.graph = nullptr;
-    for (FaSlot & f : p.fa) {
-        if (f.plan) tsr_hip_fa_plan_free(d->ctx, f.plan);
-        if (f.mf32) tsr_hip_free(d->ctx, f.mf32);
-        f.plan = nullptr;
-        f.mf32 = nullptr;
+        // (a view names its parent in src[0]: a chain of views is a chain of uses)
     }
+    g.out.resize(n);
+    for (int i = 0; i < n; ++i) {
+        const tsr_gg_tensor * t = nodes[i];
+        if (is_noop(t->op)) continue;
+        const tsr_gg_tensor * b = t->op == TSR_GG_OP_SET_ROWS ? base_of(t) : t;
+        g.out[i] = {b->data, b->data + nbytes_of(d, b)};
+    }
+    return g;
 }
 
 // The FLASH_ATTN_EXT chunk lists of a plan from the masks and new cells of this run.
@@ -1278,6 +1846,12 @@ int refresh_fa(tsr_gg_dev * d, Plan & p, bool * changed) {
             auto it = d->shadows.find(f.kidx);
             if (it == d->shadows.end() || it->second.size() < 8 * (size_t)f.kidx_n)
                 return d->fail(TSR_GG_E_UNSUPPORTED, "FLASH_ATTN_EXT: the new-cell indices were not written by the host");
+            if (f.vidx) {                                   // one launch stores k and v into the K indices' cells
+                auto iv = d->shadows.find(f.vidx);
+                if (iv == d->shadows.end() || iv->second.size() < 8 * (size_t)f.kidx_n ||
+                    memcmp(iv->second.data(), it->second.data(), 8 * (size_t)f.kidx_n) != 0)
+                    return d->fail(TSR_GG_E_UNSUPPORTED, "attention: the K and V SET_ROWS write different cells");
+            }
             const int64_t * ix = (const int64_t *)it->second.data();
             for (uint32_t j = 0; j < f.kidx_n; ++j) {
                 if (ix[j] < 0 || ix[j] > 0xFFFFFFFFll) return d->fail(TSR_GG_E_ARG, "FLASH_ATTN_EXT: new cell %lld", (long long)ix[j]);
@@ -1367,7 +1941,9 @@ int tsr_gg_close(tsr_gg_dev * d) {
         std::lock_guard<std::recursive_mutex> lk(d->mtx);
         drop_plans(d);
         for (auto & [a, w] : d->weights) if (d->ctx && w.w) tsr_hip_weight_free(d->ctx, w.w);
+        for (auto & [a, w] : d->fused) if (d->ctx && w.w) tsr_hip_weight_free(d->ctx, w.w);
         d->weights.clear();
+        d->fused.clear();
         while (!d->buffers.empty()) tsr_gg_buffer_free(d->buffers.back());
         if (d->ctx) tsr_hip_close(d->ctx);
         d->ctx = nullptr;
@@ -1554,6 +2130,23 @@ int tsr_gg_buffer_clear(tsr_gg_buffer * b, uint8_t value) {
     return b->size ? d->hip(tsr_hip_memset(d->ctx, b->mem, value, b->size), "buffer clear") : TSR_GG_OK;
 }
 
+int tsr_gg_buffer_cpy_tensor(tsr_gg_buffer * b, const tsr_gg_tensor * src, const tsr_gg_tensor * dst) {
+    if (b == nullptr || src == nullptr || dst == nullptr) return TSR_GG_E_ARG;
+    tsr_gg_dev * d = b->dev;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    if (d->ctx == nullptr) return 0;
+    const size_t n = nbytes_of(d, src);
+    if (n == 0 || n != nbytes_of(d, dst)) return 0;
+    void *sp = nullptr, *dp = nullptr;
+    std::string why;
+    if (!dev_ptr(d, src->data, n, &sp, &why) || !dev_ptr(d, dst->data, n, &dp, &why)) return 0;
+    drop_weights_in(d, dst->data, dst->data + n);
+    d->shadows.erase(dst->data);                          // the host no longer knows the values
+    d->masks.erase(dst->data);
+    const int rc = tsr_hip_copy_async(d->ctx, dp, sp, n, d->stream);
+    return rc ? d->hip(rc, "cpy_tensor") : 1;
+}
+
 int tsr_gg_buffer_free(tsr_gg_buffer * b) {
     if (b == nullptr) return TSR_GG_E_ARG;
     tsr_gg_dev * d = b->dev;
@@ -1600,9 +2193,9 @@ int tsr_gg_supports_op(tsr_gg_dev * d, const tsr_gg_tensor * op, char * why, siz
         }
     } else {
         Plan p;
-        Lowerer L{d, false, &p, {}};
+        Lowerer L(d, false, &p);
         const tsr_gg_tensor * one[1] = {op};
-        Graph g = make_graph(one, 1);
+        Graph g = make_graph(d, one, 1);
         int bad = -1;
         ok = L.lower(g, &bad);
         w = L.why;
@@ -1615,8 +2208,8 @@ int tsr_gg_lower(tsr_gg_dev * d, const tsr_gg_tensor * const * nodes, int n, tsr
     if (d == nullptr || (n && nodes == nullptr) || n < 0 || n_out == nullptr || cap < 0) return TSR_GG_E_ARG;
     std::lock_guard<std::recursive_mutex> lk(d->mtx);
     Plan p;
-    Lowerer L{d, false, &p, {}};
-    Graph g = make_graph(nodes, n);
+    Lowerer L(d, false, &p);
+    Graph g = make_graph(d, nodes, n);
     int bad = -1;
     const tsr_gg_stats saved = d->st;
     const bool ok = L.lower(g, &bad);
@@ -1632,7 +2225,7 @@ int tsr_gg_graph_compute(tsr_gg_dev * d, const tsr_gg_tensor * const * nodes, in
     std::lock_guard<std::recursive_mutex> lk(d->mtx);
     if (d->ctx == nullptr) return d->fail(TSR_GG_E_NODEV, "a probe device runs no graph");
     d->st.graphs++;
-    const uint64_t key = tsr_gg_graph_key(nodes, n, d->epoch);
+    const uint64_t key = tsr_gg_graph_key(nodes, n, d->epoch * 4 + d->options);
     auto it = d->plans.find(key);
     if (it == d->plans.end()) {
         d->st.plan_misses++;
@@ -1643,8 +2236,8 @@ int tsr_gg_graph_compute(tsr_gg_dev * d, const tsr_gg_tensor * const * nodes, in
             d->plans.erase(lru);
         }
         Plan p;
-        Lowerer L{d, true, &p, {}};
-        Graph g = make_graph(nodes, n);
+        Lowerer L(d, true, &p);
+        Graph g = make_graph(d, nodes, n);
         int bad = -1;
         if (!L.lower(g, &bad)) {
             free_plan(d, p);
@@ -1700,6 +2293,13 @@ int tsr_gg_synchronize(tsr_gg_dev * d) {
     if ((rc = tsr_hip_get_flags(d->ctx, &fl, 1)) != 0) return d->hip(rc, "device flags");
     if (fl) return d->fail(TSR_GG_E_FLAG, "a kernel raised device flags 0x%x (1: an index out of range, 2: an expired "
                                           "FLASH_ATTN_EXT wait, 4: an XCD placement check): the results are not valid", fl);
+    return TSR_GG_OK;
+}
+
+int tsr_gg_set_options(tsr_gg_dev * d, uint32_t options) {
+    if (d == nullptr || (options & ~TSR_GG_OPT_NO_FUSION)) return TSR_GG_E_ARG;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    d->options = options;
     return TSR_GG_OK;
 }
 

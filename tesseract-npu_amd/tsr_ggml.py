@@ -27,10 +27,10 @@ FLAG_INPUT, FLAG_OUTPUT, FLAG_PARAM, FLAG_COMPUTE = 1, 2, 4, 16
 USAGE_ANY, USAGE_WEIGHTS, USAGE_COMPUTE = 0, 1, 2
 MODE_UNDECIDED, MODE_LINEAR, MODE_WEIGHTS, MODE_KV = 0, 1, 2, 3
 (CALL_MUL_MAT, CALL_FLASH_ATTN, CALL_SET_ROWS, CALL_RMS_NORM, CALL_ADD, CALL_ROPE, CALL_SWIGLU, CALL_GET_ROWS,
- CALL_ARGMAX) = range(1, 10)
+ CALL_ARGMAX, CALL_ROPE_TABLE, CALL_ROPE_KV) = range(1, 12)
 CALL_NAMES = {CALL_MUL_MAT: "MUL_MAT", CALL_FLASH_ATTN: "FLASH_ATTN_EXT", CALL_SET_ROWS: "SET_ROWS",
               CALL_RMS_NORM: "RMS_NORM", CALL_ADD: "ADD", CALL_ROPE: "ROPE", CALL_SWIGLU: "SWIGLU",
-              CALL_GET_ROWS: "GET_ROWS", CALL_ARGMAX: "ARGMAX"}
+              CALL_GET_ROWS: "GET_ROWS", CALL_ARGMAX: "ARGMAX", CALL_ROPE_TABLE: "ROPE_TABLE", CALL_ROPE_KV: "ROPE_KV"}
 
 EXPORTS = (
     "tsr_gg_open", "tsr_gg_close", "tsr_gg_last_error", "tsr_gg_hip_ctx", "tsr_gg_register_type",
@@ -38,8 +38,10 @@ EXPORTS = (
     "tsr_gg_buffer_size", "tsr_gg_buffer_init_tensor", "tsr_gg_buffer_set_tensor", "tsr_gg_buffer_get_tensor",
     "tsr_gg_buffer_memset_tensor", "tsr_gg_buffer_clear", "tsr_gg_buffer_free", "tsr_gg_buffer_mode",
     "tsr_gg_supports_op", "tsr_gg_graph_compute", "tsr_gg_synchronize", "tsr_gg_get_stats", "tsr_gg_lower",
-    "tsr_gg_kv_parse_name", "tsr_gg_graph_key", "tsr_gg_quantize_q8_0",
+    "tsr_gg_kv_parse_name", "tsr_gg_graph_key", "tsr_gg_quantize_q8_0", "tsr_gg_set_options",
+    "tsr_gg_buffer_cpy_tensor",
 )
+OPT_NO_FUSION = 1
 
 
 class Tensor(C.Structure):
@@ -124,6 +126,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "tsr_gg_kv_parse_name": ([C.c_char_p, C.POINTER(u32), C.POINTER(C.c_int)], C.c_int),
         "tsr_gg_graph_key": ([C.POINTER(TP), C.c_int, u64], u64),
         "tsr_gg_quantize_q8_0": ([vp, C.c_int64, vp], C.c_int),
+        "tsr_gg_set_options": ([vp, u32], C.c_int),
+        "tsr_gg_buffer_cpy_tensor": ([vp, TP, TP], C.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -196,6 +200,12 @@ class Buffer:
     def memset_tensor(self, t: Tensor, value: int, offset: int, size: int) -> None:
         self.dev.check(self.dev.L.tsr_gg_buffer_memset_tensor(self.h, C.byref(t), value, offset, size), "memset_tensor")
 
+    def cpy_tensor(self, src: Tensor, dst: Tensor) -> bool:
+        rc = self.dev.L.tsr_gg_buffer_cpy_tensor(self.h, C.byref(src), C.byref(dst))
+        if rc < 0:
+            self.dev.check(rc, "cpy_tensor")
+        return rc == 1
+
     def clear(self, value: int = 0) -> None:
         self.dev.check(self.dev.L.tsr_gg_buffer_clear(self.h, value), "clear")
 
@@ -252,7 +262,16 @@ class Device:
         return bool(rc), why.value.decode()
 
     def graph_compute(self, nodes) -> None:
-        self.check(self.L.tsr_gg_graph_compute(self.h, _node_array(nodes), len(nodes)), "graph_compute")
+        """nodes: Tensor records, or an array from prepare() (built once, for a graph run many times)."""
+        arr = nodes if isinstance(nodes, tuple) else (_node_array(nodes), len(nodes))
+        self.check(self.L.tsr_gg_graph_compute(self.h, arr[0], arr[1]), "graph_compute")
+
+    @staticmethod
+    def prepare(nodes) -> tuple:
+        return (_node_array(nodes), len(nodes))
+
+    def set_options(self, options: int) -> None:
+        self.check(self.L.tsr_gg_set_options(self.h, options), "set_options")
 
     def synchronize(self) -> None:
         self.check(self.L.tsr_gg_synchronize(self.h), "synchronize")

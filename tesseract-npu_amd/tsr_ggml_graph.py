@@ -1,8 +1,9 @@
-"""A small stand-in for ggml's graph construction, for driving libtsr_ggml in tests: tensors with ggml's
-shapes and byte strides (ggml.c's new_tensor / view / reshape / permute rules: a view's view_src is the
-base tensor and its offset accumulates), op nodes with ggml's op_params layout, a bump allocator over
-the adapter's buffers, and llama.cpp's Llama graph (src/models/llama.cpp with FLASH_ATTN_EXT over a q8_0
-cache: src/llama-graph.cpp build_attn_mha, src/llama-kv-cache.cpp cpy_k / get_k)."""
+"""A small stand-in for ggml's graph construction, for driving libtsr_ggml where llama.cpp is absent
+(the tests, the bench's adapter leg): tensors with ggml's shapes and byte strides (ggml.c's new_tensor /
+view / reshape / permute rules: a view's view_src is the base tensor and its offset accumulates), op
+nodes with ggml's op_params layout, a bump allocator over the adapter's buffers, and llama.cpp's Llama
+graph (src/models/llama.cpp with FLASH_ATTN_EXT over a q8_0 cache: src/llama-graph.cpp build_attn_mha,
+src/llama-kv-cache.cpp cpy_k / get_k)."""
 from __future__ import annotations
 
 import struct
@@ -261,6 +262,20 @@ class LlamaGraph:
             m[r, :pos0 + r + 1] = 0.0
         b.set_tensor(self.kq_mask, m)
         b.set_tensor(self.out_ids, np.array([T - 1], np.int32))
+
+    def set_position(self, pos0: int) -> None:
+        """The inputs of a step at positions pos0 .. pos0 + T - 1 but the token ids (a decode loop that
+        feeds the greedy token on the device)."""
+        T, n_kv = self.T, self.n_kv
+        pos = pos0 + np.arange(T, dtype=np.int32)
+        b = self.buf
+        b.set_tensor(self.inp_pos, pos)
+        b.set_tensor(self.k_idxs, pos.astype(np.int64))
+        b.set_tensor(self.v_idxs, pos.astype(np.int64))
+        m = np.full((T, n_kv), -np.inf, np.float16)
+        for r in range(T):
+            m[r, :pos0 + r + 1] = 0.0
+        b.set_tensor(self.kq_mask, m)
 
     def logits_host(self) -> np.ndarray:
         return self.buf.get_tensor(self.logits, 4 * self.cfg.n_vocab).view(np.float32)

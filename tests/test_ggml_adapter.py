@@ -9,7 +9,7 @@ import re
 import numpy as np
 import pytest
 
-import ggml_like as GL
+import tsr_ggml_graph as GL
 import tsr_ggml as G
 import tsr_hip
 import tsr_llama as LL
@@ -260,11 +260,12 @@ def declare_model(p, cfg, kv_size):
 
 
 @pytest.mark.parametrize("T", [1, 24])
-def test_lower_llama_graph(T):
-    """llama.cpp's Llama graph lowers to the library calls of the reference's op list: per layer one
-    RMS_NORM+MUL record (fused), the Q / K / V MUL_MATs, two ROPEs, two SET_ROWS_KV, one FLASH_ATTN_EXT
-    (scale from op_params[0], q's token stride, the new-cell indices of the K SET_ROWS), the o MUL_MAT
-    with the residual ADD fused (tsr_fuse_mm_add), RMS_NORM+MUL, gate, up, SWIGLU, down+ADD."""
+def test_lower_llama_graph_unfused(T):
+    """With fusions off, llama.cpp's Llama graph lowers to the library calls of the reference's op list:
+    per layer one RMS_NORM+MUL record, the Q / K / V MUL_MATs, two ROPEs, two SET_ROWS_KV, one
+    FLASH_ATTN_EXT (scale from op_params[0], q's token stride, the new-cell indices of the K SET_ROWS),
+    the o MUL_MAT with the residual ADD (tsr_fuse_mm_add, kept in every lowering), RMS_NORM+MUL, gate,
+    up, SWIGLU, down+ADD."""
     cfg = LL.tiny_config()
     p = Probe()
     p.kvbuf = p.dev.buffer(1 << 24)
@@ -272,12 +273,13 @@ def test_lower_llama_graph(T):
     kv_size = 512
     W, caches = declare_model(p, cfg, kv_size)
     g = GL.LlamaGraph(p.dev, cfg, W, caches, kv_size, T, 256, argmax=True)
+    p.dev.set_options(G.OPT_NO_FUSION)
     calls = p.dev.lower(g.ctx.nodes)
     names = [c["name"] for c in calls]
     L = cfg.n_layer
     per_layer = ["RMS_NORM", "MUL_MAT", "MUL_MAT", "MUL_MAT", "ROPE", "ROPE", "SET_ROWS", "SET_ROWS", "FLASH_ATTN_EXT",
-                 "MUL_MAT", "RMS_NORM", "MUL_MAT", "MUL_MAT", "SWIGLU", "MUL_MAT"]
-    last = per_layer[:10] + ["GET_ROWS", "GET_ROWS", "ADD"] + per_layer[10:]
+                 "MUL_MAT", "ADD", "RMS_NORM", "MUL_MAT", "MUL_MAT", "SWIGLU", "MUL_MAT", "ADD"]
+    last = per_layer[:10] + ["GET_ROWS", "GET_ROWS", "ADD"] + per_layer[11:]
     want = ["GET_ROWS"] + per_layer * (L - 1) + last + ["RMS_NORM", "MUL_MAT", "ARGMAX"]
     assert names == want
     nodes = g.ctx.nodes
@@ -294,17 +296,60 @@ def test_lower_llama_graph(T):
     norms = [c for c in calls if c["name"] == "RMS_NORM"]
     assert all(c["node2"] >= 0 and nodes[c["node2"]].op == G.OP_MUL for c in norms)
     assert np.float32(norms[0]["scale"]) == np.float32(cfg.eps)
-    mms = [c for c in calls if c["name"] == "MUL_MAT"]
-    fused = [c for c in mms if c["node2"] >= 0]
-    assert len(fused) == 2 * L - 1                                 # o (but the last layer's) and down
-    for c in fused:
-        add = nodes[c["node2"]]
-        assert add.op == G.OP_ADD and c["y"] == add.data and c["add"] != 0 and c["T"] in (T, 1)
+    assert all(c["node2"] == -1 for c in calls if c["name"] == "MUL_MAT")
     ropes = [c for c in calls if c["name"] == "ROPE"]
     assert all(r["n_dims"] == D and r["mode"] == cfg.rope_mode and r["add"] == g.inp_pos.data for r in ropes)
     assert np.float32(ropes[0]["scale"]) == np.float32(cfg.rope_base)
     sets = [c for c in calls if c["name"] == "SET_ROWS"]
     assert [s["which"] for s in sets] == [0, 1] * L and all(s["T"] == T and s["N"] == cfg.E for s in sets)
+    p.dev.close()
+
+
+@pytest.mark.parametrize("T", [1, 24])
+def test_lower_llama_graph_fused(T):
+    """The same graph lowered with its fusions: the decoder's launch list. One token, per layer: the
+    Q|K|V matvec with the attention RMS_NORM folded in (its rows concatenated), one ROPE + SET_ROWS_KV +
+    FLASH_ATTN_EXT launch (the angle table once per graph), o + residual, gate|up with the FFN norm and
+    the SWIGLU epilogue, down + residual. A ubatch (T = 24): the norms stay calls (the matrix-core
+    MUL_MATs take no norm), the Q|K|V MUL_MAT, ROPE_KV, the planned FLASH_ATTN_EXT."""
+    cfg = LL.tiny_config()
+    p = Probe()
+    p.kvbuf = p.dev.buffer(1 << 24)
+    p.koff = 0
+    kv_size = 512
+    W, caches = declare_model(p, cfg, kv_size)
+    g = GL.LlamaGraph(p.dev, cfg, W, caches, kv_size, T, 256, argmax=True)
+    calls = p.dev.lower(g.ctx.nodes)
+    names = [c["name"] for c in calls]
+    L, D, H, E = cfg.n_layer, cfg.head_dim, cfg.n_head, cfg.E
+    nodes = g.ctx.nodes
+    if T == 1:
+        first = ["MUL_MAT", "ROPE_TABLE", "FLASH_ATTN_EXT", "MUL_MAT", "MUL_MAT", "MUL_MAT"]
+        mid = ["MUL_MAT", "FLASH_ATTN_EXT", "MUL_MAT", "MUL_MAT", "MUL_MAT"]
+        last = ["MUL_MAT", "FLASH_ATTN_EXT", "MUL_MAT", "GET_ROWS", "GET_ROWS", "ADD", "MUL_MAT", "MUL_MAT"]
+        want = ["GET_ROWS"] + first + mid * (L - 2) + last + ["MUL_MAT", "ARGMAX"]
+    else:
+        per = ["RMS_NORM", "MUL_MAT", "ROPE_KV", "FLASH_ATTN_EXT", "MUL_MAT", "RMS_NORM", "MUL_MAT", "MUL_MAT"]
+        last = per[:5] + ["GET_ROWS", "GET_ROWS", "ADD", "MUL_MAT", "MUL_MAT"]   # one row from here: folds again
+        want = ["GET_ROWS"] + per * (L - 1) + last + ["MUL_MAT", "ARGMAX"]
+    assert names == want
+    mms = [c for c in calls if c["name"] == "MUL_MAT"]
+    qkv = [c for c in mms if c["N"] == H * D + 2 * E]
+    glu = [c for c in mms if c["flags"] == tsr_hip.MM_GLU]
+    assert len(qkv) == L and len(glu) == L
+    assert all(c["y"] == 0 for c in qkv)                          # the plan's Q|K|V rows
+    for c in glu:
+        assert c["N"] == 2 * cfg.n_ff and nodes[c["node"]].op == G.OP_GLU and c["y"] == nodes[c["node"]].data
+    folded = [c for c in mms if c["node2"] >= 0 and nodes[c["node2"]].op == G.OP_RMS_NORM or c["node3"] >= 0]
+    if T == 1:
+        assert len(folded) == 2 * L + 1                            # Q|K|V and gate|up of every layer, the head
+        assert all(np.float32(c["scale"]) == np.float32(cfg.eps) for c in folded)
+    fas = [c for c in calls if c["name"] == "FLASH_ATTN_EXT"]
+    assert all(f["n_dims"] == D and f["mode"] == cfg.rope_mode and f["x_stride"] == H * D + 2 * E for f in fas)
+    assert all(f["w"] == g.k_idxs.data and f["add"] == g.kq_mask.data for f in fas)
+    if T > 1:
+        rk = [c for c in calls if c["name"] == "ROPE_KV"]
+        assert len(rk) == L and all(r["T"] == T and r["add"] == g.k_idxs.data for r in rk)
     p.dev.close()
 
 

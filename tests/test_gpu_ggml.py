@@ -7,7 +7,7 @@ import ctypes as C
 import numpy as np
 import pytest
 
-import ggml_like as GL
+import tsr_ggml_graph as GL
 import tsr_ggml as G
 import tsr_hip as H
 import tsr_llama as LL
@@ -42,11 +42,15 @@ def history_images(ref, cfg, hist):
                     rope_base=1000000.0), 640, 300, 4),
     (LL.tiny_config("tiny-gqa8", n_head=8, n_head_kv=1, head_dim=128, n_embd=512, n_ff=768, n_vocab=1000), 300, 250, 4),
 ], ids=["q4k", "q80-neox", "gqa8-d128"])
-def test_llama_decode_through_adapter(gdev, oc, cfg, kv_size, hist, n_steps):
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
+def test_llama_decode_through_adapter(gdev, oc, cfg, kv_size, hist, n_steps, fused):
     """One decode token per graph_compute of llama.cpp's graph: the first run lowers and runs the calls,
     the second captures them into a HIP graph, the rest replay it with only the FLASH_ATTN_EXT chunk
-    lists re-planned from the written masks; logits, greedy tokens and the caches equal the oracle's."""
-    print(f"\nadapter decode {cfg.name}: kv {kv_size} history {hist} steps {n_steps}", flush=True)
+    lists re-planned from the written masks; logits, greedy tokens and the caches equal the oracle's.
+    Fused: the decoder's launch list (Q|K|V with the norm, one ROPE + SET_ROWS_KV + FA launch, gate|up
+    with the GLU epilogue); unfused: one call per node."""
+    print(f"\nadapter decode {cfg.name} fused={fused}: kv {kv_size} history {hist} steps {n_steps}", flush=True)
+    gdev.set_options(0 if fused else G.OPT_NO_FUSION)
     w = LL.SyntheticWeights(cfg, cache=True)
     ref = oracle_model(oc, cfg, w, kv_size, hist)
     _, W, caches, wbuf, kvbuf = GL.load_model(gdev, cfg, w, kv_size, history_images(ref, cfg, hist))
@@ -77,6 +81,7 @@ def test_llama_decode_through_adapter(gdev, oc, cfg, kv_size, hist, n_steps):
     g.free()
     kvbuf.free()
     wbuf.free()
+    gdev.set_options(0)
 
 
 @pytest.mark.parametrize("cfg,T,hist", [
@@ -84,11 +89,13 @@ def test_llama_decode_through_adapter(gdev, oc, cfg, kv_size, hist, n_steps):
     (LL.tiny_config("tiny-qwen", wfmt=H.FMT_Q8_0, ofmt=H.FMT_Q8_0, rope_mode=H.ROPE_NEOX, eps=1e-6,
                     rope_base=1000000.0), 20, 0),
 ], ids=["q4k-T32", "q80-T20-from0"])
-def test_llama_prefill_then_decode_through_adapter(gdev, oc, cfg, T, hist):
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
+def test_llama_prefill_then_decode_through_adapter(gdev, oc, cfg, T, hist, fused):
     """A ubatch of T tokens (the MUL_MATs on the matrix cores, the causal FLASH_ATTN_EXT with the ubatch's
     cells newest last), then a decode token, through the adapter: logits equal the oracle's forward and
     step, the caches its bytes."""
-    print(f"\nadapter prefill {cfg.name}: T {T} after {hist}", flush=True)
+    print(f"\nadapter prefill {cfg.name} fused={fused}: T {T} after {hist}", flush=True)
+    gdev.set_options(0 if fused else G.OPT_NO_FUSION)
     kv_size = 256
     w = LL.SyntheticWeights(cfg, cache=True)
     ref = oracle_model(oc, cfg, w, kv_size, hist)
@@ -111,6 +118,7 @@ def test_llama_prefill_then_decode_through_adapter(gdev, oc, cfg, T, hist):
     gdev.synchronize()
     for x in (gp, gd, kvbuf, wbuf):
         x.free()
+    gdev.set_options(0)
 
 
 def test_weight_types_converted_to_q8_0(gdev, oc):

@@ -125,7 +125,7 @@ __device__ __forceinline__ FaDecBlock fa_dec_block(const FaDecArgs & a) {
 constexpr uint32_t kDecLds = 256 + 512 + 64 + 128 + 16 + 128 + 16 + 4096 + 1024 + 1024 + 4096 + 48;
 
 template <int D, bool ROPE, bool LOCAL>
-__global__ __launch_bounds__(256, 6) void k_fa_dec(FaDecArgs a) {
+__global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     constexpr uint32_t NBD = D / 32u;                             // K / V blocks of a head
     __shared__ __align__(16) uint8_t lds[kDecLds];
     uint32_t * s_t64 = (uint32_t *)lds;

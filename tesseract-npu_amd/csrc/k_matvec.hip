@@ -38,13 +38,6 @@ namespace tsr {
 constexpr int kMvWaves = 16;
 constexpr uint32_t kXq4Stride = 272u;   // LDS bytes per quantized 256-value block (k slots on distinct banks)
 
-__device__ __forceinline__ void store_y(const MvArgs & a, uint32_t t, uint32_t row, float v) {
-    float * yp = a.y + (size_t)t * a.y_stride + row;
-    if (a.add) v = sadd(a.add[(size_t)t * a.add_stride + row], v);
-    else if (a.acc) v = sadd(*yp, v);
-    *yp = v;
-}
-
 // Partial p[w] of every row of the workgroup, by wave w from its own terms in LDS (s_t[row][s], nb
 // terms per row): p = ((+0 + t_w) + t_w+16) + ... in order of s. The same wave wrote those terms,
 // and the LDS executes one wave's operations in order, so no workgroup barrier is needed here.
@@ -68,14 +61,17 @@ __device__ __forceinline__ void mv_wave_partials(const WGeom & g, const float * 
 
 // After a workgroup barrier: the 16-partial tree of each row on an aligned 16-lane row of threads
 // (lane i holds p[i]; the DPP pairs xor 1, xor 2, half mirror, mirror are the tree's pairs, and
-// f32 addition is commutative), then y. Every thread of the workgroup calls it.
+// f32 addition is commutative), then y. Every thread of the workgroup calls it. add0: the addend of
+// the thread's row in the first round (loaded early by the caller; used when a.add is set).
 // GLU: weight rows 2j and 2j + 1 are the gate and up rows of output j (the workgroup's row block starts
-// at an even row and holds whole pairs); the pair's two results meet by a swizzle (their 16-lane rows
-// are lanes xor 16 apart) and y[j] = SWIGLU(gate, up) -- the GGML_GLU_OP_SWIGLU that follows the
-// gate and up MUL_MATs, computed once per output. t64: lane j holds the EXPK table entry j.
+// at an even row and holds whole pairs). The row results go to s_y (LDS, nrow floats, free after the
+// partials), and after a barrier one thread per output forms y[j] = SWIGLU(gate, up) -- the
+// GGML_GLU_OP_SWIGLU that follows the gate and up MUL_MATs -- on whole waves (64 outputs per wave, so
+// that the EXPK table lookup, a cross-lane read, runs with every lane active). t64: lane j holds the
+// EXPK table entry j.
 template <bool GLU>
-__device__ __forceinline__ void mv_tree_store(const MvArgs & a, const float * s_p, uint32_t nrow, uint32_t row_lo,
-                                              uint32_t t, bool slow, uint32_t t64) {
+__device__ __forceinline__ void mv_tree_store(const MvArgs & a, const float * s_p, float * s_y, uint32_t nrow,
+                                              uint32_t row_lo, uint32_t t, bool slow, uint32_t t64, float add0) {
     for (uint32_t base = 0; base < nrow * 16u; base += blockDim.x) {   // uniform trip count
         const uint32_t idx = base + threadIdx.x, rl = idx >> 4;
         float v = rl < nrow ? s_p[idx] : 0.0f;
@@ -91,12 +87,24 @@ __device__ __forceinline__ void mv_tree_store(const MvArgs & a, const float * s_
             v = sadd(v, dpp_f<kDppRowHalfMirror>(v));
             v = sadd(v, dpp_f<kDppRowMirror>(v));
         }
-        if constexpr (GLU) {
-            const float u = xor16_f(v);                               // the up row of the pair
-            const float h = swiglu_reg(v, u, a.ex, t64);              // every lane: the table is read by bpermute
-            if ((idx & 31u) == 0u && rl < nrow) a.y[(size_t)t * a.y_stride + ((row_lo + rl) >> 1)] = h;
-        } else {
-            if ((idx & 15u) == 0u && rl < nrow) store_y(a, t, row_lo + rl, v);
+        if ((idx & 15u) == 0u && rl < nrow) {
+            if constexpr (GLU) {
+                s_y[rl] = v;
+            } else {
+                float * yp = a.y + (size_t)t * a.y_stride + row_lo + rl;
+                if (a.add) v = sadd(base == 0u ? add0 : a.add[(size_t)t * a.add_stride + row_lo + rl], v);
+                else if (a.acc) v = sadd(*yp, v);
+                *yp = v;
+            }
+        }
+    }
+    if constexpr (GLU) {
+        lds_barrier();
+        const uint32_t nout = nrow >> 1, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        for (uint32_t j0 = 64u * w; j0 < nout; j0 += blockDim.x) {   // whole waves
+            const uint32_t j = j0 + __lane_id(), jc = min(j, nout - 1u);
+            const float h = swiglu_reg(s_y[2u * jc], s_y[2u * jc + 1u], a.ex, t64);
+            if (j < nout) a.y[(size_t)t * a.y_stride + (row_lo >> 1) + j] = h;
         }
     }
 }
@@ -200,16 +208,44 @@ __device__ __forceinline__ float prep_norm_scale(float * s_sq, uint32_t K, float
 }
 
 // ---------------------------------------------------------------------------------------------
-// Q4_K. LDS: x quants [16 waves][kx][272 B] | sub-block sums [16][kx][8] int | d [16][kx] |
-// terms [rb][nsb] | partials [rb][16] | slow flags [16].
-// Lane unit = (row, super-block): 8 quant loads (piece j: group g = j / 2, low nibbles = values
-// 64g + 16 (j % 2) + 0..15, high nibbles = the same + 32) and one meta load.
+// Q4_K. LDS: x quants [16 areas][kx][272 B] | sub-block sums [16][kx][8] int | d [16][kx] |
+// terms [rb][nsb] | partials [rb][16] | 16 words | kPrepNorm: K squares + 2 slots.
+// Block s of x lives in area s mod 16 at index s / 16 (area w holds the blocks of partial p[w]).
+// Lane unit = (row, super-block): 8 quant pieces (piece j: group g = j / 2, low nibbles = values
+// 64g + 16 (j % 2) + 0..15, high nibbles = the same + 32) and one meta piece. F adjacent lanes share
+// a unit when a wave has few units (F = 4: at most 16, F = 2: at most 32): lane q of the F loads
+// pieces (8/F) q .. (8/F)(q + 1) - 1 and the meta, computes the integer sums of its sub-blocks, and
+// the F lanes add them by DPP (integer sums: exact in any order). A wave instruction then carries
+// 64 lanes of work instead of 64/F.
+//
+// x: the leader waves (the first 4 or 8) load x before any weight load of the workgroup (round r:
+// the 16-lane row h of a leader holds block 16r + 4 (v mod 4) + h, lane i of the row its values
+// 16i .. 16i + 15), apply the fused RMS_NORM (kPrepNorm: squares into LDS, the two halves of the 128
+// ordered partials on leaders 0 and 1, the scale through LDS flags), quantize every block (QACT
+// A256, 16-lane-row form: four blocks per wave) into LDS, and count themselves done on a flag.
+// Every wave, leaders included, issues its weight loads first and waits for the flag only when it
+// needs x. Vector-memory counters retire in order, so a leader's wait for x must never cover a
+// weight load: its x loads precede its weight loads, and their number is the same on every path
+// (measured: when the count differed between paths the compiler's join waited for the weights too,
+// and the quantization ended 1.8 us after x had arrived instead of 0.3 us). The x of the oldest
+// waves also returns first when the compute unit's requests queue behind the weight stream.
 // ---------------------------------------------------------------------------------------------
-// XM: 0 -- each wave picks its x form (one block: the whole-wave form); 1 / 2 -- every wave takes the
-// one-block / four-block form (the fused preparation, whose loads and indices are then compile-time).
-template <int P, bool ISUMS, int PREP, int XM, bool GLU>      // P: passes whose loads are in registers at once
+// Unit of lane slot ul in pass p when every pass covers upw units: u = upw p + ul (slot-major as in
+// mv_unit).
+__device__ __forceinline__ MvUnit mv_unit_f(uint32_t p, uint32_t ul, uint32_t upw, uint32_t R, uint32_t nunit) {
+    const uint32_t u = upw * p + ul;
+    const uint32_t uc = min(u, (nunit ? nunit : 1u) - 1u);
+    MvUnit m;
+    m.k = uc / R;
+    m.r = uc - m.k * R;
+    m.valid = u < nunit;
+    return m;
+}
+
+template <int F, bool ISUMS, int PREP, bool GLU>
 __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
+    constexpr uint32_t UPW = 64u / (uint32_t)F, NP = 8u / (uint32_t)F;   // units per pass, pieces per lane
     const WGeom g = wgeom(a.N, a.K >> 8, a.rb, true);
     const uint32_t nsb = g.nb, kx = g.q + (g.rem ? 1u : 0u);
     const int lane = (int)__lane_id();
@@ -217,146 +253,108 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     const uint32_t t = blockIdx.y;
     const float * x = a.x + (size_t)t * a.x_stride;
     const uint32_t B = blockIdx.x, row_lo = B * g.rb, nrow = wl_rows(g, B);
-    const uint32_t nunit = nrow * cnt, npass = (nunit + 63u) >> 6;
+    const uint32_t nunit = nrow * cnt, npass = (nunit + UPW - 1u) / UPW;
     int8_t * s_xq = (int8_t *)lds;
     int * s_xb = (int *)(lds + kMvWaves * kx * kXq4Stride);
     float * s_xd = (float *)(s_xb + kMvWaves * kx * 8u);
     float * s_t = s_xd + kMvWaves * kx;
     float * s_p = s_t + ((a.rb * nsb + 3u) & ~3u);                // 16-byte aligned
-    int * s_slow = (int *)(s_p + a.rb * 16u);
-    float * s_sq = (float *)(s_slow + 16);                        // kPrepNorm: K squares + 2 slots
+    float * s_sq = (float *)((int *)(s_p + a.rb * 16u) + 16);     // kPrepNorm: K squares + 2 slots
+    // 0 leaders with squares stored, 1 hi-half ready, 2 scale ready, 3 hi half, 4 scale,
+    // 5 leaders with quants stored, 6 some block has 0 < |d| < 2^-60
+    __shared__ uint32_t s_ctl[8];
 
-    // x first (vector-memory counters retire in order): the 16-lane row h = lane / 16 of the wave
-    // holds block k = 4 i + h of round i, lane i of the row its values 16 i .. 16 i + 15
-    // A wave with one block (cnt == 1) quantizes it with the whole wave instead (lane l: values
-    // 4 l .. 4 l + 3), a quarter of the per-lane work.
+    // Leaders: NL = 4 nlg waves; leader v handles the rounds r = v / 4 + nlg i (i = 0, 1, ...), its row h
+    // block 16 r + 4 (v mod 4) + h. The first RPL rounds of a leader are loaded before any weight load
+    // (unconditionally, at clamped addresses, so that every path has the same count of loads in flight
+    // and the waits for x never include a weight load); later rounds (K > 16384 only) after them.
+    constexpr uint32_t RPL = PREP == kPrepNorm ? 1u : 2u;
+    const uint32_t nrx = (nsb + 15u) >> 4;                        // rounds of 16 blocks
+    const uint32_t nlg = PREP == kPrepNorm ? nrx : min((nrx + 1u) >> 1, 2u);   // kPrepNorm: K <= 8192
+    const uint32_t nl = 4u * nlg, rg = w >> 2;
+    const bool leader = w < nl;
     const uint32_t h4 = (uint32_t)lane >> 4, l16 = (uint32_t)lane & 15u;
-    const bool one = XM == 0 ? cnt <= 1u : XM == 1;               // wave-uniform
-    auto load_x = [&](uint32_t i, float4 (&xr)[4]) {
-        const uint32_t s = min(w + 16u * (4u * i + h4), nsb - 1u);
+    auto xblk = [&](uint32_t r) -> uint32_t { return 16u * r + 4u * (w & 3u) + h4; };
+    auto xidx = [&](uint32_t r, uint32_t c) -> uint32_t { return 256u * min(xblk(r), nsb - 1u) + 16u * l16 + 4u * c; };
+    auto load_xr = [&](uint32_t r, float4 (&xr)[4]) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) xr[c] = *(const float4 *)(x + 256u * s + 16u * l16 + 4u * (uint32_t)c);
+        for (uint32_t c = 0; c < 4u; ++c) xr[c] = *(const float4 *)(x + xidx(r, c));
     };
-    auto xoff = [&](uint32_t c) -> uint32_t {                      // offset of float4 c of round 0
-        return one ? 256u * min(w, nsb - 1u) + 4u * (uint32_t)lane
-                   : 256u * min(w + 16u * h4, nsb - 1u) + 16u * l16 + 4u * c;
-    };
-    constexpr int NV = XM == 1 ? 1 : 4;                           // float4s of x per lane (prep forms)
-    float4 xv[4], pv[NV];
-    if (one) xv[0] = *(const float4 *)(x + xoff(0u));
-    else load_x(0u, xv);
-    if constexpr (PREP == kPrepNorm) {
-        const float * pl = a.pw ? a.pw : x;                       // without MUL: a valid address, unused
+    float4 xv[RPL][4], pv[4];                                     // pv: the norm weights of the leader's round
+    if (threadIdx.x < 8u) lds_st(s_ctl + threadIdx.x, 0u);
+    if (leader) {
 #pragma unroll
-        for (int c = 0; c < NV; ++c) pv[c] = *(const float4 *)(pl + xoff((uint32_t)c));
-    }
-    // kPrepNorm with one block per wave (K <= 4096): waves 12..15, which quantize before they issue
-    // their weight loads, also load the whole row (lane L = 64 (w - 12) + l: values 16 L .. 16 L + 15)
-    // and compute the scale alone, so that no wave waits for another that is held issuing its loads
-    constexpr bool SPLIT = PREP == kPrepNorm && XM == 1;
-    __shared__ uint32_t s_ctl[8];                                 // squares done, hi ready, s ready, hi, s
-    const uint32_t L = 64u * (w - 12u) + (uint32_t)lane;
-    float4 nv[4];
-    if constexpr (SPLIT) {
-        if (threadIdx.x == 0u) { lds_st(s_ctl, 0u); lds_st(s_ctl + 1, 0u); lds_st(s_ctl + 2, 0u); }
-        if (w >= 12u) {
+        for (uint32_t i = 0; i < RPL; ++i) load_xr(rg + nlg * i, xv[i]);
+        if constexpr (PREP == kPrepNorm) {
+            const float * pl = a.pw ? a.pw : x;                   // without MUL: a valid address, unused
 #pragma unroll
-            for (uint32_t c = 0; c < 4u; ++c) nv[c] = *(const float4 *)(x + min(16u * L + 4u * c, a.K - 4u));
+            for (uint32_t c = 0; c < 4u; ++c) pv[c] = *(const float4 *)(pl + xidx(rg, c));
         }
-        lds_wait_writes();                                        // the cleared flags before the barrier
     }
     uint32_t t64 = 0;
     if constexpr (GLU) t64 = a.ex.t64[lane];
+    lds_wait_writes();                                            // the cleared flags before the barrier
     x_first_barrier();
 
-    uint4 qv[P][8], mv[P];
-    auto load = [&](uint32_t p0) {
+    const uint32_t q = (uint32_t)lane % (uint32_t)F, ul = (uint32_t)lane / (uint32_t)F;
+    uint4 qv[NP], mv;
+    {
+        const MvUnit m = mv_unit_f(0u, ul, UPW, nrow, nunit);     // unconditional (clamped address)
+        const uint32_t sl = min(wl_slot(g, w, m.k), nsb - 1u);
+        mv = *(const uint4 *)(a.w + wl_meta_off(g, B, nrow, sl, m.r));
 #pragma unroll
-        for (int pp = 0; pp < P; ++pp) {
-            const MvUnit m = mv_unit(min(p0 + (uint32_t)pp, npass ? npass - 1u : 0u), lane, nrow, nunit);
-            const uint32_t sl = min(wl_slot(g, w, m.k), nsb - 1u);
-            mv[pp] = *(const uint4 *)(a.w + wl_meta_off(g, B, nrow, sl, m.r));
+        for (uint32_t jj = 0; jj < NP; ++jj) qv[jj] = *(const uint4 *)(a.w + wl_quant_off(g, B, nrow, NP * q + jj, sl, m.r));
+    }
+    // the addend of this thread's first stored row (tree store, first round); loaded by every thread
+    // at a clamped address, so that the count of loads in flight does not depend on the call
+    float add0;
+    {
+        const float * ap = (!GLU && a.add != nullptr) ? a.add + (size_t)t * a.add_stride + row_lo : x;
+        add0 = ap[min(threadIdx.x >> 4, nrow - 1u)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    if (leader) {
+        bool tiny_any = false;
+        auto qround = [&](uint32_t r, const float4 (&xr)[4]) {
+            float d;
+            int s16;
+            bool tiny;
+            const uint4 qq = qact_a256_row(xr, &d, &s16, &tiny);
+            const int s32 = s16 + dpp_i<kDppXor1>(s16);           // sum of the 32 quants of a sub-block
+            const uint32_t b = xblk(r);
+            if (b < nsb) {
+                const uint32_t xo = (b & 15u) * kx + (b >> 4);
+                *(uint4 *)(s_xq + xo * kXq4Stride + 16u * l16) = qq;
+                if ((l16 & 1u) == 0u) s_xb[xo * 8u + (l16 >> 1)] = s32;
+                if (l16 == 0u) s_xd[xo] = d;
+                tiny_any |= tiny;
+            }
+        };
+        if constexpr (PREP == kPrepNorm) {
+            if (xblk(rg) < nsb) {
 #pragma unroll
-            for (uint32_t j = 0; j < 8u; ++j) qv[pp][j] = *(const uint4 *)(a.w + wl_quant_off(g, B, nrow, j, sl, m.r));
-        }
-    };
-    // QACT A256 of the wave's blocks s = w + 16 k, four at a time. Round 0 is outside the loop: a
-    // loop whose body loads makes the compiler wait for every outstanding load at its header, and
-    // round 0 must wait only for the x loads issued before the weights.
-    bool tiny_any = false;
-    auto qact_round = [&](uint32_t i, const float4 (&xr)[4]) {
-        float d;
-        int s16;
-        bool tiny;
-        const uint4 qq = qact_a256_row(xr, &d, &s16, &tiny);
-        const int s32 = s16 + dpp_i<kDppXor1>(s16);               // sum of the 32 quants of a sub-block
-        const uint32_t k = 4u * i + h4;
-        if (k < cnt) {
-            const uint32_t xo = w * kx + k;
-            *(uint4 *)(s_xq + xo * kXq4Stride + 16u * l16) = qq;
-            if ((l16 & 1u) == 0u) s_xb[xo * 8u + (l16 >> 1)] = s32;
-            if (l16 == 0u) s_xd[xo] = d;
-            tiny_any |= tiny;
-        }
-    };
-    auto qact_first = [&]() {
-        if (!one) { qact_round(0u, xv); return; }
-        float d;
-        int s4;
-        bool tiny;
-        const uint32_t qq = qact_a256_wave(xv[0], &d, &s4, &tiny);
-        const int s32 = sum8_i(s4);                               // the 32 quants of sub-block lane / 8
-        const uint32_t xo = w * kx;
-        *(uint32_t *)(s_xq + xo * kXq4Stride + 4u * (uint32_t)lane) = qq;
-        if ((lane & 7) == 0) s_xb[xo * 8u + ((uint32_t)lane >> 3)] = s32;
-        if (lane == 0) s_xd[xo] = d;
-        tiny_any |= tiny;
-    };
-    // Waves 12..15 quantize their first round before they issue their weight loads: the weight
-    // stream of a compute unit is accepted at the rate HBM delivers it, so these waves would wait
-    // to issue anyway, and their QACT is then off the critical path. Waves 0..11 keep the memory
-    // pipe busy from the start and quantize while their loads are in flight (a wave blocked on
-    // issuing a load cannot quantize; the split was measured: 12 beats 4, 8 and none).
-    if constexpr (PREP == kPrepNone) {
-        if (w >= 12u && cnt) qact_first();
-        load(0u);                                                 // unconditional (clamped)
-        __builtin_amdgcn_sched_barrier(0);
-        if (w < 12u && cnt) qact_first();
-    } else if constexpr (SPLIT) {
-        if (w < 12u) {
-            load(0u);
-            __builtin_amdgcn_sched_barrier(0);
-            lds_flag_wait(s_ctl + 2, 1u);
-            const float sc = __uint_as_float(lds_ld(s_ctl + 4));
-            xv[0] = prep_norm_apply(xv[0], sc, pv[0], a.pw != nullptr);
-            if (cnt) qact_first();
-        } else {
-            // the squares of the row (strided layout: partial i reads i, i + 128, ...), then count the wave
-#pragma unroll
-            for (uint32_t c = 0; c < 4u; ++c) {
-                const uint32_t j = 16u * L + 4u * c;
-                if (j < a.K) *(float4 *)(s_sq + j) = sq4(nv[c]);
+                for (uint32_t c = 0; c < 4u; ++c) *(float4 *)(s_sq + xidx(rg, c)) = sq4(xv[0][c]);
             }
             lds_wait_writes();
             if (lane == 0) __hip_atomic_fetch_add(s_ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (w >= 14u) {                                       // no part in the chain: stream now
-                load(0u);
-                __builtin_amdgcn_sched_barrier(0);
-            } else {                                              // partials 0..63 (wave 12), 64..127 (wave 13)
-                lds_flag_wait(s_ctl, 4u);
-                // every partial has K / 128 terms (K % 256 == 0): branch-free reads (clamped index) and a
-                // select on the wave-uniform count, so that the 32 reads are in flight together
-                const uint32_t i = 64u * (w - 12u) + (uint32_t)lane, nk = a.K >> 7;
-                float v[32], p = 0.0f;
+            if (w < 2u) {                                         // partials 0..63 (leader 0), 64..127 (leader 1)
+                lds_flag_wait(s_ctl, nl);
+                // every partial has K / 128 terms: reads at clamped indices, a select on the count
+                const uint32_t i = 64u * w + (uint32_t)lane;
+                float p = 0.0f;
+                for (uint32_t j0 = 0; j0 < a.K; j0 += 128u * 16u) {
+                    float v[16];
 #pragma unroll
-                for (uint32_t k = 0; k < 32u; ++k) v[k] = s_sq[min(i + 128u * k, a.K - 1u)];
+                    for (uint32_t k = 0; k < 16u; ++k) v[k] = s_sq[min(j0 + i + 128u * k, a.K - 1u)];
 #pragma unroll
-                for (uint32_t k = 0; k < 32u; ++k) {
-                    const float q = p + v[k];                     // plain additions: see rms_tree64
-                    p = k < nk ? q : p;
+                    for (uint32_t k = 0; k < 16u; ++k) {
+                        const float s = p + v[k];                 // plain additions: see rms_tree64
+                        p = j0 + i + 128u * k < a.K ? s : p;
+                    }
                 }
                 p = rms_tree64(p);
-                if (w == 13u) {
+                if (w == 1u) {
                     if (lane == 0) lds_st(s_ctl + 3, __float_as_uint(p));
                     if (lane == 0) lds_flag_set(s_ctl + 1, 1u);
                 } else {
@@ -365,101 +363,96 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
                     if (lane == 0) lds_st(s_ctl + 4, __float_as_uint(sc));
                     if (lane == 0) lds_flag_set(s_ctl + 2, 1u);
                 }
-                load(0u);
-                __builtin_amdgcn_sched_barrier(0);
             }
             lds_flag_wait(s_ctl + 2, 1u);
             const float sc = __uint_as_float(lds_ld(s_ctl + 4));
-            xv[0] = prep_norm_apply(xv[0], sc, pv[0], a.pw != nullptr);
-            if (cnt) qact_first();
+#pragma unroll
+            for (uint32_t c = 0; c < 4u; ++c) xv[0][c] = prep_norm_apply(xv[0][c], sc, pv[c], a.pw != nullptr);
+            if (rg < nrx) qround(rg, xv[0]);
+        } else {
+            if (rg < nrx) qround(rg, xv[0]);
+            if (rg + nlg < nrx) qround(rg + nlg, xv[RPL - 1u]);
+            for (uint32_t r = rg + 2u * nlg; r < nrx; r += nlg) {  // K > 16384 only: loaded behind the weights
+                float4 xr[4];
+                load_xr(r, xr);
+                qround(r, xr);
+            }
         }
-    } else {
-        load(0u);                                                 // the norm runs under the weight stream
-        __builtin_amdgcn_sched_barrier(0);
-        float4 sq[NV];
-#pragma unroll
-        for (int c = 0; c < NV; ++c) sq[c] = sq4(xv[c]);
-        if (XM == 1 ? cnt == 1u : h4 < cnt) {                     // this lane's values are x's (not clamped copies)
-#pragma unroll
-            for (int c = 0; c < NV; ++c) *(float4 *)(s_sq + xoff((uint32_t)c)) = sq[c];
-        }
-        const float sc = prep_norm_scale(s_sq, a.K, a.inv_n, a.eps);
-#pragma unroll
-        for (int c = 0; c < NV; ++c) xv[c] = prep_norm_apply(xv[c], sc, pv[c], a.pw != nullptr);
-        if (cnt) qact_first();
+        if (__ballot(tiny_any) != 0ull && lane == 0) lds_st(s_ctl + 6, 1u);
+        lds_wait_writes();
+        if (lane == 0) __hip_atomic_fetch_add(s_ctl + 5, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    for (uint32_t i = 1; 4u * i < cnt; ++i) {                     // K > 16384 only (never with a prep)
-        float4 xr[4];
-        load_x(i, xr);
-        qact_round(i, xr);
-    }
-    const bool slow = __ballot(tiny_any) != 0ull;                 // wave-uniform
+    lds_flag_wait(s_ctl + 5, nl);
+    const bool slow = lds_ld(s_ctl + 6) != 0u;                    // workgroup-uniform
 
     const uint32_t m4 = 0x0F0F0F0Fu;
-    for (uint32_t p0 = 0; p0 < npass; p0 += P) {
-        if (p0) load(p0);
+    for (uint32_t p = 0; p < npass; ++p) {
+        if (p) {
+            const MvUnit m = mv_unit_f(p, ul, UPW, nrow, nunit);
+            const uint32_t sl = min(wl_slot(g, w, m.k), nsb - 1u);
+            mv = *(const uint4 *)(a.w + wl_meta_off(g, B, nrow, sl, m.r));
 #pragma unroll
-        for (int pp = 0; pp < P; ++pp) {
-            if (p0 + (uint32_t)pp >= npass) break;
-            const MvUnit m = mv_unit(p0 + (uint32_t)pp, lane, nrow, nunit);
-            const uint32_t xo = w * kx + m.k;
-            const int8_t * xb = s_xq + xo * kXq4Stride;
-            int S[8];
+            for (uint32_t jj = 0; jj < NP; ++jj)
+                qv[jj] = *(const uint4 *)(a.w + wl_quant_off(g, B, nrow, NP * q + jj, sl, m.r));
+        }
+        const MvUnit m = mv_unit_f(p, ul, UPW, nrow, nunit);
+        const uint32_t xo = w * kx + m.k;
+        const int8_t * xb = s_xq + xo * kXq4Stride;
+        const int * bsp = s_xb + xo * 8u;
+        // scales: byte 4 + j = sc_j | (m_j & 3) << 6; nibble j of bytes 12..15 = m_j >> 2
+        const uint4 mt = mv;
+        int isum = 0, msum = 0;
 #pragma unroll
-            for (int gg = 0; gg < 4; ++gg) {
-                int lo = 0, hi = 0;
+        for (uint32_t gi = 0; gi < NP / 2u; ++gi) {
+            const uint32_t gg = (NP / 2u) * q + gi;               // group of sub-blocks 2gg (low), 2gg + 1 (high)
+            int lo = 0, hi = 0;
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const uint4 qw = qv[pp][2 * gg + hh];
-                    const int4 xl = *(const int4 *)(xb + 64 * gg + 16 * hh);
-                    const int4 xh = *(const int4 *)(xb + 64 * gg + 32 + 16 * hh);
-                    lo = dot4((int)(qw.x & m4), xl.x, lo);
-                    lo = dot4((int)(qw.y & m4), xl.y, lo);
-                    lo = dot4((int)(qw.z & m4), xl.z, lo);
-                    lo = dot4((int)(qw.w & m4), xl.w, lo);
-                    hi = dot4((int)((qw.x >> 4) & m4), xh.x, hi);
-                    hi = dot4((int)((qw.y >> 4) & m4), xh.y, hi);
-                    hi = dot4((int)((qw.z >> 4) & m4), xh.z, hi);
-                    hi = dot4((int)((qw.w >> 4) & m4), xh.w, hi);
-                }
-                S[2 * gg] = lo;
-                S[2 * gg + 1] = hi;
+            for (uint32_t hh = 0; hh < 2u; ++hh) {
+                const uint4 qw = qv[2u * gi + hh];
+                const int4 xl = *(const int4 *)(xb + 64u * gg + 16u * hh);
+                const int4 xh = *(const int4 *)(xb + 64u * gg + 32u + 16u * hh);
+                lo = dot4((int)(qw.x & m4), xl.x, lo);
+                lo = dot4((int)(qw.y & m4), xl.y, lo);
+                lo = dot4((int)(qw.z & m4), xl.z, lo);
+                lo = dot4((int)(qw.w & m4), xl.w, lo);
+                hi = dot4((int)((qw.x >> 4) & m4), xh.x, hi);
+                hi = dot4((int)((qw.y >> 4) & m4), xh.y, hi);
+                hi = dot4((int)((qw.z >> 4) & m4), xh.z, hi);
+                hi = dot4((int)((qw.w >> 4) & m4), xh.w, hi);
             }
-            const int4 b0 = *(const int4 *)(s_xb + xo * 8u), b1 = *(const int4 *)(s_xb + xo * 8u + 4u);
-            const int bs[8] = { b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w };
-            const float dx = s_xd[xo];
-            // scales: byte 4 + j = sc_j | (m_j & 3) << 6; nibble j of bytes 12..15 = m_j >> 2
-            const uint4 mt = mv[pp];
-            int isum = 0, msum = 0;
-#pragma unroll
-            for (uint32_t j = 0; j < 8u; ++j) {
-                const uint32_t wd = j < 4u ? mt.y : mt.z, sh = 8u * (j & 3u);
-                const int sc = (int)__builtin_amdgcn_ubfe(wd, sh, 6);
-                const int mn = (int)(__builtin_amdgcn_ubfe(wd, sh + 6u, 2) | (__builtin_amdgcn_ubfe(mt.w, 4u * j, 4) << 2));
-                isum += __mul24(sc, S[j]);                        // |S_j| < 2^16, sc < 64: v_mad_i32_i24
-                msum += __mul24(mn, bs[j]);
-            }
-            const float d = h2f_fast(mt.x & 0xFFFFu), dm = h2f_fast(mt.x >> 16);
-            float tt;
-            if (!slow) tt = (d * dx) * (float)isum - (dm * dx) * (float)msum;
-            else tt = ssub(smul(smul(d, dx), i2f(isum)), smul(smul(dm, dx), i2f(msum)));
-            const uint32_t s = w + 16u * m.k;
-            if (m.valid) {
-                s_t[m.r * nsb + s] = tt;
-                if (ISUMS && t == 0u) {
-                    a.isums[(size_t)(row_lo + m.r) * 2u * nsb + 2u * s] = isum;
-                    a.isums[(size_t)(row_lo + m.r) * 2u * nsb + 2u * s + 1u] = msum;
-                }
+            const int2 bs = *(const int2 *)(bsp + 2u * gg);
+            const uint32_t wd = gg < 2u ? mt.y : mt.z, sh = 16u * (gg & 1u);
+            const int sc0 = (int)__builtin_amdgcn_ubfe(wd, sh, 6), sc1 = (int)__builtin_amdgcn_ubfe(wd, sh + 8u, 6);
+            const int mn0 = (int)(__builtin_amdgcn_ubfe(wd, sh + 6u, 2) | (__builtin_amdgcn_ubfe(mt.w, 8u * gg, 4) << 2));
+            const int mn1 = (int)(__builtin_amdgcn_ubfe(wd, sh + 14u, 2) | (__builtin_amdgcn_ubfe(mt.w, 8u * gg + 4u, 4) << 2));
+            isum += __mul24(sc0, lo) + __mul24(sc1, hi);          // |S_j| < 2^16, sc < 64: v_mad_i32_i24
+            msum += __mul24(mn0, bs.x) + __mul24(mn1, bs.y);
+        }
+        if constexpr (F >= 2) {
+            isum += dpp_i<kDppXor1>(isum);
+            msum += dpp_i<kDppXor1>(msum);
+        }
+        if constexpr (F >= 4) {
+            isum += dpp_i<kDppXor2>(isum);
+            msum += dpp_i<kDppXor2>(msum);
+        }
+        const float dx = s_xd[xo];
+        const float d = h2f_fast(mt.x & 0xFFFFu), dm = h2f_fast(mt.x >> 16);
+        float tt;
+        if (!slow) tt = (d * dx) * (float)isum - (dm * dx) * (float)msum;
+        else tt = ssub(smul(smul(d, dx), i2f(isum)), smul(smul(dm, dx), i2f(msum)));
+        const uint32_t s = w + 16u * m.k;
+        if (m.valid && q == 0u) {
+            s_t[m.r * nsb + s] = tt;
+            if (ISUMS && t == 0u) {
+                a.isums[(size_t)(row_lo + m.r) * 2u * nsb + 2u * s] = isum;
+                a.isums[(size_t)(row_lo + m.r) * 2u * nsb + 2u * s + 1u] = msum;
             }
         }
     }
     mv_wave_partials(g, s_t, s_p, nrow, w, slow);
-    if (lane == 0) s_slow[w] = slow ? 1 : 0;
     lds_barrier();
-    bool any_slow = false;
-#pragma unroll
-    for (int i = 0; i < kMvWaves; ++i) any_slow |= s_slow[i] != 0;
-    mv_tree_store<GLU>(a, s_p, nrow, row_lo, t, any_slow, t64);
+    mv_tree_store<GLU>(a, s_p, s_t, nrow, row_lo, t, slow, t64, add0);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -515,6 +508,11 @@ __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
         }
     };
     load(0u);                                                     // unconditional: no join before QACT
+    float add0 = 0.0f;                                            // the addend of this thread's first stored row
+    if constexpr (!GLU) {
+        if (a.add != nullptr && (threadIdx.x & 15u) == 0u && (threadIdx.x >> 4) < nrow)
+            add0 = a.add[(size_t)t * a.add_stride + row_lo + (threadIdx.x >> 4)];
+    }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (PREP == kPrepNorm) {
         float4 sq[XP];
@@ -569,7 +567,7 @@ __global__ __launch_bounds__(1024) void k_mv_q80(MvArgs a) {
     }
     mv_wave_partials(g, s_t, s_p, nrow, w, false);
     lds_barrier();
-    mv_tree_store<GLU>(a, s_p, nrow, row_lo, t, false, t64);
+    mv_tree_store<GLU>(a, s_p, s_t, nrow, row_lo, t, false, t64, add0);
 }
 
 }  // namespace tsr
@@ -601,15 +599,25 @@ size_t tsr_mv_prep_lds(uint32_t prep, uint32_t K) {   // K squares (16-byte padd
     return prep == tsr::kPrepNorm ? 4u * (((size_t)K + 3u) & ~(size_t)3u) + 32u : 0u;
 }
 
-template <int P, int PREP, int XM, bool GLU>
+template <int F, int PREP, bool GLU>
 static void launch_q4k(const tsr::MvArgs & a, dim3 grid, size_t lds, hipStream_t s) {
-    if constexpr (PREP == tsr::kPrepNone && XM == 0 && !GLU) {
+    if constexpr (PREP == tsr::kPrepNone && !GLU) {
         if (a.isums) {
-            hipLaunchKernelGGL((tsr::k_mv_q4k<P, true, PREP, XM, GLU>), grid, dim3(1024), lds, s, a);
+            hipLaunchKernelGGL((tsr::k_mv_q4k<F, true, PREP, GLU>), grid, dim3(1024), lds, s, a);
             return;
         }
     }
-    hipLaunchKernelGGL((tsr::k_mv_q4k<P, false, PREP, XM, GLU>), grid, dim3(1024), lds, s, a);
+    hipLaunchKernelGGL((tsr::k_mv_q4k<F, false, PREP, GLU>), grid, dim3(1024), lds, s, a);
+}
+template <int F>
+static void launch_q4k_v(const tsr::MvArgs & a, dim3 grid, size_t lds, hipStream_t s) {
+    if (a.prep == tsr::kPrepNorm) {
+        if (a.glu) launch_q4k<F, tsr::kPrepNorm, true>(a, grid, lds, s);
+        else launch_q4k<F, tsr::kPrepNorm, false>(a, grid, lds, s);
+    } else {
+        if (a.glu) launch_q4k<F, tsr::kPrepNone, true>(a, grid, lds, s);
+        else launch_q4k<F, tsr::kPrepNone, false>(a, grid, lds, s);
+    }
 }
 template <int P, int PREP, bool GLU>
 static void launch_q80(const tsr::MvArgs & a, dim3 grid, size_t lds, hipStream_t s) {
@@ -646,18 +654,11 @@ int tsr_launch_mv_q4_k(const tsr::MvArgs & a, hipStream_t s) {
     const uint32_t nsb = a.K / 256u;
     const size_t lds = mv_lds_fixed(TSR_HIP_FMT_Q4_K, nsb) + mv_lds_rows(a.rb, nsb) + tsr_mv_prep_lds(a.prep, a.K);
     const dim3 grid((a.N + a.rb - 1u) / a.rb, a.T);
-    if (a.prep == tsr::kPrepNorm) {                               // 36 load registers per pass
-        if (nsb <= 16u) {                                         // every wave: one super-block at most
-            if (a.glu) launch_q4k<1, tsr::kPrepNorm, 1, true>(a, grid, lds, s);
-            else launch_q4k<1, tsr::kPrepNorm, 1, false>(a, grid, lds, s);
-        } else {
-            if (a.glu) launch_q4k<1, tsr::kPrepNorm, 2, true>(a, grid, lds, s);
-            else launch_q4k<1, tsr::kPrepNorm, 2, false>(a, grid, lds, s);
-        }
-    } else {
-        if (a.glu) launch_q4k<1, tsr::kPrepNone, 0, true>(a, grid, lds, s);
-        else launch_q4k<1, tsr::kPrepNone, 0, false>(a, grid, lds, s);
-    }
+    // lanes per unit: the units of the wave with the most (rb rows x ceil(nsb / 16) slots) in one pass
+    const uint32_t upw = a.rb * ((nsb + 15u) / 16u);
+    if (upw <= 16u) launch_q4k_v<4>(a, grid, lds, s);
+    else if (upw <= 32u) launch_q4k_v<2>(a, grid, lds, s);
+    else launch_q4k_v<1>(a, grid, lds, s);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -137,6 +137,61 @@ __device__ __forceinline__ uint32_t row16_or(uint32_t m) {
     return m | (uint32_t)dpp_i<kDppRowMirror>((int)m);
 }
 
+// The common case of qact_a256_row in about a third of its instructions: a wave whose 64 lanes hold
+// only finite values, in whose rows amax is 0 or >= 2^-60, and whose rows' values of magnitude amax
+// all have one sign (the first largest is then any of them). A lane's largest positive and largest
+// negative magnitudes are a signed and an unsigned maximum of the raw bits; the quant of y = iscale x
+// (|y| <= 127 (1 + 2^-23)^2) is the low byte of the bits of y + 1.5 2^23, an f32 sum in [2^23, 2^24)
+// rounded to the integer nearest y, ties to even (1.5 2^23 is even), which is round_even8(y).
+// Returns false, wave-uniformly, when the wave does not qualify; the general form then runs.
+__device__ __forceinline__ bool qact_a256_row_fast(const float4 (&v)[4], uint4 * out, float * d, int * s16,
+                                                   bool * tiny) {
+    float xs[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { xs[4 * i] = v[i].x; xs[4 * i + 1] = v[i].y; xs[4 * i + 2] = v[i].z; xs[4 * i + 3] = v[i].w; }
+    int32_t ps[8];
+    uint32_t ns[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        ps[i] = max((int32_t)fb(xs[2 * i]), (int32_t)fb(xs[2 * i + 1]));
+        ns[i] = max(fb(xs[2 * i]), fb(xs[2 * i + 1]));
+    }
+#pragma unroll
+    for (int w = 4; w >= 1; w >>= 1) {
+#pragma unroll
+        for (int i = 0; i < w; ++i) { ps[i] = max(ps[i], ps[i + w]); ns[i] = max(ns[i], ns[i + w]); }
+    }
+    const uint32_t pm = ps[0] >= 0 ? (uint32_t)ps[0] : 0u;                 // largest positive magnitude
+    const uint32_t nm = ns[0] >= 0x80000000u ? (ns[0] & 0x7FFFFFFFu) : 0u;  // largest negative magnitude
+    const uint32_t m = umax_u(pm, nm);
+    if (__ballot(m >= 0x7F800000u) != 0ull) return false;                 // Inf or NaN in the wave
+    uint32_t amax = row16_umax(m);
+    amax = amax < 0x00800000u ? 0u : amax;
+    const bool zero = amax == 0u;
+    if (__ballot(!zero && amax < 0x21800000u) != 0ull) return false;      // FM products
+    const uint32_t sg = row16_or(zero ? 0u : ((pm == amax ? 1u : 0u) | (nm == amax ? 2u : 0u)));
+    if (__ballot(sg == 3u) != 0ull) return false;                         // +amax and -amax in a row
+    const float mx = bf(amax | (sg == 2u ? 0x80000000u : 0u));
+    const float iscale = zero ? 0.0f : -127.0f / mx;                      // = sdiv: both normal
+    uint32_t pk[4];
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t[j] = fb(iscale * xs[4 * i + j] + 12582912.0f);
+        pk[i] = pack4_i8((int32_t)t[0], (int32_t)t[1], (int32_t)t[2], (int32_t)t[3]);
+        s = dot4((int)pk[i], 0x01010101, s);
+    }
+    const float dd = zero ? 0.0f : 1.0f / iscale;                         // = srcp: both normal
+    const uint32_t ad = fb(dd) & 0x7FFFFFFFu;
+    *d = dd;
+    *s16 = s;
+    *tiny = ad != 0u && ad < 0x21800000u;
+    *out = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    return true;
+}
+
 // One A256 block held by an aligned 16-lane row: lane i of the row holds values 16 i .. 16 i + 15
 // (v[0..3]); the four rows of a wave quantize four blocks at once. Every lane of the wave must be
 // active. Returns the lane's 16 quants (bytes in value order); *d = the block's d (every lane of
@@ -146,6 +201,10 @@ __device__ __forceinline__ uint32_t row16_or(uint32_t m) {
 // The plain product iscale x rounds like FM(iscale, x) when the block's amax >= 2^-60 (see
 // qact_a32_lane); if any row of the wave has 0 < amax < 2^-60 the whole wave uses FM.
 __device__ __forceinline__ uint4 qact_a256_row(const float4 (&v)[4], float * d, int * s16, bool * tiny) {
+    {
+        uint4 r;
+        if (qact_a256_row_fast(v, &r, d, s16, tiny)) return r;
+    }
     float xs[16];
 #pragma unroll
     for (int i = 0; i < 4; ++i) { xs[4 * i] = v[i].x; xs[4 * i + 1] = v[i].y; xs[4 * i + 2] = v[i].z; xs[4 * i + 3] = v[i].w; }

@@ -149,6 +149,36 @@ __device__ __forceinline__ float4 prep_norm_apply(float4 v, float s, float4 w, b
     if (has_w) { v.x = smul(v.x, w.x); v.y = smul(v.y, w.y); v.z = smul(v.z, w.z); v.w = smul(v.w, w.w); }
     return v;
 }
+// prep_norm_apply over a leader's 16 values when the wave qualifies (wave-uniform result): the scale
+// is a normal number and every x and w is a normal number or a zero. DAZ is then the identity; x s
+// can be subnormal (FTZ) or overflow, never NaN; (x s) w can be subnormal or NaN (Inf 0), each
+// fixed with one class test. The result equals FM(FM(x, s), w) of the general form.
+__device__ __forceinline__ bool prep_norm_apply_fast(float4 (&v)[4], float s, const float4 (&w)[4], bool has_w) {
+    constexpr int kBad = 0x297;                                   // NaN, +-Inf, +-subnormal
+    bool bad = !__builtin_amdgcn_class(s, 0x108);                 // +-normal
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        bad |= __builtin_amdgcn_class(v[c].x, kBad) | __builtin_amdgcn_class(v[c].y, kBad) |
+               __builtin_amdgcn_class(v[c].z, kBad) | __builtin_amdgcn_class(v[c].w, kBad);
+        if (has_w)
+            bad |= __builtin_amdgcn_class(w[c].x, kBad) | __builtin_amdgcn_class(w[c].y, kBad) |
+                   __builtin_amdgcn_class(w[c].z, kBad) | __builtin_amdgcn_class(w[c].w, kBad);
+    }
+    if (__ballot(bad) != 0ull) return false;
+    auto ftz = [](float r) { return __builtin_amdgcn_class(r, 0x90) ? bf(fb(r) & 0x80000000u) : r; };
+    auto one = [&](float x, float wv) {
+        const float t = ftz(x * s);
+        if (!has_w) return t;
+        const float y = ftz(t * wv);
+        return __builtin_amdgcn_class(y, 0x3) ? bf(kNaN) : y;
+    };
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        v[c].x = one(v[c].x, w[c].x); v[c].y = one(v[c].y, w[c].y);
+        v[c].z = one(v[c].z, w[c].z); v[c].w = one(v[c].w, w[c].w);
+    }
+    return true;
+}
 __device__ __forceinline__ float4 sq4(float4 v) { return make_float4(sq_rule(v.x), sq_rule(v.y), sq_rule(v.z), sq_rule(v.w)); }
 // LDS flags between the waves of one workgroup (all resident together). A writer makes its earlier LDS
 // writes complete (lgkmcnt(0)) before it writes the flag; a reader polls the flag with volatile LDS
@@ -222,9 +252,8 @@ __device__ __forceinline__ float prep_norm_scale(float * s_sq, uint32_t K, float
 // the 16-lane row h of a leader holds block 16r + 4 (v mod 4) + h, lane i of the row its values
 // 16i .. 16i + 15), apply the fused RMS_NORM (kPrepNorm: squares into LDS, the two halves of the 128
 // ordered partials on leaders 0 and 1, the scale through LDS flags), quantize every block (QACT
-// A256, 16-lane-row form: four blocks per wave) into LDS, and count themselves done on a flag.
-// Every wave, leaders included, issues its weight loads first and waits for the flag only when it
-// needs x. Vector-memory counters retire in order, so a leader's wait for x must never cover a
+// A256, 16-lane-row form: four blocks per wave) into LDS; a workgroup barrier then publishes x to every wave.
+// Every wave, leaders included, issues its weight loads before that barrier. Vector-memory counters retire in order, so a leader's wait for x must never cover a
 // weight load: its x loads precede its weight loads, and their number is the same on every path
 // (measured: when the count differed between paths the compiler's join waited for the weights too,
 // and the quantization ended 1.8 us after x had arrived instead of 0.3 us). The x of the oldest
@@ -260,8 +289,8 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     float * s_t = s_xd + kMvWaves * kx;
     float * s_p = s_t + ((a.rb * nsb + 3u) & ~3u);                // 16-byte aligned
     float * s_sq = (float *)((int *)(s_p + a.rb * 16u) + 16);     // kPrepNorm: K squares + 2 slots
-    // 0 leaders with squares stored, 1 hi-half ready, 2 scale ready, 3 hi half, 4 scale,
-    // 5 leaders with quants stored, 6 some block has 0 < |d| < 2^-60
+    // 0 leaders with squares stored, 1 halves of the RMS sum stored, 3 lo half, 4 hi half,
+    // 6 some block has 0 < |d| < 2^-60
     __shared__ uint32_t s_ctl[8];
 
     // Leaders: NL = 4 nlg waves; leader v handles the rounds r = v / 4 + nlg i (i = 0, 1, ...), its row h
@@ -297,14 +326,16 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     x_first_barrier();
 
     const uint32_t q = (uint32_t)lane % (uint32_t)F, ul = (uint32_t)lane / (uint32_t)F;
-    uint4 qv[NP], mv;
-    {
-        const MvUnit m = mv_unit_f(0u, ul, UPW, nrow, nunit);     // unconditional (clamped address)
+    // pass p's loads (the unit clamped to the last: a pass beyond the wave's units loads a valid address)
+    auto loadp = [&](uint32_t p, uint4 (&qv)[NP], uint4 & mv) {
+        const MvUnit m = mv_unit_f(p, ul, UPW, nrow, nunit);
         const uint32_t sl = min(wl_slot(g, w, m.k), nsb - 1u);
-        mv = *(const uint4 *)(a.w + wl_meta_off(g, B, nrow, sl, m.r));
 #pragma unroll
         for (uint32_t jj = 0; jj < NP; ++jj) qv[jj] = *(const uint4 *)(a.w + wl_quant_off(g, B, nrow, NP * q + jj, sl, m.r));
-    }
+        mv = *(const uint4 *)(a.w + wl_meta_off(g, B, nrow, sl, m.r));   // last: the terms use it last
+    };
+    uint4 qa[NP], ma;
+    loadp(0u, qa, ma);
     // the addend of this thread's first stored row (tree store, first round); loaded by every thread
     // at a clamped address, so that the count of loads in flight does not depend on the call
     float add0;
@@ -332,42 +363,45 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
             }
         };
         if constexpr (PREP == kPrepNorm) {
+            const uint32_t nk = a.K >> 7;                         // terms per partial (K % 256 == 0)
             if (xblk(rg) < nsb) {
 #pragma unroll
                 for (uint32_t c = 0; c < 4u; ++c) *(float4 *)(s_sq + xidx(rg, c)) = sq4(xv[0][c]);
             }
             lds_wait_writes();
             if (lane == 0) __hip_atomic_fetch_add(s_ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (w < 2u) {                                         // partials 0..63 (leader 0), 64..127 (leader 1)
+            if (w < 2u) {
                 lds_flag_wait(s_ctl, nl);
-                // every partial has K / 128 terms: reads at clamped indices, a select on the count
                 const uint32_t i = 64u * w + (uint32_t)lane;
                 float p = 0.0f;
-                for (uint32_t j0 = 0; j0 < a.K; j0 += 128u * 16u) {
-                    float v[16];
+                // batches of 32 reads in flight; a full batch adds without selects
+                for (uint32_t k0 = 0; k0 < nk; k0 += 32u) {
+                    float v[32];
 #pragma unroll
-                    for (uint32_t k = 0; k < 16u; ++k) v[k] = s_sq[min(j0 + i + 128u * k, a.K - 1u)];
+                    for (uint32_t k = 0; k < 32u; ++k) v[k] = s_sq[i + 128u * min(k0 + k, nk - 1u)];
+                    if (k0 + 32u <= nk) {
 #pragma unroll
-                    for (uint32_t k = 0; k < 16u; ++k) {
-                        const float s = p + v[k];                 // plain additions: see rms_tree64
-                        p = j0 + i + 128u * k < a.K ? s : p;
+                        for (uint32_t k = 0; k < 32u; ++k) p = p + v[k];   // plain additions: see rms_tree64
+                    } else {
+#pragma unroll
+                        for (uint32_t k = 0; k < 32u; ++k) {
+                            const float t = p + v[k];
+                            p = k0 + k < nk ? t : p;
+                        }
                     }
                 }
                 p = rms_tree64(p);
-                if (w == 1u) {
-                    if (lane == 0) lds_st(s_ctl + 3, __float_as_uint(p));
-                    if (lane == 0) lds_flag_set(s_ctl + 1, 1u);
-                } else {
-                    lds_flag_wait(s_ctl + 1, 1u);
-                    const float sc = rms_scale(p, __uint_as_float(lds_ld(s_ctl + 3)), a.inv_n, a.eps);
-                    if (lane == 0) lds_st(s_ctl + 4, __float_as_uint(sc));
-                    if (lane == 0) lds_flag_set(s_ctl + 2, 1u);
-                }
+                if (lane == 0) lds_st(s_ctl + 3 + w, __float_as_uint(p));
+                lds_wait_writes();
+                if (lane == 0) __hip_atomic_fetch_add(s_ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
-            lds_flag_wait(s_ctl + 2, 1u);
-            const float sc = __uint_as_float(lds_ld(s_ctl + 4));
+            lds_flag_wait(s_ctl + 1, 2u);                         // both halves: every leader forms the scale
+            const float sc = rms_scale(__uint_as_float(lds_ld(s_ctl + 3)), __uint_as_float(lds_ld(s_ctl + 4)),
+                                       a.inv_n, a.eps);
+            if (!prep_norm_apply_fast(xv[0], sc, pv, a.pw != nullptr)) {
 #pragma unroll
-            for (uint32_t c = 0; c < 4u; ++c) xv[0][c] = prep_norm_apply(xv[0][c], sc, pv[c], a.pw != nullptr);
+                for (uint32_t c = 0; c < 4u; ++c) xv[0][c] = prep_norm_apply(xv[0][c], sc, pv[c], a.pw != nullptr);
+            }
             if (rg < nrx) qround(rg, xv[0]);
         } else {
             if (rg < nrx) qround(rg, xv[0]);
@@ -379,22 +413,14 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
             }
         }
         if (__ballot(tiny_any) != 0ull && lane == 0) lds_st(s_ctl + 6, 1u);
-        lds_wait_writes();
-        if (lane == 0) __hip_atomic_fetch_add(s_ctl + 5, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    lds_flag_wait(s_ctl + 5, nl);
+    // every wave waits here for the leaders' quants (a bare barrier: loads in flight stay in flight; a
+    // polling loop here made the compiler's waits for the weight loads after it conservative)
+    lds_barrier();
     const bool slow = lds_ld(s_ctl + 6) != 0u;                    // workgroup-uniform
 
     const uint32_t m4 = 0x0F0F0F0Fu;
-    for (uint32_t p = 0; p < npass; ++p) {
-        if (p) {
-            const MvUnit m = mv_unit_f(p, ul, UPW, nrow, nunit);
-            const uint32_t sl = min(wl_slot(g, w, m.k), nsb - 1u);
-            mv = *(const uint4 *)(a.w + wl_meta_off(g, B, nrow, sl, m.r));
-#pragma unroll
-            for (uint32_t jj = 0; jj < NP; ++jj)
-                qv[jj] = *(const uint4 *)(a.w + wl_quant_off(g, B, nrow, NP * q + jj, sl, m.r));
-        }
+    auto term = [&](uint32_t p, const uint4 (&qv)[NP], const uint4 & mv) {
         const MvUnit m = mv_unit_f(p, ul, UPW, nrow, nunit);
         const uint32_t xo = w * kx + m.k;
         const int8_t * xb = s_xq + xo * kXq4Stride;
@@ -449,6 +475,10 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
                 a.isums[(size_t)(row_lo + m.r) * 2u * nsb + 2u * s + 1u] = msum;
             }
         }
+    };
+    for (uint32_t p = 0; p < npass; ++p) {
+        if (p) loadp(p, qa, ma);
+        term(p, qa, ma);
     }
     mv_wave_partials(g, s_t, s_p, nrow, w, slow);
     lds_barrier();

@@ -150,38 +150,30 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     }
     const uint32_t item = blk.x / per_item, tt = (blk.x / 4u) % a.maxtiles, c = blk.x & 3u;
     const uint32_t g = blk.g, G = a.G, nh = a.n_head, E = a.E, nbk = E / 32u;
-    const FaItem it = a.items[item];
-    const FaSeg sg(it, c);
-    if (tt >= sg.nseg) return;                                    // no such segment (block-uniform)
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t ng = (a.kc.kv_size + 15u) / 16u;
-    // the segment's groups (clamped: loads of a missing group stay inside the item)
-    uint32_t ug[4];
-    bool gv[4];
-#pragma unroll
-    for (uint32_t k = 0; k < 4u; ++k) {
-        const uint32_t gi = 4u * tt + k;
-        gv[k] = gi < sg.nu;
-        ug[k] = min(sg.u_first + 4u * min(gi, sg.nu - 1u), ng - 1u);
-    }
+    // Everything that does not depend on the work item is requested before the item itself: the item
+    // read is a dependent round trip ahead of the K and V addresses, and the query values (whose
+    // quantization is the first step) then arrive at the same time as the item.
+    // (scalars in device memory are read with vector loads: a scalar load shares its counter with the
+    // LDS operations, so every LDS wait of the quantization below would wait for it too)
     int64_t cell_new = -1;
     int32_t pos = 0;
     if constexpr (ROPE) {
-        cell_new = *a.cell;
-        if (a.rtab == nullptr) pos = *a.pos;
+        cell_new = (int64_t)__builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(fa_rsrc(a.cell, 8u), 0, 0, 0));
+        if (a.rtab == nullptr) pos = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(fa_rsrc(a.pos, 4u), 0, 0, 0);
     }
     const uint32_t t64v = a.ex.t64[lane];
     // the launch's tag: reducer 0's epoch of the KV head + 1 (the epochs advance at the end of a launch);
     // what this workgroup writes carries its XCD too
     const uint32_t xcc = xcc_id();
-    const uint32_t tag = (a.ep[(size_t)g * G * (D / 64u)] + 1u) & kTagMask, tagw = tag | (xcc << 28);
-    // ROPE angles of the token (table): first, so that waiting for them is not waiting for K and V
+    const uint32_t epv = __builtin_amdgcn_raw_buffer_load_b32(fa_rsrc(a.ep + (size_t)g * G * (D / 64u), 4u), 0, 0, 0);
+    const uint32_t tag = (epv + 1u) & kTagMask, tagw = tag | (xcc << 28);
+    // ROPE angles of the token (table)
     float2 cs_tab = make_float2(0.0f, 0.0f);
     if constexpr (ROPE) {
         if (a.rtab != nullptr) cs_tab = *(const float2 *)(a.rtab + 2u * min(lane, a.n_dims / 2u - 1u));
     }
-
-    // ---- loads: the query values, the K rows of the thread's (cell, block), the V of its wave ----
+    // the query values (ROPE: the token's Q|K|V row, the new k and v rows too)
     const uint32_t nslot = G * D / 4u;                            // 8 lanes per 32-value block
     const float * qrow = a.q + (size_t)g * G * D;
     const uint32_t kslot = tid - nslot, vslot = kslot - D / 4u;
@@ -197,6 +189,69 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     const int32_t dj = (ROPE && a.neox && jh0 < a.n_dims) ? (jh0 < half ? (int32_t)half : -(int32_t)half) : 0;
     const float4 qpart = ROPE ? *(const float4 *)(qsrc + dj) : qv0;
     __builtin_amdgcn_sched_barrier(0);
+
+    // the work item, one word per lane (a vector load: waiting for it does not wait for the LDS traffic
+    // of the quantization, which runs while it is in flight)
+    static_assert(sizeof(FaItem) == 36, "FaItem: 9 words");
+    const uint32_t itw = ((const uint32_t *)(a.items + item))[min(lane, 8u)];
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- QACT of the query heads (ROPE: rotated first), the new k and v rows ----
+    uint32_t qq = 0;
+    float Dq = 0.0f;
+    if constexpr (ROPE) {
+        float c_l, s_l;
+        if (a.rtab != nullptr) {
+            c_l = cs_tab.x;
+            s_l = cs_tab.y;
+        } else {
+            rope_cs_lane(pos, half, a.ts, a.m, lane, &c_l, &s_l);
+        }
+        const float4 rot = rope4(qv0, qpart, jh0, a.n_dims, a.neox != 0u, c_l, s_l);   // every lane (bpermute)
+        const float4 r = is_v ? qv0 : rot;
+        qq = qact_a32_lane(r, &Dq);                               // every lane (8-lane groups)
+        if (tid < nslot) {
+            *(uint32_t *)(s_q + 4u * tid) = qq;
+            if ((lane & 7u) == 0u) s_dx[tid >> 3] = Dq;
+        } else if (is_k) {
+            *(uint32_t *)(s_kq + 4u * kslot) = qq;
+            if ((lane & 7u) == 0u) s_kd[kslot >> 3] = Dq;
+        } else if (is_v) {
+            *(uint32_t *)(s_vq + 4u * vslot) = qq;
+            if ((lane & 7u) == 0u) s_vd[vslot >> 3] = Dq;
+        }
+    } else {
+        qq = qact_a32_lane(qv0, &Dq);
+        if (tid < nslot) {
+            *(uint32_t *)(s_q + 4u * tid) = qq;
+            if ((lane & 7u) == 0u) s_dx[tid >> 3] = Dq;
+        }
+    }
+    if (tid < 64u) s_t64[tid] = t64v;
+
+    FaItem it;
+    it.t = __builtin_amdgcn_readlane(itw, 0);
+    it.u0 = __builtin_amdgcn_readlane(itw, 1);
+    it.n = __builtin_amdgcn_readlane(itw, 2);
+    it.c_lo = __builtin_amdgcn_readlane(itw, 3);
+    it.c_hi = __builtin_amdgcn_readlane(itw, 4);
+    it.general = __builtin_amdgcn_readlane(itw, 5);
+    it.s_off = __builtin_amdgcn_readlane(itw, 6);
+    it.tile0 = __builtin_amdgcn_readlane(itw, 7);
+    it.ntiles = __builtin_amdgcn_readlane(itw, 8);
+    const FaSeg sg(it, c);
+    if (tt >= sg.nseg) return;                                    // no such segment (block-uniform)
+    const uint32_t ng = (a.kc.kv_size + 15u) / 16u;
+    // the segment's groups (clamped: loads of a missing group stay inside the item)
+    uint32_t ug[4];
+    bool gv[4];
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; ++k) {
+        const uint32_t gi = 4u * tt + k;
+        gv[k] = gi < sg.nu;
+        ug[k] = min(sg.u_first + 4u * min(gi, sg.nu - 1u), ng - 1u);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     // K: thread = (cell j, block b = wave)
     const uint32_t j = lane, kkj = j >> 4, rrj = j & 15u;
     const uint32_t bk = wave < NBD ? wave : 0u;
@@ -210,29 +265,7 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     const uint32_t bv = wave < NBD ? wave : 0u, b0 = bv & ~1u;    // the 64-value slice: blocks b0, b0 + 1
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- QACT of the query heads (ROPE: rotated first), the new k and v rows ----
     if constexpr (ROPE) {
-        float c_l, s_l;
-        if (a.rtab != nullptr) {
-            c_l = cs_tab.x;
-            s_l = cs_tab.y;
-        } else {
-            rope_cs_lane(pos, half, a.ts, a.m, lane, &c_l, &s_l);
-        }
-        const float4 rot = rope4(qv0, qpart, jh0, a.n_dims, a.neox != 0u, c_l, s_l);   // every lane (bpermute)
-        const float4 r = is_v ? qv0 : rot;
-        float Dq;
-        const uint32_t qq = qact_a32_lane(r, &Dq);                // every lane (8-lane groups)
-        if (tid < nslot) {
-            *(uint32_t *)(s_q + 4u * tid) = qq;
-            if ((lane & 7u) == 0u) s_dx[tid >> 3] = Dq;
-        } else if (is_k) {
-            *(uint32_t *)(s_kq + 4u * kslot) = qq;
-            if ((lane & 7u) == 0u) s_kd[kslot >> 3] = Dq;
-        } else if (is_v) {
-            *(uint32_t *)(s_vq + 4u * vslot) = qq;
-            if ((lane & 7u) == 0u) s_vd[vslot >> 3] = Dq;
-        }
         const bool cell_ok = cell_new >= 0 && cell_new < (int64_t)a.kc.kv_size && cell_new < (int64_t)a.vc.kv_size;
         if (item == 0u && tt == 0u && c == (it.u0 & 3u)) {       // the caches' copy of the new rows
             if (cell_ok && (is_k || is_v))
@@ -247,15 +280,7 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
             }
             if (!cell_ok && tid == 0u && g == 0u && a.bad != nullptr) *a.bad = 1;
         }
-    } else {
-        float Dq;
-        const uint32_t qq = qact_a32_lane(qv0, &Dq);
-        if (tid < nslot) {
-            *(uint32_t *)(s_q + 4u * tid) = qq;
-            if ((lane & 7u) == 0u) s_dx[tid >> 3] = Dq;
-        }
     }
-    if (tid < 64u) s_t64[tid] = t64v;
     lds_barrier();                                                // K and V stay in flight
 
     // ---- scores: the block terms of (cell j, block b) for every head ----

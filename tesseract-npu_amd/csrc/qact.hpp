@@ -19,7 +19,42 @@ __device__ __forceinline__ uint32_t umax_u(uint32_t a, uint32_t b) { return a > 
 
 // One A32 block held by the 8 lanes of an aligned group: returns this lane's 4 quants packed
 // little-endian and the block's D in *D (every lane of the group).
+// The common case of qact_a32_lane: a wave whose values are all finite and whose blocks have amax = 0
+// or amax >= 2^-60. DAZ then acts on the maximum only (a subnormal maximum means a block of zeros after
+// DAZ), d = amax / 127 and RC(d) are plain IEEE operations on normal numbers, the plain product
+// rounds like FM (see below), and f32(fp16(d)) is the hardware's RNE conversion (fp16 denormals on),
+// which is the rule's for every finite d. Returns false, wave-uniformly, when the wave does not
+// qualify; the general form then runs.
+__device__ __forceinline__ bool qact_a32_lane_fast(const float4 v, uint32_t * out, float * D) {
+    const float xs[4] = { v.x, v.y, v.z, v.w };
+    bool nonfin = false;
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        nonfin |= __builtin_amdgcn_class(xs[i], 0x207);           // NaN, +-Inf
+        m = umax_u(m, fb(xs[i]) & 0x7FFFFFFFu);
+    }
+    if (__ballot(nonfin) != 0ull) return false;
+    m = umax_u(m, (uint32_t)dpp_i<kDppXor1>((int)m));
+    m = umax_u(m, (uint32_t)dpp_i<kDppXor2>((int)m));
+    m = umax_u(m, (uint32_t)dpp_i<kDppRowHalfMirror>((int)m));
+    m = m < 0x00800000u ? 0u : m;
+    if (__ballot(m != 0u && m < 0x21800000u) != 0ull) return false;
+    const float d = bf(m) / 127.0f;                               // = sdiv: normal operands and result
+    const float id = m ? 1.0f / d : 0.0f;                         // = srcp
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) packed |= ((uint32_t)round_away8(xs[i] * id) & 0xFFu) << (8 * i);
+    *out = packed;
+    *D = (float)(_Float16)d;
+    return true;
+}
+
 __device__ __forceinline__ uint32_t qact_a32_lane(const float4 v, float * D) {
+    {
+        uint32_t r;
+        if (qact_a32_lane_fast(v, &r, D)) return r;
+    }
     const float xs[4] = { v.x, v.y, v.z, v.w };
     uint32_t m = 0;
 #pragma unroll

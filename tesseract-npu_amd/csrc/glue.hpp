@@ -161,6 +161,43 @@ __device__ __forceinline__ void rope_cs_lane(int32_t pos, uint32_t half, float t
 // NORMAL pairs (2i, 2i + 1) lie inside the 4 values; NEOX pairs (i, i + half) take the partner from
 // `part` (the 4 values half away). y0 = FS(FM(x0, c), FM(x1, s)), y1 = FA(FM(x0, s), FM(x1, c));
 // values from n_dims on are kept.
+// rope4 when the lane's angles come from the table in registers -- csa: (cos, sin) of angles i, i + 1,
+// csb: of angles i + 2, i + 3, with i the lane's first angle (NORM: jh0 / 2, NEOX: jh0 mod n_dims / 2)
+// -- and the wave qualifies (wave-uniform result): every x, partner, cos and sin a normal number or a
+// zero. DAZ is then the identity; a product can be subnormal (FTZ) or overflow, never NaN; the sum or
+// difference of two such products can be subnormal or NaN (Inf - Inf); each case is one class test.
+// The result equals rope4's. Returns false when the wave does not qualify.
+__device__ __forceinline__ bool rope4_tab_fast(float4 & out, float4 v, float4 part, uint32_t jh0, uint32_t n_dims,
+                                               bool neox, float4 csa, float4 csb) {
+    const uint32_t half = n_dims / 2u;
+    const float x[4] = { v.x, v.y, v.z, v.w }, pr[4] = { part.x, part.y, part.z, part.w };
+    const float c[4] = { csa.x, neox ? csa.z : csa.x, neox ? csb.x : csa.z, neox ? csb.z : csa.z };
+    const float sn[4] = { csa.y, neox ? csa.w : csa.y, neox ? csb.y : csa.w, neox ? csb.w : csa.w };
+    constexpr int kBad = 0x297;                                   // NaN, +-Inf, +-subnormal
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        bad |= __builtin_amdgcn_class(x[k], kBad) | __builtin_amdgcn_class(c[k], kBad) | __builtin_amdgcn_class(sn[k], kBad);
+        if (neox) bad |= __builtin_amdgcn_class(pr[k], kBad);
+    }
+    if (__ballot(bad) != 0ull) return false;
+    auto ftz = [](float r) { return __builtin_amdgcn_class(r, 0x90) ? bf(fb(r) & 0x80000000u) : r; };
+    float y[4];
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; ++k) {
+        const uint32_t jh = jh0 + k;
+        const bool first = neox ? jh < half : (jh & 1u) == 0u;
+        const float x0 = first ? x[k] : (neox ? pr[k] : x[k ^ 1u]);
+        const float x1 = first ? (neox ? pr[k] : x[k ^ 1u]) : x[k];
+        const float p1 = ftz(x0 * (first ? c[k] : sn[k])), p2 = ftz(x1 * (first ? sn[k] : c[k]));
+        float r = ftz(first ? p1 - p2 : p1 + p2);
+        r = __builtin_amdgcn_class(r, 0x3) ? bf(kNaN) : r;
+        y[k] = jh < n_dims ? r : x[k];
+    }
+    out = make_float4(y[0], y[1], y[2], y[3]);
+    return true;
+}
+
 __device__ __forceinline__ float4 rope4(float4 v, float4 part, uint32_t jh0, uint32_t n_dims, bool neox, float c_l,
                                         float s_l) {
     const uint32_t half = n_dims / 2u;

@@ -168,11 +168,6 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     const uint32_t xcc = xcc_id();
     const uint32_t epv = __builtin_amdgcn_raw_buffer_load_b32(fa_rsrc(a.ep + (size_t)g * G * (D / 64u), 4u), 0, 0, 0);
     const uint32_t tag = (epv + 1u) & kTagMask, tagw = tag | (xcc << 28);
-    // ROPE angles of the token (table)
-    float2 cs_tab = make_float2(0.0f, 0.0f);
-    if constexpr (ROPE) {
-        if (a.rtab != nullptr) cs_tab = *(const float2 *)(a.rtab + 2u * min(lane, a.n_dims / 2u - 1u));
-    }
     // the query values (ROPE: the token's Q|K|V row, the new k and v rows too)
     const uint32_t nslot = G * D / 4u;                            // 8 lanes per 32-value block
     const float * qrow = a.q + (size_t)g * G * D;
@@ -182,9 +177,26 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     const float * src = a.q + (size_t)nh * D + (size_t)g * D + (is_v ? E + 4u * vslot : 4u * (is_k ? kslot : 0u));
     const uint32_t jq = 4u * min(tid, nslot - 1u);
     const float * qsrc = (ROPE && tid >= nslot) ? src : qrow + jq;
-    const float4 qv0 = *(const float4 *)qsrc;
     const uint32_t half = a.n_dims / 2u;
     const uint32_t jh0 = tid < nslot ? jq % D : (is_k ? 4u * kslot : D);
+    // ROPE angles of the token (table): lane l's pair for the general form (read across lanes), and
+    // the pairs of the lane's own 4 values for the fast form (n_dims >= 8: NORM angles jh0 / 2 .. + 1,
+    // NEOX angles jh0 mod half .. + 3; clamped, even, so each float4 is aligned)
+    float2 cs_tab = make_float2(0.0f, 0.0f);
+    float4 cs_a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), cs_b = cs_a;
+    const bool tab_fast = ROPE && a.rtab != nullptr && a.n_dims >= 8u;
+    if constexpr (ROPE) {
+        if (a.rtab != nullptr) {
+            cs_tab = *(const float2 *)(a.rtab + 2u * min(lane, half - 1u));
+            if (tab_fast) {
+                const uint32_t ib = a.neox ? (jh0 < half ? jh0 : (jh0 < a.n_dims ? jh0 - half : 0u)) : min(jh0, a.n_dims) >> 1;
+                const uint32_t ia = min(ib, half - 2u) & ~1u, ic = min(ib + 2u, half - 2u) & ~1u;
+                cs_a = *(const float4 *)(a.rtab + 2u * ia);
+                cs_b = *(const float4 *)(a.rtab + 2u * ic);
+            }
+        }
+    }
+    const float4 qv0 = *(const float4 *)qsrc;
     // ROPE NEOX: the 4 values half a rotation away (their own address otherwise: no load waits on a branch)
     const int32_t dj = (ROPE && a.neox && jh0 < a.n_dims) ? (jh0 < half ? (int32_t)half : -(int32_t)half) : 0;
     const float4 qpart = ROPE ? *(const float4 *)(qsrc + dj) : qv0;
@@ -207,7 +219,9 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
         } else {
             rope_cs_lane(pos, half, a.ts, a.m, lane, &c_l, &s_l);
         }
-        const float4 rot = rope4(qv0, qpart, jh0, a.n_dims, a.neox != 0u, c_l, s_l);   // every lane (bpermute)
+        float4 rot;
+        if (!(tab_fast && rope4_tab_fast(rot, qv0, qpart, jh0, a.n_dims, a.neox != 0u, cs_a, cs_b)))
+            rot = rope4(qv0, qpart, jh0, a.n_dims, a.neox != 0u, c_l, s_l);   // every lane (bpermute)
         const float4 r = is_v ? qv0 : rot;
         qq = qact_a32_lane(r, &Dq);                               // every lane (8-lane groups)
         if (tid < nslot) {

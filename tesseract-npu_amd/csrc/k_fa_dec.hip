@@ -208,9 +208,8 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     const uint32_t itw = ((const uint32_t *)(a.items + item))[min(lane, 8u)];
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- QACT of the query heads (ROPE: rotated first), the new k and v rows ----
-    uint32_t qq = 0;
-    float Dq = 0.0f;
+    // ---- ROPE of the query heads and the new k row ----
+    float4 r = qv0;
     if constexpr (ROPE) {
         float c_l, s_l;
         if (a.rtab != nullptr) {
@@ -222,27 +221,10 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
         float4 rot;
         if (!(tab_fast && rope4_tab_fast(rot, qv0, qpart, jh0, a.n_dims, a.neox != 0u, cs_a, cs_b)))
             rot = rope4(qv0, qpart, jh0, a.n_dims, a.neox != 0u, c_l, s_l);   // every lane (bpermute)
-        const float4 r = is_v ? qv0 : rot;
-        qq = qact_a32_lane(r, &Dq);                               // every lane (8-lane groups)
-        if (tid < nslot) {
-            *(uint32_t *)(s_q + 4u * tid) = qq;
-            if ((lane & 7u) == 0u) s_dx[tid >> 3] = Dq;
-        } else if (is_k) {
-            *(uint32_t *)(s_kq + 4u * kslot) = qq;
-            if ((lane & 7u) == 0u) s_kd[kslot >> 3] = Dq;
-        } else if (is_v) {
-            *(uint32_t *)(s_vq + 4u * vslot) = qq;
-            if ((lane & 7u) == 0u) s_vd[vslot >> 3] = Dq;
-        }
-    } else {
-        qq = qact_a32_lane(qv0, &Dq);
-        if (tid < nslot) {
-            *(uint32_t *)(s_q + 4u * tid) = qq;
-            if ((lane & 7u) == 0u) s_dx[tid >> 3] = Dq;
-        }
+        r = is_v ? qv0 : rot;
     }
-    if (tid < 64u) s_t64[tid] = t64v;
 
+    // ---- the work item; the segment's K and V requested (the quantization below runs while they fly) ----
     FaItem it;
     it.t = __builtin_amdgcn_readlane(itw, 0);
     it.u0 = __builtin_amdgcn_readlane(itw, 1);
@@ -265,7 +247,6 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
         gv[k] = gi < sg.nu;
         ug[k] = min(sg.u_first + 4u * min(gi, sg.nu - 1u), ng - 1u);
     }
-    __builtin_amdgcn_sched_barrier(0);
     // K: thread = (cell j, block b = wave)
     const uint32_t j = lane, kkj = j >> 4, rrj = j & 15u;
     const uint32_t bk = wave < NBD ? wave : 0u;
@@ -277,8 +258,31 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     // (value l % 16, group l / 16) for the matrix-core operand
     const uint32_t hr = lane >> 4, kk = (lane >> 2) & 3u, quad = lane & 3u;
     const uint32_t bv = wave < NBD ? wave : 0u, b0 = bv & ~1u;    // the 64-value slice: blocks b0, b0 + 1
+    // V: the scales of the lane's 4 cells in the slice's two blocks (8 contiguous bytes each), and the
+    // matrix-core operand
+    uint2 mvb[2];
+#pragma unroll
+    for (uint32_t e = 0; e < 2u; ++e)
+        mvb[e] = *(const uint2 *)((const uint16_t *)a.vc.base + ((size_t)ug[kk] * nbk + (size_t)g * NBD + b0 + e) * 16u +
+                                  4u * quad);
+    const uint8_t * vq = a.vc.base + a.vc.quant_off + ((size_t)ug[lane >> 4] * E + (size_t)g * D + 32u * bv + (lane & 15u)) * 16u;
+    int4 bq0 = *(const int4 *)vq, bq1 = *(const int4 *)(vq + 256u);
     __builtin_amdgcn_sched_barrier(0);
 
+    // ---- QACT of the query heads, the new k and v rows ----
+    float Dq;
+    const uint32_t qq = qact_a32_lane(r, &Dq);                    // every lane (8-lane groups)
+    if (tid < nslot) {
+        *(uint32_t *)(s_q + 4u * tid) = qq;
+        if ((lane & 7u) == 0u) s_dx[tid >> 3] = Dq;
+    } else if (is_k) {
+        *(uint32_t *)(s_kq + 4u * kslot) = qq;
+        if ((lane & 7u) == 0u) s_kd[kslot >> 3] = Dq;
+    } else if (is_v) {
+        *(uint32_t *)(s_vq + 4u * vslot) = qq;
+        if ((lane & 7u) == 0u) s_vd[vslot >> 3] = Dq;
+    }
+    if (tid < 64u) s_t64[tid] = t64v;
     if constexpr (ROPE) {
         const bool cell_ok = cell_new >= 0 && cell_new < (int64_t)a.kc.kv_size && cell_new < (int64_t)a.vc.kv_size;
         if (item == 0u && tt == 0u && c == (it.u0 & 3u)) {       // the caches' copy of the new rows
@@ -323,15 +327,6 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
             s_t[(h * 4u + wave) * 64u + j] = 0.0f + t;
         }
     }
-    // the V rows load now: K first across the whole launch, V during the exchange of the maxima
-    // the scales of the lane's 4 cells in the slice's two blocks (8 contiguous bytes each)
-    uint2 mvb[2];
-#pragma unroll
-    for (uint32_t e = 0; e < 2u; ++e)
-        mvb[e] = *(const uint2 *)((const uint16_t *)a.vc.base + ((size_t)ug[kk] * nbk + (size_t)g * NBD + b0 + e) * 16u +
-                                  4u * quad);
-    const uint8_t * vq = a.vc.base + a.vc.quant_off + ((size_t)ug[lane >> 4] * E + (size_t)g * D + 32u * bv + (lane & 15u)) * 16u;
-    int4 bq0 = *(const int4 *)vq, bq1 = *(const int4 *)(vq + 256u);
     __syncthreads();
     // wave h = head h: tree16 over the block terms, the mask, the segment maximum
     const uint32_t floor_key = maxt_key_f(bf(kMFloor));

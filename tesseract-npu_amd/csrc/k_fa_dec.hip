@@ -499,13 +499,17 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     }
 }
 
-// The reducers of a KV head: workgroup (head r, 64-value part vp), thread = (value, channel c), polls the
-// segments' results of its head until every one carries the launch's tag, then chains channel c's
-// segments in order (AT 6.4 O, 6.5 l), CTREE over the channels (AT 5.6), merges the items in chunk
-// order (AMERGE) and normalizes (ANORM, AT 5.7). Slots and results carry the launch's tag (an epoch + 1,
-// one epoch word per reducer, each advanced by its reducer at its end): nothing is cleared, and a store
-// that lands after an expired wait carries a tag no later launch expects. A reducer only waits for
-// segments, which come before it in dispatch order.
+// The reducers of a KV head: workgroup (head r, 64-value part vp), thread = (value, channel c): channel c's
+// chains of segment results in order (AT 6.4 O, 6.5 l), CTREE over the channels (AT 5.6), the merge of
+// the items in chunk order (AMERGE) and ANORM (AT 5.7). With one round of items (<= kRedItems, the
+// decode at up to 6 K cells) the row-sum side comes first: the chunk maxima and the segments' row sums
+// are stored at the segments' EXP step, so the merge factors and the l merge are done while the
+// segments' P.V still runs, and only the O side waits for the last segment. Several rounds poll each
+// round's outputs, row sums and maxima together (their reducers start late: the grid is larger than the
+// resident workgroups). Every result carries
+// the launch's tag (an epoch + 1, one epoch word per reducer, each advanced by its reducer at its end):
+// nothing is cleared, and a store that lands after an expired wait carries a tag no later launch
+// expects. A reducer only waits for segments, which come before it in dispatch order.
 constexpr uint32_t kRedItems = 3;                                 // items loaded per round
 
 template <int D, bool LOCAL>
@@ -528,49 +532,39 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
         s_it[3u * k + 2u] = ik.tile0;
     }
     __syncthreads();
+    // the segments of channel c of the round's items
+    auto round_items = [&](uint32_t k0, uint32_t (&ns)[kRedItems], uint32_t (&tl0)[kRedItems]) {
+#pragma unroll
+        for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+            const uint32_t k = min(k0 + kq, ni - 1u);
+            FaItem ik{};
+            ik.u0 = s_it[3u * k];
+            ik.n = s_it[3u * k + 1u];
+            tl0[kq] = s_it[3u * k + 2u];
+            ns[kq] = FaSeg(ik, c).nseg;
+        }
+    };
     float O = 0.0f, l = 0.0f, mr = 0.0f;
-    for (uint32_t k0 = 0; k0 < ni; k0 += kRedItems) {
-        // wave c polls its round's results until every one carries the launch's tag: lane v's value of
-        // channel c in each segment, lane s's row sum of segment s, lane kq's chunk maximum of item kq
-        uint64_t po[kRedItems][8], pl[kRedItems], pm;
-        uint32_t ns[kRedItems];
+    if (ni <= kRedItems) {
+        // One round: the row-sum side first (its data are published at the segments' EXP step), the
+        // merge factors and the l merge on wave 0 while the other waves already poll the outputs.
+        const uint32_t k0 = 0;
+        float fx = 0.0f;
+        uint32_t ns[kRedItems], tl0[kRedItems];
+        round_items(k0, ns, tl0);
+        uint64_t pl[kRedItems], pm;
         uint32_t spins = 0;
         for (;;) {
             bool ok = true;
 #pragma unroll
             for (uint32_t kq = 0; kq < kRedItems; ++kq) {
-                const uint32_t k = min(k0 + kq, ni - 1u);
-                FaItem ik{};
-                ik.u0 = s_it[3u * k];
-                ik.n = s_it[3u * k + 1u];
-                const uint32_t tile0 = s_it[3u * k + 2u];
-                const FaSeg sc(ik, c);
-                ns[kq] = sc.nseg;
-#pragma unroll
-                for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
-                    const size_t row = ((size_t)(tile0 + min(sgi, max(sc.nseg, 1u) - 1u)) * 4u + c) * nh + hh;
-                    po[kq][sgi] = ld_tag(a.seg_o + row * D + v);
-                }
-                const size_t lrow = ((size_t)(tile0 + min(lane, max(sc.nseg, 1u) - 1u)) * 4u + c) * nh + hh;
+                const size_t lrow = ((size_t)(tl0[kq] + min(lane, max(ns[kq], 1u) - 1u)) * 4u + c) * nh + hh;
                 pl[kq] = ld_tag(a.seg_l + lrow);
-            }
-            pm = ld_tag(a.m_item + (size_t)min(k0 + min(lane, kRedItems - 1u), ni - 1u) * nh + hh);
-            bool near = true;                                     // every writer shared this XCD
-#pragma unroll
-            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
-#pragma unroll
-                for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
-                    ok &= sgi >= ns[kq] || tag_is((uint32_t)(po[kq][sgi] >> 32), tag);
-                    near &= sgi >= ns[kq] || (uint32_t)(po[kq][sgi] >> 60) == xcc;
-                }
                 ok &= lane >= ns[kq] || tag_is((uint32_t)(pl[kq] >> 32), tag);
             }
+            pm = ld_tag(a.m_item + (size_t)min(k0 + min(lane, kRedItems - 1u), ni - 1u) * nh + hh);
             ok &= tag_is((uint32_t)(pm >> 32), tag);
-            if (__all(ok)) {
-                if (LOCAL && __any(!near) && lane == 0u && a.bad != nullptr)
-                    __hip_atomic_fetch_or(a.bad, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
+            if (__all(ok)) break;
             if (++spins >= a.spin_max) {
                 if (lane == 0u && a.bad != nullptr)
                     __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -578,34 +572,21 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
             }
             __builtin_amdgcn_s_sleep(2);
         }
-        float xo[kRedItems][8], xl[kRedItems][8], mkr[kRedItems];
+        float mkr[kRedItems];
 #pragma unroll
-        for (uint32_t kq = 0; kq < kRedItems; ++kq) {
-#pragma unroll
-            for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
-                xo[kq][sgi] = bf((uint32_t)po[kq][sgi]);
-                xl[kq][sgi] = bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pl[kq], (int)sgi));
-            }
+        for (uint32_t kq = 0; kq < kRedItems; ++kq) {             // channel c's segment sums in order
             mkr[kq] = bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pm, (int)kq));
-        }
+            float Lc = 0.0f;
 #pragma unroll
-        for (uint32_t kq = 0; kq < kRedItems; ++kq) {             // channel c's segments in order
-            float Oc = 0.0f, Lc = 0.0f;
-#pragma unroll
-            for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
-                if (sgi < ns[kq]) {
-                    Oc = sadd_n(Oc, xo[kq][sgi]);
-                    Lc = sadd_n(Lc, xl[kq][sgi]);
-                }
-            }
-            s_x[(kq * 4u + c) * 64u + lane] = Oc;
+            for (uint32_t sgi = 0; sgi < 8u; ++sgi)
+                if (sgi < ns[kq]) Lc = sadd_n(Lc, bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pl[kq], (int)sgi)));
             if (lane == 0u) s_x[1024u + kq * 4u + c] = Lc;
         }
         __syncthreads();
-        if (c == 0u) {                                            // CTREE, then AMERGE, in chunk order
+        if (c == 0u) {
             // the running maxima are a MAXT scan of the chunk maxima, so every merge factor of the round is
-            // known before the merge: lane 2 kq + b evaluates EXP((prev - mrun_kq) scale) for b = 0 (the
-            // running sums) or EXP((m_kq - mrun_kq) scale) for b = 1 (the chunk's), all at once
+            // known now: lane 2 kq + b evaluates EXP((prev - mrun_kq) scale) for b = 0 (the running sums) or
+            // EXP((m_kq - mrun_kq) scale) for b = 1 (the chunk's), all at once; kept for the O side
             float mrun[kRedItems], prev[kRedItems];
             float m = mr;
 #pragma unroll
@@ -622,27 +603,197 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
                     from = (lane & 1u) ? mkr[kq] : prev[kq];
                     to = mrun[kq];
                 }
-            const float fx = expk(smul_n(ssub_n(from, to), a.scale), a.ex, s_t64);
+            fx = expk(smul_n(ssub_n(from, to), a.scale), a.ex, s_t64);
 #pragma unroll
-            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+            for (uint32_t kq = 0; kq < kRedItems; ++kq) {        // CTREE, then AMERGE, in chunk order: l
                 if (k0 + kq >= ni) break;
-                const float * x = s_x + kq * 256u + lane;
-                const float ok = ctree4(x[0], x[64], x[128], x[192]);
                 const float * xl4 = s_x + 1024u + kq * 4u;
                 const float lk = ctree4(xl4[0], xl4[1], xl4[2], xl4[3]);
                 if (k0 + kq == 0u) {
-                    O = ok;
                     l = lk;
                 } else {
                     const float fa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq));
                     const float fbv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq + 1));
                     l = sadd_n(smul_n(l, fa), smul_n(lk, fbv));
-                    O = sadd_n(smul_n(O, fa), smul_n(ok, fbv));
                 }
                 mr = mrun[kq];
             }
         }
+        // ---- the segments' outputs: lane v's value of channel c in each segment ----
+        uint64_t po[kRedItems][8];
+        spins = 0;
+        for (;;) {
+            bool ok = true, near = true;                          // near: every writer shared this XCD
+            round_items(k0, ns, tl0);                             // (re-read: fewer registers held)
+#pragma unroll
+            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+#pragma unroll
+                for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
+                    const size_t row = ((size_t)(tl0[kq] + min(sgi, max(ns[kq], 1u) - 1u)) * 4u + c) * nh + hh;
+                    po[kq][sgi] = ld_tag(a.seg_o + row * D + v);
+                }
+            }
+#pragma unroll
+            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+#pragma unroll
+                for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
+                    ok &= sgi >= ns[kq] || tag_is((uint32_t)(po[kq][sgi] >> 32), tag);
+                    near &= sgi >= ns[kq] || (uint32_t)(po[kq][sgi] >> 60) == xcc;
+                }
+            }
+            if (__all(ok)) {
+                if (LOCAL && __any(!near) && lane == 0u && a.bad != nullptr)
+                    __hip_atomic_fetch_or(a.bad, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            if (++spins >= a.spin_max) {
+                if (lane == 0u && a.bad != nullptr)
+                    __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+#pragma unroll
+        for (uint32_t kq = 0; kq < kRedItems; ++kq) {             // channel c's segments in order
+            float Oc = 0.0f;
+#pragma unroll
+            for (uint32_t sgi = 0; sgi < 8u; ++sgi)
+                if (sgi < ns[kq]) Oc = sadd_n(Oc, bf((uint32_t)po[kq][sgi]));
+            s_x[(kq * 4u + c) * 64u + lane] = Oc;
+        }
         __syncthreads();
+        if (c == 0u) {                                            // CTREE, then AMERGE, in chunk order: O
+#pragma unroll
+            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+                if (k0 + kq >= ni) break;
+                const float * x = s_x + kq * 256u + lane;
+                const float ok = ctree4(x[0], x[64], x[128], x[192]);
+                if (k0 + kq == 0u) {
+                    O = ok;
+                } else {
+                    const float fa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq));
+                    const float fbv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq + 1));
+                    O = sadd_n(smul_n(O, fa), smul_n(ok, fbv));
+                }
+            }
+        }
+    } else {
+        // Several rounds: each round polls its items' outputs, row sums and maxima together
+        for (uint32_t k0 = 0; k0 < ni; k0 += kRedItems) {
+            // wave c polls its round's results until every one carries the launch's tag: lane v's value of
+            // channel c in each segment, lane s's row sum of segment s, lane kq's chunk maximum of item kq
+            uint64_t po[kRedItems][8], pl[kRedItems], pm;
+            uint32_t ns[kRedItems];
+            uint32_t spins = 0;
+            for (;;) {
+                bool ok = true;
+#pragma unroll
+                for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+                    const uint32_t k = min(k0 + kq, ni - 1u);
+                    FaItem ik{};
+                    ik.u0 = s_it[3u * k];
+                    ik.n = s_it[3u * k + 1u];
+                    const uint32_t tile0 = s_it[3u * k + 2u];
+                    const FaSeg sc(ik, c);
+                    ns[kq] = sc.nseg;
+#pragma unroll
+                    for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
+                        const size_t row = ((size_t)(tile0 + min(sgi, max(sc.nseg, 1u) - 1u)) * 4u + c) * nh + hh;
+                        po[kq][sgi] = ld_tag(a.seg_o + row * D + v);
+                    }
+                    const size_t lrow = ((size_t)(tile0 + min(lane, max(sc.nseg, 1u) - 1u)) * 4u + c) * nh + hh;
+                    pl[kq] = ld_tag(a.seg_l + lrow);
+                }
+                pm = ld_tag(a.m_item + (size_t)min(k0 + min(lane, kRedItems - 1u), ni - 1u) * nh + hh);
+                bool near = true;                                     // every writer shared this XCD
+#pragma unroll
+                for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+#pragma unroll
+                    for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
+                        ok &= sgi >= ns[kq] || tag_is((uint32_t)(po[kq][sgi] >> 32), tag);
+                        near &= sgi >= ns[kq] || (uint32_t)(po[kq][sgi] >> 60) == xcc;
+                    }
+                    ok &= lane >= ns[kq] || tag_is((uint32_t)(pl[kq] >> 32), tag);
+                }
+                ok &= tag_is((uint32_t)(pm >> 32), tag);
+                if (__all(ok)) {
+                    if (LOCAL && __any(!near) && lane == 0u && a.bad != nullptr)
+                        __hip_atomic_fetch_or(a.bad, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                if (++spins >= a.spin_max) {
+                    if (lane == 0u && a.bad != nullptr)
+                        __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            float xo[kRedItems][8], xl[kRedItems][8], mkr[kRedItems];
+#pragma unroll
+            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+#pragma unroll
+                for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
+                    xo[kq][sgi] = bf((uint32_t)po[kq][sgi]);
+                    xl[kq][sgi] = bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pl[kq], (int)sgi));
+                }
+                mkr[kq] = bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pm, (int)kq));
+            }
+#pragma unroll
+            for (uint32_t kq = 0; kq < kRedItems; ++kq) {             // channel c's segments in order
+                float Oc = 0.0f, Lc = 0.0f;
+#pragma unroll
+                for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
+                    if (sgi < ns[kq]) {
+                        Oc = sadd_n(Oc, xo[kq][sgi]);
+                        Lc = sadd_n(Lc, xl[kq][sgi]);
+                    }
+                }
+                s_x[(kq * 4u + c) * 64u + lane] = Oc;
+                if (lane == 0u) s_x[1024u + kq * 4u + c] = Lc;
+            }
+            __syncthreads();
+            if (c == 0u) {                                            // CTREE, then AMERGE, in chunk order
+                // the running maxima are a MAXT scan of the chunk maxima, so every merge factor of the round is
+                // known before the merge: lane 2 kq + b evaluates EXP((prev - mrun_kq) scale) for b = 0 (the
+                // running sums) or EXP((m_kq - mrun_kq) scale) for b = 1 (the chunk's), all at once
+                float mrun[kRedItems], prev[kRedItems];
+                float m = mr;
+#pragma unroll
+                for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+                    prev[kq] = m;
+                    mrun[kq] = k0 + kq == 0u ? mkr[kq] : maxt(m, mkr[kq]);
+                    m = mrun[kq];
+                }
+                const uint32_t jk = min(lane >> 1, kRedItems - 1u);  // lanes 2 kq, 2 kq + 1 hold item kq's factors
+                float from = 0.0f, to = 0.0f;
+#pragma unroll
+                for (uint32_t kq = 0; kq < kRedItems; ++kq)
+                    if (jk == kq) {
+                        from = (lane & 1u) ? mkr[kq] : prev[kq];
+                        to = mrun[kq];
+                    }
+                const float fx = expk(smul_n(ssub_n(from, to), a.scale), a.ex, s_t64);
+#pragma unroll
+                for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+                    if (k0 + kq >= ni) break;
+                    const float * x = s_x + kq * 256u + lane;
+                    const float ok = ctree4(x[0], x[64], x[128], x[192]);
+                    const float * xl4 = s_x + 1024u + kq * 4u;
+                    const float lk = ctree4(xl4[0], xl4[1], xl4[2], xl4[3]);
+                    if (k0 + kq == 0u) {
+                        O = ok;
+                        l = lk;
+                    } else {
+                        const float fa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq));
+                        const float fbv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq + 1));
+                        l = sadd_n(smul_n(l, fa), smul_n(lk, fbv));
+                        O = sadd_n(smul_n(O, fa), smul_n(ok, fbv));
+                    }
+                    mr = mrun[kq];
+                }
+            }
+            __syncthreads();
+        }
     }
     if (c == 0u) a.out[(size_t)hh * D + v] = smul_n(O, srcp(maxt(l, bf(kLFloor))));   // ANORM
     // every segment of the KV head has read the epochs (its flag is in): the next launch's tags

@@ -742,7 +742,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configs")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic passes")
-    ap.add_argument("--eager", action="store_true", help="time everything as direct launches: no HIP graph is built")
+    ap.add_argument("--eager", action="store_true",
+                    help="time everything as direct launches: no HIP graph is built (so the adapter leg, which "
+                         "replays a captured graph, is skipped too)")
     ap.add_argument("--no-adapter", action="store_true", help="skip the decode through the ggml-backend adapter")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--pmc-prefill-child", action="store_true", help=argparse.SUPPRESS)
@@ -794,7 +796,8 @@ def main() -> int:
     caches = [(L["kc"].get_bytes(0), L["vc"].get_bytes(1)) for L in m.layers]
     e2e["caches"] = None if args.no_cpu else caches
     m.free()
-    adapter = None if args.no_adapter else adapter_decode(ev, e2e, caches, args.steps)
+    # the adapter always replays a captured graph: --eager (the kernel-trace profile's form) skips it
+    adapter = None if (args.no_adapter or args.eager) else adapter_decode(ev, e2e, caches, args.steps)
     del caches
 
     also = {} if args.no_extra else extra_workloads(dev, ev, stream, 200, eager=args.eager)

@@ -212,14 +212,14 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     float4 r = qv0;
     if constexpr (ROPE) {
         float c_l, s_l;
-        if (a.rtab != nullptr) {
+        if (__builtin_expect(a.rtab != nullptr, 1)) {
             c_l = cs_tab.x;
             s_l = cs_tab.y;
         } else {
             rope_cs_lane(pos, half, a.ts, a.m, lane, &c_l, &s_l);
         }
         float4 rot;
-        if (!(tab_fast && rope4_tab_fast(rot, qv0, qpart, jh0, a.n_dims, a.neox != 0u, cs_a, cs_b)))
+        if (__builtin_expect(!(tab_fast && rope4_tab_fast(rot, qv0, qpart, jh0, a.n_dims, a.neox != 0u, cs_a, cs_b)), 0))
             rot = rope4(qv0, qpart, jh0, a.n_dims, a.neox != 0u, c_l, s_l);   // every lane (bpermute)
         r = is_v ? qv0 : rot;
     }
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     if (tid < 64u) s_t64[tid] = t64v;
     if constexpr (ROPE) {
         const bool cell_ok = cell_new >= 0 && cell_new < (int64_t)a.kc.kv_size && cell_new < (int64_t)a.vc.kv_size;
-        if (item == 0u && tt == 0u && c == (it.u0 & 3u)) {       // the caches' copy of the new rows
+        if (__builtin_expect(item == 0u && tt == 0u && c == (it.u0 & 3u), 0)) {       // the caches' copy of the new rows
             if (cell_ok && (is_k || is_v))
             {
                 KvArgs kv;                                        // per-lane choice of the plane, field by field
@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     const uint32_t u_j = ug[kkj];
     const int64_t cell_j = 16 * (int64_t)u_j + rrj;
     if (wave < NBD) {
-        if (ROPE && cell_j == cell_new) {                         // the new cell: the fresh k row
+        if (__builtin_expect(ROPE && cell_j == cell_new, 0)) {                         // the new cell: the fresh k row
             kr0 = *(const int4 *)(s_kq + 32u * wave);
             kr1 = *(const int4 *)(s_kq + 32u * wave + 16u);
             km = f2h_exact(s_kd[wave]);
@@ -379,7 +379,7 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
         for (;;) {
             if (want) v = ld_co16(rk, off);
             if (__all(tag_is(v.y, tag) && tag_is(v.w, tag))) break;
-            if (++spins >= a.spin_max) {
+            if (__builtin_expect(++spins >= a.spin_max, 0)) {
                 if (lane == 0u && a.bad != nullptr)
                     __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
@@ -545,7 +545,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
         }
     };
     float O = 0.0f, l = 0.0f, mr = 0.0f;
-    if (ni <= kRedItems) {
+    if (__builtin_expect(ni <= kRedItems, 1)) {
         // One round: the row-sum side first (its data are published at the segments' EXP step), the
         // merge factors and the l merge on wave 0 while the other waves already poll the outputs.
         const uint32_t k0 = 0;
@@ -565,7 +565,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
             pm = ld_tag(a.m_item + (size_t)min(k0 + min(lane, kRedItems - 1u), ni - 1u) * nh + hh);
             ok &= tag_is((uint32_t)(pm >> 32), tag);
             if (__all(ok)) break;
-            if (++spins >= a.spin_max) {
+            if (__builtin_expect(++spins >= a.spin_max, 0)) {
                 if (lane == 0u && a.bad != nullptr)
                     __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
@@ -642,11 +642,11 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
                 }
             }
             if (__all(ok)) {
-                if (LOCAL && __any(!near) && lane == 0u && a.bad != nullptr)
+                if (__builtin_expect(LOCAL && __any(!near) && lane == 0u && a.bad != nullptr, 0))
                     __hip_atomic_fetch_or(a.bad, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
-            if (++spins >= a.spin_max) {
+            if (__builtin_expect(++spins >= a.spin_max, 0)) {
                 if (lane == 0u && a.bad != nullptr)
                     __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
@@ -717,11 +717,11 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
                 }
                 ok &= tag_is((uint32_t)(pm >> 32), tag);
                 if (__all(ok)) {
-                    if (LOCAL && __any(!near) && lane == 0u && a.bad != nullptr)
+                    if (__builtin_expect(LOCAL && __any(!near) && lane == 0u && a.bad != nullptr, 0))
                         __hip_atomic_fetch_or(a.bad, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;
                 }
-                if (++spins >= a.spin_max) {
+                if (__builtin_expect(++spins >= a.spin_max, 0)) {
                     if (lane == 0u && a.bad != nullptr)
                         __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;

@@ -50,7 +50,7 @@ __device__ __forceinline__ void mv_wave_partials(const WGeom & g, const float * 
     for (uint32_t rl = __lane_id(); rl < nrow; rl += 64u) {
         const float * tr = s_t + (size_t)rl * g.nb + w;
         float p = 0.0f;
-        if (!slow) {
+        if (__builtin_expect(!slow, 1)) {
             for (uint32_t k = 0; k < cw; ++k) p = p + tr[16u * k];
         } else {
             for (uint32_t k = 0; k < cw; ++k) p = sadd(p, tr[16u * k]);
@@ -75,7 +75,7 @@ __device__ __forceinline__ void mv_tree_store(const MvArgs & a, const float * s_
     for (uint32_t base = 0; base < nrow * 16u; base += blockDim.x) {   // uniform trip count
         const uint32_t idx = base + threadIdx.x, rl = idx >> 4;
         float v = rl < nrow ? s_p[idx] : 0.0f;
-        if (!slow) {
+        if (__builtin_expect(!slow, 1)) {
             v = v + dpp_f<kDppXor1>(v);
             v = v + dpp_f<kDppXor2>(v);
             v = v + dpp_f<kDppRowHalfMirror>(v);
@@ -398,7 +398,7 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
             lds_flag_wait(s_ctl + 1, 2u);                         // both halves: every leader forms the scale
             const float sc = rms_scale(__uint_as_float(lds_ld(s_ctl + 3)), __uint_as_float(lds_ld(s_ctl + 4)),
                                        a.inv_n, a.eps);
-            if (!prep_norm_apply_fast(xv[0], sc, pv, a.pw != nullptr)) {
+            if (__builtin_expect(!prep_norm_apply_fast(xv[0], sc, pv, a.pw != nullptr), 0)) {
 #pragma unroll
                 for (uint32_t c = 0; c < 4u; ++c) xv[0][c] = prep_norm_apply(xv[0][c], sc, pv[c], a.pw != nullptr);
             }
@@ -471,7 +471,7 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
         const float dx = s_xd[xo];
         const float d = h2f_fast(mt.x & 0xFFFFu), dm = h2f_fast(mt.x >> 16);
         float tt;
-        if (!slow) tt = (d * dx) * (float)isum - (dm * dx) * (float)msum;
+        if (__builtin_expect(!slow, 1)) tt = (d * dx) * (float)isum - (dm * dx) * (float)msum;
         else tt = ssub(smul(smul(d, dx), i2f(isum)), smul(smul(dm, dx), i2f(msum)));
         const uint32_t s = w + 16u * m.k;
         if (m.valid && q == 0u) {

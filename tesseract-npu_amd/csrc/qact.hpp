@@ -53,7 +53,7 @@ __device__ __forceinline__ bool qact_a32_lane_fast(const float4 v, uint32_t * ou
 __device__ __forceinline__ uint32_t qact_a32_lane(const float4 v, float * D) {
     {
         uint32_t r;
-        if (qact_a32_lane_fast(v, &r, D)) return r;
+        if (__builtin_expect(qact_a32_lane_fast(v, &r, D), 1)) return r;
     }
     const float xs[4] = { v.x, v.y, v.z, v.w };
     uint32_t m = 0;
@@ -238,7 +238,7 @@ __device__ __forceinline__ bool qact_a256_row_fast(const float4 (&v)[4], uint4 *
 __device__ __forceinline__ uint4 qact_a256_row(const float4 (&v)[4], float * d, int * s16, bool * tiny) {
     {
         uint4 r;
-        if (qact_a256_row_fast(v, &r, d, s16, tiny)) return r;
+        if (__builtin_expect(qact_a256_row_fast(v, &r, d, s16, tiny), 1)) return r;
     }
     float xs[16];
 #pragma unroll

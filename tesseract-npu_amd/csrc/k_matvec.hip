@@ -690,10 +690,13 @@ int tsr_launch_mv_q4_k(const tsr::MvArgs & a, hipStream_t s) {
     const uint32_t nsb = a.K / 256u;
     const size_t lds = mv_lds_fixed(TSR_HIP_FMT_Q4_K, nsb) + mv_lds_rows(a.rb, nsb) + tsr_mv_prep_lds(a.prep, a.K);
     const dim3 grid((a.N + a.rb - 1u) / a.rb, a.T);
-    // lanes per unit: the units of the wave with the most (rb rows x ceil(nsb / 16) slots) in one pass
+    // lanes per unit from the units of the wave with the most (rb rows x ceil(nsb / 16) slots): two up
+    // to 64 units (two passes), one above. Four lanes would cut the o shape's instructions further
+    // (0.2 us alone), but a decode layer then runs four matvec kernels instead of three, and their
+    // code no longer fits the instruction cache together with the attention kernel's: the layer in
+    // sequence was 0.5 us slower.
     const uint32_t upw = a.rb * ((nsb + 15u) / 16u);
-    if (upw <= 16u) launch_q4k_v<4>(a, grid, lds, s);
-    else if (upw <= 32u) launch_q4k_v<2>(a, grid, lds, s);
+    if (upw <= 64u) launch_q4k_v<2>(a, grid, lds, s);
     else launch_q4k_v<1>(a, grid, lds, s);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }

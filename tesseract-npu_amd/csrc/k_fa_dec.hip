@@ -156,19 +156,9 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     // quantization is the first step) then arrive at the same time as the item.
     // (scalars in device memory are read with vector loads: a scalar load shares its counter with the
     // LDS operations, so every LDS wait of the quantization below would wait for it too)
-    int64_t cell_new = -1;
-    int32_t pos = 0;
-    if constexpr (ROPE) {
-        cell_new = (int64_t)__builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(fa_rsrc(a.cell, 8u), 0, 0, 0));
-        if (a.rtab == nullptr) pos = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(fa_rsrc(a.pos, 4u), 0, 0, 0);
-    }
-    const uint32_t t64v = a.ex.t64[lane];
-    // the launch's tag: reducer 0's epoch of the KV head + 1 (the epochs advance at the end of a launch);
-    // what this workgroup writes carries its XCD too
-    const uint32_t xcc = xcc_id();
-    const uint32_t epv = __builtin_amdgcn_raw_buffer_load_b32(fa_rsrc(a.ep + (size_t)g * G * (D / 64u), 4u), 0, 0, 0);
-    const uint32_t tag = (epv + 1u) & kTagMask, tagw = tag | (xcc << 28);
-    // the query values (ROPE: the token's Q|K|V row, the new k and v rows too)
+    // First every address, from the kernel arguments only and branch-free (a branch splits the code, and
+    // each argument was then read where first used: one dependent scalar round trip apiece, four to six
+    // in a row); then, after a scheduling barrier, every load at once.
     const uint32_t nslot = G * D / 4u;                            // 8 lanes per 32-value block
     const float * qrow = a.q + (size_t)g * G * D;
     const uint32_t kslot = tid - nslot, vslot = kslot - D / 4u;
@@ -179,34 +169,48 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     const float * qsrc = (ROPE && tid >= nslot) ? src : qrow + jq;
     const uint32_t half = a.n_dims / 2u;
     const uint32_t jh0 = tid < nslot ? jq % D : (is_k ? 4u * kslot : D);
-    // ROPE angles of the token (table): lane l's pair for the general form (read across lanes), and
-    // the pairs of the lane's own 4 values for the fast form (n_dims >= 8: NORM angles jh0 / 2 .. + 1,
-    // NEOX angles jh0 mod half .. + 3; clamped, even, so each float4 is aligned)
-    float2 cs_tab = make_float2(0.0f, 0.0f);
-    float4 cs_a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), cs_b = cs_a;
-    const bool tab_fast = ROPE && a.rtab != nullptr && a.n_dims >= 8u;
-    if constexpr (ROPE) {
-        if (a.rtab != nullptr) {
-            cs_tab = *(const float2 *)(a.rtab + 2u * min(lane, half - 1u));
-            if (tab_fast) {
-                const uint32_t ib = a.neox ? (jh0 < half ? jh0 : (jh0 < a.n_dims ? jh0 - half : 0u)) : min(jh0, a.n_dims) >> 1;
-                const uint32_t ia = min(ib, half - 2u) & ~1u, ic = min(ib + 2u, half - 2u) & ~1u;
-                cs_a = *(const float4 *)(a.rtab + 2u * ia);
-                cs_b = *(const float4 *)(a.rtab + 2u * ic);
-            }
-        }
-    }
-    const float4 qv0 = *(const float4 *)qsrc;
     // ROPE NEOX: the 4 values half a rotation away (their own address otherwise: no load waits on a branch)
     const int32_t dj = (ROPE && a.neox && jh0 < a.n_dims) ? (jh0 < half ? (int32_t)half : -(int32_t)half) : 0;
-    const float4 qpart = ROPE ? *(const float4 *)(qsrc + dj) : qv0;
+    // ROPE angles of the token (table): lane l's pair for the general form (read across lanes), and
+    // the pairs of the lane's own 4 values for the fast form (n_dims >= 8: NORM angles jh0 / 2 .. + 1,
+    // NEOX angles jh0 mod half .. + 3; clamped, even, so each float4 is aligned); buffer loads over the
+    // table, an empty range without one (such loads return 0 and touch nothing)
+    const bool tab_fast = ROPE && a.rtab != nullptr && a.n_dims >= 8u;
+    const uint32_t nx = 0u - (a.neox != 0u ? 1u : 0u);            // all ones for NEOX (a select, not a branch)
+    const uint32_t ib = (nx & (jh0 < half ? jh0 : (jh0 < a.n_dims ? jh0 - half : 0u))) | (~nx & (min(jh0, a.n_dims) >> 1));
+    const uint32_t ia = tab_fast ? min(ib, half - 2u) & ~1u : 0u, ic = tab_fast ? min(ib + 2u, half - 2u) & ~1u : 0u;
+    const __amdgpu_buffer_rsrc_t rt = fa_rsrc(a.rtab, ROPE && a.rtab != nullptr ? 4u * a.n_dims : 0u);
+    // without a table: the position; with one, an empty range
+    const __amdgpu_buffer_rsrc_t rpos = fa_rsrc(a.pos, ROPE && a.rtab == nullptr ? 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rcell = fa_rsrc(a.cell, ROPE ? 8u : 0u);
+    const __amdgpu_buffer_rsrc_t rep = fa_rsrc(a.ep + (size_t)g * G * (D / 64u), 4u);
+    const uint32_t * itp = (const uint32_t *)(a.items + item) + min(lane, 8u);
     __builtin_amdgcn_sched_barrier(0);
 
+    const int64_t cell_new = ROPE ? (int64_t)__builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rcell, 0, 0, 0))
+                                  : (int64_t)-1;
+    const int32_t pos = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rpos, 0, 0, 0);
+    const uint32_t t64v = a.ex.t64[lane];
+    // the launch's tag: reducer 0's epoch of the KV head + 1 (the epochs advance at the end of a launch)
+    const uint32_t epv = __builtin_amdgcn_raw_buffer_load_b32(rep, 0, 0, 0);
+    float2 cs_tab = make_float2(0.0f, 0.0f);
+    float4 cs_a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), cs_b = cs_a;
+    if constexpr (ROPE) {
+        cs_tab = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rt, 8u * min(lane, half - 1u), 0, 0));
+        cs_a = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rt, 8u * ia, 0, 0));
+        cs_b = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rt, 8u * ic, 0, 0));
+    }
+    const float4 qv0 = *(const float4 *)qsrc;
+    const float4 qpart = ROPE ? *(const float4 *)(qsrc + dj) : qv0;
     // the work item, one word per lane (a vector load: waiting for it does not wait for the LDS traffic
     // of the quantization, which runs while it is in flight)
     static_assert(sizeof(FaItem) == 36, "FaItem: 9 words");
-    const uint32_t itw = ((const uint32_t *)(a.items + item))[min(lane, 8u)];
+    const uint32_t itw = *itp;
     __builtin_amdgcn_sched_barrier(0);
+    // what this workgroup writes carries its XCD in the tag's high bits (read here, after the loads
+    // above: the register read is a volatile asm, which no load is scheduled across)
+    const uint32_t xcc = xcc_id();
+    const uint32_t tag = (epv + 1u) & kTagMask, tagw = tag | (xcc << 28);
 
     // ---- ROPE of the query heads and the new k row ----
     float4 r = qv0;

@@ -132,32 +132,33 @@ struct FaArgs {
 // The one-launch decode FLASH_ATTN_EXT (k_fa_dec.hip): one query row over a plan's device work list,
 // one workgroup per ATTPV segment (64 cells of one channel of one chunk, one KV head).
 struct FaDecArgs {
+    // The fields that the first loads of every workgroup need, contiguous at the start: they are
+    // fetched as one block of kernel arguments instead of one scalar round trip per scattered field.
     const float * q;         // the query row [n_head][D]; with ROPE the token's unrotated Q|K|V row
+    const FaItem * items;    // the plan's work list (n_items items, chunk order)
+    uint32_t * ep;           // [n_head_kv][reducer] epochs (zero at creation); a launch's tag is epoch + 1
+    // ROPE + SET_ROWS_KV folded in (cell != 0): position *pos or the angle table rtab, new cell *cell
+    const int32_t * pos;
+    const int64_t * cell;
+    const float * rtab;
+    uint32_t G, n_head, E, n_dims, neox, n_items, maxtiles, n_head_kv;
     KvArgs kc, vc;
-    uint32_t D, G, n_head, n_head_kv, E;
+    uint32_t D;
     float scale;
     const float * mask;      // GENERAL: the f32 mask row (mstride floats)
     uint32_t mstride;
-    const FaItem * items;    // the plan's work list (n_items items, chunk order)
-    uint32_t n_items, maxtiles;
     // results as (f32 bits | tag << 32): segment results [tile][4][n_head][D], segment row sums
     // [tile][4][n_head], chunk maxima [item][n_head]
     uint64_t * seg_o;
     uint64_t * seg_l;
     uint64_t * m_item;
     uint32_t * keys;         // [n_head_kv][n_items][maxtiles][4] 32-byte slots: (MAXT key, tag) of 4 heads
-    uint32_t * ep;           // [n_head_kv][reducer] epochs (zero at creation); a launch's tag is epoch + 1
     uint32_t spin_max;       // polls of a wait before it gives up (*bad |= 2)
     uint32_t n_xcd;          // XCDs of the device (workgroups go to them round-robin); 0: unknown
     float * out;             // [n_head][D]
-    ExpkTab ex;
-    // ROPE + SET_ROWS_KV folded in (cell != 0): position *pos or the angle table rtab, new cell *cell
-    const int32_t * pos;
-    const int64_t * cell;
     int32_t * bad;
-    uint32_t n_dims, neox;
     float ts, m;
-    const float * rtab;
+    ExpkTab ex;
 };
 
 // ROPE over T tokens of n_heads heads (head h of token t at x + t * x_stride + h * head_dim).

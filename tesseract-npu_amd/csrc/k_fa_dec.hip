@@ -187,6 +187,11 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     const uint32_t * itp = (const uint32_t *)(a.items + item) + min(lane, 8u);
     __builtin_amdgcn_sched_barrier(0);
 
+    // the work item first, one word per lane: the oldest load returns first (loads retire in order), so
+    // the K and V addresses, which depend on it, wait for it alone; the ROPE and quantization of the
+    // query then run while K and V fly (a vector load: waiting for it does not wait for LDS traffic)
+    static_assert(sizeof(FaItem) == 36, "FaItem: 9 words");
+    const uint32_t itw = *itp;
     const int64_t cell_new = ROPE ? (int64_t)__builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rcell, 0, 0, 0))
                                   : (int64_t)-1;
     const int32_t pos = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rpos, 0, 0, 0);
@@ -202,33 +207,13 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     }
     const float4 qv0 = *(const float4 *)qsrc;
     const float4 qpart = ROPE ? *(const float4 *)(qsrc + dj) : qv0;
-    // the work item, one word per lane (a vector load: waiting for it does not wait for the LDS traffic
-    // of the quantization, which runs while it is in flight)
-    static_assert(sizeof(FaItem) == 36, "FaItem: 9 words");
-    const uint32_t itw = *itp;
     __builtin_amdgcn_sched_barrier(0);
     // what this workgroup writes carries its XCD in the tag's high bits (read here, after the loads
     // above: the register read is a volatile asm, which no load is scheduled across)
     const uint32_t xcc = xcc_id();
     const uint32_t tag = (epv + 1u) & kTagMask, tagw = tag | (xcc << 28);
 
-    // ---- ROPE of the query heads and the new k row ----
-    float4 r = qv0;
-    if constexpr (ROPE) {
-        float c_l, s_l;
-        if (__builtin_expect(a.rtab != nullptr, 1)) {
-            c_l = cs_tab.x;
-            s_l = cs_tab.y;
-        } else {
-            rope_cs_lane(pos, half, a.ts, a.m, lane, &c_l, &s_l);
-        }
-        float4 rot;
-        if (__builtin_expect(!(tab_fast && rope4_tab_fast(rot, qv0, qpart, jh0, a.n_dims, a.neox != 0u, cs_a, cs_b)), 0))
-            rot = rope4(qv0, qpart, jh0, a.n_dims, a.neox != 0u, c_l, s_l);   // every lane (bpermute)
-        r = is_v ? qv0 : rot;
-    }
-
-    // ---- the work item; the segment's K and V requested (the quantization below runs while they fly) ----
+    // ---- the work item; the segment's K and V requested (ROPE and QACT below run while they fly) ----
     FaItem it;
     it.t = __builtin_amdgcn_readlane(itw, 0);
     it.u0 = __builtin_amdgcn_readlane(itw, 1);
@@ -272,6 +257,22 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     const uint8_t * vq = a.vc.base + a.vc.quant_off + ((size_t)ug[lane >> 4] * E + (size_t)g * D + 32u * bv + (lane & 15u)) * 16u;
     int4 bq0 = *(const int4 *)vq, bq1 = *(const int4 *)(vq + 256u);
     __builtin_amdgcn_sched_barrier(0);
+
+    // ---- ROPE of the query heads and the new k row ----
+    float4 r = qv0;
+    if constexpr (ROPE) {
+        float c_l, s_l;
+        if (__builtin_expect(a.rtab != nullptr, 1)) {
+            c_l = cs_tab.x;
+            s_l = cs_tab.y;
+        } else {
+            rope_cs_lane(pos, half, a.ts, a.m, lane, &c_l, &s_l);
+        }
+        float4 rot;
+        if (__builtin_expect(!(tab_fast && rope4_tab_fast(rot, qv0, qpart, jh0, a.n_dims, a.neox != 0u, cs_a, cs_b)), 0))
+            rot = rope4(qv0, qpart, jh0, a.n_dims, a.neox != 0u, c_l, s_l);   // every lane (bpermute)
+        r = is_v ? qv0 : rot;
+    }
 
     // ---- QACT of the query heads, the new k and v rows ----
     float Dq;

@@ -195,7 +195,6 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     const int64_t cell_new = ROPE ? (int64_t)__builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rcell, 0, 0, 0))
                                   : (int64_t)-1;
     const int32_t pos = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rpos, 0, 0, 0);
-    const uint32_t t64v = a.ex.t64[lane];
     // the launch's tag: reducer 0's epoch of the KV head + 1 (the epochs advance at the end of a launch)
     const uint32_t epv = __builtin_amdgcn_raw_buffer_load_b32(rep, 0, 0, 0);
     float2 cs_tab = make_float2(0.0f, 0.0f);
@@ -207,13 +206,16 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     }
     const float4 qv0 = *(const float4 *)qsrc;
     const float4 qpart = ROPE ? *(const float4 *)(qsrc + dj) : qv0;
+    // the EXPK table (kernel-argument memory) last: nothing before the quantization's LDS stores waits
+    // for it
+    const uint32_t t64v = a.ex.t64[lane];
     __builtin_amdgcn_sched_barrier(0);
     // what this workgroup writes carries its XCD in the tag's high bits (read here, after the loads
     // above: the register read is a volatile asm, which no load is scheduled across)
     const uint32_t xcc = xcc_id();
     const uint32_t tag = (epv + 1u) & kTagMask, tagw = tag | (xcc << 28);
 
-    // ---- the work item; the segment's K and V requested (ROPE and QACT below run while they fly) ----
+    // ---- the work item; the segment's K requested (ROPE and QACT below run while it flies) ----
     FaItem it;
     it.t = __builtin_amdgcn_readlane(itw, 0);
     it.u0 = __builtin_amdgcn_readlane(itw, 1);
@@ -243,19 +245,6 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
                             (size_t)rrj * 16u;
     int4 kr0 = *(const int4 *)kbase, kr1 = *(const int4 *)(kbase + 256u);
     uint32_t km = ((const uint16_t *)a.kc.base)[((size_t)ug[kkj] * nbk + (size_t)g * NBD + bk) * 16u + rrj];
-    // V: wave b = value block b; lane (head row hr, group kk, cell quad) for the weights, lane
-    // (value l % 16, group l / 16) for the matrix-core operand
-    const uint32_t hr = lane >> 4, kk = (lane >> 2) & 3u, quad = lane & 3u;
-    const uint32_t bv = wave < NBD ? wave : 0u, b0 = bv & ~1u;    // the 64-value slice: blocks b0, b0 + 1
-    // V: the scales of the lane's 4 cells in the slice's two blocks (8 contiguous bytes each), and the
-    // matrix-core operand
-    uint2 mvb[2];
-#pragma unroll
-    for (uint32_t e = 0; e < 2u; ++e)
-        mvb[e] = *(const uint2 *)((const uint16_t *)a.vc.base + ((size_t)ug[kk] * nbk + (size_t)g * NBD + b0 + e) * 16u +
-                                  4u * quad);
-    const uint8_t * vq = a.vc.base + a.vc.quant_off + ((size_t)ug[lane >> 4] * E + (size_t)g * D + 32u * bv + (lane & 15u)) * 16u;
-    int4 bq0 = *(const int4 *)vq, bq1 = *(const int4 *)(vq + 256u);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- ROPE of the query heads and the new k row ----
@@ -304,7 +293,22 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
             if (!cell_ok && tid == 0u && g == 0u && a.bad != nullptr) *a.bad = 1;
         }
     }
-    lds_barrier();                                                // K and V stay in flight
+    lds_barrier();                                                // K stays in flight
+    // V is requested only now: K streams alone first (the scores wait for it; V is needed at P.V)
+    // V: wave b = value block b; lane (head row hr, group kk, cell quad) for the weights, lane
+    // (value l % 16, group l / 16) for the matrix-core operand
+    const uint32_t hr = lane >> 4, kk = (lane >> 2) & 3u, quad = lane & 3u;
+    const uint32_t bv = wave < NBD ? wave : 0u, b0 = bv & ~1u;    // the 64-value slice: blocks b0, b0 + 1
+    // V: the scales of the lane's 4 cells in the slice's two blocks (8 contiguous bytes each), and the
+    // matrix-core operand
+    uint2 mvb[2];
+#pragma unroll
+    for (uint32_t e = 0; e < 2u; ++e)
+        mvb[e] = *(const uint2 *)((const uint16_t *)a.vc.base + ((size_t)ug[kk] * nbk + (size_t)g * NBD + b0 + e) * 16u +
+                                  4u * quad);
+    const uint8_t * vq = a.vc.base + a.vc.quant_off + ((size_t)ug[lane >> 4] * E + (size_t)g * D + 32u * bv + (lane & 15u)) * 16u;
+    int4 bq0 = *(const int4 *)vq, bq1 = *(const int4 *)(vq + 256u);
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- scores: the block terms of (cell j, block b) for every head ----
     const uint32_t u_j = ug[kkj];

@@ -16,7 +16,8 @@
 //              products for the 4 heads (16 values each)
 //   results    the segment's O (G x D) and l (G) to the plan, each value with the launch's tag in one
 //              8-byte agent-coherent store
-//   reduce     G x D/64 reducer workgroups per KV head, after every segment in dispatch order: each
+//   reduce     G x D/64 reducer workgroups per KV head (ahead of the segments in dispatch order when
+//              the grid is resident at once, after them otherwise): each
 //              polls the results until all carry the tag, then chains, in order, the segments of every
 //              channel of every item
 //              for its 64 values of one head, CTREE over the channels, merges the items in chunk order
@@ -24,7 +25,8 @@
 // The chunk maximum needs every score of the chunk before any P.V of it (p depends on it bit for bit),
 // and the segment chains need every segment: two exchanges between workgroups, the least the reference's
 // order allows. Segments of one item are consecutive in dispatch order, so every segment an item's
-// wait needs has been dispatched before or is dispatched next (no wait can starve).
+// wait needs has been dispatched before or is dispatched next (no wait can starve); reducers wait on
+// segments only, and no segment waits on a reducer.
 //
 // ROPE (the layer's ROPE + SET_ROWS_KV folded in): q is then the token's unrotated Q|K|V row. Every
 // workgroup rotates and quantizes its KV head's query heads, the new k row (and quantizes the new v
@@ -142,13 +144,18 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     uint32_t * s_key = (uint32_t *)(lds + 11360);                 // [4] segment maxima (keys)
     float * s_m = (float *)(lds + 11376);                         // [4] chunk maxima
 
-    const uint32_t per_item = 4u * a.maxtiles;
+    const uint32_t per_item = 4u * a.maxtiles, nred = a.G * (D / 64u), nseg_slots = a.n_items * per_item;
     const FaDecBlock blk = fa_dec_block<LOCAL>(a);
-    if (blk.x >= a.n_items * per_item) {                          // the KV head's reducers
-        fa_dec_reduce<D, LOCAL>(a, lds, blk.x - a.n_items * per_item, blk.g);
+    // The KV head's reducers: first in dispatch order when the whole grid is resident at once (they
+    // then poll from the start, and finish sooner), after the segments otherwise (then the reducers
+    // would hold slots that segments need; segments never wait on reducers)
+    const uint32_t xr = a.red_first ? blk.x : blk.x - nseg_slots;
+    if (a.red_first ? blk.x < nred : blk.x >= nseg_slots) {
+        fa_dec_reduce<D, LOCAL>(a, lds, xr, blk.g);
         return;
     }
-    const uint32_t item = blk.x / per_item, tt = (blk.x / 4u) % a.maxtiles, c = blk.x & 3u;
+    const uint32_t xs = a.red_first ? blk.x - nred : blk.x;       // the segment slot
+    const uint32_t item = xs / per_item, tt = (xs / 4u) % a.maxtiles, c = xs & 3u;
     const uint32_t g = blk.g, G = a.G, nh = a.n_head, E = a.E, nbk = E / 32u;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     // Everything that does not depend on the work item is requested before the item itself: the item

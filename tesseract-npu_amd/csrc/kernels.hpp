@@ -155,6 +155,7 @@ struct FaDecArgs {
     uint32_t * keys;         // [n_head_kv][n_items][maxtiles][4] 32-byte slots: (MAXT key, tag) of 4 heads
     uint32_t spin_max;       // polls of a wait before it gives up (*bad |= 2)
     uint32_t n_xcd;          // XCDs of the device (workgroups go to them round-robin); 0: unknown
+    uint32_t red_first;      // reducers dispatched ahead of the segments (the grid is resident at once)
     float * out;             // [n_head][D]
     int32_t * bad;
     float ts, m;

@@ -715,6 +715,10 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
         d.ep = (uint32_t *)(plan->dev + plan->o_EP);
         d.spin_max = ctx->fa_spin_max;
         d.n_xcd = ctx->n_xcd;
+        {   // reducers first when the grid is resident at once (4 of the kernel's 5 workgroups per CU)
+            const uint64_t wgs = ((uint64_t)plan->n_items * plan->maxtiles * 4u + G * (plan->D / 64u)) * plan->n_head_kv;
+            d.red_first = ctx->n_cu > 0 && wgs <= 4u * (uint64_t)ctx->n_cu ? 1u : 0u;
+        }
         d.out = out_dev;
         d.ex = ctx->expk;
         d.bad = ctx->flags_dev;                              // the rope form below names its own

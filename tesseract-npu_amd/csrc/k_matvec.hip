@@ -312,13 +312,15 @@ __global__ __launch_bounds__(1024) void k_mv_q4k(MvArgs a) {
     float4 xv[RPL][4], pv[4];                                     // pv: the norm weights of the leader's round
     if (threadIdx.x < 8u) lds_st(s_ctl + threadIdx.x, 0u);
     if (leader) {
-#pragma unroll
-        for (uint32_t i = 0; i < RPL; ++i) load_xr(rg + nlg * i, xv[i]);
+        // the norm weights first: in a decode layer they were last read a token ago and come from HBM,
+        // while x was written by the launch before (layer in sequence 49.7 -> 49.0 us)
         if constexpr (PREP == kPrepNorm) {
             const float * pl = a.pw ? a.pw : x;                   // without MUL: a valid address, unused
 #pragma unroll
             for (uint32_t c = 0; c < 4u; ++c) pv[c] = *(const float4 *)(pl + xidx(rg, c));
         }
+#pragma unroll
+        for (uint32_t i = 0; i < RPL; ++i) load_xr(rg + nlg * i, xv[i]);
     }
     uint32_t t64 = 0;
     if constexpr (GLU) t64 = a.ex.t64[lane];

@@ -202,8 +202,6 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     const int64_t cell_new = ROPE ? (int64_t)__builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rcell, 0, 0, 0))
                                   : (int64_t)-1;
     const int32_t pos = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rpos, 0, 0, 0);
-    // the launch's tag: reducer 0's epoch of the KV head + 1 (the epochs advance at the end of a launch)
-    const uint32_t epv = __builtin_amdgcn_raw_buffer_load_b32(rep, 0, 0, 0);
     float2 cs_tab = make_float2(0.0f, 0.0f);
     float4 cs_a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), cs_b = cs_a;
     if constexpr (ROPE) {
@@ -213,9 +211,12 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     }
     const float4 qv0 = *(const float4 *)qsrc;
     const float4 qpart = ROPE ? *(const float4 *)(qsrc + dj) : qv0;
-    // the EXPK table (kernel-argument memory) last: nothing before the quantization's LDS stores waits
-    // for it
+    // the EXPK table (kernel-argument memory) and the epochs last: nothing before the quantization's LDS
+    // stores waits for them (loads retire in order; the epochs were written by the previous launch, in
+    // a decode layer's sequence too long ago to be in a cache)
     const uint32_t t64v = a.ex.t64[lane];
+    // the launch's tag: reducer 0's epoch of the KV head + 1 (the epochs advance at the end of a launch)
+    const uint32_t epv = __builtin_amdgcn_raw_buffer_load_b32(rep, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     // what this workgroup writes carries its XCD in the tag's high bits (read here, after the loads
     // above: the register read is a volatile asm, which no load is scheduled across)

@@ -641,8 +641,8 @@ int weight_of(tsr_gg_dev * d, const tsr_gg_tensor * t, bool build, Weight ** out
     w.nbytes = nb;
     w.N = (uint32_t)t->ne[1];
     w.K = (uint32_t)t->ne[0];
-    if (!build || d->ctx == nullptr) {
-        static Weight probe;
+    if (!build || d->ctx == nullptr) {                        // a question only: the shape, per thread
+        thread_local Weight probe;
         probe = w;
         *out = &probe;
         return TSR_GG_OK;
@@ -686,8 +686,8 @@ int fused_weight_of(tsr_gg_dev * d, const std::vector<const tsr_gg_tensor *> & t
         w.N += (uint32_t)t->ne[1];
         w.parts.emplace_back(t->data, nb);
     }
-    if (!build || d->ctx == nullptr) {
-        static Weight probe;
+    if (!build || d->ctx == nullptr) {                        // a question only: the shape, per thread
+        thread_local Weight probe;
         probe = w;
         *out = &probe;
         return TSR_GG_OK;

@@ -351,7 +351,9 @@ int tsr_hip_get_rows(tsr_hip_ctx * ctx, const float * src_dev, uint64_t src_stri
 
 /* The greedy token pick over logits rows (argmax_row, sw/tools/klcheck.cpp:777-785; std::max_element,
  * sw/ggml-tesseract/tests/test-tsr-mtp.cpp:77-79): out_dev[r] = the first index of the largest value
- * of row r; NaN is never the largest; a row with no value above -inf gives 0. */
+ * of row r; NaN is never the largest; a row with no value above -inf gives 0. Up to 8 rows of at
+ * least 32768 values are picked in two passes whose slice results live in a small per-context array:
+ * such calls on different streams of one context must not overlap in time. */
 int tsr_hip_argmax(tsr_hip_ctx * ctx, const float * x_dev, uint32_t n, uint32_t rows, uint64_t x_stride,
                    int32_t * out_dev, void * stream);
 

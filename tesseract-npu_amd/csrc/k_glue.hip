@@ -304,6 +304,72 @@ __global__ __launch_bounds__(1024) void k_argmax(const float * x, uint64_t x_str
     }
 }
 
+// ARGMAX of long rows (the vocabulary) in two passes: workgroup (b, row) scans the slice
+// [b span, min((b + 1) span, n)) as k_argmax scans a row and stores its (value, index) as one 8-byte
+// word; then one wave per row picks among the slices. The pick -- the largest value, then the lowest
+// index, only values above -inf -- does not depend on the order of the picks, so the result is
+// k_argmax's. span is a multiple of 4.
+__global__ __launch_bounds__(1024) void k_argmax_part(const float * x, uint64_t x_stride, uint32_t n, uint32_t span,
+                                                      uint64_t * part) {
+    __shared__ float s_v[16];
+    __shared__ uint32_t s_i[16];
+    const float * xr = x + (size_t)blockIdx.y * x_stride;
+    const uint32_t lo = blockIdx.x * span, hi = min(n, lo + span);
+    float v = -__builtin_inff();
+    uint32_t i = 0xFFFFFFFFu;
+    if ((((uintptr_t)xr) & 15u) == 0u && (n & 3u) == 0u) {
+        const uint32_t q_hi = hi / 4u;
+        for (uint32_t q0 = lo / 4u; q0 < q_hi; q0 += 1024u * kAmBatch) {
+            float4 e[kAmBatch];
+#pragma unroll
+            for (uint32_t k = 0; k < kAmBatch; ++k) {
+                const uint32_t q = q0 + threadIdx.x + 1024u * k;
+                e[k] = q < q_hi ? *(const float4 *)(xr + 4u * q) : make_float4(-__builtin_inff(), -__builtin_inff(),
+                                                                                 -__builtin_inff(), -__builtin_inff());
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < kAmBatch; ++k) {
+                const uint32_t j = 4u * (q0 + threadIdx.x + 1024u * k);
+                if (e[k].x > v) { v = e[k].x; i = j; }
+                if (e[k].y > v) { v = e[k].y; i = j + 1u; }
+                if (e[k].z > v) { v = e[k].z; i = j + 2u; }
+                if (e[k].w > v) { v = e[k].w; i = j + 3u; }
+            }
+        }
+    } else {
+        for (uint32_t j = lo + threadIdx.x; j < hi; j += blockDim.x) {
+            const float e = xr[j];
+            if (e > v) { v = e; i = j; }
+        }
+    }
+    for (int d = 32; d >= 1; d >>= 1) {
+        const int src = (int)(__lane_id() ^ (uint32_t)d);
+        am_pick(v, i, shfl_f(v, src), (uint32_t)shfl_i((int)i, src));
+    }
+    const uint32_t wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if (__lane_id() == 0u) { s_v[wave] = v; s_i[wave] = i; }
+    __syncthreads();
+    if (threadIdx.x == 0u) {
+        for (uint32_t w = 1; w < nw; ++w) am_pick(v, i, s_v[w], s_i[w]);
+        part[(size_t)blockIdx.y * gridDim.x + blockIdx.x] = ((uint64_t)i << 32) | __float_as_uint(v);
+    }
+}
+__global__ __launch_bounds__(64) void k_argmax_pick(const uint64_t * part, uint32_t nb, int32_t * out) {
+    const uint32_t lane = threadIdx.x;
+    float v = -__builtin_inff();
+    uint32_t i = 0xFFFFFFFFu;
+    if (lane < nb) {
+        const uint64_t w = part[(size_t)blockIdx.x * nb + lane];
+        v = __uint_as_float((uint32_t)w);
+        i = (uint32_t)(w >> 32);
+    }
+    for (int d = 32; d >= 1; d >>= 1) {
+        const int src = (int)(lane ^ (uint32_t)d);
+        am_pick(v, i, shfl_f(v, src), (uint32_t)shfl_i((int)i, src));
+    }
+    if (lane == 0u) out[blockIdx.x] = i == 0xFFFFFFFFu ? 0 : (int32_t)i;
+}
+
 }  // namespace tsr
 
 // ---- launchers ------------------------------------------------------------------------------------
@@ -361,7 +427,17 @@ int tsr_launch_get_rows(const float * src, uint64_t src_stride, uint32_t n, uint
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-int tsr_launch_argmax(const float * x, uint64_t x_stride, uint32_t n, uint32_t rows, int32_t * out, hipStream_t s) {
-    hipLaunchKernelGGL(tsr::k_argmax, dim3(rows), dim3(1024), 0, s, x, x_stride, n, out);
+int tsr_launch_argmax(const float * x, uint64_t x_stride, uint32_t n, uint32_t rows, int32_t * out, uint64_t * part,
+                      hipStream_t s) {
+    // long rows, few of them: slices of ~4096 values over up to kAmParts workgroups a row (one
+    // workgroup reading the 128256-value vocabulary alone spent ~8 us on its compute unit's loads)
+    if (part != nullptr && rows <= tsr::kAmRows && n >= 32768u) {
+        const uint32_t nb = min(tsr::kAmParts, (n + 4095u) / 4096u);
+        const uint32_t span = ((n + nb - 1u) / nb + 3u) & ~3u;
+        hipLaunchKernelGGL(tsr::k_argmax_part, dim3(nb, rows), dim3(1024), 0, s, x, x_stride, n, span, part);
+        hipLaunchKernelGGL(tsr::k_argmax_pick, dim3(rows), dim3(64), 0, s, part, nb, out);
+    } else {
+        hipLaunchKernelGGL(tsr::k_argmax, dim3(rows), dim3(1024), 0, s, x, x_stride, n, out);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }

@@ -17,6 +17,7 @@ struct QactArgs {
 
 // EXPK constants (VU 6.3): LK = round(log2(e) 2^38), c_k = round(ln(2)^k / k! 2^32),
 // t64[j] = round(2^(j/64) 2^30); computed on the host from their definitions.
+constexpr uint32_t kAmRows = 8, kAmParts = 32;   // ARGMAX two-pass form: rows, slices per row
 struct ExpkTab {
     uint32_t t64[64];
     uint64_t lk, c1, c2, c3;
@@ -221,7 +222,9 @@ int tsr_launch_add(const float * a, uint64_t a_stride, const float * b, uint64_t
                    uint64_t y_stride, uint32_t n, uint32_t rows, hipStream_t s);
 int tsr_launch_get_rows(const float * src, uint64_t src_stride, uint32_t n, uint32_t n_src, const int32_t * ids,
                         uint32_t count, float * dst, uint64_t dst_stride, int32_t * bad, hipStream_t s);
-int tsr_launch_argmax(const float * x, uint64_t x_stride, uint32_t n, uint32_t rows, int32_t * out, hipStream_t s);
+// part: the two-pass form's slice results (kAmRows x kAmParts words; null: one pass)
+int tsr_launch_argmax(const float * x, uint64_t x_stride, uint32_t n, uint32_t rows, int32_t * out, uint64_t * part,
+                      hipStream_t s);
 int tsr_launch_rope_kv(const tsr::RopeKvArgs & a, uint32_t T, hipStream_t s);
 // LDS bytes the fused x preparation adds to a matvec launch (0 when none)
 size_t tsr_mv_prep_lds(uint32_t prep, uint32_t K);

@@ -135,9 +135,14 @@ struct tsr_hip_ctx {
     uint32_t fa_spin_max = 1u << 20;    // polls of the fused decode FA's tile-key wait (s_sleep 1 each)
     uint8_t * fa_fixed = nullptr;       // device address of this device's fixed FA array (tsr_fa_fixed_init)
     hipStream_t pick(void * s) const { return s ? (hipStream_t)s : stream; }
-    // The device flag word raised by a kernel given no flag word of its own (tsr_hip_get_flags).
+    // The device flag word raised by a kernel given no flag word of its own (tsr_hip_get_flags), in a
+    // small allocation that also holds the two-pass ARGMAX's slice results after its first 256 bytes
+    // (written before they are read in every call; calls on different streams of one context that
+    // overlap share them).
+    static constexpr size_t kFlagsBytes = 256 + (size_t)tsr::kAmRows * tsr::kAmParts * 8u;
     int32_t * flags_dev = nullptr;
     int32_t * flag(int32_t * p) const { return p ? p : flags_dev; }
+    uint64_t * am_part() const { return (uint64_t *)((uint8_t *)flags_dev + 256); }
 };
 
 struct tsr_hip_weight {

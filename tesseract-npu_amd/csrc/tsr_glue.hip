@@ -119,5 +119,5 @@ int tsr_hip_argmax(tsr_hip_ctx * ctx, const float * x_dev, uint32_t n, uint32_t 
     if (!rows_ok(n, rows, x_stride) || n > 0x7FFFFFFFu || rows > 0x7FFFFFFFu) return TSR_HIP_E_ARG;
     std::lock_guard<std::mutex> lk(ctx->mtx);
     const hipStream_t s = enter(ctx, stream);
-    return tsr_launch_argmax(x_dev, x_stride, n, rows, out_dev, s);
+    return tsr_launch_argmax(x_dev, x_stride, n, rows, out_dev, ctx->am_part(), s);
 }

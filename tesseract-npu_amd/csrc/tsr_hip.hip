@@ -111,7 +111,7 @@ int tsr_hip_open(int device, tsr_hip_ctx ** out) {
         return rc;
     }
     if ((rc = tsr_fa_fixed_init(c)) != 0 ||                       // the device address of the fixed FA array
-        (rc = hip_err(hipMalloc((void **)&c->flags_dev, 256), "hipMalloc flags")) != 0 ||
+        (rc = hip_err(hipMalloc((void **)&c->flags_dev, tsr_hip_ctx::kFlagsBytes), "hipMalloc flags")) != 0 ||
         (rc = hip_err(hipMemsetAsync(c->flags_dev, 0, 256, c->stream), "hipMemset flags")) != 0 ||
         (rc = hip_err(hipStreamSynchronize(c->stream), "hipStreamSynchronize")) != 0 ||
         (rc = xcd_calibrate(c)) != 0) {

@@ -218,14 +218,24 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
     nl = cfg.n_layer
     f4 = 4
     w3 = nq + 2 * E
-    ops = {
-        "mul_mat_norm qkv Q4_K 6144x4096": (
-            lambda i: d.mul_mat_norm(L[i % nl]["wqkv"], m.x, 1, n, cfg.eps, L[i % nl]["attn_norm"], m.qkv, w3,
-                                     stream=stream), nl, mv_bytes(w3, n) + 4 * n, "k_mv_q4k<norm>"),
-        "rope+set_rows_kv+flash_attn": (
-            lambda i: d.flash_attn_plan_rope_tab(m.plan, m.qkv, L[i % nl]["kc"], L[i % nl]["vc"], m.scale, cfg.head_dim,
-                                                 cfg.rope_mode, m.rtab, m.cell_ptr, m.att, nq, bad=m.bad, stream=stream),
-            nl, 2 * kv_size * (E // 32) * 34 + 4 * w3 + 4 * nq, "k_fa_dec"),
+    kv_b = 2 * kv_size * (E // 32) * 34 + 4 * w3 + 4 * nq
+    if m.qkv_in_attn:           # the decoder's attention half: one launch with the Q|K|V rows
+        ops = {"mul_mat_norm qkv+rope+set_rows_kv+flash_attn (one launch)": (
+            lambda i: d.attn_qkv_plan_rope_tab(m.plan, L[i % nl]["wqkv"], m.x, cfg.eps, L[i % nl]["attn_norm"], m.qkv,
+                                               L[i % nl]["kc"], L[i % nl]["vc"], m.scale, cfg.head_dim, cfg.rope_mode,
+                                               m.rtab, m.cell_ptr, m.att, nq, bad=m.bad, stream=stream),
+            nl, mv_bytes(w3, n) + 4 * n + kv_b, "k_fa_dec<qkv>")}
+    else:
+        ops = {
+            "mul_mat_norm qkv Q4_K 6144x4096": (
+                lambda i: d.mul_mat_norm(L[i % nl]["wqkv"], m.x, 1, n, cfg.eps, L[i % nl]["attn_norm"], m.qkv, w3,
+                                         stream=stream), nl, mv_bytes(w3, n) + 4 * n, "k_mv_q4k<norm>"),
+            "rope+set_rows_kv+flash_attn": (
+                lambda i: d.flash_attn_plan_rope_tab(m.plan, m.qkv, L[i % nl]["kc"], L[i % nl]["vc"], m.scale,
+                                                     cfg.head_dim, cfg.rope_mode, m.rtab, m.cell_ptr, m.att, nq,
+                                                     bad=m.bad, stream=stream),
+                nl, kv_b, "k_fa_dec")}
+    ops.update({
         "mul_mat o Q4_K 4096x4096 +res": (lambda i: d.mul_mat(L[i % nl]["wo"], m.att, 1, nq, m.h, n, add=m.x, add_stride=n,
                                                               stream=stream), nl, mv_bytes(n, nq) + 4 * n, "k_mv_q4k"),
         "mul_mat_norm+glu gate|up Q4_K 28672x4096": (
@@ -244,7 +254,7 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
                    4 * cfg.n_vocab, "k_argmax"),
         "get_rows": (lambda i: d.get_rows(m.tok_embd, n, n, cfg.n_vocab, m.tok, 1, m.h, n, bad=m.bad, stream=stream), 1,
                      8 * n, "k_get_rows"),
-    }
+    })
     per_op = {}
     for name, (fn, count, nbytes, kname) in ops.items():
         for i in range(3):
@@ -608,7 +618,10 @@ def pmc_child(reps: int = 3) -> int:
         rows = dev.upload(S.normal(S.seed_of("pmc", f"kv{which}"), pos * E))
         dev.kv_set_rows(kv, which, rows, pos, E, idx)
         rows.free()
-    qkv = dev.upload(S.normal(S.seed_of("pmc", "qkv"), w3))
+    qkv = dev.alloc(4 * w3)
+    w_qkv = dev.weight(cfg.wfmt, np.concatenate([wts.quant(f"blk.0.attn_{t}.weight", N, cfg.n_embd, cfg.wfmt)
+                                                 for t, N in (("q", nq), ("k", E), ("v", E))]), w3, cfg.n_embd)
+    an = dev.upload(wts.norm("blk.0.attn_norm.weight"))
     params = dev.upload(LL.LlamaDecoder._params(pos))
     rtab, att, bad = dev.alloc(4 * cfg.head_dim), dev.alloc(4 * nq), dev.alloc(4).fill(0)
     plan = dev.fa_plan(cfg.head_dim, cfg.n_head, cfg.n_head_kv, 1, kv_size)
@@ -622,9 +635,10 @@ def pmc_child(reps: int = 3) -> int:
         dev.mul_mat_norm(w_gu, xb, 1, cfg.n_embd, cfg.eps, nw, gb, cfg.n_ff, flags=tsr_hip.MM_GLU, stream=dev.stream)
     for _ in range(reps):      # the decoder's down, residual addend
         dev.mul_mat(w_dn, gb, 1, cfg.n_ff, yb, cfg.n_embd, add=xb, add_stride=cfg.n_embd, stream=dev.stream)
-    for _ in range(reps):      # the decoder's attention launch
-        dev.flash_attn_plan_rope_tab(plan, qkv, kc, vc, np.float32(1.0 / np.sqrt(cfg.head_dim)), cfg.head_dim,
-                                     cfg.rope_mode, rtab, params.ptr + 8, att, nq, bad=bad, stream=dev.stream)
+    for _ in range(reps):      # the decoder's attention launch (with its Q|K|V rows)
+        dev.attn_qkv_plan_rope_tab(plan, w_qkv, xb, cfg.eps, an, qkv, kc, vc, np.float32(1.0 / np.sqrt(cfg.head_dim)),
+                                   cfg.head_dim, cfg.rope_mode, rtab, params.ptr + 8, att, nq, bad=bad,
+                                   stream=dev.stream)
     ev.device_sync()
     assert int(bad.read(np.int32, (1,))[0]) == 0
     plan.free()
@@ -707,7 +721,8 @@ def measure_prefill_counters(reps: int = 2) -> dict:
 
 
 def measure_traffic(reps: int = 3) -> dict:
-    """HBM bytes per launch of the gate|up and down matvecs and of the decode attention launch:
+    """HBM bytes per launch of the gate|up and down matvecs and of the decode attention launch (with the
+    layer's Q|K|V rows):
     FETCH_SIZE and WRITE_SIZE (KiB per dispatch, two separate rocprofv3 passes), each scaled by the
     same counter's reading for the calibration copy (COPY_BYTES read and COPY_BYTES written)."""
     if shutil.which("rocprofv3") is None:

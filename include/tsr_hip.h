@@ -230,6 +230,23 @@ int tsr_hip_flash_attn_plan_rope_tab(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * 
                                      tsr_hip_kv * kc, tsr_hip_kv * vc, float scale, uint32_t n_dims, int mode,
                                      const float * tab_dev, const int64_t * cell_dev, int32_t * bad_dev,
                                      const float * mask_f32_dev, float * out_dev, uint64_t out_stride, void * stream);
+/* The attention half of a decode layer in one call: bit-identical to
+ *   tsr_hip_mul_mat_norm(w_qkv, x_dev, T = 1, eps, norm_w_dev -> qkv_dev)
+ * followed by tsr_hip_flash_attn_plan_rope_tab(plan, qkv_dev, ...) -- the RMS_NORM + MUL, Q|K|V
+ * MUL_MAT, ROPE, SET_ROWS_KV and FLASH_ATTN_EXT records of sw/ctrl/tests/test_fw_m7_layer.cpp:646-686.
+ * qkv_dev receives the unrotated Q|K|V row as the MUL_MAT writes it. When the one-launch decode form
+ * places each KV head's workgroups on one XCD (n_head_kv a multiple of the device's XCD count), its
+ * workgroups with work fit the device at once (4 per compute unit: at the Llama-3-8B shape up to ~4.5 K
+ * cells), w_qkv is Q4_K with K <= 4096 and the buffers are 16-byte aligned, it is one launch: workgroups of the launch
+ * compute each KV head's Q|K|V rows on that head's XCD while its segments load K. Otherwise the two
+ * calls run. w_qkv: N = (n_head + 2 n_head_kv) D rows of K = the x row's length; x_dev and qkv_dev must
+ * not overlap. Shapes and errors otherwise as the two calls. (No counterpart in the reference: its
+ * records run one after another.) */
+int tsr_hip_attn_qkv_plan_rope_tab(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const tsr_hip_weight * w_qkv,
+                                   const float * x_dev, float eps, const float * norm_w_dev, float * qkv_dev,
+                                   tsr_hip_kv * kc, tsr_hip_kv * vc, float scale, uint32_t n_dims, int mode,
+                                   const float * tab_dev, const int64_t * cell_dev, int32_t * bad_dev,
+                                   const float * mask_f32_dev, float * out_dev, uint64_t out_stride, void * stream);
 int tsr_hip_fa_plan_free(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan);
 /* The one-launch decode form of the planned FLASH_ATTN_EXT (one query row) runs a workgroup per ATTPV
  * segment and exchanges the chunk maxima and the segment results between its workgroups (no

@@ -38,7 +38,9 @@
 #include "glue.hpp"
 #include "kernels.hpp"
 #include "kvstore.hpp"
+#include "mv_q4k.hpp"
 #include "qact.hpp"
+#include "wlayout.hpp"
 
 namespace tsr {
 
@@ -126,10 +128,138 @@ __device__ __forceinline__ FaDecBlock fa_dec_block(const FaDecArgs & a) {
 // p [4][64] 1024 | digits [4 waves][1024] | keys 16 | maxima 16 | flag 16.
 constexpr uint32_t kDecLds = 256 + 512 + 64 + 128 + 16 + 128 + 16 + 4096 + 1024 + 1024 + 4096 + 48;
 
-template <int D, bool ROPE, bool LOCAL>
+// ---- the Q|K|V rows of the launch (FaDecArgs::qkv_w) ----------------------------------------------
+// Workgroup j of KV head g computes 16 rows of the Q|K|V MUL_MAT with the fused RMS_NORM + MUL: j < G D/16
+// the rows 16 j .. of its q heads, then its k head's, then its v head's, bit-identical to k_mv_q4k with
+// kPrepNorm (the same x preparation, A256 quantization, Q4_K terms and 16-partial tree). K <= 4096: one
+// super-block per (row, partial), so thread (wave v, lane 16 i + r) computes the term of super-block
+// 4 v + i of row r, which is the row's partial p[4 v + i] (+0 + term), and the thread holding x block
+// b = 4 v + i (16 values per lane) quantizes it. Its loads are issued at once: the norm weights and x,
+// then (after a bare barrier, so that every wave's x is ahead in the queue) its unit's 9 weight pieces
+// (from any row block of the weight's layout) and the epoch. The rows go to qkv_y
+// with plain stores (the XCD's L2); after they are complete (vmcnt) the workgroup raises its flag.
+// LDS (bytes): x quants [16][272] | sub-block sums [16][8] | scales [16] | partials [16][16] |
+// control 16 | squares [K].
+constexpr uint32_t kQkvMaxK = 4096;
+constexpr uint32_t kQkvLds = 16 * kXq4Stride + 16 * 8 * 4 + 16 * 4 + 16 * 16 * 4 + 16 + 4 * kQkvMaxK;
+
+template <int D>
+__device__ __forceinline__ void fa_qkv_rows(const FaDecArgs & a, uint8_t * lds, uint32_t j, uint32_t g) {
+    int8_t * s_xq = (int8_t *)lds;
+    int * s_xb = (int *)(lds + 16u * kXq4Stride);
+    float * s_xd = (float *)(s_xb + 16u * 8u);
+    float * s_p = s_xd + 16u;                                     // [row][partial]
+    uint32_t * s_ctl = (uint32_t *)(s_p + 256u);                  // halves of the RMS sum, tiny flag
+    float * s_sq = (float *)(s_ctl + 4u);
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, v = tid >> 6;
+    const uint32_t G = a.G, K = a.qkv_K, nsb = K >> 8;
+    const WGeom wg = wgeom(a.qkv_N, nsb, a.qkv_rb, true);
+    const uint32_t jq = G * (D / 16u), jk = jq + D / 16u;
+    const uint32_t row0 = j < jq ? g * G * D + 16u * j
+                                 : a.n_head * D + (j < jk ? g * D + 16u * (j - jq) : a.E + g * D + 16u * (j - jk));
+    // x block b = 4 v + i (lane 16 i + l16: values 16 l16 .. + 15) and the unit (super-block b, row l16)
+    const uint32_t i4 = lane >> 4, l16 = lane & 15u, b = 4u * v + i4, bc = min(b, nsb - 1u);
+    const bool has_w = a.qkv_pw != nullptr;
+    const float * pl = has_w ? a.qkv_pw : a.qkv_x;                // without MUL: a valid address, unused
+    const uint32_t n = row0 + l16, B = n / wg.rb, rin = n - B * wg.rb, R = wl_rows(wg, B), sl = wl_slot_of(wg, bc);
+    float4 pv[4], xv[4];
+#pragma unroll
+    for (uint32_t c = 0; c < 4u; ++c) pv[c] = *(const float4 *)(pl + 256u * bc + 16u * l16 + 4u * c);
+#pragma unroll
+    for (uint32_t c = 0; c < 4u; ++c) xv[c] = *(const float4 *)(a.qkv_x + 256u * bc + 16u * l16 + 4u * c);
+    // every wave's x requests enter the compute unit's memory queue before any weight request (a bare
+    // barrier orders the issue and waits for no load): the queue serves them in order
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 qv[8];
+#pragma unroll
+    for (uint32_t jj = 0; jj < 8u; ++jj) qv[jj] = *(const uint4 *)(a.qkv_w + wl_quant_off(wg, B, R, jj, sl, rin));
+    const uint4 mv = *(const uint4 *)(a.qkv_w + wl_meta_off(wg, B, R, sl, rin));
+    const uint32_t epv = a.ep[(size_t)g * G * (D / 64u)];         // the launch's tag: epoch + 1
+    __builtin_amdgcn_sched_barrier(0);
+
+    // RMS_NORM: the squares, the two halves of the 128 ordered partials on waves 0 and 1, the scale
+    if (b < nsb) {
+#pragma unroll
+        for (uint32_t c = 0; c < 4u; ++c) *(float4 *)(s_sq + 256u * b + 16u * l16 + 4u * c) = sq4(xv[c]);
+    }
+    if (tid == 0u) s_ctl[2] = 0u;
+    lds_barrier();
+    if (v < 2u) {
+        const uint32_t i = 64u * v + lane, nk = K >> 7;           // terms per partial
+        float p = 0.0f;
+        for (uint32_t k0 = 0; k0 < nk; k0 += 32u) {
+            float t[32];
+#pragma unroll
+            for (uint32_t k = 0; k < 32u; ++k) t[k] = s_sq[i + 128u * min(k0 + k, nk - 1u)];
+#pragma unroll
+            for (uint32_t k = 0; k < 32u; ++k) {
+                const float q = p + t[k];                         // plain additions: see rms_tree64
+                p = k0 + k < nk ? q : p;
+            }
+        }
+        p = rms_tree64(p);
+        if (lane == 0u) s_ctl[v] = __float_as_uint(p);
+    }
+    lds_barrier();
+    const float sc = rms_scale(__uint_as_float(s_ctl[0]), __uint_as_float(s_ctl[1]), a.qkv_inv_n, a.qkv_eps);
+    if (__builtin_expect(!prep_norm_apply_fast(xv, sc, pv, has_w), 0)) {
+#pragma unroll
+        for (uint32_t c = 0; c < 4u; ++c) xv[c] = prep_norm_apply(xv[c], sc, pv[c], has_w);
+    }
+    // QACT A256 of block b (a 16-lane row per block)
+    float d;
+    int s16;
+    bool tiny;
+    const uint4 qq = qact_a256_row(xv, &d, &s16, &tiny);
+    const int s32 = s16 + dpp_i<kDppXor1>(s16);                   // sum of the 32 quants of a sub-block
+    if (b < nsb) {
+        *(uint4 *)(s_xq + b * kXq4Stride + 16u * l16) = qq;
+        if ((l16 & 1u) == 0u) s_xb[b * 8u + (l16 >> 1)] = s32;
+        if (l16 == 0u) s_xd[b] = d;
+    }
+    if (__ballot(tiny && b < nsb) != 0ull && lane == 0u) s_ctl[2] = 1u;
+    lds_barrier();
+    const bool slow = s_ctl[2] != 0u;                             // some block has 0 < |Dx| < 2^-60
+
+    // the unit's term = partial p[b] of row l16 (+0 + term); partials of missing super-blocks are +0
+    int isum, msum;
+    q4k_unit_sums<8>(qv, mv, s_xq + bc * kXq4Stride, s_xb + bc * 8u, 0u, isum, msum);
+    const float dx = s_xd[bc];
+    const float dq = h2f_fast(mv.x & 0xFFFFu), dm = h2f_fast(mv.x >> 16);
+    float tt;
+    if (__builtin_expect(!slow, 1)) tt = 0.0f + ((dq * dx) * (float)isum - (dm * dx) * (float)msum);
+    else tt = sadd(0.0f, ssub(smul(smul(dq, dx), i2f(isum)), smul(smul(dm, dx), i2f(msum))));
+    s_p[16u * l16 + b] = b < nsb ? tt : 0.0f;
+    lds_barrier();
+    // the 16-partial tree of row tid / 16 (lane i of the 16-lane row holds p[i])
+    float y = s_p[tid];
+    if (__builtin_expect(!slow, 1)) {
+        y = y + dpp_f<kDppXor1>(y);
+        y = y + dpp_f<kDppXor2>(y);
+        y = y + dpp_f<kDppRowHalfMirror>(y);
+        y = y + dpp_f<kDppRowMirror>(y);
+        y = canon(y);
+    } else {
+        y = sadd(y, dpp_f<kDppXor1>(y));
+        y = sadd(y, dpp_f<kDppXor2>(y));
+        y = sadd(y, dpp_f<kDppRowHalfMirror>(y));
+        y = sadd(y, dpp_f<kDppRowMirror>(y));
+    }
+    if ((tid & 15u) == 0u) a.qkv_y[row0 + (tid >> 4)] = y;
+    vm_wait();                                                    // the rows are in the L2
+    lds_barrier();
+    if (tid == 0u) {
+        const uint32_t tagw = ((epv + 1u) & kTagMask) | (xcc_id() << 28);
+        __hip_atomic_store(a.qkv_flag + (size_t)g * 64u + j, tagw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+}
+
+template <int D, bool ROPE, bool LOCAL, bool QKV>
 __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     constexpr uint32_t NBD = D / 32u;                             // K / V blocks of a head
-    __shared__ __align__(16) uint8_t lds[kDecLds];
+    __shared__ __align__(16) uint8_t lds[QKV && kQkvLds > kDecLds ? kQkvLds : kDecLds];
     uint32_t * s_t64 = (uint32_t *)lds;
     int8_t * s_q = (int8_t *)(lds + 256);                         // [G][D]
     float * s_dx = (float *)(lds + 768);                          // [G][NBD]
@@ -145,7 +275,14 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     float * s_m = (float *)(lds + 11376);                         // [4] chunk maxima
 
     const uint32_t per_item = 4u * a.maxtiles, nred = a.G * (D / 64u), nseg_slots = a.n_items * per_item;
-    const FaDecBlock blk = fa_dec_block<LOCAL>(a);
+    FaDecBlock blk = fa_dec_block<LOCAL>(a);
+    if constexpr (QKV) {                                          // the Q|K|V rows first in dispatch order
+        if (blk.x < a.nq) {
+            fa_qkv_rows<D>(a, lds, blk.x, blk.g);
+            return;
+        }
+        blk.x -= a.nq;
+    }
     // The KV head's reducers: first in dispatch order when the whole grid is resident at once (they
     // then poll from the start, and finish sooner), after the segments otherwise (then the reducers
     // would hold slots that segments need; segments never wait on reducers)
@@ -209,8 +346,11 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
         cs_a = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rt, 8u * ia, 0, 0));
         cs_b = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rt, 8u * ic, 0, 0));
     }
-    const float4 qv0 = *(const float4 *)qsrc;
-    const float4 qpart = ROPE ? *(const float4 *)(qsrc + dj) : qv0;
+    float4 qv0, qpart;
+    if constexpr (!QKV) {                                         // (in the launch: after its rows' flags)
+        qv0 = *(const float4 *)qsrc;
+        qpart = ROPE ? *(const float4 *)(qsrc + dj) : qv0;
+    }
     // the EXPK table (kernel-argument memory) and the epochs last: nothing before the quantization's LDS
     // stores waits for them (loads retire in order; the epochs were written by the previous launch, in
     // a decode layer's sequence too long ago to be in a cache)
@@ -254,6 +394,29 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     int4 kr0 = *(const int4 *)kbase, kr1 = *(const int4 *)(kbase + 256u);
     uint32_t km = ((const uint16_t *)a.kc.base)[((size_t)ug[kkj] * nbk + (size_t)g * NBD + bk) * 16u + rrj];
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (QKV) {
+        // every wave polls the flags of its KV head's row workgroups (lane j: workgroup j), then loads its
+        // Q|K|V values (agent-coherent loads: the rows were stored in this launch)
+        const uint32_t * fl = a.qkv_flag + (size_t)g * 64u + min(lane, a.nq - 1u);
+        uint32_t fv = 0u, spins = 0;
+        for (;;) {
+            fv = ld_co_u(fl);
+            if (__all(tag_is(fv, tag))) break;
+            if (__builtin_expect(++spins >= a.spin_max, 0)) {
+                if (lane == 0u && a.bad != nullptr)
+                    __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);                  // the value loads stay behind the poll
+        if (__builtin_expect(__any(tag_is(fv, tag) && (fv >> 28) != xcc), 0) && lane == 0u && a.bad != nullptr)
+            __hip_atomic_fetch_or(a.bad, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const __amdgpu_buffer_rsrc_t rq = fa_rsrc(a.q, 4u * (nh * D + 2u * E));
+        const uint32_t qo = 4u * (uint32_t)(qsrc - a.q);
+        qv0 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, qo, 0, kSc1));
+        qpart = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 4u * (uint32_t)dj, 0, kSc1));
+    }
 
     // ---- ROPE of the query heads and the new k row ----
     float4 r = qv0;
@@ -820,11 +983,19 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
 }  // namespace tsr
 
 int tsr_launch_fa_dec(const tsr::FaDecArgs & a, hipStream_t s) {
-    const uint32_t per_head = a.n_items * a.maxtiles * 4u + a.G * (a.D / 64u);   // segments, then reducers
+    // (Q|K|V rows,) segments and reducers of each KV head
+    const uint32_t per_head = a.n_items * a.maxtiles * 4u + a.G * (a.D / 64u) + (a.qkv_w != nullptr ? a.nq : 0u);
     const bool local = a.n_xcd != 0u && a.n_head_kv % a.n_xcd == 0u;
     const dim3 grid = local ? dim3(per_head * a.n_head_kv, 1) : dim3(per_head, a.n_head_kv);
     const bool rope = a.cell != nullptr;
-#define TSR_DEC(DD, RR, LL) hipLaunchKernelGGL((tsr::k_fa_dec<DD, RR, LL>), grid, dim3(256), 0, s, a)
+    if (a.qkv_w != nullptr) {                                     // the host checked the shape
+        if (!local || !rope || a.qkv_K > tsr::kQkvMaxK || a.nq > 64u) return -2;
+        if (a.D == 128u) hipLaunchKernelGGL((tsr::k_fa_dec<128, true, true, true>), grid, dim3(256), 0, s, a);
+        else if (a.D == 64u) hipLaunchKernelGGL((tsr::k_fa_dec<64, true, true, true>), grid, dim3(256), 0, s, a);
+        else return -2;
+        return hipGetLastError() == hipSuccess ? 0 : -4;
+    }
+#define TSR_DEC(DD, RR, LL) hipLaunchKernelGGL((tsr::k_fa_dec<DD, RR, LL, false>), grid, dim3(256), 0, s, a)
     switch (a.D * 4u + (rope ? 2u : 0u) + (local ? 1u : 0u)) {
         case 256: TSR_DEC(64, false, false); break;
         case 257: TSR_DEC(64, false, true); break;

@@ -161,6 +161,17 @@ struct FaDecArgs {
     int32_t * bad;
     float ts, m;
     ExpkTab ex;
+    // The token's Q|K|V row computed in the same launch (qkv_w != 0; ROPE, one XCD per KV head): nq
+    // workgroups per KV head, first in dispatch order, each compute 16 of the KV head's rows (its q
+    // heads, then its k and v heads) of MUL_MAT(W, RMS_NORM(x) * pw) into qkv_y (== q) and raise a
+    // flag with the launch's tag; the segments read q after every flag of their KV head is up
+    const uint8_t * qkv_w;   // Q4_K weight layout (wlayout.hpp): qkv_N = (n_head + 2 n_head_kv) D rows of qkv_K
+    const float * qkv_x;     // the token's row [qkv_K]
+    const float * qkv_pw;    // the norm's MUL weight [qkv_K] (nullable)
+    float * qkv_y;
+    uint32_t * qkv_flag;     // [n_head_kv][64] (tag | XCD << 28) words
+    uint32_t qkv_N, qkv_K, qkv_rb, nq;
+    float qkv_eps, qkv_inv_n;
 };
 
 // ROPE over T tokens of n_heads heads (head h of token t at x + t * x_stride + h * head_dim).

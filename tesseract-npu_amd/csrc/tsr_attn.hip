@@ -557,9 +557,10 @@ struct tsr_hip_fa_plan {
     uint64_t cells_max = 0;
     uint8_t * dev = nullptr;
     size_t o_items = 0, o_S = 0, o_Mp = 0, o_OP = 0, o_LP = 0, o_SO = 0, o_SL = 0, o_MI = 0, o_TK = 0, o_EP = 0,
-           bytes = 0;
+           o_QF = 0, bytes = 0;
     bool set = false, general = false;
     uint32_t n_items = 0, maxtiles = 0, max_groups = 0, mstride = 0;   // the shape a launch bakes in
+    uint32_t seg_work = 0;   // the decode form's segments with work (64 cells of one channel) per KV head
     uint64_t cells = 0;
 };
 
@@ -605,6 +606,8 @@ int tsr_hip_fa_plan_create(tsr_hip_ctx * ctx, uint32_t D, uint32_t n_head, uint3
     // the decode form's segment slots (32 bytes) and per-reducer epochs (<= 4 heads x 2 value parts)
     p->o_TK = off; off = up256(off + (T == 1u ? 32u * 8u * 4u * (size_t)items * n_head_kv : 0u));
     p->o_EP = off; off = up256(off + (T == 1u ? 4u * 8u * (size_t)n_head_kv : 0u));
+    // the flags of the Q|K|V row workgroups (tsr_hip_attn_qkv_plan_rope_tab): 64 words per KV head
+    p->o_QF = off; off = up256(off + (T == 1u ? 4u * 64u * (size_t)n_head_kv : 0u));
     p->bytes = off;
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
@@ -673,14 +676,32 @@ int tsr_hip_fa_plan_set(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan, const uint32_
     plan->mstride = mstride;
     plan->general = general;
     plan->cells = w.cells;
+    plan->seg_work = 0u;
+    for (const tsr::FaItem & it : w.items)
+        for (uint32_t c = 0; c < 4u; ++c) {                     // k_fa_dec.hip FaSeg: channel c's groups
+            const uint32_t uf = it.u0 + ((c + 4u - (it.u0 & 3u)) & 3u), ue = it.u0 + it.n;
+            const uint32_t nu = uf < ue ? (ue - 1u - uf) / 4u + 1u : 0u;
+            plan->seg_work += (nu + 3u) / 4u;
+        }
     if (shape_changed) *shape_changed = changed ? 1 : 0;
     return TSR_HIP_OK;
 }
 
 // The planned FLASH_ATTN_EXT launch (optionally with ROPE + SET_ROWS_KV in the score kernel).
+static bool aligned16(const void * p) { return ((uintptr_t)p & 15u) == 0u; }
+
+// The Q|K|V MUL_MAT computed inside the one-launch decode form (tsr_hip_attn_qkv_plan_rope_tab).
+struct QkvIn {
+    const tsr_hip_weight * w;
+    const float * x;
+    const float * pw;
+    float eps;
+};
+
 static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const float * q_dev, uint64_t q_stride,
                           const tsr_hip_kv * kc, const tsr_hip_kv * vc, float scale, const float * mask_f32_dev,
-                          float * out_dev, uint64_t out_stride, const tsr::FaArgs * rope, void * stream) {
+                          float * out_dev, uint64_t out_stride, const tsr::FaArgs * rope, void * stream,
+                          const QkvIn * qkv = nullptr) {
     if (ctx == nullptr || plan == nullptr || q_dev == nullptr || kc == nullptr || vc == nullptr || out_dev == nullptr)
         return TSR_HIP_E_ARG;
     if (!plan->set || (plan->general && mask_f32_dev == nullptr)) return TSR_HIP_E_MASK;
@@ -715,8 +736,22 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
         d.ep = (uint32_t *)(plan->dev + plan->o_EP);
         d.spin_max = ctx->fa_spin_max;
         d.n_xcd = ctx->n_xcd;
-        {   // reducers first when the grid is resident at once (4 of the kernel's 5 workgroups per CU)
-            const uint64_t wgs = ((uint64_t)plan->n_items * plan->maxtiles * 4u + G * (plan->D / 64u)) * plan->n_head_kv;
+        if (qkv != nullptr) {                                // 16 rows per workgroup, first in dispatch order
+            d.qkv_w = qkv->w->dev;
+            d.qkv_x = qkv->x;
+            d.qkv_pw = qkv->pw;
+            d.qkv_y = const_cast<float *>(q_dev);
+            d.qkv_flag = (uint32_t *)(plan->dev + plan->o_QF);
+            d.qkv_N = qkv->w->N;
+            d.qkv_K = qkv->w->K;
+            d.qkv_rb = qkv->w->rb;
+            d.nq = (G + 2u) * plan->D / 16u;
+            d.qkv_eps = qkv->eps;
+            d.qkv_inv_n = 1.0f / (float)qkv->w->K;          // correctly rounded (IEEE division), as the matvec's
+        }
+        {   // reducers first when the grid is resident at once (4 workgroups per CU: the kernel holds 4 or 5)
+            const uint64_t wgs = ((uint64_t)plan->n_items * plan->maxtiles * 4u + G * (plan->D / 64u) + d.nq) *
+                                 plan->n_head_kv;
             d.red_first = ctx->n_cu > 0 && wgs <= 4u * (uint64_t)ctx->n_cu ? 1u : 0u;
         }
         d.out = out_dev;
@@ -737,8 +772,14 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
         ctx->ctr.flash_attn_calls++;
         ctx->ctr.flash_attn_kv_bytes += plan->cells * (uint64_t)E / 32u * 34u * 2u;
         if (rope != nullptr) ctx->ctr.set_rows_calls += 2u;
+        if (qkv != nullptr) {
+            ctx->ctr.mul_mat_calls++;
+            ctx->ctr.mul_mat_rows += qkv->w->N;
+            ctx->ctr.mul_mat_weight_bytes += (uint64_t)qkv->w->N * (qkv->w->K / 256u) * 144u;
+        }
         return tsr_launch_fa_dec(d, ctx->pick(stream)) ? TSR_HIP_E_HIP : TSR_HIP_OK;
     }
+    if (qkv != nullptr) return TSR_HIP_E_SHAPE;              // (the caller checked the decode form)
     tsr::FaPlan p{};
     p.n_items = plan->n_items;
     p.maxtiles = plan->maxtiles;
@@ -820,4 +861,41 @@ int tsr_hip_flash_attn_plan_rope_tab(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * 
     if (rc) return rc;
     r.rtab = tab_dev;
     return fa_plan_launch(ctx, plan, qkv_dev, 0u, kc, vc, scale, mask_f32_dev, out_dev, out_stride, &r, stream);
+}
+
+// MUL_MAT_NORM of the Q|K|V weight, then the planned FLASH_ATTN_EXT with ROPE + SET_ROWS_KV, in one launch
+// when the decode form places every workgroup of a KV head on one XCD: the KV head's Q|K|V rows are
+// computed by workgroups of the same launch on that XCD while its segments already load K.
+int tsr_hip_attn_qkv_plan_rope_tab(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const tsr_hip_weight * w_qkv,
+                                   const float * x_dev, float eps, const float * norm_w_dev, float * qkv_dev,
+                                   tsr_hip_kv * kc, tsr_hip_kv * vc, float scale, uint32_t n_dims, int mode,
+                                   const float * tab_dev, const int64_t * cell_dev, int32_t * bad_dev,
+                                   const float * mask_f32_dev, float * out_dev, uint64_t out_stride, void * stream) {
+    if (ctx == nullptr || plan == nullptr || w_qkv == nullptr || x_dev == nullptr || qkv_dev == nullptr ||
+        tab_dev == nullptr || ((uintptr_t)tab_dev & 7u) != 0u)
+        return TSR_HIP_E_ARG;
+    const uint32_t D = plan->D, nkv = plan->n_head_kv, G = nkv ? plan->n_head / nkv : 0u;
+    if (w_qkv->N != (plan->n_head + 2u * nkv) * D) return TSR_HIP_E_SHAPE;
+    tsr::FaArgs r;
+    int rc = fa_rope_args(plan, n_dims, mode, cell_dev, bad_dev, r);
+    if (rc) return rc;
+    r.rtab = tab_dev;
+    const uint32_t K = w_qkv->K;
+    const bool apart = (uintptr_t)qkv_dev + 4u * (size_t)w_qkv->N <= (uintptr_t)x_dev ||
+                           (uintptr_t)x_dev + 4u * (size_t)K <= (uintptr_t)qkv_dev;
+    const bool one = plan->set && !(plan->general && mask_f32_dev == nullptr) && G <= 4u && plan->n_items <= 256u &&
+                     ctx->n_xcd != 0u && nkv % ctx->n_xcd == 0u && w_qkv->fmt == TSR_HIP_FMT_Q4_K && K % 256u == 0u &&
+                     K <= 4096u && aligned16(x_dev) && (norm_w_dev == nullptr || aligned16(norm_w_dev)) &&
+                     aligned16(qkv_dev) && apart &&
+                     // the workgroups with work resident at once (4 per CU); with more, the row workgroups
+                     // hold slots that segments need (measured: 8208 cells 24.8 -> 26.3 us, 4136 cells
+                     // 20.1 -> 18.9 us)
+                     ((uint64_t)plan->seg_work + G * (D / 64u) + (G + 2u) * D / 16u) * nkv <= 4u * (uint64_t)ctx->n_cu;
+    if (!one) {                                                   // the two records, two launches
+        rc = tsr_hip_mul_mat_norm(ctx, w_qkv, x_dev, 1u, K, eps, norm_w_dev, qkv_dev, w_qkv->N, nullptr, 0u, 0u, stream);
+        if (rc) return rc;
+        return fa_plan_launch(ctx, plan, qkv_dev, 0u, kc, vc, scale, mask_f32_dev, out_dev, out_stride, &r, stream);
+    }
+    const QkvIn q{ w_qkv, x_dev, norm_w_dev, eps };
+    return fa_plan_launch(ctx, plan, qkv_dev, 0u, kc, vc, scale, mask_f32_dev, out_dev, out_stride, &r, stream, &q);
 }

@@ -37,7 +37,7 @@ EXPORTS = (
     "tsr_hip_fa_plan_free", "tsr_hip_graph_begin", "tsr_hip_graph_end", "tsr_hip_graph_launch", "tsr_hip_graph_free",
     "tsr_hip_mul_mat_norm", "tsr_hip_rope_kv", "tsr_hip_flash_attn_plan_rope", "tsr_hip_rope_table",
     "tsr_hip_flash_attn_plan_rope_tab", "tsr_hip_mul_mat_epi", "tsr_hip_set_fa_wait_limit",
-    "tsr_hip_flash_attn_noalloc", "tsr_hip_get_flags", "tsr_hip_msum_mask_f32",
+    "tsr_hip_flash_attn_noalloc", "tsr_hip_get_flags", "tsr_hip_msum_mask_f32", "tsr_hip_attn_qkv_plan_rope_tab",
 )
 
 
@@ -119,6 +119,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "tsr_hip_set_fa_wait_limit": ([vp, u32], C.c_int),
         "tsr_hip_flash_attn_plan_rope_tab": ([vp, vp, vp, vp, vp, C.c_float, u32, C.c_int, vp, vp, vp, vp, vp, u64, vp],
                                              C.c_int),
+        "tsr_hip_attn_qkv_plan_rope_tab": ([vp, vp, vp, vp, C.c_float, vp, vp, vp, vp, C.c_float, u32, C.c_int, vp, vp,
+                                            vp, vp, vp, u64, vp], C.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -481,6 +483,17 @@ class Device:
                                                        mode, self._p(tab), self._p(cell), self._p(bad),
                                                        self._p(mask_f32), self._p(out), out_stride, stream),
                "flash_attn_plan_rope_tab")
+
+    def attn_qkv_plan_rope_tab(self, plan: "FaPlan", w_qkv: Weight, x, eps: float, norm_w, qkv, kc: KvCache,
+                               vc: KvCache, scale: float, n_dims: int, mode: int, tab, cell, out, out_stride: int,
+                               bad=None, mask_f32=None, stream=None) -> None:
+        """mul_mat_norm(w_qkv, x, 1, ..., eps, norm_w -> qkv) then flash_attn_plan_rope_tab(plan, qkv, ...), in
+        one launch where the decode form allows it (same bits either way)."""
+        _check(self.L.tsr_hip_attn_qkv_plan_rope_tab(self.ctx, plan.h, w_qkv.h, self._p(x), float(eps), self._p(norm_w),
+                                                     self._p(qkv), kc.h, vc.h, float(scale), n_dims, mode,
+                                                     self._p(tab), self._p(cell), self._p(bad), self._p(mask_f32),
+                                                     self._p(out), out_stride, stream),
+               "attn_qkv_plan_rope_tab")
 
     def graph_begin(self, stream=None) -> None:
         _check(self.L.tsr_hip_graph_begin(self.ctx, stream), "graph_begin")

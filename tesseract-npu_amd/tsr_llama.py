@@ -20,9 +20,10 @@ With fused=True (the default) RMS_NORM + MUL runs inside the Q|K|V and gate|up M
 (tsr_hip_mul_mat_norm), SWIGLU in the epilogue of the gate|up MUL_MAT (TSR_HIP_MM_GLU over gate / up
 rows interleaved), and ROPE with both SET_ROWS_KV inside the planned FLASH_ATTN_EXT
 (tsr_hip_flash_attn_plan_rope_tab, the angles of the token's position made once per token by
-tsr_hip_rope_table; eager steps, planned on the host, use tsr_hip_rope_kv): at the Llama-3-8B shape a
-layer is five launches (the planned decode FLASH_ATTN_EXT is one), each fusion bit-identical to the ops
-it replaces. fused=False runs every op of the list as its own call.
+tsr_hip_rope_table; eager steps, planned on the host, use tsr_hip_rope_kv), and with the planned form
+the Q|K|V MUL_MAT joins that launch too (tsr_hip_attn_qkv_plan_rope_tab: one launch where each KV head's
+workgroups share an XCD, else the two calls): at the Llama-3-8B shape a layer is four launches, each
+fusion bit-identical to the ops it replaces. fused=False runs every op of the list as its own call.
 The token embedding is a GET_ROWS of an f32 table. Row concatenation leaves every row's result
 unchanged (each output row is its own dot product with the same quantized activation), and ROPE
 of q and k heads in one launch is the same per-head rotation. A residual addend is one FA(add, v),
@@ -148,9 +149,11 @@ class LlamaDecoder:
     """The model on one device: weights uploaded once, one q8_0 K and V cache per layer of kv_size
     cells, and the activation buffers of one decode token."""
 
-    def __init__(self, dev: H.Device, cfg: LlamaConfig, weights: SyntheticWeights, kv_size: int, fused: bool = True):
+    def __init__(self, dev: H.Device, cfg: LlamaConfig, weights: SyntheticWeights, kv_size: int, fused: bool = True,
+                 qkv_in_attn: bool = True):
         self.dev, self.cfg, self.kv_size = dev, cfg, kv_size
         self.fused = fused
+        self.qkv_in_attn = qkv_in_attn     # planned decode: the Q|K|V MUL_MAT inside the attention launch
         c = cfg
         f4 = 4
         self.tok_embd = dev.upload(np.ascontiguousarray(weights.embedding(), np.float32))
@@ -340,7 +343,12 @@ class LlamaDecoder:
             d.rope_table(self.pos_ptr, c.head_dim, c.rope_base, self.rtab, stream=stream)
         for L in self.layers:
             fa_done = False
-            if self.fused:
+            if fa_tab and self.qkv_in_attn:                       # Q|K|V, ROPE, SET_ROWS_KV and FA: one call
+                d.attn_qkv_plan_rope_tab(self.plan, L["wqkv"], self.x, c.eps, L["attn_norm"], self.qkv, L["kc"],
+                                         L["vc"], self.scale, c.head_dim, c.rope_mode, self.rtab, self.cell_ptr,
+                                         self.att, nq, bad=self.bad, stream=stream)
+                fa_done = True
+            elif self.fused:
                 d.mul_mat_norm(L["wqkv"], self.x, 1, n, c.eps, L["attn_norm"], self.qkv, w3, stream=stream)
                 if fa_tab:                                        # ROPE + SET_ROWS_KV inside the FA launch
                     d.flash_attn_plan_rope_tab(self.plan, self.qkv, L["kc"], L["vc"], self.scale, c.head_dim,

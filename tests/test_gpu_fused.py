@@ -1,6 +1,7 @@
 """GPU fused decode-layer entry points through the C ABI, bit for bit against the oracle's separate
 ops on the same seeded inputs: MUL_MAT of RMS_NORM(x) * w (tsr_hip_mul_mat_norm), the gate / up
-MUL_MAT with its SWIGLU epilogue (TSR_HIP_MM_GLU) and ROPE + SET_ROWS_KV (tsr_hip_rope_kv)."""
+MUL_MAT with its SWIGLU epilogue (TSR_HIP_MM_GLU), ROPE + SET_ROWS_KV (tsr_hip_rope_kv) and the
+attention half of a decode layer in one launch (tsr_hip_attn_qkv_plan_rope_tab)."""
 import numpy as np
 import pytest
 
@@ -279,6 +280,104 @@ def test_flash_attn_plan_rope(dev, oc, n_kv, pos, cell, n_head, n_head_kv, D, mo
     plan.free()
     kc.free()
     vc.free()
+
+
+@pytest.mark.parametrize("fmt,K,n_kv,pos,cell,n_head,n_head_kv,D,mode,n_dims,general", [
+    (H.FMT_Q4_K, 4096, 4232, 4200, 4200, 32, 8, 128, H.ROPE_NORMAL, 128, False),   # Llama-3-8B decode layer
+    (H.FMT_Q4_K, 4096, 4232, 5000, 100, 32, 8, 128, H.ROPE_NEOX, 128, "swa"),      # wrapped window, new cell 100
+    (H.FMT_Q4_K, 2048, 2100, 2090, 2068, 16, 8, 128, H.ROPE_NEOX, 64, False),      # G = 2
+    (H.FMT_Q4_K, 1024, 1500, 1400, 1400, 8, 8, 64, H.ROPE_NORMAL, 64, True),       # G = 1, GENERAL mask, D 64
+    (H.FMT_Q4_K, 768, 640, 600, 600, 24, 8, 64, H.ROPE_NEOX, 64, False),           # 3 super-blocks, G = 3
+    (H.FMT_Q4_K, 1024, 1500, 1400, 1400, 12, 4, 64, H.ROPE_NORMAL, 32, False),     # 4 KV heads: two launches
+    (H.FMT_Q4_K, 8192, 300, 257, 257, 32, 8, 128, H.ROPE_NORMAL, 128, False),      # K > 4096: two launches
+    (H.FMT_Q8_0, 1024, 300, 257, 257, 16, 8, 64, H.ROPE_NEOX, 64, False),          # Q8_0: two launches
+], ids=lambda v: str(v))
+def test_attn_qkv_plan_rope_tab(dev, oc, fmt, K, n_kv, pos, cell, n_head, n_head_kv, D, mode, n_dims, general):
+    """tsr_hip_attn_qkv_plan_rope_tab against the oracle's RMS_NORM + MUL, Q|K|V MUL_MAT, ROPE,
+    SET_ROWS_KV and FLASH_ATTN_EXT of one decode token (the Q|K|V row, the output and both caches),
+    twice on one plan (the second launch tags with the next epoch), and against the two calls it
+    replaces."""
+    import math
+    print(f"\nattn_qkv_plan_rope_tab fmt {fmt} K {K} n_kv {n_kv} pos {pos} cell {cell} heads {n_head}/{n_head_kv} "
+          f"D {D} mode {mode} n_dims {n_dims} general {general}", flush=True)
+    rng = np.random.default_rng(n_kv + pos + D + K)
+    E, nq = n_head_kv * D, n_head * D
+    N = nq + 2 * E
+    swa = general == "swa"
+    general = general is True
+    kv_size = 16 * -(-n_kv // 16) if general else n_kv
+    k0 = np.zeros((kv_size, E // 32 * 34), np.uint8)
+    v0 = np.zeros_like(k0)
+    hist = n_kv if swa else max(pos, cell)
+    oc.kv_set_rows(k0, S.normal(21 + D, hist * E).reshape(hist, E), np.arange(hist))
+    oc.kv_set_rows(v0, S.normal(22 + D, hist * E).reshape(hist, E), np.arange(hist))
+    blocks = S.quant_rows(fmt, S.seed_of("attn-qkv", f"{fmt}-{N}-{K}"), N, K)
+    x = _x_rows(K, 1, N + K)
+    x[0, :SPECIALS.size] = rng.standard_normal(SPECIALS.size).astype(np.float32)   # a finite row: q feeds FA
+    nw = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    eps = 1e-5
+    row = oc.mul_mat(fmt, blocks, K, oc.rms_norm(x, eps, nw[None]), threads=8)
+    base = 500000.0
+    ts = theta_scale(base, n_dims)
+    neox = mode != H.ROPE_NORMAL
+    q = oc.rope(np.ascontiguousarray(row[:, :nq]), np.array([pos], np.int32), D, n_dims, neox, ts)
+    k = oc.rope(np.ascontiguousarray(row[:, nq:nq + E]), np.array([pos], np.int32), D, n_dims, neox, ts)
+    kw, vw = k0.copy(), v0.copy()
+    oc.kv_set_rows(kw, k, np.array([cell], np.int64))
+    oc.kv_set_rows(vw, np.ascontiguousarray(row[:, nq + E:]), np.array([cell], np.int64))
+    scale = np.float32(1.0 / math.sqrt(D))
+    mf = None
+    if general:
+        mask = np.full((1, n_kv), -np.inf, np.float16)
+        mask[0, :hist + 1] = 0
+        mask[0, rng.integers(0, hist + 1, hist // 7)] = -1.75
+        mask[0, cell] = 0.5
+        msum = oc.msum(mask)
+        mf = oc.mask_f32(mask, scale)
+    elif swa:
+        msum = np.zeros(12, np.uint32)
+        msum[0], msum[1], msum[2] = 0x4D55534D, 1, n_kv
+        msum[8], msum[9], msum[10], msum[11] = 0, cell + 1, min(cell + 1000, n_kv - 300), n_kv
+    else:
+        msum = np.zeros(12, np.uint32)
+        msum[0], msum[1], msum[2], msum[9] = 0x4D55534D, 1, n_kv, hist + 1
+    runs = np.array([[cell, cell + 1]], np.uint32)
+    want = oc.flash_attn(q, kw, vw, D, n_head, n_head_kv, scale, msum, mf, new_runs=runs)
+    wt = dev.weight(fmt, blocks, N, K)
+    kc, vc = dev.kv(E, kv_size), dev.kv(E, kv_size)
+    plan = dev.fa_plan(D, n_head, n_head_kv, 1, kv_size)
+    plan.set(msum, runs, mask_f32=general)
+    xb, nb = dev.upload(x), dev.upload(nw)
+    qkv, out, bad = dev.alloc(4 * N), dev.alloc(4 * nq), dev.upload(np.zeros(1, np.int32))
+    pb, cb = dev.upload(np.array([pos], np.int32)), dev.upload(np.array([cell], np.int64))
+    mb = None if mf is None else dev.upload(mf)
+    tab = dev.alloc(4 * n_dims)
+    dev.rope_table(pb, n_dims, base, tab)
+    for rep in range(3):
+        kc.set_bytes(0, k0)
+        vc.set_bytes(1, v0)
+        qkv.write(np.full(N, np.nan, np.float32))
+        out.write(np.full(nq, np.nan, np.float32))
+        if rep < 2:
+            dev.attn_qkv_plan_rope_tab(plan, wt, xb, eps, nb, qkv, kc, vc, scale, n_dims, mode, tab, cb, out, nq,
+                                       bad=bad, mask_f32=mb)
+        else:                                                     # the two calls it replaces
+            dev.mul_mat_norm(wt, xb, 1, K, eps, nb, qkv, N)
+            dev.flash_attn_plan_rope_tab(plan, qkv, kc, vc, scale, n_dims, mode, tab, cb, out, nq, bad=bad, mask_f32=mb)
+        what = f"call {rep}"
+        assert_bits_equal(qkv.read(np.float32, (1, N)), row, f"Q|K|V row, {what}")
+        assert_bits_equal(out.read(np.float32, (1, nq)), want, f"attention, {what}")
+        assert (kc.get_bytes(0).reshape(kv_size, -1) == kw).all(), what
+        assert (vc.get_bytes(1).reshape(kv_size, -1) == vw).all(), what
+        assert bad.read(np.int32, (1,))[0] == 0, what
+    half = dev.weight(fmt, blocks[:N // 2], N // 2, K)
+    with pytest.raises(H.TsrHipError):                            # a weight of another row count
+        dev.attn_qkv_plan_rope_tab(plan, half, xb, eps, nb, qkv, kc, vc, scale, n_dims, mode, tab, cb, out, nq, bad=bad)
+    half.free()
+    plan.free()
+    kc.free()
+    vc.free()
+    wt.free()
 
 
 @pytest.mark.parametrize("pos,n_dims,m", [(0, 128, 1.0), (7, 64, 1.0), (4231, 128, 1.0), (131071, 128, 0.75),

@@ -72,7 +72,9 @@ def test_decode_matches_oracle(dev, oc, cfg, kv_size, hist, n_steps, fused):
     (LL.tiny_config(), 300, 254, 5),              # cells 255 .. 259: the plan grows a second chunk at 257
     (LL.tiny_config("tiny-qwen", wfmt=H.FMT_Q8_0, ofmt=H.FMT_Q8_0, rope_mode=H.ROPE_NEOX, eps=1e-6,
                     rope_base=1000000.0), 640, 300, 3),
-], ids=["q4k-norm-grow", "q80-neox"])
+    (LL.tiny_config("tiny-kv8", n_head=16, n_head_kv=8, head_dim=64, n_embd=512, n_ff=768, n_vocab=1000), 300, 254,
+     4),                                          # 8 KV heads: Q|K|V inside the attention launch
+], ids=["q4k-norm-grow", "q80-neox", "q4k-kv8"])
 def test_decode_graph_matches_oracle(dev, oc, cfg, kv_size, hist, n_steps):
     """The same decode as one graph replay per token: FLASH_ATTN_EXT from the device-resident plan, the
     position / cell and the plan copied in stream order, the greedy token fed back on the device."""

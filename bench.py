@@ -401,13 +401,13 @@ def adapter_decode(ev, e2e, caches, steps: int) -> dict:
     ms = ev.elapsed_ms(e0, e1)
     gd.synchronize()                                       # TSR_GG_E_FLAG if a kernel raised a flag
     s1 = gd.stats()
-    calls = [c["name"] for c in gd.lower(g.ctx.nodes)]
+    calls = [c["name"] for c in gd.lower(g.ctx.nodes) if not c["flags"] & G.CALL_IN_NEXT]
     out = {"tok_s": round(steps / (ms * 1e-3), 2), "ms_per_token": round(ms / steps, 5),
            "host_ms_per_token": round(host_ms, 4), "replays": s1["replays"] - s0["replays"],
            "plan_hits": s1["plan_hits"] - s0["plan_hits"], "launches_per_token": len(calls),
            "graph_nodes": len(g.ctx.nodes), "token0_logits_bit_equal_to_decoder": same,
            "setup_s": round(setup_s, 2),
-           "path": "tsr_gg_graph_compute over llama.cpp's graph (fused: Q|K|V + norm, ROPE+SET_ROWS+FA, "
+           "path": "tsr_gg_graph_compute over llama.cpp's graph (fused: Q|K|V + norm + ROPE+SET_ROWS+FA, "
                    "gate|up + norm + GLU), captured once, replayed per token"}
     g.free()
     kvbuf.free()

@@ -203,7 +203,9 @@ int tsr_gg_get_stats(tsr_gg_dev * dev, tsr_gg_stats * out);
  *     the FLASH_ATTN_EXT: one MUL_MAT over their rows into a plan buffer, then for one token one
  *     ROPE + SET_ROWS_KV + FLASH_ATTN_EXT launch (TSR_GG_CALL_ROPE_TABLE once per graph), for more
  *     tokens TSR_GG_CALL_ROPE_KV and the planned FLASH_ATTN_EXT; the K and V SET_ROWS must then write
- *     the same cells (else graph_compute fails: TSR_GG_E_UNSUPPORTED);
+ *     the same cells (else graph_compute fails: TSR_GG_E_UNSUPPORTED); for one token with the norm
+ *     folded into that MUL_MAT, the MUL_MAT runs inside the FLASH_ATTN_EXT call
+ *     (tsr_hip_attn_qkv_plan_rope_tab) and its own call carries TSR_GG_CALL_IN_NEXT in flags;
  *   - the gate and up MUL_MATs read only by a SWIGLU: one MUL_MAT with the GLU epilogue.
  * Each fusion leaves the results bit-identical to the unfused calls. */
 #define TSR_GG_CALL_MUL_MAT     1
@@ -217,6 +219,7 @@ int tsr_gg_get_stats(tsr_gg_dev * dev, tsr_gg_stats * out);
 #define TSR_GG_CALL_ARGMAX      9
 #define TSR_GG_CALL_ROPE_TABLE 10   /* the ROPE angles of a decode token, once per graph */
 #define TSR_GG_CALL_ROPE_KV    11   /* ROPE of q and k + SET_ROWS of k and v over a ubatch's Q|K|V rows */
+#define TSR_GG_CALL_IN_NEXT    0x80000000u   /* flags: the call's work runs inside its group's FLASH_ATTN_EXT call */
 typedef struct tsr_gg_call {
     int32_t kind, node, node2, node3;
     uint32_t N, K, T, flags;            /* MUL_MAT: rows, K, tokens, TSR_HIP_MM_* ; elementwise: n, rows */

@@ -1631,14 +1631,27 @@ struct Lowerer {
                 const float eps = fo->eps;
                 const float * nw = (const float *)NW.p;
                 c.run = [=](const Plan &) { return tsr_hip_mul_mat_norm(ctx, hw, xp, T, xs, eps, nw, yp, ys, nullptr, 0, flags, s); };
+                if (gr.attn && T == 1u && fuse) qkv_in = QkvIn{ (int)plan->calls.size() - 1, hw, xp, nw, eps };
             } else {
                 c.run = [=](const Plan &) { return tsr_hip_mul_mat(ctx, hw, xp, T, xs, yp, ys, nullptr, 0, flags, s); };
             }
             if (gr.attn) qkv_rows = yp;
+        } else if (fo && gr.attn && T == 1u && fuse) {
+            qkv_in = QkvIn{ (int)plan->calls.size() - 1, nullptr, nullptr, nullptr, 0.0f };
         }
         return true;
     }
     float * qkv_rows = nullptr;                            // the Q|K|V rows of the group being emitted
+    // A one-token Q|K|V MUL_MAT with its norm folded in: the attention call of its group runs it
+    // (tsr_hip_attn_qkv_plan_rope_tab) and its own call becomes a no-op marked TSR_GG_CALL_IN_NEXT.
+    struct QkvIn {
+        int call = -1;
+        const tsr_hip_weight * w = nullptr;
+        const float * x = nullptr;
+        const float * nw = nullptr;
+        float eps = 0.0f;
+    };
+    QkvIn qkv_in;                                          // of the group being emitted
 
     // The attention of a group: ROPE of q and k, SET_ROWS of k and v, FLASH_ATTN_EXT.
     bool group_attn(const Graph & g, const Group & gr) {
@@ -1691,6 +1704,7 @@ struct Lowerer {
         }
         Call & c = add(TSR_GG_CALL_FLASH_ATTN, gr.fa);
         fa_call_info(c, f, 0, row, g.nodes[gr.fa]->data);
+        if (T == 1 && qkv_in.call >= 0) plan->calls[qkv_in.call].info.flags |= TSR_GG_CALL_IN_NEXT;
         c.info.n_dims = (uint32_t)n_dims;
         c.info.mode = (uint32_t)mode;
         c.info.node2 = gr.mm_last;
@@ -1712,7 +1726,17 @@ struct Lowerer {
             float * qkv = qkv_rows;
             const uint32_t nd = (uint32_t)n_dims, D = f.D, H = f.H, Hk = f.Hk;
             const int64_t * cells = (const int64_t *)kp;
-            if (T == 1) {
+            if (T == 1 && qkv_in.call >= 0) {                // the group's Q|K|V MUL_MAT runs here
+                const float * tb = tab;
+                const QkvIn q = qkv_in;
+                plan->calls[q.call].run = [](const Plan &) { return (int)TSR_HIP_OK; };
+                c.run = [=](const Plan & pl) {
+                    const FaSlot & fs = pl.fa[slot];
+                    return tsr_hip_attn_qkv_plan_rope_tab(ctx, fs.plan, q.w, q.x, q.eps, q.nw, qkv, kc, vc, scale, nd, mode,
+                                                          tb, cells, nullptr, fs.general ? fs.mf32 : nullptr, (float *)op,
+                                                          os, s);
+                };
+            } else if (T == 1) {
                 const float * tb = tab;
                 c.run = [=](const Plan & pl) {
                     const FaSlot & fs = pl.fa[slot];
@@ -1753,11 +1777,16 @@ struct Lowerer {
                     *bad_node = i;
                     return false;
                 }
-                if (gr.attn) pending_qkv[group_mm[i]] = qkv_rows;
+                if (gr.attn) {
+                    pending_qkv[group_mm[i]] = qkv_rows;
+                    pending_in[group_mm[i]] = qkv_in;
+                    qkv_in = QkvIn{};
+                }
                 if (!gr.attn) continue;                        // the SWIGLU node is this call
             }
             if (group_fa[i] >= 0) {
                 qkv_rows = pending_qkv[group_fa[i]];
+                qkv_in = pending_in.count(group_fa[i]) ? pending_in[group_fa[i]] : QkvIn{};
                 if (!group_attn(g, groups[group_fa[i]])) {
                     *bad_node = i;
                     return false;
@@ -1793,6 +1822,7 @@ struct Lowerer {
         return true;
     }
     std::map<int, float *> pending_qkv;                     // group -> its Q|K|V rows (between the two emissions)
+    std::map<int, QkvIn> pending_in;                        // group -> its one-token Q|K|V MUL_MAT (to run inside)
 };
 
 Graph make_graph(const tsr_gg_dev * d, const tsr_gg_tensor * const * nodes, int n) {

@@ -31,6 +31,7 @@ MODE_UNDECIDED, MODE_LINEAR, MODE_WEIGHTS, MODE_KV = 0, 1, 2, 3
 CALL_NAMES = {CALL_MUL_MAT: "MUL_MAT", CALL_FLASH_ATTN: "FLASH_ATTN_EXT", CALL_SET_ROWS: "SET_ROWS",
               CALL_RMS_NORM: "RMS_NORM", CALL_ADD: "ADD", CALL_ROPE: "ROPE", CALL_SWIGLU: "SWIGLU",
               CALL_GET_ROWS: "GET_ROWS", CALL_ARGMAX: "ARGMAX", CALL_ROPE_TABLE: "ROPE_TABLE", CALL_ROPE_KV: "ROPE_KV"}
+CALL_IN_NEXT = 0x80000000    # flags: the call's work runs inside its group's FLASH_ATTN_EXT call
 
 EXPORTS = (
     "tsr_gg_open", "tsr_gg_close", "tsr_gg_last_error", "tsr_gg_hip_ctx", "tsr_gg_register_type",

@@ -309,8 +309,9 @@ def test_lower_llama_graph_unfused(T):
 def test_lower_llama_graph_fused(T):
     """The same graph lowered with its fusions: the decoder's launch list. One token, per layer: the
     Q|K|V matvec with the attention RMS_NORM folded in (its rows concatenated), one ROPE + SET_ROWS_KV +
-    FLASH_ATTN_EXT launch (the angle table once per graph), o + residual, gate|up with the FFN norm and
-    the SWIGLU epilogue, down + residual. A ubatch (T = 24): the norms stay calls (the matrix-core
+    FLASH_ATTN_EXT launch (the angle table once per graph; the Q|K|V matvec runs inside it, its call
+    marked CALL_IN_NEXT), o + residual, gate|up with the FFN norm and the SWIGLU epilogue, down +
+    residual. A ubatch (T = 24): the norms stay calls (the matrix-core
     MUL_MATs take no norm), the Q|K|V MUL_MAT, ROPE_KV, the planned FLASH_ATTN_EXT."""
     cfg = LL.tiny_config()
     p = Probe()
@@ -338,6 +339,9 @@ def test_lower_llama_graph_fused(T):
     glu = [c for c in mms if c["flags"] == tsr_hip.MM_GLU]
     assert len(qkv) == L and len(glu) == L
     assert all(c["y"] == 0 for c in qkv)                          # the plan's Q|K|V rows
+    # one token: the Q|K|V matvec (norm folded) runs inside its attention call
+    assert all(bool(c["flags"] & G.CALL_IN_NEXT) == (T == 1) for c in qkv)
+    assert not any(c["flags"] & G.CALL_IN_NEXT for c in calls if c not in qkv)
     for c in glu:
         assert c["N"] == 2 * cfg.n_ff and nodes[c["node"]].op == G.OP_GLU and c["y"] == nodes[c["node"]].data
     folded = [c for c in mms if c["node2"] >= 0 and nodes[c["node2"]].op == G.OP_RMS_NORM or c["node3"] >= 0]

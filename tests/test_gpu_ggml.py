@@ -41,7 +41,8 @@ def history_images(ref, cfg, hist):
     (LL.tiny_config("tiny-qwen", wfmt=H.FMT_Q8_0, ofmt=H.FMT_Q8_0, rope_mode=H.ROPE_NEOX, eps=1e-6,
                     rope_base=1000000.0), 640, 300, 4),
     (LL.tiny_config("tiny-gqa8", n_head=8, n_head_kv=1, head_dim=128, n_embd=512, n_ff=768, n_vocab=1000), 300, 250, 4),
-], ids=["q4k", "q80-neox", "gqa8-d128"])
+    (LL.tiny_config("tiny-kv8", n_head=16, n_head_kv=8, head_dim=64, n_embd=512, n_ff=768, n_vocab=1000), 300, 250, 4),
+], ids=["q4k", "q80-neox", "gqa8-d128", "q4k-kv8"])
 @pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
 def test_llama_decode_through_adapter(gdev, oc, cfg, kv_size, hist, n_steps, fused):
     """One decode token per graph_compute of llama.cpp's graph: the first run lowers and runs the calls,

@@ -380,6 +380,72 @@ def test_attn_qkv_plan_rope_tab(dev, oc, fmt, K, n_kv, pos, cell, n_head, n_head
     wt.free()
 
 
+def test_attn_qkv_plan_rope_tab_wait_expires(dev, oc):
+    """The attention launch with its Q|K|V rows, its bounded waits (the row workgroups' flags, the chunk
+    maxima, the reducers' polls) forced to expire from the host (a poll limit of 1): the launch still
+    ends and raises *bad = 2; the next launch with the default limit is bit-exact again (the flags carry
+    the launch's tag: nothing needs clearing)."""
+    import math
+    n_kv, pos, n_head, n_head_kv, D, K = 4232, 4100, 32, 8, 128, 4096
+    E, nq = n_head_kv * D, n_head * D
+    N = nq + 2 * E
+    k0 = np.zeros((n_kv, E // 32 * 34), np.uint8)
+    v0 = np.zeros_like(k0)
+    oc.kv_set_rows(k0, S.normal(31, n_kv * E).reshape(n_kv, E), np.arange(n_kv))
+    oc.kv_set_rows(v0, S.normal(32, n_kv * E).reshape(n_kv, E), np.arange(n_kv))
+    blocks = S.quant_rows(H.FMT_Q4_K, S.seed_of("attn-qkv-expire", "w"), N, K)
+    x = S.normal(33, K).reshape(1, K)
+    nw = (1.0 + 0.1 * S.normal(34, K)).astype(np.float32)
+    eps = 1e-5
+    row = oc.mul_mat(H.FMT_Q4_K, blocks, K, oc.rms_norm(x, eps, nw[None]), threads=8)
+    base = 500000.0
+    ts = theta_scale(base, D)
+    q = oc.rope(np.ascontiguousarray(row[:, :nq]), np.array([pos], np.int32), D, D, False, ts)
+    k = oc.rope(np.ascontiguousarray(row[:, nq:nq + E]), np.array([pos], np.int32), D, D, False, ts)
+    kw, vw = k0.copy(), v0.copy()
+    oc.kv_set_rows(kw, k, np.array([pos], np.int64))
+    oc.kv_set_rows(vw, np.ascontiguousarray(row[:, nq + E:]), np.array([pos], np.int64))
+    msum = np.zeros(12, np.uint32)
+    msum[0], msum[1], msum[2], msum[9] = 0x4D55534D, 1, n_kv, pos + 1
+    runs = np.array([[pos, pos + 1]], np.uint32)
+    scale = np.float32(1.0 / math.sqrt(D))
+    want = oc.flash_attn(q, kw, vw, D, n_head, n_head_kv, scale, msum, new_runs=runs)
+    wt = dev.weight(H.FMT_Q4_K, blocks, N, K)
+    kc, vc = dev.kv(E, n_kv), dev.kv(E, n_kv)
+    plan = dev.fa_plan(D, n_head, n_head_kv, 1, n_kv)
+    plan.set(msum, runs)
+    xb, nb, qkv = dev.upload(x), dev.upload(nw), dev.alloc(4 * N)
+    pb, cb = dev.upload(np.array([pos], np.int32)), dev.upload(np.array([pos], np.int64))
+    tab = dev.alloc(4 * D)
+    dev.rope_table(pb, D, base, tab)
+    expired = 0
+    try:
+        for limit in (1, 0, 1, 0):
+            kc.set_bytes(0, k0)
+            vc.set_bytes(1, v0)
+            bad, out = dev.upload(np.zeros(1, np.int32)), dev.alloc(4 * nq)
+            dev.set_fa_wait_limit(limit)
+            dev.attn_qkv_plan_rope_tab(plan, wt, xb, eps, nb, qkv, kc, vc, scale, D, H.ROPE_NORMAL, tab, cb, out, nq,
+                                       bad=bad)
+            dev.sync()
+            got_bad = int(bad.read(np.int32, (1,))[0])
+            assert got_bad in (0, 2), got_bad
+            if limit:
+                expired |= got_bad
+            else:
+                assert got_bad == 0
+                assert_bits_equal(qkv.read(np.float32, (1, N)), row, "Q|K|V row after an expired wait")
+                assert_bits_equal(out.read(np.float32, (1, nq)), want, "after an expired wait")
+                assert (kc.get_bytes(0).reshape(n_kv, -1) == kw).all()
+        assert expired == 2, "a poll limit of 1 never expired"
+    finally:
+        dev.set_fa_wait_limit(0)
+        plan.free()
+        kc.free()
+        vc.free()
+        wt.free()
+
+
 @pytest.mark.parametrize("pos,n_dims,m", [(0, 128, 1.0), (7, 64, 1.0), (4231, 128, 1.0), (131071, 128, 0.75),
                                           (-5, 8, 1.0), (1000, 2, 1.25)])
 def test_rope_table(dev, oc, pos, n_dims, m):

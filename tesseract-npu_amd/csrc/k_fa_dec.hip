@@ -129,19 +129,22 @@ __device__ __forceinline__ FaDecBlock fa_dec_block(const FaDecArgs & a) {
 constexpr uint32_t kDecLds = 256 + 512 + 64 + 128 + 16 + 128 + 16 + 4096 + 1024 + 1024 + 4096 + 48;
 
 // ---- the Q|K|V rows of the launch (FaDecArgs::qkv_w) ----------------------------------------------
-// Workgroup j of KV head g computes 16 rows of the Q|K|V MUL_MAT with the fused RMS_NORM + MUL: j < G D/16
-// the rows 16 j .. of its q heads, then its k head's, then its v head's, bit-identical to k_mv_q4k with
-// kPrepNorm (the same x preparation, A256 quantization, Q4_K terms and 16-partial tree). K <= 4096: one
+// Workgroup j of KV head g computes rows 24 j .. 24 j + 23 of the KV head's rows (its q heads', then its
+// k head's, then its v head's) of the Q|K|V MUL_MAT with the fused RMS_NORM + MUL, bit-identical to
+// k_mv_q4k with kPrepNorm (the same x preparation, A256 quantization, Q4_K terms and 16-partial tree).
+// 24 rows: (G + 2) D / 24 workgroups, one per compute unit of the XCD at the Llama-3-8B shape (with 16
+// rows, half the units held two and their quantization came ~1.5 us later). K <= 4096: one
 // super-block per (row, partial), so thread (wave v, lane 16 i + r) computes the term of super-block
 // 4 v + i of row r, which is the row's partial p[4 v + i] (+0 + term), and the thread holding x block
-// b = 4 v + i (16 values per lane) quantizes it. Its loads are issued at once: the norm weights and x,
-// then (after a bare barrier, so that every wave's x is ahead in the queue) its unit's 9 weight pieces
-// (from any row block of the weight's layout) and the epoch. The rows go to qkv_y
+// b = 4 v + i (16 values per lane) quantizes it; rows 16 .. 23 are a second unit of the threads of
+// waves 0 and 1, loaded once the first unit's registers are free. The first loads are issued at once:
+// the norm weights and x, then (after a bare barrier, so that every wave's x is ahead in the queue) the
+// unit's 9 weight pieces (from any row block of the weight's layout) and the epoch. The rows go to qkv_y
 // with plain stores (the XCD's L2); after they are complete (vmcnt) the workgroup raises its flag.
-// LDS (bytes): x quants [16][272] | sub-block sums [16][8] | scales [16] | partials [16][16] |
+// LDS (bytes): x quants [16][272] | sub-block sums [16][8] | scales [16] | partials [24][16] |
 // control 16 | squares [K].
-constexpr uint32_t kQkvMaxK = 4096;
-constexpr uint32_t kQkvLds = 16 * kXq4Stride + 16 * 8 * 4 + 16 * 4 + 16 * 16 * 4 + 16 + 4 * kQkvMaxK;
+constexpr uint32_t kQkvMaxK = 4096, kQkvRows = 24;
+constexpr uint32_t kQkvLds = 16 * kXq4Stride + 16 * 8 * 4 + 16 * 4 + kQkvRows * 16 * 4 + 16 + 4 * kQkvMaxK;
 
 template <int D>
 __device__ __forceinline__ void fa_qkv_rows(const FaDecArgs & a, uint8_t * lds, uint32_t j, uint32_t g) {
@@ -149,19 +152,24 @@ __device__ __forceinline__ void fa_qkv_rows(const FaDecArgs & a, uint8_t * lds, 
     int * s_xb = (int *)(lds + 16u * kXq4Stride);
     float * s_xd = (float *)(s_xb + 16u * 8u);
     float * s_p = s_xd + 16u;                                     // [row][partial]
-    uint32_t * s_ctl = (uint32_t *)(s_p + 256u);                  // halves of the RMS sum, tiny flag
+    uint32_t * s_ctl = (uint32_t *)(s_p + 16u * kQkvRows);        // halves of the RMS sum, tiny flag
     float * s_sq = (float *)(s_ctl + 4u);
     const uint32_t tid = threadIdx.x, lane = tid & 63u, v = tid >> 6;
     const uint32_t G = a.G, K = a.qkv_K, nsb = K >> 8;
     const WGeom wg = wgeom(a.qkv_N, nsb, a.qkv_rb, true);
-    const uint32_t jq = G * (D / 16u), jk = jq + D / 16u;
-    const uint32_t row0 = j < jq ? g * G * D + 16u * j
-                                 : a.n_head * D + (j < jk ? g * D + 16u * (j - jq) : a.E + g * D + 16u * (j - jk));
-    // x block b = 4 v + i (lane 16 i + l16: values 16 l16 .. + 15) and the unit (super-block b, row l16)
+    // the KV head's rows in order: its q heads', its k head's, its v head's; the weight row of each
+    const uint32_t nset = (G + 2u) * D;
+    auto wrow = [&](uint32_t r) -> uint32_t {
+        r = min(r, nset - 1u);
+        return r < G * D ? g * G * D + r : a.n_head * D + (r < (G + 1u) * D ? g * D + (r - G * D) : a.E + g * D + (r - (G + 1u) * D));
+    };
+    // x block b = 4 v + i (lane 16 i + l16: values 16 l16 .. + 15) and the first unit (super-block b,
+    // row l16 of the workgroup's 24)
     const uint32_t i4 = lane >> 4, l16 = lane & 15u, b = 4u * v + i4, bc = min(b, nsb - 1u);
     const bool has_w = a.qkv_pw != nullptr;
     const float * pl = has_w ? a.qkv_pw : a.qkv_x;                // without MUL: a valid address, unused
-    const uint32_t n = row0 + l16, B = n / wg.rb, rin = n - B * wg.rb, R = wl_rows(wg, B), sl = wl_slot_of(wg, bc);
+    const uint32_t r_0 = kQkvRows * j;
+    const uint32_t n = wrow(r_0 + l16), B = n / wg.rb, rin = n - B * wg.rb, R = wl_rows(wg, B), sl = wl_slot_of(wg, bc);
     float4 pv[4], xv[4];
 #pragma unroll
     for (uint32_t c = 0; c < 4u; ++c) pv[c] = *(const float4 *)(pl + 256u * bc + 16u * l16 + 4u * c);
@@ -223,31 +231,51 @@ __device__ __forceinline__ void fa_qkv_rows(const FaDecArgs & a, uint8_t * lds, 
     lds_barrier();
     const bool slow = s_ctl[2] != 0u;                             // some block has 0 < |Dx| < 2^-60
 
-    // the unit's term = partial p[b] of row l16 (+0 + term); partials of missing super-blocks are +0
-    int isum, msum;
-    q4k_unit_sums<8>(qv, mv, s_xq + bc * kXq4Stride, s_xb + bc * 8u, 0u, isum, msum);
-    const float dx = s_xd[bc];
-    const float dq = h2f_fast(mv.x & 0xFFFFu), dm = h2f_fast(mv.x >> 16);
-    float tt;
-    if (__builtin_expect(!slow, 1)) tt = 0.0f + ((dq * dx) * (float)isum - (dm * dx) * (float)msum);
-    else tt = sadd(0.0f, ssub(smul(smul(dq, dx), i2f(isum)), smul(smul(dm, dx), i2f(msum))));
-    s_p[16u * l16 + b] = b < nsb ? tt : 0.0f;
+    // a unit's term = partial p[s] of its row (+0 + term); partials of missing super-blocks are +0
+    auto term = [&](const uint4 (&q8)[8], const uint4 & m, uint32_t s) -> float {
+        const uint32_t sc = min(s, nsb - 1u);
+        int isum, msum;
+        q4k_unit_sums<8>(q8, m, s_xq + sc * kXq4Stride, s_xb + sc * 8u, 0u, isum, msum);
+        const float dx = s_xd[sc];
+        const float dq = h2f_fast(m.x & 0xFFFFu), dm = h2f_fast(m.x >> 16);
+        float tt;
+        if (__builtin_expect(!slow, 1)) tt = 0.0f + ((dq * dx) * (float)isum - (dm * dx) * (float)msum);
+        else tt = sadd(0.0f, ssub(smul(smul(dq, dx), i2f(isum)), smul(smul(dm, dx), i2f(msum))));
+        return s < nsb ? tt : 0.0f;
+    };
+    s_p[16u * l16 + b] = term(qv, mv, b);
+    // the second unit of waves 0 and 1 (thread t < 128: super-block t / 8, row 16 + t % 8), loaded into
+    // the first unit's registers once those are free
+    if (v < 2u) {
+        const uint32_t b2 = tid >> 3, r2 = 16u + (tid & 7u);
+        const uint32_t n2 = wrow(r_0 + r2), B2 = n2 / wg.rb, rin2 = n2 - B2 * wg.rb, R2 = wl_rows(wg, B2);
+        const uint32_t sl2 = wl_slot_of(wg, min(b2, nsb - 1u));
+#pragma unroll
+        for (uint32_t jj = 0; jj < 8u; ++jj) qv[jj] = *(const uint4 *)(a.qkv_w + wl_quant_off(wg, B2, R2, jj, sl2, rin2));
+        const uint4 mv2 = *(const uint4 *)(a.qkv_w + wl_meta_off(wg, B2, R2, sl2, rin2));
+        s_p[16u * r2 + b2] = term(qv, mv2, b2);
+    }
     lds_barrier();
-    // the 16-partial tree of row tid / 16 (lane i of the 16-lane row holds p[i])
-    float y = s_p[tid];
-    if (__builtin_expect(!slow, 1)) {
-        y = y + dpp_f<kDppXor1>(y);
-        y = y + dpp_f<kDppXor2>(y);
-        y = y + dpp_f<kDppRowHalfMirror>(y);
-        y = y + dpp_f<kDppRowMirror>(y);
-        y = canon(y);
-    } else {
+    // the 16-partial tree of each row (lane i of a 16-lane row holds p[i]): rows 0..15, then 16..23
+    auto tree = [&](float y) -> float {
+        if (__builtin_expect(!slow, 1)) {
+            y = y + dpp_f<kDppXor1>(y);
+            y = y + dpp_f<kDppXor2>(y);
+            y = y + dpp_f<kDppRowHalfMirror>(y);
+            y = y + dpp_f<kDppRowMirror>(y);
+            return canon(y);
+        }
         y = sadd(y, dpp_f<kDppXor1>(y));
         y = sadd(y, dpp_f<kDppXor2>(y));
         y = sadd(y, dpp_f<kDppRowHalfMirror>(y));
-        y = sadd(y, dpp_f<kDppRowMirror>(y));
+        return sadd(y, dpp_f<kDppRowMirror>(y));
+    };
+    const float y1 = tree(s_p[tid]);
+    if ((tid & 15u) == 0u && r_0 + (tid >> 4) < nset) a.qkv_y[wrow(r_0 + (tid >> 4))] = y1;
+    if (v < 2u) {
+        const float y2 = tree(s_p[256u + tid]);
+        if ((tid & 15u) == 0u && r_0 + 16u + (tid >> 4) < nset) a.qkv_y[wrow(r_0 + 16u + (tid >> 4))] = y2;
     }
-    if ((tid & 15u) == 0u) a.qkv_y[row0 + (tid >> 4)] = y;
     vm_wait();                                                    // the rows are in the L2
     lds_barrier();
     if (tid == 0u) {

@@ -162,7 +162,7 @@ struct FaDecArgs {
     float ts, m;
     ExpkTab ex;
     // The token's Q|K|V row computed in the same launch (qkv_w != 0; ROPE, one XCD per KV head): nq
-    // workgroups per KV head, first in dispatch order, each compute 16 of the KV head's rows (its q
+    // workgroups per KV head, first in dispatch order, each compute 24 of the KV head's rows (its q
     // heads, then its k and v heads) of MUL_MAT(W, RMS_NORM(x) * pw) into qkv_y (== q) and raise a
     // flag with the launch's tag; the segments read q after every flag of their KV head is up
     const uint8_t * qkv_w;   // Q4_K weight layout (wlayout.hpp): qkv_N = (n_head + 2 n_head_kv) D rows of qkv_K

@@ -736,7 +736,7 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
         d.ep = (uint32_t *)(plan->dev + plan->o_EP);
         d.spin_max = ctx->fa_spin_max;
         d.n_xcd = ctx->n_xcd;
-        if (qkv != nullptr) {                                // 16 rows per workgroup, first in dispatch order
+        if (qkv != nullptr) {                                // 24 rows per workgroup, first in dispatch order
             d.qkv_w = qkv->w->dev;
             d.qkv_x = qkv->x;
             d.qkv_pw = qkv->pw;
@@ -745,7 +745,7 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
             d.qkv_N = qkv->w->N;
             d.qkv_K = qkv->w->K;
             d.qkv_rb = qkv->w->rb;
-            d.nq = (G + 2u) * plan->D / 16u;
+            d.nq = ((G + 2u) * plan->D + 23u) / 24u;
             d.qkv_eps = qkv->eps;
             d.qkv_inv_n = 1.0f / (float)qkv->w->K;          // correctly rounded (IEEE division), as the matvec's
         }
@@ -890,7 +890,7 @@ int tsr_hip_attn_qkv_plan_rope_tab(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * pl
                      // the workgroups with work resident at once (4 per CU); with more, the row workgroups
                      // hold slots that segments need (measured: 8208 cells 24.8 -> 26.3 us, 4136 cells
                      // 20.1 -> 18.9 us)
-                     ((uint64_t)plan->seg_work + G * (D / 64u) + (G + 2u) * D / 16u) * nkv <= 4u * (uint64_t)ctx->n_cu;
+                     ((uint64_t)plan->seg_work + G * (D / 64u) + ((G + 2u) * D + 23u) / 24u) * nkv <= 4u * (uint64_t)ctx->n_cu;
     if (!one) {                                                   // the two records, two launches
         rc = tsr_hip_mul_mat_norm(ctx, w_qkv, x_dev, 1u, K, eps, norm_w_dev, qkv_dev, w_qkv->N, nullptr, 0u, 0u, stream);
         if (rc) return rc;

@@ -236,7 +236,7 @@ int tsr_hip_flash_attn_plan_rope_tab(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * 
  * MUL_MAT, ROPE, SET_ROWS_KV and FLASH_ATTN_EXT records of sw/ctrl/tests/test_fw_m7_layer.cpp:646-686.
  * qkv_dev receives the unrotated Q|K|V row as the MUL_MAT writes it. When the one-launch decode form
  * places each KV head's workgroups on one XCD (n_head_kv a multiple of the device's XCD count), its
- * workgroups with work fit the device at once (4 per compute unit: at the Llama-3-8B shape up to ~4.5 K
+ * workgroups with work fit the device at once (4 per compute unit: at the Llama-3-8B shape up to ~5.4 K
  * cells), w_qkv is Q4_K with K <= 4096 and the buffers are 16-byte aligned, it is one launch: workgroups of the launch
  * compute each KV head's Q|K|V rows on that head's XCD while its segments load K. Otherwise the two
  * calls run. w_qkv: N = (n_head + 2 n_head_kv) D rows of K = the x row's length; x_dev and qkv_dev must

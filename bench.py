@@ -515,6 +515,16 @@ def extra_workloads(dev, ev, stream, n: int, eager: bool = False) -> dict:
     # the planned entry point (the decode form: one launch, k_fa_dec), the plan set once for the mask
     plan = dev.fa_plan(D, n_head, n_kv_head, 1, n_kv)
     plan.set(msum)
+    # outside the timed loops: the planned launch's bits against the unplanned entry point's (both bit-exact
+    # against the oracle in the GPU tests)
+    dev.flash_attn_plan(plan, qb, n_head * D, k0, v0, scale, ob, n_head * D, stream=stream)
+    dev.sync(stream)
+    planned_out = ob.read(np.float32, (n_head * D,))
+    dev.flash_attn(qb, 1, n_head * D, k0, v0, D, n_head, n_kv_head, scale, msum, ob, n_head * D, stream=stream)
+    dev.sync(stream)
+    planned_equal = bool((planned_out.view(np.uint32) == ob.read(np.float32, (n_head * D,)).view(np.uint32)).all())
+    if not planned_equal:
+        raise SystemExit("bench: the planned FLASH_ATTN_EXT launch differs from the unplanned entry point")
     ms, ms_eager = timed(lambda i: dev.flash_attn_plan(plan, qb, n_head * D, caches[i % copies][0], caches[i % copies][1],
                                                        scale, ob, n_head * D, stream=stream))
     # the unplanned entry point (work list planned per call on the host: QK, P.V and merge launches)
@@ -526,7 +536,8 @@ def extra_workloads(dev, ev, stream, n: int, eager: bool = False) -> dict:
                                               "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                               "copies": copies, "launches_per_call": 1, "kernel": "k_fa_dec",
                                               "unplanned_us_per_call": round(ms3 * 1e3, 3),
-                                              "unplanned_launches_per_call": 3}
+                                              "unplanned_launches_per_call": 3,
+                                              "planned_bits_equal_unplanned": planned_equal}
     plan.free()
     del caches
 

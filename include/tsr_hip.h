@@ -196,8 +196,10 @@ int tsr_hip_rope_kv(tsr_hip_ctx * ctx, float * qkv_dev, uint32_t T, uint64_t str
  *   create   for T query rows of D / n_head / n_head_kv over caches of at most kv_size cells
  *   set      plans the MSUM (and new_runs, as tsr_hip_flash_attn) on the host and copies the list to
  *            the device in stream order (not under capture). *shape_changed = 1 when the list's shape
- *            (items, tiles per item, groups per item, GENERAL) differs from the previous set: launches
- *            captured before then must be captured again. mask_f32 != 0: an f32 mask copy will be given.
+ *            (items, tiles per item, groups per item, GENERAL, and for one query row whether the
+ *            workgroups of tsr_hip_attn_qkv_plan_rope_tab's one launch fit the device at once) differs
+ *            from the previous set: launches captured before then must be captured again.
+ *            mask_f32 != 0: an f32 mask copy will be given.
  *   flash_attn_plan  FLASH_ATTN_EXT with the plan's current list (capturable; numerics as
  *            tsr_hip_flash_attn). The plan's partials live in the plan: launches that use one plan run
  *            in stream order, one at a time. */
@@ -239,7 +241,11 @@ int tsr_hip_flash_attn_plan_rope_tab(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * 
  * workgroups with work fit the device at once (4 per compute unit: at the Llama-3-8B shape up to ~5.4 K
  * cells), w_qkv is Q4_K with K <= 4096 and the buffers are 16-byte aligned, it is one launch: workgroups of the launch
  * compute each KV head's Q|K|V rows on that head's XCD while its segments load K. Otherwise the two
- * calls run. w_qkv: N = (n_head + 2 n_head_kv) D rows of K = the x row's length; x_dev and qkv_dev must
+ * calls run; so do they when out_dev overlaps x_dev or norm_w_dev (in one launch a KV head's reducers
+ * write out_dev while other heads' row workgroups still read x and the norm weights). Whether the form
+ * fits is decided per tsr_hip_fa_plan_set: its *shape_changed is 1 when the decision flips, so that a
+ * captured launch is captured again. tsr_hip_counters.fa_dec_qkv_launches counts the one-launch calls.
+ * w_qkv: N = (n_head + 2 n_head_kv) D rows of K = the x row's length; x_dev and qkv_dev must
  * not overlap. Shapes and errors otherwise as the two calls. (No counterpart in the reference: its
  * records run one after another.) */
 int tsr_hip_attn_qkv_plan_rope_tab(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const tsr_hip_weight * w_qkv,
@@ -257,6 +263,11 @@ int tsr_hip_fa_plan_free(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan);
  * XCD (the dispatcher's round-robin) and exchange through its L2; a workgroup found on another XCD
  * raises *bad_dev |= 4 (results not valid). bad_dev is the argument of the _rope entry points. */
 int tsr_hip_set_fa_wait_limit(tsr_hip_ctx * ctx, uint32_t polls);
+/* Test hook (no counterpart in the reference): sets every KV head's epoch word of the plan's one-launch
+ * decode form to `epoch` (stream-ordered on the context's stream, not under capture), so that a test
+ * reaches the tag wrap (epoch 2^28 - 1 -> tag 1; a launch's tag is never 0, the value of plan memory no
+ * launch has written) without 2^28 launches. */
+int tsr_hip_fa_plan_set_epoch(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan, uint32_t epoch);
 
 /* ---- graphs -------------------------------------------------------------------------------------
  * Every launch the library makes on `stream` between begin and end is recorded (stream capture) and
@@ -385,10 +396,14 @@ int tsr_hip_argmax(tsr_hip_ctx * ctx, const float * x_dev, uint32_t n, uint32_t 
 int tsr_hip_get_flags(tsr_hip_ctx * ctx, int32_t * flags, int clear);
 
 /* ---- counters (the backend's TSR_STATS report, ggml-tesseract.cpp:3799-3866) --------------------- */
+/* fa_dec_launches: planned FLASH_ATTN_EXT calls that ran as the one-launch decode form (k_fa_dec);
+ * fa_dec_qkv_launches: those of them that also computed the layer's Q|K|V rows
+ * (tsr_hip_attn_qkv_plan_rope_tab in one launch rather than its two-call fallback). */
 typedef struct tsr_hip_counters {
     uint64_t mul_mat_calls, mul_mat_rows, mul_mat_weight_bytes;
     uint64_t flash_attn_calls, flash_attn_kv_bytes;
     uint64_t set_rows_calls, qact_calls;
+    uint64_t fa_dec_launches, fa_dec_qkv_launches;
 } tsr_hip_counters;
 int tsr_hip_get_counters(tsr_hip_ctx * ctx, tsr_hip_counters * out);
 

@@ -62,11 +62,16 @@ __device__ __forceinline__ void st_co16(__amdgpu_buffer_rsrc_t r, uint32_t off, 
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_fa, v), r, off, 0, LOCAL ? 0 : kSc1);
 }
 
-// Tags: the low 28 bits are the launch's epoch + 1 (mod 2^28), the high 4 bits the writer's XCD, so a
-// reader checks in the same word that a value is this launch's and, in the LOCAL form, that its writer
-// shared its XCD (and so its L2).
+// Tags: the low 28 bits are the launch's tag, the high 4 bits the writer's XCD, so a reader checks in the
+// same word that a value is this launch's and, in the LOCAL form, that its writer shared its XCD (and so
+// its L2). A launch's tag follows its KV head's epoch: epoch + 1, wrapping from 2^28 - 1 to 1, never 0,
+// the tag field of plan memory no launch has written yet (the plan is zeroed at creation).
 constexpr uint32_t kTagMask = 0x0FFFFFFFu;
 __device__ __forceinline__ bool tag_is(uint32_t t, uint32_t tag) { return (t & kTagMask) == tag; }
+__device__ __forceinline__ uint32_t tag_after(uint32_t epoch) {
+    const uint32_t t = (epoch & kTagMask) + 1u;
+    return t > kTagMask ? 1u : t;
+}
 
 // A result with the launch's tag in one 8-byte agent-coherent store (a reader sees both or neither) and
 // its load.
@@ -184,7 +189,7 @@ __device__ __forceinline__ void fa_qkv_rows(const FaDecArgs & a, uint8_t * lds, 
 #pragma unroll
     for (uint32_t jj = 0; jj < 8u; ++jj) qv[jj] = *(const uint4 *)(a.qkv_w + wl_quant_off(wg, B, R, jj, sl, rin));
     const uint4 mv = *(const uint4 *)(a.qkv_w + wl_meta_off(wg, B, R, sl, rin));
-    const uint32_t epv = a.ep[(size_t)g * G * (D / 64u)];         // the launch's tag: epoch + 1
+    const uint32_t epv = a.ep[(size_t)g * G * (D / 64u)];         // the epoch the launch's tag follows
     __builtin_amdgcn_sched_barrier(0);
 
     // RMS_NORM: the squares, the two halves of the 128 ordered partials on waves 0 and 1, the scale
@@ -279,7 +284,7 @@ __device__ __forceinline__ void fa_qkv_rows(const FaDecArgs & a, uint8_t * lds, 
     vm_wait();                                                    // the rows are in the L2
     lds_barrier();
     if (tid == 0u) {
-        const uint32_t tagw = ((epv + 1u) & kTagMask) | (xcc_id() << 28);
+        const uint32_t tagw = tag_after(epv) | (xcc_id() << 28);
         __hip_atomic_store(a.qkv_flag + (size_t)g * 64u + j, tagw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
 }
@@ -389,7 +394,7 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     // what this workgroup writes carries its XCD in the tag's high bits (read here, after the loads
     // above: the register read is a volatile asm, which no load is scheduled across)
     const uint32_t xcc = xcc_id();
-    const uint32_t tag = (epv + 1u) & kTagMask, tagw = tag | (xcc << 28);
+    const uint32_t tag = tag_after(epv), tagw = tag | (xcc << 28);
 
     // ---- the work item; the segment's K requested (ROPE and QACT below run while it flies) ----
     FaItem it;
@@ -731,7 +736,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
     const uint32_t r = ri / NVP, vp = ri % NVP, hh = g * G + r;
     const uint32_t c = tid >> 6, v = 64u * vp + lane;             // channel c, value v
     uint32_t * ep = a.ep + (size_t)g * G * NVP + ri;              // this reducer's epoch of the KV head
-    const uint32_t tag = (*ep + 1u) & kTagMask, xcc = xcc_id();
+    const uint32_t tag = tag_after(*ep), xcc = xcc_id();
     s_t64[lane] = a.ex.t64[lane];
     for (uint32_t k = tid; k < ni; k += blockDim.x) {
         const FaItem ik = a.items[k];

@@ -561,6 +561,7 @@ struct tsr_hip_fa_plan {
     bool set = false, general = false;
     uint32_t n_items = 0, maxtiles = 0, max_groups = 0, mstride = 0;   // the shape a launch bakes in
     uint32_t seg_work = 0;   // the decode form's segments with work (64 cells of one channel) per KV head
+    bool qkv_fits = false;   // tsr_hip_attn_qkv_plan_rope_tab's one launch fits the device at once
     uint64_t cells = 0;
 };
 
@@ -633,6 +634,19 @@ int tsr_hip_set_fa_wait_limit(tsr_hip_ctx * ctx, uint32_t polls) {
     return TSR_HIP_OK;
 }
 
+int tsr_hip_fa_plan_set_epoch(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan, uint32_t epoch) {
+    if (ctx == nullptr || plan == nullptr) return TSR_HIP_E_ARG;
+    if (plan->T != 1u) return TSR_HIP_E_SHAPE;
+    std::vector<uint32_t> words(8u * (size_t)plan->n_head_kv, epoch);
+    std::lock_guard<std::mutex> lk(ctx->mtx);
+    (void)hipSetDevice(ctx->device);
+    hipStream_t s = ctx->pick(nullptr);
+    if (tsr_capturing(s)) return TSR_HIP_E_ARG;
+    int rc = ctx->staging.copy(plan->dev + plan->o_EP, words.data(), 4u * words.size(), s);
+    if (rc) return rc;
+    return hip_err(hipStreamSynchronize(s), "fa plan epoch");
+}
+
 int tsr_hip_fa_plan_free(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan) {
     if (ctx == nullptr || plan == nullptr) return TSR_HIP_E_ARG;
     std::lock_guard<std::mutex> lk(ctx->mtx);
@@ -659,9 +673,23 @@ int tsr_hip_fa_plan_set(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan, const uint32_
     bool general = false;
     for (const tsr::FaItem & it : w.items) general |= it.general != 0u;
     const uint32_t mstride = 16u * ((msum[2] + 15u) / 16u);
+    uint32_t seg_work = 0u;
+    for (const tsr::FaItem & it : w.items)
+        for (uint32_t c = 0; c < 4u; ++c) {                     // k_fa_dec.hip FaSeg: channel c's groups
+            const uint32_t uf = it.u0 + ((c + 4u - (it.u0 & 3u)) & 3u), ue = it.u0 + it.n;
+            const uint32_t nu = uf < ue ? (ue - 1u - uf) / 4u + 1u : 0u;
+            seg_work += (nu + 3u) / 4u;
+        }
+    // the one launch of the Q|K|V rows + attention: the workgroups with work resident at once (4 per
+    // CU); with more, the row workgroups hold slots that segments need (measured at the Llama-3-8B
+    // shape: 8208 cells 24.8 -> 26.3 us in one launch, 4136 cells 20.1 -> 18.9 us)
+    const uint32_t D = plan->D, nkv = plan->n_head_kv, G = plan->n_head / nkv;
+    const bool qkv_fits = T == 1u && ctx->n_cu > 0 &&
+                          ((uint64_t)seg_work + G * (D / 64u) + ((G + 2u) * D + 23u) / 24u) * nkv <=
+                              4u * (uint64_t)ctx->n_cu;
     const bool changed = !plan->set || n_items != plan->n_items || w.maxtiles != plan->maxtiles ||
                          w.max_groups != plan->max_groups || (general && mstride != plan->mstride) ||
-                         general != plan->general;
+                         general != plan->general || qkv_fits != plan->qkv_fits;
     std::lock_guard<std::mutex> lk(ctx->mtx);
     (void)hipSetDevice(ctx->device);
     hipStream_t s = ctx->pick(stream);
@@ -676,13 +704,8 @@ int tsr_hip_fa_plan_set(tsr_hip_ctx * ctx, tsr_hip_fa_plan * plan, const uint32_
     plan->mstride = mstride;
     plan->general = general;
     plan->cells = w.cells;
-    plan->seg_work = 0u;
-    for (const tsr::FaItem & it : w.items)
-        for (uint32_t c = 0; c < 4u; ++c) {                     // k_fa_dec.hip FaSeg: channel c's groups
-            const uint32_t uf = it.u0 + ((c + 4u - (it.u0 & 3u)) & 3u), ue = it.u0 + it.n;
-            const uint32_t nu = uf < ue ? (ue - 1u - uf) / 4u + 1u : 0u;
-            plan->seg_work += (nu + 3u) / 4u;
-        }
+    plan->seg_work = seg_work;
+    plan->qkv_fits = qkv_fits;
     if (shape_changed) *shape_changed = changed ? 1 : 0;
     return TSR_HIP_OK;
 }
@@ -770,9 +793,11 @@ static int fa_plan_launch(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * plan, const
         std::lock_guard<std::mutex> lk(ctx->mtx);
         (void)hipSetDevice(ctx->device);
         ctx->ctr.flash_attn_calls++;
+        ctx->ctr.fa_dec_launches++;
         ctx->ctr.flash_attn_kv_bytes += plan->cells * (uint64_t)E / 32u * 34u * 2u;
         if (rope != nullptr) ctx->ctr.set_rows_calls += 2u;
         if (qkv != nullptr) {
+            ctx->ctr.fa_dec_qkv_launches++;
             ctx->ctr.mul_mat_calls++;
             ctx->ctr.mul_mat_rows += qkv->w->N;
             ctx->ctr.mul_mat_weight_bytes += (uint64_t)qkv->w->N * (qkv->w->K / 256u) * 144u;
@@ -881,16 +906,19 @@ int tsr_hip_attn_qkv_plan_rope_tab(tsr_hip_ctx * ctx, const tsr_hip_fa_plan * pl
     if (rc) return rc;
     r.rtab = tab_dev;
     const uint32_t K = w_qkv->K;
-    const bool apart = (uintptr_t)qkv_dev + 4u * (size_t)w_qkv->N <= (uintptr_t)x_dev ||
-                           (uintptr_t)x_dev + 4u * (size_t)K <= (uintptr_t)qkv_dev;
+    // byte ranges that the one launch reads (x, the norm weights) while it writes others (the Q|K|V row,
+    // the attention output of KV heads that finished): apart, or the two calls run
+    auto apart = [](const void * a, size_t na, const void * b, size_t nb) {
+        return a == nullptr || b == nullptr || (uintptr_t)a + na <= (uintptr_t)b || (uintptr_t)b + nb <= (uintptr_t)a;
+    };
+    const size_t out_span = 4u * (size_t)plan->n_head * D;
+    const bool disjoint = apart(qkv_dev, 4u * (size_t)w_qkv->N, x_dev, 4u * (size_t)K) &&
+                          apart(out_dev, out_span, x_dev, 4u * (size_t)K) &&
+                          apart(out_dev, out_span, norm_w_dev, 4u * (size_t)K);
     const bool one = plan->set && !(plan->general && mask_f32_dev == nullptr) && G <= 4u && plan->n_items <= 256u &&
                      ctx->n_xcd != 0u && nkv % ctx->n_xcd == 0u && w_qkv->fmt == TSR_HIP_FMT_Q4_K && K % 256u == 0u &&
                      K <= 4096u && aligned16(x_dev) && (norm_w_dev == nullptr || aligned16(norm_w_dev)) &&
-                     aligned16(qkv_dev) && apart &&
-                     // the workgroups with work resident at once (4 per CU); with more, the row workgroups
-                     // hold slots that segments need (measured: 8208 cells 24.8 -> 26.3 us, 4136 cells
-                     // 20.1 -> 18.9 us)
-                     ((uint64_t)plan->seg_work + G * (D / 64u) + ((G + 2u) * D + 23u) / 24u) * nkv <= 4u * (uint64_t)ctx->n_cu;
+                     aligned16(qkv_dev) && disjoint && plan->qkv_fits;
     if (!one) {                                                   // the two records, two launches
         rc = tsr_hip_mul_mat_norm(ctx, w_qkv, x_dev, 1u, K, eps, norm_w_dev, qkv_dev, w_qkv->N, nullptr, 0u, 0u, stream);
         if (rc) return rc;

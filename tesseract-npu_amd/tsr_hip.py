@@ -38,6 +38,7 @@ EXPORTS = (
     "tsr_hip_mul_mat_norm", "tsr_hip_rope_kv", "tsr_hip_flash_attn_plan_rope", "tsr_hip_rope_table",
     "tsr_hip_flash_attn_plan_rope_tab", "tsr_hip_mul_mat_epi", "tsr_hip_set_fa_wait_limit",
     "tsr_hip_flash_attn_noalloc", "tsr_hip_get_flags", "tsr_hip_msum_mask_f32", "tsr_hip_attn_qkv_plan_rope_tab",
+    "tsr_hip_fa_plan_set_epoch",
 )
 
 
@@ -117,6 +118,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "tsr_hip_rope_table": ([vp, vp, u32, C.c_float, C.c_float, vp, vp], C.c_int),
         "tsr_hip_mul_mat_epi": ([vp, vp, vp, u32, u64, vp, u64, vp, u64, u32, C.c_float, C.c_float, vp], C.c_int),
         "tsr_hip_set_fa_wait_limit": ([vp, u32], C.c_int),
+        "tsr_hip_fa_plan_set_epoch": ([vp, vp, u32], C.c_int),
         "tsr_hip_flash_attn_plan_rope_tab": ([vp, vp, vp, vp, vp, C.c_float, u32, C.c_int, vp, vp, vp, vp, vp, u64, vp],
                                              C.c_int),
         "tsr_hip_attn_qkv_plan_rope_tab": ([vp, vp, vp, vp, C.c_float, vp, vp, vp, vp, C.c_float, u32, C.c_int, vp, vp,
@@ -287,6 +289,11 @@ class FaPlan:
                                               C.byref(ch), stream), "fa_plan_set")
         return bool(ch.value)
 
+    def set_epoch(self, epoch: int) -> None:
+        """Test hook: every KV head's epoch word of the one-launch decode form (the next launch's tag
+        follows it)."""
+        _check(self.dev.L.tsr_hip_fa_plan_set_epoch(self.dev.ctx, self.h, epoch), "fa_plan_set_epoch")
+
     def free(self) -> None:
         if self.h:
             self.dev.L.tsr_hip_fa_plan_free(self.dev.ctx, self.h)
@@ -355,10 +362,10 @@ class Device:
         return {"n_cu": n.value, "arch": name.value.decode(), "mem_free": f.value, "mem_total": t.value}
 
     def counters(self) -> dict:
-        buf = (C.c_uint64 * 7)()
-        _check(self.L.tsr_hip_get_counters(self.ctx, buf), "get_counters")
         keys = ("mul_mat_calls", "mul_mat_rows", "mul_mat_weight_bytes", "flash_attn_calls", "flash_attn_kv_bytes",
-                "set_rows_calls", "qact_calls")
+                "set_rows_calls", "qact_calls", "fa_dec_launches", "fa_dec_qkv_launches")
+        buf = (C.c_uint64 * len(keys))()
+        _check(self.L.tsr_hip_get_counters(self.ctx, buf), "get_counters")
         return dict(zip(keys, list(buf)))
 
     # -- buffers ---------------------------------------------------------------------------------

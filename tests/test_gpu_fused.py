@@ -203,6 +203,9 @@ def test_rope_kv_bad_cell(dev, oc):
     (640, 600, 600, 64, 8, 64, H.ROPE_NORMAL, 64, False),         # G = 8: the three-launch form
     (4232, 5000, 100, 32, 8, 128, H.ROPE_NORMAL, 128, "swa"),     # wrapped sliding window over a full ring:
     (1500, 3000, 700, 12, 4, 64, H.ROPE_NEOX, 64, "swa"),         #   runs [0, cell] and [lo, n_kv), two FAST runs
+    (8192, 8191, 8191, 32, 8, 128, H.ROPE_NORMAL, 128, False),    # 4 chunks: the reducers' two rounds
+    (13000, 12999, 12999, 32, 8, 128, H.ROPE_NEOX, 128, False),   # 7 chunks: three rounds
+    (8208, 8200, 8200, 32, 8, 128, H.ROPE_NORMAL, 128, True),     # GENERAL mask over 5 chunks
 ], ids=lambda v: str(v))
 def test_flash_attn_plan_rope(dev, oc, n_kv, pos, cell, n_head, n_head_kv, D, mode, n_dims, general):
     """tsr_hip_flash_attn_plan_rope against the oracle's ROPE of q and k, SET_ROWS_KV of k and v and
@@ -282,21 +285,24 @@ def test_flash_attn_plan_rope(dev, oc, n_kv, pos, cell, n_head, n_head_kv, D, mo
     vc.free()
 
 
-@pytest.mark.parametrize("fmt,K,n_kv,pos,cell,n_head,n_head_kv,D,mode,n_dims,general", [
-    (H.FMT_Q4_K, 4096, 4232, 4200, 4200, 32, 8, 128, H.ROPE_NORMAL, 128, False),   # Llama-3-8B decode layer
-    (H.FMT_Q4_K, 4096, 4232, 5000, 100, 32, 8, 128, H.ROPE_NEOX, 128, "swa"),      # wrapped window, new cell 100
-    (H.FMT_Q4_K, 2048, 2100, 2090, 2068, 16, 8, 128, H.ROPE_NEOX, 64, False),      # G = 2
-    (H.FMT_Q4_K, 1024, 1500, 1400, 1400, 8, 8, 64, H.ROPE_NORMAL, 64, True),       # G = 1, GENERAL mask, D 64
-    (H.FMT_Q4_K, 768, 640, 600, 600, 24, 8, 64, H.ROPE_NEOX, 64, False),           # 3 super-blocks, G = 3
-    (H.FMT_Q4_K, 1024, 1500, 1400, 1400, 12, 4, 64, H.ROPE_NORMAL, 32, False),     # 4 KV heads: two launches
-    (H.FMT_Q4_K, 8192, 300, 257, 257, 32, 8, 128, H.ROPE_NORMAL, 128, False),      # K > 4096: two launches
-    (H.FMT_Q8_0, 1024, 300, 257, 257, 16, 8, 64, H.ROPE_NEOX, 64, False),          # Q8_0: two launches
+@pytest.mark.parametrize("fmt,K,n_kv,pos,cell,n_head,n_head_kv,D,mode,n_dims,general,one", [
+    (H.FMT_Q4_K, 4096, 4232, 4200, 4200, 32, 8, 128, H.ROPE_NORMAL, 128, False, True),   # Llama-3-8B decode layer
+    (H.FMT_Q4_K, 4096, 4232, 5000, 100, 32, 8, 128, H.ROPE_NEOX, 128, "swa", True),      # wrapped window, new cell 100
+    (H.FMT_Q4_K, 2048, 2100, 2090, 2068, 16, 8, 128, H.ROPE_NEOX, 64, False, True),      # G = 2
+    (H.FMT_Q4_K, 1024, 1500, 1400, 1400, 8, 8, 64, H.ROPE_NORMAL, 64, True, True),       # G = 1, GENERAL mask, D 64
+    (H.FMT_Q4_K, 768, 640, 600, 600, 24, 8, 64, H.ROPE_NEOX, 64, False, True),           # 3 super-blocks, G = 3
+    (H.FMT_Q4_K, 1024, 1500, 1400, 1400, 12, 4, 64, H.ROPE_NORMAL, 32, False, False),    # 4 KV heads: two launches
+    (H.FMT_Q4_K, 8192, 300, 257, 257, 32, 8, 128, H.ROPE_NORMAL, 128, False, False),     # K > 4096: two launches
+    (H.FMT_Q8_0, 1024, 300, 257, 257, 16, 8, 64, H.ROPE_NEOX, 64, False, False),         # Q8_0: two launches
+    (H.FMT_Q4_K, 4096, 8208, 8200, 8200, 32, 8, 128, H.ROPE_NORMAL, 128, False, False),  # beyond residency: two
+    (H.FMT_Q4_K, 4096, 5300, 5299, 5299, 32, 8, 128, H.ROPE_NEOX, 128, False, True),     # near the residency bound
 ], ids=lambda v: str(v))
-def test_attn_qkv_plan_rope_tab(dev, oc, fmt, K, n_kv, pos, cell, n_head, n_head_kv, D, mode, n_dims, general):
+def test_attn_qkv_plan_rope_tab(dev, oc, fmt, K, n_kv, pos, cell, n_head, n_head_kv, D, mode, n_dims, general, one):
     """tsr_hip_attn_qkv_plan_rope_tab against the oracle's RMS_NORM + MUL, Q|K|V MUL_MAT, ROPE,
     SET_ROWS_KV and FLASH_ATTN_EXT of one decode token (the Q|K|V row, the output and both caches),
     twice on one plan (the second launch tags with the next epoch), and against the two calls it
-    replaces."""
+    replaces. `one`: whether the one-launch form is expected to run (the counter of such launches says
+    which ran; its two-call fallback gives the same bits)."""
     import math
     print(f"\nattn_qkv_plan_rope_tab fmt {fmt} K {K} n_kv {n_kv} pos {pos} cell {cell} heads {n_head}/{n_head_kv} "
           f"D {D} mode {mode} n_dims {n_dims} general {general}", flush=True)
@@ -359,8 +365,11 @@ def test_attn_qkv_plan_rope_tab(dev, oc, fmt, K, n_kv, pos, cell, n_head, n_head
         qkv.write(np.full(N, np.nan, np.float32))
         out.write(np.full(nq, np.nan, np.float32))
         if rep < 2:
+            n0 = dev.counters()["fa_dec_qkv_launches"]
             dev.attn_qkv_plan_rope_tab(plan, wt, xb, eps, nb, qkv, kc, vc, scale, n_dims, mode, tab, cb, out, nq,
                                        bad=bad, mask_f32=mb)
+            ran_one = dev.counters()["fa_dec_qkv_launches"] - n0
+            assert ran_one == (1 if one else 0), f"one-launch form ran {ran_one} times, expected {int(one)}"
         else:                                                     # the two calls it replaces
             dev.mul_mat_norm(wt, xb, 1, K, eps, nb, qkv, N)
             dev.flash_attn_plan_rope_tab(plan, qkv, kc, vc, scale, n_dims, mode, tab, cb, out, nq, bad=bad, mask_f32=mb)

@@ -469,6 +469,14 @@ def test_vs_ref_fa_decode(oc, ref):
     _fa_case(oc, ref, 1000, 1024, 4, 4, 128, new_runs=[[999, 1000]])
 
 
+@pytest.mark.parametrize("n_kv", [8192, 13000])
+def test_vs_ref_fa_decode_chunks(oc, ref, n_kv):
+    """BASELINE configs[2]'s shape (32 q / 8 KV heads, D 128) at 8192 cells (4 chunks of 2048: three
+    online merges, tsr_ref_at.c:600-633) and at 13000 cells (7 chunks, a short last one), the newest
+    cell last."""
+    _fa_case(oc, ref, n_kv, n_kv, 32, 8, 128, new_runs=[[n_kv - 1, n_kv]], seed=n_kv)
+
+
 def test_vs_ref_fa_masks(oc, ref):
     T = 40
     m = np.full((T, T), -np.inf, np.float16)

@@ -115,6 +115,10 @@ int tsr_gg_close(tsr_gg_dev * dev);
 const char * tsr_gg_last_error(const tsr_gg_dev * dev);
 /* The libtsr_hip context of a GPU device (NULL for a probe device). */
 void * tsr_gg_hip_ctx(tsr_gg_dev * dev);
+/* device_i.get_memory (ggml-tesseract.cpp:4046-4057): free and total bytes of the device's memory
+ * (hipMemGetInfo of the GPU; the reference reports its weight heap), from which llama.cpp sizes -ngl.
+ * A probe device reports 0 and 0. */
+int tsr_gg_get_memory(tsr_gg_dev * dev, size_t * free_bytes, size_t * total_bytes);
 
 /* A weight type ggml can dequantize (its type_traits: blck_size values in type_size bytes per block,
  * to_float(blocks, floats, n_values)). MUL_MAT weights of the type are converted to Q8_0 when first
@@ -153,6 +157,13 @@ int tsr_gg_buffer_clear(tsr_gg_buffer * buf, uint8_t value);
  * (ggml then copies through the host), or a negative code. */
 int tsr_gg_buffer_cpy_tensor(tsr_gg_buffer * buf, const tsr_gg_tensor * src, const tsr_gg_tensor * dst);
 int tsr_gg_buffer_free(tsr_gg_buffer * buf);
+/* buffer_i.reset (ggml-tesseract.cpp:2015-2024): ggml-alloc is about to lay the buffer's tensors out
+ * anew. A buffer whose storage is not decided yet forgets the tensors init_tensor announced (it is
+ * decided from the ones announced after); a buffer that is not KV planes forgets the mask summaries
+ * and the host copies of index inputs kept for addresses inside it, so that no FLASH_ATTN_EXT is
+ * planned from what an earlier layout wrote there (a mask not written again since fails the
+ * graph_compute that needs it). Decided storage, weights and KV planes stay. */
+int tsr_gg_buffer_reset(tsr_gg_buffer * buf);
 /* The storage the buffer got: 0 undecided, 1 device memory, 2 weights, 3 KV planes. */
 int tsr_gg_buffer_mode(const tsr_gg_buffer * buf);
 

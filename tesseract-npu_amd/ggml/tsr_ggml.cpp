@@ -585,6 +585,267 @@ bool overlap(const Rows & a, const Rows & b) {
 }
 bool same_rows(const Rows & a, const Rows & b) { return a.a == b.a && a.stride == b.stride && a.n == b.n && a.rows == b.rows; }
 
+// ---- acceptance rules ------------------------------------------------------------------------------
+// A node is accepted when every requirement of its op's table holds. A table is a list of named
+// predicates over a snapshot of the fields the rules read (the op's "facts", gathered once, null-safe);
+// they are checked in table order and the first that fails is the refusal, reported as
+//   "<OP> <rule>: <requirement> [<the facts>]"
+// so that a refusal names the rule, what it asks for and what the node has.
+template <class F> struct Rule {
+    const char * id;                 // a short stable name of the requirement
+    bool (*ok)(const F &);
+    const char * need;               // what the node must have
+};
+
+std::string strf(const char * f, ...) {
+    char b[512];
+    va_list ap;
+    va_start(ap, f);
+    vsnprintf(b, sizeof b, f, ap);
+    va_end(ap);
+    return b;
+}
+
+template <class F, size_t N>
+bool check_rules(const char * op, const F & f, const Rule<F> (&rules)[N], std::string * why) {
+    for (const Rule<F> & r : rules) {
+        if (r.ok(f)) continue;
+        *why = strf("%s %s: %s [%s]", op, r.id, r.need, f.show().c_str());
+        return false;
+    }
+    return true;
+}
+
+const char * type_name(int32_t t) {
+    switch (t) {
+        case TSR_GG_TYPE_F32: return "f32";
+        case TSR_GG_TYPE_F16: return "f16";
+        case TSR_GG_TYPE_BF16: return "bf16";
+        case TSR_GG_TYPE_Q8_0: return "q8_0";
+        case TSR_GG_TYPE_Q4_K: return "q4_K";
+        case TSR_GG_TYPE_I32: return "i32";
+        case TSR_GG_TYPE_I64: return "i64";
+        default: return t >= TSR_GG_TYPE_FOREIGN ? "registered" : "other";
+    }
+}
+
+std::string dims(const tsr_gg_tensor * t) {
+    if (t == nullptr) return "none";
+    return strf("'%s' %s [%lld,%lld,%lld,%lld]", t->name, type_name(t->type), (long long)t->ne[0], (long long)t->ne[1],
+                (long long)t->ne[2], (long long)t->ne[3]);
+}
+
+// MUL_MAT: a weight matrix of this device times rows of f32 activations.
+struct MmFacts {
+    const tsr_gg_dev * d = nullptr;
+    const tsr_gg_tensor * node = nullptr, * w = nullptr, * x = nullptr;
+    std::string show() const { return "w " + dims(w) + ", x " + dims(x) + ", out " + dims(node); }
+};
+const Rule<MmFacts> kMulMatRules[] = {
+    {"operands", [](const MmFacts & f) { return f.w != nullptr && f.x != nullptr; },
+     "a weight matrix in src0 and activation rows in src1"},
+    {"f32-io", [](const MmFacts & f) { return f.x->type == TSR_GG_TYPE_F32 && f.node->type == TSR_GG_TYPE_F32; },
+     "f32 activations and an f32 result"},
+    {"weight-home", [](const MmFacts & f) {
+         const tsr_gg_buffer * b = base_of(f.w)->buffer;
+         return b != nullptr && b->dev == f.d && b->usage != TSR_GG_USAGE_COMPUTE; },
+     "src0 held by a weights (or any-usage) buffer of this device, not a compute buffer"},
+    {"whole-weight", [](const MmFacts & f) {
+         const tsr_gg_tensor * b = base_of(f.w);
+         return f.w->view_src == nullptr || (f.w->data == b->data && same_shape(f.w, b)); },
+     "src0 to be a whole weight tensor (a view covering all of it at most)"},
+    {"matrix", [](const MmFacts & f) { return f.w->ne[2] == 1 && f.w->ne[3] == 1; },
+     "src0 to be one 2-D matrix (ne2 = ne3 = 1)"},
+    {"device-format", [](const MmFacts & f) { return loadable(f.d, f.w->type); },
+     "src0 in q8_0 or q4_K, or in a type the device converts to q8_0 when it loads (f32, f16, bf16, registered)"},
+    {"dense", [](const MmFacts & f) { return contiguous(f.d, f.w) && contiguous(f.d, f.x) && contiguous(f.d, f.node); },
+     "contiguous src0, src1 and result"},
+    {"k-range", [](const MmFacts & f) {
+         const int64_t K = f.w->ne[0], N = f.w->ne[1];
+         return K >= 32 && K <= (int64_t)kKMax && K % (f.w->type == TSR_GG_TYPE_Q4_K ? 256 : 32) == 0 && N >= 1 &&
+                N <= 0x7FFFFFFF; },
+     "32 <= K <= K_MAX (32768), K a multiple of the weight's block (32; q4_K 256), 1 <= N < 2^31"},
+    {"shapes", [](const MmFacts & f) {
+         return f.x->ne[0] == f.w->ne[0] && f.node->ne[0] == f.w->ne[1] && nrows(f.x) == nrows(f.node); },
+     "src1 rows of K values and one result row of N values per src1 row"},
+    {"x-aligned", [](const MmFacts & f) { return f.x->data % kAlign == 0; }, "src1 starting on a 64-byte boundary"},
+};
+
+// RMS_NORM: f32 rows normalized into rows of the same shape.
+struct NormFacts {
+    const tsr_gg_tensor * node = nullptr, * x = nullptr;
+    std::string show() const { return "x " + dims(x) + ", out " + dims(node); }
+};
+const Rule<NormFacts> kNormRules[] = {
+    {"operand", [](const NormFacts & f) { return f.x != nullptr; }, "a source"},
+    {"same-shape", [](const NormFacts & f) { return same_shape(f.x, f.node) && f.node->type == TSR_GG_TYPE_F32; },
+     "an f32 result of the source's shape"},
+};
+
+// ADD: a + b with b repeating whole rows of a.
+struct AddFacts {
+    const tsr_gg_tensor * node = nullptr, * a = nullptr, * b = nullptr;
+    std::string show() const { return "a " + dims(a) + ", b " + dims(b) + ", out " + dims(node); }
+};
+const Rule<AddFacts> kAddRules[] = {
+    {"operands", [](const AddFacts & f) { return f.a != nullptr && f.b != nullptr; }, "two sources"},
+    {"same-shape", [](const AddFacts & f) { return same_shape(f.a, f.node); }, "a result of a's shape"},
+};
+
+// ROPE: rotation of f32 heads by token positions (NORMAL, NEOX and IMROPE pairings).
+struct RopeFacts {
+    const tsr_gg_tensor * node = nullptr, * x = nullptr, * pos = nullptr, * ff = nullptr;
+    int32_t n_dims = 0, mode = 0;
+    float base = 0.0f, ext = 0.0f;
+    std::string show() const {
+        return strf("x %s, pos %s, mode=%d n_dims=%d freq_base=%g ext_factor=%g", dims(x).c_str(), dims(pos).c_str(), mode,
+                    n_dims, base, ext);
+    }
+    static bool heads(const tsr_gg_tensor * t, const tsr_gg_tensor * shape) {
+        const uint64_t hd = (uint64_t)shape->ne[0];
+        return t->type == TSR_GG_TYPE_F32 && t->nb[0] == 4 && t->nb[1] == 4 * hd && t->ne[3] == 1 &&
+               (shape->ne[2] <= 1 || t->nb[2] % 4 == 0);
+    }
+};
+const Rule<RopeFacts> kRopeRules[] = {
+    {"operands", [](const RopeFacts & f) { return f.x != nullptr && f.pos != nullptr; }, "a source and positions"},
+    {"mode", [](const RopeFacts & f) {
+         return f.mode == TSR_HIP_ROPE_NORMAL || f.mode == TSR_HIP_ROPE_NEOX || f.mode == TSR_HIP_ROPE_IMROPE; },
+     "the NORMAL, NEOX or IMROPE pairing (no multi-section or vision modes)"},
+    {"no-yarn", [](const RopeFacts & f) { return f.ext == 0.0f; }, "ext_factor 0 (no YaRN extrapolation mix)"},
+    {"no-offset", [](const RopeFacts & f) { return f.node->op_params[15] == 0; }, "no position offset parameter"},
+    {"same-shape", [](const RopeFacts & f) { return same_shape(f.x, f.node); }, "a result of the source's shape"},
+    {"f32-heads", [](const RopeFacts & f) { return RopeFacts::heads(f.x, f.node) && RopeFacts::heads(f.node, f.node); },
+     "f32 source and result laid out [head_dim, n_heads, n_tokens] with each token's heads contiguous"},
+    {"n-dims", [](const RopeFacts & f) {
+         return f.n_dims >= 2 && f.n_dims % 2 == 0 && f.n_dims <= f.node->ne[0] && f.n_dims <= 1024; },
+     "an even n_dims of at least 2 and at most head_dim (and 1024)"},
+    {"positions", [](const RopeFacts & f) {
+         const int64_t T = f.node->ne[2];
+         return f.pos->type == TSR_GG_TYPE_I32 && f.pos->ne[0] >= (f.mode == TSR_HIP_ROPE_IMROPE ? 4 * T : T); },
+     "I32 positions, one per token (four per token for IMROPE)"},
+    {"imrope-positions", [](const RopeFacts & f) {
+         return f.mode != TSR_HIP_ROPE_IMROPE || strstr(f.pos->name, "inp_pos") != nullptr; },
+     "IMROPE positions from the graph input inp_pos (its four sections per token)"},
+    {"freq-base", [](const RopeFacts & f) { return f.base > 0.0f && std::isfinite(f.base); }, "a finite positive freq_base"},
+    {"freq-factors", [](const RopeFacts & f) {
+         return f.ff == nullptr || (f.ff->type == TSR_GG_TYPE_F32 && f.ff->ne[0] >= f.n_dims / 2); },
+     "frequency factors, when given, as an f32 vector of at least n_dims / 2"},
+};
+
+// GLU: SWIGLU of a gate and an up half (two sources, or one source of both halves).
+struct GluFacts {
+    const tsr_gg_tensor * node = nullptr, * g = nullptr, * u = nullptr;
+    std::string show() const {
+        return strf("glu op %d swapped %d, gate %s, up %s, out %s", node->op_params[0], node->op_params[1], dims(g).c_str(),
+                    dims(u).c_str(), dims(node).c_str());
+    }
+};
+const Rule<GluFacts> kGluRules[] = {
+    {"swiglu", [](const GluFacts & f) { return f.node->op_params[0] == TSR_GG_GLU_SWIGLU; }, "the SWIGLU kind of GLU"},
+    {"operand", [](const GluFacts & f) { return f.g != nullptr; }, "a gate source"},
+    {"split-shapes", [](const GluFacts & f) { return f.u == nullptr || (same_shape(f.g, f.node) && same_shape(f.u, f.node)); },
+     "gate, up and result of one shape (two-source form)"},
+    {"fused-halves", [](const GluFacts & f) {
+         return f.u != nullptr ||
+                (f.node->op_params[1] == 0 && f.g->ne[0] == 2 * f.node->ne[0] && nrows(f.g) == nrows(f.node)); },
+     "one source row of 2n values per result row of n, gate half first (one-source form)"},
+};
+
+// GET_ROWS: rows of a 2-D f32 table picked by one vector of I32 ids.
+struct GetRowsFacts {
+    const tsr_gg_tensor * node = nullptr, * src = nullptr, * ids = nullptr;
+    std::string show() const { return "table " + dims(src) + ", ids " + dims(ids) + ", out " + dims(node); }
+};
+const Rule<GetRowsFacts> kGetRowsRules[] = {
+    {"operands", [](const GetRowsFacts & f) { return f.src != nullptr && f.ids != nullptr; }, "a table and ids"},
+    {"table", [](const GetRowsFacts & f) {
+         return f.src->ne[2] == 1 && f.src->ne[3] == 1 && f.src->ne[0] == f.node->ne[0]; },
+     "a 2-D table whose rows have the result's width"},
+    {"ids", [](const GetRowsFacts & f) {
+         return f.ids->type == TSR_GG_TYPE_I32 && f.ids->ne[1] == 1 && f.ids->ne[2] == 1; },
+     "one vector of I32 ids"},
+};
+
+// SET_ROWS into one layer's KV cache (the SET_ROWS_KV kind).
+struct SetRowsFacts {
+    const tsr_gg_tensor * node = nullptr, * src = nullptr, * idx = nullptr;
+    const tsr_gg_dev * d = nullptr;
+    bool kv = false;
+    std::string kv_note;
+    std::string show() const {
+        return "rows " + dims(src) + ", cells " + dims(idx) + ", cache " + dims(node) + (kv ? "" : " (" + kv_note + ")");
+    }
+};
+const Rule<SetRowsFacts> kSetRowsRules[] = {
+    {"operands", [](const SetRowsFacts & f) { return f.src != nullptr && f.idx != nullptr; }, "rows and cell indices"},
+    {"kv-dest", [](const SetRowsFacts & f) { return f.kv; }, "a destination in a KV-cache tensor of this device"},
+    {"from-cell-0", [](const SetRowsFacts & f) { return f.node->data == base_of(f.node)->data; },
+     "the destination view to begin at the cache's cell 0"},
+    {"i64-cells", [](const SetRowsFacts & f) {
+         return f.idx->type == TSR_GG_TYPE_I64 && f.idx->ne[1] == 1 && f.idx->ne[2] == 1 && f.idx->ne[3] == 1 &&
+                contiguous(f.d, f.idx); },
+     "the cell indices as one contiguous I64 vector"},
+};
+
+// FLASH_ATTN_EXT: softmax attention of f32 q over one layer's q8_0 K and V planes.
+struct FaFacts {
+    const tsr_gg_tensor * node = nullptr, * q = nullptr, * k = nullptr, * v = nullptr, * mask = nullptr;
+    float scale = 0.0f, max_bias = 0.0f, softcap = 0.0f;
+    int32_t prec = 0, n_kv_max = 0;
+    uint32_t D = 0, T = 0, H = 0, n_kv = 0, Hk = 0;
+    bool k_kv = false, v_kv = false;
+    KvTensor kk, vk;
+    std::string kv_note;
+    std::string show() const {
+        return strf("D=%u T=%u H=%u H_kv=%u n_kv=%u scale=%g max_bias=%g softcap=%g prec=%d n_kv_max=%d; q %s, k %s, v %s, "
+                    "mask %s%s%s", D, T, H, Hk, n_kv, scale, max_bias, softcap, prec, n_kv_max, dims(q).c_str(),
+                    dims(k).c_str(), dims(v).c_str(), dims(mask).c_str(), kv_note.empty() ? "" : "; ", kv_note.c_str());
+    }
+};
+const Rule<FaFacts> kFaRules[] = {
+    {"operands", [](const FaFacts & f) { return f.q != nullptr && f.k != nullptr && f.v != nullptr; }, "q, K and V sources"},
+    {"no-sinks", [](const FaFacts & f) { return f.node->src[4] == nullptr; }, "no attention-sink source"},
+    {"plain-softmax", [](const FaFacts & f) {
+         return f.max_bias == 0.0f && f.softcap == 0.0f && f.n_kv_max == 0 && (f.prec == 0 || f.prec == 10); },
+     "a plain scaled softmax: no ALiBi max_bias, no logit softcap, no n_kv_max, default or F32 precision"},
+    {"types", [](const FaFacts & f) {
+         return f.q->type == TSR_GG_TYPE_F32 && f.k->type == TSR_GG_TYPE_Q8_0 && f.v->type == TSR_GG_TYPE_Q8_0 &&
+                f.node->type == TSR_GG_TYPE_F32; },
+     "q F32, K and V q8_0, an F32 result"},
+    {"head-dim", [](const FaFacts & f) {
+         return (f.D == 64 || f.D == 128 || f.D == 256 || f.D == 512) && f.k->ne[0] == f.D && f.v->ne[0] == f.D; },
+     "one head size D for q, K and V, D in {64, 128, 256, 512}"},
+    {"gqa", [](const FaFacts & f) {
+         return f.Hk != 0 && f.H % f.Hk == 0 && f.H / f.Hk <= 64 && f.v->ne[1] == f.n_kv && f.v->ne[2] == f.Hk &&
+                f.q->ne[3] == 1 && f.k->ne[3] == 1 && f.v->ne[3] == 1 && f.T >= 1 && f.n_kv >= 1; },
+     "n_head a multiple of n_head_kv (at most 64 per KV head), V's cells and heads equal to K's, one sequence stream"},
+    {"out-layout", [](const FaFacts & f) {
+         return f.node->nb[0] == 4 && f.node->nb[1] == 4ull * f.D && (f.T <= 1 || f.node->nb[2] % 4 == 0) &&
+                f.node->ne[0] == f.D && f.node->ne[1] == f.H && f.node->ne[2] == f.T; },
+     "a result laid out [D, n_head, n_tokens] with each token's heads contiguous"},
+    {"rows", [](const FaFacts & f) { return f.T <= kFaTMax; }, "at most 680 query tokens per call"},
+    {"mask", [](const FaFacts & f) {
+         return f.mask == nullptr || (f.mask->type == TSR_GG_TYPE_F16 && f.mask->ne[0] == f.n_kv && f.mask->ne[1] == f.T &&
+                                      f.mask->ne[2] == 1 && f.mask->ne[3] == 1 && f.mask->nb[0] == 2); },
+     "no mask, or an F16 mask of n_kv columns and one row per query token"},
+    {"kv-views", [](const FaFacts & f) { return f.k_kv && f.v_kv; }, "K and V viewing KV-cache tensors of this device"},
+    {"one-layer", [](const FaFacts & f) {
+         return f.kk.which == TSR_HIP_KV_K && f.vk.which == TSR_HIP_KV_V && f.kk.E == f.Hk * f.D && f.vk.E == f.kk.E &&
+                f.vk.kv_size == f.kk.kv_size; },
+     "K and V as the K and V planes of one layer, E = n_head_kv D values per cell"},
+    {"from-cell-0", [](const FaFacts & f) {
+         const size_t cell_b = (size_t)f.kk.E / 32 * 34, head_b = (size_t)f.D / 32 * 34;
+         for (const tsr_gg_tensor * t : {f.k, f.v})
+             if (t->nb[0] != 34 || (f.n_kv > 1 && t->nb[1] != cell_b) || (f.Hk > 1 && t->nb[2] != head_b) ||
+                 t->data != base_of(t)->data)
+                 return false;
+         return true; },
+     "K and V views of the caches' cells from cell 0, cells a cache row apart, heads D/32 blocks apart"},
+    {"fits-cache", [](const FaFacts & f) { return f.n_kv <= f.kk.kv_size; }, "n_kv no larger than the cache"},
+    {"scale", [](const FaFacts & f) { return f.scale > 0.0f && std::isfinite(f.scale); }, "a finite positive scale"},
+};
+
 // The ggml rows of a weight read back from its buffer, as blocks of its device format: Q8_0 / Q4_K
 // unchanged, other types to f32 and quantized to Q8_0 (ggml's quantize_row_q8_0_ref).
 int weight_blocks(tsr_gg_dev * d, const tsr_gg_tensor * t, const void * p, uint32_t * fmt, std::vector<uint8_t> * out) {
@@ -781,24 +1042,15 @@ struct Lowerer {
     // MUL_MAT, with the ADD / SCALE / softcap behind it when it is their only source of this value.
     bool mul_mat(const Graph & g, int i, int * consumed) {
         const tsr_gg_tensor * node = g.nodes[i];
-        const tsr_gg_tensor * w = node->src[0];
-        const tsr_gg_tensor * x = node->src[1];
-        if (w == nullptr || x == nullptr) return refuse("MUL_MAT without both sources");
-        if (node->type != TSR_GG_TYPE_F32 || x->type != TSR_GG_TYPE_F32) return refuse("MUL_MAT: the result and src1 must be f32");
-        if (w->ne[2] != 1 || w->ne[3] != 1) return refuse("MUL_MAT: src0 is a batch of matrices (ne2 or ne3 not 1)");
-        if (!contiguous(d, w) || !contiguous(d, x) || !contiguous(d, node)) return refuse("MUL_MAT: an operand is not contiguous");
-        if (!loadable(d, w->type)) return refuse("MUL_MAT: the weight type has no device format (not loadable)");
+        MmFacts mf;
+        mf.d = d;
+        mf.node = node;
+        mf.w = node->src[0];
+        mf.x = node->src[1];
+        if (!check_rules("MUL_MAT", mf, kMulMatRules, &why)) return false;
+        const tsr_gg_tensor * w = mf.w;
+        const tsr_gg_tensor * x = mf.x;
         const int64_t K = w->ne[0], N = w->ne[1];
-        if (K < 32 || K % 32 != 0 || K > (int64_t)kKMax || (w->type == TSR_GG_TYPE_Q4_K && K % 256 != 0) || N < 1 ||
-            N > 0x7FFFFFFF)
-            return refuse("MUL_MAT: K > K_MAX, K %% 32 != 0 or N out of range");
-        if (x->ne[0] != K || node->ne[0] != N || nrows(x) != nrows(node)) return refuse("MUL_MAT: shapes do not match");
-        const tsr_gg_tensor * wb = base_of(w);
-        if (wb->buffer == nullptr || wb->buffer->dev != d || wb->buffer->usage == TSR_GG_USAGE_COMPUTE)
-            return refuse("MUL_MAT: src0 is not a weight in a weights buffer of this device");
-        if (w->view_src != nullptr && (w->data != wb->data || !same_shape(w, wb)))
-            return refuse("MUL_MAT: src0 is a slice of a weight");
-        if (x->data % kAlign != 0) return refuse("MUL_MAT: src1 is not 64-byte aligned");
         // src1 = RMS_NORM(x') * w folded into this matvec: the norm runs on x' inside it
         const int xi = g.index_of(x);
         const Fold * fo = xi >= 0 && xi < (int)fold_of.size() && fold_of[xi] >= 0 ? &folds[fold_of[xi]] : nullptr;
@@ -867,7 +1119,7 @@ struct Lowerer {
             last = i;
             if (!f32_rows(d, node, "dst", &Y, &why)) return false;
         }
-        if (overlap(X, Y)) return refuse("MUL_MAT: src1 and the result overlap");
+        if (overlap(X, Y)) return refuse("MUL_MAT in-place: the result may not share bytes with src1");
         Call & c = add(TSR_GG_CALL_MUL_MAT, i);
         c.info.node2 = n2;
         c.info.node3 = n3;
@@ -911,11 +1163,27 @@ struct Lowerer {
         return true;
     }
 
+    // The ROPE acceptance rules of a node (also of the q rotation a fused attention call performs).
+    bool rope_rules(const tsr_gg_tensor * node, RopeFacts * rf) {
+        rf->node = node;
+        rf->x = node->src[0];
+        rf->pos = node->src[1];
+        rf->ff = node->src[2];
+        rf->n_dims = node->op_params[1];
+        rf->mode = node->op_params[2];
+        rf->base = param_f32(node, 5);
+        rf->ext = param_f32(node, 7);
+        return check_rules("ROPE", *rf, kRopeRules, &why);
+    }
+
     // RMS_NORM, with the MUL by a weight row behind it when it is the norm's only user.
     bool rms_norm(const Graph & g, int i, int * consumed) {
         const tsr_gg_tensor * node = g.nodes[i];
-        const tsr_gg_tensor * x = node->src[0];
-        if (x == nullptr || !same_shape(x, node) || node->type != TSR_GG_TYPE_F32) return refuse("RMS_NORM: source and result differ in shape");
+        NormFacts nf;
+        nf.node = node;
+        nf.x = node->src[0];
+        if (!check_rules("RMS_NORM", nf, kNormRules, &why)) return false;
+        const tsr_gg_tensor * x = nf.x;
         Rows X, Y, W;
         if (!f32_rows(d, x, "source", &X, &why)) return false;
         const tsr_gg_tensor * out = node;
@@ -934,7 +1202,7 @@ struct Lowerer {
         }
         if (!f32_rows(d, out, "result", &Y, &why)) return false;
         if (wt && !f32_rows(d, wt, "weight", &W, &why)) return false;
-        if (overlap(X, Y) && !same_rows(X, Y)) return refuse("RMS_NORM: source and result overlap");
+        if (overlap(X, Y) && !same_rows(X, Y)) return refuse("RMS_NORM in-place: the result is the source itself or apart from it");
         Call & c = add(TSR_GG_CALL_RMS_NORM, i);
         c.info.node2 = n2;
         c.info.N = X.n;
@@ -963,17 +1231,23 @@ struct Lowerer {
 
     bool add_op(const Graph & g, int i) {
         const tsr_gg_tensor * node = g.nodes[i];
-        const tsr_gg_tensor * a = node->src[0];
-        const tsr_gg_tensor * b = node->src[1];
-        if (a == nullptr || b == nullptr || !same_shape(a, node)) return refuse("ADD: a and the result differ in shape");
+        AddFacts af;
+        af.node = node;
+        af.a = node->src[0];
+        af.b = node->src[1];
+        if (!check_rules("ADD", af, kAddRules, &why)) return false;
+        const tsr_gg_tensor * a = af.a;
+        const tsr_gg_tensor * b = af.b;
         Rows A, B, Y;
         if (!f32_rows(d, a, "a", &A, &why) || !f32_rows(d, b, "b", &B, &why) || !f32_rows(d, node, "result", &Y, &why))
             return false;
-        if (B.n != Y.n || (B.rows != 1 && (B.rows > Y.rows || Y.rows % B.rows != 0)) ||
-            (B.rows != 1 && B.rows != Y.rows && (node->ne[2] > 1 || node->ne[3] > 1)))
-            return refuse("ADD: b '%s' is not broadcast by whole rows", b->name);
+        // b repeats: one row for all, or every row, or (2-D results) a period of whole rows
+        const bool whole_rows = B.n == Y.n && (B.rows == 1 || B.rows == Y.rows ||
+                                               (Y.rows % B.rows == 0 && node->ne[2] <= 1 && node->ne[3] <= 1));
+        if (!whole_rows)
+            return refuse("ADD row-broadcast: b must repeat whole rows of the result [%s]", af.show().c_str());
         if ((overlap(A, Y) && !same_rows(A, Y)) || (overlap(B, Y) && !same_rows(B, Y)))
-            return refuse("ADD: an operand and the result overlap");
+            return refuse("ADD in-place: the result is an operand itself or apart from both");
         Call & c = add(TSR_GG_CALL_ADD, i);
         c.info.N = Y.n;
         c.info.T = Y.rows;
@@ -998,41 +1272,27 @@ struct Lowerer {
 
     bool rope(const Graph & g, int i) {
         const tsr_gg_tensor * node = g.nodes[i];
-        const tsr_gg_tensor * x = node->src[0];
-        const tsr_gg_tensor * pos = node->src[1];
-        const tsr_gg_tensor * ff = node->src[2];
-        const int32_t n_dims = node->op_params[1], mode = node->op_params[2];
-        const float freq_base = param_f32(node, 5), freq_scale = param_f32(node, 6), ext = param_f32(node, 7),
-                    attn = param_f32(node, 8);
-        if (mode != TSR_HIP_ROPE_NORMAL && mode != TSR_HIP_ROPE_NEOX && mode != TSR_HIP_ROPE_IMROPE)
-            return refuse("ROPE mode %d (multi-section / vision) is not on the device", mode);
-        if (ext != 0.0f) return refuse("ROPE with YaRN ext_factor %g", ext);
-        if (node->op_params[15] != 0) return refuse("ROPE with a position offset");
-        if (x == nullptr || pos == nullptr || !same_shape(x, node)) return refuse("ROPE: source and result differ in shape");
+        RopeFacts rf;
+        if (!rope_rules(node, &rf)) return false;
+        const tsr_gg_tensor * x = rf.x;
+        const tsr_gg_tensor * pos = rf.pos;
+        const tsr_gg_tensor * ff = rf.ff;
+        const int32_t n_dims = rf.n_dims, mode = rf.mode;
+        const float freq_base = rf.base, freq_scale = param_f32(node, 6), attn = param_f32(node, 8);
         const uint32_t hd = (uint32_t)node->ne[0], nh = (uint32_t)node->ne[1], T = (uint32_t)node->ne[2];
-        for (const tsr_gg_tensor * t : {x, node})
-            if (t->type != TSR_GG_TYPE_F32 || t->nb[0] != 4 || t->nb[1] != 4ull * hd || t->ne[3] != 1 || (T > 1 && t->nb[2] % 4))
-                return refuse("ROPE '%s' is not f32 [head_dim, n_heads, n_tokens] with contiguous heads", t->name);
-        if (n_dims < 2 || n_dims % 2 || (uint32_t)n_dims > hd || n_dims > 1024) return refuse("ROPE: n_dims %d", n_dims);
-        if (pos->type != TSR_GG_TYPE_I32 || pos->ne[0] < (mode == TSR_HIP_ROPE_IMROPE ? 4 * (int64_t)T : (int64_t)T))
-            return refuse("ROPE: positions are not I32 of n_tokens");
-        if (mode == TSR_HIP_ROPE_IMROPE && strstr(pos->name, "inp_pos") == nullptr)
-            return refuse("IMROPE: the positions '%s' are not llama.cpp's inp_pos input", pos->name);
-        if (!(freq_base > 0.0f) || !std::isfinite(freq_base)) return refuse("ROPE: freq_base %g", freq_base);
         const uint64_t xs = T > 1 ? x->nb[2] / 4 : (uint64_t)hd * nh, ys = T > 1 ? node->nb[2] / 4 : (uint64_t)hd * nh;
         void *xp, *yp, *pp, *fp = nullptr;
         const size_t xb = ((size_t)(T - 1) * xs + (size_t)hd * nh) * 4, yb = ((size_t)(T - 1) * ys + (size_t)hd * nh) * 4;
         std::string w2;
         if (!dev_ptr(d, x->data, xb, &xp, &w2) || !dev_ptr(d, node->data, yb, &yp, &w2) ||
             !dev_ptr(d, pos->data, 4 * (size_t)pos->ne[0], &pp, &w2))
-            return refuse("ROPE: %s", w2.c_str());
+            return refuse("ROPE device-rows: source, result and positions in device memory of this device (%s)", w2.c_str());
         if (ff != nullptr) {
-            if (ff->type != TSR_GG_TYPE_F32 || ff->ne[0] < n_dims / 2 || !contiguous(d, ff))
-                return refuse("ROPE freq_factors '%s' is not an f32 vector of n_dims/2", ff->name);
-            if (!dev_ptr(d, ff->data, 4 * (size_t)ff->ne[0], &fp, &w2)) return refuse("ROPE freq_factors: %s", w2.c_str());
+            if (!contiguous(d, ff) || !dev_ptr(d, ff->data, 4 * (size_t)ff->ne[0], &fp, &w2))
+                return refuse("ROPE freq-factors: a contiguous vector in device memory of this device (%s)", w2.c_str());
         }
         if (x->data != node->data && x->data < node->data + yb && node->data < x->data + xb)
-            return refuse("ROPE: source and result overlap");
+            return refuse("ROPE in-place: the result is the source itself or apart from it");
         Call & c = add(TSR_GG_CALL_ROPE, i);
         c.info.N = hd;
         c.info.K = nh;
@@ -1061,18 +1321,18 @@ struct Lowerer {
 
     bool glu(const Graph & g, int i) {
         const tsr_gg_tensor * node = g.nodes[i];
-        if (node->op_params[0] != TSR_GG_GLU_SWIGLU) return refuse("GLU %d is not on the device (SWIGLU)", node->op_params[0]);
-        const tsr_gg_tensor * gt = node->src[0];
-        const tsr_gg_tensor * ut = node->src[1];
+        GluFacts gf;
+        gf.node = node;
+        gf.g = node->src[0];
+        gf.u = node->src[1];
+        if (!check_rules("GLU", gf, kGluRules, &why)) return false;
+        const tsr_gg_tensor * gt = gf.g;
+        const tsr_gg_tensor * ut = gf.u;
         Rows G, U, Y;
         if (!f32_rows(d, node, "result", &Y, &why)) return false;
         if (ut != nullptr) {
-            if (!same_shape(gt, node) || !same_shape(ut, node)) return refuse("GLU: gate, up and the result differ in shape");
             if (!f32_rows(d, gt, "gate", &G, &why) || !f32_rows(d, ut, "up", &U, &why)) return false;
         } else {
-            if (node->op_params[1] != 0) return refuse("GLU: the swapped single form is not supported");
-            if (gt == nullptr || gt->ne[0] != 2 * node->ne[0] || nrows(gt) != nrows(node))
-                return refuse("GLU: the single form's source is not [2n, rows]");
             if (!f32_rows(d, gt, "gate|up", &G, &why)) return false;
             U = G;
             U.a += 4ull * (uint64_t)node->ne[0];
@@ -1080,7 +1340,7 @@ struct Lowerer {
             G.n = U.n = (uint32_t)node->ne[0];
         }
         if ((overlap(G, Y) && !same_rows(G, Y)) || (overlap(U, Y) && !same_rows(U, Y)))
-            return refuse("GLU: an operand and the result overlap");
+            return refuse("GLU in-place: the result is a source itself or apart from both");
         Call & c = add(TSR_GG_CALL_SWIGLU, i);
         c.info.N = Y.n;
         c.info.T = Y.rows;
@@ -1105,18 +1365,20 @@ struct Lowerer {
 
     bool get_rows(const Graph & g, int i) {
         const tsr_gg_tensor * node = g.nodes[i];
-        const tsr_gg_tensor * src = node->src[0];
-        const tsr_gg_tensor * ids = node->src[1];
-        if (src == nullptr || ids == nullptr || src->ne[2] != 1 || src->ne[3] != 1 || ids->ne[1] != 1 || ids->ne[2] != 1 ||
-            src->ne[0] != node->ne[0])
-            return refuse("GET_ROWS: only 2D sources with one id vector");
-        if (ids->type != TSR_GG_TYPE_I32) return refuse("GET_ROWS: ids are not I32");
+        GetRowsFacts gf;
+        gf.node = node;
+        gf.src = node->src[0];
+        gf.ids = node->src[1];
+        if (!check_rules("GET_ROWS", gf, kGetRowsRules, &why)) return false;
+        const tsr_gg_tensor * src = gf.src;
+        const tsr_gg_tensor * ids = gf.ids;
         Rows S, Y;
-        if (!f32_rows(d, src, "source", &S, &why) || !f32_rows(d, node, "result", &Y, &why)) return false;
+        if (!f32_rows(d, src, "table", &S, &why) || !f32_rows(d, node, "result", &Y, &why)) return false;
         void * ip = nullptr;
         std::string w2;
-        if (!dev_ptr(d, ids->data, 4 * (size_t)ids->ne[0], &ip, &w2)) return refuse("GET_ROWS ids: %s", w2.c_str());
-        if (overlap(S, Y)) return refuse("GET_ROWS: source and result overlap");
+        if (!dev_ptr(d, ids->data, 4 * (size_t)ids->ne[0], &ip, &w2))
+            return refuse("GET_ROWS device-ids: the ids in device memory of this device (%s)", w2.c_str());
+        if (overlap(S, Y)) return refuse("GET_ROWS in-place: the result may not share bytes with the table");
         Call & c = add(TSR_GG_CALL_GET_ROWS, i);
         c.info.N = S.n;
         c.info.K = S.rows;
@@ -1142,12 +1404,14 @@ struct Lowerer {
         const tsr_gg_tensor * node = g.nodes[i];
         const tsr_gg_tensor * x = node->src[0];
         Rows X;
-        if (x == nullptr || !f32_rows(d, x, "source", &X, &why)) return x ? false : refuse("ARGMAX without a source");
+        if (x == nullptr) return refuse("ARGMAX operand: a source of f32 rows [none]");
+        if (!f32_rows(d, x, "source", &X, &why)) return false;
         if (node->type != TSR_GG_TYPE_I32 || node->ne[0] != (int64_t)X.rows || !contiguous(d, node))
-            return refuse("ARGMAX: the result is not I32 [rows]");
+            return refuse("ARGMAX i32-index: one contiguous I32 index per source row [out %s]", dims(node).c_str());
         void * yp = nullptr;
         std::string w2;
-        if (!dev_ptr(d, node->data, 4ull * X.rows, &yp, &w2)) return refuse("ARGMAX: %s", w2.c_str());
+        if (!dev_ptr(d, node->data, 4ull * X.rows, &yp, &w2))
+            return refuse("ARGMAX device-rows: the result in device memory of this device (%s)", w2.c_str());
         Call & c = add(TSR_GG_CALL_ARGMAX, i);
         c.info.N = X.n;
         c.info.T = X.rows;
@@ -1168,20 +1432,24 @@ struct Lowerer {
     // SET_ROWS into a KV-cache tensor (the SET_ROWS_KV kind).
     bool set_rows(const Graph & g, int i) {
         const tsr_gg_tensor * node = g.nodes[i];
-        const tsr_gg_tensor * src = node->src[0];
-        const tsr_gg_tensor * idx = node->src[1];
-        if (src == nullptr || idx == nullptr) return refuse("SET_ROWS without both sources");
+        SetRowsFacts sf;
+        sf.d = d;
+        sf.node = node;
+        sf.src = node->src[0];
+        sf.idx = node->src[1];
         KvTensor kp;
-        std::string w2;
-        if (!kv_probe(d, node, &kp, &w2)) return refuse("SET_ROWS does not write a KV cache of this device: %s", w2.c_str());
-        if (node->data != base_of(node)->data) return refuse("SET_ROWS: the destination view does not start at cell 0");
-        if (idx->type != TSR_GG_TYPE_I64 || idx->ne[1] != 1 || idx->ne[2] != 1 || idx->ne[3] != 1 || !contiguous(d, idx))
-            return refuse("SET_ROWS: the indices are not one I64 vector");
+        sf.kv = kv_probe(d, node, &kp, &sf.kv_note);
+        if (!check_rules("SET_ROWS", sf, kSetRowsRules, &why)) return false;
+        const tsr_gg_tensor * src = sf.src;
+        const tsr_gg_tensor * idx = sf.idx;
         Rows S;
         if (!f32_rows(d, src, "rows", &S, &why)) return false;
-        if (S.n != kp.E || (int64_t)S.rows != idx->ne[0]) return refuse("SET_ROWS: rows of %u values, the cache has E = %u", S.n, kp.E);
+        if (S.n != kp.E || (int64_t)S.rows != idx->ne[0])
+            return refuse("SET_ROWS row-width: one source row of E = %u values per cell index [%s]", kp.E, sf.show().c_str());
         void * ip = nullptr;
-        if (!dev_ptr(d, idx->data, 8 * (size_t)idx->ne[0], &ip, &w2)) return refuse("SET_ROWS indices: %s", w2.c_str());
+        std::string w2;
+        if (!dev_ptr(d, idx->data, 8 * (size_t)idx->ne[0], &ip, &w2))
+            return refuse("SET_ROWS device-cells: the cell indices in device memory of this device (%s)", w2.c_str());
         Call & c = add(TSR_GG_CALL_SET_ROWS, i);
         c.info.N = S.n;
         c.info.T = S.rows;
@@ -1218,67 +1486,58 @@ struct Lowerer {
     };
     bool fa_info(const Graph & g, int i, FaInfo * f) {
         const tsr_gg_tensor * node = g.nodes[i];
-        const tsr_gg_tensor * q = node->src[0];
-        const tsr_gg_tensor * k = node->src[1];
-        const tsr_gg_tensor * v = node->src[2];
-        const tsr_gg_tensor * mask = node->src[3];
-        if (q == nullptr || k == nullptr || v == nullptr) return refuse("FLASH_ATTN_EXT without q / k / v");
-        if (node->src[4] != nullptr) return refuse("FLASH_ATTN_EXT with attention sinks");
-        const float scale = param_f32(node, 0), max_bias = param_f32(node, 1), softcap = param_f32(node, 2);
-        const int32_t prec = node->op_params[3], n_kv_max = node->op_params[4];
-        if (max_bias != 0.0f || softcap != 0.0f || n_kv_max != 0 || (prec != 0 && prec != 10))
-            return refuse("FLASH_ATTN_EXT with ALiBi, a softcap, n_kv_max or a precision other than F32");
-        const uint32_t D = (uint32_t)q->ne[0], T = (uint32_t)q->ne[1], H = (uint32_t)q->ne[2];
-        const uint32_t n_kv = (uint32_t)k->ne[1], Hk = (uint32_t)k->ne[2];
-        if (q->type != TSR_GG_TYPE_F32 || k->type != TSR_GG_TYPE_Q8_0 || v->type != TSR_GG_TYPE_Q8_0 || node->type != TSR_GG_TYPE_F32)
-            return refuse("FLASH_ATTN_EXT: q F32, K / V q8_0 only");
-        if ((D != 64 && D != 128 && D != 256 && D != 512) || k->ne[0] != D || v->ne[0] != D || v->ne[1] != n_kv ||
-            v->ne[2] != Hk || Hk == 0 || H % Hk != 0 || H / Hk > 64 || q->ne[3] != 1 || k->ne[3] != 1 || v->ne[3] != 1 ||
-            T < 1 || n_kv < 1)
-            return refuse("FLASH_ATTN_EXT shape: D = DK = DV in {64, 128, 256, 512}, n_head %% n_head_kv = 0, one stream");
-        if (node->nb[0] != 4 || node->nb[1] != 4ull * D || (T > 1 && node->nb[2] % 4 != 0) || node->ne[0] != D ||
-            node->ne[1] != H || node->ne[2] != T)
-            return refuse("FLASH_ATTN_EXT: the result's layout");
-        if (T > kFaTMax) return refuse("FLASH_ATTN_EXT of %u tokens (at most %u)", T, kFaTMax);
-        if (mask != nullptr && (mask->type != TSR_GG_TYPE_F16 || mask->ne[0] != n_kv || mask->ne[1] != T || mask->ne[2] != 1 ||
-                                mask->ne[3] != 1 || mask->nb[0] != 2))
-            return refuse("FLASH_ATTN_EXT: the mask is not F16 [n_kv, n_tokens]");
-        KvTensor kk, vk;
-        std::string w2;
-        if (!kv_probe(d, k, &kk, &w2)) return refuse("FLASH_ATTN_EXT: K '%s' is not a KV cache view: %s", k->name, w2.c_str());
-        if (!kv_probe(d, v, &vk, &w2)) return refuse("FLASH_ATTN_EXT: V '%s' is not a KV cache view: %s", v->name, w2.c_str());
-        if (kk.which != TSR_HIP_KV_K || vk.which != TSR_HIP_KV_V || kk.E != Hk * D || vk.E != kk.E || vk.kv_size != kk.kv_size)
-            return refuse("FLASH_ATTN_EXT: K / V are not the K and V planes of one layer with E = n_head_kv D");
-        const size_t cell_b = (size_t)kk.E / 32 * 34, head_b = (size_t)D / 32 * 34;
-        for (const tsr_gg_tensor * t : {k, v})
-            if (t->nb[0] != 34 || (n_kv > 1 && t->nb[1] != cell_b) || (Hk > 1 && t->nb[2] != head_b) ||
-                t->data != base_of(t)->data)
-                return refuse("FLASH_ATTN_EXT: '%s' is not the cache's cells from cell 0 with heads %zu bytes apart", t->name, head_b);
-        if (n_kv > kk.kv_size) return refuse("FLASH_ATTN_EXT: %u cells of a cache of %u", n_kv, kk.kv_size);
+        FaFacts ff;
+        ff.node = node;
+        ff.q = node->src[0];
+        ff.k = node->src[1];
+        ff.v = node->src[2];
+        ff.mask = node->src[3];
+        ff.scale = param_f32(node, 0);
+        ff.max_bias = param_f32(node, 1);
+        ff.softcap = param_f32(node, 2);
+        ff.prec = node->op_params[3];
+        ff.n_kv_max = node->op_params[4];
+        if (ff.q != nullptr && ff.k != nullptr && ff.v != nullptr) {
+            ff.D = (uint32_t)ff.q->ne[0];
+            ff.T = (uint32_t)ff.q->ne[1];
+            ff.H = (uint32_t)ff.q->ne[2];
+            ff.n_kv = (uint32_t)ff.k->ne[1];
+            ff.Hk = (uint32_t)ff.k->ne[2];
+            std::string kn, vn;
+            ff.k_kv = kv_probe(d, ff.k, &ff.kk, &kn);
+            ff.v_kv = kv_probe(d, ff.v, &ff.vk, &vn);
+            if (!ff.k_kv) ff.kv_note = "K: " + kn;
+            if (!ff.v_kv) ff.kv_note += std::string(ff.kv_note.empty() ? "" : "; ") + "V: " + vn;
+        }
+        if (!check_rules("FLASH_ATTN_EXT", ff, kFaRules, &why)) return false;
+        const tsr_gg_tensor * k = ff.k;
+        const uint32_t D = ff.D, T = ff.T, H = ff.H;
         f->os = T > 1 ? node->nb[2] / 4 : (uint64_t)H * D;
+        std::string w2;
         if (!dev_ptr(d, node->data, ((size_t)(T - 1) * f->os + (size_t)H * D) * 4, &f->op, &w2))
-            return refuse("FLASH_ATTN_EXT: %s", w2.c_str());
-        if (!(scale > 0.0f) || !std::isfinite(scale)) return refuse("FLASH_ATTN_EXT: scale %g", scale);
-        // the new cells: a SET_ROWS of this graph into the same K cache, earlier, with indices from the host
+            return refuse("FLASH_ATTN_EXT device-rows: the result in device memory of this device (%s)", w2.c_str());
+        // the new cells: the indices of an earlier SET_ROWS of this graph into the same K cache, which the
+        // host writes (their copy on the host orders the chunk plan: the newest cells last)
         for (int j = 0; j < i; ++j) {
             const tsr_gg_tensor * sj = g.nodes[j];
             if (sj->op != TSR_GG_OP_SET_ROWS || base_of(sj)->data != base_of(k)->data || sj->src[1] == nullptr) continue;
             const tsr_gg_tensor * ix = sj->src[1];
             if (ix->op != TSR_GG_OP_NONE || g.index_of(ix) >= 0)
-                return refuse("FLASH_ATTN_EXT: the new-cell indices '%s' are computed by the graph, not written by the host", ix->name);
+                return refuse("FLASH_ATTN_EXT host-cells: new-cell indices the host writes, not a result of the graph [%s]",
+                              dims(ix).c_str());
             f->kidx = ix->data;
             f->kidx_n = (uint32_t)ix->ne[0];
         }
         f->D = D;
         f->T = T;
         f->H = H;
-        f->Hk = Hk;
-        f->n_kv = n_kv;
-        f->kv_size = kk.kv_size;
-        f->scale = scale;
-        f->mask = mask ? mask->data : 0;
+        f->Hk = ff.Hk;
+        f->n_kv = ff.n_kv;
+        f->kv_size = ff.kk.kv_size;
+        f->scale = ff.scale;
+        f->mask = ff.mask ? ff.mask->data : 0;
         f->kbase = base_of(k)->data;
-        f->vbase = base_of(v)->data;
+        f->vbase = base_of(ff.v)->data;
         return true;
     }
     void fa_call_info(Call & c, const FaInfo & f, uint64_t q, uint64_t qs, uint64_t y) {
@@ -1332,12 +1591,12 @@ struct Lowerer {
         if (!fa_info(g, i, &f)) return false;
         const tsr_gg_tensor * q = g.nodes[i]->src[0];
         if (q->nb[0] != 4 || q->nb[2] != 4ull * f.D || (f.T > 1 && q->nb[1] % 4 != 0))
-            return refuse("FLASH_ATTN_EXT: q's heads are not contiguous per token");
+            return refuse("FLASH_ATTN_EXT q-rows: each token's q heads contiguous, D floats apart [q %s]", dims(q).c_str());
         const uint64_t qs = f.T > 1 ? q->nb[1] / 4 : (uint64_t)f.H * f.D;
         void * qp = nullptr;
         std::string w2;
         if (!dev_ptr(d, q->data, ((size_t)(f.T - 1) * qs + (size_t)f.H * f.D) * 4, &qp, &w2))
-            return refuse("FLASH_ATTN_EXT: %s", w2.c_str());
+            return refuse("FLASH_ATTN_EXT device-q: q in device memory of this device (%s)", w2.c_str());
         Call & c = add(TSR_GG_CALL_FLASH_ATTN, i);
         fa_call_info(c, f, q->data, qs, g.nodes[i]->data);
         if (build) {
@@ -1639,6 +1898,10 @@ struct Lowerer {
         } else if (fo && gr.attn && T == 1u && fuse) {
             qkv_in = QkvIn{ (int)plan->calls.size() - 1, nullptr, nullptr, nullptr, 0.0f };
         }
+        if (qkv_in.call >= 0) {                            // what the attention call will read, and where
+            span(X, &qkv_in.x_lo, &qkv_in.x_hi);
+            span(NW, &qkv_in.w_lo, &qkv_in.w_hi);
+        }
         return true;
     }
     float * qkv_rows = nullptr;                            // the Q|K|V rows of the group being emitted
@@ -1650,6 +1913,7 @@ struct Lowerer {
         const float * x = nullptr;
         const float * nw = nullptr;
         float eps = 0.0f;
+        uint64_t x_lo = 0, x_hi = 0, w_lo = 0, w_hi = 0;   // ggml bytes of x and of the norm weight
     };
     QkvIn qkv_in;                                          // of the group being emitted
 
@@ -1658,16 +1922,16 @@ struct Lowerer {
         FaInfo f;
         if (!fa_info(g, gr.fa, &f)) return false;
         const tsr_gg_tensor * rq = gr.rq;
-        const int32_t n_dims = rq->op_params[1], mode = rq->op_params[2];
-        const float base = param_f32(rq, 5), attn = param_f32(rq, 8);
-        if (!(base > 0.0f) || !std::isfinite(base)) return refuse("ROPE: freq_base %g", base);
-        const tsr_gg_tensor * pos = rq->src[1];
-        if (mode == TSR_HIP_ROPE_IMROPE && strstr(pos->name, "inp_pos") == nullptr)
-            return refuse("IMROPE: the positions '%s' are not llama.cpp's inp_pos input", pos->name);
+        RopeFacts rf;                                          // the q rotation the call performs
+        if (!rope_rules(rq, &rf)) return false;
+        const int32_t n_dims = rf.n_dims, mode = rf.mode;
+        const float base = rf.base, attn = param_f32(rq, 8);
+        const tsr_gg_tensor * pos = rf.pos;
         void *pp = nullptr, *kp = nullptr;
         std::string w2;
         if (!dev_ptr(d, pos->data, 4 * (size_t)pos->ne[0], &pp, &w2) || !dev_ptr(d, gr.kidx->data, 8 * (size_t)gr.T, &kp, &w2))
-            return refuse("attention: %s", w2.c_str());
+            return refuse("attention device-inputs: positions and cell indices in device memory of this device (%s)",
+                          w2.c_str());
         const uint32_t T = gr.T, row = f.H * f.D + 2 * f.Hk * f.D;
         float * tab = nullptr;
         if (T == 1) {                                        // the token's angle table, once per graph
@@ -1702,6 +1966,12 @@ struct Lowerer {
             rc.info.scale = base;
             rc.info.add = gr.kidx->data;
         }
+        // the one-token Q|K|V MUL_MAT moves into this call only while its x and norm weight still hold at
+        // this node what they held at the MUL_MATs' place (no node in between writes them: ggml-alloc may
+        // give bytes whose last reader has run to a later node)
+        if (qkv_in.call >= 0 && (g.written_between(gr.mm_last, gr.fa, qkv_in.x_lo, qkv_in.x_hi) ||
+                                 g.written_between(gr.mm_last, gr.fa, qkv_in.w_lo, qkv_in.w_hi)))
+            qkv_in = QkvIn{};
         Call & c = add(TSR_GG_CALL_FLASH_ATTN, gr.fa);
         fa_call_info(c, f, 0, row, g.nodes[gr.fa]->data);
         if (T == 1 && qkv_in.call >= 0) plan->calls[qkv_in.call].info.flags |= TSR_GG_CALL_IN_NEXT;
@@ -1806,10 +2076,15 @@ struct Lowerer {
                 case TSR_GG_OP_ARGMAX: ok = argmax(g, i); break;
                 case TSR_GG_OP_SET_ROWS: ok = set_rows(g, i); break;
                 case TSR_GG_OP_FLASH_ATTN_EXT: ok = flash_attn(g, i); break;
-                case TSR_GG_OP_MUL: ok = refuse("MUL is on the device only behind an RMS_NORM whose only user it is"); break;
-                case TSR_GG_OP_SCALE: ok = refuse("SCALE is on the device only behind a MUL_MAT (its epilogue)"); break;
-                case TSR_GG_OP_UNARY: ok = refuse("TANH is on the device only inside a MUL_MAT's softcap"); break;
-                default: ok = refuse("op %d is not on the device", node->op); break;
+                case TSR_GG_OP_MUL:
+                    ok = refuse("MUL norm-weight: the weight multiply right behind an RMS_NORM it alone reads [%s]",
+                                dims(node).c_str());
+                    break;
+                case TSR_GG_OP_SCALE:
+                case TSR_GG_OP_UNARY:
+                    ok = refuse("SCALE/TANH epilogue: only as the tail of a MUL_MAT it alone reads [%s]", dims(node).c_str());
+                    break;
+                default: ok = refuse("op %d: not on the device (no kernel for it)", node->op); break;
             }
             if (!ok) {
                 *bad_node = i;
@@ -2197,6 +2472,35 @@ int tsr_gg_buffer_free(tsr_gg_buffer * b) {
     return TSR_GG_OK;
 }
 
+int tsr_gg_buffer_reset(tsr_gg_buffer * b) {
+    if (b == nullptr) return TSR_GG_E_ARG;
+    tsr_gg_dev * d = b->dev;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    if (b->mode == kUndecided) b->tensors.clear();
+    if (b->mode != kKv) {
+        const uint64_t lo = b->vbase, hi = b->vbase + b->size;
+        auto forget = [&](auto & m) {
+            for (auto it = m.lower_bound(lo); it != m.end() && it->first < hi;) it = m.erase(it);
+        };
+        forget(d->masks);
+        forget(d->shadows);
+    }
+    return TSR_GG_OK;
+}
+
+int tsr_gg_get_memory(tsr_gg_dev * d, size_t * free_bytes, size_t * total_bytes) {
+    if (d == nullptr || free_bytes == nullptr || total_bytes == nullptr) return TSR_GG_E_ARG;
+    std::lock_guard<std::recursive_mutex> lk(d->mtx);
+    *free_bytes = *total_bytes = 0;
+    if (d->ctx == nullptr) return TSR_GG_OK;
+    size_t f = 0, t = 0;
+    const int rc = tsr_hip_device_info(d->ctx, nullptr, nullptr, 0, &f, &t);
+    if (rc) return d->hip(rc, "device memory");
+    *free_bytes = f;
+    *total_bytes = t;
+    return TSR_GG_OK;
+}
+
 int tsr_gg_supports_op(tsr_gg_dev * d, const tsr_gg_tensor * op, char * why, size_t why_len) {
     if (d == nullptr || op == nullptr) return TSR_GG_E_ARG;
     std::lock_guard<std::recursive_mutex> lk(d->mtx);
@@ -2208,10 +2512,13 @@ int tsr_gg_supports_op(tsr_gg_dev * d, const tsr_gg_tensor * op, char * why, siz
     const tsr_gg_tensor * s0 = op->src[0];
     if (op->op == TSR_GG_OP_MUL) {
         const tsr_gg_tensor * o = s0 && s0->op == TSR_GG_OP_RMS_NORM ? op->src[1] : (op->src[1] && op->src[1]->op == TSR_GG_OP_RMS_NORM ? s0 : nullptr);
-        if (o == nullptr) { ok = false; w = "MUL is on the device only behind an RMS_NORM (its weight)"; }
-        else if (o->type != TSR_GG_TYPE_F32 || o->ne[0] != op->ne[0] || !same_shape(op, op->src[0] == o ? op->src[1] : s0)) {
+        if (o == nullptr) {
             ok = false;
-            w = "RMS_NORM + MUL: the weight is not an f32 row of the norm's width";
+            w = "MUL norm-weight: the weight multiply of an RMS_NORM's output, the only MUL the device runs [" +
+                dims(op->src[0]) + " * " + dims(op->src[1]) + "]";
+        } else if (o->type != TSR_GG_TYPE_F32 || o->ne[0] != op->ne[0] || !same_shape(op, op->src[0] == o ? op->src[1] : s0)) {
+            ok = false;
+            w = "MUL norm-weight: an f32 weight row as wide as the normalized rows [" + dims(o) + "]";
         }
     } else if (op->op == TSR_GG_OP_SCALE || op->op == TSR_GG_OP_UNARY) {
         const bool tanh_ok = op->op == TSR_GG_OP_SCALE || op->op_params[0] == TSR_GG_UNARY_TANH;
@@ -2219,7 +2526,8 @@ int tsr_gg_supports_op(tsr_gg_dev * d, const tsr_gg_tensor * op, char * why, siz
         while (up && (up->op == TSR_GG_OP_SCALE || up->op == TSR_GG_OP_UNARY)) up = up->src[0];
         if (!tanh_ok || up == nullptr || up->op != TSR_GG_OP_MUL_MAT || (op->op == TSR_GG_OP_SCALE && param_f32(op, 1) != 0.0f)) {
             ok = false;
-            w = "SCALE / TANH are on the device only as a MUL_MAT's epilogue (SCALE, or SCALE TANH SCALE)";
+            w = "SCALE/TANH epilogue: only as the tail of a MUL_MAT, a SCALE or a softcap SCALE-TANH-SCALE chain [" +
+                dims(op) + "]";
         }
     } else {
         Plan p;

@@ -40,7 +40,7 @@ EXPORTS = (
     "tsr_gg_buffer_memset_tensor", "tsr_gg_buffer_clear", "tsr_gg_buffer_free", "tsr_gg_buffer_mode",
     "tsr_gg_supports_op", "tsr_gg_graph_compute", "tsr_gg_synchronize", "tsr_gg_get_stats", "tsr_gg_lower",
     "tsr_gg_kv_parse_name", "tsr_gg_graph_key", "tsr_gg_quantize_q8_0", "tsr_gg_set_options",
-    "tsr_gg_buffer_cpy_tensor",
+    "tsr_gg_buffer_cpy_tensor", "tsr_gg_buffer_reset", "tsr_gg_get_memory",
 )
 OPT_NO_FUSION = 1
 
@@ -117,6 +117,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "tsr_gg_buffer_get_tensor": ([vp, TP, vp, sz, sz], C.c_int),
         "tsr_gg_buffer_memset_tensor": ([vp, TP, C.c_uint8, sz, sz], C.c_int),
         "tsr_gg_buffer_clear": ([vp, C.c_uint8], C.c_int),
+        "tsr_gg_buffer_reset": ([vp], C.c_int),
+        "tsr_gg_get_memory": ([vp, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)], C.c_int),
         "tsr_gg_buffer_free": ([vp], C.c_int),
         "tsr_gg_buffer_mode": ([vp], C.c_int),
         "tsr_gg_supports_op": ([vp, TP, C.c_char_p, sz], C.c_int),
@@ -210,6 +212,10 @@ class Buffer:
     def clear(self, value: int = 0) -> None:
         self.dev.check(self.dev.L.tsr_gg_buffer_clear(self.h, value), "clear")
 
+    def reset(self) -> None:
+        """ggml-alloc lays the buffer out anew (buffer_i.reset)."""
+        self.dev.check(self.dev.L.tsr_gg_buffer_reset(self.h), "reset")
+
     def free(self) -> None:
         if self.h:
             self.dev.L.tsr_gg_buffer_free(self.h)
@@ -247,6 +253,12 @@ class Device:
 
     def alloc_size(self, t: Tensor) -> int:
         return int(self.L.tsr_gg_alloc_size(self.h, C.byref(t)))
+
+    def memory(self) -> tuple:
+        """(free, total) bytes of the device's memory (device_i.get_memory)."""
+        f, t = C.c_size_t(), C.c_size_t()
+        self.check(self.L.tsr_gg_get_memory(self.h, C.byref(f), C.byref(t)), "get_memory")
+        return int(f.value), int(t.value)
 
     def register_type(self, name: str, blck: int, tsize: int, to_float) -> int:
         cb = TO_FLOAT(to_float)

@@ -140,18 +140,18 @@ def test_supports_op_mul_mat():
     p.ok(p.node(c.mul_mat(w, x)))
     p.ok(p.node(c.mul_mat(p.w(G.Q8_0, [896, 64], "w80"), p.a(G.F32, [896, 1]))))
     p.ok(p.node(c.mul_mat(p.w(G.F16, [128, 32], "w16"), p.a(G.F32, [128, 2]))))      # converted to Q8_0
-    p.no(p.node(c.mul_mat(w, p.a(G.F16, [4096, 7]))), "src1 must be f32")
-    p.no(p.node(c.mul_mat(p.w(G.F32, [96 + 16, 8], "odd"), p.a(G.F32, [112, 1]))), "K % 32")
-    p.no(p.node(c.mul_mat(p.w(G.Q8_0, [32768 + 32, 2], "big"), p.a(G.F32, [32800, 1]))), "K_MAX")
-    p.no(p.node(c.mul_mat(p.a(G.Q8_0, [4096, 16], "wact"), p.a(G.F32, [4096, 1]))), "not a weight")
-    p.no(p.node(c.mul_mat(p.w(G.Q8_0, [64, 8, 2], "batched"), p.a(G.F32, [64, 1, 2]))), "batch of matrices")
-    p.no(p.node(c.mul_mat(p.w(G.I32, [64, 8], "ints"), p.a(G.F32, [64, 1]))), "not loadable")
+    p.no(p.node(c.mul_mat(w, p.a(G.F16, [4096, 7]))), "MUL_MAT f32-io")
+    p.no(p.node(c.mul_mat(p.w(G.F32, [96 + 16, 8], "odd"), p.a(G.F32, [112, 1]))), "MUL_MAT k-range")
+    p.no(p.node(c.mul_mat(p.w(G.Q8_0, [32768 + 32, 2], "big"), p.a(G.F32, [32800, 1]))), "MUL_MAT k-range.*K_MAX")
+    p.no(p.node(c.mul_mat(p.a(G.Q8_0, [4096, 16], "wact"), p.a(G.F32, [4096, 1]))), "MUL_MAT weight-home")
+    p.no(p.node(c.mul_mat(p.w(G.Q8_0, [64, 8, 2], "batched"), p.a(G.F32, [64, 1, 2]))), "MUL_MAT matrix")
+    p.no(p.node(c.mul_mat(p.w(G.I32, [64, 8], "ints"), p.a(G.F32, [64, 1]))), "MUL_MAT device-format")
     xt = p.node(c.permute(p.a(G.F32, [64, 4]), 1, 0, 2, 3))
-    p.no(p.node(c.mul_mat(p.w(G.F32, [4, 64], "w4"), xt)), "not contiguous")
+    p.no(p.node(c.mul_mat(p.w(G.F32, [4, 64], "w4"), xt)), "MUL_MAT dense")
     # a src1 view that is not 64-byte aligned
     big = p.a(G.F32, [64 * 3 + 8])
     v = p.node(c.view(big, [64, 1], [256], 8 * 4))
-    p.no(p.node(c.mul_mat(p.w(G.F32, [64, 8], "w64"), v)), "64-byte aligned")
+    p.no(p.node(c.mul_mat(p.w(G.F32, [64, 8], "w64"), v)), "MUL_MAT x-aligned")
     p.dev.close()
 
 
@@ -174,24 +174,24 @@ def test_supports_op_flash_attn():
     p.ok(fa_graph(p))
     p.ok(fa_graph(p, T=64))
     p.ok(fa_graph(p, mask_type=None))
-    p.no(fa_graph(p, q_type=G.F16), "q F32")
-    p.no(fa_graph(p, max_bias=8.0), "ALiBi")
-    p.no(fa_graph(p, softcap=30.0), "softcap")
-    p.no(fa_graph(p, mask_type=G.F32), "mask is not F16")
-    p.no(fa_graph(p, T=681), "681 tokens")
-    p.no(fa_graph(p, H=9), "n_head % n_head_kv")
+    p.no(fa_graph(p, q_type=G.F16), "FLASH_ATTN_EXT types: q F32")
+    p.no(fa_graph(p, max_bias=8.0), "FLASH_ATTN_EXT plain-softmax.*max_bias=8")
+    p.no(fa_graph(p, softcap=30.0), "FLASH_ATTN_EXT plain-softmax.*softcap=30")
+    p.no(fa_graph(p, mask_type=G.F32), "FLASH_ATTN_EXT mask:")
+    p.no(fa_graph(p, T=681), "FLASH_ATTN_EXT rows:.*T=681")
+    p.no(fa_graph(p, H=9), "FLASH_ATTN_EXT gqa")
     t = fa_graph(p)
     t.src[4] = t.src[0]
-    p.no(t, "sinks")
+    p.no(t, "FLASH_ATTN_EXT no-sinks")
     # K / V from a weights buffer, not a KV cache
     c = p.c
     q = p.node(c.permute(p.a(G.F32, [128, 8, 1]), 0, 2, 1, 3))
     kw = p.w(G.Q8_0, [128, 256, 2], "cache_k_l0")
-    p.no(p.node(c.flash_attn_ext(q, kw, kw, None, 0.1)), "not a KV cache view")
+    p.no(p.node(c.flash_attn_ext(q, kw, kw, None, 0.1)), "FLASH_ATTN_EXT kv-views")
     # V and K swapped
     t = fa_graph(p)
     t.src[1], t.src[2] = t.src[2], t.src[1]
-    p.no(t, "K and V planes")
+    p.no(t, "FLASH_ATTN_EXT one-layer")
     p.dev.close()
 
 
@@ -202,36 +202,36 @@ def test_supports_op_glue():
     n = p.node(c.rms_norm(x, 1e-5))
     p.ok(n)
     p.ok(p.node(c.mul(n, p.w(G.F32, [256], "norm.weight"))))
-    p.no(p.node(c.mul(x, p.a(G.F32, [256, 4]))), "behind an RMS_NORM")
+    p.no(p.node(c.mul(x, p.a(G.F32, [256, 4]))), "MUL norm-weight")
     p.ok(p.node(c.add(x, p.a(G.F32, [256, 4]))))
     p.ok(p.node(c.add(x, p.a(G.F32, [256, 1]))))
-    p.no(p.node(c.add(x, p.a(G.F32, [256, 3]))), "broadcast by whole rows")
+    p.no(p.node(c.add(x, p.a(G.F32, [256, 3]))), "ADD row-broadcast")
     g, u = p.a(G.F32, [128, 2]), p.a(G.F32, [128, 2])
     p.ok(p.node(c.swiglu_split(g, u)))
     geglu = p.node(c.swiglu_split(g, u))
     geglu.op_params[0] = 1
-    p.no(geglu, "SWIGLU")
+    p.no(geglu, "GLU swiglu")
     pos = p.a(G.I32, [4], "inp_pos")
     h = p.a(G.F32, [64, 4, 4])
     p.ok(p.node(c.rope_ext(h, pos, 64, 0, 10000.0)))
     p.ok(p.node(c.rope_ext(h, pos, 32, 2, 10000.0)))
-    p.no(p.node(c.rope_ext(h, pos, 64, 8, 10000.0)), "mode 8")
-    p.no(p.node(c.rope_ext(h, pos, 64, 0, 10000.0, ext_factor=1.0)), "YaRN")
+    p.no(p.node(c.rope_ext(h, pos, 64, 8, 10000.0)), "ROPE mode:.*mode=8")
+    p.no(p.node(c.rope_ext(h, pos, 64, 0, 10000.0, ext_factor=1.0)), "ROPE no-yarn")
     emb = p.w(G.F32, [256, 1000], "token_embd.weight")
     ids = p.a(G.I32, [3], "inp_tokens")
     p.ok(p.node(c.get_rows(emb, ids)))
-    p.no(p.node(c.get_rows(p.w(G.Q4_K, [256, 1000], "token_embd.q"), ids)), "not f32 rows")
+    p.no(p.node(c.get_rows(p.w(G.Q4_K, [256, 1000], "token_embd.q"), ids)), "table .* is not f32 rows")
     lg = p.a(G.F32, [1000, 2])
     p.ok(p.node(c.argmax(lg)))
     mm = p.node(c.mul_mat(p.w(G.Q8_0, [256, 64], "wo"), x))
     p.ok(p.node(c.scale(mm, 0.5)))
-    p.no(p.node(c.scale(x, 0.5)), "epilogue")
-    p.no(p.node(c.tanh(x)), "epilogue")
+    p.no(p.node(c.scale(x, 0.5)), "SCALE/TANH epilogue")
+    p.no(p.node(c.tanh(x)), "SCALE/TANH epilogue")
     rows = p.a(G.F32, [256, 4])
     idx = p.a(G.I64, [4], "k_idxs")
     p.ok(p.node(c.set_rows(p.kc, rows, idx)))
-    p.no(p.node(c.set_rows(p.a(G.F32, [256, 16]), rows, idx)), "does not write a KV cache")
-    p.no(p.node(c.set_rows(p.kc, rows, p.a(G.I32, [4]))), "I64")
+    p.no(p.node(c.set_rows(p.a(G.F32, [256, 16]), rows, idx)), "SET_ROWS kv-dest")
+    p.no(p.node(c.set_rows(p.kc, rows, p.a(G.I32, [4]))), "SET_ROWS i64-cells")
     for op in (G.OP_VIEW, G.OP_RESHAPE, G.OP_PERMUTE, G.OP_TRANSPOSE, G.OP_NONE):
         t = p.a(G.F32, [4])
         t.op = op
@@ -357,6 +357,31 @@ def test_lower_llama_graph_fused(T):
     p.dev.close()
 
 
+def test_qkv_stays_a_call_when_x_is_overwritten_before_attention():
+    """The one-token Q|K|V MUL_MAT runs inside its FLASH_ATTN_EXT call only while its x (the norm's
+    input) is unchanged at that node: with a node between the two writing x's bytes (ggml-alloc reusing
+    them), that layer keeps the MUL_MAT as its own call, and the other layers are unchanged."""
+    cfg = LL.tiny_config()
+    p = Probe()
+    p.kvbuf = p.dev.buffer(1 << 24)
+    p.koff = 0
+    W, caches = declare_model(p, cfg, 512)
+    g = GL.LlamaGraph(p.dev, cfg, W, caches, 512, 1, 256, argmax=True)
+    nodes = g.ctx.nodes
+
+    def qkv_flags():
+        calls = p.dev.lower(nodes)
+        return [bool(c["flags"] & G.CALL_IN_NEXT) for c in calls
+                if c["name"] == "MUL_MAT" and c["N"] == cfg.n_head * cfg.head_dim + 2 * cfg.E]
+
+    assert qkv_flags() == [True] * cfg.n_layer
+    x0 = next(t for t in nodes if t.name.startswith(b"inp_embd"))
+    rk = next(t for t in nodes if t.op == G.OP_ROPE and t.name.startswith(b"Kcur-0"))
+    rk.data = x0.data                                    # layer 0's K rotation lands on x
+    assert qkv_flags() == [False] + [True] * (cfg.n_layer - 1)
+    p.dev.close()
+
+
 def test_fusion_refused_when_the_result_overlaps_an_input():
     """MUL_MAT + ADD is fused only when the fused result does not overlap src1 (the fused record writes
     the ADD's result while src1 is read: tsr-build.h's "not read or written in between")."""
@@ -421,6 +446,35 @@ def test_graph_key_identity():
     assert build(512) != a
     assert build(256, eps=1e-3) != a
     assert G.graph_key([], 1) != G.graph_key([], 2)
+
+
+def test_buffer_reset_forgets_the_announced_layout():
+    """buffer_i.reset (ggml-tesseract.cpp:2015-2024): a buffer laid out anew before its storage is
+    decided is decided from the tensors announced after the reset only. Here the tensors announced
+    after it are two KV caches, so the buffer becomes KV planes; the same announcements without the
+    reset (a stray f32 tensor before them) give device memory. A probe device reports no memory."""
+    dev = G.Device(-1)
+    c = GL.Ctx()
+    assert dev.memory() == (0, 0)
+    wb = dev.buffer(1 << 20, G.USAGE_WEIGHTS)
+    wt = c.new(G.Q8_0, [256, 16], "w")
+    c.place(wt, wb, 0)
+    modes = []
+    for reset in (True, False):
+        b = dev.buffer(1 << 20)
+        c.place(c.new(G.F32, [256], "stray"), b, 0)
+        if reset:
+            b.reset()
+        off = c.place(c.new(G.Q8_0, [256, 64, 1], "cache_k_l0"), b, 0)
+        c.place(c.new(G.Q8_0, [256, 64, 1], "cache_v_l0"), b, off)
+        assert b.mode == G.MODE_UNDECIDED
+        x = c.new(G.F32, [256, 1], "x")                  # not announced: its address only
+        x.data, x.buffer = b.base, b.h
+        ok, why = dev.supports_op(c.mul_mat(wt, x))      # reading x's bytes decides the buffer's storage
+        assert not ok
+        modes.append(b.mode)
+    assert modes == [G.MODE_KV, G.MODE_LINEAR]
+    dev.close()
 
 
 def test_probe_device_has_no_memory():

@@ -313,3 +313,32 @@ def test_device_flag_reported(gdev):
     assert (img[3] != 0).any() and (np.delete(img, 3, axis=0) == 0).all()
     cbuf.free()
     kvbuf.free()
+
+
+def test_reset_compute_buffer_forgets_mask_summaries(gdev, oc):
+    """buffer_i.reset of the compute buffer (ggml-tesseract.cpp:2015-2024): the mask summaries and cell
+    index copies kept for its addresses are forgotten, so a graph_compute whose mask was not written
+    again since fails (TSR_GG_E_UNSUPPORTED) instead of planning FLASH_ATTN_EXT from an earlier
+    layout's summary; with the inputs written again the token is the oracle's, bit for bit. Also
+    device_i.get_memory of the GPU."""
+    free_b, total_b = gdev.memory()
+    assert 0 < free_b <= total_b and total_b > 100 << 30
+    cfg, kv_size, hist = LL.tiny_config(), 512, 100
+    w = LL.SyntheticWeights(cfg, cache=True)
+    ref = oracle_model(oc, cfg, w, kv_size, hist)
+    _, W, caches, wbuf, kvbuf = GL.load_model(gdev, cfg, w, kv_size, history_images(ref, cfg, hist))
+    g = GL.LlamaGraph(gdev, cfg, W, caches, kv_size, 1, 256, argmax=True)
+    ts = ts_of(cfg)
+    g.set_inputs([7], hist)
+    gdev.graph_compute(g.ctx.nodes)
+    assert_bits_equal(g.logits_host(), ref.step(7, hist, ts, 256), "before the reset")
+    g.buf.reset()
+    with pytest.raises(G.GGError) as e:
+        gdev.graph_compute(g.ctx.nodes)
+    assert e.value.code == G.E_UNSUPPORTED and "mask" in str(e.value)
+    g.set_inputs([9], hist + 1)
+    gdev.graph_compute(g.ctx.nodes)
+    assert_bits_equal(g.logits_host(), ref.step(9, hist + 1, ts, 256), "after the reset, inputs written again")
+    gdev.synchronize()
+    for x in (g, kvbuf, wbuf):
+        x.free()

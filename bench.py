@@ -69,6 +69,8 @@ class HipEvents:
         self.h.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
         self.h.hipGraphExecDestroy.argtypes = [C.c_void_p]
         self.h.hipGraphDestroy.argtypes = [C.c_void_p]
+        # device pointers are 64-bit: without argtypes ctypes would pass them as (truncated) C ints
+        self.h.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
 
     def event(self):
         e = C.c_void_p()
@@ -273,7 +275,7 @@ def e2e_decode(dev, ev, steps: int, warmup: int, eager: bool = False) -> dict:
     return out
 
 
-def cpu_decode(e2e: dict, max_seconds: float = 12.0, max_tokens: int = 4) -> dict:
+def cpu_decode(e2e: dict, max_seconds: float = 40.0, max_tokens: int = 5) -> dict:
     """The oracle's decode of the same model (the reference numerics restated in C, MUL_MAT on all the
     host cores available, up to 16) from the same cache state (the GPU's prefilled cache bytes, read
     back): token 0 at position CTX with the same first id, then the oracle's own greedy tokens, for
@@ -320,7 +322,7 @@ def cpu_decode(e2e: dict, max_seconds: float = 12.0, max_tokens: int = 4) -> dic
         tok, n = nxt, n + 1
         if sum(times) >= max_seconds:
             break
-    per = float(np.mean(times))
+    per = float(np.median(times))
     # the same first token on one thread (position CTX again: it rewrites its cell with the same rows)
     ref.threads = 1
     t0 = time.perf_counter()
@@ -330,7 +332,8 @@ def cpu_decode(e2e: dict, max_seconds: float = 12.0, max_tokens: int = 4) -> dic
     return {"value": round(1.0 / per, 4), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": (f"{n} decode tokens of the same Llama-3-8B-arch Q4_K model at positions {CTX}..{CTX + n - 1} "
                        f"by oracle/oracle_llama.py over oracle/oc_*.c ({threads} threads in MUL_MAT), "
-                       f"{per:.2f} s per token"),
+                       f"median {per:.2f} s per token"),
+            "statistic": f"median of {n} tokens",
             "single_thread": {"value": round(1.0 / one_s, 4), "unit": "tok/s", "cores": 1,
                               "sample": f"token 0 again at position {CTX} on one thread, {one_s:.2f} s",
                               "token0_logits_bit_equal": one_equal},
@@ -338,6 +341,107 @@ def cpu_decode(e2e: dict, max_seconds: float = 12.0, max_tokens: int = 4) -> dic
             "ggml_cpu": "not measured (unavailable offline: llama.cpp/ggml is an un-vendored submodule)",
             "parity": {"token0_logits_bit_equal": logits_equal, "greedy_tokens_equal": bool(same_tokens),
                        "tokens_compared": n}}
+
+
+def cpu_configs(threads: int, runs: int = 5) -> dict:
+    """The oracle (the reference's numerics restated in C, oracle/oc_*.c) on BASELINE configs[0]-[3]'s
+    workloads, drawn from the same seeds as the GPU legs under "also", on the host cores: each at one
+    thread and at `threads` threads, the median of `runs` timed runs after one untimed run. MUL_MAT is
+    threaded over output rows (like the reference's mvm_rows pool, sw/sim/tsr_sim.c:1608-1647); the
+    causal prefill FLASH_ATTN_EXT over query rows (each row is planned and computed on its own, so the
+    row blocks give the whole call's bits); the decode FLASH_ATTN_EXT is one sequential call (its chunk
+    plan depends on all of a token's KV heads: a split by head would be another computation). The
+    prefill MUL_MATs time a sample of 32 of the 512 token rows (rows are independent) and report the
+    full call's rate."""
+    import concurrent.futures as cf
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle
+    oc = oracle.Oracle()
+
+    def med(fn):
+        t0 = time.perf_counter()
+        fn()
+        first = time.perf_counter() - t0
+        ts = [first] if first > 0.25 else []       # a long run is its own warm-up: it counts
+        while len(ts) < runs:
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    def both(fn_of_threads, unit_of):
+        r = {}
+        for th in sorted({1, threads}):
+            s = med(lambda: fn_of_threads(th))
+            r[f"threads_{th}"] = {"seconds": round(s, 6), **unit_of(s)}
+        return r
+
+    out = {"runs": runs, "statistic": "median", "kind": "port", "threads_all": threads, "host": host_info()}
+    # configs[0]: Q8_0 matvec 4864 x 896 (the GPU leg's seeds)
+    N, K = 4864, 896
+    w = S.quant_rows(0, S.seed_of("cfg1", "w"), N, K)
+    x = S.normal(S.seed_of("cfg1", "x"), K)
+    nb = N * (K // 32) * 34 + 4 * K + 4 * N
+    out["q8_0_matvec_4864x896"] = both(lambda th: oc.mul_mat(0, w, K, x, threads=th),
+                                       lambda s: {"us_per_call": round(s * 1e6, 1), "GB/s": round(nb / s / 1e9, 3)})
+    # configs[1]: Q4_K up 14336 x 4096 then down 4096 x 14336
+    up = S.quant_rows(1, S.seed_of("cfg2", "w_up"), 14336, 4096)
+    dn = S.quant_rows(1, S.seed_of("cfg2", "w_down"), 4096, 14336)
+    xu = S.normal(S.seed_of("cfg2", "x"), 4096)
+
+    def pair(th):
+        h = oc.mul_mat(1, up, 4096, xu, threads=th)
+        oc.mul_mat(1, dn, 14336, h, threads=th)
+    nb = 2 * (14336 * 16 * 144) + 4 * (4096 + 14336) * 2
+    out["ffn_pair_q4k_14336x4096_4096x14336"] = both(pair, lambda s: {"us_per_step": round(s * 1e6, 1),
+                                                                      "GB/s": round(nb / s / 1e9, 3)})
+    del up, dn
+    # configs[2]: FLASH_ATTN_EXT decode, 8192 cells, 32 q / 8 KV heads, D 128
+    n_kv, E = 8192, 1024
+    kc = np.zeros((n_kv, E // 32 * 34), np.uint8)
+    vc = np.zeros_like(kc)
+    oc.kv_set_rows(kc, S.normal(S.seed_of("cfg3", "k"), n_kv * E).reshape(n_kv, E), np.arange(n_kv))
+    oc.kv_set_rows(vc, S.normal(S.seed_of("cfg3", "v"), n_kv * E).reshape(n_kv, E), np.arange(n_kv))
+    q = S.normal(S.seed_of("cfg3", "q"), 32 * 128).astype(np.float16).astype(np.float32).reshape(1, -1)
+    ms = oc.msum(np.zeros((1, n_kv), np.float16))
+    scale = np.float32(1.0 / np.sqrt(128))
+    s = med(lambda: oc.flash_attn(q, kc, vc, 128, 32, 8, scale, ms))
+    nb = 2 * n_kv * E // 32 * 34 + 2 * 32 * 128 + 4 * 32 * 128
+    out["fa_decode_q8kv_8192_32q8kv_d128"] = {"threads_1": {"seconds": round(s, 6), "us_per_call": round(s * 1e6, 1),
+                                                            "GB/s": round(nb / s / 1e9, 3)},
+                                              "note": "one sequential call (the plan spans all KV heads)"}
+    del kc, vc
+    # configs[3]: prefill MUL_MATs (a 32-row sample of the 512 token rows) and the causal FA over 512 tokens
+    T, K, Ts = 512, 4096, 32
+    xs = S.normal(S.seed_of("cfg4", "x"), T * K).reshape(T, K)[:: T // Ts][:Ts]
+    for name, N in (("prefill_q8_0_512x4096x4096", 4096), ("prefill_q8_0_512x14336x4096", 14336)):
+        w = S.quant_rows(0, S.seed_of("cfg4", "w_" + str(N)), N, K)
+        ops = 2 * T * N * K
+        out[name] = both(lambda th: oc.mul_mat(0, w, K, xs, threads=th),
+                         lambda s, ops=ops: {"seconds_per_512_rows": round(s * T / Ts, 4),
+                                             "int8_GOPS": round(ops / (s * T / Ts) / 1e9, 2)})
+        out[name]["sample"] = f"{Ts} of the {T} token rows (every {T // Ts}th)"
+        del w
+    T, E = 512, 1024
+    kc = np.zeros((T, E // 32 * 34), np.uint8)
+    vc = np.zeros_like(kc)
+    oc.kv_set_rows(kc, S.normal(S.seed_of("cfg4", "fa_k"), T * E).reshape(T, E), np.arange(T))
+    oc.kv_set_rows(vc, S.normal(S.seed_of("cfg4", "fa_v"), T * E).reshape(T, E), np.arange(T))
+    qp = S.normal(S.seed_of("cfg4", "fa_q"), T * 4096).reshape(T, 4096).astype(np.float16).astype(np.float32)
+    mask = np.full((T, T), -np.inf, np.float16)
+    mask[np.tril_indices(T)] = 0
+
+    def fa_rows(th):
+        cuts = np.linspace(0, T, th + 1).astype(int)
+        blocks = [(a, b) for a, b in zip(cuts[:-1], cuts[1:]) if b > a]
+        run = lambda ab: oc.flash_attn(qp[ab[0]:ab[1]], kc, vc, 128, 32, 8, scale, oc.msum(mask[ab[0]:ab[1]]), None,
+                                       [[0, T]])
+        if len(blocks) == 1:
+            return run(blocks[0])
+        with cf.ThreadPoolExecutor(len(blocks)) as ex:        # ctypes calls release the GIL
+            return list(ex.map(run, blocks))
+    out["fa_prefill_causal_512_32q8kv_d128"] = both(fa_rows, lambda s: {"ms_per_call": round(s * 1e3, 2)})
+    return out
 
 
 def host_info() -> dict:
@@ -611,7 +715,6 @@ def pmc_child(reps: int = 3) -> int:
     wts = LL.SyntheticWeights(cfg)
     dev = tsr_hip.Device(0)
     ev = HipEvents()
-    ev.h.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
     src, dst = dev.alloc(COPY_BYTES), dev.alloc(COPY_BYTES)
     src.fill(1)
     gu = np.stack([wts.quant("blk.0.ffn_gate.weight", cfg.n_ff, cfg.n_embd, cfg.wfmt),
@@ -655,6 +758,103 @@ def pmc_child(reps: int = 3) -> int:
     plan.free()
     dev.close()
     return 0
+
+
+# BASELINE configs[0]-[2] in the configs counter child: (name, kernel substring, algorithmic bytes per launch)
+PMC_CONFIGS = [("q8_0_matvec_4864x896", "k_mv_q80", 4864 * 28 * 34 + 4 * 896 + 4 * 4864),
+               ("q4k_up_14336x4096", "k_mv_q4k", 14336 * 16 * 144 + 4 * 4096 + 4 * 14336),
+               ("q4k_down_4096x14336", "k_mv_q4k", 4096 * 56 * 144 + 4 * 14336 + 4 * 4096),
+               ("fa_decode_q8kv_8192_32q8kv_d128", "k_fa_dec", 2 * 8192 * 1024 // 32 * 34 + 2 * 4096 + 4 * 4096)]
+
+
+def pmc_configs_child(reps: int = 3) -> int:
+    """Counter child for BASELINE configs[0]-[2] (run under rocprofv3 --pmc): the calibration copy, then
+    `reps` launches each, over device copies that rotate (no launch finds its bytes in a cache the one
+    before filled), of the Q8_0 matvec 4864 x 896, the Q4_K up 14336 x 4096 and down 4096 x 14336
+    matvecs, and the planned FLASH_ATTN_EXT decode at 8192 cells (one k_fa_dec launch), with the seeds
+    of the timed legs."""
+    dev = tsr_hip.Device(0)
+    ev = HipEvents()
+    src, dst = dev.alloc(COPY_BYTES), dev.alloc(COPY_BYTES)
+    src.fill(1)
+    dev.sync()
+    for _ in range(reps):
+        assert ev.h.hipMemcpyAsync(dst.ptr, src.ptr, COPY_BYTES, 3, dev.stream) == 0
+    ev.device_sync()
+    src.free()
+    dst.free()
+    w8 = S.quant_rows(0, S.seed_of("cfg1", "w"), 4864, 896)
+    ws = [dev.weight(0, w8, 4864, 896) for _ in range(reps)]
+    xb, yb = dev.upload(S.normal(S.seed_of("cfg1", "x"), 896)), dev.alloc(4 * 14336)
+    for i in range(reps):
+        dev.mul_mat(ws[i], xb, 1, 896, yb, 4864)
+    dev.sync()
+    del ws
+    for name, N, K in (("w_up", 14336, 4096), ("w_down", 4096, 14336)):
+        blocks = S.quant_rows(1, S.seed_of("cfg2", name), N, K)
+        ws = [dev.weight(1, blocks, N, K) for _ in range(reps)]
+        xk = dev.upload(S.normal(S.seed_of("cfg2", "x" + name), K))
+        for i in range(reps):
+            dev.mul_mat(ws[i], xk, 1, K, yb, N)
+        dev.sync()
+        del ws
+    n_kv, E, n_head, D = 8192, 1024, 32, 128
+    idx = dev.upload(np.arange(n_kv, dtype=np.int64))
+    caches = []
+    for i in range(reps):
+        kc, vc = dev.kv(E, n_kv), dev.kv(E, n_kv)
+        for which, kv in ((0, kc), (1, vc)):
+            rows = dev.upload(S.normal(S.seed_of("cfg3", "kv"[which]), n_kv * E))
+            dev.kv_set_rows(kv, which, rows, n_kv, E, idx)
+            rows.free()
+        caches.append((kc, vc))
+    qb = dev.upload(S.normal(S.seed_of("cfg3", "q"), n_head * D).astype(np.float16).astype(np.float32))
+    ob = dev.alloc(4 * n_head * D)
+    plan = dev.fa_plan(D, n_head, 8, 1, n_kv)
+    plan.set(tsr_hip.msum_build_f16(np.zeros((1, n_kv), np.float16)))
+    for i in range(reps):
+        dev.flash_attn_plan(plan, qb, n_head * D, caches[i][0], caches[i][1], np.float32(1.0 / np.sqrt(D)), ob, n_head * D)
+    dev.sync()
+    assert dev.get_flags() == 0
+    plan.free()
+    dev.close()
+    return 0
+
+
+def measure_config_traffic(reps: int = 3) -> dict:
+    """HBM bytes per launch of the configs[0]-[2] kernels: FETCH_SIZE and WRITE_SIZE (two rocprofv3
+    --pmc passes over the configs child), each scaled by the counter's reading for the calibration copy;
+    with each kernel's algorithmic bytes and their ratio."""
+    if shutil.which("rocprofv3") is None:
+        return {"error": "rocprofv3 not found"}
+    workdir = tempfile.mkdtemp(prefix="tsr_pmc_")
+    try:
+        res = {name: {"algorithmic_bytes": ab} for name, _, ab in PMC_CONFIGS}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            rows = _pmc_pass(counter, workdir, "--pmc-configs-child")
+            copy = sorted((v for _, k, v in rows if "copyBuffer" in k), reverse=True)[:reps]
+            cal = COPY_BYTES / (float(np.median(copy)) * 1024.0)
+            seen = {}
+            for _, k, v in rows:
+                for name, kern, _ in PMC_CONFIGS:
+                    if kern in k:
+                        seen.setdefault(kern, []).append(v)
+                        break
+            q4 = seen.get("k_mv_q4k", [])
+            per = {"q8_0_matvec_4864x896": seen.get("k_mv_q80", []), "q4k_up_14336x4096": q4[:reps],
+                   "q4k_down_4096x14336": q4[reps:], "fa_decode_q8kv_8192_32q8kv_d128": seen.get("k_fa_dec", [])}
+            for name, vals in per.items():
+                if len(vals) != reps:
+                    raise RuntimeError(f"{counter}: {name}: {len(vals)} dispatches")
+                res[name][counter] = round(float(np.median(vals)) * 1024.0 * cal)
+            res["calibration_" + counter] = round(cal, 4)
+        for name, _, ab in PMC_CONFIGS:
+            r = res[name]
+            r["traffic"] = r["FETCH_SIZE"] + r["WRITE_SIZE"]
+            r["traffic_ratio"] = round(r["traffic"] / ab, 4)
+        return res
+    finally:
+        shutil.rmtree(workdir, ignore_errors=True)
 
 
 def _pmc_pass(counter: str, workdir: str, child: str = "--pmc-child") -> list:
@@ -774,9 +974,12 @@ def main() -> int:
     ap.add_argument("--no-adapter", action="store_true", help="skip the decode through the ggml-backend adapter")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--pmc-prefill-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--pmc-configs-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.pmc_child:
         return pmc_child()
+    if args.pmc_configs_child:
+        return pmc_configs_child()
     if args.pmc_prefill_child:
         return pmc_prefill_child()
     if args.gpus != 1:
@@ -788,7 +991,7 @@ def main() -> int:
         return 2
 
     # traffic passes first: child processes under rocprofv3, before this process touches the GPU
-    traffic = prefill_counters = None
+    traffic = prefill_counters = config_traffic = None
     if not args.no_traffic:
         try:
             traffic = measure_traffic()
@@ -799,6 +1002,10 @@ def main() -> int:
                 prefill_counters = measure_prefill_counters()
             except Exception as e:
                 prefill_counters = {"error": str(e)[:300]}
+            try:
+                config_traffic = measure_config_traffic()
+            except Exception as e:
+                config_traffic = {"error": str(e)[:300]}
 
     dev = tsr_hip.Device(0)
     info = dev.info()
@@ -829,9 +1036,14 @@ def main() -> int:
     also = {} if args.no_extra else extra_workloads(dev, ev, stream, 200, eager=args.eager)
     if prefill_counters is not None:
         also["prefill_counters"] = prefill_counters
+    if config_traffic is not None:
+        also["config_traffic"] = config_traffic
     if adapter is not None:
         also["adapter_decode_llama3_8b_q4k"] = adapter
     cpu = None if args.no_cpu else cpu_decode(e2e)
+    if cpu is not None:
+        print("bench: CPU baselines of configs[0]-[3]", file=sys.stderr, flush=True)
+        cpu["per_config"] = cpu_configs(cpu["cores"])
     ms_tok = e2e["ms_per_token"]
     out = {
         "metric": METRIC,

@@ -141,15 +141,21 @@ constexpr uint32_t kDecLds = 256 + 512 + 64 + 128 + 16 + 128 + 16 + 4096 + 1024 
 // rows, half the units held two and their quantization came ~1.5 us later). K <= 4096: one
 // super-block per (row, partial), so thread (wave v, lane 16 i + r) computes the term of super-block
 // 4 v + i of row r, which is the row's partial p[4 v + i] (+0 + term), and the thread holding x block
-// b = 4 v + i (16 values per lane) quantizes it; rows 16 .. 23 are a second unit of the threads of
-// waves 0 and 1, loaded once the first unit's registers are free. The first loads are issued at once:
-// the norm weights and x, then (after a bare barrier, so that every wave's x is ahead in the queue) the
-// unit's 9 weight pieces (from any row block of the weight's layout) and the epoch. The rows go to qkv_y
-// with plain stores (the XCD's L2); after they are complete (vmcnt) the workgroup raises its flag.
+// b = 4 v + i (16 values per lane) quantizes it; rows 16 .. 23 are a second unit shared by thread
+// pairs: threads 2 u and 2 u + 1 hold unit u (super-block u / 8, row 16 + u % 8), four pieces each,
+// their integer sums met by DPP. Every load is issued at once and every wave issues the same ones (the
+// memory counters retire in order, so a wave's waits never cover loads another path lacks): the norm
+// weights and x, then (after a bare barrier, so that every wave's x is ahead in the queue) the first
+// unit's 9 weight pieces (from any row block of the weight's layout), the epoch (read into a register
+// only at the end: a wait for it would cover the weights), the second unit's pieces straight into LDS
+// and its meta. The rows go to qkv_y with plain stores (the XCD's L2); after they are complete (vmcnt)
+// the workgroup raises its flag.
 // LDS (bytes): x quants [16][272] | sub-block sums [16][8] | scales [16] | partials [24][16] |
-// control 16 | squares [K].
+// control 16 | squares [K] | second unit [4 waves][4 pieces][64 lanes][16].
 constexpr uint32_t kQkvMaxK = 4096, kQkvRows = 24;
-constexpr uint32_t kQkvLds = 16 * kXq4Stride + 16 * 8 * 4 + 16 * 4 + kQkvRows * 16 * 4 + 16 + 4 * kQkvMaxK;
+constexpr uint32_t kQkvStage = 16 * kXq4Stride + 16 * 8 * 4 + 16 * 4 + kQkvRows * 16 * 4 + 16 + 4 * kQkvMaxK;
+constexpr uint32_t kQkvLds = kQkvStage + 4 * 4 * 64 * 16;
+static_assert(kQkvStage % 16 == 0, "the second unit's pieces land on 16-byte lanes");
 
 template <int D>
 __device__ __forceinline__ void fa_qkv_rows(const FaDecArgs & a, uint8_t * lds, uint32_t j, uint32_t g) {
@@ -189,7 +195,14 @@ __device__ __forceinline__ void fa_qkv_rows(const FaDecArgs & a, uint8_t * lds, 
 #pragma unroll
     for (uint32_t jj = 0; jj < 8u; ++jj) qv[jj] = *(const uint4 *)(a.qkv_w + wl_quant_off(wg, B, R, jj, sl, rin));
     const uint4 mv = *(const uint4 *)(a.qkv_w + wl_meta_off(wg, B, R, sl, rin));
-    const uint32_t epv = a.ep[(size_t)g * G * (D / 64u)];         // the epoch the launch's tag follows
+    uint32_t epv = a.ep[(size_t)g * G * (D / 64u)];               // the epoch the launch's tag follows
+    const uint32_t u2 = tid >> 1, hq = tid & 1u, b2 = u2 >> 3, r2 = 16u + (u2 & 7u);
+    const uint32_t n2 = wrow(r_0 + r2), B2 = n2 / wg.rb, rin2 = n2 - B2 * wg.rb, R2 = wl_rows(wg, B2);
+    const uint32_t sl2 = wl_slot_of(wg, min(b2, nsb - 1u));
+    uint4 q4[4];
+#pragma unroll
+    for (uint32_t jj = 0; jj < 4u; ++jj) q4[jj] = *(const uint4 *)(a.qkv_w + wl_quant_off(wg, B2, R2, 4u * hq + jj, sl2, rin2));
+    const uint4 mv2 = *(const uint4 *)(a.qkv_w + wl_meta_off(wg, B2, R2, sl2, rin2));
     __builtin_amdgcn_sched_barrier(0);
 
     // RMS_NORM: the squares, the two halves of the 128 ordered partials on waves 0 and 1, the scale
@@ -202,12 +215,12 @@ __device__ __forceinline__ void fa_qkv_rows(const FaDecArgs & a, uint8_t * lds, 
     if (v < 2u) {
         const uint32_t i = 64u * v + lane, nk = K >> 7;           // terms per partial
         float p = 0.0f;
-        for (uint32_t k0 = 0; k0 < nk; k0 += 32u) {
-            float t[32];
+        for (uint32_t k0 = 0; k0 < nk; k0 += 16u) {             // 16-read batches: the second unit holds registers
+            float t[16];
 #pragma unroll
-            for (uint32_t k = 0; k < 32u; ++k) t[k] = s_sq[i + 128u * min(k0 + k, nk - 1u)];
+            for (uint32_t k = 0; k < 16u; ++k) t[k] = s_sq[i + 128u * min(k0 + k, nk - 1u)];
 #pragma unroll
-            for (uint32_t k = 0; k < 32u; ++k) {
+            for (uint32_t k = 0; k < 16u; ++k) {
                 const float q = p + t[k];                         // plain additions: see rms_tree64
                 p = k0 + k < nk ? q : p;
             }
@@ -237,28 +250,28 @@ __device__ __forceinline__ void fa_qkv_rows(const FaDecArgs & a, uint8_t * lds, 
     const bool slow = s_ctl[2] != 0u;                             // some block has 0 < |Dx| < 2^-60
 
     // a unit's term = partial p[s] of its row (+0 + term); partials of missing super-blocks are +0
-    auto term = [&](const uint4 (&q8)[8], const uint4 & m, uint32_t s) -> float {
-        const uint32_t sc = min(s, nsb - 1u);
-        int isum, msum;
-        q4k_unit_sums<8>(q8, m, s_xq + sc * kXq4Stride, s_xb + sc * 8u, 0u, isum, msum);
-        const float dx = s_xd[sc];
+    auto term = [&](int isum, int msum, const uint4 & m, uint32_t s) -> float {
+        const float dx = s_xd[min(s, nsb - 1u)];
         const float dq = h2f_fast(m.x & 0xFFFFu), dm = h2f_fast(m.x >> 16);
         float tt;
         if (__builtin_expect(!slow, 1)) tt = 0.0f + ((dq * dx) * (float)isum - (dm * dx) * (float)msum);
         else tt = sadd(0.0f, ssub(smul(smul(dq, dx), i2f(isum)), smul(smul(dm, dx), i2f(msum))));
         return s < nsb ? tt : 0.0f;
     };
-    s_p[16u * l16 + b] = term(qv, mv, b);
-    // the second unit of waves 0 and 1 (thread t < 128: super-block t / 8, row 16 + t % 8), loaded into
-    // the first unit's registers once those are free
-    if (v < 2u) {
-        const uint32_t b2 = tid >> 3, r2 = 16u + (tid & 7u);
-        const uint32_t n2 = wrow(r_0 + r2), B2 = n2 / wg.rb, rin2 = n2 - B2 * wg.rb, R2 = wl_rows(wg, B2);
-        const uint32_t sl2 = wl_slot_of(wg, min(b2, nsb - 1u));
-#pragma unroll
-        for (uint32_t jj = 0; jj < 8u; ++jj) qv[jj] = *(const uint4 *)(a.qkv_w + wl_quant_off(wg, B2, R2, jj, sl2, rin2));
-        const uint4 mv2 = *(const uint4 *)(a.qkv_w + wl_meta_off(wg, B2, R2, sl2, rin2));
-        s_p[16u * r2 + b2] = term(qv, mv2, b2);
+    {
+        const uint32_t sc = min(b, nsb - 1u);
+        int isum, msum;
+        q4k_unit_sums<8>(qv, mv, s_xq + sc * kXq4Stride, s_xb + sc * 8u, 0u, isum, msum);
+        s_p[16u * l16 + b] = term(isum, msum, mv, b);
+    }
+    {
+        const uint32_t sc = min(b2, nsb - 1u);
+        int isum, msum;
+        q4k_unit_sums<4>(q4, mv2, s_xq + sc * kXq4Stride, s_xb + sc * 8u, hq, isum, msum);
+        isum += dpp_i<kDppXor1>(isum);                            // exact: the pair's two halves
+        msum += dpp_i<kDppXor1>(msum);
+        const float tt = term(isum, msum, mv2, b2);
+        if (hq == 0u) s_p[16u * r2 + b2] = tt;
     }
     lds_barrier();
     // the 16-partial tree of each row (lane i of a 16-lane row holds p[i]): rows 0..15, then 16..23
@@ -283,6 +296,7 @@ __device__ __forceinline__ void fa_qkv_rows(const FaDecArgs & a, uint8_t * lds, 
     }
     vm_wait();                                                    // the rows are in the L2
     lds_barrier();
+    asm volatile("" : "+v"(epv));                                 // a register value: no earlier wait for it
     if (tid == 0u) {
         const uint32_t tagw = tag_after(epv) | (xcc_id() << 28);
         __hip_atomic_store(a.qkv_flag + (size_t)g * 64u + j, tagw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);

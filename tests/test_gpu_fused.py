@@ -389,6 +389,67 @@ def test_attn_qkv_plan_rope_tab(dev, oc, fmt, K, n_kv, pos, cell, n_head, n_head
     wt.free()
 
 
+@pytest.mark.parametrize("alias", ["out=x", "out=norm"])
+def test_attn_qkv_overlapping_buffers_run_two_launches(dev, oc, alias):
+    """The one-launch form reads x and the norm weight in its row workgroups while its reducers write
+    the attention output: when the output overlaps either, the entry point runs the two launches
+    instead (the launch counter says so), and the results are those of the ops in order (the Q|K|V
+    row from x before the output overwrites it)."""
+    import math
+    n_kv, pos, n_head, n_head_kv, D, K = 4232, 4200, 32, 8, 128, 4096
+    print(f"\nattn_qkv overlapping buffers {alias}", flush=True)
+    E, nq = n_head_kv * D, n_head * D
+    N = nq + 2 * E
+    fmt = H.FMT_Q4_K
+    k0 = np.zeros((n_kv, E // 32 * 34), np.uint8)
+    v0 = np.zeros_like(k0)
+    oc.kv_set_rows(k0, S.normal(41, pos * E).reshape(pos, E), np.arange(pos))
+    oc.kv_set_rows(v0, S.normal(42, pos * E).reshape(pos, E), np.arange(pos))
+    blocks = S.quant_rows(fmt, S.seed_of("attn-qkv-alias", "w"), N, K)
+    x = S.normal(S.seed_of("attn-qkv-alias", "x"), K).reshape(1, K)
+    nw = (1.0 + 0.1 * S.normal(S.seed_of("attn-qkv-alias", "nw"), K)).astype(np.float32)
+    eps = 1e-5
+    row = oc.mul_mat(fmt, blocks, K, oc.rms_norm(x, eps, nw[None]), threads=8)
+    ts = theta_scale(500000.0, D)
+    q = oc.rope(np.ascontiguousarray(row[:, :nq]), np.array([pos], np.int32), D, D, False, ts)
+    k = oc.rope(np.ascontiguousarray(row[:, nq:nq + E]), np.array([pos], np.int32), D, D, False, ts)
+    kw, vw = k0.copy(), v0.copy()
+    oc.kv_set_rows(kw, k, np.array([pos], np.int64))
+    oc.kv_set_rows(vw, np.ascontiguousarray(row[:, nq + E:]), np.array([pos], np.int64))
+    scale = np.float32(1.0 / math.sqrt(D))
+    msum = np.zeros(12, np.uint32)
+    msum[0], msum[1], msum[2], msum[9] = 0x4D55534D, 1, n_kv, pos + 1
+    runs = np.array([[pos, pos + 1]], np.uint32)
+    want = oc.flash_attn(q, kw, vw, D, n_head, n_head_kv, scale, msum, None, new_runs=runs)
+    wt = dev.weight(fmt, blocks, N, K)
+    kc, vc = dev.kv(E, n_kv), dev.kv(E, n_kv)
+    plan = dev.fa_plan(D, n_head, n_head_kv, 1, n_kv)
+    plan.set(msum, runs)
+    xb, nb = dev.upload(x), dev.upload(nw)
+    qkv, bad = dev.alloc(4 * N), dev.upload(np.zeros(1, np.int32))
+    pb, cb = dev.upload(np.array([pos], np.int32)), dev.upload(np.array([pos], np.int64))
+    tab = dev.alloc(4 * D)
+    dev.rope_table(pb, D, 500000.0, tab)
+    out = xb if alias == "out=x" else nb                          # nq == K floats: the whole buffer
+    for rep in range(2):
+        xb.write(x)
+        nb.write(nw)
+        kc.set_bytes(0, k0)
+        vc.set_bytes(1, v0)
+        n0 = dev.counters()["fa_dec_qkv_launches"]
+        dev.attn_qkv_plan_rope_tab(plan, wt, xb, eps, nb, qkv, kc, vc, scale, D, H.ROPE_NORMAL, tab, cb, out, nq, bad=bad)
+        assert dev.counters()["fa_dec_qkv_launches"] == n0, "the one-launch form ran over overlapping buffers"
+        assert_bits_equal(qkv.read(np.float32, (1, N)), row, f"Q|K|V row, call {rep}")
+        assert_bits_equal(out.read(np.float32, (1, nq)), want, f"attention, call {rep}")
+        assert (kc.get_bytes(0).reshape(n_kv, -1) == kw).all()
+        assert (vc.get_bytes(1).reshape(n_kv, -1) == vw).all()
+        assert bad.read(np.int32, (1,))[0] == 0
+    plan.free()
+    kc.free()
+    vc.free()
+    wt.free()
+
+
 def test_attn_qkv_plan_rope_tab_wait_expires(dev, oc):
     """The attention launch with its Q|K|V rows, its bounded waits (the row workgroups' flags, the chunk
     maxima, the reducers' polls) forced to expire from the host (a poll limit of 1): the launch still

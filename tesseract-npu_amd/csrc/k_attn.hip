@@ -458,16 +458,18 @@ __global__ __launch_bounds__(64 * kPvWaves) void k_fa_pv(FaArgs a, FaPlan p) {
     using PB = PvBlock<D, VS>;
     constexpr uint32_t DV = PB::DV, BB = PB::BB;
     const uint32_t G = a.G, nh = a.n_head;
+    // the launch has one wave per segment of its longest channel (nw <= kPvMaxSeg), so the segment
+    // results need nw slots: the LDS is sized by the launch
+    const uint32_t nw = blockDim.x >> 6;
     uint32_t * s_t64 = (uint32_t *)lds;                           // EXPK table
     float * s_c = (float *)(lds + 256);                           // [seg][4 heads][DV]
-    float * s_l = s_c + kPvMaxSeg * 4u * DV;                      // [seg][4 heads]
-    uint8_t * s_dg = (uint8_t *)(s_l + kPvMaxSeg * 4u);          // per wave: [BB blocks][4 heads][4 digits][4 groups][16]
+    float * s_l = s_c + nw * 4u * DV;                             // [seg][4 heads]
+    uint8_t * s_dg = (uint8_t *)(s_l + nw * 4u);                  // per wave: [BB blocks][4 heads][4 digits][4 groups][16]
     const uint32_t t64v = a.ex.t64[threadIdx.x & 63u];            // first: the table write waits for it only
     const uint32_t item = blockIdx.x >> 2, c = blockIdx.x & 3u, g = blockIdx.y;
     const uint32_t hg = blockIdx.z / VS, vh = blockIdx.z % VS;
     const FaItem it = fa_item<INL>(a, p, item);
     const uint32_t lane = __lane_id(), wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t nw = blockDim.x >> 6;
     const uint32_t h = g * G + min(4u * hg + (lane >> 4), G - 1u);
     const PB pb(a, it, c, g, hg, vh, a.S + (size_t)it.s_off * nh + (size_t)h * (16u * it.n));
     uint8_t * dg = s_dg + (size_t)wave * (BB * 1024u);
@@ -628,7 +630,7 @@ static int launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, u
     uint32_t vs = 1;
     while (vs < 4u && a.D / (2u * vs) >= 64u && blocks * vs < 2ull * n_cu) vs *= 2u;
     const uint32_t dv = a.D / vs, bb = std::min(4u, dv / 32u);
-    const size_t lds_pv = 256u + 4u * (size_t)tsr::kPvMaxSeg * 4u * dv + 4u * tsr::kPvMaxSeg * 4u + 1024u * bb * nwv;
+    const size_t lds_pv = 256u + 4u * (size_t)nwv * 4u * dv + 4u * nwv * 4u + 1024u * bb * nwv;
     const dim3 gpv(4u * p.n_items, a.n_head_kv, (a.G + 3u) / 4u * vs);
     const dim3 bpv(64u * nwv);
 #define TSR_PV(DD, VV) hipLaunchKernelGGL((tsr::k_fa_pv<DD, INL, VV>), gpv, bpv, lds_pv, s, a, p)

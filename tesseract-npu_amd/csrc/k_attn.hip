@@ -67,7 +67,7 @@ template <int D, int VS>
 struct PvBlock {
     static constexpr uint32_t DV = D / VS;                        // values of the block (>= 64)
     static constexpr uint32_t NBV = DV / 32;                      // their value blocks
-    static constexpr uint32_t BB = NBV < 4 ? NBV : 4;             // blocks per batch (2 or 4)
+    static constexpr uint32_t BB = 2;                             // blocks per batch: one 64-value slice (fewer registers: more waves per SIMD)
     static constexpr uint32_t NBT = NBV / BB;                     // batches
     static_assert(DV >= 64 && NBV % BB == 0, "value part");
     // the loads of one segment: scores, value scales and the value quants of a batch
@@ -629,7 +629,7 @@ static int launch_fa(const tsr::FaArgs & a, const tsr::FaPlan & p, uint32_t T, u
     const uint64_t blocks = 4ull * p.n_items * a.n_head_kv * ((a.G + 3u) / 4u);
     uint32_t vs = 1;
     while (vs < 4u && a.D / (2u * vs) >= 64u && blocks * vs < 2ull * n_cu) vs *= 2u;
-    const uint32_t dv = a.D / vs, bb = std::min(4u, dv / 32u);
+    const uint32_t dv = a.D / vs, bb = 2u;                        // PvBlock::BB
     const size_t lds_pv = 256u + 4u * (size_t)nwv * 4u * dv + 4u * nwv * 4u + 1024u * bb * nwv;
     const dim3 gpv(4u * p.n_items, a.n_head_kv, (a.G + 3u) / 4u * vs);
     const dim3 bpv(64u * nwv);

@@ -773,14 +773,55 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
     };
     float O = 0.0f, l = 0.0f, mr = 0.0f;
     if (__builtin_expect(ni <= kRedItems, 1)) {
-        // One round: the row-sum side first (its data are published at the segments' EXP step), the
-        // merge factors and the l merge on wave 0 while the other waves already poll the outputs.
+        // One round: the chunk maxima first (the merge factors on wave 0), then the row sums (published at
+        // the segments' EXP step) and the l merge on wave 0 while the other waves already poll the outputs.
         const uint32_t k0 = 0;
         float fx = 0.0f;
         uint32_t ns[kRedItems], tl0[kRedItems];
         round_items(k0, ns, tl0);
         uint64_t pl[kRedItems], pm;
         uint32_t spins = 0;
+        // the chunk maxima first (an item's first segment stores them once its chunk's segments have
+        // met, well before the row sums of the last segments): wave 0 forms the merge factors while the
+        // row sums are still coming
+        for (;;) {
+            pm = ld_tag(a.m_item + (size_t)min(k0 + min(lane, kRedItems - 1u), ni - 1u) * nh + hh);
+            if (__all(tag_is((uint32_t)(pm >> 32), tag))) break;
+            if (__builtin_expect(++spins >= a.spin_max, 0)) {
+                if (lane == 0u && a.bad != nullptr)
+                    __hip_atomic_fetch_or(a.bad, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        float mkr[kRedItems], mrun[kRedItems];
+        {
+            // the running maxima are a MAXT scan of the chunk maxima, so every merge factor of the round is
+            // known now: lane 2 kq + b evaluates EXP((prev - mrun_kq) scale) for b = 0 (the running sums) or
+            // EXP((m_kq - mrun_kq) scale) for b = 1 (the chunk's), all at once; kept for both merges
+            float prev[kRedItems];
+            float m = mr;
+#pragma unroll
+            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+                mkr[kq] = bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pm, (int)kq));
+                prev[kq] = m;
+                mrun[kq] = k0 + kq == 0u ? mkr[kq] : maxt(m, mkr[kq]);
+                m = mrun[kq];
+            }
+            if (c == 0u) {
+                const uint32_t jk = min(lane >> 1, kRedItems - 1u);  // lanes 2 kq, 2 kq + 1 hold item kq's factors
+                float from = 0.0f, to = 0.0f;
+#pragma unroll
+                for (uint32_t kq = 0; kq < kRedItems; ++kq)
+                    if (jk == kq) {
+                        from = (lane & 1u) ? mkr[kq] : prev[kq];
+                        to = mrun[kq];
+                    }
+                fx = expk(smul_n(ssub_n(from, to), a.scale), a.ex, s_t64);
+            }
+        }
+        // the row sums of channel c's segments
+        spins = 0;
         for (;;) {
             bool ok = true;
 #pragma unroll
@@ -789,8 +830,6 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
                 pl[kq] = ld_tag(a.seg_l + lrow);
                 ok &= lane >= ns[kq] || tag_is((uint32_t)(pl[kq] >> 32), tag);
             }
-            pm = ld_tag(a.m_item + (size_t)min(k0 + min(lane, kRedItems - 1u), ni - 1u) * nh + hh);
-            ok &= tag_is((uint32_t)(pm >> 32), tag);
             if (__all(ok)) break;
             if (__builtin_expect(++spins >= a.spin_max, 0)) {
                 if (lane == 0u && a.bad != nullptr)
@@ -799,10 +838,8 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
             }
             __builtin_amdgcn_s_sleep(2);
         }
-        float mkr[kRedItems];
 #pragma unroll
         for (uint32_t kq = 0; kq < kRedItems; ++kq) {             // channel c's segment sums in order
-            mkr[kq] = bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pm, (int)kq));
             float Lc = 0.0f;
 #pragma unroll
             for (uint32_t sgi = 0; sgi < 8u; ++sgi)
@@ -811,26 +848,6 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
         }
         __syncthreads();
         if (c == 0u) {
-            // the running maxima are a MAXT scan of the chunk maxima, so every merge factor of the round is
-            // known now: lane 2 kq + b evaluates EXP((prev - mrun_kq) scale) for b = 0 (the running sums) or
-            // EXP((m_kq - mrun_kq) scale) for b = 1 (the chunk's), all at once; kept for the O side
-            float mrun[kRedItems], prev[kRedItems];
-            float m = mr;
-#pragma unroll
-            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
-                prev[kq] = m;
-                mrun[kq] = k0 + kq == 0u ? mkr[kq] : maxt(m, mkr[kq]);
-                m = mrun[kq];
-            }
-            const uint32_t jk = min(lane >> 1, kRedItems - 1u);  // lanes 2 kq, 2 kq + 1 hold item kq's factors
-            float from = 0.0f, to = 0.0f;
-#pragma unroll
-            for (uint32_t kq = 0; kq < kRedItems; ++kq)
-                if (jk == kq) {
-                    from = (lane & 1u) ? mkr[kq] : prev[kq];
-                    to = mrun[kq];
-                }
-            fx = expk(smul_n(ssub_n(from, to), a.scale), a.ex, s_t64);
 #pragma unroll
             for (uint32_t kq = 0; kq < kRedItems; ++kq) {        // CTREE, then AMERGE, in chunk order: l
                 if (k0 + kq >= ni) break;

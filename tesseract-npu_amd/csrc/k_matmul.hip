@@ -18,9 +18,13 @@
 // operations are the spec operations; NaN is canonicalized when y is stored.
 //
 // Work split. A workgroup of 16 waves computes one 32 x 32 tile; wave j computes partial p_j
-// (blocks b = j, j + 16, ... in order: consecutive slots of the weight layout, wlayout.hpp). Each
-// wave issues the loads of up to kMmPre of its blocks at once, then runs their matrix-core steps.
-// The 16 partials meet in LDS and one thread per output adds the tree ((p0 + p1) + (p2 + p3)) + ...
+// (blocks b = j, j + 16, ... in order: consecutive slots of the weight layout, wlayout.hpp). A wave
+// requests block k + 1 once the matrix core has read block k's operands, and two workgroups share a
+// compute unit (at most 64 VGPRs), so that one's loads overlap the other's VALU work: the three VALU
+// operations per output are the bound. The loads are raw buffer loads (a 32-bit lane offset set up
+// once, the block step in a scalar offset where it is uniform), so that the loop has no 64-bit
+// address arithmetic. The 16 partials meet in LDS and one thread per output adds the tree
+// ((p0 + p1) + (p2 + p3)) + ...
 //
 // Lane layouts (gfx950): an operand lane l supplies row l % 32 of its matrix and k = 16 (l / 32) ..
 // 16 (l / 32) + 15; the result lane l holds column l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4,
@@ -36,7 +40,21 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr uint32_t kMmPre = 8;   // blocks whose loads one wave keeps in flight
+// Raw buffer loads over a window of bytes: 32-bit offsets (a vector part and a scalar part), and
+// a load at or past the window's end returns 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t brsrc(const void * p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ v4i bload128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ uint32_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ float bloadf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+
 
 // QACT A32 of T token rows into the block-major layout: 8 lanes per (token, block), 4 values each
 // (qact_a32_lane: the spec rule, as for the QA image of k_qact).
@@ -56,53 +74,92 @@ __global__ __launch_bounds__(256) void k_qact_mm(const float * x, uint64_t x_str
     }
 }
 
-__global__ __launch_bounds__(1024) void k_mm_q80(MmArgs a) {
+// The tile (row tile tx, token tile ty) of a workgroup. Workgroups are dispatched to the XCDs in
+// turn (linear workgroup i on XCD i mod 8). The plain grid (gx, gy) runs the row tiles of one token
+// tile together: an XCD's share of a weight of up to ~2 MB stays in its 4 MB L2 from one token tile
+// to the next. The grouped grid (8 gy, gx / 8), for larger weights, gives row tile tx to XCD tx mod 8
+// and its token tiles to that XCD one after another, so that the weight tile is read from memory once
+// and then from the L2 by the token tiles running beside it.
+__device__ __forceinline__ void mm_tile(bool grouped, uint32_t & tx, uint32_t & ty) {
+    if (grouped) {
+        tx = (blockIdx.x & 7u) + 8u * blockIdx.y;
+        ty = blockIdx.x >> 3;
+    } else {
+        tx = blockIdx.x;
+        ty = blockIdx.y;
+    }
+}
+
+__global__ __launch_bounds__(1024, 8) void k_mm_q80(MmArgs a) {
     __shared__ float s_p[16][1024];                                // partial j of output (lane, r)
     const WGeom g = wgeom(a.N, a.K >> 5, a.rb, false);
     const uint32_t lane = __lane_id(), j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t n0 = blockIdx.x * 32u, t0 = blockIdx.y * 32u;
+    uint32_t tx, ty;
+    mm_tile(a.grouped != 0u, tx, ty);
+    const uint32_t n0 = tx * 32u, t0 = ty * 32u;
     const uint32_t h = lane >> 5, c = lane & 31u;
     // operand rows of this lane (clamped: rows / tokens beyond the matrix are not stored)
     const uint32_t n = min(n0 + c, a.N - 1u), t = min(t0 + c, a.T - 1u);
     const uint32_t B = n / g.rb, R = wl_rows(g, B), rr = n - B * g.rb;  // row block of the row
-    const uint8_t * wq = a.w + wl_quant_off(g, B, R, h, 0u, rr);         // + 16 R slot
-    const uint8_t * wm = a.w + wl_meta_off(g, B, R, 0u, rr);             // + 2 R slot
-    const uint8_t * xq = a.qa + (size_t)t * 32u + 16u * h;                     // + 32 T b
-    const float * xd = (const float *)(a.qa + a.d_off) + t;                      // + T b
+    // buffer windows: the row blocks of the workgroup's rows (the host checks that they span less
+    // than 2^31 bytes), the activation scratch; a load at offset >= 2^31 reads 0 (the k = 1 column
+    // of the scale product)
+    const uint32_t B0 = n0 / g.rb, B1 = (min(n0 + 31u, a.N - 1u)) / g.rb;
+    const uint64_t wbase = (uint64_t)B0 * g.bstride;
+    const uint64_t wend = B1 + 1u < g.nblk ? (uint64_t)(B1 + 1u) * g.bstride : wl_bytes(g);
+    const __amdgpu_buffer_rsrc_t rw = brsrc(a.w + wbase, (uint32_t)(wend - wbase));
+    const __amdgpu_buffer_rsrc_t rx = brsrc(a.qa, a.d_off + 4u * a.T * g.nb);
     const uint32_t cnt = wl_count(g, j), sl0 = wl_slot(g, j, 0u);
+    uint32_t ow = (uint32_t)(wl_quant_off(g, B, R, h, sl0, rr) - wbase);   // + 16 R per slot
+    uint32_t om = h ? 0x80000000u : (uint32_t)(wl_meta_off(g, B, R, sl0, rr) - wbase);   // + 2 R
+    const uint32_t sw = 16u * R, sm = 2u * R;
+    const uint32_t ox = 32u * t + 16u * h, od = h ? 0x80000000u : a.d_off + 4u * t;
+    const uint32_t sx = 512u * a.T, sd = 64u * a.T;                // per block of the wave (b += 16)
+    uint32_t bx = 32u * a.T * j, bd = 4u * a.T * j;                // scalar: block b = j + 16 k
 
     v16f p;
 #pragma unroll
     for (int r = 0; r < 16; ++r) p[r] = 0.0f;
-    for (uint32_t k0 = 0; k0 < cnt; k0 += kMmPre) {
-        v4i wa[kMmPre], xb[kMmPre];
-        float dw[kMmPre], dx[kMmPre];
-#pragma unroll
-        for (uint32_t i = 0; i < kMmPre; ++i) {                    // clamped: every load is issued
-            const uint32_t k = min(k0 + i, cnt - 1u), sl = sl0 + k, b = j + 16u * k;
-            wa[i] = *(const v4i *)(wq + (size_t)16u * R * sl);
-            xb[i] = *(const v4i *)(xq + (size_t)32u * a.T * b);
-            dw[i] = h2f_fast(*(const uint16_t *)(wm + (size_t)2u * R * sl));
-            dx[i] = xd[(size_t)a.T * b];
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < kMmPre; ++i) {
-            if (k0 + i >= cnt) break;
-            v16i is = {};
-            is = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa[i], xb[i], is, 0, 0, 0);
-            v16f P = {};
-            P = __builtin_amdgcn_mfma_f32_32x32x2f32(h ? 0.0f : dw[i], h ? 0.0f : dx[i], P, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) p[r] = p[r] + P[r] * (float)is[r];
-        }
+    // one block ahead: the next block's loads are issued once the matrix core has read this one's.
+    // Every load is of a block the wave owns (k < cnt; the window's range check covers the vector
+    // offset, which is how the k = 1 lanes read 0, and is not relied on for the scalar offset).
+    v4i wa = {}, xb = {};
+    uint32_t dwh = 0u;
+    float dx = 0.0f;
+    if (cnt > 0u) {
+        wa = bload128(rw, ow, 0u);
+        xb = bload128(rx, ox, bx);
+        dwh = bload16(rw, om, 0u);
+        dx = bloadf(rx, od, bd);
     }
+    for (uint32_t k = 0; k < cnt; ++k) {
+        v16i is = {};
+        is = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, xb, is, 0, 0, 0);
+        v16f P = {};
+        P = __builtin_amdgcn_mfma_f32_32x32x2f32(h2f_fast(dwh), dx, P, 0, 0, 0);
+        if (k + 1u < cnt) {                                        // wave-uniform
+            ow += sw;
+            om += sm;
+            bx += sx;
+            bd += sd;
+            wa = bload128(rw, ow, 0u);
+            xb = bload128(rx, ox, bx);
+            dwh = bload16(rw, om, 0u);
+            dx = bloadf(rx, od, bd);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = p[r] + P[r] * (float)is[r];
+    }
+    // the lane index again (not kept in a register through the loop)
+    uint32_t ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-        *(float4 *)&s_p[j][16u * lane + 4u * (uint32_t)r] = make_float4(p[4 * r], p[4 * r + 1], p[4 * r + 2], p[4 * r + 3]);
+        *(float4 *)&s_p[j][16u * ln + 4u * (uint32_t)r] = make_float4(p[4 * r], p[4 * r + 1], p[4 * r + 2], p[4 * r + 3]);
     lds_barrier();
 
     // one thread per output: o = 16 lane' + r of the wave layout above
-    const uint32_t o = threadIdx.x, ol = o >> 4, r = o & 15u;
+    const uint32_t o = 64u * j + ln, ol = o >> 4, r = o & 15u;
     const uint32_t tt = t0 + (ol & 31u), nn = n0 + 8u * (r >> 2) + 4u * (ol >> 5) + (r & 3u);
     float v[16];
 #pragma unroll
@@ -336,7 +393,12 @@ int tsr_launch_qact_mm(const float * x, uint64_t x_stride, uint32_t K, uint32_t 
 }
 
 int tsr_launch_mm_q8_0(const tsr::MmArgs & a, hipStream_t s) {
-    const dim3 grid((a.N + 31u) / 32u, (a.T + 31u) / 32u);
-    hipLaunchKernelGGL(tsr::k_mm_q80, grid, dim3(1024), 0, s, a);
+    const tsr::WGeom g = tsr::wgeom(a.N, a.K >> 5, a.rb, false);
+    if ((uint64_t)(31u / a.rb + 2u) * g.bstride >= 0x80000000ull) return -2;   // a tile's buffer window
+    const uint32_t gx = (a.N + 31u) / 32u, gy = (a.T + 31u) / 32u;
+    tsr::MmArgs m = a;
+    m.grouped = (gx & 7u) == 0u && (uint64_t)a.N * (a.K / 32u) * 34u > (24ull << 20) ? 1u : 0u;
+    const dim3 grid = m.grouped ? dim3(8u * gy, gx / 8u) : dim3(gx, gy);
+    hipLaunchKernelGGL(tsr::k_mm_q80, grid, dim3(1024), 0, s, m);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }

@@ -74,6 +74,7 @@ struct MmArgs {
     uint32_t s_off, tp;
     uint32_t glu;            // Q4_K: rows 2j, 2j + 1 are gate / up of output j: y[j] = SWIGLU(gate, up)
     ExpkTab ex;              // glu
+    uint32_t grouped;        // set by the launch: the grid's tile order (k_matmul.hip: mm_tile)
 };
 
 // A KV plane (see k_kv.hip for the layout).

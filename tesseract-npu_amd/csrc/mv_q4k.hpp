@@ -21,32 +21,46 @@ __device__ __forceinline__ float4 prep_norm_apply(float4 v, float s, float4 w, b
     return v;
 }
 // prep_norm_apply over a lane's 16 values when the wave qualifies (wave-uniform result): the scale
-// is a normal number and every x and w is a normal number or a zero. DAZ is then the identity; x s
-// can be subnormal (FTZ) or overflow, never NaN; (x s) w can be subnormal or NaN (Inf 0), each
-// fixed with one class test. The result equals FM(FM(x, s), w) of the general form.
+// is a normal number, every x and w is a normal number or a zero, and no product x s or (x s) w of
+// nonzero factors can be subnormal or overflow. Then DAZ and FTZ are the identity and no NaN arises,
+// so the plain products equal FM(FM(x, s), w) of the general form. The test runs on bounds, not per
+// product: with a value's magnitude bits t = bits << 1 (sign dropped), t >= 0xFF000000 is Inf or NaN
+// and t - 1 < 0x00FFFFFF a subnormal (a zero wraps to 0xFFFFFFFF, above every other value), so one
+// maximum of t and one minimum of t - 1 over the lane give the largest and the smallest nonzero
+// magnitude; rounding is monotonic, so every product of nonzero factors lies between the products of
+// the bounds (rounded the same way).
 __device__ __forceinline__ bool prep_norm_apply_fast(float4 (&v)[4], float s, const float4 (&w)[4], bool has_w) {
-    constexpr int kBad = 0x297;                                   // NaN, +-Inf, +-subnormal
-    bool bad = !__builtin_amdgcn_class(s, 0x108);                 // +-normal
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        bad |= __builtin_amdgcn_class(v[c].x, kBad) | __builtin_amdgcn_class(v[c].y, kBad) |
-               __builtin_amdgcn_class(v[c].z, kBad) | __builtin_amdgcn_class(v[c].w, kBad);
-        if (has_w)
-            bad |= __builtin_amdgcn_class(w[c].x, kBad) | __builtin_amdgcn_class(w[c].y, kBad) |
-                   __builtin_amdgcn_class(w[c].z, kBad) | __builtin_amdgcn_class(w[c].w, kBad);
-    }
-    if (__ballot(bad) != 0ull) return false;
-    auto ftz = [](float r) { return __builtin_amdgcn_class(r, 0x90) ? bf(fb(r) & 0x80000000u) : r; };
-    auto one = [&](float x, float wv) {
-        const float t = ftz(x * s);
-        if (!has_w) return t;
-        const float y = ftz(t * wv);
-        return __builtin_amdgcn_class(y, 0x3) ? bf(kNaN) : y;
+    uint32_t xhi = 0u, xlo = 0xFFFFFFFFu, whi = 0u, wlo = 0xFFFFFFFFu;
+    auto acc = [](uint32_t & hi, uint32_t & lo, float a, float b) {
+        const uint32_t ta = fb(a) << 1, tb = fb(b) << 1;
+        hi = max(hi, max(ta, tb));
+        lo = min(lo, min(ta - 1u, tb - 1u));
     };
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-        v[c].x = one(v[c].x, w[c].x); v[c].y = one(v[c].y, w[c].y);
-        v[c].z = one(v[c].z, w[c].z); v[c].w = one(v[c].w, w[c].w);
+        acc(xhi, xlo, v[c].x, v[c].y);
+        acc(xhi, xlo, v[c].z, v[c].w);
+        if (has_w) {
+            acc(whi, wlo, w[c].x, w[c].y);
+            acc(whi, wlo, w[c].z, w[c].w);
+        }
+    }
+    constexpr float kMin = 0x1p-126f, kMax = 0x1.fffffep127f;
+    const float as = __builtin_fabsf(s);
+    bool ok = __builtin_amdgcn_class(s, 0x108) && xhi < 0xFF000000u && xlo >= 0x00FFFFFFu;   // s: +-normal
+    const float tlo = bf((xlo + 1u) >> 1) * as, thi = bf(xhi >> 1) * as;
+    const bool xz = xlo == 0xFFFFFFFFu;                           // every x a zero: every product a zero
+    ok = ok && (xz || (tlo >= kMin && thi <= kMax));
+    if (has_w) {
+        ok = ok && whi < 0xFF000000u && wlo >= 0x00FFFFFFu;
+        const float ylo = tlo * bf((wlo + 1u) >> 1), yhi = thi * bf(whi >> 1);
+        ok = ok && (xz || wlo == 0xFFFFFFFFu || (ylo >= kMin && yhi <= kMax));
+    }
+    if (__ballot(!ok) != 0ull) return false;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        v[c].x = v[c].x * s; v[c].y = v[c].y * s; v[c].z = v[c].z * s; v[c].w = v[c].w * s;
+        if (has_w) { v[c].x = v[c].x * w[c].x; v[c].y = v[c].y * w[c].y; v[c].z = v[c].z * w[c].z; v[c].w = v[c].w * w[c].w; }
     }
     return true;
 }

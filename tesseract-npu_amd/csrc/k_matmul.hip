@@ -243,26 +243,42 @@ __device__ __forceinline__ uint32_t q4k_m(const uint4 mt, uint32_t j) {
 
 // GLU: weight rows 2j and 2j + 1 are the gate and up rows of output j; their results are in adjacent
 // lanes of the output phase and y[j] = SWIGLU(gate, up) (as the matvec's GLU epilogue).
+// Without GLU, at most 128 VGPRs: two workgroups share a compute unit (measured faster); the GLU form's
+// epilogue would spill there, and it keeps one.
 template <bool GLU>
-__global__ __launch_bounds__(512) void k_mm_q4k(MmArgs a) {
+__global__ __launch_bounds__(512, GLU ? 2 : 4) void k_mm_q4k(MmArgs a) {
     __shared__ float s_p[16][1024];                                // partial pj of output (r, lane)
     __shared__ int s_slow[8];
     const WGeom g = wgeom(a.N, a.K >> 8, a.rb, true);
     const uint32_t lane = __lane_id(), j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t n0 = blockIdx.x * 32u, t0 = blockIdx.y * 32u;
+    uint32_t tx, ty;
+    mm_tile(a.grouped != 0u, tx, ty);
+    const uint32_t n0 = tx * 32u, t0 = ty * 32u;
     const uint32_t h = lane >> 5, c = lane & 31u;
     // operand rows of this lane (clamped: rows / tokens beyond the matrix are not stored)
     const uint32_t n = min(n0 + c, a.N - 1u), t = min(t0 + c, a.T - 1u);
     const uint32_t B = n / g.rb, R = wl_rows(g, B), rr = n - B * g.rb;
-    const uint8_t * wq = a.w + wl_quant_off(g, B, R, h, 0u, rr);  // piece 2 gg + h, slot sl: + 16 R (2 gg nb + sl)
-    const uint8_t * wm = a.w + wl_meta_off(g, B, R, 0u, rr);      // + 16 R sl
-    const uint8_t * xq = a.qa + (size_t)t * 32u + 16u * h;         // sub-block jb: + 32 T jb
-    const int32_t * xs = (const int32_t *)(a.qa + a.s_off) + t;    // + T jb
-    const float * xd = (const float *)(a.qa + a.d_off) + t0 + 4u * h;   // + tp s + 8 q: tokens of result r = 4 q + i
+    // buffer windows (as k_mm_q80): the row blocks of the tile's rows, the activation scratch; a load at
+    // offset >= 2^31 reads 0 (the k = 1 column of the scale products)
+    const uint32_t B0 = n0 / g.rb, B1 = (min(n0 + 31u, a.N - 1u)) / g.rb;
+    const uint64_t wbase = (uint64_t)B0 * g.bstride;
+    const uint64_t wend = B1 + 1u < g.nblk ? (uint64_t)(B1 + 1u) * g.bstride : wl_bytes(g);
+    const __amdgpu_buffer_rsrc_t rw = brsrc(a.w + wbase, (uint32_t)(wend - wbase));
+    const __amdgpu_buffer_rsrc_t rx = brsrc(a.qa, a.d_off + 4u * a.tp * g.nb);
+    const uint32_t owq = (uint32_t)(wl_quant_off(g, B, R, h, 0u, rr) - wbase);   // piece 2 gg + h: + 16 R (2 gg nb + sl)
+    const uint32_t owm = (uint32_t)(wl_meta_off(g, B, R, 0u, rr) - wbase);       // + 16 R sl
+    const uint32_t sR = 16u * R, sG = 32u * R * g.nb;
+    const uint32_t ox = 32u * t + 16u * h;                        // quants of sub-block jb: + 32 T jb
+    const uint32_t obs = a.s_off + 4u * t + 4u * a.T * h;         // sums of sub-block 2 q + h: + 4 T 2 q
+    const uint32_t odx = h ? 0x80000000u : a.d_off + 4u * (t0 + c);   // token t0 + c's scale: + 4 tp s
     const uint32_t m4 = 0x0F0F0F0Fu;
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    // byte-wise q * f of a dword of quants q <= 15 and f <= 7 (no byte carries into the next: q f <= 105)
+    auto bmul = [](uint32_t q, uint32_t f) -> int {
+        return (int)__builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q) * (u16x2){(unsigned short)f, (unsigned short)f});
+    };
     bool slow = false;
-    // wave j computes partials j and j + 8 (8 waves of up to 256 VGPRs: one wave per partial at 16
-    // waves would leave 128 and spill)
+    // wave j computes partials j and j + 8 (8 waves of up to 256 VGPRs)
     for (uint32_t half = 0; half < 2u; ++half) {
     const uint32_t pj = j + 8u * half, cnt = wl_count(g, pj), sl0 = wl_slot(g, pj, 0u);
     v16f p;
@@ -272,51 +288,65 @@ __global__ __launch_bounds__(512) void k_mm_q4k(MmArgs a) {
         const uint32_t sl = sl0 + k, s = pj + 16u * k;
         v4i wv[4], xv[8];
 #pragma unroll
-        for (int gg = 0; gg < 4; ++gg) wv[gg] = *(const v4i *)(wq + (size_t)16u * R * (2u * gg * g.nb + sl));
-        const uint4 mt = *(const uint4 *)(wm + (size_t)16u * R * sl);
+        for (uint32_t gg = 0; gg < 4u; ++gg) wv[gg] = bload128(rw, owq + sR * sl + sG * gg, 0u);
+        const uint4 mt = __builtin_bit_cast(uint4, bload128(rw, owm + sR * sl, 0u));
 #pragma unroll
-        for (int jb = 0; jb < 8; ++jb) xv[jb] = *(const v4i *)(xq + (size_t)32u * a.T * (8u * s + jb));
+        for (uint32_t jb = 0; jb < 8u; ++jb) xv[jb] = bload128(rx, ox, 32u * a.T * (8u * s + jb));
         float bsf[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) bsf[q] = (float)xs[(size_t)a.T * (8u * s + 2u * q + h)];
-        float4 dx4[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) dx4[q] = *(const float4 *)(xd + (size_t)a.tp * s + 8u * q);
+        for (uint32_t q = 0; q < 4u; ++q) bsf[q] = (float)(int)__builtin_amdgcn_raw_buffer_load_b32(rx, (int)obs, (int)(4u * a.T * (8u * s + 2u * q)), 0);
+        const float dxl = bloadf(rx, odx, 4u * a.tp * s);
 
         v16f ms = {};
 #pragma unroll
         for (uint32_t q = 0; q < 4u; ++q)
             ms = __builtin_amdgcn_mfma_f32_32x32x2f32(bsf[q], (float)q4k_m(mt, 2u * q + h), ms, 0, 0, 0);
-        v16i isum = {};
+        // isum = sum_j sc_j S_j on the matrix core: sc_j = 8 a_j + b_j (a_j, b_j <= 7), the weight quants
+        // scaled by a_j and by b_j (<= 105: int8) into two exact int32 accumulators, isum = 8 A + B
+        v16i ia = {}, ib = {};
 #pragma unroll
         for (uint32_t gg = 0; gg < 4u; ++gg) {
-            const v4i lo = { wv[gg][0] & (int)m4, wv[gg][1] & (int)m4, wv[gg][2] & (int)m4, wv[gg][3] & (int)m4 };
-            const v4i hi = { (wv[gg][0] >> 4) & (int)m4, (wv[gg][1] >> 4) & (int)m4, (wv[gg][2] >> 4) & (int)m4,
-                             (wv[gg][3] >> 4) & (int)m4 };
-            v16i s0 = {}, s1 = {};
-            s0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xv[2 * gg], lo, s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(xv[2 * gg + 1], hi, s1, 0, 0, 0);
-            const int sc0 = (int)q4k_sc(mt, 2u * gg), sc1 = (int)q4k_sc(mt, 2u * gg + 1u);
+            const uint32_t sc0 = q4k_sc(mt, 2u * gg), sc1 = q4k_sc(mt, 2u * gg + 1u);
+            v4i la, lb, ha, hb;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) isum[r] += __mul24(sc0, s0[r]) + __mul24(sc1, s1[r]);
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t lo = (uint32_t)wv[gg][e] & m4, hi = ((uint32_t)wv[gg][e] >> 4) & m4;
+                la[e] = bmul(lo, sc0 >> 3);
+                lb[e] = bmul(lo, sc0 & 7u);
+                ha[e] = bmul(hi, sc1 >> 3);
+                hb[e] = bmul(hi, sc1 & 7u);
+            }
+            ia = __builtin_amdgcn_mfma_i32_32x32x32_i8(xv[2 * gg], la, ia, 0, 0, 0);
+            ib = __builtin_amdgcn_mfma_i32_32x32x32_i8(xv[2 * gg], lb, ib, 0, 0, 0);
+            ia = __builtin_amdgcn_mfma_i32_32x32x32_i8(xv[2 * gg + 1], ha, ia, 0, 0, 0);
+            ib = __builtin_amdgcn_mfma_i32_32x32x32_i8(xv[2 * gg + 1], hb, ib, 0, 0, 0);
         }
+        v16i isum;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) isum[r] = (ia[r] << 3) + ib[r];
         const float d = h2f_fast(mt.x & 0xFFFFu), dm = h2f_fast(mt.x >> 16);
-        const float dxs[16] = { dx4[0].x, dx4[0].y, dx4[0].z, dx4[0].w, dx4[1].x, dx4[1].y, dx4[1].z, dx4[1].w,
-                                dx4[2].x, dx4[2].y, dx4[2].z, dx4[2].w, dx4[3].x, dx4[3].y, dx4[3].z, dx4[3].w };
-        bool tiny = false;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t ad = fb(dxs[r]) & 0x7FFFFFFFu;
-            tiny |= ad != 0u && ad < 0x21800000u;
+        {
+            const uint32_t ad = fb(dxl) & 0x7FFFFFFFu;            // the 32 tokens' scales, one a lane
+            slow = slow || __ballot(ad != 0u && ad < 0x21800000u) != 0ull;   // wave-uniform, sticky
         }
-        slow = slow || __ballot(tiny) != 0ull;                       // wave-uniform, sticky
         if (!slow) {
+            // d Dx and dmin Dx as outer products on the matrix core (one IEEE product each; k = 1 is zero)
+            v16f P1 = {}, P2 = {};
+            P1 = __builtin_amdgcn_mfma_f32_32x32x2f32(dxl, h ? 0.0f : d, P1, 0, 0, 0);
+            P2 = __builtin_amdgcn_mfma_f32_32x32x2f32(dxl, h ? 0.0f : dm, P2, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float tt = (d * dxs[r]) * (float)isum[r] - (dm * dxs[r]) * ms[r];
+                const float tt = P1[r] * (float)isum[r] - P2[r] * ms[r];
                 p[r] = p[r] + tt;
             }
         } else {
+            // tokens of result r = 4 q + i: t0 + 8 q + 4 h + i
+            const float * xd = (const float *)(a.qa + a.d_off) + (size_t)a.tp * s + t0 + 4u * h;
+            float4 dx4[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) dx4[q] = *(const float4 *)(xd + 8u * q);
+            const float dxs[16] = { dx4[0].x, dx4[0].y, dx4[0].z, dx4[0].w, dx4[1].x, dx4[1].y, dx4[1].z, dx4[1].w,
+                                    dx4[2].x, dx4[2].y, dx4[2].z, dx4[2].w, dx4[3].x, dx4[3].y, dx4[3].z, dx4[3].w };
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const float tt = ssub(smul(smul(d, dxs[r]), i2f(isum[r])), smul(smul(dm, dxs[r]), ms[r]));
@@ -379,9 +409,14 @@ int tsr_launch_qact_mm4(const float * x, uint64_t x_stride, uint32_t K, uint32_t
 }
 
 int tsr_launch_mm_q4_k(const tsr::MmArgs & a, hipStream_t s) {
-    const dim3 grid((a.N + 31u) / 32u, (a.T + 31u) / 32u);
-    if (a.glu) hipLaunchKernelGGL(tsr::k_mm_q4k<true>, grid, dim3(512), 0, s, a);
-    else hipLaunchKernelGGL(tsr::k_mm_q4k<false>, grid, dim3(512), 0, s, a);
+    const tsr::WGeom g = tsr::wgeom(a.N, a.K >> 8, a.rb, true);
+    if ((uint64_t)(31u / a.rb + 2u) * g.bstride >= 0x80000000ull) return -2;   // a tile's buffer window
+    const uint32_t gx = (a.N + 31u) / 32u, gy = (a.T + 31u) / 32u;
+    tsr::MmArgs m = a;
+    m.grouped = (gx & 7u) == 0u && (uint64_t)a.N * (a.K / 256u) * 144u > (48ull << 20) ? 1u : 0u;   // measured
+    const dim3 grid = m.grouped ? dim3(8u * gy, gx / 8u) : dim3(gx, gy);
+    if (a.glu) hipLaunchKernelGGL(tsr::k_mm_q4k<true>, grid, dim3(512), 0, s, m);
+    else hipLaunchKernelGGL(tsr::k_mm_q4k<false>, grid, dim3(512), 0, s, m);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -423,6 +423,10 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     it.ntiles = __builtin_amdgcn_readlane(itw, 8);
     const FaSeg sg(it, c);
     if (tt >= sg.nseg) return;                                    // no such segment (block-uniform)
+    // A short lone segment (a tail chunk's: fewer than 4 groups) shares its compute unit with two full
+    // segments and, the youngest, was served last: it ended ~1-1.5 us after them and held up the
+    // reducers. Its waves issue first.
+    if (a.n_items > 1u && sg.nseg == 1u && sg.nu < 4u) __builtin_amdgcn_s_setprio(2);
     const uint32_t ng = (a.kc.kv_size + 15u) / 16u;
     // the segment's groups (clamped: loads of a missing group stay inside the item)
     uint32_t ug[4];

@@ -732,8 +732,8 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
 
 // The reducers of a KV head: workgroup (head r, 64-value part vp), thread = (value, channel c): channel c's
 // chains of segment results in order (AT 6.4 O, 6.5 l), CTREE over the channels (AT 5.6), the merge of
-// the items in chunk order (AMERGE) and ANORM (AT 5.7). With one round of items (<= kRedItems, the
-// decode at up to 6 K cells) the row-sum side comes first: the chunk maxima and the segments' row sums
+// the items in chunk order (AMERGE) and ANORM (AT 5.7). With one round of items (<= kRedItems or exactly
+// 4: the decode at up to ~8 K cells) the row-sum side comes first: the chunk maxima and the segments' row sums
 // are stored at the segments' EXP step, so the merge factors and the l merge are done while the
 // segments' P.V still runs, and only the O side waits for the last segment. Several rounds poll each
 // round's outputs, row sums and maxima together (their reducers start late: the grid is larger than the
@@ -741,7 +741,7 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
 // the launch's tag (an epoch + 1, one epoch word per reducer, each advanced by its reducer at its end):
 // nothing is cleared, and a store that lands after an expired wait carries a tag no later launch
 // expects. A reducer only waits for segments, which come before it in dispatch order.
-constexpr uint32_t kRedItems = 3;                                 // items loaded per round
+constexpr uint32_t kRedItems = 3;                                 // items loaded per round (several rounds)
 
 template <int D, bool LOCAL>
 __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds, uint32_t ri, uint32_t g) {
@@ -764,9 +764,10 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
     }
     __syncthreads();
     // the segments of channel c of the round's items
-    auto round_items = [&](uint32_t k0, uint32_t (&ns)[kRedItems], uint32_t (&tl0)[kRedItems]) {
+    auto round_items = [&](uint32_t k0, auto & ns, auto & tl0) {
+        constexpr uint32_t R = sizeof(ns) / sizeof(ns[0]);
 #pragma unroll
-        for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+        for (uint32_t kq = 0; kq < R; ++kq) {
             const uint32_t k = min(k0 + kq, ni - 1u);
             FaItem ik{};
             ik.u0 = s_it[3u * k];
@@ -776,20 +777,21 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
         }
     };
     float O = 0.0f, l = 0.0f, mr = 0.0f;
-    if (__builtin_expect(ni <= kRedItems, 1)) {
+    // One round of R items (R = 3, or 4 for exactly 4 items: one round instead of 3 + 1)
+    auto one_round = [&]<uint32_t R>() {
         // One round: the chunk maxima first (the merge factors on wave 0), then the row sums (published at
         // the segments' EXP step) and the l merge on wave 0 while the other waves already poll the outputs.
         const uint32_t k0 = 0;
         float fx = 0.0f;
-        uint32_t ns[kRedItems], tl0[kRedItems];
+        uint32_t ns[R], tl0[R];
         round_items(k0, ns, tl0);
-        uint64_t pl[kRedItems], pm;
+        uint64_t pl[R], pm;
         uint32_t spins = 0;
         // the chunk maxima first (an item's first segment stores them once its chunk's segments have
         // met, well before the row sums of the last segments): wave 0 forms the merge factors while the
         // row sums are still coming
         for (;;) {
-            pm = ld_tag(a.m_item + (size_t)min(k0 + min(lane, kRedItems - 1u), ni - 1u) * nh + hh);
+            pm = ld_tag(a.m_item + (size_t)min(k0 + min(lane, R - 1u), ni - 1u) * nh + hh);
             if (__all(tag_is((uint32_t)(pm >> 32), tag))) break;
             if (__builtin_expect(++spins >= a.spin_max, 0)) {
                 if (lane == 0u && a.bad != nullptr)
@@ -798,25 +800,25 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
             }
             __builtin_amdgcn_s_sleep(2);
         }
-        float mkr[kRedItems], mrun[kRedItems];
+        float mkr[R], mrun[R];
         {
             // the running maxima are a MAXT scan of the chunk maxima, so every merge factor of the round is
             // known now: lane 2 kq + b evaluates EXP((prev - mrun_kq) scale) for b = 0 (the running sums) or
             // EXP((m_kq - mrun_kq) scale) for b = 1 (the chunk's), all at once; kept for both merges
-            float prev[kRedItems];
+            float prev[R];
             float m = mr;
 #pragma unroll
-            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+            for (uint32_t kq = 0; kq < R; ++kq) {
                 mkr[kq] = bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pm, (int)kq));
                 prev[kq] = m;
                 mrun[kq] = k0 + kq == 0u ? mkr[kq] : maxt(m, mkr[kq]);
                 m = mrun[kq];
             }
             if (c == 0u) {
-                const uint32_t jk = min(lane >> 1, kRedItems - 1u);  // lanes 2 kq, 2 kq + 1 hold item kq's factors
+                const uint32_t jk = min(lane >> 1, R - 1u);  // lanes 2 kq, 2 kq + 1 hold item kq's factors
                 float from = 0.0f, to = 0.0f;
 #pragma unroll
-                for (uint32_t kq = 0; kq < kRedItems; ++kq)
+                for (uint32_t kq = 0; kq < R; ++kq)
                     if (jk == kq) {
                         from = (lane & 1u) ? mkr[kq] : prev[kq];
                         to = mrun[kq];
@@ -829,7 +831,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
         for (;;) {
             bool ok = true;
 #pragma unroll
-            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+            for (uint32_t kq = 0; kq < R; ++kq) {
                 const size_t lrow = ((size_t)(tl0[kq] + min(lane, max(ns[kq], 1u) - 1u)) * 4u + c) * nh + hh;
                 pl[kq] = ld_tag(a.seg_l + lrow);
                 ok &= lane >= ns[kq] || tag_is((uint32_t)(pl[kq] >> 32), tag);
@@ -843,7 +845,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
             __builtin_amdgcn_s_sleep(2);
         }
 #pragma unroll
-        for (uint32_t kq = 0; kq < kRedItems; ++kq) {             // channel c's segment sums in order
+        for (uint32_t kq = 0; kq < R; ++kq) {             // channel c's segment sums in order
             float Lc = 0.0f;
 #pragma unroll
             for (uint32_t sgi = 0; sgi < 8u; ++sgi)
@@ -853,7 +855,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
         __syncthreads();
         if (c == 0u) {
 #pragma unroll
-            for (uint32_t kq = 0; kq < kRedItems; ++kq) {        // CTREE, then AMERGE, in chunk order: l
+            for (uint32_t kq = 0; kq < R; ++kq) {        // CTREE, then AMERGE, in chunk order: l
                 if (k0 + kq >= ni) break;
                 const float * xl4 = s_x + 1024u + kq * 4u;
                 const float lk = ctree4(xl4[0], xl4[1], xl4[2], xl4[3]);
@@ -868,13 +870,13 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
             }
         }
         // ---- the segments' outputs: lane v's value of channel c in each segment ----
-        uint64_t po[kRedItems][8];
+        uint64_t po[R][8];
         spins = 0;
         for (;;) {
             bool ok = true, near = true;                          // near: every writer shared this XCD
             round_items(k0, ns, tl0);                             // (re-read: fewer registers held)
 #pragma unroll
-            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+            for (uint32_t kq = 0; kq < R; ++kq) {
 #pragma unroll
                 for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
                     const size_t row = ((size_t)(tl0[kq] + min(sgi, max(ns[kq], 1u) - 1u)) * 4u + c) * nh + hh;
@@ -882,7 +884,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
                 }
             }
 #pragma unroll
-            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+            for (uint32_t kq = 0; kq < R; ++kq) {
 #pragma unroll
                 for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
                     ok &= sgi >= ns[kq] || tag_is((uint32_t)(po[kq][sgi] >> 32), tag);
@@ -902,7 +904,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
             __builtin_amdgcn_s_sleep(2);
         }
 #pragma unroll
-        for (uint32_t kq = 0; kq < kRedItems; ++kq) {             // channel c's segments in order
+        for (uint32_t kq = 0; kq < R; ++kq) {             // channel c's segments in order
             float Oc = 0.0f;
 #pragma unroll
             for (uint32_t sgi = 0; sgi < 8u; ++sgi)
@@ -912,7 +914,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
         __syncthreads();
         if (c == 0u) {                                            // CTREE, then AMERGE, in chunk order: O
 #pragma unroll
-            for (uint32_t kq = 0; kq < kRedItems; ++kq) {
+            for (uint32_t kq = 0; kq < R; ++kq) {
                 if (k0 + kq >= ni) break;
                 const float * x = s_x + kq * 256u + lane;
                 const float ok = ctree4(x[0], x[64], x[128], x[192]);
@@ -925,6 +927,11 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
                 }
             }
         }
+    };
+    if (__builtin_expect(ni <= kRedItems, 1)) {
+        one_round.template operator()<kRedItems>();
+    } else if (ni == 4u) {
+        one_round.template operator()<4u>();
     } else {
         // Several rounds: each round polls its items' outputs, row sums and maxima together
         for (uint32_t k0 = 0; k0 < ni; k0 += kRedItems) {

@@ -172,3 +172,22 @@ def test_mm_q4_k_glu(dev, oc, T, N, K):
     u = oc.mul_mat(1, blocks[1::2], K, x, threads=8)
     assert_bits_equal(got, oc.swiglu(g, u), f"GLU T {T} {N}x{K}")
     w.free()
+
+
+def test_mm_q4_k_glu_llama_gate_up(dev, oc):
+    """The Llama-3-8B gate|up with the GLU epilogue (W[28672 x 4096] Q4_K, 66 MB: the XCD-grouped tile
+    order), 40 tokens: every output against the oracle's gate and up MUL_MATs then SWIGLU."""
+    T, N, K = 40, 28672, 4096
+    print(f"\nmm Q4_K GLU T {T} {N}x{K}", flush=True)
+    blocks = S.quant_rows(1, 93, N, K)
+    x = S.normal(94, T * K).reshape(T, K)
+    x[7] = special_row(K, 5)
+    w = dev.weight(1, blocks, N, K)
+    yb = dev.alloc(4 * T * (N // 2))
+    dev.mul_mat(w, dev.upload(x), T, K, yb, N // 2, flags=tsr_hip.MM_GLU)
+    got = yb.read(np.float32, (T, N // 2))
+    g = oc.mul_mat(1, blocks[0::2], K, x, threads=8)
+    u = oc.mul_mat(1, blocks[1::2], K, x, threads=8)
+    assert_bits_equal(got, oc.swiglu(g, u), "GLU 8B gate|up")
+    w.free()
+    yb.free()

@@ -17,19 +17,23 @@ __device__ __forceinline__ float expk_with(float v, const ExpkTab & e, Lookup t6
     const uint32_t a = u & 0x7FFFFFFFu;
     const bool neg = (u >> 31) != 0u;
     const uint32_t ev = a >> 23;
-    // T = floor(Mv LK / 2^(156 - ev)) for ev <= 156 (larger ev: overflow / underflow below)
-    const uint64_t mv = 0x00800000u | (a & 0x007FFFFFu);
+    // T = floor(Mv LK / 2^(156 - ev)) for ev <= 156 (larger ev: overflow / underflow below). Mv < 2^24
+    // and LK < 2^39 (log2(e) 2^38): the exact product, from 32-bit pieces, fits 63 bits.
+    const uint32_t mv = 0x00800000u | (a & 0x007FFFFFu);
     const uint32_t sh = 156u - min(ev, 156u);
-    const uint64_t prod = mv * e.lk;
+    const uint32_t lk_lo = (uint32_t)e.lk, lk_hi = (uint32_t)(e.lk >> 32);
+    const uint64_t prod = ((uint64_t)(__umulhi(mv, lk_lo) + mv * lk_hi) << 32) | (uint64_t)(mv * lk_lo);
     const uint64_t T = sh >= 64u ? 0ull : (prod >> sh);
     const uint32_t Thi = (uint32_t)(T >> 32), Tlo = (uint32_t)T;
     const int32_t n0 = neg ? -(int32_t)(Thi + (Tlo ? 1u : 0u)) : (int32_t)Thi;
     const uint32_t F = neg ? 0u - Tlo : Tlo;
-    const uint64_t G = F & 0x03FFFFFFu;
-    const uint64_t pf = (G * (e.c1 + ((G * (e.c2 + ((G * e.c3) >> 32))) >> 32))) >> 32;
-    const uint64_t t = t64(F >> 26);
-    const uint64_t M = t + ((t * pf) >> 32);
-    const bool hiM = M >= (1ull << 31);
+    // the cubic in fixed point: G < 2^26 and c1, c2, c3 < 2^32 (ln2^k / k! 2^32), and every sum below stays
+    // under 2^32, so each (G x) >> 32 is the high word of one 32-bit product; likewise t < 2^31, pf < 2^26
+    const uint32_t G = F & 0x03FFFFFFu;
+    const uint32_t pf = __umulhi(G, (uint32_t)e.c1 + __umulhi(G, (uint32_t)e.c2 + __umulhi(G, (uint32_t)e.c3)));
+    const uint32_t t = t64(F >> 26);
+    const uint32_t M = t + __umulhi(t, pf);                       // < 2^31 + 2^25
+    const bool hiM = M >= (1u << 31);
     const uint32_t drop = hiM ? 8u : 7u;
     uint32_t sig = (uint32_t)(M >> drop);
     const uint32_t rem = (uint32_t)M & ((1u << drop) - 1u), half = 1u << (drop - 1u);

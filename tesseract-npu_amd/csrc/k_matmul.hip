@@ -57,15 +57,17 @@ __device__ __forceinline__ float bloadf(__amdgpu_buffer_rsrc_t r, uint32_t voff,
 
 
 // QACT A32 of T token rows into the block-major layout: 8 lanes per (token, block), 4 values each
-// (qact_a32_lane: the spec rule, as for the QA image of k_qact).
+// (qact_a32_lane: the spec rule, as for the QA image of k_qact). Pairs run token-fastest: a wave's 8
+// pairs read one 128-byte line of x each and write 256 contiguous bytes of quants (block-fastest
+// pairs wrote 32 bytes 16 KiB apart). The host keeps T (K / 32) below 2^32.
 __global__ __launch_bounds__(256) void k_qact_mm(const float * x, uint64_t x_stride, uint32_t K, uint32_t T,
                                                  uint8_t * xq, float * xd) {
     const uint32_t nb = K >> 5;
-    const uint64_t pair = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;   // (token, block)
+    const uint32_t pair = (blockIdx.x * blockDim.x + threadIdx.x) >> 3;   // (block, token)
     const uint32_t l8 = threadIdx.x & 7u;
-    const uint64_t npair = (uint64_t)T * nb;
-    const uint64_t pc = pair < npair ? pair : npair - 1u;         // clamped: whole 8-lane groups stay active
-    const uint32_t t = (uint32_t)(pc / nb), b = (uint32_t)(pc % nb);
+    const uint32_t npair = T * nb;
+    const uint32_t pc = pair < npair ? pair : npair - 1u;         // clamped: whole 8-lane groups stay active
+    const uint32_t b = pc / T, t = pc - b * T;
     float D;
     const uint32_t q = qact_a32_lane(*(const float4 *)(x + (size_t)t * x_stride + 32u * b + 4u * l8), &D);
     if (pair < npair) {
@@ -204,15 +206,17 @@ __global__ __launch_bounds__(1024, 8) void k_mm_q80(MmArgs a) {
 // (qact_a256_row: lane i holds values 16 i .. 16 i + 15, half i & 1 of sub-block i / 2). Writes
 // the quants xq [K/32][T][32 B], the sub-block sums xs [K/32][T] and the scales xd [K/256][tp]
 // (tp >= T, a multiple of 32; tokens T .. tp - 1 get d = 0). Every lane of a wave stays active
-// (the row operations need them): lanes past the last pair quantize a copy and store nothing.
+// (the row operations need them): lanes past the last pair quantize a copy and store nothing. Pairs
+// run token-fastest (a wave's 4 rows write the quants of 4 consecutive tokens); the host keeps
+// tp (K / 256) 16 below 2^32.
 __global__ __launch_bounds__(256) void k_qact_mm4(const float * x, uint64_t x_stride, uint32_t K, uint32_t T,
                                                   uint32_t tp, uint8_t * xq, int32_t * xs, float * xd) {
     const uint32_t nsb = K >> 8;
-    const uint64_t pair = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;   // (token < tp, super-block)
+    const uint32_t pair = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;   // (super-block, token < tp)
     const uint32_t l16 = threadIdx.x & 15u;
-    const uint64_t npair = (uint64_t)tp * nsb;
-    const uint64_t pc = pair < npair ? pair : npair - 1u;
-    const uint32_t t = (uint32_t)(pc / nsb), sb = (uint32_t)(pc % nsb);
+    const uint32_t npair = tp * nsb;
+    const uint32_t pc = pair < npair ? pair : npair - 1u;
+    const uint32_t sb = pc / tp, t = pc - sb * tp;
     const uint32_t tc = t < T ? t : T - 1u;
     const float * xp = x + (size_t)tc * x_stride + 256u * sb + 16u * l16;
     float4 v[4];
@@ -403,6 +407,7 @@ __global__ __launch_bounds__(512, GLU ? 2 : 4) void k_mm_q4k(MmArgs a) {
 int tsr_launch_qact_mm4(const float * x, uint64_t x_stride, uint32_t K, uint32_t T, uint32_t tp, uint8_t * xq,
                         int32_t * xs, float * xd, hipStream_t s) {
     const uint64_t threads = (uint64_t)tp * (K / 256u) * 16u;
+    if (threads + 255u >= 0x100000000ull) return -2;              // 32-bit pair indices
     hipLaunchKernelGGL(tsr::k_qact_mm4, dim3((uint32_t)((threads + 255u) / 256u)), dim3(256), 0, s, x, x_stride, K, T,
                        tp, xq, xs, xd);
     return hipGetLastError() == hipSuccess ? 0 : -4;
@@ -423,6 +428,7 @@ int tsr_launch_mm_q4_k(const tsr::MmArgs & a, hipStream_t s) {
 int tsr_launch_qact_mm(const float * x, uint64_t x_stride, uint32_t K, uint32_t T, uint8_t * xq, float * xd,
                        hipStream_t s) {
     const uint64_t threads = (uint64_t)T * (K / 32u) * 8u;
+    if (threads + 255u >= 0x100000000ull) return -2;              // 32-bit pair indices
     hipLaunchKernelGGL(tsr::k_qact_mm, dim3((uint32_t)((threads + 255u) / 256u)), dim3(256), 0, s, x, x_stride, K, T, xq, xd);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }

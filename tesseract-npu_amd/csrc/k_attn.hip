@@ -136,7 +136,8 @@ struct PvBlock {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // EXPK results are zero, normal, Inf or NaN (never subnormal)
-            pz[i] = (cv && head_ok) ? expk(smul_n(ssub_n(ss[i], m), a.scale), a.ex, s_t64) : 0.0f;
+            const float ez = expk_diff(ss[i], m, a.scale, a.ex, s_t64);   // straight-line, then the select
+            pz[i] = (cv && head_ok) ? ez : 0.0f;
             const uint32_t f = f_field(pz[i]);
             pnf |= f == 255u ? 1u : 0u;
             pe = max(pe, f == 255u ? 0u : f);
@@ -239,12 +240,12 @@ struct PvBlock {
             if (hi2 >= G) continue;
             const uint32_t h2 = g * G + hi2;
             float O = 0.0f;
-            for (uint32_t seg = 0; seg < nseg; ++seg) O = sadd_n(O, s_c[(seg * 4u + r4) * DV + v]);
+            for (uint32_t seg = 0; seg < nseg; ++seg) O = sadd_z(O, s_c[(seg * 4u + r4) * DV + v]);
             const size_t slot = ((size_t)item * 4u + c) * nh + h2;
-            a.OP[slot * D + vh * DV + v] = O;
+            a.OP[slot * D + vh * DV + v] = canon(O);
             if (vh == 0u && v == 0u) {
                 float l = 0.0f;
-                for (uint32_t seg = 0; seg < nseg; ++seg) l = sadd_n(l, s_l[seg * 4u + r4]);
+                for (uint32_t seg = 0; seg < nseg; ++seg) l = sadd_c(l, s_l[seg * 4u + r4]);
                 a.LP[slot] = l;
             }
         }
@@ -575,18 +576,18 @@ __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
                 from = (L & 1u) ? mk[k] : (k == 0u ? mr : mrun[k - 1u]);
                 to = mrun[k];
             }
-        const float fx = expk(smul_n(ssub_n(from, to), a.scale), a.ex, s_t64);
+        const float fx = expk_diff(from, to, a.scale, a.ex, s_t64);
 #pragma unroll
         for (uint32_t k = 0; k < kMergeItems; ++k) {
             if (k >= kn) break;
-            const float ok = ctree4(R.op[k][0], R.op[k][1], R.op[k][2], R.op[k][3]);
-            const float lk = ctree4(R.lp[k][0], R.lp[k][1], R.lp[k][2], R.lp[k][3]);
+            const float ok = ctree4_o(R.op[k][0], R.op[k][1], R.op[k][2], R.op[k][3]);
+            const float lk = ctree4_l(R.lp[k][0], R.lp[k][1], R.lp[k][2], R.lp[k][3]);
             if (k0 + k == 0u) { O = ok; l = lk; }
             else {
                 const float fa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)k));
                 const float fbv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)k + 1));
-                l = sadd_n(smul_n(l, fa), smul_n(lk, fbv));
-                O = sadd_n(smul_n(O, fa), smul_n(ok, fbv));
+                l = sadd_c(smul_c(l, fa), smul_c(lk, fbv));
+                O = sadd_z(smul_z(O, fa), smul_z(ok, fbv));
             }
             mr = mrun[k];
         }

@@ -637,7 +637,8 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
     if (wave < G) {
         const uint32_t h = wave;
         // EXPK results are zero, normal, Inf or NaN (never subnormal)
-        const float p = in ? expk(smul_n(ssub_n(s_S[h * 64u + j], s_m[h]), a.scale), a.ex, s_t64) : 0.0f;
+        const float ez = expk_diff(s_S[h * 64u + j], s_m[h], a.scale, a.ex, s_t64);
+        const float p = in ? ez : 0.0f;
         s_P[h * 64u + j] = p;
         const uint32_t f = f_field(p);
         const bool badl = __any(f == 255u);
@@ -823,7 +824,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
                         from = (lane & 1u) ? mkr[kq] : prev[kq];
                         to = mrun[kq];
                     }
-                fx = expk(smul_n(ssub_n(from, to), a.scale), a.ex, s_t64);
+                fx = expk_diff(from, to, a.scale, a.ex, s_t64);
             }
         }
         // the row sums of channel c's segments
@@ -849,7 +850,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
             float Lc = 0.0f;
 #pragma unroll
             for (uint32_t sgi = 0; sgi < 8u; ++sgi)
-                if (sgi < ns[kq]) Lc = sadd_n(Lc, bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pl[kq], (int)sgi)));
+                if (sgi < ns[kq]) Lc = sadd_c(Lc, bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pl[kq], (int)sgi)));
             if (lane == 0u) s_x[1024u + kq * 4u + c] = Lc;
         }
         __syncthreads();
@@ -858,13 +859,13 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
             for (uint32_t kq = 0; kq < R; ++kq) {        // CTREE, then AMERGE, in chunk order: l
                 if (k0 + kq >= ni) break;
                 const float * xl4 = s_x + 1024u + kq * 4u;
-                const float lk = ctree4(xl4[0], xl4[1], xl4[2], xl4[3]);
+                const float lk = ctree4_l(xl4[0], xl4[1], xl4[2], xl4[3]);
                 if (k0 + kq == 0u) {
                     l = lk;
                 } else {
                     const float fa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq));
                     const float fbv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq + 1));
-                    l = sadd_n(smul_n(l, fa), smul_n(lk, fbv));
+                    l = sadd_c(smul_c(l, fa), smul_c(lk, fbv));
                 }
                 mr = mrun[kq];
             }
@@ -908,7 +909,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
             float Oc = 0.0f;
 #pragma unroll
             for (uint32_t sgi = 0; sgi < 8u; ++sgi)
-                if (sgi < ns[kq]) Oc = sadd_n(Oc, bf((uint32_t)po[kq][sgi]));
+                if (sgi < ns[kq]) Oc = sadd_z(Oc, bf((uint32_t)po[kq][sgi]));
             s_x[(kq * 4u + c) * 64u + lane] = Oc;
         }
         __syncthreads();
@@ -917,13 +918,13 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
             for (uint32_t kq = 0; kq < R; ++kq) {
                 if (k0 + kq >= ni) break;
                 const float * x = s_x + kq * 256u + lane;
-                const float ok = ctree4(x[0], x[64], x[128], x[192]);
+                const float ok = ctree4_o(x[0], x[64], x[128], x[192]);
                 if (k0 + kq == 0u) {
                     O = ok;
                 } else {
                     const float fa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq));
                     const float fbv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq + 1));
-                    O = sadd_n(smul_n(O, fa), smul_n(ok, fbv));
+                    O = sadd_z(smul_z(O, fa), smul_z(ok, fbv));
                 }
             }
         }
@@ -999,8 +1000,8 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
 #pragma unroll
                 for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
                     if (sgi < ns[kq]) {
-                        Oc = sadd_n(Oc, xo[kq][sgi]);
-                        Lc = sadd_n(Lc, xl[kq][sgi]);
+                        Oc = sadd_z(Oc, xo[kq][sgi]);
+                        Lc = sadd_c(Lc, xl[kq][sgi]);
                     }
                 }
                 s_x[(kq * 4u + c) * 64u + lane] = Oc;
@@ -1027,22 +1028,22 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
                         from = (lane & 1u) ? mkr[kq] : prev[kq];
                         to = mrun[kq];
                     }
-                const float fx = expk(smul_n(ssub_n(from, to), a.scale), a.ex, s_t64);
+                const float fx = expk_diff(from, to, a.scale, a.ex, s_t64);
 #pragma unroll
                 for (uint32_t kq = 0; kq < kRedItems; ++kq) {
                     if (k0 + kq >= ni) break;
                     const float * x = s_x + kq * 256u + lane;
-                    const float ok = ctree4(x[0], x[64], x[128], x[192]);
+                    const float ok = ctree4_o(x[0], x[64], x[128], x[192]);
                     const float * xl4 = s_x + 1024u + kq * 4u;
-                    const float lk = ctree4(xl4[0], xl4[1], xl4[2], xl4[3]);
+                    const float lk = ctree4_l(xl4[0], xl4[1], xl4[2], xl4[3]);
                     if (k0 + kq == 0u) {
                         O = ok;
                         l = lk;
                     } else {
                         const float fa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq));
                         const float fbv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fx), 2 * (int)kq + 1));
-                        l = sadd_n(smul_n(l, fa), smul_n(lk, fbv));
-                        O = sadd_n(smul_n(O, fa), smul_n(ok, fbv));
+                        l = sadd_c(smul_c(l, fa), smul_c(lk, fbv));
+                        O = sadd_z(smul_z(O, fa), smul_z(ok, fbv));
                     }
                     mr = mrun[kq];
                 }

@@ -47,7 +47,7 @@ __device__ __forceinline__ bool prep_norm_apply_fast(float4 (&v)[4], float s, co
     }
     constexpr float kMin = 0x1p-126f, kMax = 0x1.fffffep127f;
     const float as = __builtin_fabsf(s);
-    bool ok = __builtin_amdgcn_class(s, 0x108) && xhi < 0xFF000000u && xlo >= 0x00FFFFFFu;   // s: +-normal
+    bool ok = __builtin_amdgcn_classf(s, 0x108) && xhi < 0xFF000000u && xlo >= 0x00FFFFFFu;   // s: +-normal
     const float tlo = bf((xlo + 1u) >> 1) * as, thi = bf(xhi >> 1) * as;
     const bool xz = xlo == 0xFFFFFFFFu;                           // every x a zero: every product a zero
     ok = ok && (xz || (tlo >= kMin && thi <= kMax));

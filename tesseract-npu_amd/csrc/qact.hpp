@@ -31,7 +31,7 @@ __device__ __forceinline__ bool qact_a32_lane_fast(const float4 v, uint32_t * ou
     uint32_t m = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        nonfin |= __builtin_amdgcn_class(xs[i], 0x207);           // NaN, +-Inf
+        nonfin |= __builtin_amdgcn_classf(xs[i], 0x207);           // NaN, +-Inf
         m = umax_u(m, fb(xs[i]) & 0x7FFFFFFFu);
     }
     if (__ballot(nonfin) != 0ull) return false;

@@ -30,7 +30,10 @@ __device__ __forceinline__ float fin(float r) {
     return bf(e == 0u ? (u & 0x80000000u) : nan);
 }
 // NaN -> canonical only (results that cannot be subnormal).
-__device__ __forceinline__ float canon(float r) { return (fb(r) & 0x7FFFFFFFu) > 0x7F800000u ? bf(kNaN) : r; }
+__device__ __forceinline__ float canon(float r) { return __builtin_amdgcn_classf(r, 0x3) ? bf(kNaN) : r; }
+// FTZ only (a NaN keeps the payload the operation gave it): for chains whose values are canonicalized
+// where they leave the chain, since every later IEEE operation keeps a NaN a NaN.
+__device__ __forceinline__ float ftz(float r) { return __builtin_amdgcn_classf(r, 0x90) ? bf(fb(r) & 0x80000000u) : r; }
 
 __device__ __forceinline__ float sadd(float a, float b) { return fin(daz(a) + daz(b)); }
 __device__ __forceinline__ float ssub(float a, float b) { return fin(daz(a) - daz(b)); }
@@ -43,12 +46,18 @@ __device__ __forceinline__ float srcp(float a) { return fin(1.0f / daz(a)); }
 // NaN canonicalization, each tested with one v_cmp_class (mask 0x90: -/+ subnormal; 0x3: NaN).
 __device__ __forceinline__ float fin_n(float r) {
     const uint32_t u = fb(r);
-    const uint32_t o = __builtin_amdgcn_class(r, 0x90) ? (u & 0x80000000u) : u;
-    return bf(__builtin_amdgcn_class(r, 0x3) ? kNaN : o);
+    const uint32_t o = __builtin_amdgcn_classf(r, 0x90) ? (u & 0x80000000u) : u;
+    return bf(__builtin_amdgcn_classf(r, 0x3) ? kNaN : o);
 }
 __device__ __forceinline__ float sadd_n(float a, float b) { return fin_n(a + b); }
 __device__ __forceinline__ float ssub_n(float a, float b) { return fin_n(a - b); }
 __device__ __forceinline__ float smul_n(float a, float b) { return fin_n(a * b); }
+// The two halves of that rule where the other half provably changes nothing: _c when the result can
+// never be subnormal (canonical NaN kept), _z inside a chain that is canonicalized where it ends.
+__device__ __forceinline__ float sadd_c(float a, float b) { return canon(a + b); }
+__device__ __forceinline__ float smul_c(float a, float b) { return canon(a * b); }
+__device__ __forceinline__ float sadd_z(float a, float b) { return ftz(a + b); }
+__device__ __forceinline__ float smul_z(float a, float b) { return ftz(a * b); }
 
 // int32 -> f32 RNE (v_cvt_f32_i32 rounds to nearest even).
 __device__ __forceinline__ float i2f(int32_t v) { return (float)v; }

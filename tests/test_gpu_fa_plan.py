@@ -123,3 +123,47 @@ def test_flash_attn_plan_tag_wrap(dev, oc, epoch):
     finally:
         plan.free()
         _free(c)
+
+
+@pytest.mark.parametrize("a,flushed", [(7.16, True), (5.3, False)])
+def test_flash_attn_plan_subnormal_merge(dev, oc, a, flushed):
+    """The online merge's FTZ: the first 2048-cell chunk holds the only nonzero values (one cell, 127 2^-24
+    in every dimension: O ~ 7.6e-6), the second a cell whose score is a 128 higher (q all ones, k all a), so
+    the first chunk's merge factor is EXPK(-11.3 a) (scale 1/sqrt(128)). At a = 7.16 it is ~6.6e-36, a
+    normal number, and O times it (~5e-41) is subnormal: the f32 rule flushes it and every output is +0.
+    At a = 5.3 the product (~7e-32) is normal and survives to the output."""
+    D, n_head, n_head_kv, n_kv = 128, 32, 8, 4096
+    E = n_head_kv * D
+    print(f"\nsubnormal merge a={a}", flush=True)
+    kf = np.zeros((n_kv, E), np.float32)
+    vf = np.zeros((n_kv, E), np.float32)
+    kf[3000, :] = a
+    vf[5, :] = 127 * 2.0 ** -24
+    kc = np.zeros((n_kv, E // 32 * 34), np.uint8)
+    vc = np.zeros_like(kc)
+    oc.kv_set_rows(kc, kf, np.arange(n_kv))
+    oc.kv_set_rows(vc, vf, np.arange(n_kv))
+    qh = np.ones((1, n_head * D), np.float32)
+    scale = np.float32(1.0 / math.sqrt(D))
+    msum = oc.msum(np.zeros((1, n_kv), np.float16))
+    want = oc.flash_attn(qh, kc, vc, D, n_head, n_head_kv, scale, msum)
+    assert (np.count_nonzero(want) == 0) == flushed
+    K_, V_ = dev.kv(E, n_kv), dev.kv(E, n_kv)
+    K_.set_bytes(0, kc)
+    V_.set_bytes(1, vc)
+    q = dev.upload(qh)
+    plan = dev.fa_plan(D, n_head, n_head_kv, 1, n_kv)
+    try:
+        plan.set(msum)
+        out = dev.alloc(4 * n_head * D)
+        out.write(np.full(n_head * D, np.nan, np.float32))
+        dev.flash_attn_plan(plan, q, n_head * D, K_, V_, scale, out, n_head * D)
+        assert_bits_equal(out.read(np.float32, (1, n_head * D)), want, f"planned, a={a}")
+        out.write(np.full(n_head * D, np.nan, np.float32))
+        dev.flash_attn(q, 1, n_head * D, K_, V_, D, n_head, n_head_kv, scale, msum, out, n_head * D)
+        assert_bits_equal(out.read(np.float32, (1, n_head * D)), want, f"unplanned, a={a}")
+        assert dev.get_flags() == 0
+    finally:
+        plan.free()
+        K_.free()
+        V_.free()

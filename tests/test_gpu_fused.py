@@ -74,6 +74,35 @@ def test_mul_mat_norm_specials(dev, oc):
     wt.free()
 
 
+@pytest.mark.parametrize("fmt,K", [(H.FMT_Q4_K, 4096), (H.FMT_Q8_0, 896), (H.FMT_Q8_0, 8192)], ids=lambda v: str(v))
+def test_norm_subnormal_squares(dev, oc, fmt, K):
+    """RMS_NORM with eps = 0 over rows whose squares are partly subnormal: values ~1e-18 square to normal
+    numbers, values ~3e-20 to subnormals (~1e-39) that the rule flushes to +0 before the sum. Kept, they
+    would move the sum's low bits and with it the scale. The standalone RMS_NORM and the fused MUL_MAT
+    (the norm in the matvec's leaders) against the oracle."""
+    N, T = 256, 4
+    print(f"\nnorm subnormal squares fmt {fmt} K {K}", flush=True)
+    rng = np.random.default_rng(K + fmt)
+    x = (rng.standard_normal((T, K)) * 1e-18).astype(np.float32)
+    tiny = rng.random((T, K)) < 0.5
+    x[tiny] = (rng.standard_normal(int(tiny.sum())) * 3e-20).astype(np.float32)
+    x[3] = (rng.standard_normal(K) * 3e-20).astype(np.float32)         # every square subnormal: scale of +0
+    sq = (x.astype(np.float64) ** 2)
+    assert ((sq > 0) & (sq < 2.0 ** -126)).sum() > K                  # the case is there
+    nw = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    want_n = oc.rms_norm(x, 0.0, nw[None])
+    xb, nb = dev.upload(x), dev.upload(nw)
+    yb = dev.alloc(x.nbytes)
+    dev.rms_norm(xb, K, T, K, 0.0, yb, K, w=nb, w_stride=K)
+    assert_bits_equal(yb.read(np.float32, (T, K)), want_n, "rms_norm eps 0")
+    blocks = S.quant_rows(fmt, S.seed_of("fused-norm", f"sub-{fmt}-{K}"), N, K)
+    wt = dev.weight(fmt, blocks, N, K)
+    ym = dev.alloc(4 * T * N)
+    dev.mul_mat_norm(wt, xb, T, K, 0.0, nb, ym, N)
+    assert_bits_equal(ym.read(np.float32, (T, N)), oc.mul_mat(fmt, blocks, K, want_n, threads=8), "mul_mat_norm eps 0")
+    wt.free()
+
+
 @pytest.mark.parametrize("fmt,F,K,T,norm", [
     (H.FMT_Q4_K, 14336, 4096, 1, True),   # Llama-3-8B gate|up with the ffn norm
     (H.FMT_Q4_K, 14336, 4096, 1, False),

@@ -498,7 +498,8 @@ __global__ __launch_bounds__(64 * kPvWaves) void k_fa_pv(FaArgs a, FaPlan p) {
 // first round's before the EXPK table is published), then runs CTREE over the 4 channels, the online
 // merge in chunk order and finally ANORM (AT 5.6, 5.7). The running maxima of a round are
 // wave-uniform, so its 2 kMergeItems merge factors are evaluated by as many lanes at once and read
-// back with readlane.
+// back with readlane. A row of one chunk has nothing to merge: its lanes load the four channel
+// partials and row sums only and go straight to CTREE and ANORM (the general path's bits for cnt 1).
 // ---------------------------------------------------------------------------------------------
 constexpr uint32_t kMergeItems = 4;                              // chunks loaded per round
 constexpr uint32_t kMergeHeads = 4;                              // heads per block
@@ -515,6 +516,21 @@ __global__ __launch_bounds__(256) void k_fa_merge(FaArgs a, FaPlan p) {
     const uint32_t first = INL ? p.tok_first[t] : a.tok_first[t];
     const uint32_t cnt = INL ? p.tok_count[t] : a.tok_count[t];  // >= 1 (a row without cells has one empty chunk)
     const uint32_t h = h0 + min(i, hn - 1u);                      // waves past the group load, then leave
+
+    if (cnt == 1u) {                                              // one chunk (workgroup-uniform): no merge,
+        float op[4], lp[4];                                       // so no maxima, items or factors to load
+#pragma unroll
+        for (uint32_t c = 0; c < 4u; ++c) {
+            const size_t slot = ((size_t)first * 4u + c) * nh + h;
+            op[c] = a.OP[slot * D + 64u * sl + L];
+            lp[c] = a.LP[slot];
+        }
+        if (i >= hn) return;
+        const float O = ctree4_o(op[0], op[1], op[2], op[3]);
+        const float l = ctree4_l(lp[0], lp[1], lp[2], lp[3]);
+        a.out[(size_t)t * a.out_stride + (size_t)h * D + 64u * sl + L] = smul_n(O, srcp(maxt(l, bf(kLFloor))));
+        return;
+    }
 
     struct Round {
         float op[kMergeItems][4], lp[kMergeItems][4];

@@ -427,15 +427,16 @@ __global__ __launch_bounds__(256) void k_fa_qk(FaArgs a, FaPlan p) {
                 is = dot4(w1.z, x1.z, is);
                 is = dot4(w1.w, x1.w, is);
                 // SEG (AT 6.2): p_k = +0 + (dK Dx) f32(isum); |terms| >= 2^-48 or 0 (fp16 scales), so
-                // the plain operations never meet a subnormal; NaN is canonicalized below
-                const float t = (h2f_fast(km[kb]) * s_dx[i * NBD + kb]) * (float)is;
-                p[kb] = 0.0f + t;
+                // the plain operations never meet a subnormal; NaN is canonicalized below. The +0 is
+                // added once to the tree's result instead: a -0 term changes a node only when every
+                // term under it is -0, and then the node is -0 where the rule's is +0
+                p[kb] = (h2f_fast(km[kb]) * s_dx[i * NBD + kb]) * (float)is;
             }
 #pragma unroll
             for (int w = 16; w > 1; w >>= 1)
 #pragma unroll
                 for (int k = 0; k < w / 2; ++k) p[k] = p[2 * k] + p[2 * k + 1];
-            s = canon(p[0]);
+            s = canon(p[0] + 0.0f);
             if (it.general) {
                 const float m = a.mask[(size_t)it.t * a.mstride + cell];
                 s = fb(m) == kNegInf ? bf(kNegInf) : sadd(s, m);

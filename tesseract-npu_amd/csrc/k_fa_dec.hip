@@ -553,9 +553,9 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
             is = dot4(kr1.y, x1.y, is);
             is = dot4(kr1.z, x1.z, is);
             is = dot4(kr1.w, x1.w, is);
-            // SEG (AT 6.2): p_k = +0 + (dK Dx) f32(isum); |terms| >= 2^-48 or 0 (fp16 scales)
-            const float t = (dk * s_dx[h * NBD + wave]) * (float)is;
-            s_t[(h * 4u + wave) * 64u + j] = 0.0f + t;
+            // SEG (AT 6.2): p_k = +0 + (dK Dx) f32(isum); |terms| >= 2^-48 or 0 (fp16 scales); the +0
+            // goes to the tree's result (see k_fa_qk)
+            s_t[(h * 4u + wave) * 64u + j] = (dk * s_dx[h * NBD + wave]) * (float)is;
         }
     }
     __syncthreads();
@@ -575,7 +575,7 @@ __global__ __launch_bounds__(256, 4) void k_fa_dec(FaDecArgs a) {
             for (int w = 16; w > 1; w >>= 1)
 #pragma unroll
                 for (int k = 0; k < w / 2; ++k) p[k] = p[2 * k] + p[2 * k + 1];
-            s = canon(p[0]);
+            s = canon(p[0] + 0.0f);
             if (it.general) {
                 const float mval = a.mask[(size_t)it.t * a.mstride + (uint32_t)cell_j];
                 s = fb(mval) == kNegInf ? bf(kNegInf) : sadd(s, mval);

@@ -51,12 +51,14 @@ __device__ __forceinline__ int wave_sum_i(int v) {
     return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
 }
 
-// CTREE over 4 channel partials. Row sums (ctree4_l): every segment row sum is +0 or at least 2^-126
-// (its largest p, a normal EXPK value, enters LSUM as an integer >= 2^23 times 2^(E - 23)), and sums of
-// such non-negative values never reach the subnormal range, so only the NaN canonicalization acts.
+// CTREE over 4 channel partials. Row sums (ctree4_l): every segment row sum is +0, at least 2^-126
+// (its largest p, a normal EXPK value, enters LSUM as an integer >= 2^23 times 2^(E - 23)), +Inf or the
+// canonical NaN, and sums of such non-negative values never reach the subnormal range, never form
+// Inf - Inf and keep the canonical NaN: the plain additions are the rule's (so are the row-sum chains
+// over segments, plain additions as well).
 // Output partials (ctree4_o) can be tiny: FTZ at every step, the NaN payload canonicalized where the
 // merged output is stored.
-__device__ __forceinline__ float ctree4_l(float x0, float x1, float x2, float x3) { return sadd_c(sadd_c(x0, x1), sadd_c(x2, x3)); }
+__device__ __forceinline__ float ctree4_l(float x0, float x1, float x2, float x3) { return (x0 + x1) + (x2 + x3); }
 __device__ __forceinline__ float ctree4_o(float x0, float x1, float x2, float x3) { return sadd_z(sadd_z(x0, x1), sadd_z(x2, x3)); }
 __device__ __forceinline__ int32_t row16_isum(int32_t v) {
     v += dpp_i<kDppXor1>(v);

@@ -245,7 +245,7 @@ struct PvBlock {
             a.OP[slot * D + vh * DV + v] = canon(O);
             if (vh == 0u && v == 0u) {
                 float l = 0.0f;
-                for (uint32_t seg = 0; seg < nseg; ++seg) l = sadd_c(l, s_l[seg * 4u + r4]);
+                for (uint32_t seg = 0; seg < nseg; ++seg) l = l + s_l[seg * 4u + r4];   // see ctree4_l
                 a.LP[slot] = l;
             }
         }

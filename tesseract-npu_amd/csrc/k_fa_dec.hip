@@ -850,7 +850,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
             float Lc = 0.0f;
 #pragma unroll
             for (uint32_t sgi = 0; sgi < 8u; ++sgi)
-                if (sgi < ns[kq]) Lc = sadd_c(Lc, bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pl[kq], (int)sgi)));
+                if (sgi < ns[kq]) Lc = Lc + bf((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pl[kq], (int)sgi));   // see ctree4_l
             if (lane == 0u) s_x[1024u + kq * 4u + c] = Lc;
         }
         __syncthreads();
@@ -1001,7 +1001,7 @@ __device__ __forceinline__ void fa_dec_reduce(const FaDecArgs & a, uint8_t * lds
                 for (uint32_t sgi = 0; sgi < 8u; ++sgi) {
                     if (sgi < ns[kq]) {
                         Oc = sadd_z(Oc, xo[kq][sgi]);
-                        Lc = sadd_c(Lc, xl[kq][sgi]);
+                        Lc = Lc + xl[kq][sgi];                    // see ctree4_l
                     }
                 }
                 s_x[(kq * 4u + c) * 64u + lane] = Oc;

@@ -58,7 +58,6 @@ namespace tsr {
 // memory once.
 // ---------------------------------------------------------------------------------------------
 constexpr uint32_t kPvWaves = 8;                                  // NCG <= 128 -> <= 8 segments per channel
-constexpr uint32_t kPvMaxSeg = 8;
 
 // The P.V work of one block (chunk item, channel c, KV head g, head group hg, value part vh), shared by
 // k_fa_pv (the item's scores in global memory). Lane = (head row hr, group kk of the segment, cell quad);
@@ -460,7 +459,7 @@ __global__ __launch_bounds__(64 * kPvWaves) void k_fa_pv(FaArgs a, FaPlan p) {
     using PB = PvBlock<D, VS>;
     constexpr uint32_t DV = PB::DV, BB = PB::BB;
     const uint32_t G = a.G, nh = a.n_head;
-    // the launch has one wave per segment of its longest channel (nw <= kPvMaxSeg), so the segment
+    // the launch has one wave per segment of its longest channel (nw <= kPvWaves), so the segment
     // results need nw slots: the LDS is sized by the launch
     const uint32_t nw = blockDim.x >> 6;
     uint32_t * s_t64 = (uint32_t *)lds;                           // EXPK table

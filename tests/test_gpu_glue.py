@@ -195,3 +195,18 @@ def test_glue_argument_checks(dev):
         dev.add(b, 16, b, 16, 16, 2, b, 16, b_period=0)
     with pytest.raises(tsr_hip.TsrHipError):
         dev.swiglu(b, 8, b, 16, 16, 2, b, 16)                              # overlapping rows
+
+
+def test_swiglu_expk_sweep(dev, oc):
+    """SWIGLU (so SILU and the device EXPK under it) over 2^24 gate values: every exponent field of both
+    signs, 32768 seeded mantissas each (specials and subnormals included), u = 1, against the oracle."""
+    rng = np.random.default_rng(2024)
+    sign = np.repeat(np.arange(2, dtype=np.uint32), 256 * 32768) << 31
+    expo = np.tile(np.repeat(np.arange(256, dtype=np.uint32), 32768), 2) << 23
+    mant = rng.integers(0, 1 << 23, 2 * 256 * 32768, dtype=np.uint32)
+    mant[::32768] = 0                                             # each field's power of two (and 0, Inf)
+    g = (sign | expo | mant).view(np.float32).reshape(1024, 16384)
+    u = np.ones_like(g)
+    yb = dev.alloc(g.nbytes)
+    dev.swiglu(dev.upload(g), 16384, dev.upload(u), 16384, 16384, 1024, yb, 16384)
+    assert_bits_equal(yb.read(np.float32, (1024, 16384)), oc.swiglu(g, u), "swiglu sweep")

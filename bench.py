@@ -992,8 +992,8 @@ def main() -> int:
     if args.pmc_prefill_child:
         return pmc_prefill_child()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is a "
-                                   "design note in DESIGN.md, not measured)"}))
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is "
+                                   "designed, not built or measured)"}))
         return 2
     if args.warmup < 2 or args.steps < 1:
         print(json.dumps({"error": "--warmup must be >= 2 (an eager token and the capturing replay) and --steps >= 1"}))

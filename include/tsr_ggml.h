@@ -2,8 +2,8 @@
  * ggml-tesseract (sw/ggml-tesseract/ggml-tesseract.cpp) that decides what runs on the device, holds
  * the device's buffers and lowers a ggml graph onto the C ABI of include/tsr_hip.h.
  *
- * ggml itself is not linked. The ggml side (a small shim in the backend's registration code, shown in
- * INTEGRATION.md) fills one tsr_gg_tensor per ggml_tensor it asks about -- type and op mapped to the
+ * ggml itself is not linked. The ggml side (a small shim in the backend's registration code) fills
+ * one tsr_gg_tensor per ggml_tensor it asks about -- type and op mapped to the
  * values below, ne / nb / op_params / flags / name / view_offs copied, sources, view source, data
  * address and buffer linked -- and forwards the backend callbacks:
  *   ggml_backend_buffer_type_i   get_alignment, get_alloc_size      tsr_gg_alignment, tsr_gg_alloc_size
